@@ -1,0 +1,209 @@
+/*
+ * rfp4.h -- C ABI of the MI355X (gfx950) MXFP4 Llama decode engine.
+ *
+ * Drop-in boundary for the reference's kernel API (botBehavior/rust-fp4-blackwell).
+ * The reference launches each kernel through a cuda-oxide typed launcher,
+ *     module.<kernel>(&stream, LaunchConfig, args...) -> Result
+ * (llama_run/src/main.rs:513-534).  Every kernel entry point below keeps the
+ * reference's name and argument order and adds the stream in front; launch
+ * geometry is chosen by the library.  Buffers are device pointers owned by the
+ * caller (the reference's DeviceBuffer<T>); the engine API owns its own.
+ *
+ * Conventions
+ *  - Return 0 on success, a negative RFP4_E_* code otherwise; the message of
+ *    the last failure on this thread is rfp4_last_error().  The reference
+ *    panics on any launch error (`.unwrap()`); a binding maps a non-zero
+ *    return to that panic.
+ *  - Calls are asynchronous on `stream` except rfp4_d2h, rfp4_*_synchronize,
+ *    llama_decode_step and llama_generate, which block.
+ *  - One host thread per engine; the library is not reentrant per stream.
+ *  - rfp4_init(device) must precede every other call (CudaContext::new +
+ *    kernels::load, llama_run/src/main.rs:432,488).
+ */
+#ifndef RFP4_H
+#define RFP4_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void *rfp4_stream_t; /* a hipStream_t; NULL = the null stream */
+typedef void *rfp4_event_t;  /* a hipEvent_t */
+
+enum {
+    RFP4_OK = 0,
+    RFP4_E_INVALID = -1,     /* null pointer, zero size, bad enum */
+    RFP4_E_SHAPE = -2,       /* K not a multiple of 32, unsupported head_dim, ... */
+    RFP4_E_CAPACITY = -3,    /* exceeds a workspace or LDS plan */
+    RFP4_E_KV_OVERFLOW = -4, /* position >= max_seq */
+    RFP4_E_NOT_INIT = -5,    /* rfp4_init not called */
+    RFP4_E_ALIGN = -6,       /* pointer not 16-byte aligned where required */
+    RFP4_E_HIP = -7,         /* HIP runtime error, see rfp4_last_error() */
+    RFP4_E_NO_DEVICE = -8,
+};
+
+const char *rfp4_last_error(void);
+int rfp4_version(void);
+
+/* ------------------------------------------------------------------ runtime
+ * Replaces cuda-oxide's context / stream / DeviceBuffer / event API used by
+ * the reference (fp4_gemv/src/main.rs:144-150,177-191). */
+/* CudaContext::new(device) + kernels::load(&ctx): llama_run/src/main.rs:432,488 */
+int rfp4_init(int device);
+int rfp4_device_count(int *count);
+/* ctx.default_stream(): llama_run/src/main.rs:433 (here: a new HIP stream) */
+int rfp4_stream_create(rfp4_stream_t *stream);
+int rfp4_stream_destroy(rfp4_stream_t stream);
+int rfp4_stream_synchronize(rfp4_stream_t stream); /* stream.synchronize(): fp4_gemv/src/main.rs:177 */
+/* DeviceBuffer allocation (from_host / zeroed): llama_run/src/main.rs:436,454 */
+int rfp4_malloc(void **dptr, size_t bytes);
+int rfp4_free(void *dptr);
+/* DeviceBuffer::zeroed (a fill kernel, so it may be captured in a graph); bytes % 4 == 0 */
+int rfp4_memset_zero(void *dptr, size_t bytes, rfp4_stream_t stream);
+/* DeviceBuffer::from_host: llama_run/src/main.rs:436 */
+int rfp4_h2d(void *dst, const void *src, size_t bytes, rfp4_stream_t stream);
+/* DeviceBuffer::to_host_vec (blocking): llama_run/src/main.rs:535 */
+int rfp4_d2h(void *dst, const void *src, size_t bytes, rfp4_stream_t stream);
+/* stream.record_event / elapsed_ms: fp4_gemv/src/main.rs:179-191 */
+int rfp4_event_create(rfp4_event_t *ev);
+int rfp4_event_destroy(rfp4_event_t ev);
+int rfp4_event_record(rfp4_event_t ev, rfp4_stream_t stream);
+int rfp4_event_synchronize(rfp4_event_t ev);
+int rfp4_event_elapsed_ms(float *ms, rfp4_event_t start, rfp4_event_t end);
+
+/* ------------------------------------------------------------------ kernels */
+/* fp4_gemv(n, k, w, scales, x, y): llama_run/src/main.rs:34-77 (also
+ * fp4_gemv/src/main.rs:32-92).  W: E2M1 packed 8 per u32, low nibble first,
+ * row-major K/8 words per row; scales: f32 per (row, 32-block); x: K floats.
+ * K % 32 == 0; w and x 16-byte aligned.  All N rows are computed (the
+ * reference's grid N/8 truncates when N % 8 != 0). */
+int fp4_gemv(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint32_t *w, const float *scales,
+             const float *x, float *y);
+/* fp4_gemv with OCP E8M0 scales (one byte 2^(b-127) per row and 32-block):
+ * the BASELINE MXFP4 numerics (trackb/fp4_scale_test.cu:12). */
+int mx4_gemv(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_t *codes, const uint8_t *scales,
+             const float *x, float *y);
+/* Fused epilogues of the same kernel (llama_run/src/main.rs:523-530 folded):
+ *  mx4_gemv_residual: x_res[r] += W.x      (fp4_gemv + residual, :523-524,:529-530)
+ *  mx4_gemv_swiglu:   out[r] = silu(G.x)[r] * (U.x)[r], where G is rows
+ *                     [0,n) and U rows [pair_off, pair_off+n) of `codes`
+ *                     (fp4_gemv gate/up + swiglu, :526-528)
+ *  mx4_gemv_argmax:   y = W.x and *best_token = argmax(y) with the
+ *                     reference's tie rule (fp4_gemv lm_head + argmax, :533-534);
+ *                     workspace: ceil(n/16)*8 bytes (mx4_gemv_argmax_workspace). */
+int mx4_gemv_residual(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_t *codes,
+                      const uint8_t *scales, const float *x, float *x_res);
+int mx4_gemv_swiglu(rfp4_stream_t stream, uint32_t n, uint32_t k, uint32_t pair_off, const uint8_t *codes,
+                    const uint8_t *scales, const float *x, float *out);
+size_t mx4_gemv_argmax_workspace(uint32_t n);
+int mx4_gemv_argmax(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_t *codes, const uint8_t *scales,
+                    const float *x, float *y, void *workspace, uint32_t *best_token);
+/* rmsnorm(dim, eps, x, weight, y): llama_run/src/main.rs:79-116 */
+int rmsnorm(rfp4_stream_t stream, uint32_t dim, float eps, const float *x, const float *weight, float *y);
+/* rmsnorm with fp16 weights (the configs keep norms in fp16) */
+int rmsnorm_f16w(rfp4_stream_t stream, uint32_t dim, float eps, const float *x, const uint16_t *weight,
+                 float *y);
+/* rope(num_heads, head_dim, cos_base, cos, sin, q): llama_run/src/main.rs:118-138 */
+int rope(rfp4_stream_t stream, uint32_t num_heads, uint32_t head_dim, uint32_t cos_base, const float *cos_tab,
+         const float *sin_tab, float *q);
+/* copy_into(n, off, src, dst): llama_run/src/main.rs:140-146 (f32 KV append) */
+int copy_into(rfp4_stream_t stream, uint32_t n, uint32_t off, const float *src, float *dst);
+/* copy_into with an fp16 destination (RNE), the configs' KV-cache format */
+int kv_append_f16(rfp4_stream_t stream, uint32_t n, uint32_t off, const float *src, uint16_t *dst);
+/* attn_decode(n_heads, n_kv_heads, seq, q, kc, vc, out): llama_run/src/main.rs:148-242.
+ * Reference layout: f32 K/V [t][kv_head][64], head_dim 64.  No MAXSEQ cap:
+ * split-K over the sequence (the reference caps seq at MAXSEQ=2048, :18). */
+int attn_decode(rfp4_stream_t stream, uint32_t n_heads, uint32_t n_kv_heads, uint32_t seq, const float *q,
+                const float *kc, const float *vc, float *out);
+/* attn_decode over fp16 K/V with head_dim 64 or 128 and any token / head
+ * strides (elements): element (t, kvh, d) at t*token_stride + kvh*head_stride + d. */
+int attn_decode_f16(rfp4_stream_t stream, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                    uint32_t seq, const float *q, const uint16_t *kc, const uint16_t *vc, uint64_t token_stride,
+                    uint64_t head_stride, float *out);
+/* swiglu(n, gate, up, out): llama_run/src/main.rs:244-252 */
+int swiglu(rfp4_stream_t stream, uint32_t n, const float *gate, const float *up, float *out);
+/* residual(n, y, x): x += y, llama_run/src/main.rs:254-261 */
+int residual(rfp4_stream_t stream, uint32_t n, const float *y, float *x);
+/* argmax(n, logits, out): llama_run/src/main.rs:263-315 (ties -> lowest index) */
+int argmax(rfp4_stream_t stream, uint32_t n, const float *logits, uint32_t *out);
+/* fp4_mma_allones(out): fp4_mma/src/main.rs:18-54.  One gfx950 scaled MFMA
+ * tile; writes 128 floats (D[16][8], row-major), all 64.0. */
+int fp4_mma_allones(rfp4_stream_t stream, float *out);
+/* OCP MX quantization of rows x k values (f32, or bf16 if src_is_bf16) into
+ * E2M1 codes (k/2 bytes per row) and E8M0 scales (k/32 per row).  Same bits
+ * as the engine's weight quantizer.  No reference counterpart on the engine
+ * path (the reference quantizes with f32 absmax/6 scales on the host,
+ * llama_run/src/main.rs:334-376); needed for MXFP4 activations. */
+int mx4_quantize(rfp4_stream_t stream, uint64_t rows, uint64_t k, const void *src, int src_is_bf16,
+                 uint8_t *codes, uint8_t *scales);
+
+/* ------------------------------------------------------------------ test hooks
+ * Raw single-tile MFMA (layout pinning, the role of trackb/fp4_mapping_test.cu
+ * and trackb/fp4_scale_test.cu): a, b hold 8 dwords per lane (64 lanes),
+ * sa, sb one dword per lane; out receives the raw accumulator registers
+ * (4 floats per lane for 16x16x128, 16 for 32x32x64). */
+int rfp4_mma_tile16(rfp4_stream_t stream, const uint32_t *a, const uint32_t *b, const uint32_t *sa,
+                    const uint32_t *sb, float *out);
+int rfp4_mma_tile32(rfp4_stream_t stream, const uint32_t *a, const uint32_t *b, const uint32_t *sa,
+                    const uint32_t *sb, float *out);
+/* Hardware E2M1 conversion of n words (8 codes each) to 8n floats. */
+int rfp4_selftest_cvt_fp4(rfp4_stream_t stream, uint32_t n, const uint32_t *words, float *out);
+/* Synthetic weight generator used by the engine (rows [r0, r0+nrows)). */
+int rfp4_synth_mx_weight(rfp4_stream_t stream, uint64_t seed, uint64_t stream_id, float sigma, uint64_t k,
+                         uint64_t r0, uint64_t nrows, uint8_t *codes, uint8_t *scales);
+int rfp4_synth_f16(rfp4_stream_t stream, uint64_t seed, uint64_t stream_id, float sigma, float offset, uint64_t n,
+                   uint16_t *out);
+
+/* ------------------------------------------------------------------ engine
+ * The step loop of llama_run / llama_decode (llama_run/src/main.rs:492-570,
+ * llama_decode/src/main.rs:428-492) with the model constants of
+ * llama_run/src/main.rs:318-332 made a runtime config. */
+typedef struct rfp4_model_config {
+    uint32_t dim, n_layers, n_heads, n_kv_heads, head_dim, ffn, vocab, max_seq;
+    double theta;
+    float eps;
+    uint32_t reserved;
+} rfp4_model_config;
+
+typedef struct llama_engine llama_engine;
+
+/* Allocates weights (synthetic MXFP4 init from `seed`, generated on the
+ * device), fp16 KV caches and workspaces, and captures the step graph. */
+int llama_engine_create(const rfp4_model_config *cfg, uint64_t seed, llama_engine **out);
+int llama_engine_destroy(llama_engine *e);
+/* Fill K/V positions [0, upto) of every layer with f16(0.1 * N(0,1))
+ * (the pre-filled context of llama_decode/src/main.rs:357,375-376). */
+int llama_engine_prefill_kv(llama_engine *e, uint64_t seed, uint32_t upto);
+/* forward(tok, pos) -> argmax, blocking: llama_run/src/main.rs:492-536 */
+int llama_decode_step(llama_engine *e, uint32_t tok, uint32_t pos, uint32_t *next);
+/* Prompt-then-greedy loop without the EOS stop (llama_run/src/main.rs:544-570):
+ * feeds prompt[0..n_prompt) from position pos0, generates n_new tokens into
+ * out.  The whole loop runs on the device (one graph replay per token, token
+ * feedback through device memory); one host sync at the end. */
+int llama_generate(llama_engine *e, const uint32_t *prompt, uint32_t n_prompt, uint32_t pos0, uint32_t n_new,
+                   uint32_t *out);
+/* Asynchronous building blocks of llama_generate for timing: arm the cursor,
+ * replay n steps, read back the produced tokens. */
+int llama_engine_begin(llama_engine *e, const uint32_t *prompt, uint32_t n_prompt, uint32_t pos0,
+                       uint32_t ids_cap);
+int llama_engine_run_steps(llama_engine *e, uint32_t n_steps);
+int llama_engine_read_ids(llama_engine *e, uint32_t *ids, uint32_t count);
+/* Logits of the last step (vocab floats, blocking). */
+int llama_engine_logits(llama_engine *e, float *host_logits);
+rfp4_stream_t llama_engine_stream(llama_engine *e);
+/* 1 = replay the captured step graph (default), 0 = launch kernels eagerly */
+int llama_engine_use_graph(llama_engine *e, int enable);
+/* Device views for parity tests.  proj: 0..6 = q,k,v,o,gate,up,down; layer -1 = LM head. */
+int llama_engine_weight(llama_engine *e, int layer, int proj, const uint8_t **codes, const uint8_t **scales,
+                        size_t *code_bytes, size_t *scale_bytes);
+int llama_engine_kv(llama_engine *e, int layer, const uint16_t **k, const uint16_t **v, size_t *count);
+/* Per-token weight and KV bytes the step streams at a given position. */
+uint64_t llama_engine_weight_bytes(const llama_engine *e);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,212 @@
+// Elementwise kernels, argmax, decode-cursor bookkeeping, synthetic init and
+// the OCP MX quantizer for gfx950.
+#pragma once
+#include "common.h"
+
+// ---------------------------------------------------------------- fill (memset replacement)
+RFP4_DEV void fill_body(const FillArgs &a)
+{
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n_words;
+         i += (uint64_t)gridDim.x * blockDim.x)
+        a.p[i] = a.value;
+}
+
+// ---------------------------------------------------------------- copy_into (llama_run/src/main.rs:140-146)
+template <int DST_F16>
+RFP4_DEV void copy_into_body(const CopyArgs &a)
+{
+    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= a.n) return;
+    if (DST_F16)
+        ((uint16_t *)a.dst)[(size_t)a.off + i] = f32_to_f16_bits(a.src[i]);
+    else
+        ((float *)a.dst)[(size_t)a.off + i] = a.src[i];
+}
+
+// ---------------------------------------------------------------- swiglu / residual (llama_run/src/main.rs:244-261)
+RFP4_DEV void swiglu_body(const EltwiseArgs &a)
+{
+    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= a.n) return;
+    float g = a.a[i];
+    float s = __fdiv_rn(g, __fadd_rn(1.0f, expf(-g)));
+    a.out[i] = __fmul_rn(s, a.b[i]);
+}
+
+RFP4_DEV void residual_body(const EltwiseArgs &a)
+{
+    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= a.n) return;
+    a.out[i] = __fadd_rn(a.out[i], a.a[i]);
+}
+
+// ---------------------------------------------------------------- argmax (llama_run/src/main.rs:263-315)
+// One workgroup; strict '>' scan from (-1e30, 0); ties resolve to the lowest
+// index through the packed (value, ~index) key.
+RFP4_DEV void argmax_body(const ArgmaxArgs &a)
+{
+    __shared__ unsigned long long red[16];
+    unsigned long long best = pack_argmax(-1e30f, 0u);
+    for (uint32_t i = threadIdx.x; i < a.n; i += blockDim.x) {
+        float v = a.logits[i];
+        if (v > -1e30f) {
+            unsigned long long k = pack_argmax(v, i);
+            best = k > best ? k : best;
+        }
+    }
+    // wave reduce on the 64-bit key
+    for (int off = 32; off >= 1; off >>= 1) {
+        unsigned long long o = __shfl_xor(best, off, 64);
+        best = o > best ? o : best;
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    if (lane == 0) red[wave] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long b = red[0];
+        for (int w = 1; w < nw; w++) b = red[w] > b ? red[w] : b;
+        *a.out = 0xFFFFFFFFu - (uint32_t)(b & 0xFFFFFFFFull);
+    }
+}
+
+// ---------------------------------------------------------------- end of decode step
+RFP4_DEV void step_body(const StepArgs &a)
+{
+    __shared__ unsigned long long red[16];
+    unsigned long long best = 0ull;
+    for (uint32_t i = threadIdx.x; i < a.n_best; i += blockDim.x) best = a.best[i] > best ? a.best[i] : best;
+    for (int off = 32; off >= 1; off >>= 1) {
+        unsigned long long o = __shfl_xor(best, off, 64);
+        best = o > best ? o : best;
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    if (lane == 0) red[wave] = best;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        unsigned long long b = red[0];
+        for (int w = 1; w < nw; w++) b = red[w] > b ? red[w] : b;
+        uint32_t tok = 0xFFFFFFFFu - (uint32_t)(b & 0xFFFFFFFFull);
+        StepState st = *a.state;
+        *a.last_tok = tok;
+        uint32_t nxt = (uint32_t)st.step + 1u;
+        if (nxt >= st.n_prompt && nxt < st.ids_cap) a.ids[nxt] = tok;
+        st.step += 1;
+        st.pos += 1;
+        *a.state = st;
+    }
+}
+
+// ---------------------------------------------------------------- OCP MX block quantizer
+// Bit-exact twin of the host quantizer: shared exp = floor(log2(amax)) - 2,
+// elements RNE onto E2M1 with saturation, all-zero block -> scale byte 0.
+RFP4_DEV int floor_log2_pos(float a)
+{
+    uint32_t u = __float_as_uint(a);
+    int e = (int)((u >> 23) & 0xFFu);
+    if (e != 0) return e - 127;
+    return -118 - (int)__builtin_clz(u & 0x7FFFFFu); // subnormal u*2^-149: msb at 31-clz
+}
+
+RFP4_DEV uint32_t e2m1_rne_code(float v)
+{
+    float a = fabsf(v);
+    uint32_t c;
+    if (a <= 0.25f) c = 0;
+    else if (a < 0.75f) c = 1;
+    else if (a <= 1.25f) c = 2;
+    else if (a < 1.75f) c = 3;
+    else if (a <= 2.5f) c = 4;
+    else if (a < 3.5f) c = 5;
+    else if (a <= 5.0f) c = 6;
+    else c = 7;
+    if (__float_as_uint(v) >> 31) c |= 8u;
+    return c;
+}
+
+// Quantize 32 values; writes 16 code bytes and returns the scale byte.
+RFP4_DEV uint32_t quant_block32(const float *v, uint8_t *out16)
+{
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(v[i]));
+    int se = 0;
+    uint32_t sbyte = 0;
+    if (amax != 0.0f) {
+        se = floor_log2_pos(amax) - 2;
+        se = se < -127 ? -127 : (se > 127 ? 127 : se);
+        sbyte = (uint32_t)(se + 127);
+    }
+    uint32_t words[4] = {0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < 32; i++) {
+        float s = amax != 0.0f ? ldexpf(v[i], -se) : v[i];
+        words[i >> 3] |= e2m1_rne_code(s) << (4 * (i & 7));
+    }
+    *(uint4 *)out16 = make_uint4(words[0], words[1], words[2], words[3]);
+    return sbyte;
+}
+
+// One thread per 32-block of the synthetic weight.
+RFP4_DEV void synth_weight_body(const SynthWeightArgs &a)
+{
+    const uint64_t nb = a.k / 32;
+    const uint64_t total = a.nrows * nb;
+    for (uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (uint64_t)gridDim.x * blockDim.x) {
+        uint64_t rr = t / nb, blk = t % nb;
+        uint64_t base = (a.r0 + rr) * a.k + blk * 32;
+        float v[32];
+#pragma unroll
+        for (int i = 0; i < 32; i++) v[i] = ih4_normal(mix64(a.seed, a.stream, base + (uint64_t)i), a.coef);
+        uint32_t sb = quant_block32(v, a.packed + (rr * a.k + blk * 32) / 2);
+        a.scales[t] = (uint8_t)sb;
+    }
+}
+
+RFP4_DEV void synth_f16_body(const SynthF16Args &a)
+{
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < a.n; i += (uint64_t)gridDim.x * blockDim.x)
+        a.out[i] = f32_to_f16_bits(__fadd_rn(a.offset, ih4_normal(mix64(a.seed, a.stream, i), a.coef)));
+}
+
+// KV prefill: logical index (t*NKV + kvh)*HD + d, stored at [kvh][t][d].
+RFP4_DEV void synth_kv_body(const SynthKvArgs &a)
+{
+    const uint64_t total = (uint64_t)a.upto * a.n_kv_heads * a.head_dim;
+    for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (uint64_t)gridDim.x * blockDim.x) {
+        uint64_t d = i % a.head_dim, r = i / a.head_dim, kvh = r % a.n_kv_heads, t = r / a.n_kv_heads;
+        float v = ih4_normal(mix64(a.seed, a.stream, i), a.coef);
+        a.cache[(kvh * a.max_seq + t) * a.head_dim + d] = f32_to_f16_bits(v);
+    }
+}
+
+// f32 (SRC_BF16=0) or bf16 rows -> MXFP4, one thread per block.
+template <int SRC_BF16>
+RFP4_DEV void quant_mx_body(const QuantMxArgs &a)
+{
+    const uint64_t nb = a.k / 32, total = a.rows * nb;
+    for (uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (uint64_t)gridDim.x * blockDim.x) {
+        uint64_t r = t / nb, blk = t % nb;
+        float v[32];
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            uint64_t idx = r * a.k + blk * 32 + (uint64_t)i;
+            v[i] = SRC_BF16 ? __uint_as_float((uint32_t)((const uint16_t *)a.src)[idx] << 16)
+                            : ((const float *)a.src)[idx];
+        }
+        a.scales[t] = (uint8_t)quant_block32(v, a.packed + (r * a.k + blk * 32) / 2);
+    }
+}
+
+// ---------------------------------------------------------------- self-tests
+// out[2i], out[2i+1] = hardware E2M1 conversion of byte i&3 of in[i>>2]
+// (pins the builtin's nibble order against the host codec).
+RFP4_DEV void selftest_cvt_body(const SelftestArgs &a)
+{
+    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= a.n) return;
+    uint32_t w = a.in[i];
+    f32x2 v0 = fp4x2_to_f32<0>(w), v1 = fp4x2_to_f32<1>(w), v2 = fp4x2_to_f32<2>(w), v3 = fp4x2_to_f32<3>(w);
+    float *o = a.out + (size_t)i * 8;
+    o[0] = v0.x; o[1] = v0.y; o[2] = v1.x; o[3] = v1.y;
+    o[4] = v2.x; o[5] = v2.y; o[6] = v3.x; o[7] = v3.y;
+}

@@ -1,0 +1,440 @@
+// Llama MXFP4 decode engine: the step loop of llama_run / llama_decode
+// (llama_run/src/main.rs:492-570, llama_decode/src/main.rs:428-492),
+// rebuilt around one HIP graph per token.
+//
+// Device memory per engine:
+//  - weights (MXFP4, row-major codes + E8M0 scales), per layer
+//      qkv  [(NH+2*NKV)*HD][DIM]   q, k, v stacked: one GEMV launch
+//      o    [DIM][NH*HD]
+//      gu   [2*FFN][DIM]           gate rows then up rows: one GEMV + SwiGLU
+//      down [DIM][FFN]
+//    plus the LM head [VOCAB][DIM]; embeddings and norms fp16.
+//  - KV caches fp16 [layer][kvh][max_seq_alloc][HD] (head-major, so a split-K
+//    attention workgroup streams one contiguous token range).
+//  - a device cursor (position, step) and the token array ids[]; the LM-head
+//    GEMV reduces its argmax per workgroup and the step kernel writes the next
+//    token into ids[], so consecutive steps need no host round trip.
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <vector>
+
+#include "runtime.h"
+
+using namespace rfp4;
+
+// Stream ids of the synthetic init; the CPU oracle uses the same ids.
+static inline uint64_t stream_w(uint32_t l, uint32_t p) { return ((uint64_t)l << 8) | p; }
+static const uint64_t kStreamLm = 0xFFFF00ull;
+static const uint64_t kStreamEmbed = 0xE0000ull;
+static inline uint64_t stream_norm(uint32_t l, uint32_t w) { return 0xA0000ull + ((uint64_t)l << 1) + w; }
+static const uint64_t kStreamNormFinal = 0xAFFFFull;
+static inline uint64_t stream_kv(uint32_t l, uint32_t isv) { return 0x4B560000ull + ((uint64_t)l << 1) + isv; }
+
+struct LayerW {
+    uint8_t *qkv_c, *qkv_s, *o_c, *o_s, *gu_c, *gu_s, *d_c, *d_s;
+};
+
+struct llama_engine {
+    rfp4_model_config c{};
+    hipStream_t stream = nullptr;
+    std::vector<void *> allocs;
+    std::vector<LayerW> L;
+    uint16_t *norm_attn = nullptr, *norm_ffn = nullptr, *norm_final = nullptr, *embed = nullptr;
+    uint8_t *lm_c = nullptr, *lm_s = nullptr;
+    uint16_t *kcache = nullptr, *vcache = nullptr;
+    uint32_t max_seq_alloc = 0;
+    float *cos_tab = nullptr, *sin_tab = nullptr;
+    float *x = nullptr, *h = nullptr, *qkv = nullptr, *attn_out = nullptr, *sw = nullptr, *logits = nullptr;
+    unsigned long long *best = nullptr;
+    uint32_t n_best = 0;
+    float *attn_part = nullptr;
+    uint32_t *attn_counters = nullptr;
+    uint32_t attn_chunk = 64, attn_max_splits = 1;
+    StepState *state = nullptr;
+    uint32_t *ids = nullptr, *last_tok = nullptr;
+    uint32_t ids_alloc = 0;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t graph_exec = nullptr;
+    bool use_graph = true;
+    // host mirror of the cursor, for bounds checks
+    int64_t h_pos = 0, h_step = 0, h_ids_cap = 0;
+    bool armed = false;
+};
+
+static int dalloc(llama_engine *e, void **p, size_t bytes)
+{
+    int rc = hip_check(hipMalloc(p, bytes), "hipMalloc(engine)");
+    if (!rc) e->allocs.push_back(*p);
+    return rc;
+}
+
+template <typename T>
+static int dalloc_t(llama_engine *e, T **p, size_t count)
+{
+    return dalloc(e, (void **)p, count * sizeof(T));
+}
+
+static uint32_t qdim(const rfp4_model_config &c) { return c.n_heads * c.head_dim; }
+static uint32_t kvdim(const rfp4_model_config &c) { return c.n_kv_heads * c.head_dim; }
+
+static int validate(const rfp4_model_config &c)
+{
+    if (!c.dim || !c.n_layers || !c.n_heads || !c.n_kv_heads || !c.head_dim || !c.ffn || !c.vocab || !c.max_seq)
+        return set_error(RFP4_E_SHAPE, "model config has a zero dimension");
+    if (c.head_dim != 64 && c.head_dim != 128) return set_error(RFP4_E_SHAPE, "head_dim %u unsupported (64, 128)", c.head_dim);
+    if (c.n_heads % c.n_kv_heads || c.n_heads / c.n_kv_heads > 8)
+        return set_error(RFP4_E_SHAPE, "n_heads %u / n_kv_heads %u: group must divide and be <= 8", c.n_heads, c.n_kv_heads);
+    if (c.dim % 32 || c.ffn % 32 || qdim(c) % 32) return set_error(RFP4_E_SHAPE, "dim, ffn and n_heads*head_dim must be multiples of 32");
+    if (c.n_heads > kAttnMaxHeads) return set_error(RFP4_E_SHAPE, "n_heads %u > %u", c.n_heads, kAttnMaxHeads);
+    return RFP4_OK;
+}
+
+// ---------------------------------------------------------------- step enqueue
+static int enqueue_step(llama_engine *e)
+{
+    const rfp4_model_config &c = e->c;
+    hipStream_t s = e->stream;
+    const uint32_t qd = qdim(c), kvd = kvdim(c), hd = c.head_dim;
+    int rc;
+    EmbedArgs ea{e->embed, e->ids, e->state, e->x, c.dim, c.vocab};
+    if ((rc = launch("rfp4_embed", dim3((c.dim + 255) / 256), dim3(256), s, &ea))) return rc;
+    for (uint32_t l = 0; l < c.n_layers; l++) {
+        const LayerW &w = e->L[l];
+        uint16_t *kc = e->kcache + (size_t)l * c.n_kv_heads * e->max_seq_alloc * hd;
+        uint16_t *vc = e->vcache + (size_t)l * c.n_kv_heads * e->max_seq_alloc * hd;
+        RmsnormArgs na{e->x, e->norm_attn + (size_t)l * c.dim, e->h, c.dim, c.eps};
+        if ((rc = launch("rfp4_rmsnorm_f16w", dim3(1), dim3(1024), s, &na))) return rc;
+        GemvArgs qa{w.qkv_c, w.qkv_s, e->h, e->qkv, nullptr, qd + 2 * kvd, c.dim, 0, 0};
+        if ((rc = gemv_launch("e8m0", RFP4_EPI_STORE, qa, s, 0))) return rc;
+        RopeAppendArgs ra{e->qkv, e->cos_tab, e->sin_tab, kc, vc, &e->state->pos, c.n_heads, c.n_kv_heads, hd, e->max_seq_alloc};
+        uint32_t work = c.n_heads * hd / 2 + c.n_kv_heads * hd / 2 + kvd;
+        if ((rc = launch("rfp4_rope_append", dim3((work + 255) / 256), dim3(256), s, &ra))) return rc;
+        AttnArgs aa{};
+        aa.q = e->qkv; aa.kc = kc; aa.vc = vc; aa.out = e->attn_out;
+        aa.part = e->attn_part; aa.counters = e->attn_counters; aa.pos_ptr = &e->state->pos;
+        aa.ts = hd; aa.hs = (uint64_t)e->max_seq_alloc * hd;
+        aa.n_heads = c.n_heads; aa.n_kv_heads = c.n_kv_heads; aa.head_dim = hd; aa.seq = 0;
+        aa.chunk = e->attn_chunk; aa.max_splits = e->attn_max_splits;
+        if ((rc = attn_launch(aa, 1, s, e->attn_chunk * e->attn_max_splits))) return rc;
+        GemvArgs oa{w.o_c, w.o_s, e->attn_out, e->x, nullptr, c.dim, qd, 0, 0};
+        if ((rc = gemv_launch("e8m0", RFP4_EPI_RESIDUAL, oa, s, 0))) return rc;
+        RmsnormArgs fa{e->x, e->norm_ffn + (size_t)l * c.dim, e->h, c.dim, c.eps};
+        if ((rc = launch("rfp4_rmsnorm_f16w", dim3(1), dim3(1024), s, &fa))) return rc;
+        GemvArgs ga{w.gu_c, w.gu_s, e->h, e->sw, nullptr, c.ffn, c.dim, c.ffn, 0};
+        if ((rc = gemv_launch("e8m0", RFP4_EPI_SWIGLU, ga, s, 0))) return rc;
+        GemvArgs da{w.d_c, w.d_s, e->sw, e->x, nullptr, c.dim, c.ffn, 0, 0};
+        if ((rc = gemv_launch("e8m0", RFP4_EPI_RESIDUAL, da, s, 0))) return rc;
+    }
+    RmsnormArgs fn{e->x, e->norm_final, e->h, c.dim, c.eps};
+    if ((rc = launch("rfp4_rmsnorm_f16w", dim3(1), dim3(1024), s, &fn))) return rc;
+    GemvArgs la{e->lm_c, e->lm_s, e->h, e->logits, e->best, c.vocab, c.dim, 0, 0};
+    if ((rc = gemv_launch("e8m0", RFP4_EPI_ARGMAX, la, s, 0))) return rc;
+    StepArgs sa{e->best, e->state, e->ids, e->last_tok, e->n_best, 0};
+    return launch("rfp4_step", dim3(1), dim3(1024), s, &sa);
+}
+
+static int capture_graph(llama_engine *e)
+{
+    int rc = hip_check(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+    if (rc) return rc;
+    int rc_enq = enqueue_step(e);
+    hipGraph_t g = nullptr;
+    rc = hip_check(hipStreamEndCapture(e->stream, &g), "hipStreamEndCapture");
+    if (rc_enq) {
+        if (g) hipGraphDestroy(g);
+        return rc_enq;
+    }
+    if (rc) return rc;
+    e->graph = g;
+    return hip_check(hipGraphInstantiate(&e->graph_exec, g, nullptr, nullptr, 0), "hipGraphInstantiate");
+}
+
+static void engine_free(llama_engine *e)
+{
+    if (!e) return;
+    if (e->stream) hipStreamSynchronize(e->stream);
+    if (e->graph_exec) hipGraphExecDestroy(e->graph_exec);
+    if (e->graph) hipGraphDestroy(e->graph);
+    for (void *p : e->allocs) hipFree(p);
+    if (e->stream) hipStreamDestroy(e->stream);
+    delete e;
+}
+
+extern "C" {
+
+int llama_engine_create(const rfp4_model_config *cfg, uint64_t seed, llama_engine **out)
+{
+    if (!cfg || !out) return set_error(RFP4_E_INVALID, "llama_engine_create: null argument");
+    *out = nullptr;
+    Runtime *rt = runtime();
+    if (!rt) return set_error(RFP4_E_NOT_INIT, "rfp4_init has not been called");
+    int rc = validate(*cfg);
+    if (rc) return rc;
+    llama_engine *e = new llama_engine();
+    e->c = *cfg;
+    const rfp4_model_config &c = e->c;
+    const uint32_t qd = qdim(c), kvd = kvdim(c), hd = c.head_dim;
+    rc = hip_check(hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking), "hipStreamCreate");
+    // attention split plan over the full cache capacity
+    e->attn_chunk = attn_chunk_for(c.n_kv_heads, c.max_seq, rt->num_cus);
+    e->attn_max_splits = (c.max_seq + e->attn_chunk - 1) / e->attn_chunk;
+    e->max_seq_alloc = (e->attn_chunk * e->attn_max_splits + 255u) / 256u * 256u;
+    hipStream_t s = e->stream;
+    e->L.resize(c.n_layers);
+    const float sigma = 0.02f;
+    for (uint32_t l = 0; l < c.n_layers && !rc; l++) {
+        LayerW &w = e->L[l];
+        uint32_t nqkv = qd + 2 * kvd;
+        rc = dalloc_t(e, &w.qkv_c, (size_t)nqkv * c.dim / 2);
+        if (!rc) rc = dalloc_t(e, &w.qkv_s, (size_t)nqkv * c.dim / 32);
+        if (!rc) rc = dalloc_t(e, &w.o_c, (size_t)c.dim * qd / 2);
+        if (!rc) rc = dalloc_t(e, &w.o_s, (size_t)c.dim * qd / 32);
+        if (!rc) rc = dalloc_t(e, &w.gu_c, (size_t)2 * c.ffn * c.dim / 2);
+        if (!rc) rc = dalloc_t(e, &w.gu_s, (size_t)2 * c.ffn * c.dim / 32);
+        if (!rc) rc = dalloc_t(e, &w.d_c, (size_t)c.dim * c.ffn / 2);
+        if (!rc) rc = dalloc_t(e, &w.d_s, (size_t)c.dim * c.ffn / 32);
+        if (rc) break;
+        // q, k, v stacked; each keeps its own stream and local row index
+        rc = rfp4_synth_mx_weight(s, seed, stream_w(l, 0), sigma, c.dim, 0, qd, w.qkv_c, w.qkv_s);
+        if (!rc) rc = rfp4_synth_mx_weight(s, seed, stream_w(l, 1), sigma, c.dim, 0, kvd, w.qkv_c + (size_t)qd * c.dim / 2,
+                                           w.qkv_s + (size_t)qd * c.dim / 32);
+        if (!rc) rc = rfp4_synth_mx_weight(s, seed, stream_w(l, 2), sigma, c.dim, 0, kvd,
+                                           w.qkv_c + (size_t)(qd + kvd) * c.dim / 2, w.qkv_s + (size_t)(qd + kvd) * c.dim / 32);
+        if (!rc) rc = rfp4_synth_mx_weight(s, seed, stream_w(l, 3), sigma, qd, 0, c.dim, w.o_c, w.o_s);
+        if (!rc) rc = rfp4_synth_mx_weight(s, seed, stream_w(l, 4), sigma, c.dim, 0, c.ffn, w.gu_c, w.gu_s);
+        if (!rc) rc = rfp4_synth_mx_weight(s, seed, stream_w(l, 5), sigma, c.dim, 0, c.ffn,
+                                           w.gu_c + (size_t)c.ffn * c.dim / 2, w.gu_s + (size_t)c.ffn * c.dim / 32);
+        if (!rc) rc = rfp4_synth_mx_weight(s, seed, stream_w(l, 6), sigma, c.ffn, 0, c.dim, w.d_c, w.d_s);
+    }
+    if (!rc) rc = dalloc_t(e, &e->norm_attn, (size_t)c.n_layers * c.dim);
+    if (!rc) rc = dalloc_t(e, &e->norm_ffn, (size_t)c.n_layers * c.dim);
+    if (!rc) rc = dalloc_t(e, &e->norm_final, c.dim);
+    for (uint32_t l = 0; l < c.n_layers && !rc; l++) {
+        rc = rfp4_synth_f16(s, seed, stream_norm(l, 0), sigma, 1.0f, c.dim, e->norm_attn + (size_t)l * c.dim);
+        if (!rc) rc = rfp4_synth_f16(s, seed, stream_norm(l, 1), sigma, 1.0f, c.dim, e->norm_ffn + (size_t)l * c.dim);
+    }
+    if (!rc) rc = rfp4_synth_f16(s, seed, kStreamNormFinal, sigma, 1.0f, c.dim, e->norm_final);
+    if (!rc) rc = dalloc_t(e, &e->embed, (size_t)c.vocab * c.dim);
+    if (!rc) rc = rfp4_synth_f16(s, seed, kStreamEmbed, sigma, 0.0f, (size_t)c.vocab * c.dim, e->embed);
+    if (!rc) rc = dalloc_t(e, &e->lm_c, (size_t)c.vocab * c.dim / 2);
+    if (!rc) rc = dalloc_t(e, &e->lm_s, (size_t)c.vocab * c.dim / 32);
+    if (!rc) rc = rfp4_synth_mx_weight(s, seed, kStreamLm, sigma, c.dim, 0, c.vocab, e->lm_c, e->lm_s);
+    size_t kv_elems = (size_t)c.n_layers * c.n_kv_heads * e->max_seq_alloc * hd;
+    if (!rc) rc = dalloc_t(e, &e->kcache, kv_elems);
+    if (!rc) rc = dalloc_t(e, &e->vcache, kv_elems);
+    if (!rc) rc = fill_words((uint32_t *)e->kcache, kv_elems / 2, 0u, s);
+    if (!rc) rc = fill_words((uint32_t *)e->vcache, kv_elems / 2, 0u, s);
+    // rotary table in f64 -> f32 (llama_run/src/main.rs:462-471)
+    const uint32_t half = hd / 2;
+    std::vector<float> cosv((size_t)e->max_seq_alloc * half), sinv((size_t)e->max_seq_alloc * half);
+    for (uint32_t pos = 0; pos < e->max_seq_alloc; pos++)
+        for (uint32_t j = 0; j < half; j++) {
+            double freq = 1.0 / std::pow(c.theta, 2.0 * (double)j / (double)hd);
+            double a = (double)pos * freq;
+            cosv[(size_t)pos * half + j] = (float)std::cos(a);
+            sinv[(size_t)pos * half + j] = (float)std::sin(a);
+        }
+    if (!rc) rc = dalloc_t(e, &e->cos_tab, cosv.size());
+    if (!rc) rc = dalloc_t(e, &e->sin_tab, sinv.size());
+    if (!rc) rc = hip_check(hipMemcpyAsync(e->cos_tab, cosv.data(), cosv.size() * 4, hipMemcpyHostToDevice, s), "H2D cos");
+    if (!rc) rc = hip_check(hipMemcpyAsync(e->sin_tab, sinv.data(), sinv.size() * 4, hipMemcpyHostToDevice, s), "H2D sin");
+    // activations and workspaces
+    uint32_t big = c.dim > qd ? c.dim : qd;
+    if (!rc) rc = dalloc_t(e, &e->x, c.dim);
+    if (!rc) rc = dalloc_t(e, &e->h, big);
+    if (!rc) rc = dalloc_t(e, &e->qkv, qd + 2 * kvd);
+    if (!rc) rc = dalloc_t(e, &e->attn_out, qd);
+    if (!rc) rc = dalloc_t(e, &e->sw, c.ffn);
+    if (!rc) rc = dalloc_t(e, &e->logits, c.vocab);
+    e->n_best = gemv_blocks(c.vocab, RFP4_EPI_ARGMAX, 0);
+    if (!rc) rc = dalloc_t(e, &e->best, e->n_best);
+    if (!rc) rc = dalloc_t(e, &e->attn_part, (size_t)c.n_heads * e->attn_max_splits * (hd + 2));
+    if (!rc) rc = dalloc_t(e, &e->attn_counters, c.n_kv_heads);
+    if (!rc) rc = fill_words(e->attn_counters, c.n_kv_heads, 0u, s);
+    if (!rc) rc = dalloc(e, (void **)&e->state, sizeof(StepState));
+    e->ids_alloc = c.max_seq + 2;
+    if (!rc) rc = dalloc_t(e, &e->ids, e->ids_alloc);
+    if (!rc) rc = dalloc_t(e, &e->last_tok, 1);
+    if (!rc) rc = fill_words((uint32_t *)e->state, sizeof(StepState) / 4, 0u, s);
+    if (!rc) rc = fill_words(e->ids, e->ids_alloc, 0u, s);
+    if (!rc) rc = hip_check(hipStreamSynchronize(s), "hipStreamSynchronize(create)");
+    if (!rc) rc = capture_graph(e);
+    if (rc) {
+        engine_free(e);
+        return rc;
+    }
+    *out = e;
+    return RFP4_OK;
+}
+
+int llama_engine_destroy(llama_engine *e)
+{
+    engine_free(e);
+    return RFP4_OK;
+}
+
+int llama_engine_prefill_kv(llama_engine *e, uint64_t seed, uint32_t upto)
+{
+    if (!e) return set_error(RFP4_E_INVALID, "null engine");
+    const rfp4_model_config &c = e->c;
+    if (upto > c.max_seq) return set_error(RFP4_E_KV_OVERFLOW, "prefill %u > max_seq %u", upto, c.max_seq);
+    const float coef = ih4_coef(0.1f);
+    for (uint32_t l = 0; l < c.n_layers; l++)
+        for (uint32_t isv = 0; isv < 2; isv++) {
+            uint16_t *base = (isv ? e->vcache : e->kcache) + (size_t)l * c.n_kv_heads * e->max_seq_alloc * c.head_dim;
+            SynthKvArgs a{base, seed, stream_kv(l, isv), upto, c.n_kv_heads, c.head_dim, e->max_seq_alloc, coef, 0.0f};
+            uint64_t total = (uint64_t)upto * c.n_kv_heads * c.head_dim;
+            uint64_t blocks = (total + 255) / 256;
+            if (blocks > 65536) blocks = 65536;
+            if (blocks == 0) continue;
+            int rc = launch("rfp4_synth_kv", dim3((unsigned)blocks), dim3(256), e->stream, &a);
+            if (rc) return rc;
+        }
+    return hip_check(hipStreamSynchronize(e->stream), "hipStreamSynchronize(prefill)");
+}
+
+int llama_engine_begin(llama_engine *e, const uint32_t *prompt, uint32_t n_prompt, uint32_t pos0, uint32_t ids_cap)
+{
+    if (!e || !prompt) return set_error(RFP4_E_INVALID, "llama_engine_begin: null argument");
+    if (n_prompt == 0) return set_error(RFP4_E_INVALID, "llama_engine_begin: empty prompt");
+    if (ids_cap < n_prompt || ids_cap > e->ids_alloc) return set_error(RFP4_E_CAPACITY, "ids capacity %u out of range", ids_cap);
+    if (pos0 >= e->c.max_seq) return set_error(RFP4_E_KV_OVERFLOW, "start position %u >= max_seq %u", pos0, e->c.max_seq);
+    for (uint32_t i = 0; i < n_prompt; i++)
+        if (prompt[i] >= e->c.vocab) return set_error(RFP4_E_INVALID, "prompt token %u >= vocab %u", prompt[i], e->c.vocab);
+    int rc = hip_check(hipStreamSynchronize(e->stream), "hipStreamSynchronize(begin)");
+    if (rc) return rc;
+    rc = hip_check(hipMemcpy(e->ids, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice), "H2D prompt");
+    StepState st{(int32_t)pos0, 0, n_prompt, ids_cap};
+    if (!rc) rc = hip_check(hipMemcpy(e->state, &st, sizeof st, hipMemcpyHostToDevice), "H2D cursor");
+    if (rc) return rc;
+    e->h_pos = pos0;
+    e->h_step = 0;
+    e->h_ids_cap = ids_cap;
+    e->armed = true;
+    return RFP4_OK;
+}
+
+int llama_engine_run_steps(llama_engine *e, uint32_t n_steps)
+{
+    if (!e) return set_error(RFP4_E_INVALID, "null engine");
+    if (!e->armed) return set_error(RFP4_E_INVALID, "llama_engine_begin has not been called");
+    if (e->h_pos + n_steps > (int64_t)e->c.max_seq)
+        return set_error(RFP4_E_KV_OVERFLOW, "steps would reach position %lld >= max_seq %u", (long long)(e->h_pos + n_steps),
+                         e->c.max_seq);
+    if (e->h_step + n_steps > e->h_ids_cap - 1)
+        return set_error(RFP4_E_CAPACITY, "steps exceed the token array (%lld + %u > %lld)", (long long)e->h_step, n_steps,
+                         (long long)(e->h_ids_cap - 1));
+    for (uint32_t i = 0; i < n_steps; i++) {
+        int rc = e->use_graph ? hip_check(hipGraphLaunch(e->graph_exec, e->stream), "hipGraphLaunch") : enqueue_step(e);
+        if (rc) return rc;
+    }
+    e->h_pos += n_steps;
+    e->h_step += n_steps;
+    return RFP4_OK;
+}
+
+int llama_engine_read_ids(llama_engine *e, uint32_t *ids, uint32_t count)
+{
+    if (!e || !ids) return set_error(RFP4_E_INVALID, "null argument");
+    if (count > e->ids_alloc) return set_error(RFP4_E_CAPACITY, "count %u > %u", count, e->ids_alloc);
+    int rc = hip_check(hipMemcpyAsync(ids, e->ids, (size_t)count * 4, hipMemcpyDeviceToHost, e->stream), "D2H ids");
+    if (rc) return rc;
+    return hip_check(hipStreamSynchronize(e->stream), "hipStreamSynchronize(ids)");
+}
+
+int llama_generate(llama_engine *e, const uint32_t *prompt, uint32_t n_prompt, uint32_t pos0, uint32_t n_new,
+                   uint32_t *out)
+{
+    if (!out) return set_error(RFP4_E_INVALID, "null output");
+    if (n_new == 0) return RFP4_OK;
+    uint32_t cap = n_prompt + n_new;
+    int rc = llama_engine_begin(e, prompt, n_prompt, pos0, cap);
+    if (!rc) rc = llama_engine_run_steps(e, n_prompt + n_new - 1);
+    if (rc) return rc;
+    std::vector<uint32_t> ids(cap);
+    rc = llama_engine_read_ids(e, ids.data(), cap);
+    if (rc) return rc;
+    std::memcpy(out, ids.data() + n_prompt, (size_t)n_new * 4);
+    return RFP4_OK;
+}
+
+int llama_decode_step(llama_engine *e, uint32_t tok, uint32_t pos, uint32_t *next)
+{
+    if (!next) return set_error(RFP4_E_INVALID, "null output");
+    return llama_generate(e, &tok, 1, pos, 1, next);
+}
+
+int llama_engine_logits(llama_engine *e, float *host_logits)
+{
+    if (!e || !host_logits) return set_error(RFP4_E_INVALID, "null argument");
+    int rc = hip_check(hipMemcpyAsync(host_logits, e->logits, (size_t)e->c.vocab * 4, hipMemcpyDeviceToHost, e->stream),
+                       "D2H logits");
+    if (rc) return rc;
+    return hip_check(hipStreamSynchronize(e->stream), "hipStreamSynchronize(logits)");
+}
+
+rfp4_stream_t llama_engine_stream(llama_engine *e) { return e ? (rfp4_stream_t)e->stream : nullptr; }
+
+int llama_engine_use_graph(llama_engine *e, int enable)
+{
+    if (!e) return set_error(RFP4_E_INVALID, "null engine");
+    e->use_graph = enable != 0;
+    return RFP4_OK;
+}
+
+int llama_engine_weight(llama_engine *e, int layer, int proj, const uint8_t **codes, const uint8_t **scales,
+                        size_t *code_bytes, size_t *scale_bytes)
+{
+    if (!e || !codes || !scales || !code_bytes || !scale_bytes) return set_error(RFP4_E_INVALID, "null argument");
+    const rfp4_model_config &c = e->c;
+    const uint32_t qd = qdim(c), kvd = kvdim(c);
+    if (layer < 0) {
+        *codes = e->lm_c;
+        *scales = e->lm_s;
+        *code_bytes = (size_t)c.vocab * c.dim / 2;
+        *scale_bytes = (size_t)c.vocab * c.dim / 32;
+        return RFP4_OK;
+    }
+    if ((uint32_t)layer >= c.n_layers || proj < 0 || proj > 6) return set_error(RFP4_E_INVALID, "bad layer/proj");
+    const LayerW &w = e->L[layer];
+    size_t rows_before = 0, rows = 0, K = c.dim;
+    const uint8_t *bc = nullptr, *bs = nullptr;
+    switch (proj) {
+    case 0: bc = w.qkv_c; bs = w.qkv_s; rows_before = 0; rows = qd; break;
+    case 1: bc = w.qkv_c; bs = w.qkv_s; rows_before = qd; rows = kvd; break;
+    case 2: bc = w.qkv_c; bs = w.qkv_s; rows_before = qd + kvd; rows = kvd; break;
+    case 3: bc = w.o_c; bs = w.o_s; rows = c.dim; K = qd; break;
+    case 4: bc = w.gu_c; bs = w.gu_s; rows = c.ffn; break;
+    case 5: bc = w.gu_c; bs = w.gu_s; rows_before = c.ffn; rows = c.ffn; break;
+    default: bc = w.d_c; bs = w.d_s; rows = c.dim; K = c.ffn; break;
+    }
+    *codes = bc + rows_before * K / 2;
+    *scales = bs + rows_before * K / 32;
+    *code_bytes = rows * K / 2;
+    *scale_bytes = rows * K / 32;
+    return RFP4_OK;
+}
+
+int llama_engine_kv(llama_engine *e, int layer, const uint16_t **k, const uint16_t **v, size_t *count)
+{
+    if (!e || !k || !v || !count) return set_error(RFP4_E_INVALID, "null argument");
+    if (layer < 0 || (uint32_t)layer >= e->c.n_layers) return set_error(RFP4_E_INVALID, "bad layer");
+    size_t per = (size_t)e->c.n_kv_heads * e->max_seq_alloc * e->c.head_dim;
+    *k = e->kcache + (size_t)layer * per;
+    *v = e->vcache + (size_t)layer * per;
+    *count = per;
+    return RFP4_OK;
+}
+
+uint64_t llama_engine_weight_bytes(const llama_engine *e)
+{
+    if (!e) return 0;
+    const rfp4_model_config &c = e->c;
+    uint64_t per_layer = (uint64_t)(qdim(c) + 2 * kvdim(c)) * c.dim + (uint64_t)c.dim * qdim(c) +
+                         3ull * c.ffn * c.dim;
+    uint64_t elems = per_layer * c.n_layers + (uint64_t)c.vocab * c.dim;
+    return elems / 2 + elems / 32;
+}
+
+} // extern "C"

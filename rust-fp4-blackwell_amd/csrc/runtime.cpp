@@ -1,0 +1,493 @@
+// Host runtime of the engine: loads the embedded gfx950 code object, owns
+// the kernel table, and implements the C-ABI kernel entry points
+// (include/rfp4.h) over hipModuleLaunchKernel.
+#include "runtime.h"
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+#include <unordered_map>
+
+extern "C" const unsigned char rfp4_hsaco_start[];
+extern "C" const unsigned char rfp4_hsaco_end[];
+
+namespace rfp4 {
+
+static thread_local std::string t_err;
+static Runtime *g_rt = nullptr;
+static std::mutex g_mu;
+
+int set_error(int code, const char *fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    t_err = buf;
+    return code;
+}
+
+int hip_check(hipError_t e, const char *what)
+{
+    if (e == hipSuccess) return RFP4_OK;
+    return set_error(RFP4_E_HIP, "%s: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+Runtime *runtime() { return g_rt; }
+
+int launch(const char *name, dim3 grid, dim3 block, hipStream_t s, void *args)
+{
+    Runtime *rt = g_rt;
+    if (!rt) return set_error(RFP4_E_NOT_INIT, "rfp4_init has not been called");
+    auto it = rt->fns.find(name);
+    hipFunction_t f = nullptr;
+    if (it == rt->fns.end()) {
+        std::lock_guard<std::mutex> lk(g_mu);
+        hipError_t e = hipModuleGetFunction(&f, rt->module, name);
+        if (e != hipSuccess) return set_error(RFP4_E_HIP, "kernel %s not found: %s", name, hipGetErrorString(e));
+        rt->fns.emplace(name, f);
+    } else {
+        f = it->second;
+    }
+    if (grid.x == 0 || grid.y == 0 || grid.z == 0) return RFP4_OK; // nothing to do
+    void *params[] = {args};
+    return hip_check(hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, 0, s, params, nullptr),
+                     name);
+}
+
+} // namespace rfp4
+
+using namespace rfp4;
+
+extern "C" {
+
+const char *rfp4_last_error(void) { return t_err.c_str(); }
+int rfp4_version(void) { return 1; }
+
+int rfp4_device_count(int *count)
+{
+    if (!count) return set_error(RFP4_E_INVALID, "null count");
+    hipError_t e = hipGetDeviceCount(count);
+    if (e != hipSuccess) {
+        *count = 0;
+        return set_error(RFP4_E_NO_DEVICE, "no HIP device: %s", hipGetErrorString(e));
+    }
+    return RFP4_OK;
+}
+
+int rfp4_init(int device)
+{
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (g_rt) return g_rt->device == device ? RFP4_OK : set_error(RFP4_E_INVALID, "already initialised on device %d", g_rt->device);
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return set_error(RFP4_E_NO_DEVICE, "no HIP device available");
+    if (device < 0 || device >= n) return set_error(RFP4_E_INVALID, "device %d out of range (%d devices)", device, n);
+    int rc = hip_check(hipSetDevice(device), "hipSetDevice");
+    if (rc) return rc;
+    hipDeviceProp_t prop;
+    rc = hip_check(hipGetDeviceProperties(&prop, device), "hipGetDeviceProperties");
+    if (rc) return rc;
+    if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
+        return set_error(RFP4_E_NO_DEVICE, "device %d is %s; this library holds gfx950 code only", device, prop.gcnArchName);
+    Runtime *rt = new Runtime();
+    rt->device = device;
+    rt->num_cus = prop.multiProcessorCount;
+    rc = hip_check(hipModuleLoadData(&rt->module, rfp4_hsaco_start), "hipModuleLoadData");
+    if (rc) {
+        delete rt;
+        return rc;
+    }
+    // default workspace of the drop-in attn_decode
+    rt->attn_part_floats = (size_t)kAttnMaxHeads * kAttnMaxSplits * (128 + 2);
+    rc = hip_check(hipMalloc((void **)&rt->attn_part, rt->attn_part_floats * sizeof(float)), "hipMalloc(attn workspace)");
+    if (!rc) rc = hip_check(hipMalloc((void **)&rt->attn_counters, kAttnMaxHeads * sizeof(uint32_t)), "hipMalloc(attn counters)");
+    if (!rc) rc = hip_check(hipMemset(rt->attn_counters, 0, kAttnMaxHeads * sizeof(uint32_t)), "hipMemset");
+    if (!rc) rc = hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    if (rc) {
+        hipFree(rt->attn_part);
+        hipFree(rt->attn_counters);
+        hipModuleUnload(rt->module);
+        delete rt;
+        return rc;
+    }
+    g_rt = rt;
+    return RFP4_OK;
+}
+
+int rfp4_stream_create(rfp4_stream_t *stream)
+{
+    if (!stream) return set_error(RFP4_E_INVALID, "null stream out");
+    if (!g_rt) return set_error(RFP4_E_NOT_INIT, "rfp4_init has not been called");
+    hipStream_t s;
+    int rc = hip_check(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate");
+    if (!rc) *stream = (rfp4_stream_t)s;
+    return rc;
+}
+
+int rfp4_stream_destroy(rfp4_stream_t stream) { return hip_check(hipStreamDestroy((hipStream_t)stream), "hipStreamDestroy"); }
+int rfp4_stream_synchronize(rfp4_stream_t stream)
+{
+    return hip_check(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
+}
+
+int rfp4_malloc(void **dptr, size_t bytes)
+{
+    if (!dptr || bytes == 0) return set_error(RFP4_E_INVALID, "rfp4_malloc: null out or zero size");
+    if (!g_rt) return set_error(RFP4_E_NOT_INIT, "rfp4_init has not been called");
+    return hip_check(hipMalloc(dptr, bytes), "hipMalloc");
+}
+
+int rfp4_free(void *dptr) { return dptr ? hip_check(hipFree(dptr), "hipFree") : RFP4_OK; }
+
+int rfp4_memset_zero(void *dptr, size_t bytes, rfp4_stream_t stream)
+{
+    if (!dptr) return set_error(RFP4_E_INVALID, "rfp4_memset_zero: null pointer");
+    if (bytes % 4) return set_error(RFP4_E_INVALID, "rfp4_memset_zero: %zu bytes is not a multiple of 4", bytes);
+    return fill_words((uint32_t *)dptr, bytes / 4, 0u, (hipStream_t)stream);
+}
+
+int rfp4_h2d(void *dst, const void *src, size_t bytes, rfp4_stream_t stream)
+{
+    if (!dst || !src) return set_error(RFP4_E_INVALID, "rfp4_h2d: null pointer");
+    return hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, (hipStream_t)stream), "hipMemcpyAsync H2D");
+}
+
+int rfp4_d2h(void *dst, const void *src, size_t bytes, rfp4_stream_t stream)
+{
+    if (!dst || !src) return set_error(RFP4_E_INVALID, "rfp4_d2h: null pointer");
+    int rc = hip_check(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, (hipStream_t)stream), "hipMemcpyAsync D2H");
+    if (rc) return rc;
+    return hip_check(hipStreamSynchronize((hipStream_t)stream), "hipStreamSynchronize");
+}
+
+int rfp4_event_create(rfp4_event_t *ev)
+{
+    if (!ev) return set_error(RFP4_E_INVALID, "null event out");
+    hipEvent_t e;
+    int rc = hip_check(hipEventCreate(&e), "hipEventCreate");
+    if (!rc) *ev = (rfp4_event_t)e;
+    return rc;
+}
+int rfp4_event_destroy(rfp4_event_t ev) { return hip_check(hipEventDestroy((hipEvent_t)ev), "hipEventDestroy"); }
+int rfp4_event_record(rfp4_event_t ev, rfp4_stream_t s)
+{
+    return hip_check(hipEventRecord((hipEvent_t)ev, (hipStream_t)s), "hipEventRecord");
+}
+int rfp4_event_synchronize(rfp4_event_t ev) { return hip_check(hipEventSynchronize((hipEvent_t)ev), "hipEventSynchronize"); }
+int rfp4_event_elapsed_ms(float *ms, rfp4_event_t a, rfp4_event_t b)
+{
+    if (!ms) return set_error(RFP4_E_INVALID, "null ms");
+    return hip_check(hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b), "hipEventElapsedTime");
+}
+
+} // extern "C"
+
+// ====================================================================== launchers
+namespace rfp4 {
+
+int fill_words(uint32_t *p, uint64_t n_words, uint32_t value, hipStream_t s)
+{
+    if (n_words == 0) return RFP4_OK;
+    FillArgs a{p, n_words, value, 0};
+    uint64_t blocks = (n_words + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    return launch("rfp4_fill", dim3((unsigned)blocks), dim3(256), s, &a);
+}
+
+static bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+int gemv_check(uint32_t n, uint32_t k, const void *w, const void *sc, const float *x, const float *y)
+{
+    if (!w || !sc || !x || !y) return set_error(RFP4_E_INVALID, "gemv: null pointer");
+    if (n == 0 || k == 0) return set_error(RFP4_E_SHAPE, "gemv: n=%u k=%u must be > 0", n, k);
+    if (k % 32) return set_error(RFP4_E_SHAPE, "gemv: k=%u is not a multiple of the 32-element block", k);
+    if (!aligned16(w) || !aligned16(x)) return set_error(RFP4_E_ALIGN, "gemv: w and x must be 16-byte aligned");
+    return RFP4_OK;
+}
+
+// Rows per wave: 4 by default; 8 for wide matrices where fewer, fuller
+// workgroups still fill the device.
+int gemv_rows_per_wave(uint32_t n_logical, int epi)
+{
+    (void)epi;
+    if (n_logical >= 64u * 1024u) return 8;
+    return 4;
+}
+
+int gemv_launch(const char *scale_name, int epi, const GemvArgs &args, hipStream_t s, int r_override)
+{
+    static const char *epi_names[] = {"store", "resid", "swiglu", "argmax"};
+    int R = r_override ? r_override : gemv_rows_per_wave(args.n, epi);
+    char name[64];
+    snprintf(name, sizeof name, "rfp4_gemv_%s_%s_r%d", scale_name, epi_names[epi], R);
+    uint32_t rows_per_block = 4u * (uint32_t)R;
+    uint32_t blocks = (args.n + rows_per_block - 1) / rows_per_block;
+    GemvArgs a = args;
+    return launch(name, dim3(blocks), dim3(256), s, &a);
+}
+
+uint32_t gemv_blocks(uint32_t n_logical, int epi, int r_override)
+{
+    int R = r_override ? r_override : gemv_rows_per_wave(n_logical, epi);
+    uint32_t rows_per_block = 4u * (uint32_t)R;
+    return (n_logical + rows_per_block - 1) / rows_per_block;
+}
+
+int attn_launch(const AttnArgs &args, int kv_f16, hipStream_t s, uint32_t max_seq_for_grid)
+{
+    const char *name;
+    if (args.head_dim == 64) name = kv_f16 ? "rfp4_attn_hd64_f16" : "rfp4_attn_hd64_f32";
+    else if (args.head_dim == 128) name = kv_f16 ? "rfp4_attn_hd128_f16" : "rfp4_attn_hd128_f32";
+    else return set_error(RFP4_E_SHAPE, "attn: head_dim %u unsupported (64 or 128)", args.head_dim);
+    uint32_t splits = (max_seq_for_grid + args.chunk - 1) / args.chunk;
+    AttnArgs a = args;
+    return launch(name, dim3(a.n_kv_heads, splits), dim3(256), s, &a);
+}
+
+uint32_t attn_chunk_for(uint32_t n_kv_heads, uint32_t seq, uint32_t num_cus)
+{
+    // Enough (kv head, split) workgroups to cover every CU about twice; the
+    // chunk is a power of two in [64, 256] tokens so that a cache allocated in
+    // whole 256-token pages always holds chunk * splits tokens.
+    uint32_t target_wg = 2u * num_cus;
+    uint32_t splits_wanted = (target_wg + n_kv_heads - 1) / n_kv_heads;
+    uint32_t chunk = 64u;
+    while (chunk < 256u && (uint64_t)chunk * splits_wanted < seq) chunk *= 2u;
+    return chunk;
+}
+
+} // namespace rfp4
+
+// ====================================================================== C-ABI kernels
+extern "C" {
+
+int fp4_gemv(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint32_t *w, const float *scales, const float *x,
+             float *y)
+{
+    int rc = gemv_check(n, k, w, scales, x, y);
+    if (rc) return rc;
+    GemvArgs a{w, scales, x, y, nullptr, n, k, 0, 0};
+    return gemv_launch("f32", RFP4_EPI_STORE, a, (hipStream_t)stream, 0);
+}
+
+int mx4_gemv(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_t *codes, const uint8_t *scales,
+             const float *x, float *y)
+{
+    int rc = gemv_check(n, k, codes, scales, x, y);
+    if (rc) return rc;
+    GemvArgs a{codes, scales, x, y, nullptr, n, k, 0, 0};
+    return gemv_launch("e8m0", RFP4_EPI_STORE, a, (hipStream_t)stream, 0);
+}
+
+int mx4_gemv_residual(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_t *codes, const uint8_t *scales,
+                      const float *x, float *x_res)
+{
+    int rc = gemv_check(n, k, codes, scales, x, x_res);
+    if (rc) return rc;
+    GemvArgs a{codes, scales, x, x_res, nullptr, n, k, 0, 0};
+    return gemv_launch("e8m0", RFP4_EPI_RESIDUAL, a, (hipStream_t)stream, 0);
+}
+
+int mx4_gemv_swiglu(rfp4_stream_t stream, uint32_t n, uint32_t k, uint32_t pair_off, const uint8_t *codes,
+                    const uint8_t *scales, const float *x, float *out)
+{
+    int rc = gemv_check(n, k, codes, scales, x, out);
+    if (rc) return rc;
+    if (pair_off < n) return set_error(RFP4_E_SHAPE, "gemv_swiglu: pair_off %u overlaps the %u gate rows", pair_off, n);
+    GemvArgs a{codes, scales, x, out, nullptr, n, k, pair_off, 0};
+    return gemv_launch("e8m0", RFP4_EPI_SWIGLU, a, (hipStream_t)stream, 0);
+}
+
+size_t mx4_gemv_argmax_workspace(uint32_t n) { return (size_t)gemv_blocks(n, RFP4_EPI_ARGMAX, 0) * 8u + 64u; }
+
+int mx4_gemv_argmax(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_t *codes, const uint8_t *scales,
+                    const float *x, float *y, void *workspace, uint32_t *best_token)
+{
+    int rc = gemv_check(n, k, codes, scales, x, y);
+    if (rc) return rc;
+    if (!workspace || !best_token) return set_error(RFP4_E_INVALID, "gemv_argmax: null workspace or output");
+    unsigned long long *best = (unsigned long long *)workspace;
+    GemvArgs a{codes, scales, x, y, best, n, k, 0, 0};
+    rc = gemv_launch("e8m0", RFP4_EPI_ARGMAX, a, (hipStream_t)stream, 0);
+    if (rc) return rc;
+    // reduce the per-workgroup keys with the step kernel on a scratch cursor
+    // that lives after the keys (no ids are written: ids_cap = 0).
+    uint32_t nb = gemv_blocks(n, RFP4_EPI_ARGMAX, 0);
+    StepState *st = (StepState *)((char *)workspace + (size_t)nb * 8u);
+    rc = fill_words((uint32_t *)st, sizeof(StepState) / 4, 0u, (hipStream_t)stream);
+    if (rc) return rc;
+    StepArgs sa{best, st, nullptr, best_token, nb, 0};
+    return launch("rfp4_step", dim3(1), dim3(1024), (hipStream_t)stream, &sa);
+}
+
+int rmsnorm(rfp4_stream_t stream, uint32_t dim, float eps, const float *x, const float *weight, float *y)
+{
+    if (!x || !weight || !y) return set_error(RFP4_E_INVALID, "rmsnorm: null pointer");
+    if (dim == 0) return set_error(RFP4_E_SHAPE, "rmsnorm: dim must be > 0");
+    RmsnormArgs a{x, weight, y, dim, eps};
+    return launch("rfp4_rmsnorm_f32w", dim3(1), dim3(1024), (hipStream_t)stream, &a);
+}
+
+int rmsnorm_f16w(rfp4_stream_t stream, uint32_t dim, float eps, const float *x, const uint16_t *weight, float *y)
+{
+    if (!x || !weight || !y) return set_error(RFP4_E_INVALID, "rmsnorm: null pointer");
+    if (dim == 0) return set_error(RFP4_E_SHAPE, "rmsnorm: dim must be > 0");
+    RmsnormArgs a{x, weight, y, dim, eps};
+    return launch("rfp4_rmsnorm_f16w", dim3(1), dim3(1024), (hipStream_t)stream, &a);
+}
+
+int rope(rfp4_stream_t stream, uint32_t num_heads, uint32_t head_dim, uint32_t cos_base, const float *cos_tab,
+         const float *sin_tab, float *q)
+{
+    if (!cos_tab || !sin_tab || !q) return set_error(RFP4_E_INVALID, "rope: null pointer");
+    if (head_dim == 0 || head_dim % 2) return set_error(RFP4_E_SHAPE, "rope: head_dim %u must be even", head_dim);
+    RopeArgs a{q, cos_tab, sin_tab, num_heads, head_dim, cos_base, 0};
+    uint32_t total = num_heads * (head_dim / 2);
+    return launch("rfp4_rope", dim3((total + 255) / 256), dim3(256), (hipStream_t)stream, &a);
+}
+
+int copy_into(rfp4_stream_t stream, uint32_t n, uint32_t off, const float *src, float *dst)
+{
+    if (!src || !dst) return set_error(RFP4_E_INVALID, "copy_into: null pointer");
+    CopyArgs a{src, dst, n, off};
+    return launch("rfp4_copy_into_f32", dim3((n + 255) / 256), dim3(256), (hipStream_t)stream, &a);
+}
+
+int kv_append_f16(rfp4_stream_t stream, uint32_t n, uint32_t off, const float *src, uint16_t *dst)
+{
+    if (!src || !dst) return set_error(RFP4_E_INVALID, "kv_append_f16: null pointer");
+    CopyArgs a{src, dst, n, off};
+    return launch("rfp4_copy_into_f16", dim3((n + 255) / 256), dim3(256), (hipStream_t)stream, &a);
+}
+
+static int attn_common(hipStream_t s, uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t seq, const float *q,
+                       const void *kc, const void *vc, uint64_t ts, uint64_t hs, float *out, int f16)
+{
+    Runtime *rt = runtime();
+    if (!rt) return set_error(RFP4_E_NOT_INIT, "rfp4_init has not been called");
+    if (!q || !kc || !vc || !out) return set_error(RFP4_E_INVALID, "attn_decode: null pointer");
+    if (nkv == 0 || nh == 0 || nh % nkv) return set_error(RFP4_E_SHAPE, "attn_decode: n_heads %u not a multiple of n_kv_heads %u", nh, nkv);
+    if (nh / nkv > 8) return set_error(RFP4_E_SHAPE, "attn_decode: GQA group %u > 8", nh / nkv);
+    if (seq == 0) return set_error(RFP4_E_SHAPE, "attn_decode: seq must be >= 1");
+    if (nh > kAttnMaxHeads) return set_error(RFP4_E_CAPACITY, "attn_decode: %u heads > %u", nh, kAttnMaxHeads);
+    uint32_t chunk = attn_chunk_for(nkv, seq, rt->num_cus);
+    uint32_t splits = (seq + chunk - 1) / chunk;
+    if (splits > kAttnMaxSplits) {
+        chunk = 256;
+        splits = (seq + chunk - 1) / chunk;
+        if (splits > kAttnMaxSplits) return set_error(RFP4_E_CAPACITY, "attn_decode: seq %u too long for the default workspace", seq);
+    }
+    AttnArgs a{};
+    a.q = q; a.kc = kc; a.vc = vc; a.out = out;
+    a.part = rt->attn_part; a.counters = rt->attn_counters; a.pos_ptr = nullptr;
+    a.ts = ts; a.hs = hs;
+    a.n_heads = nh; a.n_kv_heads = nkv; a.head_dim = hd; a.seq = seq;
+    a.chunk = chunk; a.max_splits = splits;
+    return attn_launch(a, f16, s, seq);
+}
+
+int attn_decode(rfp4_stream_t stream, uint32_t n_heads, uint32_t n_kv_heads, uint32_t seq, const float *q,
+                const float *kc, const float *vc, float *out)
+{
+    return attn_common((hipStream_t)stream, n_heads, n_kv_heads, 64, seq, q, kc, vc, (uint64_t)n_kv_heads * 64u, 64u,
+                       out, 0);
+}
+
+int attn_decode_f16(rfp4_stream_t stream, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim, uint32_t seq,
+                    const float *q, const uint16_t *kc, const uint16_t *vc, uint64_t token_stride,
+                    uint64_t head_stride, float *out)
+{
+    return attn_common((hipStream_t)stream, n_heads, n_kv_heads, head_dim, seq, q, kc, vc, token_stride, head_stride,
+                       out, 1);
+}
+
+int swiglu(rfp4_stream_t stream, uint32_t n, const float *gate, const float *up, float *out)
+{
+    if (!gate || !up || !out) return set_error(RFP4_E_INVALID, "swiglu: null pointer");
+    EltwiseArgs a{gate, up, out, n, 0};
+    return launch("rfp4_swiglu", dim3((n + 255) / 256), dim3(256), (hipStream_t)stream, &a);
+}
+
+int residual(rfp4_stream_t stream, uint32_t n, const float *y, float *x)
+{
+    if (!y || !x) return set_error(RFP4_E_INVALID, "residual: null pointer");
+    EltwiseArgs a{y, nullptr, x, n, 0};
+    return launch("rfp4_residual", dim3((n + 255) / 256), dim3(256), (hipStream_t)stream, &a);
+}
+
+int argmax(rfp4_stream_t stream, uint32_t n, const float *logits, uint32_t *out)
+{
+    if (!logits || !out) return set_error(RFP4_E_INVALID, "argmax: null pointer");
+    ArgmaxArgs a{logits, out, n, 0};
+    return launch("rfp4_argmax", dim3(1), dim3(1024), (hipStream_t)stream, &a);
+}
+
+int fp4_mma_allones(rfp4_stream_t stream, float *out)
+{
+    if (!out) return set_error(RFP4_E_INVALID, "fp4_mma_allones: null pointer");
+    MmaTileArgs a{nullptr, nullptr, nullptr, nullptr, out, 0, 0};
+    return launch("rfp4_mma_allones", dim3(1), dim3(64), (hipStream_t)stream, &a);
+}
+
+int mx4_quantize(rfp4_stream_t stream, uint64_t rows, uint64_t k, const void *src, int src_is_bf16, uint8_t *codes,
+                 uint8_t *scales)
+{
+    if (!src || !codes || !scales) return set_error(RFP4_E_INVALID, "mx4_quantize: null pointer");
+    if (k == 0 || k % 32) return set_error(RFP4_E_SHAPE, "mx4_quantize: k=%llu not a multiple of 32", (unsigned long long)k);
+    if (((uintptr_t)codes & 15u) != 0) return set_error(RFP4_E_ALIGN, "mx4_quantize: codes must be 16-byte aligned");
+    QuantMxArgs a{src, codes, scales, rows, k};
+    uint64_t blocks = (rows * (k / 32) + 255) / 256;
+    if (blocks > 65536) blocks = 65536;
+    return launch(src_is_bf16 ? "rfp4_quant_mx_bf16" : "rfp4_quant_mx_f32", dim3((unsigned)blocks), dim3(256),
+                  (hipStream_t)stream, &a);
+}
+
+int rfp4_mma_tile16(rfp4_stream_t stream, const uint32_t *a, const uint32_t *b, const uint32_t *sa,
+                    const uint32_t *sb, float *out)
+{
+    if (!a || !b || !sa || !sb || !out) return set_error(RFP4_E_INVALID, "mma_tile16: null pointer");
+    MmaTileArgs args{a, b, sa, sb, out, 0, 0};
+    return launch("rfp4_mma16_tile", dim3(1), dim3(64), (hipStream_t)stream, &args);
+}
+
+int rfp4_mma_tile32(rfp4_stream_t stream, const uint32_t *a, const uint32_t *b, const uint32_t *sa,
+                    const uint32_t *sb, float *out)
+{
+    if (!a || !b || !sa || !sb || !out) return set_error(RFP4_E_INVALID, "mma_tile32: null pointer");
+    MmaTileArgs args{a, b, sa, sb, out, 0, 0};
+    return launch("rfp4_mma32_tile", dim3(1), dim3(64), (hipStream_t)stream, &args);
+}
+
+int rfp4_selftest_cvt_fp4(rfp4_stream_t stream, uint32_t n, const uint32_t *words, float *out)
+{
+    if (!words || !out) return set_error(RFP4_E_INVALID, "selftest_cvt: null pointer");
+    SelftestArgs a{words, out, n, 0};
+    return launch("rfp4_selftest_cvt", dim3((n + 255) / 256), dim3(256), (hipStream_t)stream, &a);
+}
+
+int rfp4_synth_mx_weight(rfp4_stream_t stream, uint64_t seed, uint64_t stream_id, float sigma, uint64_t k, uint64_t r0,
+                         uint64_t nrows, uint8_t *codes, uint8_t *scales)
+{
+    if (!codes || !scales) return set_error(RFP4_E_INVALID, "synth_mx_weight: null pointer");
+    if (k == 0 || k % 32) return set_error(RFP4_E_SHAPE, "synth_mx_weight: k not a multiple of 32");
+    if (((uintptr_t)codes & 15u) != 0) return set_error(RFP4_E_ALIGN, "synth_mx_weight: codes must be 16-byte aligned");
+    SynthWeightArgs a{codes, scales, seed, stream_id, r0, nrows, k, ih4_coef(sigma), 0};
+    uint64_t blocks = (nrows * (k / 32) + 255) / 256;
+    if (blocks > 262144) blocks = 262144;
+    return launch("rfp4_synth_weight", dim3((unsigned)blocks), dim3(256), (hipStream_t)stream, &a);
+}
+
+int rfp4_synth_f16(rfp4_stream_t stream, uint64_t seed, uint64_t stream_id, float sigma, float offset, uint64_t n,
+                   uint16_t *out)
+{
+    if (!out) return set_error(RFP4_E_INVALID, "synth_f16: null pointer");
+    SynthF16Args a{out, seed, stream_id, n, ih4_coef(sigma), offset};
+    uint64_t blocks = (n + 255) / 256;
+    if (blocks > 262144) blocks = 262144;
+    return launch("rfp4_synth_f16", dim3((unsigned)blocks), dim3(256), (hipStream_t)stream, &a);
+}
+
+} // extern "C"

@@ -1,0 +1,178 @@
+// Kernel argument blocks, passed by value as the single kernel parameter.
+// Shared verbatim by the host launcher (g++) and the device code (hipcc), so
+// only plain C types appear here.
+#pragma once
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+// GEMV epilogues.
+enum {
+    RFP4_EPI_STORE = 0,   // y[r] = acc
+    RFP4_EPI_RESIDUAL = 1, // y[r] += acc  (residual stream update)
+    RFP4_EPI_SWIGLU = 2,  // y[r] = silu(acc(gate row r)) * acc(up row r + pair_off)
+    RFP4_EPI_ARGMAX = 3,  // y[r] = acc, plus one packed (max, argmin-index) per workgroup
+};
+
+typedef struct GemvArgs {
+    const void *w;        // codes, row-major, K/2 bytes per row (== reference u32 words)
+    const void *scales;   // E8M0 bytes or f32, row-major, K/32 per row
+    const float *x;       // activation, K floats
+    float *y;             // output (see epilogue)
+    unsigned long long *best; // ARGMAX: one packed key per workgroup
+    uint32_t n;           // logical output rows
+    uint32_t k;           // reduction length, multiple of 32
+    uint32_t pair_off;    // SWIGLU: physical row offset of the up rows
+    uint32_t pad;
+} GemvArgs;
+
+typedef struct RmsnormArgs {
+    const float *x;
+    const void *w;        // f32 or f16 weights
+    float *y;
+    uint32_t dim;
+    float eps;
+} RmsnormArgs;
+
+typedef struct RopeArgs {
+    float *q;             // [num_heads][head_dim], rotated in place
+    const float *cosv;    // table [pos][head_dim/2]
+    const float *sinv;
+    uint32_t num_heads, head_dim, cos_base;
+    uint32_t pad;
+} RopeArgs;
+
+// Fused per-token q/k rotation and fp16 KV append for the engine.
+typedef struct RopeAppendArgs {
+    float *qkv;           // [q: nh*hd][k: nkv*hd][v: nkv*hd]
+    const float *cosv, *sinv;
+    uint16_t *kcache, *vcache; // [kvh][max_seq][hd] fp16
+    const int32_t *pos_ptr;
+    uint32_t n_heads, n_kv_heads, head_dim, max_seq;
+} RopeAppendArgs;
+
+typedef struct CopyArgs {
+    const float *src;
+    void *dst;
+    uint32_t n, off;
+} CopyArgs;
+
+typedef struct EltwiseArgs {
+    const float *a, *b;
+    float *out;
+    uint32_t n, pad;
+} EltwiseArgs;
+
+typedef struct ArgmaxArgs {
+    const float *logits;
+    uint32_t *out;
+    uint32_t n, pad;
+} ArgmaxArgs;
+
+// Split-K flash-decode attention.
+typedef struct AttnArgs {
+    const float *q;       // [n_heads][head_dim]
+    const void *kc, *vc;  // element (t, kvh, d) at t*ts + kvh*hs + d
+    float *out;           // [n_heads][head_dim]
+    float *part;          // workspace: [n_heads][max_splits][head_dim + 2]
+    uint32_t *counters;   // workspace: [n_kv_heads], zero between calls
+    const int32_t *pos_ptr; // if non-null, seq = *pos_ptr + 1
+    uint64_t ts, hs;      // token and head strides (elements)
+    uint32_t n_heads, n_kv_heads, head_dim, seq;
+    uint32_t chunk, max_splits;
+} AttnArgs;
+
+typedef struct FillArgs {
+    uint32_t *p;
+    uint64_t n_words;
+    uint32_t value, pad;
+} FillArgs;
+
+// Synthetic MXFP4 weight rows [r0, r0+nrows) of a K-wide matrix.
+typedef struct SynthWeightArgs {
+    uint8_t *packed;      // nrows * K/2
+    uint8_t *scales;      // nrows * K/32
+    uint64_t seed, stream;
+    uint64_t r0, nrows, k;
+    float coef;
+    uint32_t pad;
+} SynthWeightArgs;
+
+// Synthetic fp16 tensor: f16(offset + N*coef) over index i in [0, n).
+typedef struct SynthF16Args {
+    uint16_t *out;
+    uint64_t seed, stream, n;
+    float coef, offset;
+} SynthF16Args;
+
+// Synthetic KV prefill: positions [0, upto) of [kvh][max_seq][hd] fp16 caches.
+typedef struct SynthKvArgs {
+    uint16_t *cache;
+    uint64_t seed, stream;
+    uint32_t upto, n_kv_heads, head_dim, max_seq;
+    float coef, pad;
+} SynthKvArgs;
+
+// OCP MX quantization of f32 (or bf16) rows into codes + E8M0.
+typedef struct QuantMxArgs {
+    const void *src;      // f32 or bf16, rows x K
+    uint8_t *packed, *scales;
+    uint64_t rows, k;
+} QuantMxArgs;
+
+// Device-resident decode cursor: lets one captured step graph replay for
+// every token.  pos = absolute position, step = index into ids[].
+typedef struct StepState {
+    int32_t pos;
+    int32_t step;
+    uint32_t n_prompt;    // ids[0, n_prompt) are prompt tokens
+    uint32_t ids_cap;     // capacity of ids[]
+} StepState;
+
+// Embedding gather: x[i] = f16(embed[ids[state->step]][i]).
+typedef struct EmbedArgs {
+    const uint16_t *embed;
+    const uint32_t *ids;
+    const StepState *state;
+    float *x;
+    uint32_t dim, vocab;
+} EmbedArgs;
+
+// End-of-step bookkeeping for on-device greedy decode: reduce the LM head's
+// per-workgroup keys, record the token, advance the cursor.
+typedef struct StepArgs {
+    const unsigned long long *best;
+    StepState *state;
+    uint32_t *ids;
+    uint32_t *last_tok;
+    uint32_t n_best, pad;
+} StepArgs;
+
+// Scaled-MFMA MXFP4 GEMM: C[M][N] = A[M][K] * W[N][K]^T, both MXFP4 (E2M1 +
+// E8M0 per 32 along K), f32 output.
+typedef struct GemmArgs {
+    const uint8_t *a_codes, *a_scales;
+    const uint8_t *w_codes, *w_scales;
+    float *c;
+    uint32_t m, n, k, pad;
+} GemmArgs;
+
+typedef struct MmaTileArgs {
+    const uint32_t *a;    // per-lane A registers
+    const uint32_t *b;
+    const uint32_t *sa, *sb;
+    float *out;
+    uint32_t mode, pad;
+} MmaTileArgs;
+
+typedef struct SelftestArgs {
+    const uint32_t *in;
+    float *out;
+    uint32_t n, pad;
+} SelftestArgs;
+
+#ifdef __cplusplus
+}
+#endif

@@ -1,0 +1,119 @@
+"""End-to-end parity of the decode engine against the CPU oracle decode loop
+on the same packed weights and seeds (greedy tokens identical over the test
+horizon; llama_run/src/main.rs:492-570 is the loop both restate)."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TINY = dict(dim=256, n_layers=2, n_heads=4, n_kv_heads=2, head_dim=64, ffn=512, vocab=1024,
+            theta=10000.0, eps=1e-5, max_seq=64)
+TINY128 = dict(dim=512, n_layers=2, n_heads=8, n_kv_heads=2, head_dim=128, ffn=1024, vocab=2048,
+               theta=500000.0, eps=1e-5, max_seq=300)
+
+
+def _engine(rf, cfg, seed):
+    c = {k: v for k, v in cfg.items() if k != "max_seq"}
+    return rf.Engine(rf.model_config(max_seq=cfg["max_seq"], **c), seed)
+
+
+def _proj_rows(cfg, p):
+    qd, kvd = cfg["n_heads"] * cfg["head_dim"], cfg["n_kv_heads"] * cfg["head_dim"]
+    return [(qd, cfg["dim"]), (kvd, cfg["dim"]), (kvd, cfg["dim"]), (cfg["dim"], qd),
+            (cfg["ffn"], cfg["dim"]), (cfg["ffn"], cfg["dim"]), (cfg["dim"], cfg["ffn"])][p]
+
+
+@pytest.mark.parametrize("cfg", [TINY, TINY128])
+def test_engine_weights_bit_exact(rf, orc, cfg):
+    seed = 0x5EED
+    eng = _engine(rf, cfg, seed)
+    ref = orc.Model(cfg, seed)
+    for layer in range(cfg["n_layers"]):
+        for p in range(7):
+            c, s = eng.weight_host(layer, p)
+            np.testing.assert_array_equal(c, ref.codes(layer, p), err_msg=f"codes l{layer} p{p}")
+            np.testing.assert_array_equal(s, ref.scales(layer, p), err_msg=f"scales l{layer} p{p}")
+    c, s = eng.weight_host(-1, 0)
+    np.testing.assert_array_equal(c, ref.codes(-1, 0))
+    np.testing.assert_array_equal(s, ref.scales(-1, 0))
+    eng.close()
+
+
+@pytest.mark.parametrize("cfg", [TINY, TINY128])
+def test_engine_tokens_match_oracle(rf, orc, cfg):
+    seed = 0x5EED
+    eng = _engine(rf, cfg, seed)
+    ref = orc.Model(cfg, seed)
+    prompt = [1, 7, 42, 99, 5]
+    n_new = 24
+    gpu = eng.generate(prompt, 0, n_new)
+    cpu, margins = ref.generate(prompt, 0, n_new)
+    assert list(gpu) == list(cpu), f"gpu {list(gpu)}\ncpu {list(cpu)}\nmargins {margins}"
+    # KV cache after the run: fp16 K/V equal to the oracle's for written positions
+    hd, nkv = cfg["head_dim"], cfg["n_kv_heads"]
+    npos = len(prompt) + n_new - 1
+    for layer in range(cfg["n_layers"]):
+        k, v = eng.kv_host(layer)
+        stride = k.size // (nkv * hd)
+        kg = k.reshape(nkv, stride, hd)[:, :npos].astype(np.uint16).view(np.float16).astype(np.float32)
+        kr = ref.kcache(layer).reshape(nkv, cfg["max_seq"], hd)[:, :npos].view(np.float16).astype(np.float32)
+        assert np.max(np.abs(kg - kr)) <= 2e-3 * max(1.0, np.abs(kr).max())
+    eng.close()
+
+
+def test_engine_graph_equals_eager(rf, orc):
+    seed = 0xABC
+    eng = _engine(rf, TINY, seed)
+    prompt = [3, 1, 4, 1, 5, 9]
+    g = eng.generate(prompt, 0, 12)
+    lg = eng.logits()
+    eng.use_graph(False)
+    e = eng.generate(prompt, 0, 12)
+    le = eng.logits()
+    assert list(g) == list(e)
+    np.testing.assert_array_equal(lg, le)
+    eng.close()
+
+
+def test_decode_step_matches_generate(rf, orc):
+    """llama_decode_step (one blocking forward) equals the on-device loop."""
+    seed = 0x77
+    eng = _engine(rf, TINY, seed)
+    ref = orc.Model(TINY, seed)
+    toks = [11, 22, 33]
+    for pos, t in enumerate(toks):
+        nxt = eng.decode_step(t, pos)
+        assert nxt == ref.step(t, pos)
+    eng.close()
+
+
+def test_engine_errors(rf):
+    eng = _engine(rf, TINY, 1)
+    with pytest.raises(rf.Rfp4Error) as e:
+        eng.generate([1, 2], TINY["max_seq"] - 1, 4)  # would run past max_seq
+    assert e.value.code == -4
+    with pytest.raises(rf.Rfp4Error):
+        eng.generate([TINY["vocab"]], 0, 1)             # token out of range
+    eng.close()
+
+
+TINYLLAMA = dict(dim=2048, n_layers=22, n_heads=32, n_kv_heads=4, head_dim=64, ffn=5632, vocab=32000,
+                 theta=10000.0, eps=1e-5, max_seq=272)
+
+
+@pytest.mark.slow
+def test_tinyllama_config3_tokens(rf, orc):
+    """TinyLlama-1.1B architecture, random MXFP4 weights,
+    16-token random prompt, greedy decode; tokens identical to the oracle."""
+    seed = 0x11B
+    n_new = 256
+    r, _ = orc.xorshift32(0xC0DE, 16)
+    prompt = (r % TINYLLAMA["vocab"]).astype(np.uint32)
+    eng = _engine(rf, TINYLLAMA, seed)
+    gpu = eng.generate(prompt, 0, n_new)
+    eng.close()
+    ref = orc.Model(TINYLLAMA, seed)
+    cpu, margins = ref.generate(prompt, 0, n_new)
+    ref.close()
+    mism = np.nonzero(gpu != cpu)[0]
+    assert mism.size == 0, f"first mismatch at {mism[0]}: margin there {margins[mism[0]]:.3e}"

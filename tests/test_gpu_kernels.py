@@ -1,0 +1,385 @@
+"""GPU parity of the individual kernels against the CPU oracle (gfx950).
+
+Each test mirrors one of the reference's self-checking examples: seeded inputs,
+the oracle's CPU result, the kernel through the C ABI, and an error bound.
+"""
+import numpy as np
+import pytest
+
+from conftest import reference_rel_err
+
+pytestmark = pytest.mark.gpu
+
+FP4V = np.array([0, 0.5, 1, 1.5, 2, 3, 4, 6], dtype=np.float32)
+
+
+def _dev(rf, arr, s):
+    return rf.DeviceBuffer.from_host(np.ascontiguousarray(arr), s)
+
+
+# ---------------------------------------------------------------- codec
+def test_hw_fp4_conversion_matches_codec(rf, orc, stream):
+    """v_cvt_scalef32_pk_f32_fp4 (scale 1.0) against the E2M1 table for every
+    byte value: byte b of a word -> (low nibble, high nibble)."""
+    words = np.arange(256, dtype=np.uint32)
+    words = words | (words << 8) | (words << 16) | (words << 24)
+    dw = _dev(rf, words, stream)
+    out = rf.DeviceBuffer.zeroed(256 * 8, np.float32, stream)
+    rf.selftest_cvt_fp4(stream, 256, dw, out)
+    got = out.to_host(256 * 8, np.float32, stream).reshape(256, 4, 2)
+    lo = np.array([orc.lib().orc_e2m1_decode(b & 0xF) for b in range(256)], np.float32)
+    hi = np.array([orc.lib().orc_e2m1_decode(b >> 4) for b in range(256)], np.float32)
+    for sel in range(4):
+        np.testing.assert_array_equal(got[:, sel, 0], lo)
+        np.testing.assert_array_equal(got[:, sel, 1], hi)
+
+
+# ---------------------------------------------------------------- GEMV
+def _config1(orc, n=2048, k=2048, seed=0x12345678):
+    """uniform codes, E8M0 exponents in [-6, 2], x ~ N(0,1)."""
+    words, st = orc.xorshift32(seed, n * k // 8)
+    codes = words.view(np.uint8).copy()
+    r, st = orc.xorshift32(st, n * k // 32)
+    scales = (127 - 6 + (r % 9)).astype(np.uint8)
+    r2, st = orc.xorshift32(st, 2 * k)
+    u = r2.astype(np.uint64).reshape(k, 2)
+    x = np.array([orc.ih4_normal_from_u64(int((a << 32) | b), 1.0) for a, b in u], dtype=np.float32)
+    return codes, scales, x
+
+
+@pytest.mark.parametrize("n,k", [(2048, 2048), (4096, 4096), (1024, 14336), (300, 5632), (7, 96), (1, 32)])
+def test_mx4_gemv_parity(rf, orc, stream, n, k):
+    codes, scales, x = _config1(orc, n, k)
+    dc, ds, dx = _dev(rf, codes, stream), _dev(rf, scales, stream), _dev(rf, x, stream)
+    dy = rf.DeviceBuffer.zeroed(n, np.float32, stream)
+    rf.mx4_gemv(stream, n, k, dc, ds, dx, dy)
+    y = dy.to_host(n, np.float32, stream)
+    yref = orc.gemv_e8m0(n, k, codes, scales, x)
+    y64, absy = orc.gemv_e8m0_f64(n, k, codes, scales, x)
+    # condition-aware bound against the f64 sum, and the reference's metric at 1e-3
+    cond = np.abs(y.astype(np.float64) - y64) / np.maximum(absy, 1e-300)
+    assert cond.max() < 1e-5, f"max |y-y64|/sum|wx| = {cond.max():.3e}"
+    rel = reference_rel_err(y, yref)
+    assert (rel > 1e-3).sum() == 0, f"{(rel > 1e-3).sum()} rows over 1e-3, max {rel.max():.3e}"
+
+
+def test_fp4_gemv_reference_harness(rf, orc, stream):
+    """Replay of fp4_gemv/src/main.rs:96-175: 4096x4096, seed 0x12345678, f32
+    scales 0.5 + (r%8)*0.25, x = ((r%17)-8)*0.1, bad if rel > 1e-2."""
+    N = K = 4096
+    st = 0x12345678
+    r, st = orc.xorshift32(st, N * K)
+    codes = (r & 0xF).astype(np.uint8)
+    w = orc.pack(codes).view(np.uint32)
+    r, st = orc.xorshift32(st, N * K // 32)
+    scales = (0.5 + (r % 8).astype(np.float32) * 0.25).astype(np.float32)
+    r, st = orc.xorshift32(st, K)
+    x = (((r % 17).astype(np.float32) - 8.0) * 0.1).astype(np.float32)
+    yref = orc.gemv_f32scale(N, K, w, scales, x)
+    dw, ds, dx = _dev(rf, w, stream), _dev(rf, scales, stream), _dev(rf, x, stream)
+    dy = rf.DeviceBuffer.zeroed(N, np.float32, stream)
+    rf.fp4_gemv(stream, N, K, dw, ds, dx, dy)
+    y = dy.to_host(N, np.float32, stream)
+    rel = reference_rel_err(y, yref)
+    assert (rel > 1e-2).sum() == 0
+    assert rel.max() < 1e-3, rel.max()
+
+
+def test_gemv_one_hot_selects_column(rf, orc, stream):
+    n, k = 256, 1024
+    codes, scales, _ = _config1(orc, n, k, seed=99)
+    dc, ds = _dev(rf, codes, stream), _dev(rf, scales, stream)
+    dy = rf.DeviceBuffer.zeroed(n, np.float32, stream)
+    allc = orc.unpack(codes).reshape(n, k)
+    for col in (0, 31, 32, 517, k - 1):
+        x = np.zeros(k, np.float32)
+        x[col] = 1.0
+        rf.mx4_gemv(stream, n, k, dc, ds, _dev(rf, x, stream), dy)
+        y = dy.to_host(n, np.float32, stream)
+        expect = np.array([orc.lib().orc_e2m1_decode(int(c)) for c in allc[:, col]], np.float32) * \
+            np.array([orc.lib().orc_e8m0_decode(int(s)) for s in scales.reshape(n, k // 32)[:, col // 32]], np.float32)
+        np.testing.assert_array_equal(y, expect)
+
+
+def test_gemv_epilogues(rf, orc, stream):
+    k, n = 2048, 512
+    codes, scales, x = _config1(orc, 2 * n, k, seed=7)
+    dc, ds, dx = _dev(rf, codes, stream), _dev(rf, scales, stream), _dev(rf, x, stream)
+    full = orc.gemv_e8m0(2 * n, k, codes, scales, x)
+    # swiglu: gate rows [0,n), up rows [n, 2n)
+    dout = rf.DeviceBuffer.zeroed(n, np.float32, stream)
+    rf.mx4_gemv_swiglu(stream, n, k, n, dc, ds, dx, dout)
+    got = dout.to_host(n, np.float32, stream)
+    ref = orc.swiglu(full[:n], full[n:])
+    assert reference_rel_err(got, ref).max() < 1e-3
+    # residual: x_res += W x
+    base = np.linspace(-1, 1, 2 * n).astype(np.float32)
+    dres = _dev(rf, base, stream)
+    rf.mx4_gemv_residual(stream, 2 * n, k, dc, ds, dx, dres)
+    got = dres.to_host(2 * n, np.float32, stream)
+    assert reference_rel_err(got, orc.residual(full, base)).max() < 1e-3
+    # argmax (ties -> lowest index)
+    ws = rf.DeviceBuffer(rf.mx4_gemv_argmax_workspace(2 * n))
+    dbest = rf.DeviceBuffer.zeroed(1, np.uint32, stream)
+    dy = rf.DeviceBuffer.zeroed(2 * n, np.float32, stream)
+    rf.mx4_gemv_argmax(stream, 2 * n, k, dc, ds, dx, dy, ws, dbest)
+    y = dy.to_host(2 * n, np.float32, stream)
+    assert int(dbest.to_host(1, np.uint32, stream)[0]) == orc.argmax(y)
+    assert reference_rel_err(y, full).max() < 1e-3
+
+
+# ---------------------------------------------------------------- norm / rope / attention
+def test_rmsnorm_reference_harness(rf, orc, stream):
+    """llama_rmsnorm/src/main.rs:59-116: seed 0x9e3779b9, dim 2048, rel > 1e-4 is bad."""
+    DIM, EPS = 2048, 1e-5
+    r, st = orc.xorshift32(0x9E3779B9, DIM)
+    x = (((r % 2001).astype(np.float32) - 1000.0) / 500.0).astype(np.float32)
+    r, st = orc.xorshift32(st, DIM)
+    w = (0.5 + (r % 1000).astype(np.float32) / 1000.0).astype(np.float32)
+    yref = orc.rmsnorm(x, w, EPS)
+    dx, dw = _dev(rf, x, stream), _dev(rf, w, stream)
+    dy = rf.DeviceBuffer.zeroed(DIM, np.float32, stream)
+    rf.rmsnorm(stream, DIM, EPS, dx, dw, dy)
+    assert reference_rel_err(dy.to_host(DIM, np.float32, stream), yref).max() < 1e-5
+
+
+@pytest.mark.parametrize("dim", [2048, 4096, 100])
+def test_rmsnorm_f16_weights(rf, orc, stream, dim):
+    rng = np.random.default_rng(dim)
+    x = rng.standard_normal(dim).astype(np.float32)
+    w16 = (1 + 0.02 * rng.standard_normal(dim)).astype(np.float16)
+    yref = orc.rmsnorm(x, w16.astype(np.float32), 1e-5)
+    dy = rf.DeviceBuffer.zeroed(dim, np.float32, stream)
+    rf.rmsnorm_f16w(stream, dim, 1e-5, _dev(rf, x, stream), _dev(rf, w16.view(np.uint16), stream), dy)
+    assert reference_rel_err(dy.to_host(dim, np.float32, stream), yref).max() < 1e-5
+
+
+@pytest.mark.parametrize("heads,hd,theta,pos", [(32, 64, 500000.0, 37), (32, 64, 10000.0, 2047), (8, 128, 500000.0, 4100)])
+def test_rope_parity(rf, orc, stream, heads, hd, theta, pos):
+    """llama_rope/src/main.rs:46-124 (seed 0x13579bdf) over the engine's table."""
+    r, _ = orc.xorshift32(0x13579BDF, heads * hd)
+    q = (((r % 2001).astype(np.float32) - 1000.0) / 500.0).astype(np.float32)
+    cos_t, sin_t = orc.rope_table(pos + 1, hd, theta)
+    half = hd // 2
+    qref = orc.rope(q, heads, hd, cos_t[pos * half:(pos + 1) * half], sin_t[pos * half:(pos + 1) * half])
+    dq = _dev(rf, q, stream)
+    rf.rope(stream, heads, hd, pos * half, _dev(rf, cos_t, stream), _dev(rf, sin_t, stream), dq)
+    got = dq.to_host(heads * hd, np.float32, stream)
+    np.testing.assert_array_equal(got, qref)  # no fused multiply-add: bit-identical
+
+
+def test_attn_decode_reference_harness(rf, orc, stream):
+    """llama_attn_decode/src/main.rs:132-221: 32q/8kv, hd 64, seq 512, seed 0xabcd1234, f32 KV."""
+    NH, NKV, HD, SEQ = 32, 8, 64, 512
+    r, _ = orc.xorshift32(0xABCD1234, NH * HD + 2 * SEQ * NKV * HD)
+    vals = (((r % 2001).astype(np.float32) - 1000.0) / 700.0).astype(np.float32)
+    q = vals[:NH * HD]
+    kc = vals[NH * HD:NH * HD + SEQ * NKV * HD]
+    vc = vals[NH * HD + SEQ * NKV * HD:]
+    oref = orc.attn_decode(NH, NKV, HD, SEQ, q, kc, vc, NKV * HD, HD)
+    dout = rf.DeviceBuffer.zeroed(NH * HD, np.float32, stream)
+    rf.attn_decode(stream, NH, NKV, SEQ, _dev(rf, q, stream), _dev(rf, kc, stream), _dev(rf, vc, stream), dout)
+    got = dout.to_host(NH * HD, np.float32, stream)
+    rel = reference_rel_err(got, oref)
+    assert (rel > 1e-4).sum() == 0, rel.max()
+
+
+@pytest.mark.parametrize("nh,nkv,hd,seq", [(32, 4, 64, 512), (32, 4, 64, 2048), (32, 8, 128, 4097), (32, 8, 128, 1),
+                                           (32, 8, 128, 300), (16, 16, 64, 65)])
+def test_attn_decode_f16_parity(rf, orc, stream, nh, nkv, hd, seq):
+    """BASELINE config 2 attention: fp16 KV ~ N(0,1), head-major [kvh][t][hd]."""
+    rng = np.random.default_rng(seq * 7 + hd)
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    cap = seq + 5
+    kc = rng.standard_normal(nkv * cap * hd).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal(nkv * cap * hd).astype(np.float16).view(np.uint16)
+    oref = orc.attn_decode(nh, nkv, hd, seq, q, kc, vc, hd, cap * hd)
+    dout = rf.DeviceBuffer.zeroed(nh * hd, np.float32, stream)
+    rf.attn_decode_f16(stream, nh, nkv, hd, seq, _dev(rf, q, stream), _dev(rf, kc, stream), _dev(rf, vc, stream),
+                       hd, cap * hd, dout)
+    got = dout.to_host(nh * hd, np.float32, stream)
+    rel = reference_rel_err(got, oref)
+    assert (rel > 1e-4).sum() == 0, rel.max()
+
+
+def test_swiglu_residual_copy(rf, orc, stream):
+    rng = np.random.default_rng(3)
+    n = 5632
+    g = (3 * rng.standard_normal(n)).astype(np.float32)
+    u = rng.standard_normal(n).astype(np.float32)
+    dout = rf.DeviceBuffer.zeroed(n, np.float32, stream)
+    rf.swiglu(stream, n, _dev(rf, g, stream), _dev(rf, u, stream), dout)
+    got = dout.to_host(n, np.float32, stream)
+    assert reference_rel_err(got, orc.swiglu(g, u)).max() < 2e-6
+    x = rng.standard_normal(n).astype(np.float32)
+    dx = _dev(rf, x, stream)
+    rf.residual(stream, n, _dev(rf, u, stream), dx)
+    np.testing.assert_array_equal(dx.to_host(n, np.float32, stream), orc.residual(u, x))
+    dst = rf.DeviceBuffer.zeroed(3 * n, np.float32, stream)
+    rf.copy_into(stream, n, n, _dev(rf, x, stream), dst)
+    got = dst.to_host(3 * n, np.float32, stream)
+    np.testing.assert_array_equal(got[n:2 * n], x)
+    assert not got[:n].any() and not got[2 * n:].any()
+    d16 = rf.DeviceBuffer.zeroed(2 * n, np.uint16, stream)
+    rf.kv_append_f16(stream, n, n, _dev(rf, x, stream), d16)
+    np.testing.assert_array_equal(d16.to_host(2 * n, np.uint16, stream)[n:], x.astype(np.float16).view(np.uint16))
+
+
+@pytest.mark.parametrize("n", [32000, 128256, 5])
+def test_argmax_ties_lowest(rf, orc, stream, n):
+    rng = np.random.default_rng(n)
+    v = rng.standard_normal(n).astype(np.float32)
+    v[n // 3] = 9.0
+    v[n // 2] = 9.0  # tie: lowest index wins
+    out = rf.DeviceBuffer.zeroed(1, np.uint32, stream)
+    rf.argmax(stream, n, _dev(rf, v, stream), out)
+    got = int(out.to_host(1, np.uint32, stream)[0])
+    assert got == orc.argmax(v) == n // 3
+
+
+# ---------------------------------------------------------------- synthetic init / quantizer bit-exactness
+@pytest.mark.parametrize("k,rows", [(2048, 96), (4096, 33), (14336, 8)])
+def test_synth_weight_bit_exact(rf, orc, stream, k, rows):
+    seed, sid = 0xC0FFEE, (3 << 8) | 5
+    c_ref, s_ref = orc.synth_mx_weight(seed, sid, 0.02, k, 17, rows)
+    dc = rf.DeviceBuffer(rows * k // 2)
+    ds = rf.DeviceBuffer(rows * k // 32)
+    rf.synth_mx_weight(stream, seed, sid, 0.02, k, 17, rows, dc, ds)
+    np.testing.assert_array_equal(dc.to_host(rows * k // 2, np.uint8, stream), c_ref)
+    np.testing.assert_array_equal(ds.to_host(rows * k // 32, np.uint8, stream), s_ref)
+
+
+def test_synth_f16_bit_exact(rf, orc, stream):
+    n = 1 << 16
+    ref = orc.synth_f16(11, 0xE0000, 0.02, 1.0, n)
+    d = rf.DeviceBuffer.zeroed(n, np.uint16, stream)
+    rf.synth_f16(stream, 11, 0xE0000, 0.02, 1.0, n, d)
+    np.testing.assert_array_equal(d.to_host(n, np.uint16, stream), ref)
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_quantize_bit_exact(rf, orc, stream, bf16):
+    rng = np.random.default_rng(5)
+    rows, k = 64, 512
+    w = (rng.standard_normal((rows, k)) * np.exp(rng.uniform(-20, 20, (rows, 1)))).astype(np.float32)
+    w[3, :32] = 0.0                      # all-zero block
+    w[4, :32] = np.float32(-0.0)
+    w[5, 5] = 1e-41                      # subnormal
+    if bf16:
+        src = (w.view(np.uint32) >> 16).astype(np.uint16)
+        w = (src.astype(np.uint32) << 16).view(np.float32).reshape(rows, k)
+    else:
+        src = w
+    c_ref, s_ref = orc.quant_mx(w)
+    dc = rf.DeviceBuffer(rows * k // 2)
+    ds = rf.DeviceBuffer(rows * k // 32)
+    rf.mx4_quantize(stream, rows, k, _dev(rf, src, stream), bf16, dc, ds)
+    np.testing.assert_array_equal(dc.to_host(rows * k // 2, np.uint8, stream), c_ref)
+    np.testing.assert_array_equal(ds.to_host(rows * k // 32, np.uint8, stream), s_ref)
+
+
+# ---------------------------------------------------------------- MFMA tiles (trackb method)
+def _e2m1(v):
+    a = abs(v)
+    c = int(np.where(FP4V == a)[0][0])
+    return c | (8 if v < 0 else 0)
+
+
+def _ue8m0(s):
+    return 127 + int(round(np.log2(s)))
+
+
+def _tile_data(rows, cols, kk):
+    SV = [0.5, 1.0, 2.0, 4.0]
+    A = np.array([[FP4V[(i * 7 + k * 3) % 8] for k in range(kk)] for i in range(rows)], np.float32)
+    B = np.array([[FP4V[(k * 5 + j * 2) % 8] for j in range(cols)] for k in range(kk)], np.float32)
+    nb = kk // 32
+    SFA = np.array([[SV[(i + b) % 4] for b in range(nb)] for i in range(rows)], np.float32)
+    SFB = np.array([[SV[(j + 2 * b) % 4] for j in range(cols)] for b in range(nb)], np.float32)
+    return A, B, SFA, SFB
+
+
+def _pack_lanes(M, idx_fn, rows_are_first):
+    """Pack a logical operand into 64 lanes x 8 dwords under a layout idx_fn(lane, n) -> (row/col, k)."""
+    regs = np.zeros((64, 8), np.uint32)
+    for lane in range(64):
+        for n in range(32):
+            a, k = idx_fn(lane, n)
+            v = M[a, k] if rows_are_first else M[k, a]
+            regs[lane, n // 8] |= np.uint32(_e2m1(v) << (4 * (n % 8)))
+    return regs
+
+
+def test_mfma16_layout_and_scales(rf, orc, stream):
+    """Pin v_mfma_scale_f32_16x16x128_f8f6f4 (E2M1 x E2M1, E8M0 scales): lane l
+    holds row (col) l%16 and K = 32*(l//16) + n for nibble n; D register r of
+    lane l is D[4*(l//16)+r][l%16]; the scale byte of lane l is block l//16 of
+    row (col) l%16."""
+    A, B, SFA, SFB = _tile_data(16, 16, 128)
+    Dref = np.zeros((16, 16), np.float64)
+    for i in range(16):
+        for j in range(16):
+            Dref[i, j] = sum(A[i, k] * SFA[i, k // 32] * B[k, j] * SFB[k // 32, j] for k in range(128))
+    layout = lambda lane, n: (lane % 16, 32 * (lane // 16) + n)
+    ra = _pack_lanes(A, layout, True)
+    rb = _pack_lanes(B, layout, False)
+    sa = np.array([_ue8m0(SFA[l % 16, l // 16]) for l in range(64)], np.uint32)
+    sb = np.array([_ue8m0(SFB[l // 16, l % 16]) for l in range(64)], np.uint32)
+    out = rf.DeviceBuffer.zeroed(64 * 4, np.float32, stream)
+    rf.mma_tile16(stream, _dev(rf, ra, stream), _dev(rf, rb, stream), _dev(rf, sa, stream), _dev(rf, sb, stream), out)
+    regs = out.to_host(256, np.float32, stream).reshape(64, 4)
+    D = np.zeros((16, 16), np.float64)
+    for lane in range(64):
+        for r in range(4):
+            D[4 * (lane // 16) + r, lane % 16] = regs[lane, r]
+    if not np.array_equal(D, Dref):
+        # diagnostics: transposed D?
+        Dt = np.zeros((16, 16))
+        for lane in range(64):
+            for r in range(4):
+                Dt[lane % 16, 4 * (lane // 16) + r] = regs[lane, r]
+        pytest.fail(f"layout mismatch: {np.sum(D != Dref)}/256 differ; transposed-D mismatches "
+                    f"{np.sum(Dt != Dref)}; D[0,:4]={D[0, :4]} ref={Dref[0, :4]}")
+
+
+def test_mfma32_layout_and_scales(rf, orc, stream):
+    """Pin v_mfma_scale_f32_32x32x64_f8f6f4: lane l holds row (col) l%32 and
+    K = 32*(l//32) + n; D register r of lane l is
+    D[8*(r//4) + 4*(l//32) + r%4][l%32]."""
+    A, B, SFA, SFB = _tile_data(32, 32, 64)
+    Dref = np.zeros((32, 32), np.float64)
+    for i in range(32):
+        for j in range(32):
+            Dref[i, j] = sum(A[i, k] * SFA[i, k // 32] * B[k, j] * SFB[k // 32, j] for k in range(64))
+    layout = lambda lane, n: (lane % 32, 32 * (lane // 32) + n)
+    ra = _pack_lanes(A, layout, True)
+    rb = _pack_lanes(B, layout, False)
+    sa = np.array([_ue8m0(SFA[l % 32, l // 32]) for l in range(64)], np.uint32)
+    sb = np.array([_ue8m0(SFB[l // 32, l % 32]) for l in range(64)], np.uint32)
+    out = rf.DeviceBuffer.zeroed(64 * 16, np.float32, stream)
+    rf.mma_tile32(stream, _dev(rf, ra, stream), _dev(rf, rb, stream), _dev(rf, sa, stream), _dev(rf, sb, stream), out)
+    regs = out.to_host(1024, np.float32, stream).reshape(64, 16)
+    D = np.zeros((32, 32), np.float64)
+    for lane in range(64):
+        for r in range(16):
+            D[8 * (r // 4) + 4 * (lane // 32) + r % 4, lane % 32] = regs[lane, r]
+    assert np.array_equal(D, Dref), f"{np.sum(D != Dref)}/1024 differ; D[0,:4]={D[0, :4]} ref={Dref[0, :4]}"
+
+
+def test_fp4_mma_allones(rf, stream):
+    """fp4_mma/src/main.rs:75-85: every output element is exactly 64.0."""
+    out = rf.DeviceBuffer.zeroed(128, np.float32, stream)
+    rf.fp4_mma_allones(stream, out)
+    got = out.to_host(128, np.float32, stream)
+    assert np.all(got == 64.0), got[:8]
+
+
+def test_invalid_shapes_return_errors(rf, stream):
+    buf = rf.DeviceBuffer(4096)
+    with pytest.raises(rf.Rfp4Error) as e:
+        rf.mx4_gemv(stream, 16, 33, buf, buf, buf, buf)
+    assert e.value.code == -2
+    with pytest.raises(rf.Rfp4Error):
+        rf.attn_decode(stream, 6, 4, 10, buf, buf, buf, buf)
+    with pytest.raises(rf.Rfp4Error):
+        rf.attn_decode(stream, 8, 4, 0, buf, buf, buf, buf)
