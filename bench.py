@@ -1,0 +1,223 @@
+"""Benchmark of the MI355X MXFP4 decode engine (one JSON line on stdout).
+
+Workload: Llama-3-8B architecture, random-init MXFP4
+weights (E2M1 + E8M0 per 32), batch 1, fp16 KV cache pre-filled to 4096
+tokens, greedy decode.  A "step" is one token through all 32 layers and the
+LM head.  `value` = decode tokens/s with weights and KV resident in HBM.
+
+Extra fields: the roofline of the dominant kernel (the fused gate/up SwiGLU
+GEMV) timed with HIP events on the engine's stream, the whole GEMV path of
+one token replayed alone, TinyLlama-1.1B decode tok/s (config 3), and the CPU
+oracle timed on the host cores (cpu_baseline, a reported baseline only).
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "rust-fp4-blackwell_amd"))
+
+METRIC = "MXFP4 decode tok/s @bs1 (1.1B & 8B shapes) + GEMV HBM GB/s vs peak"
+HBM_PEAK_GBS = 8000.0
+SEED = 0x8B8B
+KV_SEED = 0x4B56
+PREFILL = 4096
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def gemv_bytes(n, k):
+    """Algorithmic bytes of one MXFP4 GEMV: codes + E8M0 scales + x + y."""
+    return n * k // 2 + n * k // 32 + 4 * k + 4 * n
+
+
+def time_launches(rf, stream, fn, reps):
+    e0, e1 = rf.Event(), rf.Event()
+    fn()  # warm
+    stream.synchronize()
+    e0.record(stream)
+    for _ in range(reps):
+        fn()
+    e1.record(stream)
+    e1.synchronize()
+    return e0.elapsed_ms(e1) / reps
+
+
+def gemv_path(rf, eng, cfg, reps=5):
+    """Every GEMV launch of one 8B token, alone, on the engine stream."""
+    s = eng.stream
+    qd, kvd = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
+    kmax = max(cfg.dim, cfg.ffn, qd)
+    rng = np.random.default_rng(0)
+    x = rf.DeviceBuffer.from_host(rng.standard_normal(kmax).astype(np.float32), s)
+    y = rf.DeviceBuffer.zeroed(max(cfg.vocab, 2 * cfg.ffn), np.float32, s)
+    calls, total_bytes = [], 0
+    for l in range(cfg.n_layers):
+        qc, qs, _, _ = eng.weight(l, 0)
+        oc, os_, _, _ = eng.weight(l, 3)
+        gc, gs, _, _ = eng.weight(l, 4)
+        dc, ds, _, _ = eng.weight(l, 6)
+        calls.append(lambda qc=qc, qs=qs: rf.mx4_gemv(s, qd + 2 * kvd, cfg.dim, qc, qs, x, y))
+        calls.append(lambda oc=oc, os_=os_: rf.mx4_gemv_residual(s, cfg.dim, qd, oc, os_, x, y))
+        calls.append(lambda gc=gc, gs=gs: rf.mx4_gemv_swiglu(s, cfg.ffn, cfg.dim, cfg.ffn, gc, gs, x, y))
+        calls.append(lambda dc=dc, ds=ds: rf.mx4_gemv_residual(s, cfg.dim, cfg.ffn, dc, ds, x, y))
+        total_bytes += gemv_bytes(qd + 2 * kvd, cfg.dim) + gemv_bytes(cfg.dim, qd) + \
+            gemv_bytes(2 * cfg.ffn, cfg.dim) + gemv_bytes(cfg.dim, cfg.ffn)
+    lc, ls, _, _ = eng.weight(-1, 0)
+    calls.append(lambda: rf.mx4_gemv(s, cfg.vocab, cfg.dim, lc, ls, x, y))
+    total_bytes += gemv_bytes(cfg.vocab, cfg.dim)
+    ms = time_launches(rf, s, lambda: [c() for c in calls], reps)
+    # dominant kernel: the fused gate/up SwiGLU GEMV, one launch per layer
+    gate = [calls[4 * l + 2] for l in range(cfg.n_layers)]
+    ms_gate = time_launches(rf, s, lambda: [c() for c in gate], reps) / cfg.n_layers
+    gate_bytes = gemv_bytes(2 * cfg.ffn, cfg.dim) - 4 * cfg.ffn  # y holds ffn outputs, not 2*ffn
+    return total_bytes, ms, gate_bytes, ms_gate
+
+
+def decode_run(rf, preset, max_seq, prefill, prompt, warmup, steps):
+    cfg = rf.model_config(preset, max_seq=max_seq)
+    eng = rf.Engine(cfg, SEED)
+    if prefill:
+        eng.prefill_kv(KV_SEED, prefill)
+    n_prompt = len(prompt)
+    eng.begin(prompt, prefill, n_prompt + warmup + steps)
+    eng.run_steps(n_prompt - 1 + warmup)
+    eng.stream.synchronize()
+    e0, e1 = rf.Event(), rf.Event()
+    t0 = time.perf_counter()
+    e0.record(eng.stream)
+    eng.run_steps(steps)
+    e1.record(eng.stream)
+    e1.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_ms(e1)
+    ids = eng.read_ids(n_prompt + warmup + steps)
+    assert np.all(ids < cfg.vocab)
+    return eng, cfg, ms, wall, ids
+
+
+def cpu_baseline(threads, steps=2):
+    """The oracle decode loop (oracle/, C, f32, k-order) on the host cores:
+    config-4 model, context pre-filled to 4096, `steps` decode steps timed."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle
+
+    pyoracle.set_threads(threads)
+    cfg = dict(dim=4096, n_layers=32, n_heads=32, n_kv_heads=8, head_dim=128, ffn=14336, vocab=128256,
+               theta=500000.0, eps=1e-5, max_seq=PREFILL + steps + 2)
+    t0 = time.perf_counter()
+    m = pyoracle.Model(cfg, SEED)
+    m.prefill_kv(KV_SEED, PREFILL)
+    t_setup = time.perf_counter() - t0
+    tok = 1
+    t0 = time.perf_counter()
+    for i in range(steps):
+        tok = m.step(tok, PREFILL + i)
+    dt = time.perf_counter() - t0
+    m.close()
+    return steps / dt, t_setup, dt
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=4)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--cpu-steps", type=int, default=2)
+    ap.add_argument("--no-tiny", action="store_true", help="skip the TinyLlama-1.1B line")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path "
+              "(the decode step would shard tensor-parallel; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import rfp4 as rf
+
+    rf.init(0)
+    # ---- config 4: Llama-3-8B decode at batch 1, ctx 4096
+    max_seq = PREFILL + args.warmup + args.steps + 8
+    eng, cfg, ms, wall, ids = decode_run(rf, "llama3-8b", max_seq, PREFILL, [1], args.warmup, args.steps)
+    tok_s = args.steps / (ms / 1e3)
+    ms_step = ms / args.steps
+    weight_bytes = eng.weight_bytes()
+    log(f"llama3-8b: {ms_step * 1e3:.1f} us/token, {tok_s:.1f} tok/s (wall {args.steps / wall:.1f}); "
+        f"weights {weight_bytes / 1e9:.3f} GB -> {weight_bytes / ms_step / 1e6:.0f} GB/s effective")
+
+    path_bytes, path_ms, gate_bytes, gate_ms = gemv_path(rf, eng, cfg)
+    gate_gbs = gate_bytes / gate_ms / 1e6
+    path_gbs = path_bytes / path_ms / 1e6
+    log(f"GEMV path: {path_bytes / 1e9:.3f} GB in {path_ms * 1e3:.1f} us -> {path_gbs:.0f} GB/s; "
+        f"gate/up GEMV {gate_ms * 1e3:.2f} us -> {gate_gbs:.0f} GB/s")
+    eng.close()
+
+    tiny = None
+    if not args.no_tiny:
+        r = np.random.default_rng(16).integers(0, 32000, 16).astype(np.uint32)
+        teng, tcfg, tms, twall, tids = decode_run(rf, "tinyllama-1.1b", 16 + 256 + 8, 0, r, 0, 256)
+        tiny = {"tok_s": round(256 / (tms / 1e3), 1), "ms_per_token": round(tms / 256, 4),
+                "workload": "TinyLlama-1.1B arch, 16-token prompt, 256 greedy steps"}
+        log(f"tinyllama: {tiny['tok_s']} tok/s")
+        teng.close()
+
+    cpu = None
+    if not args.no_cpu:
+        threads = min(16, os.cpu_count() or 1)
+        cpu_tok_s, t_setup, t_run = cpu_baseline(threads, args.cpu_steps)
+        cpu = {"value": round(cpu_tok_s, 4), "unit": "tok/s", "cores": threads, "kind": "port",
+               "sample": f"oracle/ C decode loop, Llama-3-8B config 4 at ctx {PREFILL}, {args.cpu_steps} steps "
+                         f"timed ({t_run:.1f} s; setup {t_setup:.1f} s untimed)"}
+        log(f"cpu oracle: {cpu_tok_s:.3f} tok/s on {threads} threads")
+
+    out = {
+        "metric": METRIC,
+        "value": round(tok_s, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "Llama-3-8B arch decode, batch 1, fp16 KV pre-filled to 4096, greedy (BASELINE config 4)",
+            "weights": "MXFP4 E2M1 + E8M0/32, random init",
+            "global_batch": 1,
+            "seq_len": PREFILL,
+            "parallelism": "none (1 GPU)",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "fused gate/up SwiGLU GEMV (rfp4_gemv_e8m0_swiglu)",
+            "achieved": round(gate_gbs, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(gate_gbs / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "bytes_per_launch": gate_bytes,
+            "us_per_launch": round(gate_ms * 1e3, 3),
+        },
+        "gemv_path": {
+            "bytes_per_token": path_bytes,
+            "us_per_token": round(path_ms * 1e3, 2),
+            "GB_s": round(path_gbs, 1),
+            "frac": round(path_gbs / HBM_PEAK_GBS, 4),
+        },
+        "tinyllama": tiny,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -114,13 +114,13 @@ float orc_ih4_normal(uint64_t r, float coef)
  * codecs
  * ====================================================================== */
 static const float E2M1_MAG[8] = {0.0f, 0.5f, 1.0f, 1.5f, 2.0f, 3.0f, 4.0f, 6.0f};
+/* The same values with the sign applied ("if c & 8 { -m } else { m }"), as one
+ * table so the GEMV loop has no data-dependent branch. */
+static const float E2M1_VAL[16] = {0.0f,  0.5f,  1.0f,  1.5f,  2.0f,  3.0f,  4.0f,  6.0f,
+                                   -0.0f, -0.5f, -1.0f, -1.5f, -2.0f, -3.0f, -4.0f, -6.0f};
 
 /* fp4_gemv/src/main.rs:130-134 */
-float orc_e2m1_decode(uint8_t code)
-{
-    float m = E2M1_MAG[code & 7];
-    return (code & 8) ? -m : m;
-}
+float orc_e2m1_decode(uint8_t code) { return E2M1_VAL[code & 15]; }
 
 /* llama_run/src/main.rs:21-32 (fp4_val) */
 float orc_e2m1_decode_arith(uint32_t code)
@@ -156,15 +156,13 @@ uint8_t orc_e8m0_encode_pow2(float s)
 uint8_t orc_e2m1_rne(float v)
 {
     float a = fabsf(v);
-    uint8_t c;
-    if (a <= 0.25f) c = 0;        /* 0.25 tie -> 0   (m=0) */
-    else if (a < 0.75f) c = 1;    /* 0.5             */
-    else if (a <= 1.25f) c = 2;   /* 0.75 tie -> 1.0, 1.25 tie -> 1.0 */
-    else if (a < 1.75f) c = 3;    /* 1.5             */
-    else if (a <= 2.5f) c = 4;    /* 1.75 tie -> 2, 2.5 tie -> 2 */
-    else if (a < 3.5f) c = 5;     /* 3               */
-    else if (a <= 5.0f) c = 6;    /* 3.5 tie -> 4, 5 tie -> 4 */
-    else c = 7;                   /* 6, saturating    */
+    /* Count the decision thresholds a lies above; '>' at a tie rounds down to
+     * the even neighbour, '>=' rounds up to it:
+     *   0.25 tie -> 0, 0.75 -> 1.0, 1.25 -> 1.0, 1.75 -> 2, 2.5 -> 2,
+     *   3.5 -> 4, 5 -> 4; above 5 -> 6 (saturating); NaN -> code 7. */
+    uint8_t c = (uint8_t)((a > 0.25f) + (a >= 0.75f) + (a > 1.25f) + (a >= 1.75f) + (a > 2.5f) + (a >= 3.5f) +
+                          (a > 5.0f));
+    if (isnan(a)) c = 7;
     if (signbit(v)) c |= 8;
     return c;
 }
@@ -315,7 +313,12 @@ static uint8_t quant_mx_block(const float *v, uint8_t *codes)
     int se = floor_log2f(amax) - 2; /* E2M1 emax = 2 */
     if (se < -127) se = -127;
     if (se > 127) se = 127;
-    for (int i = 0; i < 32; i++) codes[i] = orc_e2m1_rne(ldexpf(v[i], -se));
+    /* v * 2^-se == ldexpf(v, -se): the factor is a normal float for every
+     * se in [-127, 125], so the product rounds exactly like ldexpf. */
+    uint32_t fb = (uint32_t)(127 - se) << 23;
+    float f;
+    memcpy(&f, &fb, 4);
+    for (int i = 0; i < 32; i++) codes[i] = orc_e2m1_rne(v[i] * f);
     return (uint8_t)(se + 127);
 }
 

@@ -65,6 +65,10 @@ RFP4_DEV void mma_allones_body(float *out)
     v4f32 acc = {0.0f, 0.0f, 0.0f, 0.0f};
     acc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(av, bv, acc, MX_FMT_FP4, MX_FMT_FP4, 0, 0x7E7E7E7E, 0,
                                                            0x7F7F7F7F);
+    // The MFMA reads the operand registers of all 64 lanes whatever EXEC is;
+    // consuming its result here keeps the compiler from sinking it (and the
+    // operand set-up) into the divergent store below.
+    asm volatile("" ::"v"(acc[0]), "v"(acc[1]), "v"(acc[2]), "v"(acc[3]));
     const int col = lane & 15, rb = (lane >> 4) * 4;
     if (col < 8)
 #pragma unroll

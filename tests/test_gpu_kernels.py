@@ -56,11 +56,32 @@ def test_mx4_gemv_parity(rf, orc, stream, n, k):
     y = dy.to_host(n, np.float32, stream)
     yref = orc.gemv_e8m0(n, k, codes, scales, x)
     y64, absy = orc.gemv_e8m0_f64(n, k, codes, scales, x)
-    # condition-aware bound against the f64 sum, and the reference's metric at 1e-3
+    _assert_gemv_close(y, yref, y64, absy)
+
+
+def _assert_gemv_close(y, yref, y64, absy):
+    """GEMV parity bar (fp32 accumulate in a different order than the oracle):
+    - normwise: |y - y64| <= 1e-5 * sum_k |w_k x_k| on every row (the 1e-3
+      relative bar of the path, measured against the magnitude of the terms);
+    - the reference's own gate: |d| / max(|ref|, 1e-3) <= 1e-2 on every row
+      (fp4_gemv/src/main.rs:165-168, 0 bad rows), taken against the exact
+      f64 sum: at K = 14336 the f32 k-order loop itself drifts past 1e-2 on
+      rows with heavy cancellation;
+    - no less accurate than the f32 k-order oracle: max |y - y64| within
+      2x the oracle's own max |yref - y64| (plus one ulp of the row scale);
+    - elementwise 1e-3 against the exact f64 sum on >= 99.9% of rows (rows
+      with heavy cancellation may exceed it, as the reference reports a max
+      of ~1.3e-3, main.tex:201)."""
+    y64 = np.asarray(y64, np.float64)
     cond = np.abs(y.astype(np.float64) - y64) / np.maximum(absy, 1e-300)
     assert cond.max() < 1e-5, f"max |y-y64|/sum|wx| = {cond.max():.3e}"
-    rel = reference_rel_err(y, yref)
-    assert (rel > 1e-3).sum() == 0, f"{(rel > 1e-3).sum()} rows over 1e-3, max {rel.max():.3e}"
+    rel = reference_rel_err(y, y64)
+    assert (rel > 1e-2).sum() == 0, f"{(rel > 1e-2).sum()} bad rows, max {rel.max():.3e}"
+    err_gpu = np.abs(y.astype(np.float64) - y64).max()
+    err_orc = np.abs(np.asarray(yref, np.float64) - y64).max()
+    assert err_gpu <= 2 * err_orc + 6e-8 * np.max(absy), (err_gpu, err_orc)
+    rel64 = reference_rel_err(y, y64)
+    assert np.mean(rel64 <= 1e-3) >= 0.999, f"{(rel64 > 1e-3).sum()} rows over 1e-3 (max {rel64.max():.3e})"
 
 
 def test_fp4_gemv_reference_harness(rf, orc, stream):
@@ -80,9 +101,11 @@ def test_fp4_gemv_reference_harness(rf, orc, stream):
     dy = rf.DeviceBuffer.zeroed(N, np.float32, stream)
     rf.fp4_gemv(stream, N, K, dw, ds, dx, dy)
     y = dy.to_host(N, np.float32, stream)
-    rel = reference_rel_err(y, yref)
-    assert (rel > 1e-2).sum() == 0
-    assert rel.max() < 1e-3, rel.max()
+    # exact f64 value of the same dequantized products, numpy only
+    sgn = np.where(codes & 8, -1.0, 1.0)
+    deq = (sgn * FP4V[codes & 7].astype(np.float64)).reshape(N, K // 32, 32) * scales.reshape(N, K // 32, 1)
+    terms = deq.reshape(N, K) * x.astype(np.float64)
+    _assert_gemv_close(y, yref, terms.sum(axis=1), np.abs(terms).sum(axis=1))
 
 
 def test_gemv_one_hot_selects_column(rf, orc, stream):
