@@ -94,6 +94,10 @@ int mx4_gemv(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_t *codes,
  *  mx4_gemv_argmax:   y = W.x and *best_token = argmax(y) with the
  *                     reference's tie rule (fp4_gemv lm_head + argmax, :533-534);
  *                     workspace: ceil(n/16)*8 bytes (mx4_gemv_argmax_workspace). */
+/* rmsnorm + fp4_gemv (llama_run/src/main.rs:513-514 fused): y = W.(x*rms*w_norm),
+ * rms = 1/sqrt(sum(x^2)/k + eps), fp16 norm weights. */
+int mx4_gemv_rmsnorm(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_t *codes, const uint8_t *scales,
+                     const float *x, const uint16_t *norm_w, float eps, float *y);
 int mx4_gemv_residual(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_t *codes,
                       const uint8_t *scales, const float *x, float *x_res);
 int mx4_gemv_swiglu(rfp4_stream_t stream, uint32_t n, uint32_t k, uint32_t pair_off, const uint8_t *codes,
@@ -149,6 +153,10 @@ int rfp4_mma_tile16(rfp4_stream_t stream, const uint32_t *a, const uint32_t *b, 
                     const uint32_t *sb, float *out);
 int rfp4_mma_tile32(rfp4_stream_t stream, const uint32_t *a, const uint32_t *b, const uint32_t *sa,
                     const uint32_t *sb, float *out);
+/* Test hook: force the GEMV variant of later launches on this thread
+ * (rows per wave 2/4/8, up-front K-slices or 0 for the slice loop;
+ * 0, -1 = automatic).  No reference counterpart. */
+int rfp4_debug_gemv_variant(int rows_per_wave, int slices);
 /* Hardware E2M1 conversion of n words (8 codes each) to 8n floats. */
 int rfp4_selftest_cvt_fp4(rfp4_stream_t stream, uint32_t n, const uint32_t *words, float *out);
 /* Synthetic weight generator used by the engine (rows [r0, r0+nrows)). */

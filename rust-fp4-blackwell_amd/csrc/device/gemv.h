@@ -8,10 +8,13 @@
 //
 // Mapping (wave64): lane l owns 16-byte chunk c = l + 64*s of every row it
 // touches (32 codes = exactly one scale block), so one global_load_dwordx4
-// per row covers 1 KiB of a row contiguously across the wave.  The lane loads
-// its 32 activations once per slice and reuses them for all R rows of the
-// wave; partial sums are reduced across the wave with DPP at the end.
-// A workgroup is 4 waves = 4R logical rows.
+// per row covers 1 KiB of a row contiguously across the wave.  A workgroup
+// (4 waves, 4R logical rows) stages x in LDS once -- optionally RMS-normalized
+// on the way (the rmsnorm launch of llama_run/src/main.rs:513,525 folded in)
+// -- and each lane reads its 32 activations per slice from LDS and reuses them
+// for all R rows of its wave.  Weight loads are double-buffered across
+// slices; the first slice is issued before x is staged.  Partial sums are
+// reduced across the wave with DPP at the end.
 #pragma once
 #include "common.h"
 
@@ -28,10 +31,58 @@ RFP4_DEV float silu_ref(float g)
     return __fdiv_rn(g, __fadd_rn(1.0f, expf(-g)));
 }
 
-template <int SCALE_F32, int EPI, int R>
+// Stage x (K floats) into LDS; with norm_w, store x * rms * w instead
+// (rms = 1/sqrt(sum(x^2)/K + eps), llama_rmsnorm/src/main.rs:75-77).
+RFP4_DEV void stage_x(float *xs, const float *x, uint32_t k, const uint16_t *norm_w, float eps)
+{
+    __shared__ float red[4];
+    const int tid = threadIdx.x;
+    const uint32_t k4 = k >> 2;
+    if (norm_w == nullptr) {
+        for (uint32_t i = tid; i < k4; i += 256) ((float4 *)xs)[i] = ((const float4 *)x)[i];
+        __syncthreads();
+        return;
+    }
+    float ss = 0.0f;
+    for (uint32_t i = tid; i < k4; i += 256) {
+        float4 v = ((const float4 *)x)[i];
+        ((float4 *)xs)[i] = v;
+        ss = __fadd_rn(ss, __fmul_rn(v.x, v.x));
+        ss = __fadd_rn(ss, __fmul_rn(v.y, v.y));
+        ss = __fadd_rn(ss, __fmul_rn(v.z, v.z));
+        ss = __fadd_rn(ss, __fmul_rn(v.w, v.w));
+    }
+    ss = wave_sum(ss);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    float total = (red[0] + red[1]) + (red[2] + red[3]);
+    float rms = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(total, (float)k), eps)));
+    for (uint32_t i = tid; i < k; i += 256) xs[i] = __fmul_rn(__fmul_rn(xs[i], rms), f16_bits_to_f32(norm_w[i]));
+    __syncthreads();
+}
+
+// Raw scale bits now, value at use: keeps the loads free of dependent ALU
+// work so they can all be in flight together.
+template <int SCALE_F32>
+RFP4_DEV uint32_t load_scale_bits(const void *scales, size_t idx)
+{
+    if (SCALE_F32) return ((const uint32_t *)scales)[idx];
+    return ((const uint8_t *)scales)[idx];
+}
+
+template <int SCALE_F32>
+RFP4_DEV float scale_from_bits(uint32_t b)
+{
+    return SCALE_F32 ? __uint_as_float(b) : e8m0_to_f32(b);
+}
+
+// NS: K-slices of 64 chunks (2048 values) per row, fixed at compile time so
+// all loads are issued up front; NS = 0 handles any K with a slice loop.
+template <int SCALE_F32, int EPI, int R, int NS>
 RFP4_DEV void gemv_body(const GemvArgs &a)
 {
     constexpr int NP = (EPI == RFP4_EPI_SWIGLU) ? 2 * R : R;
+    extern __shared__ float xs[]; // K floats (dynamic LDS)
     __shared__ unsigned long long s_best[4];
 
     const int lane = threadIdx.x & 63;
@@ -40,34 +91,71 @@ RFP4_DEV void gemv_body(const GemvArgs &a)
     const uint32_t nchunk = a.k >> 5;
     const size_t rowbytes = (size_t)(a.k >> 1);
 
-    uint32_t prow[NP];
+    const uint8_t *rowp[NP];
+    size_t srow[NP];
 #pragma unroll
     for (int i = 0; i < R; i++) {
         uint32_t lr = lrow0 + (uint32_t)i;
         uint32_t r = lr < a.n ? lr : a.n - 1; // clamp: loads stay in bounds
-        prow[i] = r;
-        if (EPI == RFP4_EPI_SWIGLU) prow[R + i] = r + a.pair_off;
+        rowp[i] = (const uint8_t *)a.w + (size_t)r * rowbytes;
+        srow[i] = (size_t)r * nchunk;
+        if (EPI == RFP4_EPI_SWIGLU) {
+            rowp[R + i] = (const uint8_t *)a.w + (size_t)(r + a.pair_off) * rowbytes;
+            srow[R + i] = (size_t)(r + a.pair_off) * nchunk;
+        }
     }
 
+    const uint32_t clast = nchunk - 1u;
     float acc[NP];
 #pragma unroll
     for (int p = 0; p < NP; p++) acc[p] = 0.0f;
 
-    const uint8_t *wb = (const uint8_t *)a.w;
-    for (uint32_t c = (uint32_t)lane; c < nchunk; c += 64u) {
-        uint4 q[NP];
-        float sc[NP];
+    if (NS > 0) {
+        // Every load of this wave (NS slices x NP rows) is issued before x is
+        // staged: one memory round trip, straight-line code.  A lane past the
+        // last chunk re-reads the last chunk (in bounds) and gets scale 0.
+        uint4 q[NS > 0 ? NS : 1][NP];
+        uint32_t sb[NS > 0 ? NS : 1][NP];
 #pragma unroll
-        for (int p = 0; p < NP; p++) {
-            q[p] = *(const uint4 *)(wb + (size_t)prow[p] * rowbytes + (size_t)c * 16u);
-            sc[p] = load_scale<SCALE_F32>(a.scales, (size_t)prow[p] * nchunk + c);
+        for (int s = 0; s < NS; s++) {
+            const uint32_t cl = min((uint32_t)lane + 64u * (uint32_t)s, clast);
+#pragma unroll
+            for (int p = 0; p < NP; p++) {
+                q[s][p] = *(const uint4 *)(rowp[p] + (size_t)cl * 16u);
+                sb[s][p] = load_scale_bits<SCALE_F32>(a.scales, srow[p] + cl);
+            }
         }
-        float4 xv[8];
-        const float4 *xp = (const float4 *)(a.x) + (size_t)c * 8u;
+        stage_x(xs, a.x, a.k, a.norm_w, a.eps);
 #pragma unroll
-        for (int j = 0; j < 8; j++) xv[j] = xp[j];
+        for (int s = 0; s < NS; s++) {
+            const uint32_t c = (uint32_t)lane + 64u * (uint32_t)s;
+            const float live = c < nchunk ? 1.0f : 0.0f;
+            float4 xv[8];
+            const float4 *xp = (const float4 *)(xs + (size_t)min(c, clast) * 32u);
 #pragma unroll
-        for (int p = 0; p < NP; p++) acc[p] = fmaf(sc[p], dot_chunk32(q[p], xv), acc[p]);
+            for (int j = 0; j < 8; j++) xv[j] = xp[j];
+#pragma unroll
+            for (int p = 0; p < NP; p++)
+                acc[p] = fmaf(live * scale_from_bits<SCALE_F32>(sb[s][p]), dot_chunk32(q[s][p], xv), acc[p]);
+        }
+    } else {
+        // any K: one slice at a time
+        stage_x(xs, a.x, a.k, a.norm_w, a.eps);
+        for (uint32_t c = (uint32_t)lane; c < nchunk; c += 64u) {
+            uint4 q[NP];
+            float sc[NP];
+#pragma unroll
+            for (int p = 0; p < NP; p++) {
+                q[p] = *(const uint4 *)(rowp[p] + (size_t)c * 16u);
+                sc[p] = load_scale<SCALE_F32>(a.scales, srow[p] + c);
+            }
+            float4 xv[8];
+            const float4 *xp = (const float4 *)(xs + (size_t)c * 32u);
+#pragma unroll
+            for (int j = 0; j < 8; j++) xv[j] = xp[j];
+#pragma unroll
+            for (int p = 0; p < NP; p++) acc[p] = fmaf(sc[p], dot_chunk32(q[p], xv), acc[p]);
+        }
     }
 
 #pragma unroll

@@ -103,32 +103,24 @@ static int enqueue_step(llama_engine *e)
         const LayerW &w = e->L[l];
         uint16_t *kc = e->kcache + (size_t)l * c.n_kv_heads * e->max_seq_alloc * hd;
         uint16_t *vc = e->vcache + (size_t)l * c.n_kv_heads * e->max_seq_alloc * hd;
-        RmsnormArgs na{e->x, e->norm_attn + (size_t)l * c.dim, e->h, c.dim, c.eps};
-        if ((rc = launch("rfp4_rmsnorm_f16w", dim3(1), dim3(1024), s, &na))) return rc;
-        GemvArgs qa{w.qkv_c, w.qkv_s, e->h, e->qkv, nullptr, qd + 2 * kvd, c.dim, 0, 0};
+        GemvArgs qa{w.qkv_c, w.qkv_s, e->x, e->qkv, nullptr, e->norm_attn + (size_t)l * c.dim, qd + 2 * kvd, c.dim, 0, c.eps};
         if ((rc = gemv_launch("e8m0", RFP4_EPI_STORE, qa, s, 0))) return rc;
-        RopeAppendArgs ra{e->qkv, e->cos_tab, e->sin_tab, kc, vc, &e->state->pos, c.n_heads, c.n_kv_heads, hd, e->max_seq_alloc};
-        uint32_t work = c.n_heads * hd / 2 + c.n_kv_heads * hd / 2 + kvd;
-        if ((rc = launch("rfp4_rope_append", dim3((work + 255) / 256), dim3(256), s, &ra))) return rc;
         AttnArgs aa{};
         aa.q = e->qkv; aa.kc = kc; aa.vc = vc; aa.out = e->attn_out;
         aa.part = e->attn_part; aa.counters = e->attn_counters; aa.pos_ptr = &e->state->pos;
+        aa.cosv = e->cos_tab; aa.sinv = e->sin_tab; aa.k_new = e->qkv + qd; aa.v_new = e->qkv + qd + kvd;
         aa.ts = hd; aa.hs = (uint64_t)e->max_seq_alloc * hd;
         aa.n_heads = c.n_heads; aa.n_kv_heads = c.n_kv_heads; aa.head_dim = hd; aa.seq = 0;
         aa.chunk = e->attn_chunk; aa.max_splits = e->attn_max_splits;
         if ((rc = attn_launch(aa, 1, s, e->attn_chunk * e->attn_max_splits))) return rc;
-        GemvArgs oa{w.o_c, w.o_s, e->attn_out, e->x, nullptr, c.dim, qd, 0, 0};
+        GemvArgs oa{w.o_c, w.o_s, e->attn_out, e->x, nullptr, nullptr, c.dim, qd, 0, 0.0f};
         if ((rc = gemv_launch("e8m0", RFP4_EPI_RESIDUAL, oa, s, 0))) return rc;
-        RmsnormArgs fa{e->x, e->norm_ffn + (size_t)l * c.dim, e->h, c.dim, c.eps};
-        if ((rc = launch("rfp4_rmsnorm_f16w", dim3(1), dim3(1024), s, &fa))) return rc;
-        GemvArgs ga{w.gu_c, w.gu_s, e->h, e->sw, nullptr, c.ffn, c.dim, c.ffn, 0};
+        GemvArgs ga{w.gu_c, w.gu_s, e->x, e->sw, nullptr, e->norm_ffn + (size_t)l * c.dim, c.ffn, c.dim, c.ffn, c.eps};
         if ((rc = gemv_launch("e8m0", RFP4_EPI_SWIGLU, ga, s, 0))) return rc;
-        GemvArgs da{w.d_c, w.d_s, e->sw, e->x, nullptr, c.dim, c.ffn, 0, 0};
+        GemvArgs da{w.d_c, w.d_s, e->sw, e->x, nullptr, nullptr, c.dim, c.ffn, 0, 0.0f};
         if ((rc = gemv_launch("e8m0", RFP4_EPI_RESIDUAL, da, s, 0))) return rc;
     }
-    RmsnormArgs fn{e->x, e->norm_final, e->h, c.dim, c.eps};
-    if ((rc = launch("rfp4_rmsnorm_f16w", dim3(1), dim3(1024), s, &fn))) return rc;
-    GemvArgs la{e->lm_c, e->lm_s, e->h, e->logits, e->best, c.vocab, c.dim, 0, 0};
+    GemvArgs la{e->lm_c, e->lm_s, e->x, e->logits, e->best, e->norm_final, c.vocab, c.dim, 0, c.eps};
     if ((rc = gemv_launch("e8m0", RFP4_EPI_ARGMAX, la, s, 0))) return rc;
     StepArgs sa{e->best, e->state, e->ids, e->last_tok, e->n_best, 0};
     return launch("rfp4_step", dim3(1), dim3(1024), s, &sa);
@@ -177,7 +169,7 @@ int llama_engine_create(const rfp4_model_config *cfg, uint64_t seed, llama_engin
     const uint32_t qd = qdim(c), kvd = kvdim(c), hd = c.head_dim;
     rc = hip_check(hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking), "hipStreamCreate");
     // attention split plan over the full cache capacity
-    e->attn_chunk = attn_chunk_for(c.n_kv_heads, c.max_seq, rt->num_cus);
+    e->attn_chunk = attn_chunk_for(c.n_kv_heads, c.max_seq, rt->num_cus, hd, 2u);
     e->attn_max_splits = (c.max_seq + e->attn_chunk - 1) / e->attn_chunk;
     e->max_seq_alloc = (e->attn_chunk * e->attn_max_splits + 255u) / 256u * 256u;
     hipStream_t s = e->stream;
@@ -247,9 +239,9 @@ int llama_engine_create(const rfp4_model_config *cfg, uint64_t seed, llama_engin
     if (!rc) rc = dalloc_t(e, &e->attn_out, qd);
     if (!rc) rc = dalloc_t(e, &e->sw, c.ffn);
     if (!rc) rc = dalloc_t(e, &e->logits, c.vocab);
-    e->n_best = gemv_blocks(c.vocab, RFP4_EPI_ARGMAX, 0);
+    e->n_best = gemv_blocks(c.vocab, c.dim, RFP4_EPI_ARGMAX);
     if (!rc) rc = dalloc_t(e, &e->best, e->n_best);
-    if (!rc) rc = dalloc_t(e, &e->attn_part, (size_t)c.n_heads * e->attn_max_splits * (hd + 2));
+    if (!rc) rc = dalloc_t(e, &e->attn_part, (size_t)c.n_heads * e->attn_max_splits * (hd + 4));
     if (!rc) rc = dalloc_t(e, &e->attn_counters, c.n_kv_heads);
     if (!rc) rc = fill_words(e->attn_counters, c.n_kv_heads, 0u, s);
     if (!rc) rc = dalloc(e, (void **)&e->state, sizeof(StepState));

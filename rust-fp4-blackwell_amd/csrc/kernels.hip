@@ -12,19 +12,36 @@
 #define K256 extern "C" __global__ __launch_bounds__(256)
 #define K1024 extern "C" __global__ __launch_bounds__(1024)
 
-// ---- GEMV: rfp4_gemv_<scale>_<epilogue>_r<R>
-#define GEMV_KERNEL(SNAME, SF32, ENAME, EPI, R) \
-    K256 void rfp4_gemv_##SNAME##_##ENAME##_r##R(GemvArgs a) { gemv_body<SF32, EPI, R>(a); }
-#define GEMV_ALL_R(SNAME, SF32, ENAME, EPI) \
-    GEMV_KERNEL(SNAME, SF32, ENAME, EPI, 2) \
-    GEMV_KERNEL(SNAME, SF32, ENAME, EPI, 4) \
-    GEMV_KERNEL(SNAME, SF32, ENAME, EPI, 8)
+// ---- GEMV: rfp4_gemv_<scale>_<epilogue>_r<R>_s<NS>
+// (R rows per wave, NS = K/2048 slices issued up front, 0 = any K).  The host
+// selects among these (runtime.cpp gemv_variant); keep the two lists in sync.
+#define GEMV_KERNEL(SNAME, SF32, ENAME, EPI, R, NS) \
+    K256 void rfp4_gemv_##SNAME##_##ENAME##_r##R##_s##NS(GemvArgs a) { gemv_body<SF32, EPI, R, NS>(a); }
+#define GEMV_NS_FULL(SNAME, SF32, ENAME, EPI, R) \
+    GEMV_KERNEL(SNAME, SF32, ENAME, EPI, R, 0) \
+    GEMV_KERNEL(SNAME, SF32, ENAME, EPI, R, 1) \
+    GEMV_KERNEL(SNAME, SF32, ENAME, EPI, R, 2) \
+    GEMV_KERNEL(SNAME, SF32, ENAME, EPI, R, 3) \
+    GEMV_KERNEL(SNAME, SF32, ENAME, EPI, R, 4) \
+    GEMV_KERNEL(SNAME, SF32, ENAME, EPI, R, 7)
+#define GEMV_NS_SHORT(SNAME, SF32, ENAME, EPI, R) \
+    GEMV_KERNEL(SNAME, SF32, ENAME, EPI, R, 0) \
+    GEMV_KERNEL(SNAME, SF32, ENAME, EPI, R, 1) \
+    GEMV_KERNEL(SNAME, SF32, ENAME, EPI, R, 2)
 
-GEMV_ALL_R(e8m0, 0, store, RFP4_EPI_STORE)
-GEMV_ALL_R(e8m0, 0, resid, RFP4_EPI_RESIDUAL)
-GEMV_ALL_R(e8m0, 0, swiglu, RFP4_EPI_SWIGLU)
-GEMV_ALL_R(e8m0, 0, argmax, RFP4_EPI_ARGMAX)
-GEMV_ALL_R(f32, 1, store, RFP4_EPI_STORE)
+GEMV_NS_FULL(e8m0, 0, store, RFP4_EPI_STORE, 2)
+GEMV_NS_FULL(e8m0, 0, store, RFP4_EPI_STORE, 4)
+GEMV_NS_SHORT(e8m0, 0, store, RFP4_EPI_STORE, 8)
+GEMV_NS_FULL(e8m0, 0, resid, RFP4_EPI_RESIDUAL, 2)
+GEMV_NS_FULL(e8m0, 0, resid, RFP4_EPI_RESIDUAL, 4)
+GEMV_NS_SHORT(e8m0, 0, resid, RFP4_EPI_RESIDUAL, 8)
+GEMV_NS_FULL(e8m0, 0, argmax, RFP4_EPI_ARGMAX, 2)
+GEMV_NS_FULL(e8m0, 0, argmax, RFP4_EPI_ARGMAX, 4)
+GEMV_NS_SHORT(e8m0, 0, argmax, RFP4_EPI_ARGMAX, 8)
+GEMV_NS_FULL(e8m0, 0, swiglu, RFP4_EPI_SWIGLU, 2)
+GEMV_NS_SHORT(e8m0, 0, swiglu, RFP4_EPI_SWIGLU, 4)
+GEMV_KERNEL(e8m0, 0, swiglu, RFP4_EPI_SWIGLU, 4, 3)
+GEMV_NS_FULL(f32, 1, store, RFP4_EPI_STORE, 4)
 
 // ---- norm / rope / embed
 K1024 void rfp4_rmsnorm_f32w(RmsnormArgs a) { rmsnorm_body<0>(a); }

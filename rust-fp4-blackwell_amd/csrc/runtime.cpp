@@ -38,7 +38,7 @@ int hip_check(hipError_t e, const char *what)
 
 Runtime *runtime() { return g_rt; }
 
-int launch(const char *name, dim3 grid, dim3 block, hipStream_t s, void *args)
+int launch(const char *name, dim3 grid, dim3 block, hipStream_t s, void *args, unsigned shmem)
 {
     Runtime *rt = g_rt;
     if (!rt) return set_error(RFP4_E_NOT_INIT, "rfp4_init has not been called");
@@ -54,7 +54,7 @@ int launch(const char *name, dim3 grid, dim3 block, hipStream_t s, void *args)
     }
     if (grid.x == 0 || grid.y == 0 || grid.z == 0) return RFP4_OK; // nothing to do
     void *params[] = {args};
-    return hip_check(hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, 0, s, params, nullptr),
+    return hip_check(hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, shmem, s, params, nullptr),
                      name);
 }
 
@@ -95,13 +95,14 @@ int rfp4_init(int device)
     Runtime *rt = new Runtime();
     rt->device = device;
     rt->num_cus = prop.multiProcessorCount;
+    rt->max_lds = (size_t)prop.sharedMemPerBlock;
     rc = hip_check(hipModuleLoadData(&rt->module, rfp4_hsaco_start), "hipModuleLoadData");
     if (rc) {
         delete rt;
         return rc;
     }
     // default workspace of the drop-in attn_decode
-    rt->attn_part_floats = (size_t)kAttnMaxHeads * kAttnMaxSplits * (128 + 2);
+    rt->attn_part_floats = (size_t)kAttnMaxHeads * kAttnMaxSplits * (128 + 4); // [m, l, -, -, acc[hd]]
     rc = hip_check(hipMalloc((void **)&rt->attn_part, rt->attn_part_floats * sizeof(float)), "hipMalloc(attn workspace)");
     if (!rc) rc = hip_check(hipMalloc((void **)&rt->attn_counters, kAttnMaxHeads * sizeof(uint32_t)), "hipMalloc(attn counters)");
     if (!rc) rc = hip_check(hipMemset(rt->attn_counters, 0, kAttnMaxHeads * sizeof(uint32_t)), "hipMemset");
@@ -205,36 +206,84 @@ int gemv_check(uint32_t n, uint32_t k, const void *w, const void *sc, const floa
     if (n == 0 || k == 0) return set_error(RFP4_E_SHAPE, "gemv: n=%u k=%u must be > 0", n, k);
     if (k % 32) return set_error(RFP4_E_SHAPE, "gemv: k=%u is not a multiple of the 32-element block", k);
     if (!aligned16(w) || !aligned16(x)) return set_error(RFP4_E_ALIGN, "gemv: w and x must be 16-byte aligned");
+    if (g_rt && (size_t)k * 4u + 256u > g_rt->max_lds)
+        return set_error(RFP4_E_CAPACITY, "gemv: k=%u activations (%u bytes) exceed the %zu-byte LDS plan", k, k * 4u, g_rt->max_lds);
     return RFP4_OK;
 }
 
-// Rows per wave: 4 by default; 8 for wide matrices where fewer, fuller
-// workgroups still fill the device.
-int gemv_rows_per_wave(uint32_t n_logical, int epi)
+// Forced variant for tests (0 = automatic); thread-local like the error text.
+static thread_local int t_force_r = 0, t_force_ns = -1;
+
+// Compiled (R, NS) variants; must match the table in kernels.hip.
+static bool gemv_has_ns(bool f32scale, int epi, int R, int ns)
 {
-    (void)epi;
-    if (n_logical >= 64u * 1024u) return 8;
-    return 4;
+    if (ns == 0) return true;
+    bool full = ns == 1 || ns == 2 || ns == 3 || ns == 4 || ns == 7;
+    if (f32scale) return R == 4 && full;
+    if (R == 2) return full;
+    if (R == 4) return epi == RFP4_EPI_SWIGLU ? (ns >= 1 && ns <= 3) : full;
+    if (R == 8) return epi != RFP4_EPI_SWIGLU && (ns == 1 || ns == 2);
+    return false;
+}
+
+// Rows per wave R and up-front K-slices NS for a GEMV launch.  NS = K/2048
+// rounded up whenever compiled (all loads in flight at once), else the slice
+// loop.  R = 4 by default; 8 for very wide matrices with short K (fewer,
+// fuller workgroups still fill the device); 2 where 4 rows x NS slices would
+// not fit the register file.
+GemvVariant gemv_variant(uint32_t n, uint32_t k, int epi, bool f32scale)
+{
+    int ns_needed = (int)((k + 2047u) / 2048u);
+    int R = 4;
+    if (!f32scale) {
+        if (epi == RFP4_EPI_SWIGLU && ns_needed > 3) R = 2;
+        else if (epi != RFP4_EPI_SWIGLU && n >= 65536u && ns_needed <= 2) R = 8;
+    }
+    if (t_force_r) R = t_force_r;
+    int ns = gemv_has_ns(f32scale, epi, R, ns_needed) ? ns_needed : 0;
+    if (t_force_ns >= 0) ns = t_force_ns;
+    return GemvVariant{R, ns};
 }
 
 int gemv_launch(const char *scale_name, int epi, const GemvArgs &args, hipStream_t s, int r_override)
 {
     static const char *epi_names[] = {"store", "resid", "swiglu", "argmax"};
-    int R = r_override ? r_override : gemv_rows_per_wave(args.n, epi);
+    const bool f32scale = scale_name[0] == 'f';
+    GemvVariant v = gemv_variant(args.n, args.k, epi, f32scale);
+    if (r_override) v.R = r_override;
+    if (!gemv_has_ns(f32scale, epi, v.R, v.NS))
+        return set_error(RFP4_E_INVALID, "gemv: no compiled variant R=%d NS=%d for %s/%s", v.R, v.NS, scale_name,
+                         epi_names[epi]);
+    if (v.NS > 0 && (uint32_t)v.NS * 2048u < args.k)
+        return set_error(RFP4_E_INVALID, "gemv: NS=%d slices cannot cover k=%u", v.NS, args.k);
     char name[64];
-    snprintf(name, sizeof name, "rfp4_gemv_%s_%s_r%d", scale_name, epi_names[epi], R);
-    uint32_t rows_per_block = 4u * (uint32_t)R;
+    snprintf(name, sizeof name, "rfp4_gemv_%s_%s_r%d_s%d", scale_name, epi_names[epi], v.R, v.NS);
+    uint32_t rows_per_block = 4u * (uint32_t)v.R;
     uint32_t blocks = (args.n + rows_per_block - 1) / rows_per_block;
     GemvArgs a = args;
-    return launch(name, dim3(blocks), dim3(256), s, &a);
+    return launch(name, dim3(blocks), dim3(256), s, &a, a.k * 4u);
 }
 
-uint32_t gemv_blocks(uint32_t n_logical, int epi, int r_override)
+uint32_t gemv_blocks(uint32_t n_logical, uint32_t k, int epi)
 {
-    int R = r_override ? r_override : gemv_rows_per_wave(n_logical, epi);
-    uint32_t rows_per_block = 4u * (uint32_t)R;
+    GemvVariant v = gemv_variant(n_logical, k, epi, false);
+    uint32_t rows_per_block = 4u * (uint32_t)v.R;
     return (n_logical + rows_per_block - 1) / rows_per_block;
 }
+
+} // namespace rfp4
+
+extern "C" int rfp4_debug_gemv_variant(int rows_per_wave, int slices)
+{
+    using namespace rfp4;
+    if (rows_per_wave != 0 && rows_per_wave != 2 && rows_per_wave != 4 && rows_per_wave != 8)
+        return set_error(RFP4_E_INVALID, "rows_per_wave must be 0, 2, 4 or 8");
+    t_force_r = rows_per_wave;
+    t_force_ns = slices;
+    return RFP4_OK;
+}
+
+namespace rfp4 {
 
 int attn_launch(const AttnArgs &args, int kv_f16, hipStream_t s, uint32_t max_seq_for_grid)
 {
@@ -242,20 +291,32 @@ int attn_launch(const AttnArgs &args, int kv_f16, hipStream_t s, uint32_t max_se
     if (args.head_dim == 64) name = kv_f16 ? "rfp4_attn_hd64_f16" : "rfp4_attn_hd64_f32";
     else if (args.head_dim == 128) name = kv_f16 ? "rfp4_attn_hd128_f16" : "rfp4_attn_hd128_f32";
     else return set_error(RFP4_E_SHAPE, "attn: head_dim %u unsupported (64 or 128)", args.head_dim);
+    if (args.chunk == 0 || args.chunk > attn_max_chunk(args.head_dim, kv_f16 ? 2u : 4u))
+        return set_error(RFP4_E_CAPACITY, "attn: chunk %u exceeds the kernel's plan", args.chunk);
+    if (args.cosv && !kv_f16) return set_error(RFP4_E_INVALID, "attn: fused KV append needs an fp16 cache");
     uint32_t splits = (max_seq_for_grid + args.chunk - 1) / args.chunk;
     AttnArgs a = args;
     return launch(name, dim3(a.n_kv_heads, splits), dim3(256), s, &a);
 }
 
-uint32_t attn_chunk_for(uint32_t n_kv_heads, uint32_t seq, uint32_t num_cus)
+uint32_t attn_max_chunk(uint32_t head_dim, uint32_t elem_bytes)
+{
+    // tokens per workgroup step (256 threads / lanes per 16-byte-split row)
+    // times the 8 load steps each thread keeps in registers
+    uint32_t lanes_per_row = head_dim * elem_bytes / 16u;
+    return (256u / lanes_per_row) * 8u;
+}
+
+uint32_t attn_chunk_for(uint32_t n_kv_heads, uint32_t seq, uint32_t num_cus, uint32_t head_dim, uint32_t elem_bytes)
 {
     // Enough (kv head, split) workgroups to cover every CU about twice; the
-    // chunk is a power of two in [64, 256] tokens so that a cache allocated in
+    // chunk is a power of two in [64, max] tokens so that a cache allocated in
     // whole 256-token pages always holds chunk * splits tokens.
     uint32_t target_wg = 2u * num_cus;
     uint32_t splits_wanted = (target_wg + n_kv_heads - 1) / n_kv_heads;
-    uint32_t chunk = 64u;
-    while (chunk < 256u && (uint64_t)chunk * splits_wanted < seq) chunk *= 2u;
+    uint32_t cap = attn_max_chunk(head_dim, elem_bytes);
+    uint32_t chunk = 64u < cap ? 64u : cap;
+    while (chunk < cap && (uint64_t)chunk * splits_wanted < seq) chunk *= 2u;
     return chunk;
 }
 
@@ -269,7 +330,7 @@ int fp4_gemv(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint32_t *w, co
 {
     int rc = gemv_check(n, k, w, scales, x, y);
     if (rc) return rc;
-    GemvArgs a{w, scales, x, y, nullptr, n, k, 0, 0};
+    GemvArgs a{w, scales, x, y, nullptr, nullptr, n, k, 0, 0.0f};
     return gemv_launch("f32", RFP4_EPI_STORE, a, (hipStream_t)stream, 0);
 }
 
@@ -278,7 +339,17 @@ int mx4_gemv(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_t *codes,
 {
     int rc = gemv_check(n, k, codes, scales, x, y);
     if (rc) return rc;
-    GemvArgs a{codes, scales, x, y, nullptr, n, k, 0, 0};
+    GemvArgs a{codes, scales, x, y, nullptr, nullptr, n, k, 0, 0.0f};
+    return gemv_launch("e8m0", RFP4_EPI_STORE, a, (hipStream_t)stream, 0);
+}
+
+int mx4_gemv_rmsnorm(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_t *codes, const uint8_t *scales,
+                     const float *x, const uint16_t *norm_w, float eps, float *y)
+{
+    int rc = gemv_check(n, k, codes, scales, x, y);
+    if (rc) return rc;
+    if (!norm_w) return set_error(RFP4_E_INVALID, "gemv_rmsnorm: null norm weights");
+    GemvArgs a{codes, scales, x, y, nullptr, norm_w, n, k, 0, eps};
     return gemv_launch("e8m0", RFP4_EPI_STORE, a, (hipStream_t)stream, 0);
 }
 
@@ -287,7 +358,7 @@ int mx4_gemv_residual(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_
 {
     int rc = gemv_check(n, k, codes, scales, x, x_res);
     if (rc) return rc;
-    GemvArgs a{codes, scales, x, x_res, nullptr, n, k, 0, 0};
+    GemvArgs a{codes, scales, x, x_res, nullptr, nullptr, n, k, 0, 0.0f};
     return gemv_launch("e8m0", RFP4_EPI_RESIDUAL, a, (hipStream_t)stream, 0);
 }
 
@@ -297,11 +368,11 @@ int mx4_gemv_swiglu(rfp4_stream_t stream, uint32_t n, uint32_t k, uint32_t pair_
     int rc = gemv_check(n, k, codes, scales, x, out);
     if (rc) return rc;
     if (pair_off < n) return set_error(RFP4_E_SHAPE, "gemv_swiglu: pair_off %u overlaps the %u gate rows", pair_off, n);
-    GemvArgs a{codes, scales, x, out, nullptr, n, k, pair_off, 0};
+    GemvArgs a{codes, scales, x, out, nullptr, nullptr, n, k, pair_off, 0.0f};
     return gemv_launch("e8m0", RFP4_EPI_SWIGLU, a, (hipStream_t)stream, 0);
 }
 
-size_t mx4_gemv_argmax_workspace(uint32_t n) { return (size_t)gemv_blocks(n, RFP4_EPI_ARGMAX, 0) * 8u + 64u; }
+size_t mx4_gemv_argmax_workspace(uint32_t n) { return ((size_t)n + 7u) / 8u * 8u + 64u; /* >= one key per 8 rows */ }
 
 int mx4_gemv_argmax(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_t *codes, const uint8_t *scales,
                     const float *x, float *y, void *workspace, uint32_t *best_token)
@@ -310,12 +381,12 @@ int mx4_gemv_argmax(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_t 
     if (rc) return rc;
     if (!workspace || !best_token) return set_error(RFP4_E_INVALID, "gemv_argmax: null workspace or output");
     unsigned long long *best = (unsigned long long *)workspace;
-    GemvArgs a{codes, scales, x, y, best, n, k, 0, 0};
+    GemvArgs a{codes, scales, x, y, best, nullptr, n, k, 0, 0.0f};
     rc = gemv_launch("e8m0", RFP4_EPI_ARGMAX, a, (hipStream_t)stream, 0);
     if (rc) return rc;
     // reduce the per-workgroup keys with the step kernel on a scratch cursor
     // that lives after the keys (no ids are written: ids_cap = 0).
-    uint32_t nb = gemv_blocks(n, RFP4_EPI_ARGMAX, 0);
+    uint32_t nb = gemv_blocks(n, k, RFP4_EPI_ARGMAX);
     StepState *st = (StepState *)((char *)workspace + (size_t)nb * 8u);
     rc = fill_words((uint32_t *)st, sizeof(StepState) / 4, 0u, (hipStream_t)stream);
     if (rc) return rc;
@@ -373,13 +444,15 @@ static int attn_common(hipStream_t s, uint32_t nh, uint32_t nkv, uint32_t hd, ui
     if (nh / nkv > 8) return set_error(RFP4_E_SHAPE, "attn_decode: GQA group %u > 8", nh / nkv);
     if (seq == 0) return set_error(RFP4_E_SHAPE, "attn_decode: seq must be >= 1");
     if (nh > kAttnMaxHeads) return set_error(RFP4_E_CAPACITY, "attn_decode: %u heads > %u", nh, kAttnMaxHeads);
-    uint32_t chunk = attn_chunk_for(nkv, seq, rt->num_cus);
+    uint32_t eb = f16 ? 2u : 4u;
+    if (((uintptr_t)kc | (uintptr_t)vc) & 15u || (ts * eb) % 16u || (hs * eb) % 16u)
+        return set_error(RFP4_E_ALIGN, "attn_decode: K/V rows must start 16-byte aligned (strides %llu, %llu)",
+                         (unsigned long long)ts, (unsigned long long)hs);
+    uint32_t chunk = attn_chunk_for(nkv, seq, rt->num_cus, hd, eb);
     uint32_t splits = (seq + chunk - 1) / chunk;
-    if (splits > kAttnMaxSplits) {
-        chunk = 256;
-        splits = (seq + chunk - 1) / chunk;
-        if (splits > kAttnMaxSplits) return set_error(RFP4_E_CAPACITY, "attn_decode: seq %u too long for the default workspace", seq);
-    }
+    if (splits > kAttnMaxSplits)
+        return set_error(RFP4_E_CAPACITY, "attn_decode: seq %u needs %u splits of %u tokens (> %u)", seq, splits, chunk,
+                         kAttnMaxSplits);
     AttnArgs a{};
     a.q = q; a.kc = kc; a.vc = vc; a.out = out;
     a.part = rt->attn_part; a.counters = rt->attn_counters; a.pos_ptr = nullptr;

@@ -11,7 +11,7 @@
 namespace rfp4 {
 
 constexpr uint32_t kAttnMaxHeads = 128;
-constexpr uint32_t kAttnMaxSplits = 256;
+constexpr uint32_t kAttnMaxSplits = 512;
 
 struct Runtime {
     int device = 0;
@@ -21,20 +21,25 @@ struct Runtime {
     float *attn_part = nullptr;       // default split-K workspace of attn_decode
     uint32_t *attn_counters = nullptr;
     size_t attn_part_floats = 0;
+    size_t max_lds = 65536;           // LDS bytes per workgroup
 };
 
 Runtime *runtime();
 int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 int hip_check(hipError_t e, const char *what);
-int launch(const char *name, dim3 grid, dim3 block, hipStream_t s, void *args);
+int launch(const char *name, dim3 grid, dim3 block, hipStream_t s, void *args, unsigned shmem = 0);
 
 int fill_words(uint32_t *p, uint64_t n_words, uint32_t value, hipStream_t s);
 int gemv_check(uint32_t n, uint32_t k, const void *w, const void *sc, const float *x, const float *y);
-int gemv_rows_per_wave(uint32_t n_logical, int epi);
+struct GemvVariant {
+    int R, NS;
+};
+GemvVariant gemv_variant(uint32_t n, uint32_t k, int epi, bool f32scale);
 int gemv_launch(const char *scale_name, int epi, const GemvArgs &args, hipStream_t s, int r_override);
-uint32_t gemv_blocks(uint32_t n_logical, int epi, int r_override);
+uint32_t gemv_blocks(uint32_t n_logical, uint32_t k, int epi);
 int attn_launch(const AttnArgs &args, int kv_f16, hipStream_t s, uint32_t max_seq_for_grid);
-uint32_t attn_chunk_for(uint32_t n_kv_heads, uint32_t seq, uint32_t num_cus);
+uint32_t attn_max_chunk(uint32_t head_dim, uint32_t elem_bytes);
+uint32_t attn_chunk_for(uint32_t n_kv_heads, uint32_t seq, uint32_t num_cus, uint32_t head_dim, uint32_t elem_bytes);
 
 // sigma / sqrt((65536^2 - 1)/3): the Irwin-Hall(4) normal coefficient shared
 // with every host generator of the synthetic init.

@@ -22,10 +22,11 @@ typedef struct GemvArgs {
     const float *x;       // activation, K floats
     float *y;             // output (see epilogue)
     unsigned long long *best; // ARGMAX: one packed key per workgroup
+    const uint16_t *norm_w;   // optional fp16 RMSNorm weights: x -> x*rms*w first
     uint32_t n;           // logical output rows
     uint32_t k;           // reduction length, multiple of 32
     uint32_t pair_off;    // SWIGLU: physical row offset of the up rows
-    uint32_t pad;
+    float eps;            // RMSNorm epsilon (with norm_w)
 } GemvArgs;
 
 typedef struct RmsnormArgs {
@@ -79,6 +80,11 @@ typedef struct AttnArgs {
     float *part;          // workspace: [n_heads][max_splits][head_dim + 2]
     uint32_t *counters;   // workspace: [n_kv_heads], zero between calls
     const int32_t *pos_ptr; // if non-null, seq = *pos_ptr + 1
+    // Fused RoPE + fp16 KV append (null cosv = off): q is un-rotated, the
+    // current token (position seq-1) has un-rotated k_new and v_new
+    // ([n_kv_heads][head_dim]); tables are [pos][head_dim/2].
+    const float *cosv, *sinv;
+    const float *k_new, *v_new;
     uint64_t ts, hs;      // token and head strides (elements)
     uint32_t n_heads, n_kv_heads, head_dim, seq;
     uint32_t chunk, max_splits;

@@ -64,6 +64,7 @@ _SIGS = {
     "rfp4_event_elapsed_ms": (I32, [C.POINTER(F32), P, P]),
     "fp4_gemv": (I32, [P, U32, U32, P, P, P, P]),
     "mx4_gemv": (I32, [P, U32, U32, P, P, P, P]),
+    "mx4_gemv_rmsnorm": (I32, [P, U32, U32, P, P, P, P, F32, P]),
     "mx4_gemv_residual": (I32, [P, U32, U32, P, P, P, P]),
     "mx4_gemv_swiglu": (I32, [P, U32, U32, U32, P, P, P, P]),
     "mx4_gemv_argmax_workspace": (SZ, [U32]),
@@ -83,6 +84,7 @@ _SIGS = {
     "rfp4_mma_tile16": (I32, [P, P, P, P, P, P]),
     "rfp4_mma_tile32": (I32, [P, P, P, P, P, P]),
     "rfp4_selftest_cvt_fp4": (I32, [P, U32, P, P]),
+    "rfp4_debug_gemv_variant": (I32, [I32, I32]),
     "rfp4_synth_mx_weight": (I32, [P, U64, U64, F32, U64, U64, U64, P, P]),
     "rfp4_synth_f16": (I32, [P, U64, U64, F32, F32, U64, P]),
     "llama_engine_create": (I32, [C.POINTER(ModelConfig), U64, C.POINTER(P)]),
@@ -262,6 +264,10 @@ def fp4_gemv(stream, n, k, w, scales, x, y):
 
 def mx4_gemv(stream, n, k, codes, scales, x, y):
     check(load().mx4_gemv(_s(stream), n, k, _p(codes), _p(scales), _p(x), _p(y)))
+
+
+def mx4_gemv_rmsnorm(stream, n, k, codes, scales, x, norm_w, eps, y):
+    check(load().mx4_gemv_rmsnorm(_s(stream), n, k, _p(codes), _p(scales), _p(x), _p(norm_w), eps, _p(y)))
 
 
 def mx4_gemv_residual(stream, n, k, codes, scales, x, x_res):

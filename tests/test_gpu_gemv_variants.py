@@ -1,0 +1,91 @@
+"""Every compiled GEMV variant (rows per wave x up-front K-slices) and the
+fused RMSNorm prologue, against the oracle."""
+import numpy as np
+import pytest
+
+from conftest import reference_rel_err
+from test_gpu_kernels import _assert_gemv_close, _config1, _dev
+
+pytestmark = pytest.mark.gpu
+
+_VARIANTS = {  # epilogue -> {R: compiled NS}; mirrors kernels.hip and runtime.cpp gemv_has_ns
+    "store": {2: (0, 1, 2, 3, 4, 7), 4: (0, 1, 2, 3, 4, 7), 8: (0, 1, 2)},
+    "resid": {2: (0, 1, 2, 3, 4, 7), 4: (0, 1, 2, 3, 4, 7), 8: (0, 1, 2)},
+    "argmax": {2: (0, 1, 2, 3, 4, 7), 4: (0, 1, 2, 3, 4, 7), 8: (0, 1, 2)},
+    "swiglu": {2: (0, 1, 2, 3, 4, 7), 4: (0, 1, 2, 3)},
+}
+
+
+def _force(rf, r, ns):
+    rf.check(rf.load().rfp4_debug_gemv_variant(r, ns))
+
+
+@pytest.mark.parametrize("epi", ["store", "resid", "argmax", "swiglu"])
+@pytest.mark.parametrize("k", [96, 2048, 4096, 5632, 14336])
+def test_gemv_all_variants(rf, orc, stream, epi, k):
+    n = 67  # not a multiple of any workgroup row count
+    codes, scales, x = _config1(orc, 2 * n, k, seed=k + len(epi))
+    dc, ds, dx = _dev(rf, codes, stream), _dev(rf, scales, stream), _dev(rf, x, stream)
+    full = orc.gemv_e8m0(2 * n, k, codes, scales, x)
+    f64, absf = orc.gemv_e8m0_f64(2 * n, k, codes, scales, x)
+    need = (k + 2047) // 2048
+    base = np.linspace(-1, 1, n).astype(np.float32)
+    ran = 0
+    try:
+        for r, nss in _VARIANTS[epi].items():
+            for ns in nss:
+                if ns not in (0, need):
+                    continue
+                _force(rf, r, ns)
+                dy = _dev(rf, base, stream)
+                best = None
+                if epi == "store":
+                    rf.mx4_gemv(stream, n, k, dc, ds, dx, dy)
+                elif epi == "resid":
+                    rf.mx4_gemv_residual(stream, n, k, dc, ds, dx, dy)
+                elif epi == "argmax":
+                    ws = rf.DeviceBuffer(rf.mx4_gemv_argmax_workspace(n))
+                    best = rf.DeviceBuffer.zeroed(1, np.uint32, stream)
+                    rf.mx4_gemv_argmax(stream, n, k, dc, ds, dx, dy, ws, best)
+                else:
+                    rf.mx4_gemv_swiglu(stream, n, k, n, dc, ds, dx, dy)
+                got = dy.to_host(n, np.float32, stream)
+                tag = f"{epi} R={r} NS={ns} k={k}"
+                if epi in ("store", "argmax"):
+                    _assert_gemv_close(got, full[:n], f64[:n], absf[:n])
+                elif epi == "resid":
+                    # x + W.x: the GEMV's normwise bound carries through the add
+                    err = np.abs(got.astype(np.float64) - (f64[:n] + base))
+                    assert np.all(err <= 1e-5 * (absf[:n] + np.abs(base)) + 1e-30), tag
+                else:
+                    # silu(g)*u: |d| <= |silu'(g)| |dg| |u| + |silu(g)| |du|, |silu'| < 1.1
+                    g, u = f64[:n], f64[n:]
+                    silu = g / (1 + np.exp(-g))
+                    bound = 1e-5 * (1.1 * absf[:n] * np.abs(u) + np.abs(silu) * absf[n:]) + 1e-30
+                    assert np.all(np.abs(got - silu * u) <= bound), tag
+                if best is not None:
+                    assert int(best.to_host(1, np.uint32, stream)[0]) == orc.argmax(got), tag
+                ran += 1
+    finally:
+        _force(rf, 0, -1)
+    assert ran >= 2
+
+
+@pytest.mark.parametrize("n,k", [(6144, 4096), (2560, 2048), (100, 14336)])
+def test_gemv_fused_rmsnorm(rf, orc, stream, n, k):
+    """rmsnorm + fp4_gemv in one launch (llama_run/src/main.rs:513-514)."""
+    codes, scales, _ = _config1(orc, n, k, seed=n)
+    rng = np.random.default_rng(k)
+    x = (0.02 * rng.standard_normal(k)).astype(np.float32)
+    w16 = (1 + 0.02 * rng.standard_normal(k)).astype(np.float16)
+    h = orc.rmsnorm(x, w16.astype(np.float32), 1e-5)
+    f64, absf = orc.gemv_e8m0_f64(n, k, codes, scales, h)
+    dy = rf.DeviceBuffer.zeroed(n, np.float32, stream)
+    rf.mx4_gemv_rmsnorm(stream, n, k, _dev(rf, codes, stream), _dev(rf, scales, stream), _dev(rf, x, stream),
+                        _dev(rf, w16.view(np.uint16), stream), 1e-5, dy)
+    got = dy.to_host(n, np.float32, stream)
+    # the fused norm sums x^2 in another order than the oracle: its rms may
+    # differ in the last place, which the normwise bound absorbs
+    cond = np.abs(got.astype(np.float64) - f64) / np.maximum(absf, 1e-300)
+    assert cond.max() < 1e-5, cond.max()
+    assert (reference_rel_err(got, f64) > 1e-2).sum() == 0
