@@ -54,6 +54,8 @@ int rfp4_version(void);
 /* CudaContext::new(device) + kernels::load(&ctx): llama_run/src/main.rs:432,488 */
 int rfp4_init(int device);
 int rfp4_device_count(int *count);
+/* Compute units, LDS bytes per workgroup and peak clock of the initialised device. */
+int rfp4_device_info(int *num_cus, size_t *lds_per_block, int *clock_khz);
 /* ctx.default_stream(): llama_run/src/main.rs:433 (here: a new HIP stream) */
 int rfp4_stream_create(rfp4_stream_t *stream);
 int rfp4_stream_destroy(rfp4_stream_t stream);
@@ -157,8 +159,20 @@ int rfp4_mma_tile32(rfp4_stream_t stream, const uint32_t *a, const uint32_t *b, 
  * (rows per wave 2/4/8, up-front K-slices or 0 for the slice loop;
  * 0, -1 = automatic).  No reference counterpart. */
 int rfp4_debug_gemv_variant(int rows_per_wave, int slices);
+/* Test hook: GEMV implementation of later launches on this thread: 0 = auto
+ * (matrix-core kernel for E8M0 scales and k % 128 == 0, else VALU), 1 = VALU
+ * kernel, 2 = matrix-core kernel (rows_per_wave then means 16-row tiles per
+ * wave, slices the super-chunks per wave).  No reference counterpart. */
+int rfp4_debug_gemv_path(int path);
 /* Hardware E2M1 conversion of n words (8 codes each) to 8n floats. */
 int rfp4_selftest_cvt_fp4(rfp4_stream_t stream, uint32_t n, const uint32_t *words, float *out);
+/* Hardware E2M1 -> bf16 conversion with a per-word f32 scale: out[4i+s] =
+ * packed bf16 pair of byte s of words[i] times scales[i]. */
+int rfp4_selftest_cvt_bf16(rfp4_stream_t stream, uint32_t n, const uint32_t *words, const float *scales,
+                           uint32_t *out);
+/* One v_mfma_f32_16x16x32_bf16 from raw per-lane registers (4 dwords per
+ * lane for a and b); out receives 4 accumulator floats per lane. */
+int rfp4_mma_bf16_tile(rfp4_stream_t stream, const uint32_t *a, const uint32_t *b, float *out);
 /* Synthetic weight generator used by the engine (rows [r0, r0+nrows)). */
 int rfp4_synth_mx_weight(rfp4_stream_t stream, uint64_t seed, uint64_t stream_id, float sigma, uint64_t k,
                          uint64_t r0, uint64_t nrows, uint8_t *codes, uint8_t *scales);

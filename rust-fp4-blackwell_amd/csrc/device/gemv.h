@@ -61,6 +61,46 @@ RFP4_DEV void stage_x(float *xs, const float *x, uint32_t k, const uint16_t *nor
     __syncthreads();
 }
 
+// stage_x from registers (XV float4 of x and uint2 of fp16 norm weights per
+// thread, element 4*(tid + 256*v) + j, zero past K).
+template <int XV>
+RFP4_DEV void stage_x_regs(float *xs, const float4 *xr, const uint2 *wr, uint32_t k, bool norm, float eps)
+{
+    __shared__ float red[4];
+    const int tid = threadIdx.x;
+    const uint32_t k4 = k >> 2;
+    float rms = 1.0f;
+    if (norm) {
+        float ss = 0.0f;
+#pragma unroll
+        for (int v = 0; v < XV; v++) {
+            ss = __fadd_rn(ss, __fmul_rn(xr[v].x, xr[v].x));
+            ss = __fadd_rn(ss, __fmul_rn(xr[v].y, xr[v].y));
+            ss = __fadd_rn(ss, __fmul_rn(xr[v].z, xr[v].z));
+            ss = __fadd_rn(ss, __fmul_rn(xr[v].w, xr[v].w));
+        }
+        ss = wave_sum(ss);
+        if ((tid & 63) == 0) red[tid >> 6] = ss;
+        __syncthreads();
+        float total = (red[0] + red[1]) + (red[2] + red[3]);
+        rms = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(total, (float)k), eps)));
+    }
+#pragma unroll
+    for (int v = 0; v < XV; v++) {
+        const uint32_t i4 = (uint32_t)tid + 256u * (uint32_t)v;
+        if (i4 >= k4) break;
+        float4 o = xr[v];
+        if (norm) {
+            o.x = __fmul_rn(__fmul_rn(o.x, rms), f16_bits_to_f32((uint16_t)(wr[v].x & 0xFFFFu)));
+            o.y = __fmul_rn(__fmul_rn(o.y, rms), f16_bits_to_f32((uint16_t)(wr[v].x >> 16)));
+            o.z = __fmul_rn(__fmul_rn(o.z, rms), f16_bits_to_f32((uint16_t)(wr[v].y & 0xFFFFu)));
+            o.w = __fmul_rn(__fmul_rn(o.w, rms), f16_bits_to_f32((uint16_t)(wr[v].y >> 16)));
+        }
+        ((float4 *)xs)[i4] = o;
+    }
+    __syncthreads();
+}
+
 // Raw scale bits now, value at use: keeps the loads free of dependent ALU
 // work so they can all be in flight together.
 template <int SCALE_F32>
@@ -111,9 +151,21 @@ RFP4_DEV void gemv_body(const GemvArgs &a)
     for (int p = 0; p < NP; p++) acc[p] = 0.0f;
 
     if (NS > 0) {
-        // Every load of this wave (NS slices x NP rows) is issued before x is
-        // staged: one memory round trip, straight-line code.  A lane past the
+        // x (and norm weights) go into registers first, then every weight load
+        // of this wave (NS slices x NP rows): waiting for x then never waits
+        // for the weights (vmcnt retires in issue order).  A lane past the
         // last chunk re-reads the last chunk (in bounds) and gets scale 0.
+        constexpr int XV = NS > 0 ? 2 * NS : 1; // float4 of x per thread: K <= 2048 * NS
+        float4 xr[XV];
+        uint2 wr[XV];
+        const bool norm = a.norm_w != nullptr;
+#pragma unroll
+        for (int v = 0; v < XV; v++) {
+            const uint32_t i4 = threadIdx.x + 256u * (uint32_t)v;
+            const bool in = i4 < (a.k >> 2);
+            xr[v] = in ? ((const float4 *)a.x)[i4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            wr[v] = (in && norm) ? ((const uint2 *)a.norm_w)[i4] : make_uint2(0, 0);
+        }
         uint4 q[NS > 0 ? NS : 1][NP];
         uint32_t sb[NS > 0 ? NS : 1][NP];
 #pragma unroll
@@ -125,7 +177,7 @@ RFP4_DEV void gemv_body(const GemvArgs &a)
                 sb[s][p] = load_scale_bits<SCALE_F32>(a.scales, srow[p] + cl);
             }
         }
-        stage_x(xs, a.x, a.k, a.norm_w, a.eps);
+        stage_x_regs<XV>(xs, xr, wr, a.k, norm, a.eps);
 #pragma unroll
         for (int s = 0; s < NS; s++) {
             const uint32_t c = (uint32_t)lane + 64u * (uint32_t)s;

@@ -49,6 +49,37 @@ RFP4_DEV void mma32_tile_body(const MmaTileArgs &a)
     for (int r = 0; r < 16; r++) a.out[lane * 16 + r] = acc[r];
 }
 
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+
+// One v_mfma_f32_16x16x32_bf16 from raw per-lane registers: a, b hold 4
+// dwords (8 bf16) per lane; out receives the 4 accumulator floats per lane.
+RFP4_DEV void mma_bf16_tile_body(const MmaTileArgs &a)
+{
+    const int lane = threadIdx.x & 63;
+    uint4 ar = ((const uint4 *)a.a)[lane], br = ((const uint4 *)a.b)[lane];
+    bf16x8_t av = __builtin_bit_cast(bf16x8_t, ar), bv = __builtin_bit_cast(bf16x8_t, br);
+    v4f32 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 4; r++) a.out[lane * 4 + r] = acc[r];
+}
+
+// Hardware E2M1 -> bf16 conversion with a per-lane f32 scale: out word i*4+s
+// = packed bf16 pair of byte s of in[i], converted with scale[i].
+RFP4_DEV void selftest_cvt_bf16_body(const SelftestArgs &a)
+{
+    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= a.n) return;
+    uint32_t w = a.in[i];
+    float s = a.scale[i];
+    uint32_t *o = (uint32_t *)a.out + (size_t)i * 4;
+    o[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 0));
+    o[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 1));
+    o[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 2));
+    o[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 3));
+}
+
 // All-ones known answer (fp4_mma/src/main.rs:24-31): A = B = 1.0 (E2M1 0x2)
 // over K = 128 with the A scale 2^-1 (E8M0 0x7E) and B scale 1.0 (0x7F), so
 // every element is 128 * 0.5 = 64.0, the reference's expected value.  Writes

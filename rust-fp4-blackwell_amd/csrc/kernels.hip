@@ -4,6 +4,7 @@
 // value (shared/kernel_args.h).
 #include "device/common.h"
 #include "device/gemv.h"
+#include "device/gemv_mfma.h"
 #include "device/norm_rope.h"
 #include "device/attn.h"
 #include "device/misc.h"
@@ -43,6 +44,30 @@ GEMV_NS_SHORT(e8m0, 0, swiglu, RFP4_EPI_SWIGLU, 4)
 GEMV_KERNEL(e8m0, 0, swiglu, RFP4_EPI_SWIGLU, 4, 3)
 GEMV_NS_FULL(f32, 1, store, RFP4_EPI_STORE, 4)
 
+// ---- MFMA GEMV: rfp4_gemvm_<epilogue>_t<RT>_s<NSC>
+// (RT 16-row tiles per wave, NSC = ceil(K/512) super-chunks per wave issued
+// up front, 0 = loop).  Host selection: runtime.cpp gemv_mfma_has.
+#define GEMVM_KERNEL(ENAME, EPI, RT, NSC) \
+    K256 void rfp4_gemvm_##ENAME##_t##RT##_s##NSC(GemvArgs a) { gemv_mfma_body<EPI, RT, NSC>(a); }
+#define GEMVM_LONG(ENAME, EPI, RT) \
+    GEMVM_KERNEL(ENAME, EPI, RT, 0) \
+    GEMVM_KERNEL(ENAME, EPI, RT, 4) \
+    GEMVM_KERNEL(ENAME, EPI, RT, 8) \
+    GEMVM_KERNEL(ENAME, EPI, RT, 11) \
+    GEMVM_KERNEL(ENAME, EPI, RT, 16) \
+    GEMVM_KERNEL(ENAME, EPI, RT, 28)
+#define GEMVM_SHORT(ENAME, EPI, RT) \
+    GEMVM_KERNEL(ENAME, EPI, RT, 0) \
+    GEMVM_KERNEL(ENAME, EPI, RT, 4) \
+    GEMVM_KERNEL(ENAME, EPI, RT, 8)
+
+GEMVM_LONG(store, RFP4_EPI_STORE, 1)
+GEMVM_SHORT(store, RFP4_EPI_STORE, 2)
+GEMVM_LONG(resid, RFP4_EPI_RESIDUAL, 1)
+GEMVM_SHORT(swiglu, RFP4_EPI_SWIGLU, 1)
+GEMVM_SHORT(argmax, RFP4_EPI_ARGMAX, 1)
+GEMVM_SHORT(argmax, RFP4_EPI_ARGMAX, 2)
+
 // ---- norm / rope / embed
 K1024 void rfp4_rmsnorm_f32w(RmsnormArgs a) { rmsnorm_body<0>(a); }
 K1024 void rfp4_rmsnorm_f16w(RmsnormArgs a) { rmsnorm_body<1>(a); }
@@ -75,3 +100,5 @@ K256 void rfp4_selftest_cvt(SelftestArgs a) { selftest_cvt_body(a); }
 K256 void rfp4_mma16_tile(MmaTileArgs a) { mma16_tile_body(a); }
 K256 void rfp4_mma32_tile(MmaTileArgs a) { mma32_tile_body(a); }
 K256 void rfp4_mma_allones(MmaTileArgs a) { mma_allones_body(a.out); }
+K256 void rfp4_mma_bf16_tile(MmaTileArgs a) { mma_bf16_tile_body(a); }
+K256 void rfp4_selftest_cvt_bf16(SelftestArgs a) { selftest_cvt_bf16_body(a); }

@@ -118,6 +118,18 @@ int rfp4_init(int device)
     return RFP4_OK;
 }
 
+int rfp4_device_info(int *num_cus, size_t *lds_per_block, int *clock_khz)
+{
+    if (!g_rt) return set_error(RFP4_E_NOT_INIT, "rfp4_init has not been called");
+    hipDeviceProp_t prop;
+    int rc = hip_check(hipGetDeviceProperties(&prop, g_rt->device), "hipGetDeviceProperties");
+    if (rc) return rc;
+    if (num_cus) *num_cus = prop.multiProcessorCount;
+    if (lds_per_block) *lds_per_block = prop.sharedMemPerBlock;
+    if (clock_khz) *clock_khz = prop.clockRate;
+    return RFP4_OK;
+}
+
 int rfp4_stream_create(rfp4_stream_t *stream)
 {
     if (!stream) return set_error(RFP4_E_INVALID, "null stream out");
@@ -245,39 +257,114 @@ GemvVariant gemv_variant(uint32_t n, uint32_t k, int epi, bool f32scale)
     return GemvVariant{R, ns};
 }
 
+// Path: 0 = automatic, 1 = VALU kernel, 2 = MFMA kernel (tests only).
+static thread_local int t_force_path = 0;
+
+// The MFMA kernel needs E8M0 scales (folded into the bf16 conversion), K in
+// whole 128-value super-chunks and the three bf16 planes of x in LDS.
+static bool gemv_mfma_ok(uint32_t k, bool f32scale)
+{
+    if (f32scale || k % 128u) return false;
+    return !g_rt || (size_t)k * 6u + 2048u <= g_rt->max_lds;
+}
+
+// Compiled MFMA variants; must match the table in kernels.hip.
+static bool gemv_mfma_has(int epi, int rt, int nsc)
+{
+    bool lng = nsc == 0 || nsc == 4 || nsc == 8 || nsc == 11 || nsc == 16 || nsc == 28;
+    bool sht = nsc == 0 || nsc == 4 || nsc == 8;
+    switch (epi) {
+    case RFP4_EPI_STORE: return rt == 1 ? lng : (rt == 2 && sht);
+    case RFP4_EPI_RESIDUAL: return rt == 1 && lng;
+    case RFP4_EPI_SWIGLU: return rt == 1 && sht;
+    default: return (rt == 1 || rt == 2) && sht;
+    }
+}
+
+struct GemvPlan {
+    bool mfma;
+    int R, NS;               // VALU: rows per wave, K slices; MFMA: 16-row tiles, super-chunks per wave
+    uint32_t rows_per_block;
+};
+
+static GemvPlan gemv_plan(uint32_t n, uint32_t k, int epi, bool f32scale)
+{
+    GemvPlan p{};
+    // Measured on MI355X (batch 1, weights streamed from HBM): the VALU
+    // kernel with registers-first staging beats the matrix-core kernel on
+    // every decode shape (e.g. 128256x4096: 50.6 vs 69.5 us), because the
+    // matrix-core path must also convert x into three bf16 planes per
+    // workgroup.  The matrix-core kernel stays selectable (path 2).
+    p.mfma = t_force_path == 2;
+    if (p.mfma) {
+        int rt = ((epi == RFP4_EPI_STORE || epi == RFP4_EPI_ARGMAX) && n >= 65536u) ? 2 : 1;
+        if (t_force_path == 2 && t_force_r) rt = t_force_r;
+        int per_wave = (int)(((k >> 7) + 3u) / 4u);
+        int ns = gemv_mfma_has(epi, rt, per_wave) ? per_wave : 0;
+        if (t_force_path == 2 && t_force_ns >= 0) ns = t_force_ns;
+        p.R = rt;
+        p.NS = ns;
+        p.rows_per_block = 16u * (uint32_t)rt;
+    } else {
+        GemvVariant v = gemv_variant(n, k, epi, f32scale);
+        p.R = v.R;
+        p.NS = v.NS;
+        p.rows_per_block = 4u * (uint32_t)v.R;
+    }
+    return p;
+}
+
 int gemv_launch(const char *scale_name, int epi, const GemvArgs &args, hipStream_t s, int r_override)
 {
     static const char *epi_names[] = {"store", "resid", "swiglu", "argmax"};
     const bool f32scale = scale_name[0] == 'f';
-    GemvVariant v = gemv_variant(args.n, args.k, epi, f32scale);
-    if (r_override) v.R = r_override;
-    if (!gemv_has_ns(f32scale, epi, v.R, v.NS))
-        return set_error(RFP4_E_INVALID, "gemv: no compiled variant R=%d NS=%d for %s/%s", v.R, v.NS, scale_name,
-                         epi_names[epi]);
-    if (v.NS > 0 && (uint32_t)v.NS * 2048u < args.k)
-        return set_error(RFP4_E_INVALID, "gemv: NS=%d slices cannot cover k=%u", v.NS, args.k);
+    GemvPlan p = gemv_plan(args.n, args.k, epi, f32scale);
     char name[64];
-    snprintf(name, sizeof name, "rfp4_gemv_%s_%s_r%d_s%d", scale_name, epi_names[epi], v.R, v.NS);
-    uint32_t rows_per_block = 4u * (uint32_t)v.R;
-    uint32_t blocks = (args.n + rows_per_block - 1) / rows_per_block;
+    unsigned shmem;
+    if (p.mfma) {
+        if (!gemv_mfma_ok(args.k, f32scale))
+            return set_error(RFP4_E_INVALID, "gemv: MFMA path needs E8M0 scales and k %% 128 == 0 (k=%u)", args.k);
+        if (!gemv_mfma_has(epi, p.R, p.NS) || (p.NS != 0 && p.NS != (int)(((args.k >> 7) + 3u) / 4u)))
+            return set_error(RFP4_E_INVALID, "gemv: no MFMA variant RT=%d NSC=%d for %s, k=%u", p.R, p.NS,
+                             epi_names[epi], args.k);
+        snprintf(name, sizeof name, "rfp4_gemvm_%s_t%d_s%d", epi_names[epi], p.R, p.NS);
+        shmem = args.k * 6u;
+    } else {
+        if (r_override) p.R = r_override, p.rows_per_block = 4u * (uint32_t)r_override;
+        if (!gemv_has_ns(f32scale, epi, p.R, p.NS))
+            return set_error(RFP4_E_INVALID, "gemv: no compiled variant R=%d NS=%d for %s/%s", p.R, p.NS,
+                             scale_name, epi_names[epi]);
+        if (p.NS > 0 && (uint32_t)p.NS * 2048u < args.k)
+            return set_error(RFP4_E_INVALID, "gemv: NS=%d slices cannot cover k=%u", p.NS, args.k);
+        snprintf(name, sizeof name, "rfp4_gemv_%s_%s_r%d_s%d", scale_name, epi_names[epi], p.R, p.NS);
+        shmem = args.k * 4u;
+    }
+    uint32_t blocks = (args.n + p.rows_per_block - 1) / p.rows_per_block;
     GemvArgs a = args;
-    return launch(name, dim3(blocks), dim3(256), s, &a, a.k * 4u);
+    return launch(name, dim3(blocks), dim3(256), s, &a, shmem);
 }
 
 uint32_t gemv_blocks(uint32_t n_logical, uint32_t k, int epi)
 {
-    GemvVariant v = gemv_variant(n_logical, k, epi, false);
-    uint32_t rows_per_block = 4u * (uint32_t)v.R;
-    return (n_logical + rows_per_block - 1) / rows_per_block;
+    GemvPlan p = gemv_plan(n_logical, k, epi, false);
+    return (n_logical + p.rows_per_block - 1) / p.rows_per_block;
 }
 
 } // namespace rfp4
 
+extern "C" int rfp4_debug_gemv_path(int path)
+{
+    using namespace rfp4;
+    if (path < 0 || path > 2) return set_error(RFP4_E_INVALID, "path must be 0 (auto), 1 (VALU) or 2 (MFMA)");
+    t_force_path = path;
+    return RFP4_OK;
+}
+
 extern "C" int rfp4_debug_gemv_variant(int rows_per_wave, int slices)
 {
     using namespace rfp4;
-    if (rows_per_wave != 0 && rows_per_wave != 2 && rows_per_wave != 4 && rows_per_wave != 8)
-        return set_error(RFP4_E_INVALID, "rows_per_wave must be 0, 2, 4 or 8");
+    if (rows_per_wave < 0 || rows_per_wave > 8)
+        return set_error(RFP4_E_INVALID, "rows_per_wave must be 0 (auto) or a compiled variant");
     t_force_r = rows_per_wave;
     t_force_ns = slices;
     return RFP4_OK;
@@ -537,8 +624,23 @@ int rfp4_mma_tile32(rfp4_stream_t stream, const uint32_t *a, const uint32_t *b, 
 int rfp4_selftest_cvt_fp4(rfp4_stream_t stream, uint32_t n, const uint32_t *words, float *out)
 {
     if (!words || !out) return set_error(RFP4_E_INVALID, "selftest_cvt: null pointer");
-    SelftestArgs a{words, out, n, 0};
+    SelftestArgs a{words, out, nullptr, n, 0};
     return launch("rfp4_selftest_cvt", dim3((n + 255) / 256), dim3(256), (hipStream_t)stream, &a);
+}
+
+int rfp4_selftest_cvt_bf16(rfp4_stream_t stream, uint32_t n, const uint32_t *words, const float *scales,
+                           uint32_t *out)
+{
+    if (!words || !scales || !out) return set_error(RFP4_E_INVALID, "selftest_cvt_bf16: null pointer");
+    SelftestArgs a{words, (float *)out, scales, n, 0};
+    return launch("rfp4_selftest_cvt_bf16", dim3((n + 255) / 256), dim3(256), (hipStream_t)stream, &a);
+}
+
+int rfp4_mma_bf16_tile(rfp4_stream_t stream, const uint32_t *a, const uint32_t *b, float *out)
+{
+    if (!a || !b || !out) return set_error(RFP4_E_INVALID, "mma_bf16_tile: null pointer");
+    MmaTileArgs args{a, b, nullptr, nullptr, out, 0, 0};
+    return launch("rfp4_mma_bf16_tile", dim3(1), dim3(64), (hipStream_t)stream, &args);
 }
 
 int rfp4_synth_mx_weight(rfp4_stream_t stream, uint64_t seed, uint64_t stream_id, float sigma, uint64_t k, uint64_t r0,

@@ -176,6 +176,7 @@ typedef struct MmaTileArgs {
 typedef struct SelftestArgs {
     const uint32_t *in;
     float *out;
+    const float *scale;   // per-word scale (bf16 conversion test)
     uint32_t n, pad;
 } SelftestArgs;
 

@@ -49,6 +49,7 @@ _SIGS = {
     "rfp4_version": (I32, []),
     "rfp4_init": (I32, [I32]),
     "rfp4_device_count": (I32, [C.POINTER(I32)]),
+    "rfp4_device_info": (I32, [C.POINTER(I32), C.POINTER(SZ), C.POINTER(I32)]),
     "rfp4_stream_create": (I32, [C.POINTER(P)]),
     "rfp4_stream_destroy": (I32, [P]),
     "rfp4_stream_synchronize": (I32, [P]),
@@ -85,6 +86,9 @@ _SIGS = {
     "rfp4_mma_tile32": (I32, [P, P, P, P, P, P]),
     "rfp4_selftest_cvt_fp4": (I32, [P, U32, P, P]),
     "rfp4_debug_gemv_variant": (I32, [I32, I32]),
+    "rfp4_debug_gemv_path": (I32, [I32]),
+    "rfp4_selftest_cvt_bf16": (I32, [P, U32, P, P, P]),
+    "rfp4_mma_bf16_tile": (I32, [P, P, P, P]),
     "rfp4_synth_mx_weight": (I32, [P, U64, U64, F32, U64, U64, U64, P, P]),
     "rfp4_synth_f16": (I32, [P, U64, U64, F32, F32, U64, P]),
     "llama_engine_create": (I32, [C.POINTER(ModelConfig), U64, C.POINTER(P)]),

@@ -16,8 +16,78 @@ _VARIANTS = {  # epilogue -> {R: compiled NS}; mirrors kernels.hip and runtime.c
 }
 
 
-def _force(rf, r, ns):
+_MFMA_VARIANTS = {  # epilogue -> {16-row tiles per wave: compiled super-chunks per wave}
+    "store": {1: (0, 4, 8, 11, 16, 28), 2: (0, 4, 8)},
+    "resid": {1: (0, 4, 8, 11, 16, 28)},
+    "swiglu": {1: (0, 4, 8)},
+    "argmax": {1: (0, 4, 8), 2: (0, 4, 8)},
+}
+
+
+def _force(rf, r, ns, path=1):
+    rf.check(rf.load().rfp4_debug_gemv_path(path if (r or ns >= 0) else 0))
     rf.check(rf.load().rfp4_debug_gemv_variant(r, ns))
+
+
+def _run_epi(rf, stream, epi, n, k, dc, ds, dx, base):
+    dy = _dev(rf, base, stream)
+    best = None
+    if epi == "store":
+        rf.mx4_gemv(stream, n, k, dc, ds, dx, dy)
+    elif epi == "resid":
+        rf.mx4_gemv_residual(stream, n, k, dc, ds, dx, dy)
+    elif epi == "argmax":
+        ws = rf.DeviceBuffer(rf.mx4_gemv_argmax_workspace(n))
+        best = rf.DeviceBuffer.zeroed(1, np.uint32, stream)
+        rf.mx4_gemv_argmax(stream, n, k, dc, ds, dx, dy, ws, best)
+    else:
+        rf.mx4_gemv_swiglu(stream, n, k, n, dc, ds, dx, dy)
+    got = dy.to_host(n, np.float32, stream)
+    return got, (int(best.to_host(1, np.uint32, stream)[0]) if best is not None else None)
+
+
+def _check_epi(orc, epi, got, best, n, full, f64, absf, base, tag):
+    if epi in ("store", "argmax"):
+        _assert_gemv_close(got, full[:n], f64[:n], absf[:n])
+    elif epi == "resid":
+        # x + W.x: the GEMV's normwise bound carries through the add
+        err = np.abs(got.astype(np.float64) - (f64[:n] + base))
+        assert np.all(err <= 1e-5 * (absf[:n] + np.abs(base)) + 1e-30), tag
+    else:
+        # silu(g)*u: |d| <= |silu'(g)| |dg| |u| + |silu(g)| |du|, |silu'| < 1.1
+        g, u = f64[:n], f64[n:]
+        silu = g / (1 + np.exp(-g))
+        bound = 1e-5 * (1.1 * absf[:n] * np.abs(u) + np.abs(silu) * absf[n:]) + 1e-30
+        assert np.all(np.abs(got - silu * u) <= bound), tag
+    if best is not None:
+        assert best == orc.argmax(got), tag
+
+
+@pytest.mark.parametrize("epi", ["store", "resid", "argmax", "swiglu"])
+@pytest.mark.parametrize("k", [128, 2048, 4096, 5632, 8192, 14336])
+def test_gemv_mfma_variants(rf, orc, stream, epi, k):
+    """Matrix-core GEMV: every compiled (tiles, super-chunks) variant that
+    covers k, plus the super-chunk loop."""
+    n = 67
+    codes, scales, x = _config1(orc, 2 * n, k, seed=3 * k + len(epi))
+    dc, ds, dx = _dev(rf, codes, stream), _dev(rf, scales, stream), _dev(rf, x, stream)
+    full = orc.gemv_e8m0(2 * n, k, codes, scales, x)
+    f64, absf = orc.gemv_e8m0_f64(2 * n, k, codes, scales, x)
+    per_wave = (k // 128 + 3) // 4
+    base = np.linspace(-1, 1, n).astype(np.float32)
+    ran = 0
+    try:
+        for rt, nss in _MFMA_VARIANTS[epi].items():
+            for ns in nss:
+                if ns not in (0, per_wave):
+                    continue
+                _force(rf, rt, ns, path=2)
+                got, best = _run_epi(rf, stream, epi, n, k, dc, ds, dx, base)
+                _check_epi(orc, epi, got, best, n, full, f64, absf, base, f"mfma {epi} RT={rt} NSC={ns} k={k}")
+                ran += 1
+    finally:
+        _force(rf, 0, -1, path=0)
+    assert ran >= 1
 
 
 @pytest.mark.parametrize("epi", ["store", "resid", "argmax", "swiglu"])
@@ -36,38 +106,12 @@ def test_gemv_all_variants(rf, orc, stream, epi, k):
             for ns in nss:
                 if ns not in (0, need):
                     continue
-                _force(rf, r, ns)
-                dy = _dev(rf, base, stream)
-                best = None
-                if epi == "store":
-                    rf.mx4_gemv(stream, n, k, dc, ds, dx, dy)
-                elif epi == "resid":
-                    rf.mx4_gemv_residual(stream, n, k, dc, ds, dx, dy)
-                elif epi == "argmax":
-                    ws = rf.DeviceBuffer(rf.mx4_gemv_argmax_workspace(n))
-                    best = rf.DeviceBuffer.zeroed(1, np.uint32, stream)
-                    rf.mx4_gemv_argmax(stream, n, k, dc, ds, dx, dy, ws, best)
-                else:
-                    rf.mx4_gemv_swiglu(stream, n, k, n, dc, ds, dx, dy)
-                got = dy.to_host(n, np.float32, stream)
-                tag = f"{epi} R={r} NS={ns} k={k}"
-                if epi in ("store", "argmax"):
-                    _assert_gemv_close(got, full[:n], f64[:n], absf[:n])
-                elif epi == "resid":
-                    # x + W.x: the GEMV's normwise bound carries through the add
-                    err = np.abs(got.astype(np.float64) - (f64[:n] + base))
-                    assert np.all(err <= 1e-5 * (absf[:n] + np.abs(base)) + 1e-30), tag
-                else:
-                    # silu(g)*u: |d| <= |silu'(g)| |dg| |u| + |silu(g)| |du|, |silu'| < 1.1
-                    g, u = f64[:n], f64[n:]
-                    silu = g / (1 + np.exp(-g))
-                    bound = 1e-5 * (1.1 * absf[:n] * np.abs(u) + np.abs(silu) * absf[n:]) + 1e-30
-                    assert np.all(np.abs(got - silu * u) <= bound), tag
-                if best is not None:
-                    assert int(best.to_host(1, np.uint32, stream)[0]) == orc.argmax(got), tag
+                _force(rf, r, ns, path=1)
+                got, best = _run_epi(rf, stream, epi, n, k, dc, ds, dx, base)
+                _check_epi(orc, epi, got, best, n, full, f64, absf, base, f"valu {epi} R={r} NS={ns} k={k}")
                 ran += 1
     finally:
-        _force(rf, 0, -1)
+        _force(rf, 0, -1, path=0)
     assert ran >= 2
 
 

@@ -1,0 +1,74 @@
+"""Pins the two gfx950 building blocks of the MFMA GEMV against the host:
+the hardware E2M1 -> bf16 conversion with an f32 block scale, and the
+v_mfma_f32_16x16x32_bf16 operand / accumulator lane layout."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+FP4V = np.array([0, 0.5, 1, 1.5, 2, 3, 4, 6], dtype=np.float32)
+
+
+def _e2m1(c):
+    return (-1.0 if c & 8 else 1.0) * FP4V[c & 7]
+
+
+def _bf16_bits(v):
+    """RNE f32 -> bf16 bits (host reference)."""
+    u = np.asarray(v, np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint32)
+    return r.astype(np.uint16)
+
+
+def test_cvt_fp4_to_bf16_with_scale(rf, stream):
+    """Low nibble -> low bf16; value = code * 2^exponent(scale): the hardware
+    uses only the exponent field of the f32 scale (1.5 acts as 1, 0.75 as
+    0.5), which is exactly an E8M0 scale when the scale is passed as the bits
+    b << 23."""
+    scales = [1.0, 2.0 ** -10, 2.0 ** 5, 1.5, 2.0 ** -100, 2.0 ** 100, 0.75]
+    exp_only = {1.5: 1.0, 0.75: 0.5}
+    words, sc = [], []
+    for s in scales:
+        for b in range(256):
+            words.append(b | (b << 8) | (b << 16) | (b << 24))
+            sc.append(s)
+    words = np.array(words, np.uint32)
+    sc = np.array(sc, np.float32)
+    n = words.size
+    dw = rf.DeviceBuffer.from_host(words, stream)
+    ds = rf.DeviceBuffer.from_host(sc, stream)
+    out = rf.DeviceBuffer.zeroed(4 * n, np.uint32, stream)
+    rf.check(rf.load().rfp4_selftest_cvt_bf16(stream.h, n, dw.ptr, ds.ptr, out.ptr))
+    got = out.to_host(4 * n, np.uint32, stream).reshape(n, 4)
+    eff = np.array([exp_only.get(float(s), float(s)) for s in sc], np.float32)
+    lo = np.array([_e2m1(int(w) & 0xF) for w in words], np.float32) * eff
+    hi = np.array([_e2m1((int(w) >> 4) & 0xF) for w in words], np.float32) * eff
+    for s in range(4):
+        np.testing.assert_array_equal(got[:, s] & 0xFFFF, _bf16_bits(lo), err_msg=f"sel {s} low")
+        np.testing.assert_array_equal(got[:, s] >> 16, _bf16_bits(hi), err_msg=f"sel {s} high")
+
+
+def test_mfma_bf16_16x16x32_layout(rf, stream):
+    """lane l: A row l%16 / B col l%16, K = 8*(l//16) + e (bf16 e in dword
+    e//2, low half first); accumulator r of lane l = D[4*(l//16)+r][l%16]."""
+    rng = np.random.default_rng(11)
+    A = rng.integers(-4, 5, (16, 32)).astype(np.float32)
+    B = rng.integers(-4, 5, (32, 16)).astype(np.float32)
+    D = A @ B
+    ra = np.zeros((64, 8), np.uint16)
+    rb = np.zeros((64, 8), np.uint16)
+    for lane in range(64):
+        for e in range(8):
+            k = 8 * (lane // 16) + e
+            ra[lane, e] = _bf16_bits(A[lane % 16, k])
+            rb[lane, e] = _bf16_bits(B[k, lane % 16])
+    out = rf.DeviceBuffer.zeroed(256, np.float32, stream)
+    da = rf.DeviceBuffer.from_host(ra.view(np.uint32), stream)
+    db = rf.DeviceBuffer.from_host(rb.view(np.uint32), stream)
+    rf.check(rf.load().rfp4_mma_bf16_tile(stream.h, da.ptr, db.ptr, out.ptr))
+    regs = out.to_host(256, np.float32, stream).reshape(64, 4)
+    got = np.zeros((16, 16), np.float32)
+    for lane in range(64):
+        for r in range(4):
+            got[4 * (lane // 16) + r, lane % 16] = regs[lane, r]
+    np.testing.assert_array_equal(got, D)
