@@ -1,0 +1,73 @@
+"""The C-ABI boundary on the CPU: the library loads, exports every function
+include/rfp4.h declares, validates arguments before touching a device, and
+is built without any link to the oracle.  No GPU compute calls."""
+import os
+import re
+import subprocess
+
+import pytest
+
+import rfp4
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+PKG = os.path.join(ROOT, "rust-fp4-blackwell_amd")
+
+
+def test_library_exports_every_declared_function():
+    lib = rfp4.load()
+    names = rfp4.header_functions()
+    assert len(names) > 40
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_binding_covers_the_header():
+    names = set(rfp4.header_functions())
+    assert names <= set(rfp4._SIGS), sorted(names - set(rfp4._SIGS))
+
+
+def test_reference_entry_points_present():
+    """The reference's kernel names (llama_run/src/main.rs:34-315,
+    fp4_mma/src/main.rs:19) are all exported under the same names."""
+    for n in ("fp4_gemv", "rmsnorm", "rope", "copy_into", "attn_decode", "swiglu", "residual", "argmax",
+              "fp4_mma_allones"):
+        assert n in rfp4.header_functions()
+
+
+def test_shape_errors_need_no_device():
+    lib = rfp4.load()
+    p = 0x10000  # never dereferenced: validation fails first
+    assert lib.mx4_gemv(None, 16, 33, p, p, p, p) == -2          # K not a multiple of 32
+    assert b"multiple of the 32-element block" in lib.rfp4_last_error()
+    assert lib.mx4_gemv(None, 0, 64, p, p, p, p) == -2            # N = 0
+    assert lib.fp4_gemv(None, 16, 64, None, p, p, p) == -1         # null pointer
+    assert lib.mx4_gemv(None, 16, 64, p + 4, p, p, p) == -6       # misaligned codes
+    assert lib.mx4_gemv_swiglu(None, 16, 64, 8, p, p, p, p) == -2  # up rows overlap gate rows
+    assert lib.rfp4_debug_gemv_path(3) == -1
+
+
+def test_calls_before_init_fail_loudly():
+    if rfp4.device_count() > 0:
+        pytest.skip("a device is present: init would succeed")
+    lib = rfp4.load()
+    assert lib.rfp4_init(0) == -8                                  # no device: loud failure
+    p = 0x10000
+    assert lib.mx4_gemv(None, 16, 64, p, p, p, p) == -5            # not initialised
+    assert lib.rmsnorm(None, 16, 1e-5, p, p, p) == -5
+    cfg = rfp4.model_config("tinyllama-1.1b", max_seq=64)
+    import ctypes as C
+    h = C.c_void_p()
+    assert lib.llama_engine_create(C.byref(cfg), 1, C.byref(h)) == -5
+    assert h.value is None
+
+
+def test_product_does_not_link_or_name_the_oracle():
+    so = os.path.join(PKG, "librfp4.so")
+    out = subprocess.run(["readelf", "-d", so], capture_output=True, text=True).stdout
+    needed = re.findall(r"Shared library: \[(.*?)\]", out)
+    assert needed and not any("oracle" in n for n in needed), needed
+    for dirpath, _, files in os.walk(os.path.join(PKG, "csrc")):
+        for f in files:
+            text = open(os.path.join(dirpath, f), errors="ignore").read()
+            assert "orc_" not in text and "pyoracle" not in text, f
+    assert "pyoracle" not in open(os.path.join(PKG, "rfp4.py")).read()

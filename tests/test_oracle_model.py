@@ -1,0 +1,133 @@
+"""Pins the oracle's decode loop (oracle.c orc_model_*) against an
+independent float64 numpy Llama decoder run on the same packed weights:
+layer order, GQA head mapping, rotate-half RoPE, fp16 KV rounding, SwiGLU and
+the final norm + LM head (llama_run/src/main.rs:492-536).  CPU only."""
+import math
+
+import numpy as np
+
+FP4 = np.array([0, 0.5, 1, 1.5, 2, 3, 4, 6], np.float64)
+CFG = dict(dim=128, n_layers=2, n_heads=4, n_kv_heads=2, head_dim=32, ffn=256, vocab=512,
+           theta=10000.0, eps=1e-5, max_seq=32)
+
+
+def _deq(orc, codes, scales, n, k):
+    c = orc.unpack(codes).reshape(n, k)
+    v = np.where(c & 8, -1.0, 1.0) * FP4[c & 7]
+    return v * np.repeat(np.ldexp(1.0, scales.astype(np.int64) - 127).reshape(n, k // 32), 32, axis=1)
+
+
+def _f16(a):
+    return np.asarray(a).view(np.float16).astype(np.float64)
+
+
+class NumpyLlama:
+    def __init__(self, orc, m, cfg):
+        c = self.c = cfg
+        qd, kvd = c["n_heads"] * c["head_dim"], c["n_kv_heads"] * c["head_dim"]
+        shapes = [(qd, c["dim"]), (kvd, c["dim"]), (kvd, c["dim"]), (c["dim"], qd),
+                  (c["ffn"], c["dim"]), (c["ffn"], c["dim"]), (c["dim"], c["ffn"])]
+        self.W = [[_deq(orc, m.codes(l, p), m.scales(l, p), *shapes[p]) for p in range(7)]
+                  for l in range(c["n_layers"])]
+        self.lm = _deq(orc, m.codes(-1, 0), m.scales(-1, 0), c["vocab"], c["dim"])
+        self.emb = _f16(m.embed()).reshape(c["vocab"], c["dim"])
+        self.na = [_f16(m.norm(l, 0)) for l in range(c["n_layers"])]
+        self.nf = [_f16(m.norm(l, 1)) for l in range(c["n_layers"])]
+        self.nfinal = _f16(m.norm(-1, 0))
+        self.K = [np.zeros((c["max_seq"], c["n_kv_heads"], c["head_dim"])) for _ in range(c["n_layers"])]
+        self.V = [np.zeros_like(k) for k in self.K]
+
+    def _norm(self, x, w):
+        return x / np.sqrt(np.mean(x * x) + self.c["eps"]) * w
+
+    def _rope(self, v, nh, pos):
+        hd = self.c["head_dim"]
+        half = hd // 2
+        j = np.arange(half)
+        ang = pos * (1.0 / np.power(self.c["theta"], 2.0 * j / hd))
+        cs, sn = np.cos(ang).astype(np.float32), np.sin(ang).astype(np.float32)  # f32 table
+        v = v.reshape(nh, hd)
+        a, b = v[:, :half], v[:, half:]
+        return np.concatenate([a * cs - b * sn, b * cs + a * sn], axis=1)
+
+    def step(self, tok, pos):
+        c = self.c
+        nh, nkv, hd = c["n_heads"], c["n_kv_heads"], c["head_dim"]
+        x = self.emb[tok].copy()
+        for l in range(c["n_layers"]):
+            Wq, Wk, Wv, Wo, Wg, Wu, Wd = self.W[l]
+            h = self._norm(x, self.na[l])
+            q = self._rope(Wq @ h, nh, pos)
+            k = self._rope(Wk @ h, nkv, pos)
+            # fp16 KV cache (round to nearest even via numpy's IEEE conversion)
+            self.K[l][pos] = k.astype(np.float32).astype(np.float16).astype(np.float64)
+            self.V[l][pos] = (Wv @ h).reshape(nkv, hd).astype(np.float32).astype(np.float16).astype(np.float64)
+            att = np.zeros((nh, hd))
+            for hh in range(nh):
+                g = hh // (nh // nkv)
+                s = self.K[l][:pos + 1, g] @ q[hh] / math.sqrt(hd)
+                p = np.exp(s - s.max())
+                att[hh] = (p / p.sum()) @ self.V[l][:pos + 1, g]
+            x = x + Wo @ att.reshape(-1)
+            h = self._norm(x, self.nf[l])
+            gate, up = Wg @ h, Wu @ h
+            x = x + Wd @ (gate / (1 + np.exp(-gate)) * up)
+        logits = self.lm @ self._norm(x, self.nfinal)
+        return int(np.argmax(logits)), logits
+
+
+def test_oracle_decode_matches_numpy_llama(orc):
+    seed = 0xBEEF
+    m = orc.Model(CFG, seed)
+    ref = NumpyLlama(orc, m, CFG)
+    prompt = [5, 77, 300]
+    tok = prompt[0]
+    produced = 0
+    for pos in range(14):
+        t_orc, lo = m.step(tok, pos, want_logits=True)
+        t_np, ln = ref.step(tok, pos)
+        np.testing.assert_allclose(lo, ln, rtol=1e-4, atol=1e-4 * np.abs(ln).max())
+        srt = np.sort(ln)
+        if srt[-1] - srt[-2] > 1e-3 * np.abs(ln).max():
+            assert t_orc == t_np, pos
+        tok = prompt[pos + 1] if pos + 1 < len(prompt) else t_orc
+        produced += pos + 1 >= len(prompt)
+    assert produced > 8
+    m.close()
+
+
+def test_generate_equals_stepwise(orc):
+    """orc_model_generate = the step loop of llama_run/src/main.rs:544-570
+    (prompt fed token by token, then greedy feedback, no EOS stop)."""
+    seed = 0xF00D
+    prompt = [9, 8, 7, 6]
+    a = orc.Model(CFG, seed)
+    gen, margins = a.generate(prompt, 0, 10)
+    b = orc.Model(CFG, seed)
+    tok, out = prompt[0], []
+    for pos in range(len(prompt) + 10 - 1):
+        t = b.step(tok, pos)
+        if pos + 1 < len(prompt):
+            tok = prompt[pos + 1]
+        else:
+            out.append(t)
+            tok = t
+    assert list(gen) == out
+    assert np.all(margins >= 0)
+    a.close()
+    b.close()
+
+
+def test_kv_prefill_layout(orc):
+    """Pre-filled context: element (t, kvh, d) is f16(0.1 * N) at counter index
+    (t*NKV + kvh)*HD + d of the layer's stream, stored head-major."""
+    m = orc.Model(CFG, 1)
+    m.prefill_kv(0x4B56, 5)
+    kc = m.kcache(1).reshape(CFG["n_kv_heads"], CFG["max_seq"], CFG["head_dim"])
+    coef = orc.lib().orc_ih4_coef(0.1)
+    t, kvh, d = 3, 1, 17
+    idx = (t * CFG["n_kv_heads"] + kvh) * CFG["head_dim"] + d
+    v = orc.lib().orc_ih4_normal(orc.mix64(0x4B56, 0x4B560000 + 2 * 1, idx), coef)
+    assert kc[kvh, t, d] == orc.lib().orc_f32_to_f16(v)
+    assert not kc[:, 5:].any()
+    m.close()
