@@ -145,6 +145,24 @@ int fp4_mma_allones(rfp4_stream_t stream, float *out);
  * llama_run/src/main.rs:334-376); needed for MXFP4 activations. */
 int mx4_quantize(rfp4_stream_t stream, uint64_t rows, uint64_t k, const void *src, int src_is_bf16,
                  uint8_t *codes, uint8_t *scales);
+/* Batched MXFP4 GEMM c[m][n] = a[m][k] . w[n][k]^T (f32 out) on scaled MFMA.
+ * a_codes/w_codes: E2M1 rows of k/2 bytes (low nibble first); a_scales/
+ * w_scales: E8M0 rows of k/32 bytes.  k % 256 == 0, n % 4 == 0; codes and c
+ * 16-byte aligned, scales 8-byte aligned.  The reference has only the
+ * single m16n8k64 block-scaled tile (fp4_mma/src/main.rs:18-54) and its CPU
+ * closed form D = sum_k A SFA B SFB (trackb/fp4_scale_test.cu:37); this is
+ * that contraction at M x N x K.  Split-K shapes use a library workspace:
+ * calls that overlap on one device race. */
+int fp4_gemm(rfp4_stream_t stream, uint32_t m, uint32_t n, uint32_t k, const uint8_t *a_codes,
+             const uint8_t *a_scales, const uint8_t *w_codes, const uint8_t *w_scales, float *c);
+/* Test hook: force the GEMM tile (index into the compiled list, largest
+ * first: 256x256, 256x128, 128x128, 64x128, 32x128; -1 = automatic) and K
+ * split (0 = automatic) of later fp4_gemm calls on this thread.  No
+ * reference counterpart. */
+int rfp4_debug_gemm_plan(int tile, int kz);
+/* The tile and K split fp4_gemm would use for this shape (honours the test
+ * hook).  No reference counterpart. */
+int rfp4_gemm_plan(uint32_t m, uint32_t n, uint32_t k, int *tile_m, int *tile_n, int *kz);
 
 /* ------------------------------------------------------------------ test hooks
  * Raw single-tile MFMA (layout pinning, the role of trackb/fp4_mapping_test.cu

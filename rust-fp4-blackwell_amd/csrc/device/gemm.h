@@ -1,0 +1,204 @@
+// Batched MXFP4 GEMM on gfx950 scaled MFMA:
+//   C[M][N] = A[M][K] . W[N][K]^T, A and W MXFP4 (E2M1 codes two per byte,
+//   low nibble first; one E8M0 scale per 32 values along K; row-major, the
+//   layout the engine stores weights in), C f32 row-major.
+// The reference validates one m16n8k64 block-scaled tile (fp4_mma,
+// trackb/*) and has no GEMM (main.tex:228); the CPU closed form is
+// trackb/fp4_scale_test.cu:37 extended to M x N x K.
+//
+// MFMA: v_mfma_scale_f32_32x32x64_f8f6f4, both operands E2M1.  Lane l holds
+// row l%32 of its fragment and the 32 K values 32*(l/32) .. +31 of the
+// 64-wide tile, with that block's scale byte (pinned by the 32x32 layout
+// test).  K advances in steps of 256 values = 128 bytes per row: lane
+// (r, h = l/32) takes bytes 64h .. 64h+63 of the step, and MFMA t (0..3) of
+// the step consumes bytes 64h + 16t .. +15 (values 128h + 32t .. +31) with
+// scale byte 4h + t of the step.  A and W are permuted along K the same way,
+// so C is unchanged.
+//
+// Workgroup: 4 waves in a WM x WN grid, wave tile (32 FA) x (32 FB), block
+// tile BM x BN.  Each K step (BM + BN rows of 128 code bytes and 8 scale
+// bytes) is copied global -> LDS by the DMA path (global_load_lds, no
+// staging registers), double buffered: a wave reads all its operands of step
+// s from LDS, issues the DMA of step s+1 into the other buffer, then runs the
+// step's MFMAs while the copy is in flight; one barrier per step.  Code rows
+// are 128 bytes with the 16-byte chunks XOR-swizzled by row (gemm_swz).
+//
+// Grid: one dimension, tiles ordered m fastest, then n, then the K split z;
+// the linear id is first remapped so that each XCD (id % 8 at dispatch) gets
+// a contiguous range of tiles and the m-tiles sharing a W tile share its L2.
+// With kz > 1 each split writes its partial tile to part[z]; the reduce
+// kernel launched next sums the kz planes in z order, so the result does not
+// depend on the order the workgroups ran in.
+#pragma once
+#include "common.h"
+#include "mma.h"
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) uint8_t rfp4_lds_u8;
+typedef __attribute__((address_space(1))) void rfp4_glb_void;
+
+// Physical 16-byte chunk of logical chunk q in LDS row r: an XOR swizzle that
+// keeps the fragment reads of 8 (and of 16) consecutive rows on distinct banks.
+RFP4_DEV uint32_t gemm_swz(uint32_t r) { return (r ^ (r >> 3)) & 7u; }
+
+template <int WM, int WN, int FA, int FB>
+RFP4_DEV void gemm_body(const GemmArgs &g)
+{
+    static_assert(WM * WN == 4, "4 waves");
+    constexpr uint32_t BM = 32u * FA * WM, BN = 32u * FB * WN, R = BM + BN;
+    constexpr uint32_t NJ = R / 32u;                 // 8-row code blocks per wave per step (1 KB each)
+    constexpr uint32_t NSB = (R / 32u + 3u) / 4u;    // 32-row scale blocks per wave per step (256 B each)
+    constexpr uint32_t SC0 = R * 128u, STAGE = R * 128u + R * 8u;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds_raw[2 * STAGE];
+    rfp4_lds_u8 *lds = (rfp4_lds_u8 *)lds_raw;
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t wm = wave / WN, wn = wave % WN;
+    const uint32_t r32 = lane & 31u, h = lane >> 5;
+
+    // ---- tile of this workgroup
+    const uint32_t total = gridDim.x, L = blockIdx.x, q = total >> 3;
+    const uint32_t lg = (L < q * 8u) ? (L & 7u) * q + (L >> 3) : L;
+    const uint32_t mt_n = (g.m + BM - 1u) / BM, nt_n = (g.n + BN - 1u) / BN;
+    const uint32_t mt = lg % mt_n, rest = lg / mt_n, nt = rest % nt_n, z = rest / nt_n;
+    const uint32_t kbytes = g.k >> 1, nblk = g.k >> 5, nsuper = g.k >> 8;
+    const uint32_t per = (nsuper + g.kz - 1u) / g.kz;
+    const uint32_t s0 = min(nsuper, z * per), s1 = min(nsuper, s0 + per);
+
+    // ---- DMA sources.  Code block j of this wave covers tile rows 8 (wave + 4 j) .. +7; lane l
+    // fetches logical chunk (l & 7) ^ swz(row) of row 8 (wave + 4 j) + l / 8, which the DMA writes
+    // to physical chunk l & 7.  Scale block b of this wave covers rows 32 (wave + 4 b) .. +31; lane l
+    // fetches bytes 4 (l & 1) .. +3 of row 32 (wave + 4 b) + l / 2.
+    const uint8_t *src[NJ];
+#pragma unroll
+    for (uint32_t j = 0; j < NJ; j++) {
+        const uint32_t row = 8u * (wave + 4u * j) + (lane >> 3);
+        const uint32_t qq = (lane & 7u) ^ gemm_swz(row);
+        if (row < BM) src[j] = g.a_codes + (size_t)min(mt * BM + row, g.m - 1u) * kbytes + qq * 16u;
+        else src[j] = g.w_codes + (size_t)min(nt * BN + (row - BM), g.n - 1u) * kbytes + qq * 16u;
+    }
+    const uint8_t *ssrc[NSB];
+#pragma unroll
+    for (uint32_t b = 0; b < NSB; b++) {
+        const uint32_t row = min(32u * (wave + 4u * b) + (lane >> 1), R - 1u);
+        const uint8_t *base = row < BM ? g.a_scales + (size_t)min(mt * BM + row, g.m - 1u) * nblk
+                                       : g.w_scales + (size_t)min(nt * BN + (row - BM), g.n - 1u) * nblk;
+        ssrc[b] = base + (lane & 1u) * 4u;
+    }
+#define RFP4_GEMM_DMA(S, BUF)                                                                              \
+    do {                                                                                                   \
+        rfp4_lds_u8 *st_ = lds + (BUF) * STAGE;                                                            \
+        _Pragma("unroll") for (uint32_t j = 0; j < NJ; j++) __builtin_amdgcn_global_load_lds(              \
+            (rfp4_glb_void *)(src[j] + (size_t)(S) * 128u), st_ + 1024u * (wave + 4u * j), 16, 0, 0);     \
+        _Pragma("unroll") for (uint32_t b = 0; b < NSB; b++) if (wave + 4u * b < R / 32u)                  \
+            __builtin_amdgcn_global_load_lds((rfp4_glb_void *)(ssrc[b] + (size_t)(S) * 8u),                \
+                                             st_ + SC0 + 256u * (wave + 4u * b), 4, 0, 0);                 \
+    } while (0)
+
+    v16f32 acc[FA][FB];
+#pragma unroll
+    for (int fa = 0; fa < FA; fa++)
+#pragma unroll
+        for (int fb = 0; fb < FB; fb++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[fa][fb][r] = 0.0f;
+
+    // fragment rows of this lane and their swizzles
+    uint32_t aoff[FA], boff[FB], asw[FA], bsw[FB];
+#pragma unroll
+    for (int fa = 0; fa < FA; fa++) {
+        const uint32_t r = wm * (32u * FA) + 32u * fa + r32;
+        aoff[fa] = r * 128u;
+        asw[fa] = gemm_swz(r);
+    }
+#pragma unroll
+    for (int fb = 0; fb < FB; fb++) {
+        const uint32_t r = BM + wn * (32u * FB) + 32u * fb + r32;
+        boff[fb] = r * 128u;
+        bsw[fb] = gemm_swz(r);
+    }
+
+    if (s0 < s1) RFP4_GEMM_DMA(s0, 0u);
+    __builtin_amdgcn_s_waitcnt(0x0f70); // vmcnt(0): this wave's DMA has landed in LDS
+    __syncthreads();
+    for (uint32_t s = s0; s < s1; s++) {
+        const uint32_t cur = (s - s0) & 1u;
+        const rfp4_lds_u8 *st = lds + cur * STAGE;
+        // all operands of the step into registers first, then the next step's DMA, then the MFMAs
+        u32x4 av[4][FA], bv[4][FB];
+        uint32_t sa[FA], sb[FB];
+#pragma unroll
+        for (int fa = 0; fa < FA; fa++) {
+            sa[fa] = *(const __attribute__((address_space(3))) uint32_t *)(st + SC0 + (aoff[fa] >> 4) + h * 4u);
+#pragma unroll
+            for (uint32_t t = 0; t < 4; t++)
+                av[t][fa] = *(const __attribute__((address_space(3))) u32x4 *)(st + aoff[fa] +
+                                                                                (((4u * h + t) ^ asw[fa]) << 4));
+        }
+#pragma unroll
+        for (int fb = 0; fb < FB; fb++) {
+            sb[fb] = *(const __attribute__((address_space(3))) uint32_t *)(st + SC0 + (boff[fb] >> 4) + h * 4u);
+#pragma unroll
+            for (uint32_t t = 0; t < 4; t++)
+                bv[t][fb] = *(const __attribute__((address_space(3))) u32x4 *)(st + boff[fb] +
+                                                                                (((4u * h + t) ^ bsw[fb]) << 4));
+        }
+        if (s + 1u < s1) RFP4_GEMM_DMA(s + 1u, cur ^ 1u);
+#pragma unroll
+        for (uint32_t t = 0; t < 4; t++) {
+#pragma unroll
+            for (int fa = 0; fa < FA; fa++) {
+                const v8i32 a8 = {(int)av[t][fa].x, (int)av[t][fa].y, (int)av[t][fa].z, (int)av[t][fa].w, 0, 0, 0, 0};
+                const int sca = (int)((sa[fa] >> (8u * t)) & 0xFFu);
+#pragma unroll
+                for (int fb = 0; fb < FB; fb++) {
+                    const v8i32 b8 = {(int)bv[t][fb].x, (int)bv[t][fb].y, (int)bv[t][fb].z, (int)bv[t][fb].w,
+                                      0, 0, 0, 0};
+                    const int scb = (int)((sb[fb] >> (8u * t)) & 0xFFu);
+                    acc[fa][fb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, acc[fa][fb], MX_FMT_FP4,
+                                                                                  MX_FMT_FP4, 0, sca, 0, scb);
+                }
+            }
+        }
+        // the wait for the next step's DMA goes after every MFMA of this step
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_waitcnt(0x0f70); // vmcnt(0)
+        __syncthreads();
+    }
+#undef RFP4_GEMM_DMA
+
+    // ---- epilogue: accumulator r of lane l is C[8 (r/4) + 4 (l/32) + r%4][l%32] of its fragment
+    float *dst = g.kz > 1u ? g.part + (size_t)z * g.m * g.n : g.c;
+    const uint32_t m0 = mt * BM + wm * (32u * FA), n0 = nt * BN + wn * (32u * FB);
+#pragma unroll
+    for (int fa = 0; fa < FA; fa++)
+#pragma unroll
+        for (int fb = 0; fb < FB; fb++) {
+            const uint32_t col = n0 + 32u * fb + r32;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const uint32_t row = m0 + 32u * fa + 8u * (uint32_t)(r / 4) + 4u * h + (uint32_t)(r % 4);
+                if (row < g.m && col < g.n) dst[(size_t)row * g.n + col] = acc[fa][fb][r];
+            }
+        }
+}
+
+// Split-K sum: c = part[0] + part[1] + ... + part[kz-1] in that order (the
+// launch after the GEMM on the same stream, so no cross-workgroup ordering is
+// needed).  Four floats per thread.
+RFP4_DEV void gemm_reduce_body(const GemmArgs &g)
+{
+    const size_t plane = (size_t)g.m * g.n, n4 = plane / 4u;
+    for (size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x; e < n4; e += (size_t)gridDim.x * blockDim.x) {
+        float4 sum = ((const float4 *)g.part)[e];
+        for (uint32_t z = 1; z < g.kz; z++) {
+            const float4 p = ((const float4 *)(g.part + z * plane))[e];
+            sum.x = __fadd_rn(sum.x, p.x);
+            sum.y = __fadd_rn(sum.y, p.y);
+            sum.z = __fadd_rn(sum.z, p.z);
+            sum.w = __fadd_rn(sum.w, p.w);
+        }
+        ((float4 *)g.c)[e] = sum;
+    }
+}

@@ -9,6 +9,7 @@
 #include "device/attn.h"
 #include "device/misc.h"
 #include "device/mma.h"
+#include "device/gemm.h"
 
 #define K256 extern "C" __global__ __launch_bounds__(256)
 #define K1024 extern "C" __global__ __launch_bounds__(1024)
@@ -102,3 +103,14 @@ K256 void rfp4_mma32_tile(MmaTileArgs a) { mma32_tile_body(a); }
 K256 void rfp4_mma_allones(MmaTileArgs a) { mma_allones_body(a.out); }
 K256 void rfp4_mma_bf16_tile(MmaTileArgs a) { mma_bf16_tile_body(a); }
 K256 void rfp4_selftest_cvt_bf16(SelftestArgs a) { selftest_cvt_bf16_body(a); }
+
+// ---- batched MXFP4 GEMM: rfp4_gemm_<BM>x<BN> (4 waves in WM x WN, wave tile 32FA x 32FB).
+// The host picks among these (runtime.cpp gemm_plan); keep the lists in sync.
+#define GEMM_KERNEL(BM, BN, WM, WN, FA, FB) \
+    K256 void rfp4_gemm_##BM##x##BN(GemmArgs a) { gemm_body<WM, WN, FA, FB>(a); }
+GEMM_KERNEL(32, 128, 1, 4, 1, 1)
+GEMM_KERNEL(64, 128, 2, 2, 1, 2)
+GEMM_KERNEL(128, 128, 2, 2, 2, 2)
+GEMM_KERNEL(256, 128, 2, 2, 4, 2)
+GEMM_KERNEL(256, 256, 2, 2, 4, 4)
+K256 void rfp4_gemm_reduce(GemmArgs a) { gemm_reduce_body(a); }

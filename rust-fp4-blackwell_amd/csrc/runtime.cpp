@@ -106,10 +106,13 @@ int rfp4_init(int device)
     rc = hip_check(hipMalloc((void **)&rt->attn_part, rt->attn_part_floats * sizeof(float)), "hipMalloc(attn workspace)");
     if (!rc) rc = hip_check(hipMalloc((void **)&rt->attn_counters, kAttnMaxHeads * sizeof(uint32_t)), "hipMalloc(attn counters)");
     if (!rc) rc = hip_check(hipMemset(rt->attn_counters, 0, kAttnMaxHeads * sizeof(uint32_t)), "hipMemset");
+    // split-K workspace of fp4_gemm
+    if (!rc) rc = hip_check(hipMalloc((void **)&rt->gemm_part, kGemmPartFloats * sizeof(float)), "hipMalloc(gemm workspace)");
     if (!rc) rc = hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
     if (rc) {
         hipFree(rt->attn_part);
         hipFree(rt->attn_counters);
+        hipFree(rt->gemm_part);
         hipModuleUnload(rt->module);
         delete rt;
         return rc;
@@ -603,6 +606,103 @@ int mx4_quantize(rfp4_stream_t stream, uint64_t rows, uint64_t k, const void *sr
     if (blocks > 65536) blocks = 65536;
     return launch(src_is_bf16 ? "rfp4_quant_mx_bf16" : "rfp4_quant_mx_f32", dim3((unsigned)blocks), dim3(256),
                   (hipStream_t)stream, &a);
+}
+
+} // extern "C"
+
+namespace {
+
+struct GemmTile {
+    uint32_t bm, bn;
+    const char *name;
+};
+// Compiled tile shapes (kernels.hip GEMM_KERNEL), largest first.
+constexpr GemmTile kGemmTiles[] = {
+    {256, 256, "rfp4_gemm_256x256"}, {256, 128, "rfp4_gemm_256x128"}, {128, 128, "rfp4_gemm_128x128"},
+    {64, 128, "rfp4_gemm_64x128"},   {32, 128, "rfp4_gemm_32x128"},
+};
+constexpr int kGemmNumTiles = (int)(sizeof(kGemmTiles) / sizeof(kGemmTiles[0]));
+thread_local int t_gemm_tile = -1, t_gemm_kz = 0;
+
+struct GemmPlan {
+    int tile;
+    uint32_t kz;
+};
+
+uint32_t ceil_div(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
+
+// Tile: the largest one that does not waste more than a quarter of its rows
+// on m and still yields a tile per CU; else the smallest such tile, with the
+// K split raised until every CU has a workgroup (bounded by the workspace).
+GemmPlan gemm_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t num_cus)
+{
+    const uint32_t nsuper = k / 256u;
+    int pick = t_gemm_tile;
+    for (int i = 0; pick < 0 && i < kGemmNumTiles; i++) {
+        const GemmTile &t = kGemmTiles[i];
+        if (t.bm > 32u && (uint64_t)ceil_div(m, t.bm) * t.bm * 4u > (uint64_t)m * 5u) continue; // > 25% padding
+        if ((uint64_t)ceil_div(m, t.bm) * ceil_div(n, t.bn) >= num_cus || i == kGemmNumTiles - 1) pick = i;
+    }
+    const uint64_t tiles = (uint64_t)ceil_div(m, kGemmTiles[pick].bm) * ceil_div(n, kGemmTiles[pick].bn);
+    if (t_gemm_kz > 0) return {pick, std::min<uint32_t>((uint32_t)t_gemm_kz, nsuper)};
+    if (tiles >= num_cus) return {pick, 1u};
+    // steps per split: as few as reach one workgroup per CU; kz = ceil(nsuper / per) leaves no split empty
+    uint32_t per = std::max<uint32_t>(1u, nsuper / ceil_div(num_cus, tiles));
+    uint32_t kz = ceil_div(nsuper, per);
+    while (kz > 1 && (uint64_t)kz * m * n > kGemmPartFloats) kz = ceil_div(nsuper, ++per);
+    return {pick, kz};
+}
+
+} // namespace
+
+extern "C" {
+
+int fp4_gemm(rfp4_stream_t stream, uint32_t m, uint32_t n, uint32_t k, const uint8_t *a_codes,
+             const uint8_t *a_scales, const uint8_t *w_codes, const uint8_t *w_scales, float *c)
+{
+    if (!a_codes || !a_scales || !w_codes || !w_scales || !c) return set_error(RFP4_E_INVALID, "fp4_gemm: null pointer");
+    if (m == 0 || n == 0 || k == 0) return set_error(RFP4_E_SHAPE, "fp4_gemm: empty shape m=%u n=%u k=%u", m, n, k);
+    if (k % 256u) return set_error(RFP4_E_SHAPE, "fp4_gemm: k=%u must be a multiple of 256", k);
+    if (n % 4u) return set_error(RFP4_E_SHAPE, "fp4_gemm: n=%u must be a multiple of 4", n);
+    if (((uintptr_t)a_codes | (uintptr_t)w_codes | (uintptr_t)c) & 15u)
+        return set_error(RFP4_E_ALIGN, "fp4_gemm: codes and c must be 16-byte aligned");
+    if (((uintptr_t)a_scales | (uintptr_t)w_scales) & 7u)
+        return set_error(RFP4_E_ALIGN, "fp4_gemm: scales must be 8-byte aligned");
+    Runtime *rt = g_rt;
+    if (!rt) return set_error(RFP4_E_NOT_INIT, "rfp4_init has not been called");
+    GemmPlan p = gemm_plan(m, n, k, (uint32_t)rt->num_cus);
+    const GemmTile &t = kGemmTiles[p.tile];
+    const uint64_t tiles = (uint64_t)ceil_div(m, t.bm) * ceil_div(n, t.bn);
+    if (p.kz > 1 && (uint64_t)p.kz * m * n > kGemmPartFloats)
+        return set_error(RFP4_E_CAPACITY, "fp4_gemm: split-K partials %u x %u x %u exceed the workspace", p.kz, m, n);
+    if (tiles * p.kz > 0x7FFFFFFFull) return set_error(RFP4_E_SHAPE, "fp4_gemm: grid too large");
+    GemmArgs a{a_codes, a_scales, w_codes, w_scales, c, rt->gemm_part, m, n, k, p.kz};
+    int rc = launch(t.name, dim3((unsigned)(tiles * p.kz)), dim3(256), (hipStream_t)stream, &a);
+    if (rc || p.kz == 1) return rc;
+    const uint64_t n4 = (uint64_t)m * n / 4u;
+    return launch("rfp4_gemm_reduce", dim3((unsigned)std::min<uint64_t>((n4 + 255u) / 256u, 8192u)), dim3(256),
+                  (hipStream_t)stream, &a);
+}
+
+int rfp4_debug_gemm_plan(int tile, int kz)
+{
+    if (tile < -1 || tile >= kGemmNumTiles) return set_error(RFP4_E_INVALID, "tile must be -1 (auto) or 0..%d", kGemmNumTiles - 1);
+    if (kz < 0) return set_error(RFP4_E_INVALID, "kz must be 0 (auto) or positive");
+    t_gemm_tile = tile;
+    t_gemm_kz = kz;
+    return RFP4_OK;
+}
+
+int rfp4_gemm_plan(uint32_t m, uint32_t n, uint32_t k, int *tile_m, int *tile_n, int *kz)
+{
+    Runtime *rt = g_rt;
+    const uint32_t cus = rt ? (uint32_t)rt->num_cus : 256u;
+    if (k == 0 || k % 256u || m == 0 || n == 0) return set_error(RFP4_E_SHAPE, "gemm_plan: bad shape");
+    GemmPlan p = gemm_plan(m, n, k, cus);
+    if (tile_m) *tile_m = (int)kGemmTiles[p.tile].bm;
+    if (tile_n) *tile_n = (int)kGemmTiles[p.tile].bn;
+    if (kz) *kz = (int)p.kz;
+    return RFP4_OK;
 }
 
 int rfp4_mma_tile16(rfp4_stream_t stream, const uint32_t *a, const uint32_t *b, const uint32_t *sa,

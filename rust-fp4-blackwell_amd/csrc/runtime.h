@@ -13,6 +13,8 @@ namespace rfp4 {
 constexpr uint32_t kAttnMaxHeads = 128;
 constexpr uint32_t kAttnMaxSplits = 512;
 
+constexpr size_t kGemmPartFloats = (size_t)8 << 20; // 32 MiB
+
 struct Runtime {
     int device = 0;
     int num_cus = 256;
@@ -21,6 +23,7 @@ struct Runtime {
     float *attn_part = nullptr;       // default split-K workspace of attn_decode
     uint32_t *attn_counters = nullptr;
     size_t attn_part_floats = 0;
+    float *gemm_part = nullptr;       // split-K partials of fp4_gemm (kGemmPartFloats)
     size_t max_lds = 65536;           // LDS bytes per workgroup
 };
 

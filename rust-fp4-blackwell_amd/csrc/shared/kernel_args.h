@@ -159,10 +159,11 @@ typedef struct StepArgs {
 // Scaled-MFMA MXFP4 GEMM: C[M][N] = A[M][K] * W[N][K]^T, both MXFP4 (E2M1 +
 // E8M0 per 32 along K), f32 output.
 typedef struct GemmArgs {
-    const uint8_t *a_codes, *a_scales;
-    const uint8_t *w_codes, *w_scales;
-    float *c;
-    uint32_t m, n, k, pad;
+    const uint8_t *a_codes, *a_scales;   // [m][k/2], [m][k/32]
+    const uint8_t *w_codes, *w_scales;   // [n][k/2], [n][k/32]
+    float *c;                            // [m][n]
+    float *part;                         // [kz][m][n] split-K partials (kz > 1)
+    uint32_t m, n, k, kz;
 } GemmArgs;
 
 typedef struct MmaTileArgs {

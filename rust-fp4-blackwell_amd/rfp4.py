@@ -82,6 +82,9 @@ _SIGS = {
     "argmax": (I32, [P, U32, P, P]),
     "fp4_mma_allones": (I32, [P, P]),
     "mx4_quantize": (I32, [P, U64, U64, P, I32, P, P]),
+    "fp4_gemm": (I32, [P, U32, U32, U32, P, P, P, P, P]),
+    "rfp4_debug_gemm_plan": (I32, [I32, I32]),
+    "rfp4_gemm_plan": (I32, [U32, U32, U32, P, P, P]),
     "rfp4_mma_tile16": (I32, [P, P, P, P, P, P]),
     "rfp4_mma_tile32": (I32, [P, P, P, P, P, P]),
     "rfp4_selftest_cvt_fp4": (I32, [P, U32, P, P]),
@@ -337,6 +340,21 @@ def fp4_mma_allones(stream, out):
 
 def mx4_quantize(stream, rows, k, src, src_is_bf16, codes, scales):
     check(load().mx4_quantize(_s(stream), rows, k, _p(src), int(src_is_bf16), _p(codes), _p(scales)))
+
+
+def fp4_gemm(stream, m, n, k, a_codes, a_scales, w_codes, w_scales, c):
+    check(load().fp4_gemm(_s(stream), m, n, k, _p(a_codes), _p(a_scales), _p(w_codes), _p(w_scales), _p(c)))
+
+
+def debug_gemm_plan(tile=-1, kz=0):
+    check(load().rfp4_debug_gemm_plan(tile, kz))
+
+
+def gemm_plan(m, n, k):
+    """(tile_m, tile_n, kz) fp4_gemm uses for this shape."""
+    tm, tn, kz = C.c_int(), C.c_int(), C.c_int()
+    check(load().rfp4_gemm_plan(m, n, k, C.byref(tm), C.byref(tn), C.byref(kz)))
+    return tm.value, tn.value, kz.value
 
 
 def mma_tile16(stream, a, b, sa, sb, out):

@@ -44,6 +44,32 @@ def test_shape_errors_need_no_device():
     assert lib.mx4_gemv(None, 16, 64, p + 4, p, p, p) == -6       # misaligned codes
     assert lib.mx4_gemv_swiglu(None, 16, 64, 8, p, p, p, p) == -2  # up rows overlap gate rows
     assert lib.rfp4_debug_gemv_path(3) == -1
+    assert lib.fp4_gemm(None, 32, 4096, 4000, p, p, p, p, p) == -2  # K not a multiple of 256
+    assert lib.fp4_gemm(None, 32, 4098, 4096, p, p, p, p, p) == -2  # N not a multiple of 4
+    assert lib.fp4_gemm(None, 0, 4096, 4096, p, p, p, p, p) == -2   # M = 0
+    assert lib.fp4_gemm(None, 32, 4096, 4096, p + 8, p, p, p, p) == -6  # misaligned codes
+    assert lib.fp4_gemm(None, 32, 4096, 4096, p, p + 4, p, p, p) == -6  # misaligned scales
+    assert lib.fp4_gemm(None, 32, 4096, 4096, None, p, p, p, p) == -1
+    assert lib.rfp4_debug_gemm_plan(5, 0) == -1
+
+
+@pytest.mark.parametrize("m", [1, 32, 80, 512, 4096])
+@pytest.mark.parametrize("n,k", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336), (128256, 4096),
+                                 (292, 1024)])
+def test_gemm_plan_shapes(m, n, k):
+    """The automatic GEMM plan (256 CUs without a device): a compiled tile, no
+    empty K split, the split-K partials fit the workspace, and either one
+    workgroup per CU or the K split is at its maximum."""
+    tm, tn, kz = rfp4.gemm_plan(m, n, k)
+    assert (tm, tn) in [(256, 256), (256, 128), (128, 128), (64, 128), (32, 128)]
+    nsuper = k // 256
+    per = -(-nsuper // kz)
+    assert 1 <= kz <= nsuper and (kz - 1) * per < nsuper
+    assert kz == 1 or kz * m * n <= (8 << 20)
+    tiles = -(-m // tm) * -(-n // tn)
+    assert tiles * kz >= 256 or kz == nsuper or (kz + 1) * m * n > (8 << 20)
+    if m > 32:
+        assert -(-m // tm) * tm <= 1.25 * m or tm == 32   # bounded row padding
 
 
 def test_calls_before_init_fail_loudly():

@@ -1,0 +1,171 @@
+"""Batched MXFP4 GEMM (fp4_gemm, scaled MFMA) against the oracle's exact
+float64 contraction C = sum_k A SFA W SFW (trackb/fp4_scale_test.cu:37 taken
+to M x N x K; the reference has only the m16n8k64 tile, fp4_mma/src/main.rs).
+
+Bar (fp32 accumulate): |c - c64| <= 1e-5 * sum_k |a_k w_k| on every element,
+no element past the reference's 1e-2 gate, and >= 99.9% of elements within
+1e-3 relative of the exact sum (elements with heavy cancellation may exceed
+it, as for the GEMV).  Config-5 shapes too large for the CPU oracle are
+checked on sampled rows and columns: C[i][j] depends only on row i of A and
+row j of W, so a sub-GEMM of the sampled rows is an exact restatement."""
+import numpy as np
+import pytest
+
+from conftest import reference_rel_err
+
+pytestmark = pytest.mark.gpu
+
+TILES = [(256, 256), (256, 128), (128, 128), (64, 128), (32, 128)]
+CONFIG5_NK = [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336), (128256, 4096)]
+
+
+def _dev(rf, arr, s):
+    return rf.DeviceBuffer.from_host(np.ascontiguousarray(arr), s)
+
+
+def _uniform_mx(orc, rows, k, seed):
+    """Codes uniform over the 16 E2M1 codes, E8M0 exponents uniform in [-6, 2]
+    (the weight distribution of BASELINE config 1)."""
+    words, st = orc.xorshift32(seed, rows * k // 8)
+    codes = words.view(np.uint8).copy()
+    r, _ = orc.xorshift32(st, rows * k // 32)
+    return codes, (127 - 6 + (r % 9)).astype(np.uint8)
+
+
+def _bf16_normal(rows, k, seed):
+    """bf16 bits of N(0,1) samples (round to nearest even from f32)."""
+    u = np.random.default_rng(seed).standard_normal((rows, k), dtype=np.float32).view(np.uint32)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def _assert_gemm_close(c, c64, absc):
+    c = np.asarray(c, np.float64)
+    cond = np.abs(c - c64) / np.maximum(absc, 1e-300)
+    assert cond.max() < 1e-5, f"max |c-c64|/sum|aw| = {cond.max():.3e}"
+    rel = reference_rel_err(c, c64)
+    assert (rel > 1e-2).sum() == 0, f"{(rel > 1e-2).sum()} elements past 1e-2, max {rel.max():.3e}"
+    assert np.mean(rel <= 1e-3) >= 0.999, f"{(rel > 1e-3).sum()} elements over 1e-3 (max {rel.max():.3e})"
+
+
+def _gemm(rf, stream, m, n, k, ac, asc, wc, wsc):
+    d = [_dev(rf, t, stream) if isinstance(t, np.ndarray) else t for t in (ac, asc, wc, wsc)]
+    dc = rf.DeviceBuffer(m * n * 4)
+    rf.fp4_gemm(stream, m, n, k, *d, dc)
+    return dc.to_host(m * n, np.float32, stream).reshape(m, n)
+
+
+@pytest.fixture
+def forced_plan(rf):
+    yield rf.debug_gemm_plan
+    rf.debug_gemm_plan(-1, 0)
+
+
+@pytest.mark.parametrize("tile", range(len(TILES)))
+@pytest.mark.parametrize("kz", [1, 3])
+def test_gemm_every_tile_and_split(rf, orc, stream, forced_plan, tile, kz):
+    """Ragged m and n (neither a multiple of any tile), k of 4 K-steps; kz=3
+    leaves the last split empty (ceil(4/3) = 2 steps per split)."""
+    m, n, k = 80, 292, 1024
+    ac, asc = _uniform_mx(orc, m, k, 11)
+    wc, wsc = _uniform_mx(orc, n, k, 12)
+    forced_plan(tile, kz)
+    assert rf.gemm_plan(m, n, k) == (*TILES[tile], kz)
+    c = _gemm(rf, stream, m, n, k, ac, asc, wc, wsc)
+    c64, absc = orc.gemm_mx_f64(m, n, k, ac, asc, wc, wsc)
+    _assert_gemm_close(c, c64, absc)
+    c2 = _gemm(rf, stream, m, n, k, ac, asc, wc, wsc)
+    np.testing.assert_array_equal(c.view(np.uint32), c2.view(np.uint32))  # deterministic
+
+
+def test_gemm_row_permutation_is_exact(rf, orc, stream, forced_plan):
+    """Each C[i][j] is computed by the same MFMA sequence wherever row i sits
+    in its tile: permuting A's rows permutes C's rows bit for bit."""
+    m, n, k = 96, 256, 2048
+    ac, asc = _uniform_mx(orc, m, k, 21)
+    wc, wsc = _uniform_mx(orc, n, k, 22)
+    perm = np.random.default_rng(3).permutation(m)
+    forced_plan(3, 2)
+    c = _gemm(rf, stream, m, n, k, ac, asc, wc, wsc)
+    cp = _gemm(rf, stream, m, n, k, ac.reshape(m, -1)[perm], asc.reshape(m, -1)[perm], wc, wsc)
+    np.testing.assert_array_equal(c[perm].view(np.uint32), cp.view(np.uint32))
+
+
+def test_gemm_small_edges(rf, orc, stream):
+    """m = 1, n = 4 (smaller than every tile), k = 256 (a single K step),
+    an all-zero block and scale extremes 2^-127 / 2^+20."""
+    for m, n, k in [(1, 4, 256), (33, 36, 512), (7, 132, 256)]:
+        ac, asc = _uniform_mx(orc, m, k, 31 + m)
+        wc, wsc = _uniform_mx(orc, n, k, 41 + n)
+        ac.reshape(m, -1)[0, :16] = 0            # zero block in row 0
+        asc.reshape(m, -1)[-1, 0] = 0            # 2^-127
+        wsc.reshape(n, -1)[0, -1] = 127 + 20
+        c = _gemm(rf, stream, m, n, k, ac, asc, wc, wsc)
+        c64, absc = orc.gemm_mx_f64(m, n, k, ac, asc, wc, wsc)
+        _assert_gemm_close(c, c64, absc)
+
+
+def test_gemm_one_hot_selects_weight_value(rf, orc, stream):
+    """A row i = 1.0 at one K position p (code 0x2, scale 2^0): C[i][j] is
+    exactly the dequantised W[j][p]."""
+    n, k = 128, 512
+    wc, wsc = _uniform_mx(orc, n, k, 51)
+    ps = [0, 1, 31, 32, 63, 64, 127, 128, 255, 256, 300, 511]
+    m = len(ps)
+    codes = np.zeros((m, k), np.uint8)
+    for i, p in enumerate(ps):
+        codes[i, p] = 0x2
+    ac = orc.pack(codes.reshape(-1)).reshape(-1)
+    asc = np.full(m * k // 32, 127, np.uint8)
+    c = _gemm(rf, stream, m, n, k, ac, asc, wc, wsc)
+    e2m1 = np.array([0, .5, 1, 1.5, 2, 3, 4, 6, -0.0, -.5, -1, -1.5, -2, -3, -4, -6])
+    wv = e2m1[orc.unpack(wc)].reshape(n, k) * np.exp2(
+        np.repeat(wsc.reshape(n, -1).astype(np.float64) - 127, 32, axis=1))
+    for i, p in enumerate(ps):
+        np.testing.assert_array_equal(c[i], wv[:, p].astype(np.float32))
+
+
+def _config5_case(rf, orc, stream, m, n, k, sample_rows=None, sample_cols=None):
+    """bf16 activations ~N(0,1) quantised on the device (bit-exact against the
+    oracle quantiser), uniform MXFP4 weights, then the GEMM."""
+    a16 = _bf16_normal(m, k, m * 7 + k)
+    da = _dev(rf, a16, stream)
+    dac, das = rf.DeviceBuffer(m * k // 2), rf.DeviceBuffer(m * k // 32)
+    rf.mx4_quantize(stream, m, k, da, True, dac, das)
+    ac = dac.to_host(m * k // 2, np.uint8, stream)
+    asc = das.to_host(m * k // 32, np.uint8, stream)
+    a32 = (a16.astype(np.uint32) << 16).view(np.float32)
+    c_ref, s_ref = orc.quant_mx(a32)
+    np.testing.assert_array_equal(ac, c_ref)
+    np.testing.assert_array_equal(asc, s_ref)
+    wc, wsc = _uniform_mx(orc, n, k, (n * 31 + k) | 1)
+    c = _gemm(rf, stream, m, n, k, dac, das, wc, wsc)
+    rows = np.arange(m) if sample_rows is None else sample_rows
+    cols = np.arange(n) if sample_cols is None else sample_cols
+    ac2, as2 = ac.reshape(m, -1)[rows], asc.reshape(m, -1)[rows]
+    wc2, ws2 = wc.reshape(n, -1)[cols], wsc.reshape(n, -1)[cols]
+    c64, absc = orc.gemm_mx_f64(len(rows), len(cols), k, ac2, as2, wc2, ws2)
+    _assert_gemm_close(c[np.ix_(rows, cols)], c64, absc)
+    assert np.isfinite(c).all()
+
+
+@pytest.mark.parametrize("n,k", CONFIG5_NK)
+def test_gemm_config5_decode_batch32(rf, orc, stream, n, k):
+    """BASELINE config 5, decode at batch 32: the whole C against the oracle
+    (LM-head shape: 4096 sampled columns incl. both ends)."""
+    cols = None
+    if n > 16384:
+        cols = np.unique(np.concatenate([np.arange(64), n - 64 + np.arange(64),
+                                         np.random.default_rng(n).choice(n, 3968, replace=False)]))
+    _config5_case(rf, orc, stream, 32, n, k, sample_cols=cols)
+
+
+@pytest.mark.parametrize("n,k", CONFIG5_NK)
+def test_gemm_config5_prefill512(rf, orc, stream, n, k):
+    """BASELINE config 5, prefill of 512 tokens: 24 sampled rows (first and
+    last of the tile rows included) x up to 1024 sampled columns."""
+    rng = np.random.default_rng(n + k)
+    rows = np.unique(np.concatenate([[0, 1, 31, 32, 63, 64, 127, 128, 255, 256, 510, 511],
+                                     rng.choice(512, 12, replace=False)]))
+    cols = np.unique(np.concatenate([np.arange(32), n - 32 + np.arange(32),
+                                     rng.choice(n, min(n, 960), replace=False)]))
+    _config5_case(rf, orc, stream, 512, n, k, sample_rows=rows, sample_cols=cols)
