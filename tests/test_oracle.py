@@ -347,3 +347,26 @@ def test_swiglu_residual_argmax(orc):
     assert orc.argmax(v) == 1  # ties -> lowest index
     assert orc.argmax(np.array([np.nan, 1.0, np.nan], np.float32)) == 1
     assert orc.argmax(np.full(5, -np.inf, np.float32)) == 0  # nothing > -1e30
+
+
+def test_small_golden_fixtures_reproduce(orc):
+    """The committed config-1 and config-2 fixtures are what the oracle
+    computes now (a change to the oracle that moves them fails here)."""
+    import importlib.util
+    import os
+
+    from conftest import GOLDEN
+    spec = importlib.util.spec_from_file_location("make_golden", os.path.join(GOLDEN, "make_golden.py"))
+    mg = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mg)
+    fx = np.load(os.path.join(GOLDEN, "config1_gemv.npz"))
+    codes, scales, x = mg.config1_inputs()
+    assert mg.sha(codes) == str(fx["sha_codes"]) and mg.sha(x) == str(fx["sha_x"])
+    np.testing.assert_array_equal(orc.gemv_e8m0(2048, 2048, codes, scales, x), fx["y"])
+    y64, absy = orc.gemv_e8m0_f64(2048, 2048, codes, scales, x)
+    np.testing.assert_array_equal(y64, fx["y64"])
+    fx2 = np.load(os.path.join(GOLDEN, "config2_kernels.npz"))
+    r, _ = orc.xorshift32(0x13579BDF, 32 * 64)
+    q = (((r % 2001).astype(np.float32) - 1000.0) / 500.0).astype(np.float32)
+    c, s = orc.rope_table(2048, 64, 10000.0)
+    np.testing.assert_array_equal(orc.rope(q, 32, 64, c[2047 * 32:], s[2047 * 32:]), fx2["rope_pos2047"])
