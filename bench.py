@@ -7,8 +7,11 @@ LM head.  `value` = decode tokens/s with weights and KV resident in HBM.
 
 Extra fields: the roofline of the dominant kernel (the fused gate/up SwiGLU
 GEMV) timed with HIP events on the engine's stream, the whole GEMV path of
-one token replayed alone, TinyLlama-1.1B decode tok/s (config 3), and the CPU
-oracle timed on the host cores (cpu_baseline, a reported baseline only).
+one token replayed alone, TinyLlama-1.1B decode tok/s (config 3), the
+batched MXFP4 GEMM at M=32 and M=512 on the 8B shapes (config 5, TFLOP/s
+against the FP4 MFMA peak), and the CPU oracle timed on the host cores
+(cpu_baseline, a reported baseline only).  `--pmc-probe` runs only the
+launch sequence used for the HBM-traffic counter runs.
 """
 import argparse
 import json
@@ -80,6 +83,120 @@ def gemv_path(rf, eng, cfg, reps=5):
     return total_bytes, ms, gate_bytes, ms_gate
 
 
+FP4_PEAK_TFLOPS = 10100.0
+
+
+def _bf16_normal(rng, rows, k):
+    u = rng.standard_normal((rows, k), dtype=np.float32).view(np.uint32)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def gemm_config5(rf, eng, cfg, reps=2):
+    """MXFP4 GEMMs at M=32 (decode batch) and M=512 (prefill)
+    on the engine's own Llama-3-8B weights, bf16 activations ~N(0,1) quantized
+    per 32 along K (mx4_quantize).  Per config-5 shape, each launch uses a
+    different layer's weights (no cache reuse across launches); the stack pass
+    is every projection of the 32 layers plus the LM head."""
+    s = eng.stream
+    qd, kvd = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
+    rng = np.random.default_rng(5)
+    acts = {}
+    for k in sorted({cfg.dim, qd, cfg.ffn}):
+        a16 = rf.DeviceBuffer.from_host(_bf16_normal(rng, 512, k), s)
+        ac, asc = rf.DeviceBuffer(512 * k // 2), rf.DeviceBuffer(512 * k // 32)
+        rf.mx4_quantize(s, 512, k, a16, True, ac, asc)
+        acts[k] = (a16, ac, asc)
+    c = rf.DeviceBuffer(512 * max(cfg.vocab, 2 * cfg.ffn) * 4)
+    L = cfg.n_layers
+    w = {p: [eng.weight(l, p)[:2] for l in range(L)] for p in (0, 3, 4, 6)}
+    lm = eng.weight(-1, 0)[:2]
+    # config-5 shapes: (name, N, K, weight views rotating over layers)
+    shapes = [
+        ("4096x4096", cfg.dim, qd, w[3]),
+        ("1024x4096", kvd, cfg.dim, [(wc + qd * cfg.dim // 2, ws + qd * cfg.dim // 32) for wc, ws in w[0]]),
+        ("14336x4096", cfg.ffn, cfg.dim, w[4]),
+        ("4096x14336", cfg.dim, cfg.ffn, w[6]),
+        ("128256x4096", cfg.vocab, cfg.dim, [lm]),
+    ]
+    stack = [(qd + 2 * kvd, cfg.dim, w[0]), (cfg.dim, qd, w[3]), (2 * cfg.ffn, cfg.dim, w[4]),
+             (cfg.dim, cfg.ffn, w[6])]
+    out = {}
+    for m in (32, 512):
+        res = {}
+        for name, n, k, views in shapes:
+            _, ac, asc = acts[k]
+            nl = len(views)
+            calls = [lambda wc=wc, ws=ws: rf.fp4_gemm(s, m, n, k, ac, asc, wc, ws, c) for wc, ws in views]
+            ms = time_launches(rf, s, lambda: [f() for f in calls], reps) / nl
+            tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+            gbs = (n * k * 17 // 32 + m * k * 17 // 32 + 4 * m * n) / (ms * 1e-3) / 1e9
+            tm, tn, kz = rf.gemm_plan(m, n, k)
+            res[name] = {"us": round(ms * 1e3, 2), "TFLOP_s": round(tf, 1), "frac_fp4_peak": round(tf / FP4_PEAK_TFLOPS, 4),
+                         "GB_s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "tile": f"{tm}x{tn}/kz{kz}"}
+        flops = 0.0
+        calls = []
+        for l in range(L):
+            for n, k, views in stack:
+                _, ac, asc = acts[k]
+                wc, ws = views[l]
+                calls.append(lambda n=n, k=k, ac=ac, asc=asc, wc=wc, ws=ws: rf.fp4_gemm(s, m, n, k, ac, asc, wc, ws, c))
+                flops += 2.0 * m * n * k
+        calls.append(lambda: rf.fp4_gemm(s, m, cfg.vocab, cfg.dim, acts[cfg.dim][1], acts[cfg.dim][2], lm[0], lm[1], c))
+        flops += 2.0 * m * cfg.vocab * cfg.dim
+        ms = time_launches(rf, s, lambda: [f() for f in calls], reps)
+        tf = flops / (ms * 1e-3) / 1e12
+        qms = time_launches(rf, s, lambda: rf.mx4_quantize(s, m, cfg.dim, acts[cfg.dim][0], True, acts[cfg.dim][1],
+                                                           acts[cfg.dim][2]), 20)
+        out[f"m{m}"] = {"stack_us": round(ms * 1e3, 1), "stack_TFLOP": round(flops / 1e12, 4),
+                        "stack_TFLOP_s": round(tf, 1), "stack_frac_fp4_peak": round(tf / FP4_PEAK_TFLOPS, 4),
+                        "quantize_us_k4096": round(qms * 1e3, 2), "shapes": res}
+        log(f"gemm M={m}: stack {ms * 1e3:.0f} us, {tf:.0f} TFLOP/s ({100 * tf / FP4_PEAK_TFLOPS:.1f}% of FP4 peak); "
+            + ", ".join(f"{k} {v['us']}us {v['TFLOP_s']}TF" for k, v in res.items()))
+    for a16, ac, asc in acts.values():
+        a16.free(), ac.free(), asc.free()
+    c.free()
+    out["workload"] = ("Llama-3-8B projections as MXFP4 GEMMs, bf16 activations ~N(0,1) quantized to MXFP4 per 32 "
+                       "along K; stack = 32 layers x (qkv, o, gate+up, down) + LM head")
+    out["peak_TFLOP_s"] = FP4_PEAK_TFLOPS
+    return out
+
+
+def pmc_probe(rf):
+    """Fixed launch sequence for the HBM-traffic counter runs (rocprofv3
+    --pmc FETCH_SIZE, then WRITE_SIZE): the gate/up SwiGLU GEMV of all 32
+    layers of the 8B model, then a plain f32 copy of 64 Mi floats (256 MiB
+    read + 256 MiB written) used to scale the counters."""
+    cfg = rf.model_config("llama3-8b", max_seq=64)
+    eng = rf.Engine(cfg, SEED)
+    s = eng.stream
+    x = rf.DeviceBuffer.from_host(np.random.default_rng(0).standard_normal(cfg.ffn).astype(np.float32), s)
+    y = rf.DeviceBuffer.zeroed(cfg.ffn, np.float32, s)
+    for l in range(cfg.n_layers):
+        gc, gs, _, _ = eng.weight(l, 4)
+        rf.mx4_gemv_swiglu(s, cfg.ffn, cfg.dim, cfg.ffn, gc, gs, x, y)
+    s.synchronize()
+    n = 64 << 20
+    src = rf.DeviceBuffer.zeroed(n, np.float32, s)
+    dst = rf.DeviceBuffer.zeroed(n, np.float32, s)
+    for _ in range(4):
+        rf.copy_into(s, n, 0, src, dst)
+    s.synchronize()
+    eng.close()
+    print(json.dumps({"pmc_probe": "done", "gemv_launches": cfg.n_layers, "gemv_bytes": gemv_bytes(2 * cfg.ffn, cfg.dim)
+                      - 4 * cfg.ffn, "copy_launches": 4, "copy_read_bytes": 4 * n, "copy_write_bytes": 4 * n}),
+          flush=True)
+
+
+def load_traffic():
+    """HBM bytes per launch of the gate/up GEMV from the committed counter
+    summary (profiles/gemv_swiglu_llama3-8b_traffic.json), or None."""
+    p = os.path.join(ROOT, "profiles", "gemv_swiglu_llama3-8b_traffic.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        return json.load(f).get("traffic_bytes_per_launch")
+
+
 def decode_run(rf, preset, max_seq, prefill, prompt, warmup, steps):
     cfg = rf.model_config(preset, max_seq=max_seq)
     eng = rf.Engine(cfg, SEED)
@@ -132,6 +249,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--cpu-steps", type=int, default=2)
     ap.add_argument("--no-tiny", action="store_true", help="skip the TinyLlama-1.1B line")
+    ap.add_argument("--no-gemm", action="store_true", help="skip the config-5 batched GEMM figures")
+    ap.add_argument("--pmc-probe", action="store_true", help="only the launch sequence of the counter runs")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -142,6 +261,9 @@ def main():
     import rfp4 as rf
 
     rf.init(0)
+    if args.pmc_probe:
+        pmc_probe(rf)
+        return
     # ---- config 4: Llama-3-8B decode at batch 1, ctx 4096
     max_seq = PREFILL + args.warmup + args.steps + 8
     eng, cfg, ms, wall, ids = decode_run(rf, "llama3-8b", max_seq, PREFILL, [1], args.warmup, args.steps)
@@ -156,6 +278,7 @@ def main():
     path_gbs = path_bytes / path_ms / 1e6
     log(f"GEMV path: {path_bytes / 1e9:.3f} GB in {path_ms * 1e3:.1f} us -> {path_gbs:.0f} GB/s; "
         f"gate/up GEMV {gate_ms * 1e3:.2f} us -> {gate_gbs:.0f} GB/s")
+    gemm = None if args.no_gemm else gemm_config5(rf, eng, cfg)
     eng.close()
 
     tiny = None
@@ -203,7 +326,7 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gate_gbs / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": load_traffic(),
             "bytes_per_launch": gate_bytes,
             "us_per_launch": round(gate_ms * 1e3, 3),
         },
@@ -214,6 +337,7 @@ def main():
             "frac": round(path_gbs / HBM_PEAK_GBS, 4),
         },
         "tinyllama": tiny,
+        "gemm_config5": gemm,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)
