@@ -345,16 +345,21 @@ RFP4_DEV void attn_body(const AttnArgs &a)
         }
     }
 
-    // ---- last workgroup of this KV head merges all splits
-    __threadfence();
+    // ---- last workgroup of this KV head merges all splits.  Every wave waits
+    // for its own partial stores, then one agent-scope release by thread 0
+    // publishes the workgroup's stores before the counter increment (an
+    // agent-scope fence writes back the L2, so it is issued once per
+    // workgroup, not once per wave); the merging workgroup acquires once.
+    __builtin_amdgcn_s_waitcnt(0x0f70); // vmcnt(0)
     __syncthreads();
     if (tid == 0) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
         uint32_t prev = atomicAdd(&a.counters[kvh], 1u);
         s_last = (prev == nsplit - 1) ? 1 : 0;
+        if (s_last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     }
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
     attn_merge<HD>(a, kvh, G, nsplit, &vred[0][0][0], tid, lane, wave);
     if (tid == 0) a.counters[kvh] = 0u;
 }
