@@ -160,6 +160,9 @@ int fp4_gemm(rfp4_stream_t stream, uint32_t m, uint32_t n, uint32_t k, const uin
  * split (0 = automatic) of later fp4_gemm calls on this thread.  No
  * reference counterpart. */
 int rfp4_debug_gemm_plan(int tile, int kz);
+/* Test hook: tokens per split of later attn_decode / attn_decode_f16 calls
+ * on this thread (0 = automatic).  No reference counterpart. */
+int rfp4_debug_attn_chunk(uint32_t chunk);
 /* The tile and K split fp4_gemm would use for this shape (honours the test
  * hook).  No reference counterpart. */
 int rfp4_gemm_plan(uint32_t m, uint32_t n, uint32_t k, int *tile_m, int *tile_n, int *kz);

@@ -5,12 +5,14 @@
 //
 // Grid (n_kv_heads, splits).  A workgroup owns one KV head and `chunk` tokens
 // and serves every query head of its GQA group, so each K/V byte is read from
-// HBM once.  A token row is split over LPT lanes, 16 bytes each, and every
-// thread issues the K and V loads of all its tokens before any arithmetic, so
-// a workgroup costs one memory round trip.  Each split keeps a local softmax
-// state (m, l, acc[HD]); the last workgroup of a KV head to finish (agent-scope
-// counter) merges the splits: M = max m_i, L = sum l_i e^(m_i-M),
-// out = sum acc_i e^(m_i-M) / L.
+// HBM once.  A token row is split over LPT lanes, 16 bytes each.  The split is
+// walked in sub-chunks of as many rows as the registers hold (attn_sub_chunk):
+// every K and V load of a sub-chunk is issued before its arithmetic, the next
+// sub-chunk's K loads go out right after the scores and its V loads right
+// after P.V, and an online softmax (m, l, acc[HD]) carries over.  A split that
+// covers the whole sequence writes the output itself; otherwise the last
+// workgroup of a KV head to finish (agent-scope counter) merges the splits:
+// M = max m_i, L = sum l_i e^(m_i-M), out = sum acc_i e^(m_i-M) / L.
 //
 // Optional fusion (engine): with rope tables given, q and the current token's
 // k are rotated here (llama_run/src/main.rs:517-518) and the split owning
@@ -65,84 +67,79 @@ RFP4_DEV float group_sum(float v)
 }
 
 // Merge the nsplit partial states of the G heads of one KV head:
-//   M = max m_i, L = sum l_i e^(m_i - M), out = (sum acc_i e^(m_i - M)) / L.
-// scratch: >= 4*8*HD floats of LDS (the P.V reduction buffer, free by now).
-// (m, l) pairs are staged in LDS with one round of loads; the accumulators
-// are read as float4 in batches of independent loads.
+//   M = max m_i, L = sum l_i e^(m_i - M), out = (sum acc_i e^(m_i - M)) / L,
+// computed online (running max) so that every load of a batch of splits is in
+// flight at once.  Thread tid owns the float4 outputs q and q + 128 of the
+// G*HD/4 (q = tid % 128) over the splits h, h + 2, h + 4, ... (h = tid / 128);
+// the two halves are combined through LDS.  scratch: >= 256 * 6 floats of LDS.
+#define ATTN_MERGE_BATCH 8
 template <int HD>
 RFP4_DEV void attn_merge(const AttnArgs &a, uint32_t kvh, uint32_t G, uint32_t nsplit, float *scratch, int tid,
                          int lane, int wave)
 {
+    (void)lane;
+    (void)wave;
     constexpr uint32_t STRIDE = HD + 4;
-    constexpr uint32_t CAP = 4 * ATTN_MAX_GROUP * HD / 2; // (m, l) pairs that fit the scratch
-    __shared__ float s_M[ATTN_MAX_GROUP], s_L[ATTN_MAX_GROUP];
-    float *ms = scratch, *ls = scratch + CAP;
-    const bool staged = G * nsplit <= CAP;
-    if (staged) {
-        for (uint32_t i = tid; i < G * nsplit; i += blockDim.x) {
-            uint32_t g = i / nsplit, sp = i % nsplit;
-            const float *pp = a.part + ((size_t)(kvh * G + g) * a.max_splits + sp) * STRIDE;
-            ms[i] = pp[0];
-            ls[i] = pp[1];
-        }
-        __syncthreads();
-    }
-    // per head: M, then e_i = exp(m_i - M) in place of m_i, and L
-    for (uint32_t g = wave; g < G; g += 4) {
+    const uint32_t quads = G * HD / 4; // <= 256 (G <= 8, HD <= 128)
+    const uint32_t qd = (uint32_t)tid & 127u, h = (uint32_t)tid >> 7;
+    float M[2], L[2];
+    float4 o[2];
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        M[r] = -3.402823466e38f;
+        L[r] = 0.0f;
+        o[r] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const uint32_t q = qd + 128u * r;
+        if (q >= quads) continue;
+        const uint32_t g = q / (HD / 4), d4 = q % (HD / 4);
         const float *hp = a.part + (size_t)(kvh * G + g) * a.max_splits * STRIDE;
-        float M = -3.402823466e38f;
-        for (uint32_t sp = lane; sp < nsplit; sp += 64) M = fmaxf(M, staged ? ms[g * nsplit + sp] : hp[sp * STRIDE]);
-        M = wave_max(M);
-        float L = 0.0f;
-        for (uint32_t sp = lane; sp < nsplit; sp += 64) {
-            float m = staged ? ms[g * nsplit + sp] : hp[sp * STRIDE];
-            float l = staged ? ls[g * nsplit + sp] : hp[sp * STRIDE + 1];
-            float e = expf(m - M);
-            if (staged) ms[g * nsplit + sp] = e;
-            L = fmaf(l, e, L);
+        for (uint32_t sp0 = h; sp0 < nsplit; sp0 += 2u * ATTN_MERGE_BATCH) {
+            float2 ml[ATTN_MERGE_BATCH];
+            float4 v[ATTN_MERGE_BATCH];
+#pragma unroll
+            for (int j = 0; j < ATTN_MERGE_BATCH; j++) {
+                const uint32_t sp = min(sp0 + 2u * j, nsplit - 1u);
+                ml[j] = *(const float2 *)(hp + (size_t)sp * STRIDE);
+                v[j] = *(const float4 *)(hp + (size_t)sp * STRIDE + 4 + d4 * 4);
+            }
+#pragma unroll
+            for (int j = 0; j < ATTN_MERGE_BATCH; j++) {
+                if (sp0 + 2u * j >= nsplit) break;
+                const float Mn = fmaxf(M[r], ml[j].x);
+                const float ea = expf(M[r] - Mn), eb = expf(ml[j].x - Mn);
+                L[r] = fmaf(L[r], ea, ml[j].y * eb);
+                o[r].x = fmaf(o[r].x, ea, v[j].x * eb);
+                o[r].y = fmaf(o[r].y, ea, v[j].y * eb);
+                o[r].z = fmaf(o[r].z, ea, v[j].z * eb);
+                o[r].w = fmaf(o[r].w, ea, v[j].w * eb);
+                M[r] = Mn;
+            }
         }
-        L = wave_sum(L);
-        if (lane == 0) {
-            s_M[g] = M;
-            s_L[g] = L;
+    }
+    if (h == 1u) {
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            float *sh = scratch + (qd + 128u * r) * 6u;
+            sh[0] = M[r]; sh[1] = L[r]; sh[2] = o[r].x; sh[3] = o[r].y; sh[4] = o[r].z; sh[5] = o[r].w;
         }
     }
     __syncthreads();
-    // outputs: one float4 of one head per thread, all splits
-    const uint32_t quads = G * HD / 4;
-    for (uint32_t qd = tid; qd < quads; qd += blockDim.x) {
-        const uint32_t g = qd / (HD / 4), d4 = qd % (HD / 4);
-        const float *hp = a.part + (size_t)(kvh * G + g) * a.max_splits * STRIDE + 4 + d4 * 4;
-        const float M = s_M[g];
-        float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        uint32_t sp = 0;
-        for (; sp + 8 <= nsplit; sp += 8) {
-            float4 v[8];
+    if (h == 0u) {
 #pragma unroll
-            for (int j = 0; j < 8; j++) v[j] = *(const float4 *)(hp + (size_t)(sp + j) * STRIDE);
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                float e = staged ? ms[g * nsplit + sp + j] : expf(hp[(size_t)(sp + j) * STRIDE - 4 - d4 * 4] - M);
-                o.x = fmaf(v[j].x, e, o.x);
-                o.y = fmaf(v[j].y, e, o.y);
-                o.z = fmaf(v[j].z, e, o.z);
-                o.w = fmaf(v[j].w, e, o.w);
-            }
+        for (int r = 0; r < 2; r++) {
+            const uint32_t q = qd + 128u * r;
+            if (q >= quads) continue;
+            const float *sh = scratch + q * 6u;
+            const float M1 = sh[0], L1 = sh[1];
+            const float Mn = fmaxf(M[r], M1), ea = expf(M[r] - Mn), eb = expf(M1 - Mn);
+            const float Lt = fmaf(L[r], ea, L1 * eb);
+            const uint32_t g = q / (HD / 4), d4 = q % (HD / 4);
+            float *dst = a.out + (size_t)(kvh * G + g) * HD + d4 * 4;
+            dst[0] = __fdiv_rn(fmaf(o[r].x, ea, sh[2] * eb), Lt);
+            dst[1] = __fdiv_rn(fmaf(o[r].y, ea, sh[3] * eb), Lt);
+            dst[2] = __fdiv_rn(fmaf(o[r].z, ea, sh[4] * eb), Lt);
+            dst[3] = __fdiv_rn(fmaf(o[r].w, ea, sh[5] * eb), Lt);
         }
-        for (; sp < nsplit; sp++) {
-            float4 v = *(const float4 *)(hp + (size_t)sp * STRIDE);
-            float e = staged ? ms[g * nsplit + sp] : expf(hp[(size_t)sp * STRIDE - 4 - d4 * 4] - M);
-            o.x = fmaf(v.x, e, o.x);
-            o.y = fmaf(v.y, e, o.y);
-            o.z = fmaf(v.z, e, o.z);
-            o.w = fmaf(v.w, e, o.w);
-        }
-        const float L = s_L[g];
-        float *dst = a.out + (size_t)(kvh * G + g) * HD + d4 * 4;
-        dst[0] = __fdiv_rn(o.x, L);
-        dst[1] = __fdiv_rn(o.y, L);
-        dst[2] = __fdiv_rn(o.z, L);
-        dst[3] = __fdiv_rn(o.w, L);
     }
 }
 
@@ -152,11 +149,12 @@ RFP4_DEV void attn_body(const AttnArgs &a)
     constexpr int EPL = KvTraits<KT>::EPL;
     constexpr int LPT = HD / EPL;          // lanes per token row
     constexpr int TPS = 256 / LPT;         // tokens per workgroup step
+    constexpr uint32_t CAPT = TPS * ATTN_MAX_STEPS; // tokens of one sub-chunk (held in registers)
     static_assert(LPT >= 4 && LPT <= 32, "row split");
     __shared__ float qs[ATTN_MAX_GROUP][HD];
-    __shared__ float ps[ATTN_MAX_GROUP][TPS * ATTN_MAX_STEPS];
+    __shared__ float ps[ATTN_MAX_GROUP][CAPT];
     __shared__ float vred[4][ATTN_MAX_GROUP][HD];
-    __shared__ float s_m[ATTN_MAX_GROUP], s_l[ATTN_MAX_GROUP];
+    __shared__ float s_m[ATTN_MAX_GROUP], s_l[ATTN_MAX_GROUP], s_alpha[ATTN_MAX_GROUP];
     __shared__ uint16_t knew[HD], vnew[HD];
     __shared__ int s_last;
 
@@ -171,26 +169,25 @@ RFP4_DEV void attn_body(const AttnArgs &a)
     const uint32_t G = a.n_heads / a.n_kv_heads;
     const uint32_t t0 = split * chunk;
     const uint32_t nt = min(seq, t0 + chunk) - t0;
-    const uint32_t nstep = (chunk + TPS - 1) / TPS;
+    const uint32_t nsub = (nt + CAPT - 1) / CAPT;
     const uint32_t pos = seq - 1;
     const bool fused = a.cosv != nullptr;
     const bool owner = fused && (pos >= t0) && (pos < t0 + nt);
     const KT *kc = (const KT *)a.kc + (size_t)kvh * a.hs;
     const KT *vc = (const KT *)a.vc + (size_t)kvh * a.hs;
 
-    // ---- issue every K and V load of this split first
+    // ---- K and V rows of sub-chunk C: token t0 + C*CAPT + s*TPS + slot, lanes split the row
     uint4 kr[ATTN_MAX_STEPS], vr[ATTN_MAX_STEPS];
-#pragma unroll
-    for (int s = 0; s < ATTN_MAX_STEPS; s++) {
-        uint32_t t = (uint32_t)s * TPS + (uint32_t)slot;
-        kr[s] = make_uint4(0, 0, 0, 0);
-        vr[s] = make_uint4(0, 0, 0, 0);
-        if ((uint32_t)s < nstep && t < nt) {
-            size_t off = (size_t)(t0 + t) * a.ts + (size_t)li * EPL;
-            kr[s] = *(const uint4 *)(kc + off);
-            vr[s] = *(const uint4 *)(vc + off);
-        }
-    }
+#define RFP4_ATTN_LOAD(R, BASE, C)                                                              \
+    do {                                                                                        \
+        _Pragma("unroll") for (int s_ = 0; s_ < ATTN_MAX_STEPS; s_++) {                         \
+            const uint32_t t_ = (C) * CAPT + (uint32_t)s_ * TPS + (uint32_t)slot;               \
+            R[s_] = make_uint4(0, 0, 0, 0);                                                     \
+            if (t_ < nt) R[s_] = *(const uint4 *)((BASE) + (size_t)(t0 + t_) * a.ts + (size_t)li * EPL); \
+        }                                                                                       \
+    } while (0)
+    RFP4_ATTN_LOAD(kr, kc, 0u);
+    RFP4_ATTN_LOAD(vr, vc, 0u);
 
     // ---- q (rotated if fused) into LDS; the owner split appends k, v
     const float *qg = a.q + (size_t)(kvh * G) * HD;
@@ -225,92 +222,117 @@ RFP4_DEV void attn_body(const AttnArgs &a)
     } else {
         for (uint32_t i = tid; i < G * HD; i += blockDim.x) qs[i / HD][i % HD] = qg[i];
     }
-    __syncthreads();
-    if (owner) {
-        // the thread holding position `pos` takes the freshly rotated row
-        uint32_t tl = pos - t0;
-        if ((uint32_t)slot == tl % TPS) {
-            uint32_t s = tl / TPS;
-            uint4 kk, vv;
-            const uint16_t *kp = knew + li * EPL, *vp = vnew + li * EPL;
-            kk.x = kp[0] | ((uint32_t)kp[1] << 16); kk.y = kp[2] | ((uint32_t)kp[3] << 16);
-            kk.z = kp[4] | ((uint32_t)kp[5] << 16); kk.w = kp[6] | ((uint32_t)kp[7] << 16);
-            vv.x = vp[0] | ((uint32_t)vp[1] << 16); vv.y = vp[2] | ((uint32_t)vp[3] << 16);
-            vv.z = vp[4] | ((uint32_t)vp[5] << 16); vv.w = vp[6] | ((uint32_t)vp[7] << 16);
-#pragma unroll
-            for (int st = 0; st < ATTN_MAX_STEPS; st++)
-                if ((uint32_t)st == s) {
-                    kr[st] = kk;
-                    vr[st] = vv;
-                }
-        }
+    if (tid < (int)G) {
+        s_m[tid] = -3.402823466e38f;
+        s_l[tid] = 0.0f;
     }
+    __syncthreads();
 
-    // ---- scores
     float qv[ATTN_MAX_GROUP][EPL];
 #pragma unroll
     for (int g = 0; g < ATTN_MAX_GROUP; g++)
 #pragma unroll
         for (int e = 0; e < EPL; e++) qv[g][e] = (uint32_t)g < G ? qs[g][li * EPL + e] : 0.0f;
     const float scale = __fdiv_rn(1.0f, __fsqrt_rn((float)HD));
-#pragma unroll
-    for (int s = 0; s < ATTN_MAX_STEPS; s++) {
-        if ((uint32_t)s >= nstep) break;
-        float kf[EPL];
-        KvTraits<KT>::widen(kr[s], kf);
-        uint32_t t = (uint32_t)s * TPS + (uint32_t)slot;
-#pragma unroll
-        for (int g = 0; g < ATTN_MAX_GROUP; g++) {
-            if ((uint32_t)g >= G) break;
-            float d = 0.0f;
-#pragma unroll
-            for (int e = 0; e < EPL; e++) d = fmaf(qv[g][e], kf[e], d);
-            d = group_sum<LPT>(d);
-            if (li == 0 && t < nt) ps[g][t] = d * scale;
-        }
-    }
-    __syncthreads();
-
-    // ---- local softmax per head: wave w handles heads w, w+4
-    for (uint32_t g = wave; g < G; g += 4) {
-        float m = -3.402823466e38f;
-        for (uint32_t t = lane; t < nt; t += 64) m = fmaxf(m, ps[g][t]);
-        m = wave_max(m);
-        float l = 0.0f;
-        for (uint32_t t = lane; t < nt; t += 64) {
-            float p = expf(ps[g][t] - m);
-            ps[g][t] = p;
-            l += p;
-        }
-        l = wave_sum(l);
-        if (lane == 0) {
-            s_m[g] = m;
-            s_l[g] = l;
-        }
-    }
-    __syncthreads();
-
-    // ---- P.V over this thread's tokens, then reduce over token slots
     float acc[ATTN_MAX_GROUP][EPL];
 #pragma unroll
     for (int g = 0; g < ATTN_MAX_GROUP; g++)
 #pragma unroll
         for (int e = 0; e < EPL; e++) acc[g][e] = 0.0f;
+
+    for (uint32_t c = 0; c < nsub; c++) {
+        const uint32_t tb = c * CAPT, ntc = min(CAPT, nt - tb);
+        if (owner && pos - t0 >= tb && pos - t0 < tb + ntc) {
+            // the thread holding position `pos` takes the freshly rotated row
+            const uint32_t tl = pos - t0 - tb;
+            if ((uint32_t)slot == tl % TPS) {
+                const uint32_t s = tl / TPS;
+                uint4 kk, vv;
+                const uint16_t *kp = knew + li * EPL, *vp = vnew + li * EPL;
+                kk.x = kp[0] | ((uint32_t)kp[1] << 16); kk.y = kp[2] | ((uint32_t)kp[3] << 16);
+                kk.z = kp[4] | ((uint32_t)kp[5] << 16); kk.w = kp[6] | ((uint32_t)kp[7] << 16);
+                vv.x = vp[0] | ((uint32_t)vp[1] << 16); vv.y = vp[2] | ((uint32_t)vp[3] << 16);
+                vv.z = vp[4] | ((uint32_t)vp[5] << 16); vv.w = vp[6] | ((uint32_t)vp[7] << 16);
 #pragma unroll
-    for (int s = 0; s < ATTN_MAX_STEPS; s++) {
-        if ((uint32_t)s >= nstep) break;
-        uint32_t t = (uint32_t)s * TPS + (uint32_t)slot;
-        if (t >= nt) continue;
-        float vf[EPL];
-        KvTraits<KT>::widen(vr[s], vf);
+                for (int st = 0; st < ATTN_MAX_STEPS; st++)
+                    if ((uint32_t)st == s) {
+                        kr[st] = kk;
+                        vr[st] = vv;
+                    }
+            }
+        }
+
+        // ---- scores of this sub-chunk, then the next sub-chunk's K loads
+#pragma unroll
+        for (int s = 0; s < ATTN_MAX_STEPS; s++) {
+            const uint32_t t = (uint32_t)s * TPS + (uint32_t)slot;
+            if ((uint32_t)s * TPS >= ntc) break;
+            float kf[EPL];
+            KvTraits<KT>::widen(kr[s], kf);
+#pragma unroll
+            for (int g = 0; g < ATTN_MAX_GROUP; g++) {
+                if ((uint32_t)g >= G) break;
+                float d = 0.0f;
+#pragma unroll
+                for (int e = 0; e < EPL; e++) d = fmaf(qv[g][e], kf[e], d);
+                d = group_sum<LPT>(d);
+                if (li == 0 && t < ntc) ps[g][t] = d * scale;
+            }
+        }
+        if (c + 1 < nsub) RFP4_ATTN_LOAD(kr, kc, c + 1);
+        __syncthreads();
+
+        // ---- online softmax per head (wave w handles heads w, w+4):
+        //      m' = max(m, max_t s_t), p_t = e^(s_t - m'), l' = l e^(m - m') + sum_t p_t
+        for (uint32_t g = wave; g < G; g += 4) {
+            float mc = -3.402823466e38f;
+            for (uint32_t t = lane; t < ntc; t += 64) mc = fmaxf(mc, ps[g][t]);
+            mc = wave_max(mc);
+            const float m_old = s_m[g], m_new = fmaxf(m_old, mc);
+            float l = 0.0f;
+            for (uint32_t t = lane; t < ntc; t += 64) {
+                float p = expf(ps[g][t] - m_new);
+                ps[g][t] = p;
+                l += p;
+            }
+            l = wave_sum(l);
+            if (lane == 0) {
+                const float alpha = expf(m_old - m_new);
+                s_alpha[g] = alpha;
+                s_l[g] = fmaf(s_l[g], alpha, l);
+                s_m[g] = m_new;
+            }
+        }
+        __syncthreads();
+
+        // ---- rescale the running P.V, add this sub-chunk's, then the next sub-chunk's V loads
 #pragma unroll
         for (int g = 0; g < ATTN_MAX_GROUP; g++) {
             if ((uint32_t)g >= G) break;
-            float p = ps[g][t];
+            const float alpha = s_alpha[g];
 #pragma unroll
-            for (int e = 0; e < EPL; e++) acc[g][e] = fmaf(p, vf[e], acc[g][e]);
+            for (int e = 0; e < EPL; e++) acc[g][e] *= alpha;
         }
+#pragma unroll
+        for (int s = 0; s < ATTN_MAX_STEPS; s++) {
+            const uint32_t t = (uint32_t)s * TPS + (uint32_t)slot;
+            if ((uint32_t)s * TPS >= ntc) break;
+            if (t >= ntc) continue;
+            float vf[EPL];
+            KvTraits<KT>::widen(vr[s], vf);
+#pragma unroll
+            for (int g = 0; g < ATTN_MAX_GROUP; g++) {
+                if ((uint32_t)g >= G) break;
+                const float p = ps[g][t];
+#pragma unroll
+                for (int e = 0; e < EPL; e++) acc[g][e] = fmaf(p, vf[e], acc[g][e]);
+            }
+        }
+        if (c + 1 < nsub) RFP4_ATTN_LOAD(vr, vc, c + 1);
+        __syncthreads(); // ps is rewritten by the next sub-chunk
     }
+#undef RFP4_ATTN_LOAD
+
     // lanes li, li+LPT, ... of a wave hold the same dims: fold them
 #pragma unroll
     for (int g = 0; g < ATTN_MAX_GROUP; g++) {
@@ -331,6 +353,16 @@ RFP4_DEV void attn_body(const AttnArgs &a)
         }
     }
     __syncthreads();
+
+    if (nsplit == 1) {
+        // one split holds the whole sequence: normalise and write the heads' outputs
+        for (uint32_t i = tid; i < G * HD; i += blockDim.x) {
+            const uint32_t g = i / HD, d = i % HD;
+            const float v = vred[0][g][d] + vred[1][g][d] + vred[2][g][d] + vred[3][g][d];
+            a.out[(size_t)(kvh * G + g) * HD + d] = __fdiv_rn(v, s_l[g]);
+        }
+        return;
+    }
 
     // ---- write this split's partial state: [m, l, -, -, acc[HD]] per (head, split)
     const uint32_t stride = HD + 4;
@@ -364,8 +396,8 @@ RFP4_DEV void attn_body(const AttnArgs &a)
     if (tid == 0) a.counters[kvh] = 0u;
 }
 
-// Largest chunk (tokens per split) the register plan of attn_body holds.
-constexpr uint32_t attn_max_chunk(uint32_t hd, uint32_t elem_bytes)
+// Tokens of one sub-chunk (the K/V rows attn_body holds in registers at once).
+constexpr uint32_t attn_sub_chunk(uint32_t hd, uint32_t elem_bytes)
 {
     return (256u / (hd * elem_bytes / 16u)) * ATTN_MAX_STEPS;
 }

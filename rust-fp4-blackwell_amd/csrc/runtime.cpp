@@ -381,15 +381,14 @@ int attn_launch(const AttnArgs &args, int kv_f16, hipStream_t s, uint32_t max_se
     if (args.head_dim == 64) name = kv_f16 ? "rfp4_attn_hd64_f16" : "rfp4_attn_hd64_f32";
     else if (args.head_dim == 128) name = kv_f16 ? "rfp4_attn_hd128_f16" : "rfp4_attn_hd128_f32";
     else return set_error(RFP4_E_SHAPE, "attn: head_dim %u unsupported (64 or 128)", args.head_dim);
-    if (args.chunk == 0 || args.chunk > attn_max_chunk(args.head_dim, kv_f16 ? 2u : 4u))
-        return set_error(RFP4_E_CAPACITY, "attn: chunk %u exceeds the kernel's plan", args.chunk);
+    if (args.chunk == 0) return set_error(RFP4_E_INVALID, "attn: chunk must be positive");
     if (args.cosv && !kv_f16) return set_error(RFP4_E_INVALID, "attn: fused KV append needs an fp16 cache");
     uint32_t splits = (max_seq_for_grid + args.chunk - 1) / args.chunk;
     AttnArgs a = args;
     return launch(name, dim3(a.n_kv_heads, splits), dim3(256), s, &a);
 }
 
-uint32_t attn_max_chunk(uint32_t head_dim, uint32_t elem_bytes)
+uint32_t attn_sub_chunk(uint32_t head_dim, uint32_t elem_bytes)
 {
     // tokens per workgroup step (256 threads / lanes per 16-byte-split row)
     // times the 8 load steps each thread keeps in registers
@@ -397,16 +396,21 @@ uint32_t attn_max_chunk(uint32_t head_dim, uint32_t elem_bytes)
     return (256u / lanes_per_row) * 8u;
 }
 
+static thread_local uint32_t t_force_attn_chunk = 0;
+
 uint32_t attn_chunk_for(uint32_t n_kv_heads, uint32_t seq, uint32_t num_cus, uint32_t head_dim, uint32_t elem_bytes)
 {
-    // Enough (kv head, split) workgroups to cover every CU about twice; the
-    // chunk is a power of two in [64, max] tokens so that a cache allocated in
-    // whole 256-token pages always holds chunk * splits tokens.
+    if (t_force_attn_chunk) return t_force_attn_chunk;
+    // Enough (kv head, split) workgroups to cover every CU about twice, the
+    // chunk a power of two in [64, one sub-chunk] tokens, so that a cache
+    // allocated in whole 256-token pages always holds chunk * splits tokens.
+    // (A context that fits one chunk runs as one split per KV head, which
+    // writes the output itself.)
+    const uint32_t sub = attn_sub_chunk(head_dim, elem_bytes);
     uint32_t target_wg = 2u * num_cus;
     uint32_t splits_wanted = (target_wg + n_kv_heads - 1) / n_kv_heads;
-    uint32_t cap = attn_max_chunk(head_dim, elem_bytes);
-    uint32_t chunk = 64u < cap ? 64u : cap;
-    while (chunk < cap && (uint64_t)chunk * splits_wanted < seq) chunk *= 2u;
+    uint32_t chunk = 64u < sub ? 64u : sub;
+    while (chunk < sub && (uint64_t)chunk * splits_wanted < seq) chunk *= 2u;
     return chunk;
 }
 
@@ -682,6 +686,12 @@ int fp4_gemm(rfp4_stream_t stream, uint32_t m, uint32_t n, uint32_t k, const uin
     const uint64_t n4 = (uint64_t)m * n / 4u;
     return launch("rfp4_gemm_reduce", dim3((unsigned)std::min<uint64_t>((n4 + 255u) / 256u, 8192u)), dim3(256),
                   (hipStream_t)stream, &a);
+}
+
+int rfp4_debug_attn_chunk(uint32_t chunk)
+{
+    t_force_attn_chunk = chunk;
+    return RFP4_OK;
 }
 
 int rfp4_debug_gemm_plan(int tile, int kz)

@@ -84,6 +84,7 @@ _SIGS = {
     "mx4_quantize": (I32, [P, U64, U64, P, I32, P, P]),
     "fp4_gemm": (I32, [P, U32, U32, U32, P, P, P, P, P]),
     "rfp4_debug_gemm_plan": (I32, [I32, I32]),
+    "rfp4_debug_attn_chunk": (I32, [U32]),
     "rfp4_gemm_plan": (I32, [U32, U32, U32, P, P, P]),
     "rfp4_mma_tile16": (I32, [P, P, P, P, P, P]),
     "rfp4_mma_tile32": (I32, [P, P, P, P, P, P]),
@@ -344,6 +345,10 @@ def mx4_quantize(stream, rows, k, src, src_is_bf16, codes, scales):
 
 def fp4_gemm(stream, m, n, k, a_codes, a_scales, w_codes, w_scales, c):
     check(load().fp4_gemm(_s(stream), m, n, k, _p(a_codes), _p(a_scales), _p(w_codes), _p(w_scales), _p(c)))
+
+
+def debug_attn_chunk(chunk=0):
+    check(load().rfp4_debug_attn_chunk(chunk))
 
 
 def debug_gemm_plan(tile=-1, kz=0):

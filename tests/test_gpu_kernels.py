@@ -191,6 +191,19 @@ def test_rope_parity(rf, orc, stream, heads, hd, theta, pos):
     np.testing.assert_array_equal(got, qref)  # no fused multiply-add: bit-identical
 
 
+def _assert_attn_close(got, ref):
+    """Attention bar: the reference's per-element relative error 1e-4
+    (llama_attn_decode/src/main.rs:203-204, |d| / max(|ref|, 1e-3)) plus a
+    normwise floor of 1e-6 x max|ref| for outputs that are weighted averages
+    near zero (fp32 rounding of the softmax-weighted sum, different order)."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    err = np.abs(got - ref)
+    bound = 1e-4 * np.maximum(np.abs(ref), 1e-3) + 1e-6 * np.abs(ref).max()
+    bad = err > bound
+    assert not bad.any(), f"{bad.sum()} outputs off, worst rel {reference_rel_err(got, ref).max():.3e}"
+
+
 def test_attn_decode_reference_harness(rf, orc, stream):
     """llama_attn_decode/src/main.rs:132-221: 32q/8kv, hd 64, seq 512, seed 0xabcd1234, f32 KV."""
     NH, NKV, HD, SEQ = 32, 8, 64, 512
@@ -220,9 +233,7 @@ def test_attn_decode_f16_parity(rf, orc, stream, nh, nkv, hd, seq):
     dout = rf.DeviceBuffer.zeroed(nh * hd, np.float32, stream)
     rf.attn_decode_f16(stream, nh, nkv, hd, seq, _dev(rf, q, stream), _dev(rf, kc, stream), _dev(rf, vc, stream),
                        hd, cap * hd, dout)
-    got = dout.to_host(nh * hd, np.float32, stream)
-    rel = reference_rel_err(got, oref)
-    assert (rel > 1e-4).sum() == 0, rel.max()
+    _assert_attn_close(dout.to_host(nh * hd, np.float32, stream), oref)
 
 
 def test_swiglu_residual_copy(rf, orc, stream):
@@ -406,3 +417,44 @@ def test_invalid_shapes_return_errors(rf, stream):
         rf.attn_decode(stream, 6, 4, 10, buf, buf, buf, buf)
     with pytest.raises(rf.Rfp4Error):
         rf.attn_decode(stream, 8, 4, 0, buf, buf, buf, buf)
+
+
+@pytest.mark.parametrize("nh,nkv,hd,seq,chunk", [(32, 8, 128, 2500, 1000), (32, 8, 128, 2500, 4096), (32, 8, 128, 2500, 64),
+                                                 (32, 4, 64, 1500, 700), (32, 4, 64, 1500, 2000), (8, 8, 128, 129, 128),
+                                                 (64, 8, 128, 3000, 64), (64, 8, 128, 300, 0), (32, 8, 128, 4097, 0),
+                                                 (32, 8, 128, 40000, 0)])
+def test_attn_decode_f16_forced_chunks(rf, orc, stream, nh, nkv, hd, seq, chunk):
+    """Splits of several sub-chunks (online softmax across them), one split of
+    the whole sequence (no merge), many small splits, and a chunk that is not
+    a multiple of the sub-chunk."""
+    rng = np.random.default_rng(seq + chunk)
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    cap = seq + 3
+    kc = rng.standard_normal(nkv * cap * hd).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal(nkv * cap * hd).astype(np.float16).view(np.uint16)
+    oref = orc.attn_decode(nh, nkv, hd, seq, q, kc, vc, hd, cap * hd)
+    dout = rf.DeviceBuffer.zeroed(nh * hd, np.float32, stream)
+    rf.debug_attn_chunk(chunk)
+    try:
+        rf.attn_decode_f16(stream, nh, nkv, hd, seq, _dev(rf, q, stream), _dev(rf, kc, stream), _dev(rf, vc, stream),
+                           hd, cap * hd, dout)
+    finally:
+        rf.debug_attn_chunk(0)
+    _assert_attn_close(dout.to_host(nh * hd, np.float32, stream), oref)
+
+
+def test_attn_decode_reference_layout_forced_chunk(rf, orc, stream):
+    """The drop-in f32 [t][kvh][64] layout with 3 splits of 400 tokens."""
+    NH, NKV, HD, SEQ = 32, 8, 64, 1000
+    rng = np.random.default_rng(11)
+    q = rng.standard_normal(NH * HD).astype(np.float32)
+    kc = rng.standard_normal(SEQ * NKV * HD).astype(np.float32)
+    vc = rng.standard_normal(SEQ * NKV * HD).astype(np.float32)
+    oref = orc.attn_decode(NH, NKV, HD, SEQ, q, kc, vc, NKV * HD, HD)
+    dout = rf.DeviceBuffer.zeroed(NH * HD, np.float32, stream)
+    rf.debug_attn_chunk(400)
+    try:
+        rf.attn_decode(stream, NH, NKV, SEQ, _dev(rf, q, stream), _dev(rf, kc, stream), _dev(rf, vc, stream), dout)
+    finally:
+        rf.debug_attn_chunk(0)
+    _assert_attn_close(dout.to_host(NH * HD, np.float32, stream), oref)
