@@ -10,9 +10,12 @@
 // every K and V load of a sub-chunk is issued before its arithmetic, the next
 // sub-chunk's K loads go out right after the scores and its V loads right
 // after P.V, and an online softmax (m, l, acc[HD]) carries over.  A split that
-// covers the whole sequence writes the output itself; otherwise the last
-// workgroup of a KV head to finish (agent-scope counter) merges the splits:
-// M = max m_i, L = sum l_i e^(m_i-M), out = sum acc_i e^(m_i-M) / L.
+// covers the whole sequence writes the output itself; otherwise each split
+// writes its state and a second kernel (attn_merge_body, same stream) merges
+// them: M = max m_i, L = sum l_i e^(m_i-M), out = sum acc_i e^(m_i-M) / L.
+// (A last-workgroup merge inside this kernel would need an agent-scope
+// release per workgroup, an L2 writeback on gfx950, which costs more than the
+// kernel boundary.)
 //
 // Optional fusion (engine): with rope tables given, q and the current token's
 // k are rotated here (llama_run/src/main.rs:517-518) and the split owning
@@ -23,7 +26,16 @@
 #include "norm_rope.h"
 
 #define ATTN_MAX_GROUP 8
-#define ATTN_MAX_STEPS 8
+#define ATTN_MAX_STEPS 9
+
+// 16-byte row pieces each thread holds per sub-chunk: 9 for fp16 rows of 128
+// (144 tokens, so a 4096-token context needs 29 splits per KV head and 8 KV
+// heads fit one workgroup per CU), 8 otherwise.
+template <int HD, typename KT>
+constexpr int attn_steps()
+{
+    return (HD == 128 && sizeof(KT) == 2) ? 9 : 8;
+}
 
 template <typename KT>
 struct KvTraits;
@@ -149,14 +161,14 @@ RFP4_DEV void attn_body(const AttnArgs &a)
     constexpr int EPL = KvTraits<KT>::EPL;
     constexpr int LPT = HD / EPL;          // lanes per token row
     constexpr int TPS = 256 / LPT;         // tokens per workgroup step
-    constexpr uint32_t CAPT = TPS * ATTN_MAX_STEPS; // tokens of one sub-chunk (held in registers)
+    constexpr int NSTEP = attn_steps<HD, KT>();
+    constexpr uint32_t CAPT = TPS * NSTEP;  // tokens of one sub-chunk (held in registers)
     static_assert(LPT >= 4 && LPT <= 32, "row split");
     __shared__ float qs[ATTN_MAX_GROUP][HD];
     __shared__ float ps[ATTN_MAX_GROUP][CAPT];
     __shared__ float vred[4][ATTN_MAX_GROUP][HD];
     __shared__ float s_m[ATTN_MAX_GROUP], s_l[ATTN_MAX_GROUP], s_alpha[ATTN_MAX_GROUP];
     __shared__ uint16_t knew[HD], vnew[HD];
-    __shared__ int s_last;
 
     const uint32_t kvh = blockIdx.x, split = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -177,10 +189,10 @@ RFP4_DEV void attn_body(const AttnArgs &a)
     const KT *vc = (const KT *)a.vc + (size_t)kvh * a.hs;
 
     // ---- K and V rows of sub-chunk C: token t0 + C*CAPT + s*TPS + slot, lanes split the row
-    uint4 kr[ATTN_MAX_STEPS], vr[ATTN_MAX_STEPS];
+    uint4 kr[NSTEP], vr[NSTEP];
 #define RFP4_ATTN_LOAD(R, BASE, C)                                                              \
     do {                                                                                        \
-        _Pragma("unroll") for (int s_ = 0; s_ < ATTN_MAX_STEPS; s_++) {                         \
+        _Pragma("unroll") for (int s_ = 0; s_ < NSTEP; s_++) {                         \
             const uint32_t t_ = (C) * CAPT + (uint32_t)s_ * TPS + (uint32_t)slot;               \
             R[s_] = make_uint4(0, 0, 0, 0);                                                     \
             if (t_ < nt) R[s_] = *(const uint4 *)((BASE) + (size_t)(t0 + t_) * a.ts + (size_t)li * EPL); \
@@ -254,7 +266,7 @@ RFP4_DEV void attn_body(const AttnArgs &a)
                 vv.x = vp[0] | ((uint32_t)vp[1] << 16); vv.y = vp[2] | ((uint32_t)vp[3] << 16);
                 vv.z = vp[4] | ((uint32_t)vp[5] << 16); vv.w = vp[6] | ((uint32_t)vp[7] << 16);
 #pragma unroll
-                for (int st = 0; st < ATTN_MAX_STEPS; st++)
+                for (int st = 0; st < NSTEP; st++)
                     if ((uint32_t)st == s) {
                         kr[st] = kk;
                         vr[st] = vv;
@@ -264,7 +276,7 @@ RFP4_DEV void attn_body(const AttnArgs &a)
 
         // ---- scores of this sub-chunk, then the next sub-chunk's K loads
 #pragma unroll
-        for (int s = 0; s < ATTN_MAX_STEPS; s++) {
+        for (int s = 0; s < NSTEP; s++) {
             const uint32_t t = (uint32_t)s * TPS + (uint32_t)slot;
             if ((uint32_t)s * TPS >= ntc) break;
             float kf[EPL];
@@ -314,7 +326,7 @@ RFP4_DEV void attn_body(const AttnArgs &a)
             for (int e = 0; e < EPL; e++) acc[g][e] *= alpha;
         }
 #pragma unroll
-        for (int s = 0; s < ATTN_MAX_STEPS; s++) {
+        for (int s = 0; s < NSTEP; s++) {
             const uint32_t t = (uint32_t)s * TPS + (uint32_t)slot;
             if ((uint32_t)s * TPS >= ntc) break;
             if (t >= ntc) continue;
@@ -364,7 +376,8 @@ RFP4_DEV void attn_body(const AttnArgs &a)
         return;
     }
 
-    // ---- write this split's partial state: [m, l, -, -, acc[HD]] per (head, split)
+    // ---- write this split's partial state: [m, l, -, -, acc[HD]] per (head, split);
+    // the merge kernel launched next on the same stream combines them
     const uint32_t stride = HD + 4;
     for (uint32_t i = tid; i < G * HD; i += blockDim.x) {
         uint32_t g = i / HD, d = i % HD;
@@ -376,28 +389,26 @@ RFP4_DEV void attn_body(const AttnArgs &a)
             a.part[base + 1] = s_l[g];
         }
     }
+}
 
-    // ---- last workgroup of this KV head merges all splits.  Every wave waits
-    // for its own partial stores, then one agent-scope release by thread 0
-    // publishes the workgroup's stores before the counter increment (an
-    // agent-scope fence writes back the L2, so it is issued once per
-    // workgroup, not once per wave); the merging workgroup acquires once.
-    __builtin_amdgcn_s_waitcnt(0x0f70); // vmcnt(0)
-    __syncthreads();
-    if (tid == 0) {
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        uint32_t prev = atomicAdd(&a.counters[kvh], 1u);
-        s_last = (prev == nsplit - 1) ? 1 : 0;
-        if (s_last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    }
-    __syncthreads();
-    if (!s_last) return;
-    attn_merge<HD>(a, kvh, G, nsplit, &vred[0][0][0], tid, lane, wave);
-    if (tid == 0) a.counters[kvh] = 0u;
+// Merge kernel body: grid (n_kv_heads), launched after attn_body on the same
+// stream (the kernel boundary orders the partial states before these reads).
+// Computes the split count exactly as attn_body did; one split means
+// attn_body already wrote the output.
+template <int HD>
+RFP4_DEV void attn_merge_body(const AttnArgs &a)
+{
+    __shared__ float scratch[256 * 6];
+    uint32_t seq = a.pos_ptr ? (uint32_t)(*a.pos_ptr + 1) : a.seq;
+    seq = min(seq, a.chunk * a.max_splits);
+    const uint32_t nsplit = (seq + a.chunk - 1) / a.chunk;
+    if (nsplit <= 1) return;
+    const int tid = threadIdx.x;
+    attn_merge<HD>(a, blockIdx.x, a.n_heads / a.n_kv_heads, nsplit, scratch, tid, tid & 63, tid >> 6);
 }
 
 // Tokens of one sub-chunk (the K/V rows attn_body holds in registers at once).
 constexpr uint32_t attn_sub_chunk(uint32_t hd, uint32_t elem_bytes)
 {
-    return (256u / (hd * elem_bytes / 16u)) * ATTN_MAX_STEPS;
+    return (256u / (hd * elem_bytes / 16u)) * ((hd == 128u && elem_bytes == 2u) ? 9u : 8u);
 }

@@ -149,6 +149,16 @@ RFP4_DEV void gemv_body(const GemvArgs &a)
     float acc[NP];
 #pragma unroll
     for (int p = 0; p < NP; p++) acc[p] = 0.0f;
+    // residual epilogue: the rows' current values are fetched before any
+    // weight load, so the epilogue does not wait on a memory round trip
+    float yres[EPI == RFP4_EPI_RESIDUAL ? R : 1];
+    if (EPI == RFP4_EPI_RESIDUAL) {
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const uint32_t lr = lrow0 + (uint32_t)i;
+            yres[i] = lr < a.n ? a.y[lr] : 0.0f;
+        }
+    }
 
     if (NS > 0) {
         // x (and norm weights) go into registers first, then every weight load
@@ -249,7 +259,7 @@ RFP4_DEV void gemv_body(const GemvArgs &a)
             if (EPI == RFP4_EPI_STORE) {
                 a.y[lr] = acc[i];
             } else if (EPI == RFP4_EPI_RESIDUAL) {
-                a.y[lr] = __fadd_rn(a.y[lr], acc[i]);
+                a.y[lr] = __fadd_rn(yres[EPI == RFP4_EPI_RESIDUAL ? i : 0], acc[i]);
             } else { // SWIGLU: silu(gate) * up  (llama_run/src/main.rs:244-252)
                 a.y[lr] = __fmul_rn(silu_ref(acc[i]), acc[R + i]);
             }

@@ -49,7 +49,6 @@ struct llama_engine {
     unsigned long long *best = nullptr;
     uint32_t n_best = 0;
     float *attn_part = nullptr;
-    uint32_t *attn_counters = nullptr;
     uint32_t attn_chunk = 64, attn_max_splits = 1;
     StepState *state = nullptr;
     uint32_t *ids = nullptr, *last_tok = nullptr;
@@ -107,7 +106,7 @@ static int enqueue_step(llama_engine *e)
         if ((rc = gemv_launch("e8m0", RFP4_EPI_STORE, qa, s, 0))) return rc;
         AttnArgs aa{};
         aa.q = e->qkv; aa.kc = kc; aa.vc = vc; aa.out = e->attn_out;
-        aa.part = e->attn_part; aa.counters = e->attn_counters; aa.pos_ptr = &e->state->pos;
+        aa.part = e->attn_part; aa.pos_ptr = &e->state->pos;
         aa.cosv = e->cos_tab; aa.sinv = e->sin_tab; aa.k_new = e->qkv + qd; aa.v_new = e->qkv + qd + kvd;
         aa.ts = hd; aa.hs = (uint64_t)e->max_seq_alloc * hd;
         aa.n_heads = c.n_heads; aa.n_kv_heads = c.n_kv_heads; aa.head_dim = hd; aa.seq = 0;
@@ -242,8 +241,6 @@ int llama_engine_create(const rfp4_model_config *cfg, uint64_t seed, llama_engin
     e->n_best = gemv_blocks(c.vocab, c.dim, RFP4_EPI_ARGMAX);
     if (!rc) rc = dalloc_t(e, &e->best, e->n_best);
     if (!rc) rc = dalloc_t(e, &e->attn_part, (size_t)c.n_heads * e->attn_max_splits * (hd + 4));
-    if (!rc) rc = dalloc_t(e, &e->attn_counters, c.n_kv_heads);
-    if (!rc) rc = fill_words(e->attn_counters, c.n_kv_heads, 0u, s);
     if (!rc) rc = dalloc(e, (void **)&e->state, sizeof(StepState));
     e->ids_alloc = c.max_seq + 2;
     if (!rc) rc = dalloc_t(e, &e->ids, e->ids_alloc);

@@ -81,6 +81,8 @@ K256 void rfp4_attn_hd64_f32(AttnArgs a) { attn_body<64, float>(a); }
 K256 void rfp4_attn_hd64_f16(AttnArgs a) { attn_body<64, uint16_t>(a); }
 K256 void rfp4_attn_hd128_f32(AttnArgs a) { attn_body<128, float>(a); }
 K256 void rfp4_attn_hd128_f16(AttnArgs a) { attn_body<128, uint16_t>(a); }
+K256 void rfp4_attn_merge_hd64(AttnArgs a) { attn_merge_body<64>(a); }
+K256 void rfp4_attn_merge_hd128(AttnArgs a) { attn_merge_body<128>(a); }
 
 // ---- misc
 K256 void rfp4_fill(FillArgs a) { fill_body(a); }

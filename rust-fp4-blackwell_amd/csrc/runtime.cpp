@@ -104,14 +104,11 @@ int rfp4_init(int device)
     // default workspace of the drop-in attn_decode
     rt->attn_part_floats = (size_t)kAttnMaxHeads * kAttnMaxSplits * (128 + 4); // [m, l, -, -, acc[hd]]
     rc = hip_check(hipMalloc((void **)&rt->attn_part, rt->attn_part_floats * sizeof(float)), "hipMalloc(attn workspace)");
-    if (!rc) rc = hip_check(hipMalloc((void **)&rt->attn_counters, kAttnMaxHeads * sizeof(uint32_t)), "hipMalloc(attn counters)");
-    if (!rc) rc = hip_check(hipMemset(rt->attn_counters, 0, kAttnMaxHeads * sizeof(uint32_t)), "hipMemset");
     // split-K workspace of fp4_gemm
     if (!rc) rc = hip_check(hipMalloc((void **)&rt->gemm_part, kGemmPartFloats * sizeof(float)), "hipMalloc(gemm workspace)");
     if (!rc) rc = hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
     if (rc) {
         hipFree(rt->attn_part);
-        hipFree(rt->attn_counters);
         hipFree(rt->gemm_part);
         hipModuleUnload(rt->module);
         delete rt;
@@ -385,15 +382,21 @@ int attn_launch(const AttnArgs &args, int kv_f16, hipStream_t s, uint32_t max_se
     if (args.cosv && !kv_f16) return set_error(RFP4_E_INVALID, "attn: fused KV append needs an fp16 cache");
     uint32_t splits = (max_seq_for_grid + args.chunk - 1) / args.chunk;
     AttnArgs a = args;
-    return launch(name, dim3(a.n_kv_heads, splits), dim3(256), s, &a);
+    int rc = launch(name, dim3(a.n_kv_heads, splits), dim3(256), s, &a);
+    if (rc || splits <= 1) return rc;
+    // the split states are merged by a second launch (stream order, no fence)
+    return launch(args.head_dim == 64 ? "rfp4_attn_merge_hd64" : "rfp4_attn_merge_hd128", dim3(a.n_kv_heads), dim3(256),
+                  s, &a);
 }
 
 uint32_t attn_sub_chunk(uint32_t head_dim, uint32_t elem_bytes)
 {
     // tokens per workgroup step (256 threads / lanes per 16-byte-split row)
-    // times the 8 load steps each thread keeps in registers
+    // times the load steps each thread keeps in registers (9 for fp16 rows of
+    // 128, else 8: device/attn.h attn_steps)
     uint32_t lanes_per_row = head_dim * elem_bytes / 16u;
-    return (256u / lanes_per_row) * 8u;
+    uint32_t steps = (head_dim == 128u && elem_bytes == 2u) ? 9u : 8u;
+    return (256u / lanes_per_row) * steps;
 }
 
 static thread_local uint32_t t_force_attn_chunk = 0;
@@ -401,17 +404,20 @@ static thread_local uint32_t t_force_attn_chunk = 0;
 uint32_t attn_chunk_for(uint32_t n_kv_heads, uint32_t seq, uint32_t num_cus, uint32_t head_dim, uint32_t elem_bytes)
 {
     if (t_force_attn_chunk) return t_force_attn_chunk;
-    // Enough (kv head, split) workgroups to cover every CU about twice, the
-    // chunk a power of two in [64, one sub-chunk] tokens, so that a cache
-    // allocated in whole 256-token pages always holds chunk * splits tokens.
-    // (A context that fits one chunk runs as one split per KV head, which
-    // writes the output itself.)
+    // At most one (KV head, split) workgroup per CU and at least 64 tokens per
+    // split; the chunk is a whole number of workgroup steps and at most one
+    // sub-chunk (one pass over registers) unless the context needs more
+    // workgroups than CUs, in which case it is exactly one sub-chunk.
     const uint32_t sub = attn_sub_chunk(head_dim, elem_bytes);
-    uint32_t target_wg = 2u * num_cus;
-    uint32_t splits_wanted = (target_wg + n_kv_heads - 1) / n_kv_heads;
-    uint32_t chunk = 64u < sub ? 64u : sub;
-    while (chunk < sub && (uint64_t)chunk * splits_wanted < seq) chunk *= 2u;
-    return chunk;
+    const uint32_t step = 256u / (head_dim * elem_bytes / 16u);
+    uint32_t splits = (seq + 63u) / 64u;
+    uint32_t per_head = num_cus / n_kv_heads;
+    if (per_head < 1u) per_head = 1u;
+    if (splits > per_head) splits = per_head;
+    if (splits < 1u) splits = 1u;
+    uint32_t chunk = (seq + splits - 1u) / splits;
+    chunk = (chunk + step - 1u) / step * step;
+    return chunk < sub ? chunk : sub;
 }
 
 } // namespace rfp4
@@ -549,7 +555,7 @@ static int attn_common(hipStream_t s, uint32_t nh, uint32_t nkv, uint32_t hd, ui
                          kAttnMaxSplits);
     AttnArgs a{};
     a.q = q; a.kc = kc; a.vc = vc; a.out = out;
-    a.part = rt->attn_part; a.counters = rt->attn_counters; a.pos_ptr = nullptr;
+    a.part = rt->attn_part; a.pos_ptr = nullptr;
     a.ts = ts; a.hs = hs;
     a.n_heads = nh; a.n_kv_heads = nkv; a.head_dim = hd; a.seq = seq;
     a.chunk = chunk; a.max_splits = splits;

@@ -21,7 +21,6 @@ struct Runtime {
     hipModule_t module = nullptr;
     std::unordered_map<std::string, hipFunction_t> fns;
     float *attn_part = nullptr;       // default split-K workspace of attn_decode
-    uint32_t *attn_counters = nullptr;
     size_t attn_part_floats = 0;
     float *gemm_part = nullptr;       // split-K partials of fp4_gemm (kGemmPartFloats)
     size_t max_lds = 65536;           // LDS bytes per workgroup

@@ -77,8 +77,7 @@ typedef struct AttnArgs {
     const float *q;       // [n_heads][head_dim]
     const void *kc, *vc;  // element (t, kvh, d) at t*ts + kvh*hs + d
     float *out;           // [n_heads][head_dim]
-    float *part;          // workspace: [n_heads][max_splits][head_dim + 2]
-    uint32_t *counters;   // workspace: [n_kv_heads], zero between calls
+    float *part;          // workspace: [n_heads][max_splits][head_dim + 4] = (m, l, -, -, acc)
     const int32_t *pos_ptr; // if non-null, seq = *pos_ptr + 1
     // Fused RoPE + fp16 KV append (null cosv = off): q is un-rotated, the
     // current token (position seq-1) has un-rotated k_new and v_new
