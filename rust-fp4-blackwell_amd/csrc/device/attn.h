@@ -78,83 +78,6 @@ RFP4_DEV float group_sum(float v)
     return v;
 }
 
-// Merge the nsplit partial states of the G heads of one KV head:
-//   M = max m_i, L = sum l_i e^(m_i - M), out = (sum acc_i e^(m_i - M)) / L,
-// computed online (running max) so that every load of a batch of splits is in
-// flight at once.  Thread tid owns the float4 outputs q and q + 128 of the
-// G*HD/4 (q = tid % 128) over the splits h, h + 2, h + 4, ... (h = tid / 128);
-// the two halves are combined through LDS.  scratch: >= 256 * 6 floats of LDS.
-#define ATTN_MERGE_BATCH 8
-template <int HD>
-RFP4_DEV void attn_merge(const AttnArgs &a, uint32_t kvh, uint32_t G, uint32_t nsplit, float *scratch, int tid,
-                         int lane, int wave)
-{
-    (void)lane;
-    (void)wave;
-    constexpr uint32_t STRIDE = HD + 4;
-    const uint32_t quads = G * HD / 4; // <= 256 (G <= 8, HD <= 128)
-    const uint32_t qd = (uint32_t)tid & 127u, h = (uint32_t)tid >> 7;
-    float M[2], L[2];
-    float4 o[2];
-#pragma unroll
-    for (int r = 0; r < 2; r++) {
-        M[r] = -3.402823466e38f;
-        L[r] = 0.0f;
-        o[r] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        const uint32_t q = qd + 128u * r;
-        if (q >= quads) continue;
-        const uint32_t g = q / (HD / 4), d4 = q % (HD / 4);
-        const float *hp = a.part + (size_t)(kvh * G + g) * a.max_splits * STRIDE;
-        for (uint32_t sp0 = h; sp0 < nsplit; sp0 += 2u * ATTN_MERGE_BATCH) {
-            float2 ml[ATTN_MERGE_BATCH];
-            float4 v[ATTN_MERGE_BATCH];
-#pragma unroll
-            for (int j = 0; j < ATTN_MERGE_BATCH; j++) {
-                const uint32_t sp = min(sp0 + 2u * j, nsplit - 1u);
-                ml[j] = *(const float2 *)(hp + (size_t)sp * STRIDE);
-                v[j] = *(const float4 *)(hp + (size_t)sp * STRIDE + 4 + d4 * 4);
-            }
-#pragma unroll
-            for (int j = 0; j < ATTN_MERGE_BATCH; j++) {
-                if (sp0 + 2u * j >= nsplit) break;
-                const float Mn = fmaxf(M[r], ml[j].x);
-                const float ea = expf(M[r] - Mn), eb = expf(ml[j].x - Mn);
-                L[r] = fmaf(L[r], ea, ml[j].y * eb);
-                o[r].x = fmaf(o[r].x, ea, v[j].x * eb);
-                o[r].y = fmaf(o[r].y, ea, v[j].y * eb);
-                o[r].z = fmaf(o[r].z, ea, v[j].z * eb);
-                o[r].w = fmaf(o[r].w, ea, v[j].w * eb);
-                M[r] = Mn;
-            }
-        }
-    }
-    if (h == 1u) {
-#pragma unroll
-        for (int r = 0; r < 2; r++) {
-            float *sh = scratch + (qd + 128u * r) * 6u;
-            sh[0] = M[r]; sh[1] = L[r]; sh[2] = o[r].x; sh[3] = o[r].y; sh[4] = o[r].z; sh[5] = o[r].w;
-        }
-    }
-    __syncthreads();
-    if (h == 0u) {
-#pragma unroll
-        for (int r = 0; r < 2; r++) {
-            const uint32_t q = qd + 128u * r;
-            if (q >= quads) continue;
-            const float *sh = scratch + q * 6u;
-            const float M1 = sh[0], L1 = sh[1];
-            const float Mn = fmaxf(M[r], M1), ea = expf(M[r] - Mn), eb = expf(M1 - Mn);
-            const float Lt = fmaf(L[r], ea, L1 * eb);
-            const uint32_t g = q / (HD / 4), d4 = q % (HD / 4);
-            float *dst = a.out + (size_t)(kvh * G + g) * HD + d4 * 4;
-            dst[0] = __fdiv_rn(fmaf(o[r].x, ea, sh[2] * eb), Lt);
-            dst[1] = __fdiv_rn(fmaf(o[r].y, ea, sh[3] * eb), Lt);
-            dst[2] = __fdiv_rn(fmaf(o[r].z, ea, sh[4] * eb), Lt);
-            dst[3] = __fdiv_rn(fmaf(o[r].w, ea, sh[5] * eb), Lt);
-        }
-    }
-}
-
 template <int HD, typename KT>
 RFP4_DEV void attn_body(const AttnArgs &a)
 {
@@ -391,20 +314,71 @@ RFP4_DEV void attn_body(const AttnArgs &a)
     }
 }
 
-// Merge kernel body: grid (n_kv_heads), launched after attn_body on the same
+// Merge kernel body: grid (n_heads), launched after attn_body on the same
 // stream (the kernel boundary orders the partial states before these reads).
 // Computes the split count exactly as attn_body did; one split means
-// attn_body already wrote the output.
+// attn_body already wrote the output.  For query head h:
+//   M = max m_i, L = sum l_i e^(m_i - M), out = (sum acc_i e^(m_i - M)) / L,
+// computed online (running max).  Thread tid owns float4 q = tid % (HD/4) of
+// the head and the splits p, p + P, p + 2P, ... (p = tid / (HD/4), P = 256 /
+// (HD/4)), every load of a batch in flight at once; the P partial states of a
+// float4 are then combined through LDS.
+#define ATTN_MERGE_BATCH 8
 template <int HD>
 RFP4_DEV void attn_merge_body(const AttnArgs &a)
 {
-    __shared__ float scratch[256 * 6];
+    constexpr uint32_t Q = HD / 4, P = 256 / Q, STRIDE = HD + 4;
+    __shared__ float sh[P][Q][6];
     uint32_t seq = a.pos_ptr ? (uint32_t)(*a.pos_ptr + 1) : a.seq;
     seq = min(seq, a.chunk * a.max_splits);
     const uint32_t nsplit = (seq + a.chunk - 1) / a.chunk;
     if (nsplit <= 1) return;
-    const int tid = threadIdx.x;
-    attn_merge<HD>(a, blockIdx.x, a.n_heads / a.n_kv_heads, nsplit, scratch, tid, tid & 63, tid >> 6);
+    const uint32_t h = blockIdx.x; // the partial state of head h sits at (h * max_splits + split) * STRIDE
+    const uint32_t q = threadIdx.x % Q, p = threadIdx.x / Q;
+    const float *hp = a.part + (size_t)h * a.max_splits * STRIDE;
+    float M = -3.402823466e38f, L = 0.0f;
+    float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (uint32_t sp0 = p; sp0 < nsplit; sp0 += P * ATTN_MERGE_BATCH) {
+        float2 ml[ATTN_MERGE_BATCH];
+        float4 v[ATTN_MERGE_BATCH];
+#pragma unroll
+        for (int j = 0; j < ATTN_MERGE_BATCH; j++) {
+            const uint32_t sp = min(sp0 + P * j, nsplit - 1u);
+            ml[j] = *(const float2 *)(hp + (size_t)sp * STRIDE);
+            v[j] = *(const float4 *)(hp + (size_t)sp * STRIDE + 4 + q * 4);
+        }
+#pragma unroll
+        for (int j = 0; j < ATTN_MERGE_BATCH; j++) {
+            if (sp0 + P * j >= nsplit) break;
+            const float Mn = fmaxf(M, ml[j].x);
+            const float ea = expf(M - Mn), eb = expf(ml[j].x - Mn);
+            L = fmaf(L, ea, ml[j].y * eb);
+            o.x = fmaf(o.x, ea, v[j].x * eb);
+            o.y = fmaf(o.y, ea, v[j].y * eb);
+            o.z = fmaf(o.z, ea, v[j].z * eb);
+            o.w = fmaf(o.w, ea, v[j].w * eb);
+            M = Mn;
+        }
+    }
+    float *me = sh[p][q];
+    me[0] = M; me[1] = L; me[2] = o.x; me[3] = o.y; me[4] = o.z; me[5] = o.w;
+    __syncthreads();
+    if (p != 0) return;
+    for (uint32_t r = 1; r < P; r++) {
+        const float *o2 = sh[r][q];
+        const float Mn = fmaxf(M, o2[0]), ea = expf(M - Mn), eb = expf(o2[0] - Mn);
+        L = fmaf(L, ea, o2[1] * eb);
+        o.x = fmaf(o.x, ea, o2[2] * eb);
+        o.y = fmaf(o.y, ea, o2[3] * eb);
+        o.z = fmaf(o.z, ea, o2[4] * eb);
+        o.w = fmaf(o.w, ea, o2[5] * eb);
+        M = Mn;
+    }
+    float *dst = a.out + (size_t)h * HD + q * 4;
+    dst[0] = __fdiv_rn(o.x, L);
+    dst[1] = __fdiv_rn(o.y, L);
+    dst[2] = __fdiv_rn(o.z, L);
+    dst[3] = __fdiv_rn(o.w, L);
 }
 
 // Tokens of one sub-chunk (the K/V rows attn_body holds in registers at once).

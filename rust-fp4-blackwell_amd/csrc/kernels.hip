@@ -41,8 +41,15 @@ GEMV_NS_FULL(e8m0, 0, argmax, RFP4_EPI_ARGMAX, 2)
 GEMV_NS_FULL(e8m0, 0, argmax, RFP4_EPI_ARGMAX, 4)
 GEMV_NS_SHORT(e8m0, 0, argmax, RFP4_EPI_ARGMAX, 8)
 GEMV_NS_FULL(e8m0, 0, swiglu, RFP4_EPI_SWIGLU, 2)
-GEMV_NS_SHORT(e8m0, 0, swiglu, RFP4_EPI_SWIGLU, 4)
-GEMV_KERNEL(e8m0, 0, swiglu, RFP4_EPI_SWIGLU, 4, 3)
+// gate/up at R=4: capped at 128 VGPRs (4 waves per SIMD) so that every
+// workgroup of the 8B shape (896) is resident at once
+#define GEMV_KERNEL_OCC4(SNAME, SF32, ENAME, EPI, R, NS) \
+    extern "C" __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) void \
+        rfp4_gemv_##SNAME##_##ENAME##_r##R##_s##NS(GemvArgs a) { gemv_body<SF32, EPI, R, NS>(a); }
+GEMV_KERNEL_OCC4(e8m0, 0, swiglu, RFP4_EPI_SWIGLU, 4, 0)
+GEMV_KERNEL_OCC4(e8m0, 0, swiglu, RFP4_EPI_SWIGLU, 4, 1)
+GEMV_KERNEL_OCC4(e8m0, 0, swiglu, RFP4_EPI_SWIGLU, 4, 2)
+GEMV_KERNEL(e8m0, 0, swiglu, RFP4_EPI_SWIGLU, 4, 3) // 128 VGPRs would spill
 GEMV_NS_FULL(f32, 1, store, RFP4_EPI_STORE, 4)
 
 // ---- MFMA GEMV: rfp4_gemvm_<epilogue>_t<RT>_s<NSC>
