@@ -10,6 +10,7 @@
 #include "device/misc.h"
 #include "device/mma.h"
 #include "device/gemm.h"
+#include "device/gemm_skinny.h"
 
 #define K256 extern "C" __global__ __launch_bounds__(256)
 #define K1024 extern "C" __global__ __launch_bounds__(1024)
@@ -123,3 +124,12 @@ GEMM_KERNEL(128, 128, 2, 2, 2, 2)
 GEMM_KERNEL(256, 128, 2, 2, 4, 2)
 GEMM_KERNEL(256, 256, 2, 2, 4, 4)
 K256 void rfp4_gemm_reduce(GemmArgs a) { gemm_reduce_body(a); }
+// few activation rows (M <= 16, 32, 64) x 16 or 32 W rows per workgroup
+#define GEMM_SKINNY_KERNEL(M, MA, NB) \
+    K256 void rfp4_gemm_skinny_m##M##_n##NB(GemmArgs a) { gemm_skinny_body<MA, NB>(a); }
+GEMM_SKINNY_KERNEL(16, 1, 1)
+GEMM_SKINNY_KERNEL(16, 1, 2)
+GEMM_SKINNY_KERNEL(32, 2, 1)
+GEMM_SKINNY_KERNEL(32, 2, 2)
+GEMM_SKINNY_KERNEL(64, 4, 1)
+GEMM_SKINNY_KERNEL(64, 4, 2)

@@ -634,12 +634,26 @@ constexpr GemmTile kGemmTiles[] = {
     {64, 128, "rfp4_gemm_64x128"},   {32, 128, "rfp4_gemm_32x128"},
 };
 constexpr int kGemmNumTiles = (int)(sizeof(kGemmTiles) / sizeof(kGemmTiles[0]));
+// plan index of the few-row kernel (gemm_skinny.h): 16 * MA activation rows, 16 * NB W rows per workgroup
+constexpr int kGemmSkinny = kGemmNumTiles;
 thread_local int t_gemm_tile = -1, t_gemm_kz = 0;
 
 struct GemmPlan {
     int tile;
     uint32_t kz;
+    int ma = 0, nb = 0; // skinny plan only
 };
+
+bool gemm_skinny_ok(uint32_t m, uint32_t k) { return m <= 64u && k % 2048u == 0u; }
+// Measured on MI355X at m = 32: the few-row kernel wins while W is small
+// (4096x4096: 6.2 vs 9.0 us for the tiled kernel with its split-K reduce);
+// on larger W its 16-row workgroups re-read A at twice the W bytes and the
+// tiled kernel, which shares A through LDS across 128 W rows, is faster
+// (14336x4096: 11.9 vs 17.1 us).
+bool gemm_skinny_pays(uint32_t m, uint32_t n, uint32_t k)
+{
+    return gemm_skinny_ok(m, k) && (uint64_t)n * k <= (1ull << 25);
+}
 
 uint32_t ceil_div(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
 
@@ -649,6 +663,15 @@ uint32_t ceil_div(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); 
 GemmPlan gemm_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t num_cus)
 {
     const uint32_t nsuper = k / 256u;
+    if (t_gemm_tile == kGemmSkinny || (t_gemm_tile < 0 && gemm_skinny_pays(m, n, k))) {
+        // few activation rows: stream W like a GEMV; two W fragments per
+        // workgroup (half the activation re-reads) once that still leaves
+        // two workgroups per CU
+        GemmPlan p{kGemmSkinny, 1u};
+        p.ma = m <= 16u ? 1 : (m <= 32u ? 2 : 4);
+        p.nb = (uint64_t)n >= 64ull * num_cus ? 2 : 1;
+        return p;
+    }
     int pick = t_gemm_tile;
     for (int i = 0; pick < 0 && i < kGemmNumTiles; i++) {
         const GemmTile &t = kGemmTiles[i];
@@ -683,6 +706,14 @@ int fp4_gemm(rfp4_stream_t stream, uint32_t m, uint32_t n, uint32_t k, const uin
     Runtime *rt = g_rt;
     if (!rt) return set_error(RFP4_E_NOT_INIT, "rfp4_init has not been called");
     GemmPlan p = gemm_plan(m, n, k, (uint32_t)rt->num_cus);
+    if (p.tile == kGemmSkinny) {
+        if (!gemm_skinny_ok(m, k))
+            return set_error(RFP4_E_SHAPE, "fp4_gemm: the few-row kernel needs m <= 64 and k %% 2048 == 0 (m=%u k=%u)", m, k);
+        char name[48];
+        snprintf(name, sizeof name, "rfp4_gemm_skinny_m%d_n%d", 16 * p.ma, p.nb);
+        GemmArgs a{a_codes, a_scales, w_codes, w_scales, c, nullptr, m, n, k, 1u};
+        return launch(name, dim3(ceil_div(n, 16u * (uint32_t)p.nb)), dim3(256), (hipStream_t)stream, &a);
+    }
     const GemmTile &t = kGemmTiles[p.tile];
     const uint64_t tiles = (uint64_t)ceil_div(m, t.bm) * ceil_div(n, t.bn);
     if (p.kz > 1 && (uint64_t)p.kz * m * n > kGemmPartFloats)
@@ -704,7 +735,7 @@ int rfp4_debug_attn_chunk(uint32_t chunk)
 
 int rfp4_debug_gemm_plan(int tile, int kz)
 {
-    if (tile < -1 || tile >= kGemmNumTiles) return set_error(RFP4_E_INVALID, "tile must be -1 (auto) or 0..%d", kGemmNumTiles - 1);
+    if (tile < -1 || tile > kGemmSkinny) return set_error(RFP4_E_INVALID, "tile must be -1 (auto) or 0..%d", kGemmSkinny);
     if (kz < 0) return set_error(RFP4_E_INVALID, "kz must be 0 (auto) or positive");
     t_gemm_tile = tile;
     t_gemm_kz = kz;
@@ -717,8 +748,8 @@ int rfp4_gemm_plan(uint32_t m, uint32_t n, uint32_t k, int *tile_m, int *tile_n,
     const uint32_t cus = rt ? (uint32_t)rt->num_cus : 256u;
     if (k == 0 || k % 256u || m == 0 || n == 0) return set_error(RFP4_E_SHAPE, "gemm_plan: bad shape");
     GemmPlan p = gemm_plan(m, n, k, cus);
-    if (tile_m) *tile_m = (int)kGemmTiles[p.tile].bm;
-    if (tile_n) *tile_n = (int)kGemmTiles[p.tile].bn;
+    if (tile_m) *tile_m = p.tile == kGemmSkinny ? 16 * p.ma : (int)kGemmTiles[p.tile].bm;
+    if (tile_n) *tile_n = p.tile == kGemmSkinny ? 16 * p.nb : (int)kGemmTiles[p.tile].bn;
     if (kz) *kz = (int)p.kz;
     return RFP4_OK;
 }

@@ -2,10 +2,11 @@
 float64 contraction C = sum_k A SFA W SFW (trackb/fp4_scale_test.cu:37 taken
 to M x N x K; the reference has only the m16n8k64 tile, fp4_mma/src/main.rs).
 
-Bar (fp32 accumulate): |c - c64| <= 1e-5 * sum_k |a_k w_k| on every element,
-no element past the reference's 1e-2 gate, and >= 99.9% of elements within
-1e-3 relative of the exact sum (elements with heavy cancellation may exceed
-it, as for the GEMV).  Config-5 shapes too large for the CPU oracle are
+Bar (fp32 accumulate): |c - c64| <= 1e-5 * sum_k |a_k w_k| on every element;
+the reference's 1e-2 gate on every element whose exact value is not
+cancellation-dominated (|c64| >= 1e-3 * sum_k |a_k w_k|: below that, the
+normwise bound itself allows more than 1e-2 relative for any fp32 order);
+and >= 99.9% of elements within 1e-3 relative of the exact sum.  Config-5 shapes too large for the CPU oracle are
 checked on sampled rows and columns: C[i][j] depends only on row i of A and
 row j of W, so a sub-GEMM of the sampled rows is an exact restatement."""
 import numpy as np
@@ -43,7 +44,8 @@ def _assert_gemm_close(c, c64, absc):
     cond = np.abs(c - c64) / np.maximum(absc, 1e-300)
     assert cond.max() < 1e-5, f"max |c-c64|/sum|aw| = {cond.max():.3e}"
     rel = reference_rel_err(c, c64)
-    assert (rel > 1e-2).sum() == 0, f"{(rel > 1e-2).sum()} elements past 1e-2, max {rel.max():.3e}"
+    well = np.abs(c64) >= 1e-3 * absc
+    assert (rel[well] > 1e-2).sum() == 0, f"{(rel[well] > 1e-2).sum()} elements past 1e-2, max {rel[well].max():.3e}"
     assert np.mean(rel <= 1e-3) >= 0.999, f"{(rel > 1e-3).sum()} elements over 1e-3 (max {rel.max():.3e})"
 
 
@@ -75,6 +77,37 @@ def test_gemm_every_tile_and_split(rf, orc, stream, forced_plan, tile, kz):
     _assert_gemm_close(c, c64, absc)
     c2 = _gemm(rf, stream, m, n, k, ac, asc, wc, wsc)
     np.testing.assert_array_equal(c.view(np.uint32), c2.view(np.uint32))  # deterministic
+
+
+@pytest.mark.parametrize("m", [1, 7, 16, 17, 32, 33, 64])
+@pytest.mark.parametrize("n,k", [(4, 2048), (292, 2048), (1040, 6144)])
+def test_gemm_few_rows_kernel(rf, orc, stream, forced_plan, m, n, k):
+    """The few-row kernel (m <= 64, k % 2048 == 0: 16/32/64-row activation
+    fragments, 16 or 32 W rows per workgroup, K in wave quarters) on ragged
+    m and n, forced and automatic, against the oracle."""
+    ac, asc = _uniform_mx(orc, m, k, 61 + m)
+    wc, wsc = _uniform_mx(orc, n, k, 71 + n)
+    c64, absc = orc.gemm_mx_f64(m, n, k, ac, asc, wc, wsc)
+    for plan in ((5, 0), (-1, 0)):   # forced, and automatic (these shapes are small enough)
+        forced_plan(*plan)
+        tm, tn, kz = rf.gemm_plan(m, n, k)
+        assert tm == (16 if m <= 16 else 32 if m <= 32 else 64) and kz == 1
+        c = _gemm(rf, stream, m, n, k, ac, asc, wc, wsc)
+        _assert_gemm_close(c, c64, absc)
+
+
+def test_gemm_few_rows_two_w_fragments(rf, orc, stream, forced_plan):
+    """Wide N takes 32 W rows per workgroup; a ragged last workgroup."""
+    m, n, k = 32, 16400, 2048
+    ac, asc = _uniform_mx(orc, m, k, 81)
+    wc, wsc = _uniform_mx(orc, n, k, 82)
+    forced_plan(5, 0)
+    assert rf.gemm_plan(m, n, k) == (32, 32, 1)
+    c = _gemm(rf, stream, m, n, k, ac, asc, wc, wsc)
+    cols = np.unique(np.concatenate([np.arange(48), n - 48 + np.arange(48),
+                                     np.random.default_rng(1).choice(n, 400, replace=False)]))
+    c64, absc = orc.gemm_mx_f64(m, len(cols), k, ac, asc, wc.reshape(n, -1)[cols], wsc.reshape(n, -1)[cols])
+    _assert_gemm_close(c[:, cols], c64, absc)
 
 
 def test_gemm_row_permutation_is_exact(rf, orc, stream, forced_plan):
