@@ -219,6 +219,32 @@ def decode_run(rf, preset, max_seq, prefill, prompt, warmup, steps):
     return eng, cfg, ms, wall, ids
 
 
+def prefill_run(rf, eng, cfg, n=512, reps=3):
+    """Batched prefill of n random tokens at position 0 through the MXFP4 GEMM
+    (llama_engine_prefill): every projection an M=n GEMM, causal attention
+    rows, then the last row's LM head.  GPU time from stream events."""
+    prompt = np.random.default_rng(512).integers(0, cfg.vocab, n).astype(np.uint32)
+    tok = eng.prefill(prompt, 0)  # warm: workspace allocation, code objects
+    e0, e1 = rf.Event(), rf.Event()
+    best = None
+    for _ in range(reps):
+        e0.record(eng.stream)
+        t = eng.prefill(prompt, 0)
+        e1.record(eng.stream)
+        e1.synchronize()
+        ms = e0.elapsed_ms(e1)
+        best = ms if best is None else min(best, ms)
+        assert t == tok
+    qd, kvd = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
+    per_layer = (qd + 2 * kvd) * cfg.dim + cfg.dim * qd + 2 * cfg.ffn * cfg.dim + cfg.dim * cfg.ffn
+    flops = 2.0 * n * per_layer * cfg.n_layers
+    return {"tokens": n, "ms": round(best, 3), "tok_s": round(n / (best / 1e3), 1),
+            "projection_TFLOP": round(flops / 1e12, 3), "TFLOP_s": round(flops / (best / 1e3) / 1e12, 1),
+            "frac_fp4_peak": round(flops / (best / 1e3) / 1e12 / FP4_PEAK_TFLOPS, 4),
+            "workload": f"Llama-3-8B arch, {n} random tokens at position 0 through llama_engine_prefill "
+                        "(MXFP4 activations per 32), best of %d" % reps}
+
+
 def cpu_baseline(threads, steps=2):
     """The oracle decode loop (oracle/, C, f32, k-order) on the host cores:
     config-4 model, context pre-filled to 4096, `steps` decode steps timed."""
@@ -250,6 +276,7 @@ def main():
     ap.add_argument("--cpu-steps", type=int, default=2)
     ap.add_argument("--no-tiny", action="store_true", help="skip the TinyLlama-1.1B line")
     ap.add_argument("--no-gemm", action="store_true", help="skip the config-5 batched GEMM figures")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the batched prefill figure")
     ap.add_argument("--pmc-probe", action="store_true", help="only the launch sequence of the counter runs")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -279,6 +306,9 @@ def main():
     log(f"GEMV path: {path_bytes / 1e9:.3f} GB in {path_ms * 1e3:.1f} us -> {path_gbs:.0f} GB/s; "
         f"gate/up GEMV {gate_ms * 1e3:.2f} us -> {gate_gbs:.0f} GB/s")
     gemm = None if args.no_gemm else gemm_config5(rf, eng, cfg)
+    prefill = None if args.no_prefill else prefill_run(rf, eng, cfg)
+    if prefill:
+        log(f"prefill 512: {prefill['ms']} ms, {prefill['tok_s']} tok/s, {prefill['TFLOP_s']} TFLOP/s")
     eng.close()
 
     tiny = None
@@ -338,6 +368,7 @@ def main():
         },
         "tinyllama": tiny,
         "gemm_config5": gemm,
+        "prefill": prefill,
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

@@ -223,6 +223,15 @@ int llama_engine_destroy(llama_engine *e);
 int llama_engine_prefill_kv(llama_engine *e, uint64_t seed, uint32_t upto);
 /* forward(tok, pos) -> argmax, blocking: llama_run/src/main.rs:492-536 */
 int llama_decode_step(llama_engine *e, uint32_t tok, uint32_t pos, uint32_t *next);
+/* Batched prefill (no reference counterpart; the reference feeds the prompt
+ * token by token, llama_run/src/main.rs:550-556): prompt[0..n) at positions
+ * pos0.. through the MXFP4 GEMM, every projection input quantised to MXFP4
+ * per 32 along K (OCP rules).  Writes those positions' K/V and returns in
+ * *next_token the greedy token after the last one; decoding continues with
+ * llama_decode_step / llama_generate from position pos0 + n.  Blocking.
+ * Needs dim, n_heads*head_dim and ffn to be multiples of 256. */
+int llama_engine_prefill(llama_engine *e, const uint32_t *prompt, uint32_t n_prompt, uint32_t pos0,
+                         uint32_t *next_token);
 /* Prompt-then-greedy loop without the EOS stop (llama_run/src/main.rs:544-570):
  * feeds prompt[0..n_prompt) from position pos0, generates n_new tokens into
  * out.  The whole loop runs on the device (one graph replay per token, token

@@ -892,6 +892,90 @@ uint32_t orc_model_step(orc_model *m, uint32_t tok, uint32_t pos, float *logits)
     return orc_argmax(c->vocab, m->logits);
 }
 
+/* Batched prefill with MXFP4 activations (the "next" path of the decode
+ * engine: the prompt through the MXFP4 GEMM instead of token by token,
+ * llama_run/src/main.rs:550-556).  Per layer, every projection input row is
+ * RMS-normalised (or taken as is for o and down), quantised with the OCP MX
+ * rules (orc_quant_mx), multiplied by the MXFP4 weights exactly in f64
+ * (orc_gemm_mx_f64, trackb/fp4_scale_test.cu:37) and rounded to f32; RoPE, the
+ * fp16 KV append, attention (causal: row i sees positions < pos0 + i + 1),
+ * SwiGLU and the residual adds are the decode step's own
+ * (llama_run/src/main.rs:513-530).  The last row's logits come from the f32
+ * LM-head GEMV, as in a decode step.  Returns the argmax, writes the logits
+ * if asked. */
+static void gemm_rows_f32(uint32_t M, uint32_t N, uint32_t K, const uint8_t *ac, const uint8_t *as,
+                          const uint8_t *wc, const uint8_t *ws, float *out)
+{
+    double *c = (double *)malloc(sizeof(double) * (size_t)M * N);
+    double *absc = (double *)malloc(sizeof(double) * (size_t)M * N);
+    orc_gemm_mx_f64(M, N, K, ac, as, wc, ws, c, absc);
+    for (size_t i = 0; i < (size_t)M * N; i++) out[i] = (float)c[i];
+    free(c);
+    free(absc);
+}
+
+uint32_t orc_model_prefill(orc_model *m, const uint32_t *prompt, uint32_t n, uint32_t pos0, float *logits)
+{
+    const orc_model_config *c = &m->c;
+    const uint32_t half = c->head_dim / 2, hd = c->head_dim;
+    const uint32_t qd = c->n_heads * hd, kvd = c->n_kv_heads * hd;
+    if (n == 0 || pos0 + n > c->max_seq) return 0xFFFFFFFFu;
+    for (uint32_t i = 0; i < n; i++)
+        if (prompt[i] >= c->vocab) return 0xFFFFFFFFu;
+    const uint32_t kmax = c->dim > c->ffn ? (c->dim > qd ? c->dim : qd) : (c->ffn > qd ? c->ffn : qd);
+    float *X = (float *)malloc(sizeof(float) * (size_t)n * c->dim);
+    float *H = (float *)malloc(sizeof(float) * (size_t)n * kmax);
+    uint8_t *hc = (uint8_t *)malloc((size_t)n * kmax / 2), *hs = (uint8_t *)malloc((size_t)n * kmax / 32);
+    float *Q = (float *)malloc(sizeof(float) * (size_t)n * qd);
+    float *Kr = (float *)malloc(sizeof(float) * (size_t)n * kvd), *Vr = (float *)malloc(sizeof(float) * (size_t)n * kvd);
+    float *A = (float *)malloc(sizeof(float) * (size_t)n * qd);
+    float *O = (float *)malloc(sizeof(float) * (size_t)n * c->dim);
+    float *G = (float *)malloc(sizeof(float) * (size_t)n * c->ffn), *U = (float *)malloc(sizeof(float) * (size_t)n * c->ffn);
+    for (uint32_t i = 0; i < n; i++) widen_f16(m->embed + (size_t)prompt[i] * c->dim, c->dim, X + (size_t)i * c->dim);
+    for (uint32_t l = 0; l < c->n_layers; l++) {
+        widen_f16(m->norm_attn[l], c->dim, m->tmpw);
+        for (uint32_t i = 0; i < n; i++) orc_rmsnorm(c->dim, c->eps, X + (size_t)i * c->dim, m->tmpw, H + (size_t)i * c->dim);
+        orc_quant_mx(H, n, c->dim, hc, hs);
+        gemm_rows_f32(n, qd, c->dim, hc, hs, m->codes[l][ORC_WQ], m->scales[l][ORC_WQ], Q);
+        gemm_rows_f32(n, kvd, c->dim, hc, hs, m->codes[l][ORC_WK], m->scales[l][ORC_WK], Kr);
+        gemm_rows_f32(n, kvd, c->dim, hc, hs, m->codes[l][ORC_WV], m->scales[l][ORC_WV], Vr);
+        for (uint32_t i = 0; i < n; i++) {
+            const uint32_t pos = pos0 + i;
+            const float *cp = m->cosv + (size_t)pos * half, *sp = m->sinv + (size_t)pos * half;
+            orc_rope(c->n_heads, hd, cp, sp, Q + (size_t)i * qd);
+            orc_rope(c->n_kv_heads, hd, cp, sp, Kr + (size_t)i * kvd);
+            for (uint32_t kvh = 0; kvh < c->n_kv_heads; kvh++)
+                for (uint32_t d = 0; d < hd; d++) {
+                    size_t at = ((size_t)kvh * c->max_seq + pos) * hd + d;
+                    m->kc[l][at] = orc_f32_to_f16(Kr[(size_t)i * kvd + kvh * hd + d]);
+                    m->vc[l][at] = orc_f32_to_f16(Vr[(size_t)i * kvd + kvh * hd + d]);
+                }
+        }
+        for (uint32_t i = 0; i < n; i++)
+            orc_attn_decode_f16(c->n_heads, c->n_kv_heads, hd, pos0 + i + 1, Q + (size_t)i * qd, m->kc[l], m->vc[l], hd,
+                                (size_t)c->max_seq * hd, A + (size_t)i * qd);
+        orc_quant_mx(A, n, qd, hc, hs);
+        gemm_rows_f32(n, c->dim, qd, hc, hs, m->codes[l][ORC_WO], m->scales[l][ORC_WO], O);
+        orc_residual(n * c->dim, O, X);
+        widen_f16(m->norm_ffn[l], c->dim, m->tmpw);
+        for (uint32_t i = 0; i < n; i++) orc_rmsnorm(c->dim, c->eps, X + (size_t)i * c->dim, m->tmpw, H + (size_t)i * c->dim);
+        orc_quant_mx(H, n, c->dim, hc, hs);
+        gemm_rows_f32(n, c->ffn, c->dim, hc, hs, m->codes[l][ORC_WG], m->scales[l][ORC_WG], G);
+        gemm_rows_f32(n, c->ffn, c->dim, hc, hs, m->codes[l][ORC_WU], m->scales[l][ORC_WU], U);
+        orc_swiglu(n * c->ffn, G, U, H);
+        orc_quant_mx(H, n, c->ffn, hc, hs);
+        gemm_rows_f32(n, c->dim, c->ffn, hc, hs, m->codes[l][ORC_WD], m->scales[l][ORC_WD], O);
+        orc_residual(n * c->dim, O, X);
+    }
+    memcpy(m->x, X + (size_t)(n - 1) * c->dim, sizeof(float) * c->dim);
+    widen_f16(m->norm_final, c->dim, m->tmpw);
+    orc_rmsnorm(c->dim, c->eps, m->x, m->tmpw, m->h);
+    orc_gemv_e8m0(c->vocab, c->dim, m->lm_codes, m->lm_scales, m->h, m->logits);
+    if (logits) memcpy(logits, m->logits, sizeof(float) * c->vocab);
+    free(X); free(H); free(hc); free(hs); free(Q); free(Kr); free(Vr); free(A); free(O); free(G); free(U);
+    return orc_argmax(c->vocab, m->logits);
+}
+
 static float top2_margin(const float *v, uint32_t n)
 {
     float b1 = -INFINITY, b2 = -INFINITY;

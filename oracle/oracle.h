@@ -163,6 +163,13 @@ uint32_t orc_model_step(orc_model *m, uint32_t tok, uint32_t pos, float *logits)
  * first prompt token); margins[i] = top1 - top2 logit at that step (optional). */
 void orc_model_generate(orc_model *m, const uint32_t *prompt, uint32_t n_prompt, uint32_t pos0,
                         uint32_t n_new, uint32_t *out, float *margins);
+/* Batched prefill of prompt[0..n) at positions pos0.. with MXFP4 activations
+ * (every projection input quantised per 32 along K with the OCP rules, the
+ * GEMM exact in f64 then rounded to f32); writes the K/V caches of those
+ * positions; returns the argmax of the last row's logits (written to
+ * `logits` if non-null).  No reference counterpart: the reference feeds the
+ * prompt token by token (llama_run/src/main.rs:550-556). */
+uint32_t orc_model_prefill(orc_model *m, const uint32_t *prompt, uint32_t n, uint32_t pos0, float *logits);
 
 #ifdef __cplusplus
 }

@@ -73,6 +73,7 @@ _SIGS = {
     "orc_model_prefill_kv": (None, [P, U64, U32]),
     "orc_model_step": (U32, [P, U32, U32, P]),
     "orc_model_generate": (None, [P, P, U32, U32, U32, P, P]),
+    "orc_model_prefill": (U32, [P, P, U32, U32, P]),
 }
 
 _lib = None
@@ -304,6 +305,13 @@ class Model:
         margins = np.empty(n_new, dtype=np.float32)
         lib().orc_model_generate(self.h, ptr(pr), len(pr), pos0, n_new, ptr(out), ptr(margins))
         return out, margins
+
+    def prefill(self, prompt, pos0, want_logits=False):
+        """Batched prefill with MXFP4 activations; returns the next token (and logits)."""
+        pr = np.ascontiguousarray(prompt, dtype=np.uint32)
+        logits = np.empty(self.cfg["vocab"], dtype=np.float32) if want_logits else None
+        t = lib().orc_model_prefill(self.h, ptr(pr), len(pr), pos0, ptr(logits) if want_logits else None)
+        return (t, logits) if want_logits else t
 
     def close(self):
         if self.h:

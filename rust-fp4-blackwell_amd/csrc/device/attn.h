@@ -93,11 +93,14 @@ RFP4_DEV void attn_body(const AttnArgs &a)
     __shared__ float s_m[ATTN_MAX_GROUP], s_l[ATTN_MAX_GROUP], s_alpha[ATTN_MAX_GROUP];
     __shared__ uint16_t knew[HD], vnew[HD];
 
-    const uint32_t kvh = blockIdx.x, split = blockIdx.y;
+    const uint32_t kvh = blockIdx.x, split = blockIdx.y, row = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = tid % LPT, slot = tid / LPT;
     const uint32_t chunk = a.chunk;
-    uint32_t seq = a.pos_ptr ? (uint32_t)(*a.pos_ptr + 1) : a.seq;
+    uint32_t seq = (a.pos_ptr ? (uint32_t)(*a.pos_ptr + 1) : a.seq) + row;
+    const float *qrow = a.q + (size_t)row * a.q_rs;
+    float *orow = a.out + (size_t)row * a.out_rs;
+    float *prow = a.part + (size_t)row * a.n_heads * a.max_splits * (HD + 4);
     seq = min(seq, chunk * a.max_splits); // never read past the planned splits
     const uint32_t nsplit = (seq + chunk - 1) / chunk;
     if (split >= nsplit) return;
@@ -125,7 +128,7 @@ RFP4_DEV void attn_body(const AttnArgs &a)
     RFP4_ATTN_LOAD(vr, vc, 0u);
 
     // ---- q (rotated if fused) into LDS; the owner split appends k, v
-    const float *qg = a.q + (size_t)(kvh * G) * HD;
+    const float *qg = qrow + (size_t)(kvh * G) * HD;
     if (fused) {
         const uint32_t half = HD / 2;
         const float *cp = a.cosv + (size_t)pos * half, *sp = a.sinv + (size_t)pos * half;
@@ -294,7 +297,7 @@ RFP4_DEV void attn_body(const AttnArgs &a)
         for (uint32_t i = tid; i < G * HD; i += blockDim.x) {
             const uint32_t g = i / HD, d = i % HD;
             const float v = vred[0][g][d] + vred[1][g][d] + vred[2][g][d] + vred[3][g][d];
-            a.out[(size_t)(kvh * G + g) * HD + d] = __fdiv_rn(v, s_l[g]);
+            orow[(size_t)(kvh * G + g) * HD + d] = __fdiv_rn(v, s_l[g]);
         }
         return;
     }
@@ -306,10 +309,10 @@ RFP4_DEV void attn_body(const AttnArgs &a)
         uint32_t g = i / HD, d = i % HD;
         float v = vred[0][g][d] + vred[1][g][d] + vred[2][g][d] + vred[3][g][d];
         size_t base = ((size_t)(kvh * G + g) * a.max_splits + split) * stride;
-        a.part[base + 4 + d] = v;
+        prow[base + 4 + d] = v;
         if (d == 0) {
-            a.part[base] = s_m[g];
-            a.part[base + 1] = s_l[g];
+            prow[base] = s_m[g];
+            prow[base + 1] = s_l[g];
         }
     }
 }
@@ -329,13 +332,14 @@ RFP4_DEV void attn_merge_body(const AttnArgs &a)
 {
     constexpr uint32_t Q = HD / 4, P = 256 / Q, STRIDE = HD + 4;
     __shared__ float sh[P][Q][6];
-    uint32_t seq = a.pos_ptr ? (uint32_t)(*a.pos_ptr + 1) : a.seq;
+    const uint32_t row = blockIdx.z;
+    uint32_t seq = (a.pos_ptr ? (uint32_t)(*a.pos_ptr + 1) : a.seq) + row;
     seq = min(seq, a.chunk * a.max_splits);
     const uint32_t nsplit = (seq + a.chunk - 1) / a.chunk;
     if (nsplit <= 1) return;
     const uint32_t h = blockIdx.x; // the partial state of head h sits at (h * max_splits + split) * STRIDE
     const uint32_t q = threadIdx.x % Q, p = threadIdx.x / Q;
-    const float *hp = a.part + (size_t)h * a.max_splits * STRIDE;
+    const float *hp = a.part + (size_t)row * a.n_heads * a.max_splits * STRIDE + (size_t)h * a.max_splits * STRIDE;
     float M = -3.402823466e38f, L = 0.0f;
     float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (uint32_t sp0 = p; sp0 < nsplit; sp0 += P * ATTN_MERGE_BATCH) {
@@ -374,7 +378,7 @@ RFP4_DEV void attn_merge_body(const AttnArgs &a)
         o.w = fmaf(o.w, ea, o2[5] * eb);
         M = Mn;
     }
-    float *dst = a.out + (size_t)h * HD + q * 4;
+    float *dst = a.out + (size_t)row * a.out_rs + (size_t)h * HD + q * 4;
     dst[0] = __fdiv_rn(o.x, L);
     dst[1] = __fdiv_rn(o.y, L);
     dst[2] = __fdiv_rn(o.z, L);

@@ -1,0 +1,85 @@
+// Row kernels of the batched prefill (several prompt positions per launch;
+// the projections themselves run on the MXFP4 GEMM).  Each restates, per
+// row, a piece the decode step already has (embedding lookup, RMSNorm, RoPE,
+// fp16 KV append, SwiGLU) and feeds the GEMM's MXFP4 activations with the
+// OCP quantizer of the weights (quant_block32).
+#pragma once
+#include "common.h"
+#include "gemv.h"
+#include "misc.h"
+#include "norm_rope.h"
+
+// grid (rows): y[r] = widen(embed[ids[r]])  (llama_run/src/main.rs:509-510)
+RFP4_DEV void embed_rows_body(const RowsArgs &a)
+{
+    const uint32_t r = blockIdx.x;
+    uint32_t tok = a.ids[r];
+    if (tok >= a.vocab) tok = 0;
+    const uint16_t *row = a.embed + (size_t)tok * a.k;
+    for (uint32_t i = threadIdx.x; i < a.k; i += blockDim.x) a.y[(size_t)r * a.k + i] = f16_bits_to_f32(row[i]);
+}
+
+// grid (rows), dynamic LDS k floats: RMSNorm of row r with fp16 weights, in
+// the order of rmsnorm_body ((x * rms) * w, llama_run/src/main.rs:79-116),
+// then OCP MX quantisation per 32 values.
+RFP4_DEV void rmsnorm_quant_rows_body(const RowsArgs &a)
+{
+    extern __shared__ float yrow[];
+    __shared__ float red[16];
+    const uint32_t r = blockIdx.x;
+    const float *x = a.x + (size_t)r * a.k;
+    float ss = 0.0f;
+    for (uint32_t i = threadIdx.x; i < a.k; i += blockDim.x) ss = __fadd_rn(ss, __fmul_rn(x[i], x[i]));
+    const float total = block_sum(ss, red);
+    const float rms = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(total, (float)a.k), a.eps)));
+    for (uint32_t i = threadIdx.x; i < a.k; i += blockDim.x)
+        yrow[i] = __fmul_rn(__fmul_rn(x[i], rms), f16_bits_to_f32(a.w[i]));
+    __syncthreads();
+    const uint32_t nb = a.k / 32u;
+    for (uint32_t b = threadIdx.x; b < nb; b += blockDim.x) {
+        float v[32];
+#pragma unroll
+        for (int i = 0; i < 32; i++) v[i] = yrow[b * 32u + (uint32_t)i];
+        a.scales[(size_t)r * nb + b] = (uint8_t)quant_block32(v, a.codes + ((size_t)r * a.k + b * 32u) / 2);
+    }
+}
+
+// grid (rows): s = silu(gate) * up (llama_run/src/main.rs:244-252) of row r
+// (gate = columns [0, k), up = [k, 2k) of the stacked gate|up output), then
+// OCP MX quantisation per 32 values.
+RFP4_DEV void swiglu_quant_rows_body(const RowsArgs &a)
+{
+    const uint32_t r = blockIdx.x, nb = a.k / 32u;
+    const float *g = a.x + (size_t)r * 2u * a.k, *u = g + a.k;
+    for (uint32_t b = threadIdx.x; b < nb; b += blockDim.x) {
+        float v[32];
+#pragma unroll
+        for (int i = 0; i < 32; i++) {
+            const uint32_t j = b * 32u + (uint32_t)i;
+            v[i] = __fmul_rn(silu_ref(g[j]), u[j]);
+        }
+        a.scales[(size_t)r * nb + b] = (uint8_t)quant_block32(v, a.codes + ((size_t)r * a.k + b * 32u) / 2);
+    }
+}
+
+// grid (rows): RoPE of row r's q and k heads in place at position pos0 + r
+// (llama_run/src/main.rs:517-518), then fp16 k (rotated) and v into the
+// caches at that position (:519-521).
+RFP4_DEV void rope_kv_rows_body(const RopeRowsArgs &a)
+{
+    const uint32_t r = blockIdx.x, pos = a.pos0 + r, half = a.head_dim / 2u;
+    float *row = a.qkv + (size_t)r * a.row_stride;
+    const float *cp = a.cosv + (size_t)pos * half, *sp = a.sinv + (size_t)pos * half;
+    const uint32_t qd = a.n_heads * a.head_dim, kvd = a.n_kv_heads * a.head_dim;
+    for (uint32_t i = threadIdx.x; i < (a.n_heads + a.n_kv_heads) * half; i += blockDim.x) {
+        const uint32_t hh = i / half, j = i % half;
+        rope_pair(row + hh * a.head_dim, j, half, cp[j], sp[j]); // k heads follow the q heads
+    }
+    __syncthreads();
+    for (uint32_t i = threadIdx.x; i < kvd; i += blockDim.x) {
+        const uint32_t kvh = i / a.head_dim, d = i % a.head_dim;
+        const size_t at = (size_t)pos * a.ts + (size_t)kvh * a.hs + d;
+        a.kc[at] = f32_to_f16_bits(row[qd + i]);
+        a.vc[at] = f32_to_f16_bits(row[qd + kvd + i]);
+    }
+}

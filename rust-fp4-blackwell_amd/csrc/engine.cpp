@@ -14,6 +14,7 @@
 //  - a device cursor (position, step) and the token array ids[]; the LM-head
 //    GEMV reduces its argmax per workgroup and the step kernel writes the next
 //    token into ids[], so consecutive steps need no host round trip.
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -59,6 +60,11 @@ struct llama_engine {
     // host mirror of the cursor, for bounds checks
     int64_t h_pos = 0, h_step = 0, h_ids_cap = 0;
     bool armed = false;
+    // batched prefill workspace (rows of the prompt), grown on demand
+    uint32_t pf_cap = 0;
+    float *pf_x = nullptr, *pf_c = nullptr, *pf_a = nullptr, *pf_part = nullptr;
+    uint8_t *pf_codes = nullptr, *pf_scales = nullptr;
+    uint32_t *pf_ids = nullptr;
 };
 
 static int dalloc(llama_engine *e, void **p, size_t bytes)
@@ -111,7 +117,7 @@ static int enqueue_step(llama_engine *e)
         aa.ts = hd; aa.hs = (uint64_t)e->max_seq_alloc * hd;
         aa.n_heads = c.n_heads; aa.n_kv_heads = c.n_kv_heads; aa.head_dim = hd; aa.seq = 0;
         aa.chunk = e->attn_chunk; aa.max_splits = e->attn_max_splits;
-        if ((rc = attn_launch(aa, 1, s, e->attn_chunk * e->attn_max_splits))) return rc;
+        if ((rc = attn_launch(aa, 1, s, e->attn_chunk * e->attn_max_splits, 1))) return rc;
         GemvArgs oa{w.o_c, w.o_s, e->attn_out, e->x, nullptr, nullptr, c.dim, qd, 0, 0.0f};
         if ((rc = gemv_launch("e8m0", RFP4_EPI_RESIDUAL, oa, s, 0))) return rc;
         GemvArgs ga{w.gu_c, w.gu_s, e->x, e->sw, nullptr, e->norm_ffn + (size_t)l * c.dim, c.ffn, c.dim, c.ffn, c.eps};
@@ -123,6 +129,98 @@ static int enqueue_step(llama_engine *e)
     if ((rc = gemv_launch("e8m0", RFP4_EPI_ARGMAX, la, s, 0))) return rc;
     StepArgs sa{e->best, e->state, e->ids, e->last_tok, e->n_best, 0};
     return launch("rfp4_step", dim3(1), dim3(1024), s, &sa);
+}
+
+// ---------------------------------------------------------------- batched prefill
+static void dfree(llama_engine *e, void *p)
+{
+    if (!p) return;
+    hipFree(p);
+    for (size_t i = 0; i < e->allocs.size(); i++)
+        if (e->allocs[i] == p) {
+            e->allocs.erase(e->allocs.begin() + (long)i);
+            break;
+        }
+}
+
+static int prefill_reserve(llama_engine *e, uint32_t n)
+{
+    if (n <= e->pf_cap) return RFP4_OK;
+    const rfp4_model_config &c = e->c;
+    const uint32_t qd = qdim(c), kvd = kvdim(c);
+    const uint32_t cap = (n + 255u) / 256u * 256u;
+    hipStreamSynchronize(e->stream);
+    dfree(e, e->pf_x); dfree(e, e->pf_c); dfree(e, e->pf_a); dfree(e, e->pf_part);
+    dfree(e, e->pf_codes); dfree(e, e->pf_scales); dfree(e, e->pf_ids);
+    e->pf_x = e->pf_c = e->pf_a = e->pf_part = nullptr;
+    e->pf_codes = e->pf_scales = nullptr;
+    e->pf_ids = nullptr;
+    e->pf_cap = 0;
+    const size_t kmax = std::max(std::max(c.dim, qd), c.ffn);
+    const size_t ncols = std::max(std::max(qd + 2 * kvd, 2 * c.ffn), c.dim);
+    int rc = dalloc_t(e, &e->pf_x, (size_t)cap * c.dim);
+    if (!rc) rc = dalloc_t(e, &e->pf_c, (size_t)cap * ncols);
+    if (!rc) rc = dalloc_t(e, &e->pf_a, (size_t)cap * qd);
+    if (!rc) rc = dalloc_t(e, &e->pf_part, (size_t)cap * c.n_heads * e->attn_max_splits * (c.head_dim + 4));
+    if (!rc) rc = dalloc_t(e, &e->pf_codes, (size_t)cap * kmax / 2);
+    if (!rc) rc = dalloc_t(e, &e->pf_scales, (size_t)cap * kmax / 32);
+    if (!rc) rc = dalloc_t(e, &e->pf_ids, cap);
+    if (!rc) e->pf_cap = cap;
+    return rc;
+}
+
+// The prompt through the MXFP4 GEMM: llama_run/src/main.rs:550-556 feed it
+// token by token; here all n positions of a layer run at once, every
+// projection input quantised to MXFP4 per 32 along K (the GEMM is FP4 x FP4).
+static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
+{
+    const rfp4_model_config &c = e->c;
+    hipStream_t s = e->stream;
+    const uint32_t qd = qdim(c), kvd = kvdim(c), hd = c.head_dim, nqkv = qd + 2 * kvd;
+    int rc;
+    RowsArgs ea{};
+    ea.ids = e->pf_ids; ea.embed = e->embed; ea.y = e->pf_x; ea.rows = n; ea.k = c.dim; ea.vocab = c.vocab;
+    if ((rc = launch("rfp4_embed_rows", dim3(n), dim3(256), s, &ea))) return rc;
+    for (uint32_t l = 0; l < c.n_layers; l++) {
+        const LayerW &w = e->L[l];
+        uint16_t *kc = e->kcache + (size_t)l * c.n_kv_heads * e->max_seq_alloc * hd;
+        uint16_t *vc = e->vcache + (size_t)l * c.n_kv_heads * e->max_seq_alloc * hd;
+        RowsArgs na{};
+        na.x = e->pf_x; na.w = e->norm_attn + (size_t)l * c.dim; na.codes = e->pf_codes; na.scales = e->pf_scales;
+        na.rows = n; na.k = c.dim; na.eps = c.eps;
+        if ((rc = launch("rfp4_rmsnorm_quant_rows", dim3(n), dim3(256), s, &na, c.dim * 4u))) return rc;
+        if ((rc = fp4_gemm(s, n, nqkv, c.dim, e->pf_codes, e->pf_scales, w.qkv_c, w.qkv_s, e->pf_c))) return rc;
+        RopeRowsArgs ra{};
+        ra.qkv = e->pf_c; ra.cosv = e->cos_tab; ra.sinv = e->sin_tab; ra.kc = kc; ra.vc = vc;
+        ra.ts = hd; ra.hs = (uint64_t)e->max_seq_alloc * hd;
+        ra.rows = n; ra.row_stride = nqkv; ra.n_heads = c.n_heads; ra.n_kv_heads = c.n_kv_heads;
+        ra.head_dim = hd; ra.pos0 = pos0;
+        if ((rc = launch("rfp4_rope_kv_rows", dim3(n), dim3(256), s, &ra))) return rc;
+        AttnArgs aa{};
+        aa.q = e->pf_c; aa.q_rs = nqkv; aa.kc = kc; aa.vc = vc; aa.out = e->pf_a; aa.out_rs = qd;
+        aa.part = e->pf_part; aa.pos_ptr = nullptr; aa.seq = pos0 + 1; // row r sees pos0 + r + 1 positions
+        aa.ts = hd; aa.hs = (uint64_t)e->max_seq_alloc * hd;
+        aa.n_heads = c.n_heads; aa.n_kv_heads = c.n_kv_heads; aa.head_dim = hd;
+        aa.chunk = e->attn_chunk; aa.max_splits = e->attn_max_splits;
+        if ((rc = attn_launch(aa, 1, s, pos0 + n, n))) return rc;
+        if ((rc = mx4_quantize(s, n, qd, e->pf_a, 0, e->pf_codes, e->pf_scales))) return rc;
+        if ((rc = fp4_gemm(s, n, c.dim, qd, e->pf_codes, e->pf_scales, w.o_c, w.o_s, e->pf_c))) return rc;
+        if ((rc = residual(s, n * c.dim, e->pf_c, e->pf_x))) return rc;
+        na.w = e->norm_ffn + (size_t)l * c.dim;
+        if ((rc = launch("rfp4_rmsnorm_quant_rows", dim3(n), dim3(256), s, &na, c.dim * 4u))) return rc;
+        if ((rc = fp4_gemm(s, n, 2 * c.ffn, c.dim, e->pf_codes, e->pf_scales, w.gu_c, w.gu_s, e->pf_c))) return rc;
+        RowsArgs sa{};
+        sa.x = e->pf_c; sa.codes = e->pf_codes; sa.scales = e->pf_scales; sa.rows = n; sa.k = c.ffn;
+        if ((rc = launch("rfp4_swiglu_quant_rows", dim3(n), dim3(256), s, &sa))) return rc;
+        if ((rc = fp4_gemm(s, n, c.dim, c.ffn, e->pf_codes, e->pf_scales, w.d_c, w.d_s, e->pf_c))) return rc;
+        if ((rc = residual(s, n * c.dim, e->pf_c, e->pf_x))) return rc;
+    }
+    // last row: the decode step's final norm + LM head, then argmax
+    rc = hip_check(hipMemcpyAsync(e->x, e->pf_x + (size_t)(n - 1) * c.dim, c.dim * sizeof(float),
+                                  hipMemcpyDeviceToDevice, s), "hipMemcpyAsync(prefill row)");
+    if (!rc) rc = mx4_gemv_rmsnorm(s, c.vocab, c.dim, e->lm_c, e->lm_s, e->x, e->norm_final, c.eps, e->logits);
+    if (!rc) rc = argmax(s, c.vocab, e->logits, e->last_tok);
+    return rc;
 }
 
 static int capture_graph(llama_engine *e)
@@ -414,6 +512,33 @@ int llama_engine_kv(llama_engine *e, int layer, const uint16_t **k, const uint16
     *v = e->vcache + (size_t)layer * per;
     *count = per;
     return RFP4_OK;
+}
+
+int llama_engine_prefill(llama_engine *e, const uint32_t *prompt, uint32_t n_prompt, uint32_t pos0,
+                         uint32_t *next_token)
+{
+    if (!e || !prompt || !next_token || n_prompt == 0)
+        return set_error(RFP4_E_INVALID, "llama_engine_prefill: null argument or empty prompt");
+    const rfp4_model_config &c = e->c;
+    if ((uint64_t)pos0 + n_prompt > c.max_seq)
+        return set_error(RFP4_E_KV_OVERFLOW, "prefill of %u tokens at position %u runs past max_seq %u", n_prompt, pos0,
+                         c.max_seq);
+    if (c.dim % 256u || qdim(c) % 256u || c.ffn % 256u)
+        return set_error(RFP4_E_SHAPE, "prefill runs on the MXFP4 GEMM: dim, n_heads*head_dim and ffn must be multiples of 256");
+    for (uint32_t i = 0; i < n_prompt; i++)
+        if (prompt[i] >= c.vocab) return set_error(RFP4_E_INVALID, "prompt token %u out of range", prompt[i]);
+    int rc = prefill_reserve(e, n_prompt);
+    if (!rc)
+        rc = hip_check(hipMemcpyAsync(e->pf_ids, prompt, n_prompt * sizeof(uint32_t), hipMemcpyHostToDevice, e->stream),
+                       "hipMemcpyAsync(prompt)");
+    if (!rc) rc = enqueue_prefill(e, n_prompt, pos0);
+    uint32_t tok = 0;
+    if (!rc)
+        rc = hip_check(hipMemcpyAsync(&tok, e->last_tok, sizeof(uint32_t), hipMemcpyDeviceToHost, e->stream),
+                       "hipMemcpyAsync(token)");
+    if (!rc) rc = hip_check(hipStreamSynchronize(e->stream), "hipStreamSynchronize");
+    if (!rc) *next_token = tok;
+    return rc;
 }
 
 uint64_t llama_engine_weight_bytes(const llama_engine *e)

@@ -11,6 +11,7 @@
 #include "device/mma.h"
 #include "device/gemm.h"
 #include "device/gemm_skinny.h"
+#include "device/prefill.h"
 
 #define K256 extern "C" __global__ __launch_bounds__(256)
 #define K1024 extern "C" __global__ __launch_bounds__(1024)
@@ -133,3 +134,9 @@ GEMM_SKINNY_KERNEL(32, 2, 1)
 GEMM_SKINNY_KERNEL(32, 2, 2)
 GEMM_SKINNY_KERNEL(64, 4, 1)
 GEMM_SKINNY_KERNEL(64, 4, 2)
+
+// ---- batched prefill row kernels (device/prefill.h)
+K256 void rfp4_embed_rows(RowsArgs a) { embed_rows_body(a); }
+K256 void rfp4_rmsnorm_quant_rows(RowsArgs a) { rmsnorm_quant_rows_body(a); }
+K256 void rfp4_swiglu_quant_rows(RowsArgs a) { swiglu_quant_rows_body(a); }
+K256 void rfp4_rope_kv_rows(RopeRowsArgs a) { rope_kv_rows_body(a); }

@@ -374,7 +374,7 @@ extern "C" int rfp4_debug_gemv_variant(int rows_per_wave, int slices)
 
 namespace rfp4 {
 
-int attn_launch(const AttnArgs &args, int kv_f16, hipStream_t s, uint32_t max_seq_for_grid)
+int attn_launch(const AttnArgs &args, int kv_f16, hipStream_t s, uint32_t max_seq_for_grid, uint32_t rows)
 {
     const char *name;
     if (args.head_dim == 64) name = kv_f16 ? "rfp4_attn_hd64_f16" : "rfp4_attn_hd64_f32";
@@ -382,13 +382,14 @@ int attn_launch(const AttnArgs &args, int kv_f16, hipStream_t s, uint32_t max_se
     else return set_error(RFP4_E_SHAPE, "attn: head_dim %u unsupported (64 or 128)", args.head_dim);
     if (args.chunk == 0) return set_error(RFP4_E_INVALID, "attn: chunk must be positive");
     if (args.cosv && !kv_f16) return set_error(RFP4_E_INVALID, "attn: fused KV append needs an fp16 cache");
+    if (rows == 0 || (rows > 1 && args.cosv)) return set_error(RFP4_E_INVALID, "attn: fused append is one row only");
     uint32_t splits = (max_seq_for_grid + args.chunk - 1) / args.chunk;
     AttnArgs a = args;
-    int rc = launch(name, dim3(a.n_kv_heads, splits), dim3(256), s, &a);
+    int rc = launch(name, dim3(a.n_kv_heads, splits, rows), dim3(256), s, &a);
     if (rc || splits <= 1) return rc;
     // the split states are merged by a second launch (stream order, no fence)
-    return launch(args.head_dim == 64 ? "rfp4_attn_merge_hd64" : "rfp4_attn_merge_hd128", dim3(a.n_heads), dim3(256),
-                  s, &a);
+    return launch(args.head_dim == 64 ? "rfp4_attn_merge_hd64" : "rfp4_attn_merge_hd128", dim3(a.n_heads, 1, rows),
+                  dim3(256), s, &a);
 }
 
 uint32_t attn_sub_chunk(uint32_t head_dim, uint32_t elem_bytes)
@@ -561,7 +562,7 @@ static int attn_common(hipStream_t s, uint32_t nh, uint32_t nkv, uint32_t hd, ui
     a.ts = ts; a.hs = hs;
     a.n_heads = nh; a.n_kv_heads = nkv; a.head_dim = hd; a.seq = seq;
     a.chunk = chunk; a.max_splits = splits;
-    return attn_launch(a, f16, s, seq);
+    return attn_launch(a, f16, s, seq, 1);
 }
 
 int attn_decode(rfp4_stream_t stream, uint32_t n_heads, uint32_t n_kv_heads, uint32_t seq, const float *q,

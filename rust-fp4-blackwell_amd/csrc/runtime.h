@@ -39,7 +39,7 @@ struct GemvVariant {
 GemvVariant gemv_variant(uint32_t n, uint32_t k, int epi, bool f32scale);
 int gemv_launch(const char *scale_name, int epi, const GemvArgs &args, hipStream_t s, int r_override);
 uint32_t gemv_blocks(uint32_t n_logical, uint32_t k, int epi);
-int attn_launch(const AttnArgs &args, int kv_f16, hipStream_t s, uint32_t max_seq_for_grid);
+int attn_launch(const AttnArgs &args, int kv_f16, hipStream_t s, uint32_t max_seq_for_grid, uint32_t rows);
 uint32_t attn_sub_chunk(uint32_t head_dim, uint32_t elem_bytes);
 uint32_t attn_chunk_for(uint32_t n_kv_heads, uint32_t seq, uint32_t num_cus, uint32_t head_dim, uint32_t elem_bytes);
 

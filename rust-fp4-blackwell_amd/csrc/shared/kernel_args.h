@@ -87,7 +87,31 @@ typedef struct AttnArgs {
     uint64_t ts, hs;      // token and head strides (elements)
     uint32_t n_heads, n_kv_heads, head_dim, seq;
     uint32_t chunk, max_splits;
+    // Several query rows (grid z = row, batched prefill): row r reads q + r*q_rs,
+    // writes out + r*out_rs, sees seq + r positions (causal), and owns its own
+    // workspace slice of n_heads*max_splits*(head_dim+4) floats.  One row: 0, 0.
+    uint32_t q_rs, out_rs;
 } AttnArgs;
+
+// Batched prefill row kernels (device/prefill.h).
+typedef struct RowsArgs {
+    const float *x;          // rmsnorm: rows [rows][k]; swiglu: gate|up rows [rows][2k]
+    const uint16_t *w;       // rmsnorm: fp16 weights [k]
+    uint8_t *codes, *scales; // quantised rows [rows][k/2], [rows][k/32]
+    const uint32_t *ids;     // embed: token ids [rows]
+    const uint16_t *embed;   // embed: fp16 table [vocab][k]
+    float *y;                // embed: output rows [rows][k]
+    uint32_t rows, k, vocab;
+    float eps;
+} RowsArgs;
+
+typedef struct RopeRowsArgs {
+    float *qkv;               // [rows][row_stride]: n_heads q, n_kv_heads k, n_kv_heads v (head_dim each)
+    const float *cosv, *sinv; // [pos][head_dim/2]
+    uint16_t *kc, *vc;        // fp16 caches: element (t, kvh, d) at t*ts + kvh*hs + d
+    uint64_t ts, hs;
+    uint32_t rows, row_stride, n_heads, n_kv_heads, head_dim, pos0;
+} RopeRowsArgs;
 
 typedef struct FillArgs {
     uint32_t *p;

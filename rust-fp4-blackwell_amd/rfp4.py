@@ -98,6 +98,7 @@ _SIGS = {
     "llama_engine_create": (I32, [C.POINTER(ModelConfig), U64, C.POINTER(P)]),
     "llama_engine_destroy": (I32, [P]),
     "llama_engine_prefill_kv": (I32, [P, U64, U32]),
+    "llama_engine_prefill": (I32, [P, P, U32, U32, C.POINTER(U32)]),
     "llama_decode_step": (I32, [P, U32, U32, C.POINTER(U32)]),
     "llama_generate": (I32, [P, P, U32, U32, U32, P]),
     "llama_engine_begin": (I32, [P, P, U32, U32, U32]),
@@ -416,6 +417,13 @@ class Engine:
 
     def prefill_kv(self, seed: int, upto: int):
         check(load().llama_engine_prefill_kv(self.h, seed, upto))
+
+    def prefill(self, prompt, pos0: int) -> int:
+        """Batched prefill of prompt at positions pos0..; returns the next greedy token."""
+        pr = np.ascontiguousarray(prompt, dtype=np.uint32)
+        out = U32(0)
+        check(load().llama_engine_prefill(self.h, pr.ctypes.data, len(pr), pos0, C.byref(out)))
+        return out.value
 
     def decode_step(self, tok: int, pos: int) -> int:
         out = U32(0)

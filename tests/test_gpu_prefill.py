@@ -1,0 +1,161 @@
+"""Batched prefill (the prompt through the MXFP4 GEMM, activations quantised
+to MXFP4 per 32 along K) against the CPU oracle's orc_model_prefill on the
+same packed weights and seeds.  The reference feeds a prompt token by token
+(llama_run/src/main.rs:550-556); the oracle's prefill restates that loop with
+every projection input quantised by the OCP rules, so the two differ only in
+f32 summation order.  A value that lands within an ulp of an E2M1 rounding
+boundary can take the neighbouring code on one side, so logits and K/V are
+compared normwise (bars below) and greedy tokens exactly."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+TINY = dict(dim=256, n_layers=2, n_heads=4, n_kv_heads=2, head_dim=64, ffn=512, vocab=1024,
+            theta=10000.0, eps=1e-5, max_seq=64)
+TINY128 = dict(dim=512, n_layers=2, n_heads=8, n_kv_heads=2, head_dim=128, ffn=1024, vocab=2048,
+               theta=500000.0, eps=1e-5, max_seq=300)
+
+LOGIT_TOL = 2e-2   # max |gpu - oracle| / max |oracle| over the vocabulary
+KV_TOL = 2e-2      # same, per layer, over the prefilled K and V
+
+
+def _engine(rf, cfg, seed):
+    c = {k: v for k, v in cfg.items() if k != "max_seq"}
+    return rf.Engine(rf.model_config(max_seq=cfg["max_seq"], **c), seed)
+
+
+def _kv(eng, ref, cfg, layer, lo, hi):
+    hd, nkv = cfg["head_dim"], cfg["n_kv_heads"]
+    k, v = eng.kv_host(layer)
+    stride = k.size // (nkv * hd)
+    f = lambda a, s: a.reshape(nkv, s, hd)[:, lo:hi].view(np.float16).astype(np.float32)
+    return (f(k, stride), f(v, stride),
+            f(ref.kcache(layer), cfg["max_seq"]), f(ref.vcache(layer), cfg["max_seq"]))
+
+
+def _rel(a, b):
+    return float(np.max(np.abs(a - b)) / max(np.abs(b).max(), 1e-30))
+
+
+@pytest.mark.parametrize("cfg,n", [(TINY, 1), (TINY, 5), (TINY, 37), (TINY128, 3), (TINY128, 200)])
+def test_prefill_matches_oracle(rf, orc, cfg, n):
+    seed = 0x5EED + n
+    rng = np.random.default_rng(n)
+    prompt = rng.integers(0, cfg["vocab"], n, dtype=np.uint32)
+    print(f"prefill cfg dim={cfg['dim']} n={n}", flush=True)
+    eng = _engine(rf, cfg, seed)
+    ref = orc.Model(cfg, seed)
+    tok = eng.prefill(prompt, 0)
+    rtok, rlog = ref.prefill(prompt, 0, want_logits=True)
+    lg = eng.logits()
+    top2 = np.sort(rlog)[-2:]
+    assert _rel(lg, rlog) <= LOGIT_TOL, f"logits rel {_rel(lg, rlog):.3e}"
+    assert tok == rtok, f"gpu {tok} cpu {rtok} margin {top2[1] - top2[0]:.4g}"
+    for layer in range(cfg["n_layers"]):
+        kg, vg, kr, vr = _kv(eng, ref, cfg, layer, 0, n)
+        assert _rel(kg, kr) <= KV_TOL, f"K layer {layer} rel {_rel(kg, kr):.3e}"
+        assert _rel(vg, vr) <= KV_TOL, f"V layer {layer} rel {_rel(vg, vr):.3e}"
+    eng.close()
+
+
+@pytest.mark.parametrize("cfg", [TINY, TINY128])
+def test_prefill_then_decode(rf, orc, cfg):
+    """Prefill, then the on-device decode loop from position n: greedy tokens
+    identical to the oracle's prefill + decode."""
+    seed = 0xD0C
+    prompt = [1, 7, 42, 99, 5, 3, 8, 250, 17, 64, 11]
+    n_new = 16
+    eng = _engine(rf, cfg, seed)
+    ref = orc.Model(cfg, seed)
+    t0 = eng.prefill(prompt, 0)
+    r0 = ref.prefill(prompt, 0)
+    assert t0 == r0
+    gpu = eng.generate([t0], len(prompt), n_new)
+    cpu, margins = ref.generate([r0], len(prompt), n_new)
+    assert list(gpu) == list(cpu), f"gpu {list(gpu)}\ncpu {list(cpu)}\nmargins {margins}"
+    eng.close()
+
+
+@pytest.mark.parametrize("cfg", [TINY, TINY128])
+def test_prefill_in_chunks(rf, orc, cfg):
+    """A chunk prefilled at pos0 > 0 attends to the K/V of an earlier chunk
+    (causal offset: row r sees pos0 + r + 1 positions)."""
+    seed = 0xCAFE
+    head = [4, 8, 15, 16, 23]
+    chunk = list(range(100, 140))
+    eng = _engine(rf, cfg, seed)
+    ref = orc.Model(cfg, seed)
+    assert eng.prefill(head, 0) == ref.prefill(head, 0)
+    tok = eng.prefill(chunk, len(head))
+    rtok, rlog = ref.prefill(chunk, len(head), want_logits=True)
+    assert _rel(eng.logits(), rlog) <= LOGIT_TOL
+    assert tok == rtok
+    for layer in range(cfg["n_layers"]):
+        kg, vg, kr, vr = _kv(eng, ref, cfg, layer, 0, len(head) + len(chunk))
+        assert _rel(kg, kr) <= KV_TOL and _rel(vg, vr) <= KV_TOL
+    eng.close()
+
+
+def test_prefill_after_decode(rf, orc):
+    """A chunk prefilled after the decode loop wrote the first positions.  The
+    decode path keeps f32 activations, so its K/V differ from the oracle's by
+    fp16 rounding (checked below); through the MXFP4 activation quantiser such
+    a difference can move a block's absmax across a power of two and re-scale
+    all 32 values of that block, so only the greedy token is held exact."""
+    cfg, seed = TINY128, 0xCAFE
+    head = [4, 8, 15, 16, 23]
+    chunk = list(range(100, 140))
+    eng = _engine(rf, cfg, seed)
+    ref = orc.Model(cfg, seed)
+    g = eng.generate(head, 0, 1)
+    c, _ = ref.generate(head, 0, 1)
+    assert list(g) == list(c)
+    for layer in range(cfg["n_layers"]):
+        kg, vg, kr, vr = _kv(eng, ref, cfg, layer, 0, len(head))
+        assert _rel(kg, kr) <= 2e-3 and _rel(vg, vr) <= 2e-3
+    tok = eng.prefill(chunk, len(head))
+    rtok, rlog = ref.prefill(chunk, len(head), want_logits=True)
+    top2 = np.sort(rlog)[-2:]
+    assert tok == rtok, f"gpu {tok} cpu {rtok} margin {top2[1] - top2[0]:.4g}"
+    eng.close()
+
+
+def test_prefill_repeatable_and_regrows(rf):
+    """Same prompt twice gives bit-identical logits; a longer prompt after a
+    short one regrows the workspace and still matches a fresh engine."""
+    cfg, seed = TINY, 0x1234
+    eng = _engine(rf, cfg, seed)
+    p = list(range(3, 40))
+    t1 = eng.prefill(p[:4], 0)
+    l1 = eng.logits()
+    t2 = eng.prefill(p[:4], 0)
+    np.testing.assert_array_equal(eng.logits(), l1)
+    assert t1 == t2
+    t3 = eng.prefill(p, 0)
+    l3 = eng.logits()
+    fresh = _engine(rf, cfg, seed)
+    assert fresh.prefill(p, 0) == t3
+    np.testing.assert_array_equal(fresh.logits(), l3)
+    fresh.close()
+    eng.close()
+
+
+def test_prefill_errors(rf):
+    eng = _engine(rf, TINY, 1)
+    with pytest.raises(rf.Rfp4Error) as e:
+        eng.prefill([1, 2, 3], TINY["max_seq"] - 2)  # runs past max_seq
+    assert e.value.code == -4
+    with pytest.raises(rf.Rfp4Error) as e:
+        eng.prefill([TINY["vocab"]], 0)              # token out of range
+    assert e.value.code == -1
+    with pytest.raises(rf.Rfp4Error) as e:
+        eng.prefill([], 0)
+    assert e.value.code == -1
+    eng.close()
+    odd = dict(TINY, ffn=288)                        # ffn not a multiple of 256
+    eng = _engine(rf, odd, 1)
+    with pytest.raises(rf.Rfp4Error) as e:
+        eng.prefill([1, 2], 0)
+    assert e.value.code == -2
+    eng.close()

@@ -76,6 +76,77 @@ class NumpyLlama:
         return int(np.argmax(logits)), logits
 
 
+    def prefill(self, orc, toks, pos0):
+        """Batched prefill with MXFP4 activations: every projection input row
+        quantized (OCP rules, the pinned quantizer), products in float64."""
+        c = self.c
+        nh, nkv, hd = c["n_heads"], c["n_kv_heads"], c["head_dim"]
+
+        def q(rows):
+            r = np.ascontiguousarray(rows, np.float32)
+            codes, scales = orc.quant_mx(r)
+            return _deq(orc, codes, scales, r.shape[0], r.shape[1])
+
+        X = np.stack([self.emb[t] for t in toks])
+        n = len(toks)
+        for l in range(c["n_layers"]):
+            Wq, Wk, Wv, Wo, Wg, Wu, Wd = self.W[l]
+            Hq = q(np.stack([self._norm(x, self.na[l]) for x in X]))
+            Q = (Hq @ Wq.T).astype(np.float32)
+            K = (Hq @ Wk.T).astype(np.float32)
+            V = (Hq @ Wv.T).astype(np.float32)
+            att = np.zeros((n, nh * hd))
+            for i in range(n):
+                pos = pos0 + i
+                k = self._rope(K[i].astype(np.float64), nkv, pos)
+                self.K[l][pos] = k.astype(np.float32).astype(np.float16).astype(np.float64)
+                self.V[l][pos] = V[i].reshape(nkv, hd).astype(np.float16).astype(np.float64)
+            for i in range(n):
+                pos = pos0 + i
+                qi = self._rope(Q[i].astype(np.float64), nh, pos)
+                for hh in range(nh):
+                    g = hh // (nh // nkv)
+                    sc = self.K[l][:pos + 1, g] @ qi[hh] / math.sqrt(hd)
+                    p = np.exp(sc - sc.max())
+                    att[i, hh * hd:(hh + 1) * hd] = (p / p.sum()) @ self.V[l][:pos + 1, g]
+            X = X + q(att) @ Wo.T
+            Hq = q(np.stack([self._norm(x, self.nf[l]) for x in X]))
+            gate, up = Hq @ Wg.T, Hq @ Wu.T
+            X = X + q(gate / (1 + np.exp(-gate)) * up) @ Wd.T
+        logits = self.lm @ self._norm(X[-1], self.nfinal)
+        return int(np.argmax(logits)), logits
+
+
+def test_oracle_prefill_matches_numpy_llama(orc):
+    """orc_model_prefill against the float64 numpy prefill: from position 0,
+    and continuing a cache written by three decode steps (causal rows see the
+    earlier positions); logits, next token and the prefilled fp16 K/V."""
+    seed = 0x5EF1
+    m = orc.Model(CFG, seed)
+    ref = NumpyLlama(orc, m, CFG)
+    toks = [3, 77, 150, 9, 300, 41]
+    nxt, lg = m.prefill(toks, 0, want_logits=True)
+    rn, rl = ref.prefill(orc, toks, 0)
+    assert nxt == rn
+    assert np.abs(lg - rl).max() <= 1e-4 * np.abs(rl).max()
+    hd, nkv = CFG["head_dim"], CFG["n_kv_heads"]
+    for l in range(CFG["n_layers"]):
+        kc = m.kcache(l).reshape(nkv, CFG["max_seq"], hd)[:, :len(toks)].view(np.float16).astype(np.float64)
+        np.testing.assert_allclose(kc.transpose(1, 0, 2), ref.K[l][:len(toks)], rtol=2e-3, atol=2e-3)
+    m.close()
+
+    m = orc.Model(CFG, seed)
+    ref = NumpyLlama(orc, m, CFG)
+    for pos, t in enumerate([5, 6, 7]):
+        m.step(t, pos)
+        ref.step(t, pos)
+    nxt, lg = m.prefill(toks[:4], 3, want_logits=True)
+    rn, rl = ref.prefill(orc, toks[:4], 3)
+    assert nxt == rn
+    assert np.abs(lg - rl).max() <= 1e-4 * np.abs(rl).max()
+    m.close()
+
+
 def test_oracle_decode_matches_numpy_llama(orc):
     seed = 0xBEEF
     m = orc.Model(CFG, seed)
