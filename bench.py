@@ -273,7 +273,7 @@ def main():
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--cpu-steps", type=int, default=2)
+    ap.add_argument("--cpu-steps", type=int, default=20)
     ap.add_argument("--no-tiny", action="store_true", help="skip the TinyLlama-1.1B line")
     ap.add_argument("--no-gemm", action="store_true", help="skip the config-5 batched GEMM figures")
     ap.add_argument("--no-prefill", action="store_true", help="skip the batched prefill figure")
