@@ -181,11 +181,21 @@ int rfp4_mma_tile32(rfp4_stream_t stream, const uint32_t *a, const uint32_t *b, 
  * (rows per wave 2/4/8, up-front K-slices or 0 for the slice loop;
  * 0, -1 = automatic).  No reference counterpart. */
 int rfp4_debug_gemv_variant(int rows_per_wave, int slices);
-/* Test hook: GEMV implementation of later launches on this thread: 0 = auto
- * (matrix-core kernel for E8M0 scales and k % 128 == 0, else VALU), 1 = VALU
- * kernel, 2 = matrix-core kernel (rows_per_wave then means 16-row tiles per
- * wave, slices the super-chunks per wave).  No reference counterpart. */
+/* Test hook: GEMV implementation of later launches on this thread: 0 = auto,
+ * 1 = VALU kernel, 2 = bf16 matrix-core kernel (rows_per_wave then means
+ * 16-row tiles per wave, slices the super-chunks per wave), 3 = block-scaled
+ * MFMA kernel (E2M1 weights x E4M3 planes of x; E8M0 scales, k % 512 == 0,
+ * k <= 14336).  No reference counterpart. */
 int rfp4_debug_gemv_path(int path);
+/* Test hook: one GEMV launch with any epilogue (0 store, 1 residual,
+ * 2 SwiGLU with gate rows [0, n) and up rows [pair_off, pair_off + n),
+ * 3 argmax) and, when norm_w is not null, the RMSNorm of x fused in front:
+ * the engine's fused launches, reachable alone.  Argmax needs
+ * mx4_gemv_argmax_workspace(n) bytes of workspace.  No reference
+ * counterpart. */
+int rfp4_debug_gemv_fused(rfp4_stream_t stream, int epi, uint32_t n, uint32_t k, uint32_t pair_off,
+                          const uint8_t *codes, const uint8_t *scales, const float *x, const uint16_t *norm_w,
+                          float eps, float *y, void *workspace, uint32_t *best_token);
 /* Hardware E2M1 conversion of n words (8 codes each) to 8n floats. */
 int rfp4_selftest_cvt_fp4(rfp4_stream_t stream, uint32_t n, const uint32_t *words, float *out);
 /* Hardware E2M1 -> bf16 conversion with a per-word f32 scale: out[4i+s] =

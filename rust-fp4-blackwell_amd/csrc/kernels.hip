@@ -5,6 +5,7 @@
 #include "device/common.h"
 #include "device/gemv.h"
 #include "device/gemv_mfma.h"
+#include "device/gemv_mx.h"
 #include "device/norm_rope.h"
 #include "device/attn.h"
 #include "device/misc.h"
@@ -53,6 +54,28 @@ GEMV_KERNEL_OCC4(e8m0, 0, swiglu, RFP4_EPI_SWIGLU, 4, 1)
 GEMV_KERNEL_OCC4(e8m0, 0, swiglu, RFP4_EPI_SWIGLU, 4, 2)
 GEMV_KERNEL(e8m0, 0, swiglu, RFP4_EPI_SWIGLU, 4, 3) // 128 VGPRs would spill
 GEMV_NS_FULL(f32, 1, store, RFP4_EPI_STORE, 4)
+
+// ---- block-scaled MFMA GEMV: rfp4_gemvx_<epilogue>_n<NORM>_p<PER>
+// (E2M1 weights straight into v_mfma_scale_f32_16x16x128_f8f6f4, x as E4M3
+// planes; PER = ceil(K / 2048) segments of 512 per wave).  Host selection:
+// runtime.cpp gemv_mx_ok.
+#define GEMVX_KERNEL(ENAME, EPI, NORM, PER) \
+    K256 void rfp4_gemvx_##ENAME##_n##NORM##_p##PER(GemvArgs a) { gemv_mx_body<EPI, NORM, PER>(a); }
+#define GEMVX_PERS(ENAME, EPI, NORM) \
+    GEMVX_KERNEL(ENAME, EPI, NORM, 1) \
+    GEMVX_KERNEL(ENAME, EPI, NORM, 2) \
+    GEMVX_KERNEL(ENAME, EPI, NORM, 3) \
+    GEMVX_KERNEL(ENAME, EPI, NORM, 4) \
+    GEMVX_KERNEL(ENAME, EPI, NORM, 5) \
+    GEMVX_KERNEL(ENAME, EPI, NORM, 6) \
+    GEMVX_KERNEL(ENAME, EPI, NORM, 7)
+GEMVX_PERS(store, RFP4_EPI_STORE, 0)
+GEMVX_PERS(store, RFP4_EPI_STORE, 1)
+GEMVX_PERS(resid, RFP4_EPI_RESIDUAL, 0)
+GEMVX_PERS(swiglu, RFP4_EPI_SWIGLU, 0)
+GEMVX_PERS(swiglu, RFP4_EPI_SWIGLU, 1)
+GEMVX_PERS(argmax, RFP4_EPI_ARGMAX, 0)
+GEMVX_PERS(argmax, RFP4_EPI_ARGMAX, 1)
 
 // ---- MFMA GEMV: rfp4_gemvm_<epilogue>_t<RT>_s<NSC>
 // (RT 16-row tiles per wave, NSC = ceil(K/512) super-chunks per wave issued

@@ -259,8 +259,19 @@ GemvVariant gemv_variant(uint32_t n, uint32_t k, int epi, bool f32scale)
     return GemvVariant{R, ns};
 }
 
-// Path: 0 = automatic, 1 = VALU kernel, 2 = MFMA kernel (tests only).
+// Path: 0 = automatic, 1 = VALU kernel, 2 = bf16 MFMA kernel, 3 = block-scaled
+// MFMA kernel (forced paths: tests only).
 static thread_local int t_force_path = 0;
+
+// Block-scaled MFMA kernel (gemv_mx.h): E8M0 weight scales, K in whole
+// 512-value segments, at most 7 segments per wave (K <= 14336) and the E4M3
+// planes of x in LDS.
+constexpr uint32_t kGemvMxPlanes = 6;
+static bool gemv_mx_ok(uint32_t k, bool f32scale)
+{
+    if (f32scale || k % 512u || k > 7u * 2048u) return false;
+    return !g_rt || (size_t)k * kGemvMxPlanes + (k / 32u) * kGemvMxPlanes + 1024u <= g_rt->max_lds;
+}
 
 // The MFMA kernel needs E8M0 scales (folded into the bf16 conversion), K in
 // whole 128-value super-chunks and the three bf16 planes of x in LDS.
@@ -284,7 +295,7 @@ static bool gemv_mfma_has(int epi, int rt, int nsc)
 }
 
 struct GemvPlan {
-    bool mfma;
+    bool mfma, mx;
     int R, NS;               // VALU: rows per wave, K slices; MFMA: 16-row tiles, super-chunks per wave
     uint32_t rows_per_block;
 };
@@ -298,7 +309,12 @@ static GemvPlan gemv_plan(uint32_t n, uint32_t k, int epi, bool f32scale)
     // matrix-core path must also convert x into three bf16 planes per
     // workgroup.  The matrix-core kernel stays selectable (path 2).
     p.mfma = t_force_path == 2;
-    if (p.mfma) {
+    p.mx = t_force_path == 3;
+    if (p.mx) {
+        p.R = 1;
+        p.NS = (int)((k + 2047u) / 2048u);
+        p.rows_per_block = 16u;
+    } else if (p.mfma) {
         int rt = ((epi == RFP4_EPI_STORE || epi == RFP4_EPI_ARGMAX) && n >= 65536u) ? 2 : 1;
         if (t_force_path == 2 && t_force_r) rt = t_force_r;
         int per_wave = (int)(((k >> 7) + 3u) / 4u);
@@ -323,7 +339,16 @@ int gemv_launch(const char *scale_name, int epi, const GemvArgs &args, hipStream
     GemvPlan p = gemv_plan(args.n, args.k, epi, f32scale);
     char name[64];
     unsigned shmem;
-    if (p.mfma) {
+    if (p.mx) {
+        if (!gemv_mx_ok(args.k, f32scale))
+            return set_error(RFP4_E_INVALID, "gemv: block-scaled MFMA path needs E8M0 scales and k %% 512 == 0, "
+                                             "k <= 14336 (k=%u)", args.k);
+        if ((uintptr_t)args.scales % 4u) return set_error(RFP4_E_ALIGN, "gemv: block-scaled MFMA path needs 4-byte aligned scales");
+        if (epi == RFP4_EPI_RESIDUAL && args.norm_w)
+            return set_error(RFP4_E_INVALID, "gemv: no block-scaled MFMA variant of the residual GEMV with a norm");
+        snprintf(name, sizeof name, "rfp4_gemvx_%s_n%d_p%d", epi_names[epi], args.norm_w ? 1 : 0, p.NS);
+        shmem = args.k * kGemvMxPlanes + (args.k / 32u) * kGemvMxPlanes;
+    } else if (p.mfma) {
         if (!gemv_mfma_ok(args.k, f32scale))
             return set_error(RFP4_E_INVALID, "gemv: MFMA path needs E8M0 scales and k %% 128 == 0 (k=%u)", args.k);
         if (!gemv_mfma_has(epi, p.R, p.NS) || (p.NS != 0 && p.NS != (int)(((args.k >> 7) + 3u) / 4u)))
@@ -357,7 +382,8 @@ uint32_t gemv_blocks(uint32_t n_logical, uint32_t k, int epi)
 extern "C" int rfp4_debug_gemv_path(int path)
 {
     using namespace rfp4;
-    if (path < 0 || path > 2) return set_error(RFP4_E_INVALID, "path must be 0 (auto), 1 (VALU) or 2 (MFMA)");
+    if (path < 0 || path > 3)
+        return set_error(RFP4_E_INVALID, "path must be 0 (auto), 1 (VALU), 2 (bf16 MFMA) or 3 (block-scaled MFMA)");
     t_force_path = path;
     return RFP4_OK;
 }
@@ -489,6 +515,27 @@ int mx4_gemv_argmax(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_t 
     if (rc) return rc;
     // reduce the per-workgroup keys with the step kernel on a scratch cursor
     // that lives after the keys (no ids are written: ids_cap = 0).
+    uint32_t nb = gemv_blocks(n, k, RFP4_EPI_ARGMAX);
+    StepState *st = (StepState *)((char *)workspace + (size_t)nb * 8u);
+    rc = fill_words((uint32_t *)st, sizeof(StepState) / 4, 0u, (hipStream_t)stream);
+    if (rc) return rc;
+    StepArgs sa{best, st, nullptr, best_token, nb, 0};
+    return launch("rfp4_step", dim3(1), dim3(1024), (hipStream_t)stream, &sa);
+}
+
+int rfp4_debug_gemv_fused(rfp4_stream_t stream, int epi, uint32_t n, uint32_t k, uint32_t pair_off,
+                          const uint8_t *codes, const uint8_t *scales, const float *x, const uint16_t *norm_w,
+                          float eps, float *y, void *workspace, uint32_t *best_token)
+{
+    int rc = gemv_check(n, k, codes, scales, x, y);
+    if (rc) return rc;
+    if (epi < RFP4_EPI_STORE || epi > RFP4_EPI_ARGMAX) return set_error(RFP4_E_INVALID, "gemv_fused: bad epilogue %d", epi);
+    if (epi == RFP4_EPI_ARGMAX && (!workspace || !best_token))
+        return set_error(RFP4_E_INVALID, "gemv_fused: argmax needs a workspace and an output");
+    unsigned long long *best = (unsigned long long *)workspace;
+    GemvArgs a{codes, scales, x, y, best, norm_w, n, k, pair_off, eps};
+    rc = gemv_launch("e8m0", epi, a, (hipStream_t)stream, 0);
+    if (rc || epi != RFP4_EPI_ARGMAX) return rc;
     uint32_t nb = gemv_blocks(n, k, RFP4_EPI_ARGMAX);
     StepState *st = (StepState *)((char *)workspace + (size_t)nb * 8u);
     rc = fill_words((uint32_t *)st, sizeof(StepState) / 4, 0u, (hipStream_t)stream);

@@ -43,7 +43,8 @@ def test_shape_errors_need_no_device():
     assert lib.fp4_gemv(None, 16, 64, None, p, p, p) == -1         # null pointer
     assert lib.mx4_gemv(None, 16, 64, p + 4, p, p, p) == -6       # misaligned codes
     assert lib.mx4_gemv_swiglu(None, 16, 64, 8, p, p, p, p) == -2  # up rows overlap gate rows
-    assert lib.rfp4_debug_gemv_path(3) == -1
+    assert lib.rfp4_debug_gemv_path(4) == -1
+    assert lib.rfp4_debug_gemv_path(3) == 0 and lib.rfp4_debug_gemv_path(0) == 0
     assert lib.fp4_gemm(None, 32, 4096, 4000, p, p, p, p, p) == -2  # K not a multiple of 256
     assert lib.fp4_gemm(None, 32, 4098, 4096, p, p, p, p, p) == -2  # N not a multiple of 4
     assert lib.fp4_gemm(None, 0, 4096, 4096, p, p, p, p, p) == -2   # M = 0
