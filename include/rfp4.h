@@ -138,6 +138,12 @@ int argmax(rfp4_stream_t stream, uint32_t n, const float *logits, uint32_t *out)
 /* fp4_mma_allones(out): fp4_mma/src/main.rs:18-54.  One gfx950 scaled MFMA
  * tile; writes 128 floats (D[16][8], row-major), all 64.0. */
 int fp4_mma_allones(rfp4_stream_t stream, float *out);
+/* The reference's host packer (llama_run/src/main.rs:334-376, quant_fp4):
+ * per block of 32, scale = absmax/6 (1.0 for an all-zero block), codes to the
+ * nearest E2M1 magnitude (ties to the smaller), 8 codes per word low nibble
+ * first; rows x k f32 in, rows*k/8 words and rows*k/32 f32 scales out (the
+ * operands of fp4_gemv).  Host only, no device needed. */
+int fp4_quantize_absmax(const float *w, uint32_t rows, uint32_t k, uint32_t *packed, float *scales);
 /* OCP MX quantization of rows x k values (f32, or bf16 if src_is_bf16) into
  * E2M1 codes (k/2 bytes per row) and E8M0 scales (k/32 per row).  Same bits
  * as the engine's weight quantizer.  No reference counterpart on the engine
@@ -227,6 +233,24 @@ typedef struct llama_engine llama_engine;
 /* Allocates weights (synthetic MXFP4 init from `seed`, generated on the
  * device), fp16 KV caches and workspaces, and captures the step graph. */
 int llama_engine_create(const rfp4_model_config *cfg, uint64_t seed, llama_engine **out);
+/* Real weights (the reference's loader, llama_run/src/main.rs:413-460): a
+ * safetensors checkpoint with the Llama tensor names (model.layers.N.
+ * self_attn.{q,k,v,o}_proj.weight, mlp.{gate,up,down}_proj.weight,
+ * input_layernorm / post_attention_layernorm.weight, model.norm.weight,
+ * model.embed_tokens.weight, lm_head.weight or tied embeddings) in BF16, F16
+ * or F32, shapes as cfg.  Projections are quantized on the device to MXFP4
+ * (OCP rules, E8M0 per 32; mx4_quantize); norms and embeddings stay 16-bit:
+ * as stored when every one is BF16 (exact, the reference widens them to
+ * f32) or every one is F16, else rounded to bf16. */
+int llama_engine_create_from_safetensors(const rfp4_model_config *cfg, const char *path, llama_engine **out);
+/* Packed-weight cache (no reference counterpart; the reference re-quantizes
+ * at every start): the engine's MXFP4 weights, norms and embeddings with its
+ * config, written as one file, and an engine rebuilt from such a file with
+ * the given max_seq (no quantization on load). */
+int llama_engine_save(llama_engine *e, const char *path);
+int llama_engine_load(const char *path, uint32_t max_seq, llama_engine **out);
+/* The engine's config and norm/embedding format (1 = bf16, 0 = fp16). */
+int llama_engine_info(const llama_engine *e, rfp4_model_config *cfg, int *half_bf16);
 int llama_engine_destroy(llama_engine *e);
 /* Fill K/V positions [0, upto) of every layer with f16(0.1 * N(0,1))
  * (the pre-filled context of llama_decode/src/main.rs:357,375-376). */
@@ -265,6 +289,19 @@ int llama_engine_weight(llama_engine *e, int layer, int proj, const uint8_t **co
 int llama_engine_kv(llama_engine *e, int layer, const uint16_t **k, const uint16_t **v, size_t *count);
 /* Per-token weight and KV bytes the step streams at a given position. */
 uint64_t llama_engine_weight_bytes(const llama_engine *e);
+
+/* ------------------------------------------------------------------ safetensors
+ * Read-only view of a safetensors file (memory-mapped; the format the
+ * reference reads, llama_run/src/main.rs:413-430).  rfp4_st_read_f32 widens
+ * BF16, F16 or F32 to f32 exactly as the reference's `get` closure
+ * (:419-430).  No device needed. */
+typedef struct rfp4_st rfp4_st;
+int rfp4_st_open(const char *path, rfp4_st **out);
+int rfp4_st_close(rfp4_st *st);
+int rfp4_st_count(const rfp4_st *st, uint32_t *count);
+int rfp4_st_name(const rfp4_st *st, uint32_t i, const char **name);
+int rfp4_st_info(const rfp4_st *st, const char *name, char dtype[8], uint32_t *ndim, uint64_t shape[8], uint64_t *nbytes);
+int rfp4_st_read_f32(const rfp4_st *st, const char *name, float *out, uint64_t count);
 
 #ifdef __cplusplus
 }

@@ -127,6 +127,15 @@ RFP4_DEV float f16_bits_to_f32(uint16_t b)
     return (float)__builtin_bit_cast(_Float16, b);
 }
 
+// bf16 bits -> f32 (exact: the upper half of the f32 pattern)
+RFP4_DEV float bf16_bits_to_f32(uint32_t b) { return __uint_as_float(b << 16); }
+
+// A 16-bit norm weight or embedding element, stored as bf16 or fp16: exact.
+RFP4_DEV float half_bits_to_f32(uint32_t b, bool bf16)
+{
+    return bf16 ? bf16_bits_to_f32(b & 0xFFFFu) : f16_bits_to_f32((uint16_t)b);
+}
+
 // Orderable key of a float for unsigned max-reduction (NaN excluded by callers).
 RFP4_DEV uint32_t float_order_key(float f)
 {

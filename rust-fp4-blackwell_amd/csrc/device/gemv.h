@@ -33,7 +33,7 @@ RFP4_DEV float silu_ref(float g)
 
 // Stage x (K floats) into LDS; with norm_w, store x * rms * w instead
 // (rms = 1/sqrt(sum(x^2)/K + eps), llama_rmsnorm/src/main.rs:75-77).
-RFP4_DEV void stage_x(float *xs, const float *x, uint32_t k, const uint16_t *norm_w, float eps)
+RFP4_DEV void stage_x(float *xs, const float *x, uint32_t k, const uint16_t *norm_w, float eps, bool wbf16)
 {
     __shared__ float red[4];
     const int tid = threadIdx.x;
@@ -57,14 +57,14 @@ RFP4_DEV void stage_x(float *xs, const float *x, uint32_t k, const uint16_t *nor
     __syncthreads();
     float total = (red[0] + red[1]) + (red[2] + red[3]);
     float rms = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(total, (float)k), eps)));
-    for (uint32_t i = tid; i < k; i += 256) xs[i] = __fmul_rn(__fmul_rn(xs[i], rms), f16_bits_to_f32(norm_w[i]));
+    for (uint32_t i = tid; i < k; i += 256) xs[i] = __fmul_rn(__fmul_rn(xs[i], rms), half_bits_to_f32(norm_w[i], wbf16));
     __syncthreads();
 }
 
 // stage_x from registers (XV float4 of x and uint2 of fp16 norm weights per
 // thread, element 4*(tid + 256*v) + j, zero past K).
 template <int XV>
-RFP4_DEV void stage_x_regs(float *xs, const float4 *xr, const uint2 *wr, uint32_t k, bool norm, float eps)
+RFP4_DEV void stage_x_regs(float *xs, const float4 *xr, const uint2 *wr, uint32_t k, bool norm, float eps, bool wbf16)
 {
     __shared__ float red[4];
     const int tid = threadIdx.x;
@@ -91,10 +91,10 @@ RFP4_DEV void stage_x_regs(float *xs, const float4 *xr, const uint2 *wr, uint32_
         if (i4 >= k4) break;
         float4 o = xr[v];
         if (norm) {
-            o.x = __fmul_rn(__fmul_rn(o.x, rms), f16_bits_to_f32((uint16_t)(wr[v].x & 0xFFFFu)));
-            o.y = __fmul_rn(__fmul_rn(o.y, rms), f16_bits_to_f32((uint16_t)(wr[v].x >> 16)));
-            o.z = __fmul_rn(__fmul_rn(o.z, rms), f16_bits_to_f32((uint16_t)(wr[v].y & 0xFFFFu)));
-            o.w = __fmul_rn(__fmul_rn(o.w, rms), f16_bits_to_f32((uint16_t)(wr[v].y >> 16)));
+            o.x = __fmul_rn(__fmul_rn(o.x, rms), half_bits_to_f32(wr[v].x & 0xFFFFu, wbf16));
+            o.y = __fmul_rn(__fmul_rn(o.y, rms), half_bits_to_f32(wr[v].x >> 16, wbf16));
+            o.z = __fmul_rn(__fmul_rn(o.z, rms), half_bits_to_f32(wr[v].y & 0xFFFFu, wbf16));
+            o.w = __fmul_rn(__fmul_rn(o.w, rms), half_bits_to_f32(wr[v].y >> 16, wbf16));
         }
         ((float4 *)xs)[i4] = o;
     }
@@ -187,7 +187,7 @@ RFP4_DEV void gemv_body(const GemvArgs &a)
                 sb[s][p] = load_scale_bits<SCALE_F32>(a.scales, srow[p] + cl);
             }
         }
-        stage_x_regs<XV>(xs, xr, wr, a.k, norm, a.eps);
+        stage_x_regs<XV>(xs, xr, wr, a.k, norm, a.eps, a.norm_bf16 != 0);
 #pragma unroll
         for (int s = 0; s < NS; s++) {
             const uint32_t c = (uint32_t)lane + 64u * (uint32_t)s;
@@ -202,7 +202,7 @@ RFP4_DEV void gemv_body(const GemvArgs &a)
         }
     } else {
         // any K: one slice at a time
-        stage_x(xs, a.x, a.k, a.norm_w, a.eps);
+        stage_x(xs, a.x, a.k, a.norm_w, a.eps, a.norm_bf16 != 0);
         for (uint32_t c = (uint32_t)lane; c < nchunk; c += 64u) {
             uint4 q[NP];
             float sc[NP];

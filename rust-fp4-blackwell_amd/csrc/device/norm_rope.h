@@ -80,7 +80,7 @@ RFP4_DEV void rope_append_body(const RopeAppendArgs &a)
     }
 }
 
-// x[i] = embed[ids[step]][i] (fp16 -> f32): llama_run/src/main.rs:509-510,
+// x[i] = embed[ids[step]][i] (fp16 or bf16 -> f32): llama_run/src/main.rs:509-510,
 // but gathered on the device so no per-token host upload is needed.
 RFP4_DEV void embed_body(const EmbedArgs &a)
 {
@@ -88,5 +88,5 @@ RFP4_DEV void embed_body(const EmbedArgs &a)
     if (tok >= a.vocab) tok = 0;
     const uint16_t *row = a.embed + (size_t)tok * a.dim;
     for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < a.dim; i += gridDim.x * blockDim.x)
-        a.x[i] = f16_bits_to_f32(row[i]);
+        a.x[i] = half_bits_to_f32(row[i], a.bf16 != 0);
 }

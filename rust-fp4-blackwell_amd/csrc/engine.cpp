@@ -21,6 +21,7 @@
 #include <vector>
 
 #include "runtime.h"
+#include "safetensors.h"
 
 using namespace rfp4;
 
@@ -54,6 +55,7 @@ struct llama_engine {
     StepState *state = nullptr;
     uint32_t *ids = nullptr, *last_tok = nullptr;
     uint32_t ids_alloc = 0;
+    uint32_t half_bf16 = 0; // norms and embeddings hold bf16 (1) or fp16 (0) bits
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
     bool use_graph = true;
@@ -102,13 +104,14 @@ static int enqueue_step(llama_engine *e)
     hipStream_t s = e->stream;
     const uint32_t qd = qdim(c), kvd = kvdim(c), hd = c.head_dim;
     int rc;
-    EmbedArgs ea{e->embed, e->ids, e->state, e->x, c.dim, c.vocab};
+    EmbedArgs ea{e->embed, e->ids, e->state, e->x, c.dim, c.vocab, e->half_bf16};
     if ((rc = launch("rfp4_embed", dim3((c.dim + 255) / 256), dim3(256), s, &ea))) return rc;
     for (uint32_t l = 0; l < c.n_layers; l++) {
         const LayerW &w = e->L[l];
         uint16_t *kc = e->kcache + (size_t)l * c.n_kv_heads * e->max_seq_alloc * hd;
         uint16_t *vc = e->vcache + (size_t)l * c.n_kv_heads * e->max_seq_alloc * hd;
-        GemvArgs qa{w.qkv_c, w.qkv_s, e->x, e->qkv, nullptr, e->norm_attn + (size_t)l * c.dim, qd + 2 * kvd, c.dim, 0, c.eps};
+        GemvArgs qa{w.qkv_c, w.qkv_s, e->x, e->qkv, nullptr, e->norm_attn + (size_t)l * c.dim, qd + 2 * kvd, c.dim, 0, c.eps,
+                    e->half_bf16};
         if ((rc = gemv_launch("e8m0", RFP4_EPI_STORE, qa, s, 0))) return rc;
         AttnArgs aa{};
         aa.q = e->qkv; aa.kc = kc; aa.vc = vc; aa.out = e->attn_out;
@@ -118,14 +121,15 @@ static int enqueue_step(llama_engine *e)
         aa.n_heads = c.n_heads; aa.n_kv_heads = c.n_kv_heads; aa.head_dim = hd; aa.seq = 0;
         aa.chunk = e->attn_chunk; aa.max_splits = e->attn_max_splits;
         if ((rc = attn_launch(aa, 1, s, e->attn_chunk * e->attn_max_splits, 1))) return rc;
-        GemvArgs oa{w.o_c, w.o_s, e->attn_out, e->x, nullptr, nullptr, c.dim, qd, 0, 0.0f};
+        GemvArgs oa{w.o_c, w.o_s, e->attn_out, e->x, nullptr, nullptr, c.dim, qd, 0, 0.0f, 0};
         if ((rc = gemv_launch("e8m0", RFP4_EPI_RESIDUAL, oa, s, 0))) return rc;
-        GemvArgs ga{w.gu_c, w.gu_s, e->x, e->sw, nullptr, e->norm_ffn + (size_t)l * c.dim, c.ffn, c.dim, c.ffn, c.eps};
+        GemvArgs ga{w.gu_c, w.gu_s, e->x, e->sw, nullptr, e->norm_ffn + (size_t)l * c.dim, c.ffn, c.dim, c.ffn, c.eps,
+                    e->half_bf16};
         if ((rc = gemv_launch("e8m0", RFP4_EPI_SWIGLU, ga, s, 0))) return rc;
-        GemvArgs da{w.d_c, w.d_s, e->sw, e->x, nullptr, nullptr, c.dim, c.ffn, 0, 0.0f};
+        GemvArgs da{w.d_c, w.d_s, e->sw, e->x, nullptr, nullptr, c.dim, c.ffn, 0, 0.0f, 0};
         if ((rc = gemv_launch("e8m0", RFP4_EPI_RESIDUAL, da, s, 0))) return rc;
     }
-    GemvArgs la{e->lm_c, e->lm_s, e->x, e->logits, e->best, e->norm_final, c.vocab, c.dim, 0, c.eps};
+    GemvArgs la{e->lm_c, e->lm_s, e->x, e->logits, e->best, e->norm_final, c.vocab, c.dim, 0, c.eps, e->half_bf16};
     if ((rc = gemv_launch("e8m0", RFP4_EPI_ARGMAX, la, s, 0))) return rc;
     StepArgs sa{e->best, e->state, e->ids, e->last_tok, e->n_best, 0};
     return launch("rfp4_step", dim3(1), dim3(1024), s, &sa);
@@ -180,6 +184,7 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
     int rc;
     RowsArgs ea{};
     ea.ids = e->pf_ids; ea.embed = e->embed; ea.y = e->pf_x; ea.rows = n; ea.k = c.dim; ea.vocab = c.vocab;
+    ea.bf16 = e->half_bf16;
     if ((rc = launch("rfp4_embed_rows", dim3(n), dim3(256), s, &ea))) return rc;
     for (uint32_t l = 0; l < c.n_layers; l++) {
         const LayerW &w = e->L[l];
@@ -187,7 +192,7 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
         uint16_t *vc = e->vcache + (size_t)l * c.n_kv_heads * e->max_seq_alloc * hd;
         RowsArgs na{};
         na.x = e->pf_x; na.w = e->norm_attn + (size_t)l * c.dim; na.codes = e->pf_codes; na.scales = e->pf_scales;
-        na.rows = n; na.k = c.dim; na.eps = c.eps;
+        na.rows = n; na.k = c.dim; na.eps = c.eps; na.bf16 = e->half_bf16;
         if ((rc = launch("rfp4_rmsnorm_quant_rows", dim3(n), dim3(256), s, &na, c.dim * 4u))) return rc;
         if ((rc = fp4_gemm(s, n, nqkv, c.dim, e->pf_codes, e->pf_scales, w.qkv_c, w.qkv_s, e->pf_c))) return rc;
         RopeRowsArgs ra{};
@@ -218,7 +223,8 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
     // last row: the decode step's final norm + LM head, then argmax
     rc = hip_check(hipMemcpyAsync(e->x, e->pf_x + (size_t)(n - 1) * c.dim, c.dim * sizeof(float),
                                   hipMemcpyDeviceToDevice, s), "hipMemcpyAsync(prefill row)");
-    if (!rc) rc = mx4_gemv_rmsnorm(s, c.vocab, c.dim, e->lm_c, e->lm_s, e->x, e->norm_final, c.eps, e->logits);
+    GemvArgs la{e->lm_c, e->lm_s, e->x, e->logits, nullptr, e->norm_final, c.vocab, c.dim, 0, c.eps, e->half_bf16};
+    if (!rc) rc = gemv_launch("e8m0", RFP4_EPI_STORE, la, s, 0);
     if (!rc) rc = argmax(s, c.vocab, e->logits, e->last_tok);
     return rc;
 }
@@ -250,11 +256,12 @@ static void engine_free(llama_engine *e)
     delete e;
 }
 
-extern "C" {
-
-int llama_engine_create(const rfp4_model_config *cfg, uint64_t seed, llama_engine **out)
+// ---------------------------------------------------------------- creation
+// Device memory of an engine for `cfg` (weights unfilled), KV caches zeroed,
+// RoPE tables, activations and workspaces.
+static int engine_alloc(const rfp4_model_config *cfg, llama_engine **out)
 {
-    if (!cfg || !out) return set_error(RFP4_E_INVALID, "llama_engine_create: null argument");
+    if (!cfg || !out) return set_error(RFP4_E_INVALID, "llama_engine: null argument");
     *out = nullptr;
     Runtime *rt = runtime();
     if (!rt) return set_error(RFP4_E_NOT_INIT, "rfp4_init has not been called");
@@ -271,7 +278,6 @@ int llama_engine_create(const rfp4_model_config *cfg, uint64_t seed, llama_engin
     e->max_seq_alloc = (e->attn_chunk * e->attn_max_splits + 255u) / 256u * 256u;
     hipStream_t s = e->stream;
     e->L.resize(c.n_layers);
-    const float sigma = 0.02f;
     for (uint32_t l = 0; l < c.n_layers && !rc; l++) {
         LayerW &w = e->L[l];
         uint32_t nqkv = qd + 2 * kvd;
@@ -283,32 +289,13 @@ int llama_engine_create(const rfp4_model_config *cfg, uint64_t seed, llama_engin
         if (!rc) rc = dalloc_t(e, &w.gu_s, (size_t)2 * c.ffn * c.dim / 32);
         if (!rc) rc = dalloc_t(e, &w.d_c, (size_t)c.dim * c.ffn / 2);
         if (!rc) rc = dalloc_t(e, &w.d_s, (size_t)c.dim * c.ffn / 32);
-        if (rc) break;
-        // q, k, v stacked; each keeps its own stream and local row index
-        rc = rfp4_synth_mx_weight(s, seed, stream_w(l, 0), sigma, c.dim, 0, qd, w.qkv_c, w.qkv_s);
-        if (!rc) rc = rfp4_synth_mx_weight(s, seed, stream_w(l, 1), sigma, c.dim, 0, kvd, w.qkv_c + (size_t)qd * c.dim / 2,
-                                           w.qkv_s + (size_t)qd * c.dim / 32);
-        if (!rc) rc = rfp4_synth_mx_weight(s, seed, stream_w(l, 2), sigma, c.dim, 0, kvd,
-                                           w.qkv_c + (size_t)(qd + kvd) * c.dim / 2, w.qkv_s + (size_t)(qd + kvd) * c.dim / 32);
-        if (!rc) rc = rfp4_synth_mx_weight(s, seed, stream_w(l, 3), sigma, qd, 0, c.dim, w.o_c, w.o_s);
-        if (!rc) rc = rfp4_synth_mx_weight(s, seed, stream_w(l, 4), sigma, c.dim, 0, c.ffn, w.gu_c, w.gu_s);
-        if (!rc) rc = rfp4_synth_mx_weight(s, seed, stream_w(l, 5), sigma, c.dim, 0, c.ffn,
-                                           w.gu_c + (size_t)c.ffn * c.dim / 2, w.gu_s + (size_t)c.ffn * c.dim / 32);
-        if (!rc) rc = rfp4_synth_mx_weight(s, seed, stream_w(l, 6), sigma, c.ffn, 0, c.dim, w.d_c, w.d_s);
     }
     if (!rc) rc = dalloc_t(e, &e->norm_attn, (size_t)c.n_layers * c.dim);
     if (!rc) rc = dalloc_t(e, &e->norm_ffn, (size_t)c.n_layers * c.dim);
     if (!rc) rc = dalloc_t(e, &e->norm_final, c.dim);
-    for (uint32_t l = 0; l < c.n_layers && !rc; l++) {
-        rc = rfp4_synth_f16(s, seed, stream_norm(l, 0), sigma, 1.0f, c.dim, e->norm_attn + (size_t)l * c.dim);
-        if (!rc) rc = rfp4_synth_f16(s, seed, stream_norm(l, 1), sigma, 1.0f, c.dim, e->norm_ffn + (size_t)l * c.dim);
-    }
-    if (!rc) rc = rfp4_synth_f16(s, seed, kStreamNormFinal, sigma, 1.0f, c.dim, e->norm_final);
     if (!rc) rc = dalloc_t(e, &e->embed, (size_t)c.vocab * c.dim);
-    if (!rc) rc = rfp4_synth_f16(s, seed, kStreamEmbed, sigma, 0.0f, (size_t)c.vocab * c.dim, e->embed);
     if (!rc) rc = dalloc_t(e, &e->lm_c, (size_t)c.vocab * c.dim / 2);
     if (!rc) rc = dalloc_t(e, &e->lm_s, (size_t)c.vocab * c.dim / 32);
-    if (!rc) rc = rfp4_synth_mx_weight(s, seed, kStreamLm, sigma, c.dim, 0, c.vocab, e->lm_c, e->lm_s);
     size_t kv_elems = (size_t)c.n_layers * c.n_kv_heads * e->max_seq_alloc * hd;
     if (!rc) rc = dalloc_t(e, &e->kcache, kv_elems);
     if (!rc) rc = dalloc_t(e, &e->vcache, kv_elems);
@@ -328,6 +315,8 @@ int llama_engine_create(const rfp4_model_config *cfg, uint64_t seed, llama_engin
     if (!rc) rc = dalloc_t(e, &e->sin_tab, sinv.size());
     if (!rc) rc = hip_check(hipMemcpyAsync(e->cos_tab, cosv.data(), cosv.size() * 4, hipMemcpyHostToDevice, s), "H2D cos");
     if (!rc) rc = hip_check(hipMemcpyAsync(e->sin_tab, sinv.data(), sinv.size() * 4, hipMemcpyHostToDevice, s), "H2D sin");
+    // the host tables are freed on return: wait for the copies
+    if (!rc) rc = hip_check(hipStreamSynchronize(s), "hipStreamSynchronize(tables)");
     // activations and workspaces
     uint32_t big = c.dim > qd ? c.dim : qd;
     if (!rc) rc = dalloc_t(e, &e->x, c.dim);
@@ -345,8 +334,229 @@ int llama_engine_create(const rfp4_model_config *cfg, uint64_t seed, llama_engin
     if (!rc) rc = dalloc_t(e, &e->last_tok, 1);
     if (!rc) rc = fill_words((uint32_t *)e->state, sizeof(StepState) / 4, 0u, s);
     if (!rc) rc = fill_words(e->ids, e->ids_alloc, 0u, s);
-    if (!rc) rc = hip_check(hipStreamSynchronize(s), "hipStreamSynchronize(create)");
+    if (rc) {
+        engine_free(e);
+        return rc;
+    }
+    *out = e;
+    return RFP4_OK;
+}
+
+// Synthetic MXFP4 init from `seed` (generated on the device; the CPU oracle
+// uses the same counters).
+static int engine_synth(llama_engine *e, uint64_t seed)
+{
+    const rfp4_model_config &c = e->c;
+    const uint32_t qd = qdim(c), kvd = kvdim(c);
+    hipStream_t s = e->stream;
+    const float sigma = 0.02f;
+    int rc = RFP4_OK;
+    for (uint32_t l = 0; l < c.n_layers && !rc; l++) {
+        LayerW &w = e->L[l];
+        // q, k, v stacked; each keeps its own stream and local row index
+        rc = rfp4_synth_mx_weight(s, seed, stream_w(l, 0), sigma, c.dim, 0, qd, w.qkv_c, w.qkv_s);
+        if (!rc) rc = rfp4_synth_mx_weight(s, seed, stream_w(l, 1), sigma, c.dim, 0, kvd, w.qkv_c + (size_t)qd * c.dim / 2,
+                                           w.qkv_s + (size_t)qd * c.dim / 32);
+        if (!rc) rc = rfp4_synth_mx_weight(s, seed, stream_w(l, 2), sigma, c.dim, 0, kvd,
+                                           w.qkv_c + (size_t)(qd + kvd) * c.dim / 2, w.qkv_s + (size_t)(qd + kvd) * c.dim / 32);
+        if (!rc) rc = rfp4_synth_mx_weight(s, seed, stream_w(l, 3), sigma, qd, 0, c.dim, w.o_c, w.o_s);
+        if (!rc) rc = rfp4_synth_mx_weight(s, seed, stream_w(l, 4), sigma, c.dim, 0, c.ffn, w.gu_c, w.gu_s);
+        if (!rc) rc = rfp4_synth_mx_weight(s, seed, stream_w(l, 5), sigma, c.dim, 0, c.ffn,
+                                           w.gu_c + (size_t)c.ffn * c.dim / 2, w.gu_s + (size_t)c.ffn * c.dim / 32);
+        if (!rc) rc = rfp4_synth_mx_weight(s, seed, stream_w(l, 6), sigma, c.ffn, 0, c.dim, w.d_c, w.d_s);
+    }
+    for (uint32_t l = 0; l < c.n_layers && !rc; l++) {
+        rc = rfp4_synth_f16(s, seed, stream_norm(l, 0), sigma, 1.0f, c.dim, e->norm_attn + (size_t)l * c.dim);
+        if (!rc) rc = rfp4_synth_f16(s, seed, stream_norm(l, 1), sigma, 1.0f, c.dim, e->norm_ffn + (size_t)l * c.dim);
+    }
+    if (!rc) rc = rfp4_synth_f16(s, seed, kStreamNormFinal, sigma, 1.0f, c.dim, e->norm_final);
+    if (!rc) rc = rfp4_synth_f16(s, seed, kStreamEmbed, sigma, 0.0f, (size_t)c.vocab * c.dim, e->embed);
+    if (!rc) rc = rfp4_synth_mx_weight(s, seed, kStreamLm, sigma, c.dim, 0, c.vocab, e->lm_c, e->lm_s);
+    e->half_bf16 = 0;
+    return rc;
+}
+
+static int engine_finish(llama_engine *e)
+{
+    int rc = hip_check(hipStreamSynchronize(e->stream), "hipStreamSynchronize(create)");
     if (!rc) rc = capture_graph(e);
+    return rc;
+}
+
+// ---------------------------------------------------------------- real weights
+// Checkpoint names of the reference's loader (llama_run/src/main.rs:444-460).
+static const char *kProjNames[7] = {"self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight",
+                                    "self_attn.o_proj.weight", "mlp.gate_proj.weight",    "mlp.up_proj.weight",
+                                    "mlp.down_proj.weight"};
+
+struct ProjDst {
+    uint8_t *codes, *scales;
+    uint32_t rows, k;
+};
+
+// Where projection p of layer l lives in the engine (q, k, v stacked; gate, up stacked).
+static ProjDst proj_dst(llama_engine *e, uint32_t l, int p)
+{
+    const rfp4_model_config &c = e->c;
+    const uint32_t qd = qdim(c), kvd = kvdim(c);
+    LayerW &w = e->L[l];
+    switch (p) {
+    case 0: return {w.qkv_c, w.qkv_s, qd, c.dim};
+    case 1: return {w.qkv_c + (size_t)qd * c.dim / 2, w.qkv_s + (size_t)qd * c.dim / 32, kvd, c.dim};
+    case 2: return {w.qkv_c + (size_t)(qd + kvd) * c.dim / 2, w.qkv_s + (size_t)(qd + kvd) * c.dim / 32, kvd, c.dim};
+    case 3: return {w.o_c, w.o_s, c.dim, qd};
+    case 4: return {w.gu_c, w.gu_s, c.ffn, c.dim};
+    case 5: return {w.gu_c + (size_t)c.ffn * c.dim / 2, w.gu_s + (size_t)c.ffn * c.dim / 32, c.ffn, c.dim};
+    default: return {w.d_c, w.d_s, c.dim, c.ffn};
+    }
+}
+
+static int st_tensor(const StFile &f, const std::string &name, uint64_t d0, uint64_t d1, const StTensor **out)
+{
+    const StTensor *t = f.find(name);
+    if (!t) return set_error(RFP4_E_SHAPE, "checkpoint has no tensor %s", name.c_str());
+    const bool ok = d1 ? (t->shape.size() == 2 && t->shape[0] == d0 && t->shape[1] == d1)
+                       : (t->shape.size() == 1 && t->shape[0] == d0);
+    if (!ok) {
+        std::string sh;
+        for (uint64_t d : t->shape) sh += (sh.empty() ? "" : "x") + std::to_string(d);
+        return set_error(RFP4_E_SHAPE, "%s has shape [%s], the config needs [%llu%s%s]", name.c_str(), sh.c_str(),
+                         (unsigned long long)d0, d1 ? "x" : "", d1 ? std::to_string(d1).c_str() : "");
+    }
+    if (t->dtype != "BF16" && t->dtype != "F16" && t->dtype != "F32")
+        return set_error(RFP4_E_SHAPE, "%s has dtype %s (BF16, F16 or F32 expected)", name.c_str(), t->dtype.c_str());
+    *out = t;
+    return RFP4_OK;
+}
+
+// One [rows][k] checkpoint matrix -> MXFP4 (OCP rules, E8M0 per 32) with the
+// device quantizer; bf16 and f32 rows go up as stored, f16 rows widened first.
+static int load_proj(llama_engine *e, const StFile &f, const StTensor &t, uint8_t *codes, uint8_t *scales, void *stage)
+{
+    hipStream_t s = e->stream;
+    const uint64_t rows = t.shape[0], k = t.shape[1], n = rows * k;
+    int rc;
+    if (t.dtype == "F16") {
+        std::vector<float> tmp(n);
+        rc = f.read_f32(t, tmp.data(), n);
+        if (!rc) rc = hip_check(hipMemcpy(stage, tmp.data(), n * 4, hipMemcpyHostToDevice), "H2D checkpoint");
+        if (!rc) rc = mx4_quantize(s, rows, k, stage, 0, codes, scales);
+    } else {
+        const bool bf16 = t.dtype == "BF16";
+        rc = hip_check(hipMemcpy(stage, f.data(t), n * (bf16 ? 2 : 4), hipMemcpyHostToDevice), "H2D checkpoint");
+        if (!rc) rc = mx4_quantize(s, rows, k, stage, bf16 ? 1 : 0, codes, scales);
+    }
+    // the next tensor reuses the staging buffer
+    if (!rc) rc = hip_check(hipStreamSynchronize(s), "hipStreamSynchronize(load)");
+    return rc;
+}
+
+// A norm or embedding tensor as 16-bit bits in the engine's format: copied as
+// stored when it already is that format, else rounded to bf16 (RNE).
+static int load_half(llama_engine *e, const StFile &f, const StTensor &t, uint16_t *dst)
+{
+    const uint64_t n = t.numel();
+    const bool same = (e->half_bf16 && t.dtype == "BF16") || (!e->half_bf16 && t.dtype == "F16");
+    if (same) return hip_check(hipMemcpy(dst, f.data(t), n * 2, hipMemcpyHostToDevice), "H2D checkpoint");
+    std::vector<float> tmp(n);
+    int rc = f.read_f32(t, tmp.data(), n);
+    if (rc) return rc;
+    std::vector<uint16_t> h(n);
+    for (uint64_t i = 0; i < n; i++) h[i] = f32_to_bf16_rne_host(tmp[i]);
+    return hip_check(hipMemcpy(dst, h.data(), n * 2, hipMemcpyHostToDevice), "H2D checkpoint");
+}
+
+static int engine_load_safetensors(llama_engine *e, const char *path)
+{
+    const rfp4_model_config &c = e->c;
+    const uint32_t qd = qdim(c), kvd = kvdim(c);
+    StFile f;
+    int rc = f.open(path);
+    if (rc) return rc;
+    // every tensor present with the configured shape before any upload
+    const uint64_t pshape[7][2] = {{qd, c.dim}, {kvd, c.dim}, {kvd, c.dim}, {c.dim, qd},
+                                   {c.ffn, c.dim}, {c.ffn, c.dim}, {c.dim, c.ffn}};
+    std::vector<const StTensor *> proj((size_t)c.n_layers * 7), na(c.n_layers), nf(c.n_layers);
+    for (uint32_t l = 0; l < c.n_layers && !rc; l++) {
+        const std::string pre = "model.layers." + std::to_string(l) + ".";
+        for (int p = 0; p < 7 && !rc; p++) rc = st_tensor(f, pre + kProjNames[p], pshape[p][0], pshape[p][1], &proj[l * 7 + p]);
+        if (!rc) rc = st_tensor(f, pre + "input_layernorm.weight", c.dim, 0, &na[l]);
+        if (!rc) rc = st_tensor(f, pre + "post_attention_layernorm.weight", c.dim, 0, &nf[l]);
+    }
+    const StTensor *fin = nullptr, *emb = nullptr, *lm = nullptr;
+    if (!rc) rc = st_tensor(f, "model.norm.weight", c.dim, 0, &fin);
+    if (!rc) rc = st_tensor(f, "model.embed_tokens.weight", c.vocab, c.dim, &emb);
+    // a checkpoint with tied embeddings has no lm_head.weight
+    if (!rc) rc = f.find("lm_head.weight") ? st_tensor(f, "lm_head.weight", c.vocab, c.dim, &lm) : RFP4_OK;
+    if (rc) return rc;
+    if (!lm) lm = emb;
+
+    // norms and embeddings: bf16 unless every one of them is stored as f16
+    bool all_f16 = fin->dtype == "F16" && emb->dtype == "F16";
+    for (uint32_t l = 0; l < c.n_layers; l++) all_f16 = all_f16 && na[l]->dtype == "F16" && nf[l]->dtype == "F16";
+    e->half_bf16 = all_f16 ? 0u : 1u;
+
+    size_t stage_bytes = 0;
+    for (const StTensor *t : proj) stage_bytes = std::max<size_t>(stage_bytes, t->numel() * 4);
+    stage_bytes = std::max<size_t>(stage_bytes, lm->numel() * 4);
+    void *stage = nullptr;
+    rc = hip_check(hipMalloc(&stage, stage_bytes), "hipMalloc(checkpoint staging)");
+    for (uint32_t l = 0; l < c.n_layers && !rc; l++)
+        for (int p = 0; p < 7 && !rc; p++) {
+            ProjDst d = proj_dst(e, l, p);
+            rc = load_proj(e, f, *proj[l * 7 + p], d.codes, d.scales, stage);
+        }
+    if (!rc) rc = load_proj(e, f, *lm, e->lm_c, e->lm_s, stage);
+    if (stage) hipFree(stage);
+    for (uint32_t l = 0; l < c.n_layers && !rc; l++) {
+        rc = load_half(e, f, *na[l], e->norm_attn + (size_t)l * c.dim);
+        if (!rc) rc = load_half(e, f, *nf[l], e->norm_ffn + (size_t)l * c.dim);
+    }
+    if (!rc) rc = load_half(e, f, *fin, e->norm_final);
+    if (!rc) rc = load_half(e, f, *emb, e->embed);
+    return rc;
+}
+
+// ---------------------------------------------------------------- packed cache
+// File: "RFP4PACK", u32 version, u32 half_bf16, rfp4_model_config, u32 count,
+// then `count` blobs (u64 bytes + bytes) in engine_blobs order.
+static const char kPackMagic[8] = {'R', 'F', 'P', '4', 'P', 'A', 'C', 'K'};
+static const uint32_t kPackVersion = 1;
+
+static std::vector<std::pair<void *, size_t>> engine_blobs(llama_engine *e)
+{
+    const rfp4_model_config &c = e->c;
+    const uint32_t qd = qdim(c), kvd = kvdim(c), nqkv = qd + 2 * kvd;
+    std::vector<std::pair<void *, size_t>> b;
+    for (uint32_t l = 0; l < c.n_layers; l++) {
+        LayerW &w = e->L[l];
+        b.push_back({w.qkv_c, (size_t)nqkv * c.dim / 2});
+        b.push_back({w.qkv_s, (size_t)nqkv * c.dim / 32});
+        b.push_back({w.o_c, (size_t)c.dim * qd / 2});
+        b.push_back({w.o_s, (size_t)c.dim * qd / 32});
+        b.push_back({w.gu_c, (size_t)2 * c.ffn * c.dim / 2});
+        b.push_back({w.gu_s, (size_t)2 * c.ffn * c.dim / 32});
+        b.push_back({w.d_c, (size_t)c.dim * c.ffn / 2});
+        b.push_back({w.d_s, (size_t)c.dim * c.ffn / 32});
+    }
+    b.push_back({e->norm_attn, (size_t)c.n_layers * c.dim * 2});
+    b.push_back({e->norm_ffn, (size_t)c.n_layers * c.dim * 2});
+    b.push_back({e->norm_final, (size_t)c.dim * 2});
+    b.push_back({e->embed, (size_t)c.vocab * c.dim * 2});
+    b.push_back({e->lm_c, (size_t)c.vocab * c.dim / 2});
+    b.push_back({e->lm_s, (size_t)c.vocab * c.dim / 32});
+    return b;
+}
+
+extern "C" {
+
+int llama_engine_create(const rfp4_model_config *cfg, uint64_t seed, llama_engine **out)
+{
+    llama_engine *e = nullptr;
+    int rc = engine_alloc(cfg, &e);
+    if (rc) return rc;
+    rc = engine_synth(e, seed);
+    if (!rc) rc = engine_finish(e);
     if (rc) {
         engine_free(e);
         return rc;
@@ -539,6 +749,104 @@ int llama_engine_prefill(llama_engine *e, const uint32_t *prompt, uint32_t n_pro
     if (!rc) rc = hip_check(hipStreamSynchronize(e->stream), "hipStreamSynchronize");
     if (!rc) *next_token = tok;
     return rc;
+}
+
+int llama_engine_create_from_safetensors(const rfp4_model_config *cfg, const char *path, llama_engine **out)
+{
+    if (!path) return set_error(RFP4_E_INVALID, "llama_engine_create_from_safetensors: null path");
+    llama_engine *e = nullptr;
+    int rc = engine_alloc(cfg, &e);
+    if (rc) return rc;
+    rc = engine_load_safetensors(e, path);
+    if (!rc) rc = engine_finish(e);
+    if (rc) {
+        engine_free(e);
+        return rc;
+    }
+    *out = e;
+    return RFP4_OK;
+}
+
+int llama_engine_save(llama_engine *e, const char *path)
+{
+    if (!e || !path) return set_error(RFP4_E_INVALID, "llama_engine_save: null argument");
+    FILE *fp = fopen(path, "wb");
+    if (!fp) return set_error(RFP4_E_INVALID, "llama_engine_save: cannot create %s", path);
+    auto blobs = engine_blobs(e);
+    const uint32_t count = (uint32_t)blobs.size();
+    bool ok = fwrite(kPackMagic, 1, 8, fp) == 8 && fwrite(&kPackVersion, 4, 1, fp) == 1 &&
+              fwrite(&e->half_bf16, 4, 1, fp) == 1 && fwrite(&e->c, sizeof(rfp4_model_config), 1, fp) == 1 &&
+              fwrite(&count, 4, 1, fp) == 1;
+    int rc = hip_check(hipStreamSynchronize(e->stream), "hipStreamSynchronize(save)");
+    std::vector<uint8_t> host;
+    for (size_t i = 0; i < blobs.size() && ok && !rc; i++) {
+        const uint64_t n = blobs[i].second;
+        host.resize(n);
+        rc = hip_check(hipMemcpy(host.data(), blobs[i].first, n, hipMemcpyDeviceToHost), "D2H save");
+        ok = !rc && fwrite(&n, 8, 1, fp) == 1 && fwrite(host.data(), 1, n, fp) == n;
+    }
+    if (fclose(fp) != 0) ok = false;
+    if (rc) return rc;
+    if (!ok) return set_error(RFP4_E_INVALID, "llama_engine_save: write to %s failed", path);
+    return RFP4_OK;
+}
+
+int llama_engine_load(const char *path, uint32_t max_seq, llama_engine **out)
+{
+    if (!path || !out) return set_error(RFP4_E_INVALID, "llama_engine_load: null argument");
+    *out = nullptr;
+    FILE *fp = fopen(path, "rb");
+    if (!fp) return set_error(RFP4_E_INVALID, "llama_engine_load: cannot open %s", path);
+    char magic[8];
+    uint32_t version = 0, half = 0, count = 0;
+    rfp4_model_config cfg{};
+    bool ok = fread(magic, 1, 8, fp) == 8 && memcmp(magic, kPackMagic, 8) == 0 && fread(&version, 4, 1, fp) == 1 &&
+              version == kPackVersion && fread(&half, 4, 1, fp) == 1 && half <= 1 &&
+              fread(&cfg, sizeof cfg, 1, fp) == 1 && fread(&count, 4, 1, fp) == 1;
+    if (!ok) {
+        fclose(fp);
+        return set_error(RFP4_E_SHAPE, "llama_engine_load: %s is not a packed engine (version %u)", path, kPackVersion);
+    }
+    cfg.max_seq = max_seq;
+    llama_engine *e = nullptr;
+    int rc = engine_alloc(&cfg, &e);
+    if (rc) {
+        fclose(fp);
+        return rc;
+    }
+    e->half_bf16 = half;
+    auto blobs = engine_blobs(e);
+    if (count != blobs.size()) rc = set_error(RFP4_E_SHAPE, "llama_engine_load: %u blobs, the config needs %zu", count, blobs.size());
+    std::vector<uint8_t> host;
+    for (size_t i = 0; i < blobs.size() && !rc; i++) {
+        uint64_t n = 0;
+        if (fread(&n, 8, 1, fp) != 1 || n != blobs[i].second) {
+            rc = set_error(RFP4_E_SHAPE, "llama_engine_load: blob %zu has the wrong size", i);
+            break;
+        }
+        host.resize(n);
+        if (fread(host.data(), 1, n, fp) != n) {
+            rc = set_error(RFP4_E_SHAPE, "llama_engine_load: %s is truncated", path);
+            break;
+        }
+        rc = hip_check(hipMemcpy(blobs[i].first, host.data(), n, hipMemcpyHostToDevice), "H2D load");
+    }
+    fclose(fp);
+    if (!rc) rc = engine_finish(e);
+    if (rc) {
+        engine_free(e);
+        return rc;
+    }
+    *out = e;
+    return RFP4_OK;
+}
+
+int llama_engine_info(const llama_engine *e, rfp4_model_config *cfg, int *half_bf16)
+{
+    if (!e) return set_error(RFP4_E_INVALID, "llama_engine_info: null engine");
+    if (cfg) *cfg = e->c;
+    if (half_bf16) *half_bf16 = (int)e->half_bf16;
+    return RFP4_OK;
 }
 
 uint64_t llama_engine_weight_bytes(const llama_engine *e)

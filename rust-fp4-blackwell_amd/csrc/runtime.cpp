@@ -3,6 +3,8 @@
 // (include/rfp4.h) over hipModuleLaunchKernel.
 #include "runtime.h"
 
+#include <algorithm>
+#include <cmath>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
@@ -459,7 +461,7 @@ int fp4_gemv(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint32_t *w, co
 {
     int rc = gemv_check(n, k, w, scales, x, y);
     if (rc) return rc;
-    GemvArgs a{w, scales, x, y, nullptr, nullptr, n, k, 0, 0.0f};
+    GemvArgs a{w, scales, x, y, nullptr, nullptr, n, k, 0, 0.0f, 0};
     return gemv_launch("f32", RFP4_EPI_STORE, a, (hipStream_t)stream, 0);
 }
 
@@ -468,7 +470,7 @@ int mx4_gemv(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_t *codes,
 {
     int rc = gemv_check(n, k, codes, scales, x, y);
     if (rc) return rc;
-    GemvArgs a{codes, scales, x, y, nullptr, nullptr, n, k, 0, 0.0f};
+    GemvArgs a{codes, scales, x, y, nullptr, nullptr, n, k, 0, 0.0f, 0};
     return gemv_launch("e8m0", RFP4_EPI_STORE, a, (hipStream_t)stream, 0);
 }
 
@@ -478,7 +480,7 @@ int mx4_gemv_rmsnorm(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_t
     int rc = gemv_check(n, k, codes, scales, x, y);
     if (rc) return rc;
     if (!norm_w) return set_error(RFP4_E_INVALID, "gemv_rmsnorm: null norm weights");
-    GemvArgs a{codes, scales, x, y, nullptr, norm_w, n, k, 0, eps};
+    GemvArgs a{codes, scales, x, y, nullptr, norm_w, n, k, 0, eps, 0};
     return gemv_launch("e8m0", RFP4_EPI_STORE, a, (hipStream_t)stream, 0);
 }
 
@@ -487,7 +489,7 @@ int mx4_gemv_residual(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_
 {
     int rc = gemv_check(n, k, codes, scales, x, x_res);
     if (rc) return rc;
-    GemvArgs a{codes, scales, x, x_res, nullptr, nullptr, n, k, 0, 0.0f};
+    GemvArgs a{codes, scales, x, x_res, nullptr, nullptr, n, k, 0, 0.0f, 0};
     return gemv_launch("e8m0", RFP4_EPI_RESIDUAL, a, (hipStream_t)stream, 0);
 }
 
@@ -497,7 +499,7 @@ int mx4_gemv_swiglu(rfp4_stream_t stream, uint32_t n, uint32_t k, uint32_t pair_
     int rc = gemv_check(n, k, codes, scales, x, out);
     if (rc) return rc;
     if (pair_off < n) return set_error(RFP4_E_SHAPE, "gemv_swiglu: pair_off %u overlaps the %u gate rows", pair_off, n);
-    GemvArgs a{codes, scales, x, out, nullptr, nullptr, n, k, pair_off, 0.0f};
+    GemvArgs a{codes, scales, x, out, nullptr, nullptr, n, k, pair_off, 0.0f, 0};
     return gemv_launch("e8m0", RFP4_EPI_SWIGLU, a, (hipStream_t)stream, 0);
 }
 
@@ -510,7 +512,7 @@ int mx4_gemv_argmax(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_t 
     if (rc) return rc;
     if (!workspace || !best_token) return set_error(RFP4_E_INVALID, "gemv_argmax: null workspace or output");
     unsigned long long *best = (unsigned long long *)workspace;
-    GemvArgs a{codes, scales, x, y, best, nullptr, n, k, 0, 0.0f};
+    GemvArgs a{codes, scales, x, y, best, nullptr, n, k, 0, 0.0f, 0};
     rc = gemv_launch("e8m0", RFP4_EPI_ARGMAX, a, (hipStream_t)stream, 0);
     if (rc) return rc;
     // reduce the per-workgroup keys with the step kernel on a scratch cursor
@@ -533,7 +535,7 @@ int rfp4_debug_gemv_fused(rfp4_stream_t stream, int epi, uint32_t n, uint32_t k,
     if (epi == RFP4_EPI_ARGMAX && (!workspace || !best_token))
         return set_error(RFP4_E_INVALID, "gemv_fused: argmax needs a workspace and an output");
     unsigned long long *best = (unsigned long long *)workspace;
-    GemvArgs a{codes, scales, x, y, best, norm_w, n, k, pair_off, eps};
+    GemvArgs a{codes, scales, x, y, best, norm_w, n, k, pair_off, eps, 0};
     rc = gemv_launch("e8m0", epi, a, (hipStream_t)stream, 0);
     if (rc || epi != RFP4_EPI_ARGMAX) return rc;
     uint32_t nb = gemv_blocks(n, k, RFP4_EPI_ARGMAX);
@@ -653,6 +655,43 @@ int fp4_mma_allones(rfp4_stream_t stream, float *out)
     if (!out) return set_error(RFP4_E_INVALID, "fp4_mma_allones: null pointer");
     MmaTileArgs a{nullptr, nullptr, nullptr, nullptr, out, 0, 0};
     return launch("rfp4_mma_allones", dim3(1), dim3(64), (hipStream_t)stream, &a);
+}
+
+int fp4_quantize_absmax(const float *w, uint32_t rows, uint32_t k, uint32_t *packed, float *scales)
+{
+    // The reference's host packer (llama_run/src/main.rs:334-376): per block of
+    // 32, scale = absmax / 6 (1 for an all-zero block), each value / scale to
+    // the nearest E2M1 magnitude with ties to the smaller one, sign bit for
+    // negative values, 8 codes per word, low nibble first.  Nearest-with-ties-
+    // down is decided here against the midpoints of the magnitude table,
+    // which the reference's scan of |a - level| reproduces exactly: near a
+    // midpoint both differences are exact (Sterbenz), elsewhere they are far
+    // apart.
+    if (!w || !packed || !scales) return set_error(RFP4_E_INVALID, "fp4_quantize_absmax: null pointer");
+    if (rows == 0 || k == 0 || k % 32) return set_error(RFP4_E_SHAPE, "fp4_quantize_absmax: k=%u must be a positive multiple of 32", k);
+    static const float kMid[7] = {0.25f, 0.75f, 1.25f, 1.75f, 2.5f, 3.5f, 5.0f};
+    const uint32_t nb = k / 32;
+    for (uint32_t r = 0; r < rows; r++)
+        for (uint32_t b = 0; b < nb; b++) {
+            const float *x = w + (size_t)r * k + (size_t)b * 32;
+            float amax = 0.0f;
+            for (int i = 0; i < 32; i++) amax = std::max(amax, std::fabs(x[i]));
+            const float scale = amax > 0.0f ? amax / 6.0f : 1.0f;
+            scales[(size_t)r * nb + b] = scale;
+            uint32_t *dst = packed + ((size_t)r * k + (size_t)b * 32) / 8;
+            for (int wd = 0; wd < 4; wd++) {
+                uint32_t word = 0;
+                for (int j = 0; j < 8; j++) {
+                    const float v = x[wd * 8 + j] / scale, a = std::fabs(v);
+                    uint32_t code = 0;
+                    while (code < 7 && a > kMid[code]) code++;
+                    if (v < 0.0f) code |= 8u;
+                    word |= code << (4 * j);
+                }
+                dst[wd] = word;
+            }
+        }
+    return RFP4_OK;
 }
 
 int mx4_quantize(rfp4_stream_t stream, uint64_t rows, uint64_t k, const void *src, int src_is_bf16, uint8_t *codes,

@@ -99,6 +99,17 @@ _SIGS = {
     "llama_engine_create": (I32, [C.POINTER(ModelConfig), U64, C.POINTER(P)]),
     "llama_engine_destroy": (I32, [P]),
     "llama_engine_prefill_kv": (I32, [P, U64, U32]),
+    "llama_engine_create_from_safetensors": (I32, [C.POINTER(ModelConfig), C.c_char_p, C.POINTER(P)]),
+    "llama_engine_save": (I32, [P, C.c_char_p]),
+    "llama_engine_load": (I32, [C.c_char_p, U32, C.POINTER(P)]),
+    "llama_engine_info": (I32, [P, C.POINTER(ModelConfig), C.POINTER(C.c_int)]),
+    "fp4_quantize_absmax": (I32, [P, U32, U32, P, P]),
+    "rfp4_st_open": (I32, [C.c_char_p, C.POINTER(P)]),
+    "rfp4_st_close": (I32, [P]),
+    "rfp4_st_count": (I32, [P, C.POINTER(U32)]),
+    "rfp4_st_name": (I32, [P, U32, C.POINTER(C.c_char_p)]),
+    "rfp4_st_info": (I32, [P, C.c_char_p, C.c_char_p, C.POINTER(U32), P, C.POINTER(U64)]),
+    "rfp4_st_read_f32": (I32, [P, C.c_char_p, P, U64]),
     "llama_engine_prefill": (I32, [P, P, U32, U32, C.POINTER(U32)]),
     "llama_decode_step": (I32, [P, U32, U32, C.POINTER(U32)]),
     "llama_generate": (I32, [P, P, U32, U32, U32, P]),
@@ -405,16 +416,98 @@ def model_config(preset=None, max_seq=2048, **kw) -> ModelConfig:
     return ModelConfig(**d)
 
 
+def fp4_quantize_absmax(w: np.ndarray):
+    """The reference's host packer: (packed u32 [rows*k/8], f32 scales [rows*k/32])."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    rows, k = w.shape
+    packed = np.zeros(rows * k // 8, dtype=np.uint32)
+    scales = np.zeros(rows * k // 32, dtype=np.float32)
+    check(load().fp4_quantize_absmax(w.ctypes.data, rows, k, packed.ctypes.data, scales.ctypes.data))
+    return packed, scales
+
+
+class SafeTensors:
+    """Read-only safetensors view (rfp4_st_*): names, dtype/shape, f32 widening."""
+
+    def __init__(self, path: str):
+        h = P()
+        check(load().rfp4_st_open(os.fsencode(path), C.byref(h)))
+        self.h = h.value
+
+    def close(self):
+        if self.h:
+            check(load().rfp4_st_close(self.h))
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def names(self):
+        n = U32(0)
+        check(load().rfp4_st_count(self.h, C.byref(n)))
+        out = []
+        for i in range(n.value):
+            p = C.c_char_p()
+            check(load().rfp4_st_name(self.h, i, C.byref(p)))
+            out.append(p.value.decode())
+        return out
+
+    def info(self, name: str):
+        dt = C.create_string_buffer(8)
+        nd = U32(0)
+        shape = (U64 * 8)()
+        nb = U64(0)
+        check(load().rfp4_st_info(self.h, name.encode(), dt, C.byref(nd), C.cast(shape, P), C.byref(nb)))
+        return dt.value.decode(), tuple(shape[i] for i in range(nd.value)), nb.value
+
+    def read_f32(self, name: str) -> np.ndarray:
+        _, shape, _ = self.info(name)
+        out = np.empty(int(np.prod(shape)) if shape else 1, dtype=np.float32)
+        check(load().rfp4_st_read_f32(self.h, name.encode(), out.ctypes.data, out.size))
+        return out.reshape(shape)
+
+
 class Engine:
     """llama_engine: weights, fp16 KV and the captured step graph."""
 
-    def __init__(self, cfg: ModelConfig, seed: int):
+    def __init__(self, cfg: ModelConfig, seed: int, _handle=None):
         init()
         self.cfg = cfg
-        h = P()
-        check(load().llama_engine_create(C.byref(cfg), seed, C.byref(h)))
-        self.h = h.value
+        if _handle is None:
+            h = P()
+            check(load().llama_engine_create(C.byref(cfg), seed, C.byref(h)))
+            _handle = h.value
+        self.h = _handle
         self.stream = Stream(load().llama_engine_stream(self.h))
+
+    @classmethod
+    def from_safetensors(cls, cfg: ModelConfig, path: str) -> "Engine":
+        """Real weights from a safetensors checkpoint (MXFP4 by the OCP rules)."""
+        init()
+        h = P()
+        check(load().llama_engine_create_from_safetensors(C.byref(cfg), os.fsencode(path), C.byref(h)))
+        return cls(cfg, 0, _handle=h.value)
+
+    @classmethod
+    def load(cls, path: str, max_seq: int) -> "Engine":
+        """An engine rebuilt from a packed-weight file written by save()."""
+        init()
+        h = P()
+        check(load().llama_engine_load(os.fsencode(path), max_seq, C.byref(h)))
+        cfg = ModelConfig()
+        check(load().llama_engine_info(h.value, C.byref(cfg), None))
+        return cls(cfg, 0, _handle=h.value)
+
+    def save(self, path: str):
+        check(load().llama_engine_save(self.h, os.fsencode(path)))
+
+    def half_bf16(self) -> bool:
+        b = C.c_int(0)
+        check(load().llama_engine_info(self.h, None, C.byref(b)))
+        return bool(b.value)
 
     def prefill_kv(self, seed: int, upto: int):
         check(load().llama_engine_prefill_kv(self.h, seed, upto))
