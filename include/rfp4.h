@@ -187,6 +187,10 @@ int rfp4_mma_tile32(rfp4_stream_t stream, const uint32_t *a, const uint32_t *b, 
  * (rows per wave 2/4/8, up-front K-slices or 0 for the slice loop;
  * 0, -1 = automatic).  No reference counterpart. */
 int rfp4_debug_gemv_variant(int rows_per_wave, int slices);
+/* Test hook: waves per workgroup of later VALU GEMV launches on this thread
+ * (0 = automatic, 4 or 8; 8 exists for one-slice SwiGLU at 1 row per wave and
+ * store at 2).  No reference counterpart. */
+int rfp4_debug_gemv_waves(int waves);
 /* Test hook: GEMV implementation of later launches on this thread: 0 = auto,
  * 1 = VALU kernel, 2 = bf16 matrix-core kernel (rows_per_wave then means
  * 16-row tiles per wave, slices the super-chunks per wave), 3 = block-scaled
@@ -239,9 +243,9 @@ int llama_engine_create(const rfp4_model_config *cfg, uint64_t seed, llama_engin
  * input_layernorm / post_attention_layernorm.weight, model.norm.weight,
  * model.embed_tokens.weight, lm_head.weight or tied embeddings) in BF16, F16
  * or F32, shapes as cfg.  Projections are quantized on the device to MXFP4
- * (OCP rules, E8M0 per 32; mx4_quantize); norms and embeddings stay 16-bit:
- * as stored when every one is BF16 (exact, the reference widens them to
- * f32) or every one is F16, else rounded to bf16. */
+ * (OCP rules, E8M0 per 32; mx4_quantize); norm weights are held as fp16
+ * (exact for bf16 gains of magnitude 2^-17 .. 65504, as the reference's f32
+ * copies), embeddings as stored when BF16 or F16 (F32 rounded to bf16). */
 int llama_engine_create_from_safetensors(const rfp4_model_config *cfg, const char *path, llama_engine **out);
 /* Packed-weight cache (no reference counterpart; the reference re-quantizes
  * at every start): the engine's MXFP4 weights, norms and embeddings with its
@@ -249,8 +253,8 @@ int llama_engine_create_from_safetensors(const rfp4_model_config *cfg, const cha
  * the given max_seq (no quantization on load). */
 int llama_engine_save(llama_engine *e, const char *path);
 int llama_engine_load(const char *path, uint32_t max_seq, llama_engine **out);
-/* The engine's config and norm/embedding format (1 = bf16, 0 = fp16). */
-int llama_engine_info(const llama_engine *e, rfp4_model_config *cfg, int *half_bf16);
+/* The engine's config and embedding format (1 = bf16, 0 = fp16). */
+int llama_engine_info(const llama_engine *e, rfp4_model_config *cfg, int *embed_bf16);
 int llama_engine_destroy(llama_engine *e);
 /* Fill K/V positions [0, upto) of every layer with f16(0.1 * N(0,1))
  * (the pre-filled context of llama_decode/src/main.rs:357,375-376). */
@@ -302,6 +306,10 @@ int rfp4_st_count(const rfp4_st *st, uint32_t *count);
 int rfp4_st_name(const rfp4_st *st, uint32_t i, const char **name);
 int rfp4_st_info(const rfp4_st *st, const char *name, char dtype[8], uint32_t *ndim, uint64_t shape[8], uint64_t *nbytes);
 int rfp4_st_read_f32(const rfp4_st *st, const char *name, float *out, uint64_t count);
+/* The tensor as fp16 bits (no reference counterpart: how the engine stores
+ * norm weights): F16 as stored, BF16 and F32 rounded to nearest even, exact
+ * for bf16 values of magnitude 2^-17 .. 65504. */
+int rfp4_st_read_f16(const rfp4_st *st, const char *name, uint16_t *out, uint64_t count);
 
 #ifdef __cplusplus
 }

@@ -664,7 +664,7 @@ struct orc_model {
     uint16_t *embed;
     uint8_t *lm_codes, *lm_scales;
     uint16_t *kc[64], *vc[64]; /* [kvh][max_seq][hd] */
-    int half_bf16;             /* norms and embeddings hold bf16 (1) or f16 (0) bits */
+    int embed_bf16;            /* embeddings hold bf16 (1) or f16 (0) bits; norms are f16 */
     float *cosv, *sinv;
     /* scratch */
     float *x, *h, *q, *k, *v, *a, *ao, *g, *u, *sw, *d, *logits, *attn_f32_q, *tmpw;
@@ -846,15 +846,20 @@ void orc_model_prefill_kv(orc_model *m, uint64_t seed, uint32_t upto)
     parallel_rows(m->c.n_layers, prefill_layers, &c);
 }
 
-/* Norm weights and embedding rows: f16 (the synthetic init, BASELINE config
- * 3) or bf16 bits of a real checkpoint, widened exactly to f32 as the
- * reference's loader does (llama_run/src/main.rs:425-427). */
-static void widen_half(const orc_model *m, const uint16_t *src, uint32_t n, float *dst)
+/* Norm weights (f16) and embedding rows (f16 for the synthetic init of
+ * BASELINE config 3, or the bf16 bits of a real checkpoint), widened exactly
+ * to f32 as the reference's loader does (llama_run/src/main.rs:425-427). */
+static void widen_f16(const uint16_t *src, uint32_t n, float *dst)
 {
-    for (uint32_t i = 0; i < n; i++) dst[i] = m->half_bf16 ? orc_bf16_to_f32(src[i]) : orc_f16_to_f32(src[i]);
+    for (uint32_t i = 0; i < n; i++) dst[i] = orc_f16_to_f32(src[i]);
 }
 
-void orc_model_set_half_bf16(orc_model *m, int bf16) { m->half_bf16 = bf16 ? 1 : 0; }
+static void widen_embed(const orc_model *m, const uint16_t *src, uint32_t n, float *dst)
+{
+    for (uint32_t i = 0; i < n; i++) dst[i] = m->embed_bf16 ? orc_bf16_to_f32(src[i]) : orc_f16_to_f32(src[i]);
+}
+
+void orc_model_set_embed_bf16(orc_model *m, int bf16) { m->embed_bf16 = bf16 ? 1 : 0; }
 
 /* llama_run/src/main.rs:492-536 */
 uint32_t orc_model_step(orc_model *m, uint32_t tok, uint32_t pos, float *logits)
@@ -863,10 +868,10 @@ uint32_t orc_model_step(orc_model *m, uint32_t tok, uint32_t pos, float *logits)
     uint32_t half = c->head_dim / 2;
     uint32_t qd = c->n_heads * c->head_dim, kvd = c->n_kv_heads * c->head_dim;
     if (pos >= c->max_seq || tok >= c->vocab) return 0xFFFFFFFFu;
-    widen_half(m, m->embed + (size_t)tok * c->dim, c->dim, m->x);
+    widen_embed(m, m->embed + (size_t)tok * c->dim, c->dim, m->x);
     const float *cp = m->cosv + (size_t)pos * half, *sp = m->sinv + (size_t)pos * half;
     for (uint32_t l = 0; l < c->n_layers; l++) {
-        widen_half(m, m->norm_attn[l], c->dim, m->tmpw);
+        widen_f16(m->norm_attn[l], c->dim, m->tmpw);
         orc_rmsnorm(c->dim, c->eps, m->x, m->tmpw, m->h);
         orc_gemv_e8m0(qd, c->dim, m->codes[l][ORC_WQ], m->scales[l][ORC_WQ], m->h, m->q);
         orc_gemv_e8m0(kvd, c->dim, m->codes[l][ORC_WK], m->scales[l][ORC_WK], m->h, m->k);
@@ -883,7 +888,7 @@ uint32_t orc_model_step(orc_model *m, uint32_t tok, uint32_t pos, float *logits)
                             c->head_dim, (size_t)c->max_seq * c->head_dim, m->a);
         orc_gemv_e8m0(c->dim, qd, m->codes[l][ORC_WO], m->scales[l][ORC_WO], m->a, m->ao);
         orc_residual(c->dim, m->ao, m->x);
-        widen_half(m, m->norm_ffn[l], c->dim, m->tmpw);
+        widen_f16(m->norm_ffn[l], c->dim, m->tmpw);
         orc_rmsnorm(c->dim, c->eps, m->x, m->tmpw, m->h);
         orc_gemv_e8m0(c->ffn, c->dim, m->codes[l][ORC_WG], m->scales[l][ORC_WG], m->h, m->g);
         orc_gemv_e8m0(c->ffn, c->dim, m->codes[l][ORC_WU], m->scales[l][ORC_WU], m->h, m->u);
@@ -891,7 +896,7 @@ uint32_t orc_model_step(orc_model *m, uint32_t tok, uint32_t pos, float *logits)
         orc_gemv_e8m0(c->dim, c->ffn, m->codes[l][ORC_WD], m->scales[l][ORC_WD], m->sw, m->d);
         orc_residual(c->dim, m->d, m->x);
     }
-    widen_half(m, m->norm_final, c->dim, m->tmpw);
+    widen_f16(m->norm_final, c->dim, m->tmpw);
     orc_rmsnorm(c->dim, c->eps, m->x, m->tmpw, m->h);
     orc_gemv_e8m0(c->vocab, c->dim, m->lm_codes, m->lm_scales, m->h, m->logits);
     if (logits) memcpy(logits, m->logits, sizeof(float) * c->vocab);
@@ -937,9 +942,9 @@ uint32_t orc_model_prefill(orc_model *m, const uint32_t *prompt, uint32_t n, uin
     float *A = (float *)malloc(sizeof(float) * (size_t)n * qd);
     float *O = (float *)malloc(sizeof(float) * (size_t)n * c->dim);
     float *G = (float *)malloc(sizeof(float) * (size_t)n * c->ffn), *U = (float *)malloc(sizeof(float) * (size_t)n * c->ffn);
-    for (uint32_t i = 0; i < n; i++) widen_half(m, m->embed + (size_t)prompt[i] * c->dim, c->dim, X + (size_t)i * c->dim);
+    for (uint32_t i = 0; i < n; i++) widen_embed(m, m->embed + (size_t)prompt[i] * c->dim, c->dim, X + (size_t)i * c->dim);
     for (uint32_t l = 0; l < c->n_layers; l++) {
-        widen_half(m, m->norm_attn[l], c->dim, m->tmpw);
+        widen_f16(m->norm_attn[l], c->dim, m->tmpw);
         for (uint32_t i = 0; i < n; i++) orc_rmsnorm(c->dim, c->eps, X + (size_t)i * c->dim, m->tmpw, H + (size_t)i * c->dim);
         orc_quant_mx(H, n, c->dim, hc, hs);
         gemm_rows_f32(n, qd, c->dim, hc, hs, m->codes[l][ORC_WQ], m->scales[l][ORC_WQ], Q);
@@ -963,7 +968,7 @@ uint32_t orc_model_prefill(orc_model *m, const uint32_t *prompt, uint32_t n, uin
         orc_quant_mx(A, n, qd, hc, hs);
         gemm_rows_f32(n, c->dim, qd, hc, hs, m->codes[l][ORC_WO], m->scales[l][ORC_WO], O);
         orc_residual(n * c->dim, O, X);
-        widen_half(m, m->norm_ffn[l], c->dim, m->tmpw);
+        widen_f16(m->norm_ffn[l], c->dim, m->tmpw);
         for (uint32_t i = 0; i < n; i++) orc_rmsnorm(c->dim, c->eps, X + (size_t)i * c->dim, m->tmpw, H + (size_t)i * c->dim);
         orc_quant_mx(H, n, c->dim, hc, hs);
         gemm_rows_f32(n, c->ffn, c->dim, hc, hs, m->codes[l][ORC_WG], m->scales[l][ORC_WG], G);
@@ -974,7 +979,7 @@ uint32_t orc_model_prefill(orc_model *m, const uint32_t *prompt, uint32_t n, uin
         orc_residual(n * c->dim, O, X);
     }
     memcpy(m->x, X + (size_t)(n - 1) * c->dim, sizeof(float) * c->dim);
-    widen_half(m, m->norm_final, c->dim, m->tmpw);
+    widen_f16(m->norm_final, c->dim, m->tmpw);
     orc_rmsnorm(c->dim, c->eps, m->x, m->tmpw, m->h);
     orc_gemv_e8m0(c->vocab, c->dim, m->lm_codes, m->lm_scales, m->h, m->logits);
     if (logits) memcpy(logits, m->logits, sizeof(float) * c->vocab);

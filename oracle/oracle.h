@@ -144,8 +144,8 @@ typedef struct orc_model orc_model;
  * generator the device engine uses, so packed bytes are identical. */
 orc_model *orc_model_create(const orc_model_config *cfg, uint64_t seed);
 void orc_model_destroy(orc_model *m);
-/* Norms and embeddings are bf16 bit patterns (a real checkpoint) instead of f16. */
-void orc_model_set_half_bf16(orc_model *m, int bf16);
+/* Embeddings are bf16 bit patterns (a real checkpoint) instead of f16. */
+void orc_model_set_embed_bf16(orc_model *m, int bf16);
 /* Raw views for hashing / comparison against the device engine. */
 uint8_t *orc_model_codes(orc_model *m, int layer, int proj, size_t *bytes);
 uint8_t *orc_model_scales(orc_model *m, int layer, int proj, size_t *bytes);

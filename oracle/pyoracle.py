@@ -45,7 +45,7 @@ _SIGS = {
     "orc_f32_to_bf16": (U16, [F32]),
     "orc_pack_codes": (None, [P, SZ, P]),
     "orc_unpack_codes": (None, [P, SZ, P]),
-    "orc_model_set_half_bf16": (None, [P, I32]),
+    "orc_model_set_embed_bf16": (None, [P, I32]),
     "orc_quant_fp4_absmax": (None, [P, I32, I32, P, P]),
     "orc_quant_mx": (None, [P, SZ, SZ, P, P]),
     "orc_synth_mx_weight": (None, [U64, U64, F32, SZ, SZ, SZ, P, P]),
@@ -289,10 +289,10 @@ class Model:
     _PROJ = ("self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight",
              "self_attn.o_proj.weight", "mlp.gate_proj.weight", "mlp.up_proj.weight", "mlp.down_proj.weight")
 
-    def load_checkpoint(self, f32, half_bits, half_bf16):
+    def load_checkpoint(self, f32, half_bits, embed_bf16):
         """Real weights: f32 (widened checkpoint values, name -> [rows][k]) for
         the projections, quantized by the OCP MX rules; half_bits (name ->
-        uint16 bit patterns) for norms and embeddings, bf16 or f16."""
+        uint16 bit patterns): f16 norms, embeddings bf16 or f16."""
         L = self.cfg["n_layers"]
         for l in range(L):
             for p, name in enumerate(self._PROJ):
@@ -307,7 +307,7 @@ class Model:
         c, s = quant_mx(lm)
         self.codes(-1, 0)[:] = c.reshape(-1)
         self.scales(-1, 0)[:] = s.reshape(-1)
-        lib().orc_model_set_half_bf16(self.h, 1 if half_bf16 else 0)
+        lib().orc_model_set_embed_bf16(self.h, 1 if embed_bf16 else 0)
 
     def kcache(self, layer):
         return self._view(lib().orc_model_kcache, layer, dtype=np.uint16)

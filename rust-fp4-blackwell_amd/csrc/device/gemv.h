@@ -33,7 +33,7 @@ RFP4_DEV float silu_ref(float g)
 
 // Stage x (K floats) into LDS; with norm_w, store x * rms * w instead
 // (rms = 1/sqrt(sum(x^2)/K + eps), llama_rmsnorm/src/main.rs:75-77).
-RFP4_DEV void stage_x(float *xs, const float *x, uint32_t k, const uint16_t *norm_w, float eps, bool wbf16)
+RFP4_DEV void stage_x(float *xs, const float *x, uint32_t k, const uint16_t *norm_w, float eps)
 {
     __shared__ float red[4];
     const int tid = threadIdx.x;
@@ -57,16 +57,17 @@ RFP4_DEV void stage_x(float *xs, const float *x, uint32_t k, const uint16_t *nor
     __syncthreads();
     float total = (red[0] + red[1]) + (red[2] + red[3]);
     float rms = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(total, (float)k), eps)));
-    for (uint32_t i = tid; i < k; i += 256) xs[i] = __fmul_rn(__fmul_rn(xs[i], rms), half_bits_to_f32(norm_w[i], wbf16));
+    for (uint32_t i = tid; i < k; i += 256) xs[i] = __fmul_rn(__fmul_rn(xs[i], rms), f16_bits_to_f32(norm_w[i]));
     __syncthreads();
 }
 
 // stage_x from registers (XV float4 of x and uint2 of fp16 norm weights per
-// thread, element 4*(tid + 256*v) + j, zero past K).
-template <int XV>
-RFP4_DEV void stage_x_regs(float *xs, const float4 *xr, const uint2 *wr, uint32_t k, bool norm, float eps, bool wbf16)
+// thread, element 4*(tid + T*v) + j for T = 64*W threads, zero past K).
+template <int XV, int W = 4>
+RFP4_DEV void stage_x_regs(float *xs, const float4 *xr, const uint2 *wr, uint32_t k, bool norm, float eps)
 {
-    __shared__ float red[4];
+    constexpr uint32_t T = 64u * W;
+    __shared__ float red[W];
     const int tid = threadIdx.x;
     const uint32_t k4 = k >> 2;
     float rms = 1.0f;
@@ -83,18 +84,20 @@ RFP4_DEV void stage_x_regs(float *xs, const float4 *xr, const uint2 *wr, uint32_
         if ((tid & 63) == 0) red[tid >> 6] = ss;
         __syncthreads();
         float total = (red[0] + red[1]) + (red[2] + red[3]);
+#pragma unroll
+        for (int w = 4; w < W; w += 4) total += (red[w] + red[w + 1]) + (red[w + 2] + red[w + 3]);
         rms = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(total, (float)k), eps)));
     }
 #pragma unroll
     for (int v = 0; v < XV; v++) {
-        const uint32_t i4 = (uint32_t)tid + 256u * (uint32_t)v;
+        const uint32_t i4 = (uint32_t)tid + T * (uint32_t)v;
         if (i4 >= k4) break;
         float4 o = xr[v];
         if (norm) {
-            o.x = __fmul_rn(__fmul_rn(o.x, rms), half_bits_to_f32(wr[v].x & 0xFFFFu, wbf16));
-            o.y = __fmul_rn(__fmul_rn(o.y, rms), half_bits_to_f32(wr[v].x >> 16, wbf16));
-            o.z = __fmul_rn(__fmul_rn(o.z, rms), half_bits_to_f32(wr[v].y & 0xFFFFu, wbf16));
-            o.w = __fmul_rn(__fmul_rn(o.w, rms), half_bits_to_f32(wr[v].y >> 16, wbf16));
+            o.x = __fmul_rn(__fmul_rn(o.x, rms), f16_bits_to_f32((uint16_t)(wr[v].x & 0xFFFFu)));
+            o.y = __fmul_rn(__fmul_rn(o.y, rms), f16_bits_to_f32((uint16_t)(wr[v].x >> 16)));
+            o.z = __fmul_rn(__fmul_rn(o.z, rms), f16_bits_to_f32((uint16_t)(wr[v].y & 0xFFFFu)));
+            o.w = __fmul_rn(__fmul_rn(o.w, rms), f16_bits_to_f32((uint16_t)(wr[v].y >> 16)));
         }
         ((float4 *)xs)[i4] = o;
     }
@@ -118,16 +121,21 @@ RFP4_DEV float scale_from_bits(uint32_t b)
 
 // NS: K-slices of 64 chunks (2048 values) per row, fixed at compile time so
 // all loads are issued up front; NS = 0 handles any K with a slice loop.
-template <int SCALE_F32, int EPI, int R, int NS>
+// W: waves per workgroup (4, or 8 / 16 with NS > 0: more, shorter waves
+// share one staging of x).
+template <int SCALE_F32, int EPI, int R, int NS, int W = 4>
 RFP4_DEV void gemv_body(const GemvArgs &a)
 {
+    static_assert(W == 4 || NS > 0, "the slice loop stages x with 4 waves");
+    static_assert(W % 4 == 0 && W <= 16, "waves per workgroup");
     constexpr int NP = (EPI == RFP4_EPI_SWIGLU) ? 2 * R : R;
+    constexpr uint32_t T = 64u * W;
     extern __shared__ float xs[]; // K floats (dynamic LDS)
-    __shared__ unsigned long long s_best[4];
+    __shared__ unsigned long long s_best[W];
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
-    const uint32_t lrow0 = (blockIdx.x * 4u + (uint32_t)wave) * (uint32_t)R;
+    const uint32_t lrow0 = (blockIdx.x * (uint32_t)W + (uint32_t)wave) * (uint32_t)R;
     const uint32_t nchunk = a.k >> 5;
     const size_t rowbytes = (size_t)(a.k >> 1);
 
@@ -165,13 +173,13 @@ RFP4_DEV void gemv_body(const GemvArgs &a)
         // of this wave (NS slices x NP rows): waiting for x then never waits
         // for the weights (vmcnt retires in issue order).  A lane past the
         // last chunk re-reads the last chunk (in bounds) and gets scale 0.
-        constexpr int XV = NS > 0 ? 2 * NS : 1; // float4 of x per thread: K <= 2048 * NS
+        constexpr int XV = NS > 0 ? (512 * NS + (int)T - 1) / (int)T : 1; // float4 of x per thread: K <= 2048 * NS
         float4 xr[XV];
         uint2 wr[XV];
         const bool norm = a.norm_w != nullptr;
 #pragma unroll
         for (int v = 0; v < XV; v++) {
-            const uint32_t i4 = threadIdx.x + 256u * (uint32_t)v;
+            const uint32_t i4 = threadIdx.x + T * (uint32_t)v;
             const bool in = i4 < (a.k >> 2);
             xr[v] = in ? ((const float4 *)a.x)[i4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
             wr[v] = (in && norm) ? ((const uint2 *)a.norm_w)[i4] : make_uint2(0, 0);
@@ -187,7 +195,7 @@ RFP4_DEV void gemv_body(const GemvArgs &a)
                 sb[s][p] = load_scale_bits<SCALE_F32>(a.scales, srow[p] + cl);
             }
         }
-        stage_x_regs<XV>(xs, xr, wr, a.k, norm, a.eps, a.norm_bf16 != 0);
+        stage_x_regs<XV, W>(xs, xr, wr, a.k, norm, a.eps);
 #pragma unroll
         for (int s = 0; s < NS; s++) {
             const uint32_t c = (uint32_t)lane + 64u * (uint32_t)s;
@@ -202,7 +210,7 @@ RFP4_DEV void gemv_body(const GemvArgs &a)
         }
     } else {
         // any K: one slice at a time
-        stage_x(xs, a.x, a.k, a.norm_w, a.eps, a.norm_bf16 != 0);
+        stage_x(xs, a.x, a.k, a.norm_w, a.eps);
         for (uint32_t c = (uint32_t)lane; c < nchunk; c += 64u) {
             uint4 q[NP];
             float sc[NP];
@@ -245,7 +253,7 @@ RFP4_DEV void gemv_body(const GemvArgs &a)
         __syncthreads();
         if (threadIdx.x == 0) {
             unsigned long long b = s_best[0];
-            for (int w = 1; w < 4; w++) b = s_best[w] > b ? s_best[w] : b;
+            for (int w = 1; w < W; w++) b = s_best[w] > b ? s_best[w] : b;
             a.best[blockIdx.x] = b;
         }
         return;

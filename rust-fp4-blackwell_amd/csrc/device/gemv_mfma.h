@@ -33,7 +33,7 @@ RFP4_DEV uint32_t f32_to_bf16_rne_bits(float f)
 }
 
 // Stage x (optionally x*rms*w) as three bf16 planes [3][k] in LDS.
-RFP4_DEV void stage_planes(uint16_t *planes, const float *x, uint32_t k, const uint16_t *norm_w, float eps, bool wbf16)
+RFP4_DEV void stage_planes(uint16_t *planes, const float *x, uint32_t k, const uint16_t *norm_w, float eps)
 {
     __shared__ float red[4];
     const int tid = threadIdx.x;
@@ -55,7 +55,7 @@ RFP4_DEV void stage_planes(uint16_t *planes, const float *x, uint32_t k, const u
     }
     for (uint32_t i = tid; i < k; i += 256) {
         float v = x[i];
-        if (norm_w != nullptr) v = __fmul_rn(__fmul_rn(v, rms), half_bits_to_f32(norm_w[i], wbf16));
+        if (norm_w != nullptr) v = __fmul_rn(__fmul_rn(v, rms), f16_bits_to_f32(norm_w[i]));
         uint32_t hi = f32_to_bf16_rne_bits(v);
         float r1 = __fsub_rn(v, bf16_bits_to_f32(hi));
         uint32_t mid = f32_to_bf16_rne_bits(r1);
@@ -73,7 +73,7 @@ RFP4_DEV void stage_planes(uint16_t *planes, const float *x, uint32_t k, const u
 // keeps the staging from waiting on them (vmcnt retires in issue order).
 template <int XV>
 RFP4_DEV void stage_planes_regs(uint16_t *planes, const float4 *xr, const uint2 *wr, uint32_t k, bool norm,
-                                float eps, bool wbf16)
+                                float eps)
 {
     __shared__ float red[4];
     const int tid = threadIdx.x;
@@ -105,7 +105,7 @@ RFP4_DEV void stage_planes_regs(uint16_t *planes, const float4 *xr, const uint2 
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             float val = e[j];
-            if (norm) val = __fmul_rn(__fmul_rn(val, rms), half_bits_to_f32(wv[j], wbf16));
+            if (norm) val = __fmul_rn(__fmul_rn(val, rms), f16_bits_to_f32((uint16_t)wv[j]));
             uint32_t hi = f32_to_bf16_rne_bits(val);
             float r1 = __fsub_rn(val, bf16_bits_to_f32(hi));
             uint32_t mid = f32_to_bf16_rne_bits(r1);
@@ -205,7 +205,7 @@ RFP4_DEV void gemv_mfma_body(const GemvArgs &a)
                 sb[tt][s] = srow[tt][(size_t)sc * 4u];
             }
         }
-        stage_planes_regs<XV>(planes, xr, wr, k, norm, a.eps, a.norm_bf16 != 0);
+        stage_planes_regs<XV>(planes, xr, wr, k, norm, a.eps);
 #pragma unroll
         for (int s = 0; s < NSC; s++) {
             const uint32_t sc = sc0 + (uint32_t)s;
@@ -223,7 +223,7 @@ RFP4_DEV void gemv_mfma_body(const GemvArgs &a)
             }
         }
     } else {
-        stage_planes(planes, a.x, k, a.norm_w, a.eps, a.norm_bf16 != 0);
+        stage_planes(planes, a.x, k, a.norm_w, a.eps);
         for (uint32_t sc = sc0; sc < min(sc0 + per_wave, nsc); sc++) {
             uint4 q[NT];
             uint32_t sb[NT];

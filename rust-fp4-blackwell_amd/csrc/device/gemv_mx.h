@@ -105,7 +105,6 @@ RFP4_DEV void gemv_mx_body(const GemvArgs &a)
 
     // ---- 1) x (and norm weights) of this thread's blocks into registers
     constexpr bool norm = NORM != 0;
-    const bool wbf16 = a.norm_bf16 != 0;
     float4 xr[XB][8];
     uint4 wr[XB][4];
 #pragma unroll
@@ -186,8 +185,8 @@ RFP4_DEV void gemv_mx_body(const GemvArgs &a)
 #pragma unroll
                 for (int i = 0; i < 4; i++) {
                     const int e = 8 * v + 2 * i;
-                    r[e] = __fmul_rn(__fmul_rn(r[e], rms), half_bits_to_f32(h[i] & 0xFFFFu, wbf16));
-                    r[e + 1] = __fmul_rn(__fmul_rn(r[e + 1], rms), half_bits_to_f32(h[i] >> 16, wbf16));
+                    r[e] = __fmul_rn(__fmul_rn(r[e], rms), f16_bits_to_f32((uint16_t)(h[i] & 0xFFFFu)));
+                    r[e + 1] = __fmul_rn(__fmul_rn(r[e + 1], rms), f16_bits_to_f32((uint16_t)(h[i] >> 16)));
                 }
             }
         }

@@ -19,7 +19,7 @@ RFP4_DEV void embed_rows_body(const RowsArgs &a)
     for (uint32_t i = threadIdx.x; i < a.k; i += blockDim.x) a.y[(size_t)r * a.k + i] = half_bits_to_f32(row[i], a.bf16 != 0);
 }
 
-// grid (rows), dynamic LDS k floats: RMSNorm of row r with 16-bit weights, in
+// grid (rows), dynamic LDS k floats: RMSNorm of row r with fp16 weights, in
 // the order of rmsnorm_body ((x * rms) * w, llama_run/src/main.rs:79-116),
 // then OCP MX quantisation per 32 values.
 RFP4_DEV void rmsnorm_quant_rows_body(const RowsArgs &a)
@@ -33,7 +33,7 @@ RFP4_DEV void rmsnorm_quant_rows_body(const RowsArgs &a)
     const float total = block_sum(ss, red);
     const float rms = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(total, (float)a.k), a.eps)));
     for (uint32_t i = threadIdx.x; i < a.k; i += blockDim.x)
-        yrow[i] = __fmul_rn(__fmul_rn(x[i], rms), half_bits_to_f32(a.w[i], a.bf16 != 0));
+        yrow[i] = __fmul_rn(__fmul_rn(x[i], rms), f16_bits_to_f32(a.w[i]));
     __syncthreads();
     const uint32_t nb = a.k / 32u;
     for (uint32_t b = threadIdx.x; b < nb; b += blockDim.x) {

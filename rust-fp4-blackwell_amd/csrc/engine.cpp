@@ -55,7 +55,7 @@ struct llama_engine {
     StepState *state = nullptr;
     uint32_t *ids = nullptr, *last_tok = nullptr;
     uint32_t ids_alloc = 0;
-    uint32_t half_bf16 = 0; // norms and embeddings hold bf16 (1) or fp16 (0) bits
+    uint32_t embed_bf16 = 0; // embeddings hold bf16 (1) or fp16 (0) bits; norms are fp16
     hipGraph_t graph = nullptr;
     hipGraphExec_t graph_exec = nullptr;
     bool use_graph = true;
@@ -104,14 +104,13 @@ static int enqueue_step(llama_engine *e)
     hipStream_t s = e->stream;
     const uint32_t qd = qdim(c), kvd = kvdim(c), hd = c.head_dim;
     int rc;
-    EmbedArgs ea{e->embed, e->ids, e->state, e->x, c.dim, c.vocab, e->half_bf16};
+    EmbedArgs ea{e->embed, e->ids, e->state, e->x, c.dim, c.vocab, e->embed_bf16};
     if ((rc = launch("rfp4_embed", dim3((c.dim + 255) / 256), dim3(256), s, &ea))) return rc;
     for (uint32_t l = 0; l < c.n_layers; l++) {
         const LayerW &w = e->L[l];
         uint16_t *kc = e->kcache + (size_t)l * c.n_kv_heads * e->max_seq_alloc * hd;
         uint16_t *vc = e->vcache + (size_t)l * c.n_kv_heads * e->max_seq_alloc * hd;
-        GemvArgs qa{w.qkv_c, w.qkv_s, e->x, e->qkv, nullptr, e->norm_attn + (size_t)l * c.dim, qd + 2 * kvd, c.dim, 0, c.eps,
-                    e->half_bf16};
+        GemvArgs qa{w.qkv_c, w.qkv_s, e->x, e->qkv, nullptr, e->norm_attn + (size_t)l * c.dim, qd + 2 * kvd, c.dim, 0, c.eps};
         if ((rc = gemv_launch("e8m0", RFP4_EPI_STORE, qa, s, 0))) return rc;
         AttnArgs aa{};
         aa.q = e->qkv; aa.kc = kc; aa.vc = vc; aa.out = e->attn_out;
@@ -121,15 +120,14 @@ static int enqueue_step(llama_engine *e)
         aa.n_heads = c.n_heads; aa.n_kv_heads = c.n_kv_heads; aa.head_dim = hd; aa.seq = 0;
         aa.chunk = e->attn_chunk; aa.max_splits = e->attn_max_splits;
         if ((rc = attn_launch(aa, 1, s, e->attn_chunk * e->attn_max_splits, 1))) return rc;
-        GemvArgs oa{w.o_c, w.o_s, e->attn_out, e->x, nullptr, nullptr, c.dim, qd, 0, 0.0f, 0};
+        GemvArgs oa{w.o_c, w.o_s, e->attn_out, e->x, nullptr, nullptr, c.dim, qd, 0, 0.0f};
         if ((rc = gemv_launch("e8m0", RFP4_EPI_RESIDUAL, oa, s, 0))) return rc;
-        GemvArgs ga{w.gu_c, w.gu_s, e->x, e->sw, nullptr, e->norm_ffn + (size_t)l * c.dim, c.ffn, c.dim, c.ffn, c.eps,
-                    e->half_bf16};
+        GemvArgs ga{w.gu_c, w.gu_s, e->x, e->sw, nullptr, e->norm_ffn + (size_t)l * c.dim, c.ffn, c.dim, c.ffn, c.eps};
         if ((rc = gemv_launch("e8m0", RFP4_EPI_SWIGLU, ga, s, 0))) return rc;
-        GemvArgs da{w.d_c, w.d_s, e->sw, e->x, nullptr, nullptr, c.dim, c.ffn, 0, 0.0f, 0};
+        GemvArgs da{w.d_c, w.d_s, e->sw, e->x, nullptr, nullptr, c.dim, c.ffn, 0, 0.0f};
         if ((rc = gemv_launch("e8m0", RFP4_EPI_RESIDUAL, da, s, 0))) return rc;
     }
-    GemvArgs la{e->lm_c, e->lm_s, e->x, e->logits, e->best, e->norm_final, c.vocab, c.dim, 0, c.eps, e->half_bf16};
+    GemvArgs la{e->lm_c, e->lm_s, e->x, e->logits, e->best, e->norm_final, c.vocab, c.dim, 0, c.eps};
     if ((rc = gemv_launch("e8m0", RFP4_EPI_ARGMAX, la, s, 0))) return rc;
     StepArgs sa{e->best, e->state, e->ids, e->last_tok, e->n_best, 0};
     return launch("rfp4_step", dim3(1), dim3(1024), s, &sa);
@@ -184,7 +182,7 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
     int rc;
     RowsArgs ea{};
     ea.ids = e->pf_ids; ea.embed = e->embed; ea.y = e->pf_x; ea.rows = n; ea.k = c.dim; ea.vocab = c.vocab;
-    ea.bf16 = e->half_bf16;
+    ea.bf16 = e->embed_bf16;
     if ((rc = launch("rfp4_embed_rows", dim3(n), dim3(256), s, &ea))) return rc;
     for (uint32_t l = 0; l < c.n_layers; l++) {
         const LayerW &w = e->L[l];
@@ -192,7 +190,7 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
         uint16_t *vc = e->vcache + (size_t)l * c.n_kv_heads * e->max_seq_alloc * hd;
         RowsArgs na{};
         na.x = e->pf_x; na.w = e->norm_attn + (size_t)l * c.dim; na.codes = e->pf_codes; na.scales = e->pf_scales;
-        na.rows = n; na.k = c.dim; na.eps = c.eps; na.bf16 = e->half_bf16;
+        na.rows = n; na.k = c.dim; na.eps = c.eps;
         if ((rc = launch("rfp4_rmsnorm_quant_rows", dim3(n), dim3(256), s, &na, c.dim * 4u))) return rc;
         if ((rc = fp4_gemm(s, n, nqkv, c.dim, e->pf_codes, e->pf_scales, w.qkv_c, w.qkv_s, e->pf_c))) return rc;
         RopeRowsArgs ra{};
@@ -223,7 +221,7 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
     // last row: the decode step's final norm + LM head, then argmax
     rc = hip_check(hipMemcpyAsync(e->x, e->pf_x + (size_t)(n - 1) * c.dim, c.dim * sizeof(float),
                                   hipMemcpyDeviceToDevice, s), "hipMemcpyAsync(prefill row)");
-    GemvArgs la{e->lm_c, e->lm_s, e->x, e->logits, nullptr, e->norm_final, c.vocab, c.dim, 0, c.eps, e->half_bf16};
+    GemvArgs la{e->lm_c, e->lm_s, e->x, e->logits, nullptr, e->norm_final, c.vocab, c.dim, 0, c.eps};
     if (!rc) rc = gemv_launch("e8m0", RFP4_EPI_STORE, la, s, 0);
     if (!rc) rc = argmax(s, c.vocab, e->logits, e->last_tok);
     return rc;
@@ -372,7 +370,7 @@ static int engine_synth(llama_engine *e, uint64_t seed)
     if (!rc) rc = rfp4_synth_f16(s, seed, kStreamNormFinal, sigma, 1.0f, c.dim, e->norm_final);
     if (!rc) rc = rfp4_synth_f16(s, seed, kStreamEmbed, sigma, 0.0f, (size_t)c.vocab * c.dim, e->embed);
     if (!rc) rc = rfp4_synth_mx_weight(s, seed, kStreamLm, sigma, c.dim, 0, c.vocab, e->lm_c, e->lm_s);
-    e->half_bf16 = 0;
+    e->embed_bf16 = 0;
     return rc;
 }
 
@@ -451,18 +449,28 @@ static int load_proj(llama_engine *e, const StFile &f, const StTensor &t, uint8_
     return rc;
 }
 
-// A norm or embedding tensor as 16-bit bits in the engine's format: copied as
-// stored when it already is that format, else rounded to bf16 (RNE).
-static int load_half(llama_engine *e, const StFile &f, const StTensor &t, uint16_t *dst)
+// Norm weights as fp16 (RNE from BF16 / F32; exact for bf16 values of
+// magnitude 2^-17 .. 65504, i.e. any RMSNorm gain), embeddings as stored when
+// BF16 or F16 (F32 rounded to bf16).
+static int load_norm(const StFile &f, const StTensor &t, uint16_t *dst)
+{
+    std::vector<uint16_t> h(t.numel());
+    int rc = f.read_f16(t, h.data(), h.size());
+    if (!rc) rc = hip_check(hipMemcpy(dst, h.data(), h.size() * 2, hipMemcpyHostToDevice), "H2D checkpoint");
+    return rc;
+}
+
+static int load_embed(llama_engine *e, const StFile &f, const StTensor &t, uint16_t *dst)
 {
     const uint64_t n = t.numel();
-    const bool same = (e->half_bf16 && t.dtype == "BF16") || (!e->half_bf16 && t.dtype == "F16");
-    if (same) return hip_check(hipMemcpy(dst, f.data(t), n * 2, hipMemcpyHostToDevice), "H2D checkpoint");
+    if (t.dtype == "BF16" || t.dtype == "F16")
+        return hip_check(hipMemcpy(dst, f.data(t), n * 2, hipMemcpyHostToDevice), "H2D checkpoint");
     std::vector<float> tmp(n);
     int rc = f.read_f32(t, tmp.data(), n);
     if (rc) return rc;
     std::vector<uint16_t> h(n);
     for (uint64_t i = 0; i < n; i++) h[i] = f32_to_bf16_rne_host(tmp[i]);
+    (void)e;
     return hip_check(hipMemcpy(dst, h.data(), n * 2, hipMemcpyHostToDevice), "H2D checkpoint");
 }
 
@@ -491,10 +499,7 @@ static int engine_load_safetensors(llama_engine *e, const char *path)
     if (rc) return rc;
     if (!lm) lm = emb;
 
-    // norms and embeddings: bf16 unless every one of them is stored as f16
-    bool all_f16 = fin->dtype == "F16" && emb->dtype == "F16";
-    for (uint32_t l = 0; l < c.n_layers; l++) all_f16 = all_f16 && na[l]->dtype == "F16" && nf[l]->dtype == "F16";
-    e->half_bf16 = all_f16 ? 0u : 1u;
+    e->embed_bf16 = emb->dtype == "F16" ? 0u : 1u;
 
     size_t stage_bytes = 0;
     for (const StTensor *t : proj) stage_bytes = std::max<size_t>(stage_bytes, t->numel() * 4);
@@ -509,16 +514,16 @@ static int engine_load_safetensors(llama_engine *e, const char *path)
     if (!rc) rc = load_proj(e, f, *lm, e->lm_c, e->lm_s, stage);
     if (stage) hipFree(stage);
     for (uint32_t l = 0; l < c.n_layers && !rc; l++) {
-        rc = load_half(e, f, *na[l], e->norm_attn + (size_t)l * c.dim);
-        if (!rc) rc = load_half(e, f, *nf[l], e->norm_ffn + (size_t)l * c.dim);
+        rc = load_norm(f, *na[l], e->norm_attn + (size_t)l * c.dim);
+        if (!rc) rc = load_norm(f, *nf[l], e->norm_ffn + (size_t)l * c.dim);
     }
-    if (!rc) rc = load_half(e, f, *fin, e->norm_final);
-    if (!rc) rc = load_half(e, f, *emb, e->embed);
+    if (!rc) rc = load_norm(f, *fin, e->norm_final);
+    if (!rc) rc = load_embed(e, f, *emb, e->embed);
     return rc;
 }
 
 // ---------------------------------------------------------------- packed cache
-// File: "RFP4PACK", u32 version, u32 half_bf16, rfp4_model_config, u32 count,
+// File: "RFP4PACK", u32 version, u32 embed_bf16, rfp4_model_config, u32 count,
 // then `count` blobs (u64 bytes + bytes) in engine_blobs order.
 static const char kPackMagic[8] = {'R', 'F', 'P', '4', 'P', 'A', 'C', 'K'};
 static const uint32_t kPackVersion = 1;
@@ -775,7 +780,7 @@ int llama_engine_save(llama_engine *e, const char *path)
     auto blobs = engine_blobs(e);
     const uint32_t count = (uint32_t)blobs.size();
     bool ok = fwrite(kPackMagic, 1, 8, fp) == 8 && fwrite(&kPackVersion, 4, 1, fp) == 1 &&
-              fwrite(&e->half_bf16, 4, 1, fp) == 1 && fwrite(&e->c, sizeof(rfp4_model_config), 1, fp) == 1 &&
+              fwrite(&e->embed_bf16, 4, 1, fp) == 1 && fwrite(&e->c, sizeof(rfp4_model_config), 1, fp) == 1 &&
               fwrite(&count, 4, 1, fp) == 1;
     int rc = hip_check(hipStreamSynchronize(e->stream), "hipStreamSynchronize(save)");
     std::vector<uint8_t> host;
@@ -814,7 +819,7 @@ int llama_engine_load(const char *path, uint32_t max_seq, llama_engine **out)
         fclose(fp);
         return rc;
     }
-    e->half_bf16 = half;
+    e->embed_bf16 = half;
     auto blobs = engine_blobs(e);
     if (count != blobs.size()) rc = set_error(RFP4_E_SHAPE, "llama_engine_load: %u blobs, the config needs %zu", count, blobs.size());
     std::vector<uint8_t> host;
@@ -841,11 +846,11 @@ int llama_engine_load(const char *path, uint32_t max_seq, llama_engine **out)
     return RFP4_OK;
 }
 
-int llama_engine_info(const llama_engine *e, rfp4_model_config *cfg, int *half_bf16)
+int llama_engine_info(const llama_engine *e, rfp4_model_config *cfg, int *embed_bf16)
 {
     if (!e) return set_error(RFP4_E_INVALID, "llama_engine_info: null engine");
     if (cfg) *cfg = e->c;
-    if (half_bf16) *half_bf16 = (int)e->half_bf16;
+    if (embed_bf16) *embed_bf16 = (int)e->embed_bf16;
     return RFP4_OK;
 }
 

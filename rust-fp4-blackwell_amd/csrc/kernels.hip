@@ -54,6 +54,17 @@ GEMV_KERNEL_OCC4(e8m0, 0, swiglu, RFP4_EPI_SWIGLU, 4, 1)
 GEMV_KERNEL_OCC4(e8m0, 0, swiglu, RFP4_EPI_SWIGLU, 4, 2)
 GEMV_KERNEL(e8m0, 0, swiglu, RFP4_EPI_SWIGLU, 4, 3) // 128 VGPRs would spill
 GEMV_NS_FULL(f32, 1, store, RFP4_EPI_STORE, 4)
+// 8 waves per workgroup for one-slice shapes (K <= 2048), test-selectable:
+// alone faster (TinyLlama gate|up 6.18 -> 5.42 us at 1 row per wave), inside
+// the decode step slower; at K = 4096 and 14336 slower alone too (runtime.cpp
+// gemv_variant).  rfp4_gemv_e8m0_<epilogue>_r<R>_s<NS>_w<W>
+#define GEMV_KERNEL_W(ENAME, EPI, R, NS, W) \
+    extern "C" __global__ __launch_bounds__(64 * W) void rfp4_gemv_e8m0_##ENAME##_r##R##_s##NS##_w##W(GemvArgs a) \
+    {                                                                                                           \
+        gemv_body<0, EPI, R, NS, W>(a);                                                                         \
+    }
+GEMV_KERNEL_W(swiglu, RFP4_EPI_SWIGLU, 1, 1, 8)
+GEMV_KERNEL_W(store, RFP4_EPI_STORE, 2, 1, 8)
 
 // ---- block-scaled MFMA GEMV: rfp4_gemvx_<epilogue>_n<NORM>_p<PER>
 // (E2M1 weights straight into v_mfma_scale_f32_16x16x128_f8f6f4, x as E4M3

@@ -226,11 +226,14 @@ int gemv_check(uint32_t n, uint32_t k, const void *w, const void *sc, const floa
 }
 
 // Forced variant for tests (0 = automatic); thread-local like the error text.
-static thread_local int t_force_r = 0, t_force_ns = -1;
+static thread_local int t_force_r = 0, t_force_ns = -1, t_force_w = 0;
 
 // Compiled (R, NS) variants; must match the table in kernels.hip.
-static bool gemv_has_ns(bool f32scale, int epi, int R, int ns)
+static bool gemv_has_ns(bool f32scale, int epi, int R, int ns, int W = 4)
 {
+    if (W != 4) // 8-wave workgroups: one-slice SwiGLU at R = 1, store at R = 2
+        return !f32scale && W == 8 && ns == 1 &&
+               ((epi == RFP4_EPI_SWIGLU && R == 1) || (epi == RFP4_EPI_STORE && R == 2));
     if (ns == 0) return true;
     bool full = ns == 1 || ns == 2 || ns == 3 || ns == 4 || ns == 7;
     if (f32scale) return R == 4 && full;
@@ -255,10 +258,16 @@ GemvVariant gemv_variant(uint32_t n, uint32_t k, int epi, bool f32scale)
         if (epi == RFP4_EPI_SWIGLU) R = 2;
         else if (epi != RFP4_EPI_SWIGLU && n >= 65536u && ns_needed <= 2) R = 8;
     }
+    // 4 waves per workgroup: 8-wave workgroups (compiled for one-slice
+    // shapes) are faster alone (TinyLlama gate|up 6.18 -> 5.42 us) but slower
+    // inside the decode step (1313 -> 1276 tok/s, fused norm), so only forced
+    int W = 4;
     if (t_force_r) R = t_force_r;
-    int ns = gemv_has_ns(f32scale, epi, R, ns_needed) ? ns_needed : 0;
+    if (t_force_w) W = t_force_w;
+    int ns = gemv_has_ns(f32scale, epi, R, ns_needed, W) ? ns_needed : 0;
     if (t_force_ns >= 0) ns = t_force_ns;
-    return GemvVariant{R, ns};
+    if (W != 4 && !gemv_has_ns(f32scale, epi, R, ns, W)) W = 4, ns = gemv_has_ns(f32scale, epi, R, ns_needed) ? ns_needed : 0;
+    return GemvVariant{R, ns, W};
 }
 
 // Path: 0 = automatic, 1 = VALU kernel, 2 = bf16 MFMA kernel, 3 = block-scaled
@@ -298,7 +307,7 @@ static bool gemv_mfma_has(int epi, int rt, int nsc)
 
 struct GemvPlan {
     bool mfma, mx;
-    int R, NS;               // VALU: rows per wave, K slices; MFMA: 16-row tiles, super-chunks per wave
+    int R, NS, W = 4;               // VALU: rows per wave, K slices; MFMA: 16-row tiles, super-chunks per wave
     uint32_t rows_per_block;
 };
 
@@ -329,7 +338,8 @@ static GemvPlan gemv_plan(uint32_t n, uint32_t k, int epi, bool f32scale)
         GemvVariant v = gemv_variant(n, k, epi, f32scale);
         p.R = v.R;
         p.NS = v.NS;
-        p.rows_per_block = 4u * (uint32_t)v.R;
+        p.W = v.W;
+        p.rows_per_block = (uint32_t)v.W * (uint32_t)v.R;
     }
     return p;
 }
@@ -359,18 +369,22 @@ int gemv_launch(const char *scale_name, int epi, const GemvArgs &args, hipStream
         snprintf(name, sizeof name, "rfp4_gemvm_%s_t%d_s%d", epi_names[epi], p.R, p.NS);
         shmem = args.k * 6u;
     } else {
-        if (r_override) p.R = r_override, p.rows_per_block = 4u * (uint32_t)r_override;
-        if (!gemv_has_ns(f32scale, epi, p.R, p.NS))
-            return set_error(RFP4_E_INVALID, "gemv: no compiled variant R=%d NS=%d for %s/%s", p.R, p.NS,
+        if (r_override) p.R = r_override, p.rows_per_block = (uint32_t)p.W * (uint32_t)r_override;
+        if (!gemv_has_ns(f32scale, epi, p.R, p.NS, p.W))
+            return set_error(RFP4_E_INVALID, "gemv: no compiled variant R=%d NS=%d W=%d for %s/%s", p.R, p.NS, p.W,
                              scale_name, epi_names[epi]);
         if (p.NS > 0 && (uint32_t)p.NS * 2048u < args.k)
             return set_error(RFP4_E_INVALID, "gemv: NS=%d slices cannot cover k=%u", p.NS, args.k);
-        snprintf(name, sizeof name, "rfp4_gemv_%s_%s_r%d_s%d", scale_name, epi_names[epi], p.R, p.NS);
+        if (p.W == 4)
+            snprintf(name, sizeof name, "rfp4_gemv_%s_%s_r%d_s%d", scale_name, epi_names[epi], p.R, p.NS);
+        else
+            snprintf(name, sizeof name, "rfp4_gemv_%s_%s_r%d_s%d_w%d", scale_name, epi_names[epi], p.R, p.NS, p.W);
         shmem = args.k * 4u;
     }
     uint32_t blocks = (args.n + p.rows_per_block - 1) / p.rows_per_block;
     GemvArgs a = args;
-    return launch(name, dim3(blocks), dim3(256), s, &a, shmem);
+    const uint32_t threads = (p.mx || p.mfma) ? 256u : 64u * (uint32_t)p.W;
+    return launch(name, dim3(blocks), dim3(threads), s, &a, shmem);
 }
 
 uint32_t gemv_blocks(uint32_t n_logical, uint32_t k, int epi)
@@ -387,6 +401,15 @@ extern "C" int rfp4_debug_gemv_path(int path)
     if (path < 0 || path > 3)
         return set_error(RFP4_E_INVALID, "path must be 0 (auto), 1 (VALU), 2 (bf16 MFMA) or 3 (block-scaled MFMA)");
     t_force_path = path;
+    return RFP4_OK;
+}
+
+extern "C" int rfp4_debug_gemv_waves(int waves)
+{
+    using namespace rfp4;
+    if (waves != 0 && waves != 4 && waves != 8)
+        return set_error(RFP4_E_INVALID, "waves per workgroup must be 0 (auto), 4 or 8");
+    t_force_w = waves;
     return RFP4_OK;
 }
 
@@ -461,7 +484,7 @@ int fp4_gemv(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint32_t *w, co
 {
     int rc = gemv_check(n, k, w, scales, x, y);
     if (rc) return rc;
-    GemvArgs a{w, scales, x, y, nullptr, nullptr, n, k, 0, 0.0f, 0};
+    GemvArgs a{w, scales, x, y, nullptr, nullptr, n, k, 0, 0.0f};
     return gemv_launch("f32", RFP4_EPI_STORE, a, (hipStream_t)stream, 0);
 }
 
@@ -470,7 +493,7 @@ int mx4_gemv(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_t *codes,
 {
     int rc = gemv_check(n, k, codes, scales, x, y);
     if (rc) return rc;
-    GemvArgs a{codes, scales, x, y, nullptr, nullptr, n, k, 0, 0.0f, 0};
+    GemvArgs a{codes, scales, x, y, nullptr, nullptr, n, k, 0, 0.0f};
     return gemv_launch("e8m0", RFP4_EPI_STORE, a, (hipStream_t)stream, 0);
 }
 
@@ -480,7 +503,7 @@ int mx4_gemv_rmsnorm(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_t
     int rc = gemv_check(n, k, codes, scales, x, y);
     if (rc) return rc;
     if (!norm_w) return set_error(RFP4_E_INVALID, "gemv_rmsnorm: null norm weights");
-    GemvArgs a{codes, scales, x, y, nullptr, norm_w, n, k, 0, eps, 0};
+    GemvArgs a{codes, scales, x, y, nullptr, norm_w, n, k, 0, eps};
     return gemv_launch("e8m0", RFP4_EPI_STORE, a, (hipStream_t)stream, 0);
 }
 
@@ -489,7 +512,7 @@ int mx4_gemv_residual(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_
 {
     int rc = gemv_check(n, k, codes, scales, x, x_res);
     if (rc) return rc;
-    GemvArgs a{codes, scales, x, x_res, nullptr, nullptr, n, k, 0, 0.0f, 0};
+    GemvArgs a{codes, scales, x, x_res, nullptr, nullptr, n, k, 0, 0.0f};
     return gemv_launch("e8m0", RFP4_EPI_RESIDUAL, a, (hipStream_t)stream, 0);
 }
 
@@ -499,7 +522,7 @@ int mx4_gemv_swiglu(rfp4_stream_t stream, uint32_t n, uint32_t k, uint32_t pair_
     int rc = gemv_check(n, k, codes, scales, x, out);
     if (rc) return rc;
     if (pair_off < n) return set_error(RFP4_E_SHAPE, "gemv_swiglu: pair_off %u overlaps the %u gate rows", pair_off, n);
-    GemvArgs a{codes, scales, x, out, nullptr, nullptr, n, k, pair_off, 0.0f, 0};
+    GemvArgs a{codes, scales, x, out, nullptr, nullptr, n, k, pair_off, 0.0f};
     return gemv_launch("e8m0", RFP4_EPI_SWIGLU, a, (hipStream_t)stream, 0);
 }
 
@@ -512,7 +535,7 @@ int mx4_gemv_argmax(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_t 
     if (rc) return rc;
     if (!workspace || !best_token) return set_error(RFP4_E_INVALID, "gemv_argmax: null workspace or output");
     unsigned long long *best = (unsigned long long *)workspace;
-    GemvArgs a{codes, scales, x, y, best, nullptr, n, k, 0, 0.0f, 0};
+    GemvArgs a{codes, scales, x, y, best, nullptr, n, k, 0, 0.0f};
     rc = gemv_launch("e8m0", RFP4_EPI_ARGMAX, a, (hipStream_t)stream, 0);
     if (rc) return rc;
     // reduce the per-workgroup keys with the step kernel on a scratch cursor
@@ -535,7 +558,7 @@ int rfp4_debug_gemv_fused(rfp4_stream_t stream, int epi, uint32_t n, uint32_t k,
     if (epi == RFP4_EPI_ARGMAX && (!workspace || !best_token))
         return set_error(RFP4_E_INVALID, "gemv_fused: argmax needs a workspace and an output");
     unsigned long long *best = (unsigned long long *)workspace;
-    GemvArgs a{codes, scales, x, y, best, norm_w, n, k, pair_off, eps, 0};
+    GemvArgs a{codes, scales, x, y, best, norm_w, n, k, pair_off, eps};
     rc = gemv_launch("e8m0", epi, a, (hipStream_t)stream, 0);
     if (rc || epi != RFP4_EPI_ARGMAX) return rc;
     uint32_t nb = gemv_blocks(n, k, RFP4_EPI_ARGMAX);

@@ -34,7 +34,7 @@ int launch(const char *name, dim3 grid, dim3 block, hipStream_t s, void *args, u
 int fill_words(uint32_t *p, uint64_t n_words, uint32_t value, hipStream_t s);
 int gemv_check(uint32_t n, uint32_t k, const void *w, const void *sc, const float *x, const float *y);
 struct GemvVariant {
-    int R, NS;
+    int R, NS, W; // rows per wave, up-front K slices (0 = loop), waves per workgroup
 };
 GemvVariant gemv_variant(uint32_t n, uint32_t k, int epi, bool f32scale);
 int gemv_launch(const char *scale_name, int epi, const GemvArgs &args, hipStream_t s, int r_override);

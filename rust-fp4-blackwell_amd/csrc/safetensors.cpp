@@ -279,6 +279,43 @@ uint16_t f32_to_bf16_rne_host(float f)
     return (uint16_t)((u + 0x7FFFu + ((u >> 16) & 1u)) >> 16);
 }
 
+uint16_t f32_to_f16_rne_host(float f)
+{
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    const uint32_t sign = (u >> 16) & 0x8000u, a = u & 0x7FFFFFFFu;
+    if (a >= 0x7F800000u) return (uint16_t)(sign | (a > 0x7F800000u ? 0x7E00u : 0x7C00u)); // nan, inf
+    if (a >= 0x477FF000u) return (uint16_t)(sign | 0x7C00u);                               // >= 65520: inf
+    const int e = (int)(a >> 23) - 127;
+    const uint32_t m = (a & 0x7FFFFFu) | 0x800000u; // 24-bit significand, value m * 2^(e-23)
+    if (e < -14) {
+        // subnormal: units of 2^-24, q = m * 2^(e+1), rounded to nearest even
+        const int shift = -(e + 1);
+        if (shift > 25) return (uint16_t)sign; // below 2^-25: rounds to zero
+        const uint32_t q = m >> shift, rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1);
+        return (uint16_t)(sign | (q + ((rem > half || (rem == half && (q & 1u))) ? 1u : 0u)));
+    }
+    // normal: 10 fraction bits, the carry of the rounding may step the exponent
+    const uint32_t q = ((uint32_t)(e + 15) << 10) | ((m >> 13) & 0x3FFu), rem = m & 0x1FFFu;
+    return (uint16_t)(sign | (q + ((rem > 0x1000u || (rem == 0x1000u && (q & 1u))) ? 1u : 0u)));
+}
+
+int StFile::read_f16(const StTensor &t, uint16_t *out, uint64_t count) const
+{
+    if (!out) return set_error(RFP4_E_INVALID, "safetensors: null output");
+    const uint64_t n = t.numel();
+    if (count < n) return set_error(RFP4_E_CAPACITY, "safetensors: %s needs %llu halves", t.name.c_str(), (unsigned long long)n);
+    if (t.dtype == "F16") {
+        memcpy(out, data(t), n * 2);
+        return RFP4_OK;
+    }
+    std::vector<float> tmp(n);
+    int rc = read_f32(t, tmp.data(), n);
+    if (rc) return rc;
+    for (uint64_t i = 0; i < n; i++) out[i] = f32_to_f16_rne_host(tmp[i]);
+    return RFP4_OK;
+}
+
 int StFile::read_f32(const StTensor &t, float *out, uint64_t count) const
 {
     if (!out) return set_error(RFP4_E_INVALID, "safetensors: null output");
@@ -369,6 +406,14 @@ int rfp4_st_read_f32(const rfp4_st *st, const char *name, float *out, uint64_t c
     const StTensor *t = st->f.find(name);
     if (!t) return set_error(RFP4_E_INVALID, "rfp4_st_read_f32: no tensor %s", name);
     return st->f.read_f32(*t, out, count);
+}
+
+int rfp4_st_read_f16(const rfp4_st *st, const char *name, uint16_t *out, uint64_t count)
+{
+    if (!st || !name) return set_error(RFP4_E_INVALID, "rfp4_st_read_f16: null argument");
+    const StTensor *t = st->f.find(name);
+    if (!t) return set_error(RFP4_E_INVALID, "rfp4_st_read_f16: no tensor %s", name);
+    return st->f.read_f16(*t, out, count);
 }
 
 } // extern "C"

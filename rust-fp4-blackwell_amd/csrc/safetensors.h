@@ -36,6 +36,9 @@ class StFile {
     // The tensor widened to f32 (BF16, F16, F32), exactly as the reference's
     // `get` closure (llama_run/src/main.rs:419-430).
     int read_f32(const StTensor &t, float *out, uint64_t count) const;
+    // The tensor as fp16 bits: F16 as stored, BF16 / F32 rounded to nearest
+    // even (exact for bf16 values of magnitude 2^-17 .. 65504).
+    int read_f16(const StTensor &t, uint16_t *out, uint64_t count) const;
 
   private:
     int fd_ = -1;
@@ -49,5 +52,6 @@ class StFile {
 // Host conversions shared by the loaders (exact where the target holds the value).
 float f16_to_f32_host(uint16_t h);
 uint16_t f32_to_bf16_rne_host(float f);
+uint16_t f32_to_f16_rne_host(float f); // IEEE binary16, round to nearest even, overflow to inf
 
 } // namespace rfp4

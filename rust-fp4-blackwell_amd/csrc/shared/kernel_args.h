@@ -22,12 +22,11 @@ typedef struct GemvArgs {
     const float *x;       // activation, K floats
     float *y;             // output (see epilogue)
     unsigned long long *best; // ARGMAX: one packed key per workgroup
-    const uint16_t *norm_w;   // optional 16-bit RMSNorm weights: x -> x*rms*w first
+    const uint16_t *norm_w;   // optional fp16 RMSNorm weights: x -> x*rms*w first
     uint32_t n;           // logical output rows
     uint32_t k;           // reduction length, multiple of 32
     uint32_t pair_off;    // SWIGLU: physical row offset of the up rows
     float eps;            // RMSNorm epsilon (with norm_w)
-    uint32_t norm_bf16;   // norm_w holds bf16 (1) or fp16 (0) bit patterns
 } GemvArgs;
 
 typedef struct RmsnormArgs {
@@ -104,7 +103,7 @@ typedef struct RowsArgs {
     float *y;                // embed: output rows [rows][k]
     uint32_t rows, k, vocab;
     float eps;
-    uint32_t bf16;           // w and embed hold bf16 (1) or fp16 (0) bit patterns
+    uint32_t bf16;           // embed holds bf16 (1) or fp16 (0) bit patterns
 } RowsArgs;
 
 typedef struct RopeRowsArgs {

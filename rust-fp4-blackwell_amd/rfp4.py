@@ -90,6 +90,7 @@ _SIGS = {
     "rfp4_mma_tile32": (I32, [P, P, P, P, P, P]),
     "rfp4_selftest_cvt_fp4": (I32, [P, U32, P, P]),
     "rfp4_debug_gemv_variant": (I32, [I32, I32]),
+    "rfp4_debug_gemv_waves": (I32, [I32]),
     "rfp4_debug_gemv_path": (I32, [I32]),
     "rfp4_debug_gemv_fused": (I32, [P, I32, U32, U32, U32, P, P, P, P, F32, P, P, P]),
     "rfp4_selftest_cvt_bf16": (I32, [P, U32, P, P, P]),
@@ -110,6 +111,7 @@ _SIGS = {
     "rfp4_st_name": (I32, [P, U32, C.POINTER(C.c_char_p)]),
     "rfp4_st_info": (I32, [P, C.c_char_p, C.c_char_p, C.POINTER(U32), P, C.POINTER(U64)]),
     "rfp4_st_read_f32": (I32, [P, C.c_char_p, P, U64]),
+    "rfp4_st_read_f16": (I32, [P, C.c_char_p, P, U64]),
     "llama_engine_prefill": (I32, [P, P, U32, U32, C.POINTER(U32)]),
     "llama_decode_step": (I32, [P, U32, U32, C.POINTER(U32)]),
     "llama_generate": (I32, [P, P, U32, U32, U32, P]),
@@ -463,6 +465,13 @@ class SafeTensors:
         check(load().rfp4_st_info(self.h, name.encode(), dt, C.byref(nd), C.cast(shape, P), C.byref(nb)))
         return dt.value.decode(), tuple(shape[i] for i in range(nd.value)), nb.value
 
+    def read_f16(self, name: str) -> np.ndarray:
+        """fp16 bit patterns (uint16): F16 as stored, BF16 / F32 rounded to nearest even."""
+        _, shape, _ = self.info(name)
+        out = np.empty(int(np.prod(shape)) if shape else 1, dtype=np.uint16)
+        check(load().rfp4_st_read_f16(self.h, name.encode(), out.ctypes.data, out.size))
+        return out.reshape(shape)
+
     def read_f32(self, name: str) -> np.ndarray:
         _, shape, _ = self.info(name)
         out = np.empty(int(np.prod(shape)) if shape else 1, dtype=np.float32)
@@ -504,7 +513,7 @@ class Engine:
     def save(self, path: str):
         check(load().llama_engine_save(self.h, os.fsencode(path)))
 
-    def half_bf16(self) -> bool:
+    def embed_bf16(self) -> bool:
         b = C.c_int(0)
         check(load().llama_engine_info(self.h, None, C.byref(b)))
         return bool(b.value)

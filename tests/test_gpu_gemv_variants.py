@@ -236,3 +236,27 @@ def test_gemv_mx_fused_rmsnorm(rf, orc, stream, epi, n, k):
     else:
         cond = np.abs(got.astype(np.float64) - f64[:n]) / np.maximum(absf[:n], 1e-300)
         assert cond.max() < 1e-5, cond.max()
+
+
+@pytest.mark.parametrize("epi,r", [("swiglu", 1), ("store", 2)])
+@pytest.mark.parametrize("n,k", [(67, 512), (300, 2048), (5632, 2048)])
+def test_gemv_eight_wave_variants(rf, orc, stream, epi, r, n, k):
+    """8 waves per workgroup (one K slice), forced; and the automatic choice
+    on the same shape."""
+    codes, scales, x = _config1(orc, 2 * n, k, seed=n + k + r)
+    dc, ds, dx = _dev(rf, codes, stream), _dev(rf, scales, stream), _dev(rf, x, stream)
+    full = orc.gemv_e8m0(2 * n, k, codes, scales, x)
+    f64, absf = orc.gemv_e8m0_f64(2 * n, k, codes, scales, x)
+    base = np.linspace(-1, 1, n).astype(np.float32)
+    try:
+        for forced in (True, False):
+            if forced:
+                _force(rf, r, 1, path=1)
+                rf.check(rf.load().rfp4_debug_gemv_waves(8))
+            got, best = _run_epi(rf, stream, epi, n, k, dc, ds, dx, base)
+            _check_epi(orc, epi, got, best, n, full, f64, absf, base, f"{epi} R={r} W=8 k={k} forced={forced}")
+            _force(rf, 0, -1, path=0)
+            rf.check(rf.load().rfp4_debug_gemv_waves(0))
+    finally:
+        _force(rf, 0, -1, path=0)
+        rf.check(rf.load().rfp4_debug_gemv_waves(0))

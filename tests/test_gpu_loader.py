@@ -2,8 +2,8 @@
 tensor names (the reference's loader, llama_run/src/main.rs:413-460) into
 the engine, against the CPU oracle loaded with the same tensors.  The
 projections are quantized by the OCP MX rules on both sides (bit-exact),
-norms and embeddings keep the checkpoint's 16-bit values; greedy tokens must
-be identical.  Checkpoints are synthetic (no real weights in the image)."""
+norm weights are held as fp16 (exact for these gains) and embeddings keep
+the checkpoint's 16-bit values; greedy tokens must be identical.  Checkpoints are synthetic (no real weights in the image)."""
 import numpy as np
 import pytest
 
@@ -28,7 +28,7 @@ def _shapes(c):
 
 def make_checkpoint(path, c, seed, dtype="BF16", tied=False, norm_dtype=None):
     """Write a checkpoint; return (f32 values, 16-bit bits for norms/embeds as
-    the engine should hold them, half_bf16)."""
+    the engine should hold them, embed_bf16)."""
     rng = np.random.default_rng(seed)
     norm_dtype = norm_dtype or dtype
     tensors, f32 = {}, {}
@@ -48,16 +48,17 @@ def make_checkpoint(path, c, seed, dtype="BF16", tied=False, norm_dtype=None):
     if not tied:
         put("lm_head.weight", 0.02 * rng.standard_normal((c["vocab"], c["dim"])), dtype)
     stw.write(path, tensors, metadata={"format": "pt"})
-    small = [n for n in tensors if n.endswith("norm.weight") or n == "model.embed_tokens.weight"]
-    half_bf16 = not all(tensors[n][0] == "F16" for n in small)
+    # norms: fp16 (numpy's conversion rounds to nearest even, as the engine);
+    # embeddings: as stored when BF16 / F16, F32 rounded to bf16
     half = {}
-    for n in small:
-        dt, raw = tensors[n]
-        if half_bf16 and dt == "BF16" or not half_bf16 and dt == "F16":
-            half[n] = raw.reshape(-1).astype(np.uint16)
-        else:  # rounded to bf16, as the engine does
-            half[n] = stw.bf16_bits(f32[n]).reshape(-1)
-    return f32, half, half_bf16
+    for n in tensors:
+        if n.endswith("norm.weight"):
+            half[n] = f32[n].astype(np.float16).view(np.uint16).reshape(-1)
+    dt, raw = tensors["model.embed_tokens.weight"]
+    embed_bf16 = dt != "F16"
+    half["model.embed_tokens.weight"] = (raw.reshape(-1).astype(np.uint16) if dt in ("BF16", "F16")
+                                         else stw.bf16_bits(f32["model.embed_tokens.weight"]).reshape(-1))
+    return f32, half, embed_bf16
 
 
 def _cfg(rf, c):
@@ -65,9 +66,9 @@ def _cfg(rf, c):
     return rf.model_config(max_seq=c["max_seq"], **d)
 
 
-def _oracle(orc, c, f32, half, half_bf16):
+def _oracle(orc, c, f32, half, embed_bf16):
     m = orc.Model(c, 1)
-    m.load_checkpoint(f32, half, half_bf16)
+    m.load_checkpoint(f32, half, embed_bf16)
     return m
 
 
@@ -86,12 +87,12 @@ def _check_same(eng, ref, c, prompt, n_new):
 ])
 def test_checkpoint_tokens_match_oracle(rf, orc, tmp_path, c, dtype, norm_dtype, tied):
     path = str(tmp_path / "model.safetensors")
-    f32, half, half_bf16 = make_checkpoint(path, c, seed=len(dtype) + tied, dtype=dtype, tied=tied,
+    f32, half, embed_bf16 = make_checkpoint(path, c, seed=len(dtype) + tied, dtype=dtype, tied=tied,
                                            norm_dtype=norm_dtype)
     print(f"checkpoint {dtype}/{norm_dtype} tied={tied} dim={c['dim']}", flush=True)
     eng = rf.Engine.from_safetensors(_cfg(rf, c), path)
-    assert eng.half_bf16() == half_bf16
-    ref = _oracle(orc, c, f32, half, half_bf16)
+    assert eng.embed_bf16() == embed_bf16
+    ref = _oracle(orc, c, f32, half, embed_bf16)
     for layer in range(c["n_layers"]):
         for p in range(7):
             cg, sg = eng.weight_host(layer, p)
@@ -105,13 +106,13 @@ def test_checkpoint_tokens_match_oracle(rf, orc, tmp_path, c, dtype, norm_dtype,
     ref.close()
 
 
-def test_checkpoint_prefill_with_bf16_norms(rf, orc, tmp_path):
-    """The batched prefill reads the bf16 norms and embeddings too."""
+def test_checkpoint_prefill_with_bf16_embeddings(rf, orc, tmp_path):
+    """The batched prefill gathers bf16 embedding rows too."""
     c = TINY128
     path = str(tmp_path / "model.safetensors")
-    f32, half, half_bf16 = make_checkpoint(path, c, seed=9)
+    f32, half, embed_bf16 = make_checkpoint(path, c, seed=9)
     eng = rf.Engine.from_safetensors(_cfg(rf, c), path)
-    ref = _oracle(orc, c, f32, half, half_bf16)
+    ref = _oracle(orc, c, f32, half, embed_bf16)
     prompt = list(range(5, 45))
     tok = eng.prefill(prompt, 0)
     rtok, rlog = ref.prefill(prompt, 0, want_logits=True)
@@ -134,7 +135,7 @@ def test_packed_cache_round_trip(rf, orc, tmp_path):
     prompt = [3, 9, 27, 81]
     want = eng.generate(prompt, 0, 16)
     eng2 = rf.Engine.load(pack, max_seq=100)
-    assert eng2.cfg.max_seq == 100 and eng2.cfg.dim == c["dim"] and eng2.half_bf16()
+    assert eng2.cfg.max_seq == 100 and eng2.cfg.dim == c["dim"] and eng2.embed_bf16()
     for layer in (-1, 0, 1):
         for p in (range(7) if layer >= 0 else [0]):
             a, b = eng.weight_host(layer, p), eng2.weight_host(layer, p)

@@ -81,6 +81,32 @@ def test_f16_widening_is_exact_on_every_pattern(tmp_path):
     assert np.array_equal(got[np.isinf(ref)], ref[np.isinf(ref)])
 
 
+def test_f16_rounding_matches_numpy(tmp_path):
+    """rfp4_st_read_f16 (how the engine stores norm weights): every bf16 bit
+    pattern, and f32 values across the f16 normal, subnormal and overflow
+    ranges, round to nearest even exactly as numpy's float16 conversion."""
+    raw = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    r = _rng(7)
+    f = np.concatenate([
+        r.standard_normal(20000) * 10.0 ** r.uniform(-9, 5, 20000),
+        np.array([65504, 65519.99, 65520, 65536, 2 ** -24, 2 ** -25, 2 ** -25 * 1.0000001, 3 * 2 ** -26,
+                  6.1e-5, 6.0e-5, 1.0009765625, 1.00048828125, 1.000732421875, -0.0, 0.0], np.float64),
+    ]).astype(np.float32)
+    p = str(tmp_path / "h.safetensors")
+    stw.write(p, {"b": ("BF16", raw), "f": ("F32", f)})
+    with rfp4.SafeTensors(p) as st:
+        got_b, got_f = st.read_f16("b"), st.read_f16("f")
+    for got, vals in ((got_b, stw.bf16_to_f32(raw)), (got_f, f)):
+        ref = vals.astype(np.float16).view(np.uint16)
+        nan = np.isnan(vals)
+        np.testing.assert_array_equal(got[~nan], ref[~nan])
+        assert np.all(np.isnan(got[nan].view(np.float16)))
+    # bf16 gains between 2^-17 and 65504 survive exactly
+    b = stw.bf16_to_f32(raw)
+    ok = np.isfinite(b) & (np.abs(b) >= 2.0 ** -17) & (np.abs(b) <= 65504)
+    np.testing.assert_array_equal(got_b[ok].view(np.float16).astype(np.float32), b[ok])
+
+
 def _raw_file(path, header_obj, data=b"", hlen=None):
     h = header_obj if isinstance(header_obj, bytes) else json.dumps(header_obj).encode()
     with open(path, "wb") as f:
