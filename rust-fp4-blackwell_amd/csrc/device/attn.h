@@ -271,15 +271,18 @@ RFP4_DEV void attn_body(const AttnArgs &a)
     }
 #undef RFP4_ATTN_LOAD
 
-    // lanes li, li+LPT, ... of a wave hold the same dims: fold them
+    // lanes li, li+LPT, ... of a wave hold the same dims: fold them (xor 8 by
+    // DPP, 16 and 32 by the row-swap instructions; same sums as shuffles)
 #pragma unroll
     for (int g = 0; g < ATTN_MAX_GROUP; g++) {
         if ((uint32_t)g >= G) break;
 #pragma unroll
         for (int e = 0; e < EPL; e++) {
             float v = acc[g][e];
-            for (int off = LPT; off < 64; off <<= 1) v += __shfl_xor(v, off, 64);
-            acc[g][e] = v;
+            if (LPT <= 4) v += __shfl_xor(v, 4, 64);
+            if (LPT <= 8) v += dpp_mov<DPP_ROW_ROR8>(v);
+            if (LPT <= 16) v = xor16_sum(v);
+            acc[g][e] = xor32_sum(v);
         }
     }
     if (lane < LPT) {
@@ -333,23 +336,34 @@ RFP4_DEV void attn_merge_body(const AttnArgs &a)
     constexpr uint32_t Q = HD / 4, P = 256 / Q, STRIDE = HD + 4;
     __shared__ float sh[P][Q][6];
     const uint32_t row = blockIdx.z;
+    const uint32_t h = blockIdx.x; // the partial state of head h sits at (h * max_splits + split) * STRIDE
+    const uint32_t q = threadIdx.x % Q, p = threadIdx.x / Q;
+    const float *hp = a.part + (size_t)row * a.n_heads * a.max_splits * STRIDE + (size_t)h * a.max_splits * STRIDE;
+    // the first batch is loaded before the split count is known (indices
+    // clamped inside the workspace; states past the count are discarded), so
+    // the position read and these loads are one round trip
+    float2 ml[ATTN_MERGE_BATCH];
+    float4 v[ATTN_MERGE_BATCH];
+#pragma unroll
+    for (int j = 0; j < ATTN_MERGE_BATCH; j++) {
+        const uint32_t sp = min(p + P * j, a.max_splits - 1u);
+        ml[j] = *(const float2 *)(hp + (size_t)sp * STRIDE);
+        v[j] = *(const float4 *)(hp + (size_t)sp * STRIDE + 4 + q * 4);
+    }
     uint32_t seq = (a.pos_ptr ? (uint32_t)(*a.pos_ptr + 1) : a.seq) + row;
     seq = min(seq, a.chunk * a.max_splits);
     const uint32_t nsplit = (seq + a.chunk - 1) / a.chunk;
     if (nsplit <= 1) return;
-    const uint32_t h = blockIdx.x; // the partial state of head h sits at (h * max_splits + split) * STRIDE
-    const uint32_t q = threadIdx.x % Q, p = threadIdx.x / Q;
-    const float *hp = a.part + (size_t)row * a.n_heads * a.max_splits * STRIDE + (size_t)h * a.max_splits * STRIDE;
     float M = -3.402823466e38f, L = 0.0f;
     float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
     for (uint32_t sp0 = p; sp0 < nsplit; sp0 += P * ATTN_MERGE_BATCH) {
-        float2 ml[ATTN_MERGE_BATCH];
-        float4 v[ATTN_MERGE_BATCH];
+        if (sp0 != p) {
 #pragma unroll
-        for (int j = 0; j < ATTN_MERGE_BATCH; j++) {
-            const uint32_t sp = min(sp0 + P * j, nsplit - 1u);
-            ml[j] = *(const float2 *)(hp + (size_t)sp * STRIDE);
-            v[j] = *(const float4 *)(hp + (size_t)sp * STRIDE + 4 + q * 4);
+            for (int j = 0; j < ATTN_MERGE_BATCH; j++) {
+                const uint32_t sp = min(sp0 + P * j, nsplit - 1u);
+                ml[j] = *(const float2 *)(hp + (size_t)sp * STRIDE);
+                v[j] = *(const float4 *)(hp + (size_t)sp * STRIDE + 4 + q * 4);
+            }
         }
 #pragma unroll
         for (int j = 0; j < ATTN_MERGE_BATCH; j++) {

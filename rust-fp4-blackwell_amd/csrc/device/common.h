@@ -15,6 +15,7 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 #define DPP_QUAD_2301 0x4E   // quad_perm [2,3,0,1]
 #define DPP_ROW_MIRROR 0x140
 #define DPP_ROW_HALF_MIRROR 0x141
+#define DPP_ROW_ROR8 0x128   // row_ror:8 = lane ^ 8 within a row of 16
 
 
 template <int CTRL>
@@ -40,6 +41,23 @@ RFP4_DEV float wave_sum(float v)
     v += __shfl_xor(v, 16, 64);
     v += __shfl_xor(v, 32, 64);
     return v;
+}
+
+// v + v(lane ^ 16) and v + v(lane ^ 32) on the gfx950 row-swap
+// instructions (no LDS round trip).  permlane16_swap(v, v) returns v with odd
+// rows replaced by the even row below and v with even rows replaced by the
+// odd row above; the sum of the pair is v + v^16 in every lane (pinned on the
+// device), likewise permlane32_swap for the two halves of the wave.
+RFP4_DEV float xor16_sum(float v)
+{
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+}
+
+RFP4_DEV float xor32_sum(float v)
+{
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
 }
 
 RFP4_DEV float wave_max(float v)
