@@ -73,8 +73,8 @@ RFP4_DEV float group_sum(float v)
     v += dpp_mov<DPP_QUAD_2301>(v);
     if (N >= 8) v += dpp_mov<DPP_ROW_HALF_MIRROR>(v);
     if (N >= 16) v += dpp_mov<DPP_ROW_MIRROR>(v);
-    if (N >= 32) v += __shfl_xor(v, 16, 64);
-    if (N >= 64) v += __shfl_xor(v, 32, 64);
+    if (N >= 32) v = xor16_sum(v);
+    if (N >= 64) v = xor32_sum(v);
     return v;
 }
 

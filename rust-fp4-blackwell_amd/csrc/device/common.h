@@ -34,15 +34,6 @@ RFP4_DEV float row16_sum(float v)
     return v;
 }
 
-// Sum over all 64 lanes; every lane gets the total.
-RFP4_DEV float wave_sum(float v)
-{
-    v = row16_sum(v);
-    v += __shfl_xor(v, 16, 64);
-    v += __shfl_xor(v, 32, 64);
-    return v;
-}
-
 // v + v(lane ^ 16) and v + v(lane ^ 32) on the gfx950 row-swap
 // instructions (no LDS round trip).  permlane16_swap(v, v) returns v with odd
 // rows replaced by the even row below and v with even rows replaced by the
@@ -60,15 +51,32 @@ RFP4_DEV float xor32_sum(float v)
     return __uint_as_float(p[0]) + __uint_as_float(p[1]);
 }
 
+RFP4_DEV float xor16_max(float v)
+{
+    const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+
+RFP4_DEV float xor32_max(float v)
+{
+    const auto p = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+}
+
+// Sum over all 64 lanes; every lane gets the total.
+RFP4_DEV float wave_sum(float v)
+{
+    return xor32_sum(xor16_sum(row16_sum(v)));
+}
+
+
 RFP4_DEV float wave_max(float v)
 {
     v = fmaxf(v, dpp_mov<DPP_QUAD_1032>(v));
     v = fmaxf(v, dpp_mov<DPP_QUAD_2301>(v));
     v = fmaxf(v, dpp_mov<DPP_ROW_HALF_MIRROR>(v));
     v = fmaxf(v, dpp_mov<DPP_ROW_MIRROR>(v));
-    v = fmaxf(v, __shfl_xor(v, 16, 64));
-    v = fmaxf(v, __shfl_xor(v, 32, 64));
-    return v;
+    return xor32_max(xor16_max(v));
 }
 
 // ---------------------------------------------------------------- E2M1 / E8M0
