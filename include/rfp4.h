@@ -170,6 +170,12 @@ int rfp4_debug_gemm_plan(int tile, int kz);
 /* Test hook: tokens per split of later attn_decode / attn_decode_f16 calls
  * on this thread (0 = automatic).  No reference counterpart. */
 int rfp4_debug_attn_chunk(uint32_t chunk);
+/* Test hook: how later one-row attention launches on this thread (and
+ * engines created by it) merge their splits: 0 = automatic (in-kernel up to
+ * 8 splits, else a second kernel), 1 = always a second kernel, 2 = the last
+ * split of each KV head inside the attention kernel wherever it can (at most
+ * 8 splits).  No reference counterpart. */
+int rfp4_debug_attn_merge(int mode);
 /* The tile and K split fp4_gemm would use for this shape (honours the test
  * hook).  No reference counterpart. */
 int rfp4_gemm_plan(uint32_t m, uint32_t n, uint32_t k, int *tile_m, int *tile_n, int *kz);

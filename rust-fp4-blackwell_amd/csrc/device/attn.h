@@ -78,6 +78,75 @@ RFP4_DEV float group_sum(float v)
     return v;
 }
 
+// ---- in-kernel merge of the split states (no fence).  Every word another
+// workgroup reads is written and read with agent-scope atomic accesses
+// (global_store / global_load sc1: coherent on their own on gfx950, as the
+// compiler's own release/acquire sequences assume), so publishing them
+// needs only their completion (s_waitcnt vmcnt(0)) before the arrival
+// counter is bumped; no L2 writeback or invalidate.  No workgroup waits for
+// another: the one that arrives last merges, the others exit.
+RFP4_DEV void attn_store_agent(float *p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+RFP4_DEV float attn_load_agent(const float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
+
+#define ATTN_INMERGE_MAX_SPLITS 8
+// The last split's merge (at most ATTN_INMERGE_MAX_SPLITS splits): every
+// thread first issues the loads of its outputs' split values (two outputs of
+// the G x HD per thread), one wave per query head turns (m_i, l_i) into the
+// weights e^(m_i - M) and L, then each output is sum_i w_i acc_i / L with the
+// splits in order.  One round trip of loads.
+template <int HD>
+RFP4_DEV void attn_merge_last(const AttnArgs &a, const float *prow, uint32_t kvh, uint32_t G, uint32_t nsplit)
+{
+    constexpr int S = ATTN_INMERGE_MAX_SPLITS, OPT = ATTN_MAX_GROUP * HD / 256; // outputs per thread (max)
+    __shared__ uint32_t s_last;
+    __shared__ float s_w[ATTN_MAX_GROUP][S], s_L[ATTN_MAX_GROUP];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t stride = HD + 4;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // this thread's states have landed
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(a.counters + kvh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = old + 1u == nsplit ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    if (tid == 0) __hip_atomic_store(a.counters + kvh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); // for the next launch
+    // split values of this thread's outputs i = tid + 256 j
+    float v[OPT][S];
+#pragma unroll
+    for (int j = 0; j < OPT; j++) {
+        const uint32_t i = (uint32_t)tid + 256u * (uint32_t)j;
+        const uint32_t g = i / HD, d = i % HD;
+        const float *hp = prow + (size_t)(kvh * G + min(g, G - 1u)) * a.max_splits * stride + 4 + d;
+#pragma unroll
+        for (int sp = 0; sp < S; sp++) v[j][sp] = (g < G && (uint32_t)sp < nsplit) ? attn_load_agent(hp + (size_t)sp * stride) : 0.0f;
+    }
+    // weights per head (one wave per head; lane = split)
+    for (uint32_t g = (uint32_t)wave; g < G; g += 4) {
+        const float *hp = prow + (size_t)(kvh * G + g) * a.max_splits * stride;
+        const bool in = (uint32_t)lane < nsplit;
+        const float m = in ? attn_load_agent(hp + (size_t)lane * stride) : -3.402823466e38f;
+        const float l = in ? attn_load_agent(hp + (size_t)lane * stride + 1) : 0.0f;
+        const float M = wave_max(m);
+        const float w = in ? expf(m - M) : 0.0f;
+        if (in) s_w[g][lane] = w;
+        const float L = wave_sum(l * w);
+        if (lane == 0) s_L[g] = L;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < OPT; j++) {
+        const uint32_t i = (uint32_t)tid + 256u * (uint32_t)j;
+        const uint32_t g = i / HD, d = i % HD;
+        if (g >= G) break;
+        float acc = 0.0f;
+#pragma unroll
+        for (int sp = 0; sp < S; sp++)
+            if ((uint32_t)sp < nsplit) acc = fmaf(s_w[g][sp], v[j][sp], acc);
+        a.out[(size_t)(kvh * G + g) * HD + d] = __fdiv_rn(acc, s_L[g]);
+    }
+}
+
 template <int HD, typename KT>
 RFP4_DEV void attn_body(const AttnArgs &a)
 {
@@ -306,18 +375,30 @@ RFP4_DEV void attn_body(const AttnArgs &a)
     }
 
     // ---- write this split's partial state: [m, l, -, -, acc[HD]] per (head, split);
-    // the merge kernel launched next on the same stream combines them
+    // the merge kernel launched next on the same stream combines them, or
+    // (counters given) the last split of this KV head to arrive does
     const uint32_t stride = HD + 4;
+    const bool inmerge = a.counters != nullptr;
     for (uint32_t i = tid; i < G * HD; i += blockDim.x) {
         uint32_t g = i / HD, d = i % HD;
         float v = vred[0][g][d] + vred[1][g][d] + vred[2][g][d] + vred[3][g][d];
         size_t base = ((size_t)(kvh * G + g) * a.max_splits + split) * stride;
-        prow[base + 4 + d] = v;
-        if (d == 0) {
-            prow[base] = s_m[g];
-            prow[base + 1] = s_l[g];
+        if (inmerge) {
+            attn_store_agent(prow + base + 4 + d, v);
+            if (d == 0) {
+                attn_store_agent(prow + base, s_m[g]);
+                attn_store_agent(prow + base + 1, s_l[g]);
+            }
+        } else {
+            prow[base + 4 + d] = v;
+            if (d == 0) {
+                prow[base] = s_m[g];
+                prow[base + 1] = s_l[g];
+            }
         }
     }
+    if (!inmerge) return;
+    attn_merge_last<HD>(a, prow, kvh, G, nsplit);
 }
 
 // Merge kernel body: grid (n_heads), launched after attn_body on the same

@@ -52,6 +52,7 @@ struct llama_engine {
     uint32_t n_best = 0;
     float *attn_part = nullptr;
     uint32_t attn_chunk = 64, attn_max_splits = 1;
+    uint32_t *attn_counters = nullptr; // in-kernel merge of the decode step (null: merge kernel)
     StepState *state = nullptr;
     uint32_t *ids = nullptr, *last_tok = nullptr;
     uint32_t ids_alloc = 0;
@@ -119,6 +120,7 @@ static int enqueue_step(llama_engine *e)
         aa.ts = hd; aa.hs = (uint64_t)e->max_seq_alloc * hd;
         aa.n_heads = c.n_heads; aa.n_kv_heads = c.n_kv_heads; aa.head_dim = hd; aa.seq = 0;
         aa.chunk = e->attn_chunk; aa.max_splits = e->attn_max_splits;
+        aa.counters = e->attn_counters;
         if ((rc = attn_launch(aa, 1, s, e->attn_chunk * e->attn_max_splits, 1))) return rc;
         GemvArgs oa{w.o_c, w.o_s, e->attn_out, e->x, nullptr, nullptr, c.dim, qd, 0, 0.0f};
         if ((rc = gemv_launch("e8m0", RFP4_EPI_RESIDUAL, oa, s, 0))) return rc;
@@ -326,6 +328,10 @@ static int engine_alloc(const rfp4_model_config *cfg, llama_engine **out)
     e->n_best = gemv_blocks(c.vocab, c.dim, RFP4_EPI_ARGMAX);
     if (!rc) rc = dalloc_t(e, &e->best, e->n_best);
     if (!rc) rc = dalloc_t(e, &e->attn_part, (size_t)c.n_heads * e->attn_max_splits * (hd + 4));
+    if (!rc && attn_inmerge(e->attn_max_splits)) {
+        rc = dalloc_t(e, &e->attn_counters, c.n_kv_heads);
+        if (!rc) rc = fill_words(e->attn_counters, c.n_kv_heads, 0u, s);
+    }
     if (!rc) rc = dalloc(e, (void **)&e->state, sizeof(StepState));
     e->ids_alloc = c.max_seq + 2;
     if (!rc) rc = dalloc_t(e, &e->ids, e->ids_alloc);

@@ -108,10 +108,14 @@ int rfp4_init(int device)
     rc = hip_check(hipMalloc((void **)&rt->attn_part, rt->attn_part_floats * sizeof(float)), "hipMalloc(attn workspace)");
     // split-K workspace of fp4_gemm
     if (!rc) rc = hip_check(hipMalloc((void **)&rt->gemm_part, kGemmPartFloats * sizeof(float)), "hipMalloc(gemm workspace)");
+    // arrival counters of the in-kernel attention merge: zero between calls
+    if (!rc) rc = hip_check(hipMalloc((void **)&rt->attn_counters, kAttnMaxHeads * sizeof(uint32_t)), "hipMalloc(attn counters)");
+    if (!rc) rc = hip_check(hipMemset(rt->attn_counters, 0, kAttnMaxHeads * sizeof(uint32_t)), "hipMemset(attn counters)");
     if (!rc) rc = hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
     if (rc) {
         hipFree(rt->attn_part);
         hipFree(rt->gemm_part);
+        hipFree(rt->attn_counters);
         hipModuleUnload(rt->module);
         delete rt;
         return rc;
@@ -270,6 +274,16 @@ GemvVariant gemv_variant(uint32_t n, uint32_t k, int epi, bool f32scale)
     return GemvVariant{R, ns, W};
 }
 
+static thread_local int t_attn_merge = 0; // 0 automatic, 1 merge kernel, 2 in-kernel merge where it fits
+
+bool attn_inmerge(uint32_t max_splits)
+{
+    // In-kernel when the last split's merge is one round of loads (few
+    // splits); above that, the second kernel's parallel merge is faster.
+    if (max_splits <= 1 || max_splits > kAttnInmergeMaxSplits) return false;
+    return t_attn_merge != 1;
+}
+
 // Path: 0 = automatic, 1 = VALU kernel, 2 = bf16 MFMA kernel, 3 = block-scaled
 // MFMA kernel (forced paths: tests only).
 static thread_local int t_force_path = 0;
@@ -404,6 +418,14 @@ extern "C" int rfp4_debug_gemv_path(int path)
     return RFP4_OK;
 }
 
+extern "C" int rfp4_debug_attn_merge(int mode)
+{
+    using namespace rfp4;
+    if (mode < 0 || mode > 2) return set_error(RFP4_E_INVALID, "merge mode must be 0 (auto), 1 (merge kernel) or 2 (in-kernel)");
+    t_attn_merge = mode;
+    return RFP4_OK;
+}
+
 extern "C" int rfp4_debug_gemv_waves(int waves)
 {
     using namespace rfp4;
@@ -434,10 +456,12 @@ int attn_launch(const AttnArgs &args, int kv_f16, hipStream_t s, uint32_t max_se
     if (args.chunk == 0) return set_error(RFP4_E_INVALID, "attn: chunk must be positive");
     if (args.cosv && !kv_f16) return set_error(RFP4_E_INVALID, "attn: fused KV append needs an fp16 cache");
     if (rows == 0 || (rows > 1 && args.cosv)) return set_error(RFP4_E_INVALID, "attn: fused append is one row only");
+    if (args.counters && (rows != 1 || args.max_splits > kAttnInmergeMaxSplits))
+        return set_error(RFP4_E_INVALID, "attn: the in-kernel merge takes one row and at most %u splits", kAttnInmergeMaxSplits);
     uint32_t splits = (max_seq_for_grid + args.chunk - 1) / args.chunk;
     AttnArgs a = args;
     int rc = launch(name, dim3(a.n_kv_heads, splits, rows), dim3(256), s, &a);
-    if (rc || splits <= 1) return rc;
+    if (rc || splits <= 1 || a.counters) return rc;
     // the split states are merged by a second launch (stream order, no fence)
     return launch(args.head_dim == 64 ? "rfp4_attn_merge_hd64" : "rfp4_attn_merge_hd128", dim3(a.n_heads, 1, rows),
                   dim3(256), s, &a);
@@ -634,6 +658,7 @@ static int attn_common(hipStream_t s, uint32_t nh, uint32_t nkv, uint32_t hd, ui
     a.ts = ts; a.hs = hs;
     a.n_heads = nh; a.n_kv_heads = nkv; a.head_dim = hd; a.seq = seq;
     a.chunk = chunk; a.max_splits = splits;
+    if (attn_inmerge(splits)) a.counters = rt->attn_counters;
     return attn_launch(a, f16, s, seq, 1);
 }
 

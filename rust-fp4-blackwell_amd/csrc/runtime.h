@@ -23,6 +23,7 @@ struct Runtime {
     float *attn_part = nullptr;       // default split-K workspace of attn_decode
     size_t attn_part_floats = 0;
     float *gemm_part = nullptr;       // split-K partials of fp4_gemm (kGemmPartFloats)
+    uint32_t *attn_counters = nullptr; // in-kernel attention merge (kAttnMaxHeads words, zero between calls)
     size_t max_lds = 65536;           // LDS bytes per workgroup
 };
 
@@ -41,6 +42,10 @@ int gemv_launch(const char *scale_name, int epi, const GemvArgs &args, hipStream
 uint32_t gemv_blocks(uint32_t n_logical, uint32_t k, int epi);
 int attn_launch(const AttnArgs &args, int kv_f16, hipStream_t s, uint32_t max_seq_for_grid, uint32_t rows);
 uint32_t attn_sub_chunk(uint32_t head_dim, uint32_t elem_bytes);
+// Whether one-row attention with `max_splits` splits merges inside the split
+// kernel (arrival counters) instead of in a second launch.
+bool attn_inmerge(uint32_t max_splits);
+constexpr uint32_t kAttnInmergeMaxSplits = 8;
 uint32_t attn_chunk_for(uint32_t n_kv_heads, uint32_t seq, uint32_t num_cus, uint32_t head_dim, uint32_t elem_bytes);
 
 // sigma / sqrt((65536^2 - 1)/3): the Irwin-Hall(4) normal coefficient shared

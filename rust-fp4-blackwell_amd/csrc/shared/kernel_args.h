@@ -91,6 +91,10 @@ typedef struct AttnArgs {
     // writes out + r*out_rs, sees seq + r positions (causal), and owns its own
     // workspace slice of n_heads*max_splits*(head_dim+4) floats.  One row: 0, 0.
     uint32_t q_rs, out_rs;
+    // In-kernel merge (one query row): arrival counters per KV head, zero
+    // between launches; the last split of a KV head merges.  Null = the
+    // merge kernel runs after this one.
+    uint32_t *counters;
 } AttnArgs;
 
 // Batched prefill row kernels (device/prefill.h).

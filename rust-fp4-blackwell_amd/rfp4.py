@@ -91,6 +91,7 @@ _SIGS = {
     "rfp4_selftest_cvt_fp4": (I32, [P, U32, P, P]),
     "rfp4_debug_gemv_variant": (I32, [I32, I32]),
     "rfp4_debug_gemv_waves": (I32, [I32]),
+    "rfp4_debug_attn_merge": (I32, [I32]),
     "rfp4_debug_gemv_path": (I32, [I32]),
     "rfp4_debug_gemv_fused": (I32, [P, I32, U32, U32, U32, P, P, P, P, F32, P, P, P]),
     "rfp4_selftest_cvt_bf16": (I32, [P, U32, P, P, P]),

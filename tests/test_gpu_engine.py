@@ -95,3 +95,25 @@ def test_engine_errors(rf):
     with pytest.raises(rf.Rfp4Error):
         eng.generate([TINY["vocab"]], 0, 1)             # token out of range
     eng.close()
+
+
+@pytest.mark.parametrize("cfg", [TINY, TINY128])
+@pytest.mark.parametrize("mode", [1, 2])
+def test_engine_attn_merge_modes_tokens(rf, orc, cfg, mode):
+    """The decode step with the attention splits merged by a second kernel
+    (mode 1) and inside the attention kernel (mode 2): the same greedy tokens
+    as the oracle over a context that needs several splits."""
+    seed = 0x1A2B
+    rf.check(rf.load().rfp4_debug_attn_merge(mode))
+    rf.debug_attn_chunk(cfg["max_seq"] // 6 + 1)  # 6 splits over the context
+    try:
+        eng = _engine(rf, cfg, seed)
+    finally:
+        rf.debug_attn_chunk(0)
+        rf.check(rf.load().rfp4_debug_attn_merge(0))
+    ref = orc.Model(cfg, seed)
+    prompt = [2, 9, 77, 401, 5, 6, 7]
+    gpu = eng.generate(prompt, 0, 30)
+    cpu, margins = ref.generate(prompt, 0, 30)
+    assert list(gpu) == list(cpu), f"gpu {list(gpu)}\ncpu {list(cpu)}\nmargins {margins}"
+    eng.close()

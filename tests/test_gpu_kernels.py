@@ -458,3 +458,40 @@ def test_attn_decode_reference_layout_forced_chunk(rf, orc, stream):
     finally:
         rf.debug_attn_chunk(0)
     _assert_attn_close(dout.to_host(NH * HD, np.float32, stream), oref)
+
+
+@pytest.mark.parametrize("nh,nkv,hd,seq,chunk", [(32, 8, 128, 4097, 640), (32, 4, 64, 272, 0), (32, 8, 128, 300, 64),
+                                                 (64, 8, 128, 2500, 320), (32, 4, 64, 1500, 192), (16, 16, 64, 65, 16),
+                                                 (32, 8, 128, 2500, 1000), (8, 1, 128, 5000, 640), (32, 4, 64, 100, 0)])
+def test_attn_decode_f16_inkernel_merge(rf, orc, stream, nh, nkv, hd, seq, chunk):
+    """The last split of each KV head merges inside the attention kernel
+    (agent-scope atomic states, arrival counter, no second launch): against
+    the oracle, against the merge kernel, and identical over 20 repeats (a
+    stale state would show as a changed result)."""
+    rng = np.random.default_rng(seq + hd + nkv)
+    q = rng.standard_normal(nh * hd).astype(np.float32)
+    cap = seq + 3
+    kc = rng.standard_normal(nkv * cap * hd).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal(nkv * cap * hd).astype(np.float16).view(np.uint16)
+    oref = orc.attn_decode(nh, nkv, hd, seq, q, kc, vc, hd, cap * hd)
+    dq, dk, dv = _dev(rf, q, stream), _dev(rf, kc, stream), _dev(rf, vc, stream)
+    dout = rf.DeviceBuffer.zeroed(nh * hd, np.float32, stream)
+    outs = {}
+    rf.debug_attn_chunk(chunk)
+    try:
+        for mode in (1, 2):
+            rf.check(rf.load().rfp4_debug_attn_merge(mode))
+            reps = []
+            for _ in range(20 if mode == 2 else 1):
+                rf.attn_decode_f16(stream, nh, nkv, hd, seq, dq, dk, dv, hd, cap * hd, dout)
+                reps.append(dout.to_host(nh * hd, np.float32, stream))
+            for r in reps[1:]:
+                np.testing.assert_array_equal(r, reps[0])
+            outs[mode] = reps[0]
+    finally:
+        rf.debug_attn_chunk(0)
+        rf.check(rf.load().rfp4_debug_attn_merge(0))
+    _assert_attn_close(outs[2], oref)
+    _assert_attn_close(outs[1], oref)
+    scale = np.abs(outs[1]).max()
+    assert np.max(np.abs(outs[2] - outs[1])) <= 1e-6 * scale
