@@ -9,7 +9,8 @@
 // Mapping (wave64): lane l owns 16-byte chunk c = l + 64*s of every row it
 // touches (32 codes = exactly one scale block), so one global_load_dwordx4
 // per row covers 1 KiB of a row contiguously across the wave.  A workgroup
-// (4 waves, 4R logical rows) stages x in LDS once -- optionally RMS-normalized
+// (4 waves, 4R logical rows) stages x in LDS once (36 floats per 32-value
+// chunk, which keeps the per-lane reads free of bank conflicts) -- optionally RMS-normalized
 // on the way (the rmsnorm launch of llama_run/src/main.rs:513,525 folded in)
 // -- and each lane reads its 32 activations per slice from LDS and reuses them
 // for all R rows of its wave.  Weight loads are double-buffered across
@@ -31,6 +32,15 @@ RFP4_DEV float silu_ref(float g)
     return __fdiv_rn(g, __fadd_rn(1.0f, expf(-g)));
 }
 
+// x in LDS: each 32-value chunk (one scale block) takes 36 floats, so chunk
+// c starts at 16-byte slot 9c.  The dot loops read the same float4 of 64
+// consecutive chunks at once (one chunk per lane); at 9 slots per chunk any
+// 16 consecutive lanes fall on 16 distinct 16-byte bank groups (no conflict
+// with 64 four-byte banks, nor with 32), where packed 128-byte chunks would
+// put a whole wave on one or two bank groups.
+#define GEMV_XS_CHUNK 36u
+RFP4_DEV uint32_t xs_slot(uint32_t i4) { return (i4 >> 3) * 9u + (i4 & 7u); } // LDS float4 of x float4 i4
+
 // Stage x (K floats) into LDS; with norm_w, store x * rms * w instead
 // (rms = 1/sqrt(sum(x^2)/K + eps), llama_rmsnorm/src/main.rs:75-77).
 RFP4_DEV void stage_x(float *xs, const float *x, uint32_t k, const uint16_t *norm_w, float eps)
@@ -38,15 +48,16 @@ RFP4_DEV void stage_x(float *xs, const float *x, uint32_t k, const uint16_t *nor
     __shared__ float red[4];
     const int tid = threadIdx.x;
     const uint32_t k4 = k >> 2;
+    float4 *xs4 = (float4 *)xs;
     if (norm_w == nullptr) {
-        for (uint32_t i = tid; i < k4; i += 256) ((float4 *)xs)[i] = ((const float4 *)x)[i];
+        for (uint32_t i = tid; i < k4; i += 256) xs4[xs_slot(i)] = ((const float4 *)x)[i];
         __syncthreads();
         return;
     }
     float ss = 0.0f;
     for (uint32_t i = tid; i < k4; i += 256) {
         float4 v = ((const float4 *)x)[i];
-        ((float4 *)xs)[i] = v;
+        xs4[xs_slot(i)] = v;
         ss = __fadd_rn(ss, __fmul_rn(v.x, v.x));
         ss = __fadd_rn(ss, __fmul_rn(v.y, v.y));
         ss = __fadd_rn(ss, __fmul_rn(v.z, v.z));
@@ -57,7 +68,15 @@ RFP4_DEV void stage_x(float *xs, const float *x, uint32_t k, const uint16_t *nor
     __syncthreads();
     float total = (red[0] + red[1]) + (red[2] + red[3]);
     float rms = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(total, (float)k), eps)));
-    for (uint32_t i = tid; i < k; i += 256) xs[i] = __fmul_rn(__fmul_rn(xs[i], rms), f16_bits_to_f32(norm_w[i]));
+    for (uint32_t i = tid; i < k4; i += 256) {
+        float4 v = xs4[xs_slot(i)];
+        const uint16_t *w = norm_w + 4u * i;
+        v.x = __fmul_rn(__fmul_rn(v.x, rms), f16_bits_to_f32(w[0]));
+        v.y = __fmul_rn(__fmul_rn(v.y, rms), f16_bits_to_f32(w[1]));
+        v.z = __fmul_rn(__fmul_rn(v.z, rms), f16_bits_to_f32(w[2]));
+        v.w = __fmul_rn(__fmul_rn(v.w, rms), f16_bits_to_f32(w[3]));
+        xs4[xs_slot(i)] = v;
+    }
     __syncthreads();
 }
 
@@ -99,7 +118,7 @@ RFP4_DEV void stage_x_regs(float *xs, const float4 *xr, const uint2 *wr, uint32_
             o.z = __fmul_rn(__fmul_rn(o.z, rms), f16_bits_to_f32((uint16_t)(wr[v].y & 0xFFFFu)));
             o.w = __fmul_rn(__fmul_rn(o.w, rms), f16_bits_to_f32((uint16_t)(wr[v].y >> 16)));
         }
-        ((float4 *)xs)[i4] = o;
+        ((float4 *)xs)[xs_slot(i4)] = o;
     }
     __syncthreads();
 }
@@ -130,7 +149,7 @@ RFP4_DEV void gemv_body(const GemvArgs &a)
     static_assert(W % 4 == 0 && W <= 16, "waves per workgroup");
     constexpr int NP = (EPI == RFP4_EPI_SWIGLU) ? 2 * R : R;
     constexpr uint32_t T = 64u * W;
-    extern __shared__ float xs[]; // K floats (dynamic LDS)
+    extern __shared__ float xs[]; // K/32 chunks of GEMV_XS_CHUNK floats (dynamic LDS)
     __shared__ unsigned long long s_best[W];
 
     const int lane = threadIdx.x & 63;
@@ -201,7 +220,7 @@ RFP4_DEV void gemv_body(const GemvArgs &a)
             const uint32_t c = (uint32_t)lane + 64u * (uint32_t)s;
             const float live = c < nchunk ? 1.0f : 0.0f;
             float4 xv[8];
-            const float4 *xp = (const float4 *)(xs + (size_t)min(c, clast) * 32u);
+            const float4 *xp = (const float4 *)(xs + (size_t)min(c, clast) * GEMV_XS_CHUNK);
 #pragma unroll
             for (int j = 0; j < 8; j++) xv[j] = xp[j];
 #pragma unroll
@@ -220,7 +239,7 @@ RFP4_DEV void gemv_body(const GemvArgs &a)
                 sc[p] = load_scale<SCALE_F32>(a.scales, srow[p] + c);
             }
             float4 xv[8];
-            const float4 *xp = (const float4 *)(xs + (size_t)c * 32u);
+            const float4 *xp = (const float4 *)(xs + (size_t)c * GEMV_XS_CHUNK);
 #pragma unroll
             for (int j = 0; j < 8; j++) xv[j] = xp[j];
 #pragma unroll

@@ -34,15 +34,18 @@
     GEMV_KERNEL(SNAME, SF32, ENAME, EPI, R, 1) \
     GEMV_KERNEL(SNAME, SF32, ENAME, EPI, R, 2)
 
+GEMV_NS_FULL(e8m0, 0, store, RFP4_EPI_STORE, 1)
 GEMV_NS_FULL(e8m0, 0, store, RFP4_EPI_STORE, 2)
 GEMV_NS_FULL(e8m0, 0, store, RFP4_EPI_STORE, 4)
 GEMV_NS_SHORT(e8m0, 0, store, RFP4_EPI_STORE, 8)
+GEMV_NS_FULL(e8m0, 0, resid, RFP4_EPI_RESIDUAL, 1)
 GEMV_NS_FULL(e8m0, 0, resid, RFP4_EPI_RESIDUAL, 2)
 GEMV_NS_FULL(e8m0, 0, resid, RFP4_EPI_RESIDUAL, 4)
 GEMV_NS_SHORT(e8m0, 0, resid, RFP4_EPI_RESIDUAL, 8)
 GEMV_NS_FULL(e8m0, 0, argmax, RFP4_EPI_ARGMAX, 2)
 GEMV_NS_FULL(e8m0, 0, argmax, RFP4_EPI_ARGMAX, 4)
 GEMV_NS_SHORT(e8m0, 0, argmax, RFP4_EPI_ARGMAX, 8)
+GEMV_NS_FULL(e8m0, 0, swiglu, RFP4_EPI_SWIGLU, 1)
 GEMV_NS_FULL(e8m0, 0, swiglu, RFP4_EPI_SWIGLU, 2)
 // gate/up at R=4: capped at 128 VGPRs (4 waves per SIMD) so that every
 // workgroup of the 8B shape (896) is resident at once

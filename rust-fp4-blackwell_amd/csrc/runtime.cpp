@@ -218,14 +218,18 @@ int fill_words(uint32_t *p, uint64_t n_words, uint32_t value, hipStream_t s)
 
 static bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
+// LDS of the VALU GEMV: x at 36 floats per 32-value chunk (device/gemv.h).
+static uint32_t gemv_lds_bytes(uint32_t k) { return (k / 32u) * 36u * 4u; }
+
 int gemv_check(uint32_t n, uint32_t k, const void *w, const void *sc, const float *x, const float *y)
 {
     if (!w || !sc || !x || !y) return set_error(RFP4_E_INVALID, "gemv: null pointer");
     if (n == 0 || k == 0) return set_error(RFP4_E_SHAPE, "gemv: n=%u k=%u must be > 0", n, k);
     if (k % 32) return set_error(RFP4_E_SHAPE, "gemv: k=%u is not a multiple of the 32-element block", k);
     if (!aligned16(w) || !aligned16(x)) return set_error(RFP4_E_ALIGN, "gemv: w and x must be 16-byte aligned");
-    if (g_rt && (size_t)k * 4u + 256u > g_rt->max_lds)
-        return set_error(RFP4_E_CAPACITY, "gemv: k=%u activations (%u bytes) exceed the %zu-byte LDS plan", k, k * 4u, g_rt->max_lds);
+    if (g_rt && (size_t)gemv_lds_bytes(k) + 256u > g_rt->max_lds)
+        return set_error(RFP4_E_CAPACITY, "gemv: k=%u activations (%u bytes) exceed the %zu-byte LDS plan", k,
+                         gemv_lds_bytes(k), g_rt->max_lds);
     return RFP4_OK;
 }
 
@@ -241,6 +245,7 @@ static bool gemv_has_ns(bool f32scale, int epi, int R, int ns, int W = 4)
     if (ns == 0) return true;
     bool full = ns == 1 || ns == 2 || ns == 3 || ns == 4 || ns == 7;
     if (f32scale) return R == 4 && full;
+    if (R == 1) return epi != RFP4_EPI_ARGMAX && full;
     if (R == 2) return full;
     if (R == 4) return epi == RFP4_EPI_SWIGLU ? (ns >= 1 && ns <= 3) : full;
     if (R == 8) return epi != RFP4_EPI_SWIGLU && (ns == 1 || ns == 2);
@@ -249,18 +254,20 @@ static bool gemv_has_ns(bool f32scale, int epi, int R, int ns, int W = 4)
 
 // Rows per wave R and up-front K-slices NS for a GEMV launch.  NS = K/2048
 // rounded up whenever compiled (all loads in flight at once), else the slice
-// loop.  R = 4 by default; 8 for very wide matrices with short K (fewer,
-// fuller workgroups still fill the device); 2 where 4 rows x NS slices would
-// not fit the register file.
+// loop.  Measured on MI355X with x in conflict-free LDS (weights streamed
+// from HBM, 8B / TinyLlama shapes): R = 1 for the SwiGLU pair (8B gate|up
+// 12.7 us vs 12.9-13.6 at R = 2 and 17.3 at R = 4), R = 2 elsewhere (8B down
+// 9.5 us vs 11.1 at R = 4 and 10.6 at R = 1; q|k|v 5.0 vs 5.2-5.4; TinyLlama
+// LM head 7.9-8.1 vs 8.3 at R = 4), R = 8 for very wide matrices with short
+// K (8B LM head).  f32 scales: R = 4 only.
 GemvVariant gemv_variant(uint32_t n, uint32_t k, int epi, bool f32scale)
 {
     int ns_needed = (int)((k + 2047u) / 2048u);
-    // measured on MI355X: the SwiGLU (gate|up) GEMV is fastest at 2 rows per
-    // wave (4 row streams per wave; 8B gate|up 14.0 us vs 16.3 us at 4 rows)
     int R = 4;
     if (!f32scale) {
-        if (epi == RFP4_EPI_SWIGLU) R = 2;
-        else if (epi != RFP4_EPI_SWIGLU && n >= 65536u && ns_needed <= 2) R = 8;
+        if (epi == RFP4_EPI_SWIGLU) R = gemv_has_ns(f32scale, epi, 1, ns_needed) ? 1 : 2;
+        else if (n >= 65536u && ns_needed <= 2) R = 8;
+        else R = 2;
     }
     // 4 waves per workgroup: 8-wave workgroups (compiled for one-slice
     // shapes) are faster alone (TinyLlama gate|up 6.18 -> 5.42 us) but slower
@@ -393,7 +400,7 @@ int gemv_launch(const char *scale_name, int epi, const GemvArgs &args, hipStream
             snprintf(name, sizeof name, "rfp4_gemv_%s_%s_r%d_s%d", scale_name, epi_names[epi], p.R, p.NS);
         else
             snprintf(name, sizeof name, "rfp4_gemv_%s_%s_r%d_s%d_w%d", scale_name, epi_names[epi], p.R, p.NS, p.W);
-        shmem = args.k * 4u;
+        shmem = gemv_lds_bytes(args.k);
     }
     uint32_t blocks = (args.n + p.rows_per_block - 1) / p.rows_per_block;
     GemvArgs a = args;

@@ -9,10 +9,10 @@ from test_gpu_kernels import _assert_gemv_close, _config1, _dev
 pytestmark = pytest.mark.gpu
 
 _VARIANTS = {  # epilogue -> {R: compiled NS}; mirrors kernels.hip and runtime.cpp gemv_has_ns
-    "store": {2: (0, 1, 2, 3, 4, 7), 4: (0, 1, 2, 3, 4, 7), 8: (0, 1, 2)},
-    "resid": {2: (0, 1, 2, 3, 4, 7), 4: (0, 1, 2, 3, 4, 7), 8: (0, 1, 2)},
+    "store": {1: (0, 1, 2, 3, 4, 7), 2: (0, 1, 2, 3, 4, 7), 4: (0, 1, 2, 3, 4, 7), 8: (0, 1, 2)},
+    "resid": {1: (0, 1, 2, 3, 4, 7), 2: (0, 1, 2, 3, 4, 7), 4: (0, 1, 2, 3, 4, 7), 8: (0, 1, 2)},
     "argmax": {2: (0, 1, 2, 3, 4, 7), 4: (0, 1, 2, 3, 4, 7), 8: (0, 1, 2)},
-    "swiglu": {2: (0, 1, 2, 3, 4, 7), 4: (0, 1, 2, 3)},
+    "swiglu": {1: (0, 1, 2, 3, 4, 7), 2: (0, 1, 2, 3, 4, 7), 4: (0, 1, 2, 3)},
 }
 
 
