@@ -4,18 +4,22 @@
 //   out[h] = softmax((q_h . k_t) * 1/sqrt(HD)) . v_t  over t < seq, kvh = h / (NH/NKV).
 //
 // Grid (n_kv_heads, splits).  A workgroup owns one KV head and `chunk` tokens
-// and serves every query head of its GQA group, so each K/V byte is read from
-// HBM once.  A token row is split over LPT lanes, 16 bytes each.  The split is
-// walked in sub-chunks of as many rows as the registers hold (attn_sub_chunk):
-// every K and V load of a sub-chunk is issued before its arithmetic, the next
-// sub-chunk's K loads go out right after the scores and its V loads right
-// after P.V, and an online softmax (m, l, acc[HD]) carries over.  A split that
-// covers the whole sequence writes the output itself; otherwise each split
-// writes its state and a second kernel (attn_merge_body, same stream) merges
-// them: M = max m_i, L = sum l_i e^(m_i-M), out = sum acc_i e^(m_i-M) / L.
-// (A last-workgroup merge inside this kernel would need an agent-scope
-// release per workgroup, an L2 writeback on gfx950, which costs more than the
-// kernel boundary.)
+// and serves every query head of its GQA group (GT heads at compile time, the
+// real group G <= GT; heads past G carry zero q and write nothing), so each
+// K/V byte is read from HBM once.  A token row is split over LPT lanes, 16
+// bytes each.  The split is walked in sub-chunks of as many rows as the
+// registers hold (attn_steps_for): every K and V load of a sub-chunk is issued
+// before its arithmetic, the next sub-chunk's K loads go out right after the
+// scores and its V loads right after P.V.  Loads that need no position (q, the
+// current token's k and v) go out first, then the rope tables of the position,
+// then K and V, so the rotation of q overlaps the K/V stream.  Scores stay in
+// registers: one cross-wave max per head and sub-chunk, then p = 2^(s - m),
+// l and P.V in registers, an online rescale carrying (m, l, acc[HD]) from one
+// sub-chunk to the next.  A split that covers the whole sequence writes the
+// output itself; otherwise each split writes its state and the states are
+// merged, M = max m_i, L = sum l_i 2^(m_i-M), out = sum acc_i 2^(m_i-M) / L,
+// by the last split to finish (attn_merge_last, few splits) or by a second
+// kernel on the same stream (attn_merge_body).
 //
 // Optional fusion (engine): with rope tables given, q and the current token's
 // k are rotated here (llama_run/src/main.rs:517-518) and the split owning
@@ -26,16 +30,13 @@
 #include "norm_rope.h"
 
 #define ATTN_MAX_GROUP 8
-#define ATTN_MAX_STEPS 9
 
-// 16-byte row pieces each thread holds per sub-chunk: 9 for fp16 rows of 128
-// (144 tokens, so a 4096-token context needs 29 splits per KV head and 8 KV
-// heads fit one workgroup per CU), 8 otherwise.
-template <int HD, typename KT>
-constexpr int attn_steps()
-{
-    return (HD == 128 && sizeof(KT) == 2) ? 9 : 8;
-}
+// Scores are kept in base-2 units, s = (q . k) * (log2(e) / sqrt(HD)), so
+// every exponential is one v_exp_f32 (2^x) of a difference; the split states'
+// m is in the same units (softmax weights are unchanged: 2^(s2 - m2) =
+// e^(s - m)).  Relative error of a weight: the hardware 2^x (about 1 ulp)
+// plus the rounding of the scaled score (|s| * 2^-24).
+RFP4_DEV float attn_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 template <typename KT>
 struct KvTraits;
@@ -78,6 +79,27 @@ RFP4_DEV float group_sum(float v)
     return v;
 }
 
+// Sum / max over the token slots of a wave: lanes that hold the same part of
+// a row (the same lane index within groups of LPT) are combined (xor 4 by a
+// swizzle, xor 8 by DPP row_ror:8, 16 and 32 by the row-swap instructions).
+template <int LPT>
+RFP4_DEV float slots_sum(float v)
+{
+    if (LPT <= 4) v += __shfl_xor(v, 4, 64);
+    if (LPT <= 8) v += dpp_mov<DPP_ROW_ROR8>(v);
+    if (LPT <= 16) v = xor16_sum(v);
+    return xor32_sum(v);
+}
+
+template <int LPT>
+RFP4_DEV float slots_max(float v)
+{
+    if (LPT <= 4) v = fmaxf(v, __shfl_xor(v, 4, 64));
+    if (LPT <= 8) v = fmaxf(v, dpp_mov<DPP_ROW_ROR8>(v));
+    if (LPT <= 16) v = xor16_max(v);
+    return xor32_max(v);
+}
+
 // ---- in-kernel merge of the split states (no fence).  Every word another
 // workgroup reads is written and read with agent-scope atomic accesses
 // (global_store / global_load sc1: coherent on their own on gfx950, as the
@@ -90,16 +112,16 @@ RFP4_DEV float attn_load_agent(const float *p) { return __hip_atomic_load(p, __A
 
 #define ATTN_INMERGE_MAX_SPLITS 8
 // The last split's merge (at most ATTN_INMERGE_MAX_SPLITS splits): every
-// thread first issues the loads of its outputs' split values (two outputs of
-// the G x HD per thread), one wave per query head turns (m_i, l_i) into the
-// weights e^(m_i - M) and L, then each output is sum_i w_i acc_i / L with the
+// thread first issues the loads of its outputs' split values (the G x HD
+// outputs, 256 per pass), one wave per query head turns (m_i, l_i) into the
+// weights 2^(m_i - M) and L, then each output is sum_i w_i acc_i / L with the
 // splits in order.  One round trip of loads.
-template <int HD>
+template <int HD, int GT>
 RFP4_DEV void attn_merge_last(const AttnArgs &a, const float *prow, uint32_t kvh, uint32_t G, uint32_t nsplit)
 {
-    constexpr int S = ATTN_INMERGE_MAX_SPLITS, OPT = ATTN_MAX_GROUP * HD / 256; // outputs per thread (max)
+    constexpr int S = ATTN_INMERGE_MAX_SPLITS, OPT = (GT * HD + 255) / 256; // outputs per thread (max)
     __shared__ uint32_t s_last;
-    __shared__ float s_w[ATTN_MAX_GROUP][S], s_L[ATTN_MAX_GROUP];
+    __shared__ float s_w[GT][S], s_L[GT];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t stride = HD + 4;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // this thread's states have landed
@@ -128,7 +150,7 @@ RFP4_DEV void attn_merge_last(const AttnArgs &a, const float *prow, uint32_t kvh
         const float m = in ? attn_load_agent(hp + (size_t)lane * stride) : -3.402823466e38f;
         const float l = in ? attn_load_agent(hp + (size_t)lane * stride + 1) : 0.0f;
         const float M = wave_max(m);
-        const float w = in ? expf(m - M) : 0.0f;
+        const float w = in ? attn_exp2(m - M) : 0.0f;
         if (in) s_w[g][lane] = w;
         const float L = wave_sum(l * w);
         if (lane == 0) s_L[g] = L;
@@ -147,105 +169,134 @@ RFP4_DEV void attn_merge_last(const AttnArgs &a, const float *prow, uint32_t kvh
     }
 }
 
-template <int HD, typename KT>
+template <int HD, typename KT, int GT>
 RFP4_DEV void attn_body(const AttnArgs &a)
 {
     constexpr int EPL = KvTraits<KT>::EPL;
     constexpr int LPT = HD / EPL;          // lanes per token row
     constexpr int TPS = 256 / LPT;         // tokens per workgroup step
-    constexpr int NSTEP = attn_steps<HD, KT>();
+    constexpr int NSTEP = attn_steps_for(HD, (int)sizeof(KT), GT);
     constexpr uint32_t CAPT = TPS * NSTEP;  // tokens of one sub-chunk (held in registers)
+    constexpr uint32_t HALF = HD / 2;
+    constexpr int QPT = (GT * (int)HALF + 255) / 256; // q rotation pairs per thread
     static_assert(LPT >= 4 && LPT <= 32, "row split");
-    __shared__ float qs[ATTN_MAX_GROUP][HD];
-    __shared__ float ps[ATTN_MAX_GROUP][CAPT];
-    __shared__ float vred[4][ATTN_MAX_GROUP][HD];
-    __shared__ float s_m[ATTN_MAX_GROUP], s_l[ATTN_MAX_GROUP], s_alpha[ATTN_MAX_GROUP];
+    static_assert(256 % HALF == 0, "a thread's rotation pairs share one table column");
+    static_assert(GT == 1 || GT == 2 || GT == 4 || GT == 8, "group");
+    __shared__ __align__(16) float qs[GT][HD];
+    __shared__ __align__(16) float vred[4][GT][HD];
+    __shared__ float s_mx[2][4][GT], s_lred[4][GT], s_mfin[GT];
     __shared__ uint16_t knew[HD], vnew[HD];
 
     const uint32_t kvh = blockIdx.x, split = blockIdx.y, row = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int li = tid % LPT, slot = tid / LPT;
+    const uint32_t G = a.n_heads / a.n_kv_heads; // <= GT
+    const bool fused = a.cosv != nullptr;
+    const float *qg = a.q + (size_t)row * a.q_rs + (size_t)(kvh * G) * HD;
+
+    // ---- loads that need no position: this thread's q pairs (j, j + HD/2)
+    // of pair index i = tid + 256 m
+    float qa[QPT], qb[QPT];
+#pragma unroll
+    for (int m = 0; m < QPT; m++) {
+        const uint32_t i = (uint32_t)tid + 256u * (uint32_t)m;
+        const uint32_t g = i / HALF, j = i % HALF;
+        const bool in = g < G;
+        qa[m] = in ? qg[g * HD + j] : 0.0f;
+        qb[m] = in ? qg[g * HD + j + HALF] : 0.0f;
+    }
     const uint32_t chunk = a.chunk;
     uint32_t seq = (a.pos_ptr ? (uint32_t)(*a.pos_ptr + 1) : a.seq) + row;
-    const float *qrow = a.q + (size_t)row * a.q_rs;
     float *orow = a.out + (size_t)row * a.out_rs;
     float *prow = a.part + (size_t)row * a.n_heads * a.max_splits * (HD + 4);
     seq = min(seq, chunk * a.max_splits); // never read past the planned splits
     const uint32_t nsplit = (seq + chunk - 1) / chunk;
     if (split >= nsplit) return;
-    const uint32_t G = a.n_heads / a.n_kv_heads;
     const uint32_t t0 = split * chunk;
     const uint32_t nt = min(seq, t0 + chunk) - t0;
     const uint32_t nsub = (nt + CAPT - 1) / CAPT;
     const uint32_t pos = seq - 1;
-    const bool fused = a.cosv != nullptr;
     const bool owner = fused && (pos >= t0) && (pos < t0 + nt);
     const KT *kc = (const KT *)a.kc + (size_t)kvh * a.hs;
     const KT *vc = (const KT *)a.vc + (size_t)kvh * a.hs;
 
-    // ---- K and V rows of sub-chunk C: token t0 + C*CAPT + s*TPS + slot, lanes split the row
+    // ---- rope table column j = tid % (HD/2) at the position, then the K/V stream
+    float cs = 1.0f, sn = 0.0f;
+    if (fused) {
+        const uint32_t j = (uint32_t)tid % HALF;
+        cs = a.cosv[(size_t)pos * HALF + j];
+        sn = a.sinv[(size_t)pos * HALF + j];
+    }
+    // K and V rows of sub-chunk C: token t0 + C*CAPT + s*TPS + slot, lanes split
+    // the row.  Slots past the split re-read its last row (in bounds, finite;
+    // their scores are masked and their p is 0): no branch around the loads,
+    // so the wait for the rope tables below does not wait for this stream.
     uint4 kr[NSTEP], vr[NSTEP];
 #define RFP4_ATTN_LOAD(R, BASE, C)                                                              \
     do {                                                                                        \
         _Pragma("unroll") for (int s_ = 0; s_ < NSTEP; s_++) {                         \
-            const uint32_t t_ = (C) * CAPT + (uint32_t)s_ * TPS + (uint32_t)slot;               \
-            R[s_] = make_uint4(0, 0, 0, 0);                                                     \
-            if (t_ < nt) R[s_] = *(const uint4 *)((BASE) + (size_t)(t0 + t_) * a.ts + (size_t)li * EPL); \
+            const uint32_t t_ = min((C) * CAPT + (uint32_t)s_ * TPS + (uint32_t)slot, nt - 1u); \
+            R[s_] = *(const uint4 *)((BASE) + (size_t)(t0 + t_) * a.ts + (size_t)li * EPL);    \
         }                                                                                       \
     } while (0)
     RFP4_ATTN_LOAD(kr, kc, 0u);
     RFP4_ATTN_LOAD(vr, vc, 0u);
 
     // ---- q (rotated if fused) into LDS; the owner split appends k, v
-    const float *qg = qrow + (size_t)(kvh * G) * HD;
-    if (fused) {
-        const uint32_t half = HD / 2;
-        const float *cp = a.cosv + (size_t)pos * half, *sp = a.sinv + (size_t)pos * half;
-        for (uint32_t i = tid; i < G * half; i += blockDim.x) {
-            uint32_t g = i / half, j = i % half;
-            float x0 = qg[g * HD + j], x1 = qg[g * HD + j + half];
-            qs[g][j] = __fsub_rn(__fmul_rn(x0, cp[j]), __fmul_rn(x1, sp[j]));
-            qs[g][j + half] = __fadd_rn(__fmul_rn(x1, cp[j]), __fmul_rn(x0, sp[j]));
+#pragma unroll
+    for (int m = 0; m < QPT; m++) {
+        const uint32_t i = (uint32_t)tid + 256u * (uint32_t)m;
+        if (i >= GT * HALF) break;
+        const uint32_t g = i / HALF, j = i % HALF;
+        float r0 = qa[m], r1 = qb[m];
+        if (fused) {
+            r0 = __fsub_rn(__fmul_rn(qa[m], cs), __fmul_rn(qb[m], sn));
+            r1 = __fadd_rn(__fmul_rn(qb[m], cs), __fmul_rn(qa[m], sn));
         }
-        if (owner) {
-            const float *kn = a.k_new + (size_t)kvh * HD, *vn = a.v_new + (size_t)kvh * HD;
-            uint16_t *kdst = (uint16_t *)a.kc + (size_t)kvh * a.hs + (size_t)pos * a.ts;
-            uint16_t *vdst = (uint16_t *)a.vc + (size_t)kvh * a.hs + (size_t)pos * a.ts;
-            for (uint32_t j = tid; j < half; j += blockDim.x) {
-                float x0 = kn[j], x1 = kn[j + half];
-                uint16_t r0 = f32_to_f16_bits(__fsub_rn(__fmul_rn(x0, cp[j]), __fmul_rn(x1, sp[j])));
-                uint16_t r1 = f32_to_f16_bits(__fadd_rn(__fmul_rn(x1, cp[j]), __fmul_rn(x0, sp[j])));
-                knew[j] = r0;
-                knew[j + half] = r1;
-                kdst[j] = r0;
-                kdst[j + half] = r1;
-            }
-            for (uint32_t j = tid; j < HD; j += blockDim.x) {
-                uint16_t r = f32_to_f16_bits(vn[j]);
-                vnew[j] = r;
-                vdst[j] = r;
-            }
-        }
-    } else {
-        for (uint32_t i = tid; i < G * HD; i += blockDim.x) qs[i / HD][i % HD] = qg[i];
+        qs[g][j] = r0;
+        qs[g][j + HALF] = r1;
     }
-    if (tid < (int)G) {
-        s_m[tid] = -3.402823466e38f;
-        s_l[tid] = 0.0f;
+    if (owner && (uint32_t)tid < HALF) {
+        // the current token's k and v, loaded by the owner split only (after
+        // its K/V stream, so no other split waits on them)
+        const float *kn = a.k_new + (size_t)kvh * HD, *vn = a.v_new + (size_t)kvh * HD;
+        const float kna = kn[tid], knb = kn[tid + HALF], vna = vn[tid], vnb = vn[tid + HALF];
+        uint16_t *kdst = (uint16_t *)a.kc + (size_t)kvh * a.hs + (size_t)pos * a.ts;
+        uint16_t *vdst = (uint16_t *)a.vc + (size_t)kvh * a.hs + (size_t)pos * a.ts;
+        const uint16_t r0 = f32_to_f16_bits(__fsub_rn(__fmul_rn(kna, cs), __fmul_rn(knb, sn)));
+        const uint16_t r1 = f32_to_f16_bits(__fadd_rn(__fmul_rn(knb, cs), __fmul_rn(kna, sn)));
+        const uint16_t w0 = f32_to_f16_bits(vna), w1 = f32_to_f16_bits(vnb);
+        knew[tid] = r0;
+        knew[tid + HALF] = r1;
+        vnew[tid] = w0;
+        vnew[tid + HALF] = w1;
+        kdst[tid] = r0;
+        kdst[tid + HALF] = r1;
+        vdst[tid] = w0;
+        vdst[tid + HALF] = w1;
     }
     __syncthreads();
 
-    float qv[ATTN_MAX_GROUP][EPL];
+    float qv[GT][EPL];
 #pragma unroll
-    for (int g = 0; g < ATTN_MAX_GROUP; g++)
+    for (int g = 0; g < GT; g++)
 #pragma unroll
-        for (int e = 0; e < EPL; e++) qv[g][e] = (uint32_t)g < G ? qs[g][li * EPL + e] : 0.0f;
-    const float scale = __fdiv_rn(1.0f, __fsqrt_rn((float)HD));
-    float acc[ATTN_MAX_GROUP][EPL];
+        for (int e = 0; e < EPL; e += 4) {
+            const float4 v4 = *(const float4 *)&qs[g][li * EPL + e];
+            qv[g][e] = v4.x;
+            qv[g][e + 1] = v4.y;
+            qv[g][e + 2] = v4.z;
+            qv[g][e + 3] = v4.w;
+        }
+    const float scale = __fmul_rn(1.4426950408889634f, __fdiv_rn(1.0f, __fsqrt_rn((float)HD))); // log2(e) / sqrt(HD)
+    float acc[GT][EPL], lsum[GT], mrun[GT];
 #pragma unroll
-    for (int g = 0; g < ATTN_MAX_GROUP; g++)
+    for (int g = 0; g < GT; g++) {
+        lsum[g] = 0.0f;
+        mrun[g] = -3.402823466e38f;
 #pragma unroll
         for (int e = 0; e < EPL; e++) acc[g][e] = 0.0f;
+    }
 
     for (uint32_t c = 0; c < nsub; c++) {
         const uint32_t tb = c * CAPT, ntc = min(CAPT, nt - tb);
@@ -269,98 +320,86 @@ RFP4_DEV void attn_body(const AttnArgs &a)
             }
         }
 
-        // ---- scores of this sub-chunk, then the next sub-chunk's K loads
+        // ---- scores of this sub-chunk (every lane of a row gets its row's
+        //      score), this wave's max per head, then the next sub-chunk's K loads
+        float sc[NSTEP][GT], mloc[GT];
+#pragma unroll
+        for (int g = 0; g < GT; g++) mloc[g] = -3.402823466e38f;
 #pragma unroll
         for (int s = 0; s < NSTEP; s++) {
-            const uint32_t t = (uint32_t)s * TPS + (uint32_t)slot;
-            if ((uint32_t)s * TPS >= ntc) break;
+            const bool valid = (uint32_t)s * TPS + (uint32_t)slot < ntc;
             float kf[EPL];
             KvTraits<KT>::widen(kr[s], kf);
 #pragma unroll
-            for (int g = 0; g < ATTN_MAX_GROUP; g++) {
-                if ((uint32_t)g >= G) break;
+            for (int g = 0; g < GT; g++) {
                 float d = 0.0f;
 #pragma unroll
                 for (int e = 0; e < EPL; e++) d = fmaf(qv[g][e], kf[e], d);
-                d = group_sum<LPT>(d);
-                if (li == 0 && t < ntc) ps[g][t] = d * scale;
+                d = group_sum<LPT>(d) * scale;
+                sc[s][g] = valid ? d : -3.402823466e38f;
+                mloc[g] = fmaxf(mloc[g], sc[s][g]);
             }
         }
         if (c + 1 < nsub) RFP4_ATTN_LOAD(kr, kc, c + 1);
-        __syncthreads();
-
-        // ---- online softmax per head (wave w handles heads w, w+4):
-        //      m' = max(m, max_t s_t), p_t = e^(s_t - m'), l' = l e^(m - m') + sum_t p_t
-        for (uint32_t g = wave; g < G; g += 4) {
-            float mc = -3.402823466e38f;
-            for (uint32_t t = lane; t < ntc; t += 64) mc = fmaxf(mc, ps[g][t]);
-            mc = wave_max(mc);
-            const float m_old = s_m[g], m_new = fmaxf(m_old, mc);
-            float l = 0.0f;
-            for (uint32_t t = lane; t < ntc; t += 64) {
-                float p = expf(ps[g][t] - m_new);
-                ps[g][t] = p;
-                l += p;
-            }
-            l = wave_sum(l);
-            if (lane == 0) {
-                const float alpha = expf(m_old - m_new);
-                s_alpha[g] = alpha;
-                s_l[g] = fmaf(s_l[g], alpha, l);
-                s_m[g] = m_new;
-            }
-        }
-        __syncthreads();
-
-        // ---- rescale the running P.V, add this sub-chunk's, then the next sub-chunk's V loads
 #pragma unroll
-        for (int g = 0; g < ATTN_MAX_GROUP; g++) {
-            if ((uint32_t)g >= G) break;
-            const float alpha = s_alpha[g];
+        for (int g = 0; g < GT; g++) mloc[g] = slots_max<LPT>(mloc[g]);
+        if (lane == 0) {
+#pragma unroll
+            for (int g = 0; g < GT; g++) s_mx[c & 1u][wave][g] = mloc[g];
+        }
+        __syncthreads(); // s_mx is double-buffered: the next sub-chunk's writes wait for this barrier's successor
+
+        // ---- online softmax: m' = max(m, max_t s_t), acc and l scaled by
+        //      2^(m - m'), then p_t = 2^(s_t - m'), l += p_t, acc += p_t v_t (base 2)
+#pragma unroll
+        for (int g = 0; g < GT; g++) {
+            const float mx = fmaxf(fmaxf(s_mx[c & 1u][0][g], s_mx[c & 1u][1][g]),
+                                   fmaxf(s_mx[c & 1u][2][g], s_mx[c & 1u][3][g]));
+            const float mnew = fmaxf(mrun[g], mx);
+            const float alpha = attn_exp2(mrun[g] - mnew);
+            mrun[g] = mnew;
+            lsum[g] *= alpha;
 #pragma unroll
             for (int e = 0; e < EPL; e++) acc[g][e] *= alpha;
         }
 #pragma unroll
         for (int s = 0; s < NSTEP; s++) {
-            const uint32_t t = (uint32_t)s * TPS + (uint32_t)slot;
-            if ((uint32_t)s * TPS >= ntc) break;
-            if (t >= ntc) continue;
+            const bool valid = (uint32_t)s * TPS + (uint32_t)slot < ntc;
             float vf[EPL];
             KvTraits<KT>::widen(vr[s], vf);
 #pragma unroll
-            for (int g = 0; g < ATTN_MAX_GROUP; g++) {
-                if ((uint32_t)g >= G) break;
-                const float p = ps[g][t];
+            for (int g = 0; g < GT; g++) {
+                const float p = valid ? attn_exp2(sc[s][g] - mrun[g]) : 0.0f;
+                lsum[g] += p;
 #pragma unroll
                 for (int e = 0; e < EPL; e++) acc[g][e] = fmaf(p, vf[e], acc[g][e]);
             }
         }
         if (c + 1 < nsub) RFP4_ATTN_LOAD(vr, vc, c + 1);
-        __syncthreads(); // ps is rewritten by the next sub-chunk
     }
 #undef RFP4_ATTN_LOAD
 
-    // lanes li, li+LPT, ... of a wave hold the same dims: fold them (xor 8 by
-    // DPP, 16 and 32 by the row-swap instructions; same sums as shuffles)
+    // ---- fold the token slots of each wave, then the four waves through LDS
 #pragma unroll
-    for (int g = 0; g < ATTN_MAX_GROUP; g++) {
-        if ((uint32_t)g >= G) break;
+    for (int g = 0; g < GT; g++) {
+        lsum[g] = slots_sum<LPT>(lsum[g]);
 #pragma unroll
-        for (int e = 0; e < EPL; e++) {
-            float v = acc[g][e];
-            if (LPT <= 4) v += __shfl_xor(v, 4, 64);
-            if (LPT <= 8) v += dpp_mov<DPP_ROW_ROR8>(v);
-            if (LPT <= 16) v = xor16_sum(v);
-            acc[g][e] = xor32_sum(v);
-        }
+        for (int e = 0; e < EPL; e++) acc[g][e] = slots_sum<LPT>(acc[g][e]);
     }
     if (lane < LPT) {
 #pragma unroll
-        for (int g = 0; g < ATTN_MAX_GROUP; g++) {
-            if ((uint32_t)g >= G) break;
+        for (int g = 0; g < GT; g++)
 #pragma unroll
-            for (int e = 0; e < EPL; e++) vred[wave][g][li * EPL + e] = acc[g][e];
-        }
+            for (int e = 0; e < EPL; e += 4)
+                *(float4 *)&vred[wave][g][li * EPL + e] = make_float4(acc[g][e], acc[g][e + 1], acc[g][e + 2], acc[g][e + 3]);
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int g = 0; g < GT; g++) s_lred[wave][g] = lsum[g];
+    }
+    if (tid == 0) {
+#pragma unroll
+        for (int g = 0; g < GT; g++) s_mfin[g] = mrun[g];
     }
     __syncthreads();
 
@@ -369,7 +408,8 @@ RFP4_DEV void attn_body(const AttnArgs &a)
         for (uint32_t i = tid; i < G * HD; i += blockDim.x) {
             const uint32_t g = i / HD, d = i % HD;
             const float v = vred[0][g][d] + vred[1][g][d] + vred[2][g][d] + vred[3][g][d];
-            orow[(size_t)(kvh * G + g) * HD + d] = __fdiv_rn(v, s_l[g]);
+            const float l = (s_lred[0][g] + s_lred[1][g]) + (s_lred[2][g] + s_lred[3][g]);
+            orow[(size_t)(kvh * G + g) * HD + d] = __fdiv_rn(v, l);
         }
         return;
     }
@@ -383,105 +423,104 @@ RFP4_DEV void attn_body(const AttnArgs &a)
         uint32_t g = i / HD, d = i % HD;
         float v = vred[0][g][d] + vred[1][g][d] + vred[2][g][d] + vred[3][g][d];
         size_t base = ((size_t)(kvh * G + g) * a.max_splits + split) * stride;
+        const float l = (s_lred[0][g] + s_lred[1][g]) + (s_lred[2][g] + s_lred[3][g]);
         if (inmerge) {
             attn_store_agent(prow + base + 4 + d, v);
             if (d == 0) {
-                attn_store_agent(prow + base, s_m[g]);
-                attn_store_agent(prow + base + 1, s_l[g]);
+                attn_store_agent(prow + base, s_mfin[g]);
+                attn_store_agent(prow + base + 1, l);
             }
         } else {
             prow[base + 4 + d] = v;
             if (d == 0) {
-                prow[base] = s_m[g];
-                prow[base + 1] = s_l[g];
+                prow[base] = s_mfin[g];
+                prow[base + 1] = l;
             }
         }
     }
     if (!inmerge) return;
-    attn_merge_last<HD>(a, prow, kvh, G, nsplit);
+    attn_merge_last<HD, GT>(a, prow, kvh, G, nsplit);
 }
 
 // Merge kernel body: grid (n_heads), launched after attn_body on the same
 // stream (the kernel boundary orders the partial states before these reads).
 // Computes the split count exactly as attn_body did; one split means
 // attn_body already wrote the output.  For query head h:
-//   M = max m_i, L = sum l_i e^(m_i - M), out = (sum acc_i e^(m_i - M)) / L,
-// computed online (running max).  Thread tid owns float4 q = tid % (HD/4) of
-// the head and the splits p, p + P, p + 2P, ... (p = tid / (HD/4), P = 256 /
-// (HD/4)), every load of a batch in flight at once; the P partial states of a
-// float4 are then combined through LDS.
-#define ATTN_MERGE_BATCH 8
+//   M = max m_i, w_i = 2^(m_i - M), L = sum l_i w_i, out = sum w_i acc_i / L
+// (m in the base-2 units of attn_body's scores).
+// Thread tid owns output d = tid % HD and the splits p, p + P, p + 2P, ...
+// (p = tid / HD, P = 256 / HD) of each batch of ATTN_MERGE_BATCH splits.
+// Every thread issues the value loads of the first batch at once, before the
+// split count is known (indices clamped inside the workspace; values past the
+// count are discarded by select), while wave 0 loads (m_i, l_i), one split
+// per lane, and turns them into M, L and the batch's weights (LDS); the rest
+// is FMAs and one LDS combine of the P partial sums.  Up to ATTN_MERGE_BATCH
+// splits this is one round trip of loads.
+#define ATTN_MERGE_BATCH 64
 template <int HD>
 RFP4_DEV void attn_merge_body(const AttnArgs &a)
 {
-    constexpr uint32_t Q = HD / 4, P = 256 / Q, STRIDE = HD + 4;
-    __shared__ float sh[P][Q][6];
+    constexpr uint32_t P = 256 / HD, STRIDE = HD + 4, NB = ATTN_MERGE_BATCH / P;
+    __shared__ float s_w[ATTN_MERGE_BATCH];
+    __shared__ float s_part[P][HD];
+    __shared__ float s_L, s_M;
     const uint32_t row = blockIdx.z;
     const uint32_t h = blockIdx.x; // the partial state of head h sits at (h * max_splits + split) * STRIDE
-    const uint32_t q = threadIdx.x % Q, p = threadIdx.x / Q;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t d = (uint32_t)tid % HD, p = (uint32_t)tid / HD;
     const float *hp = a.part + (size_t)row * a.n_heads * a.max_splits * STRIDE + (size_t)h * a.max_splits * STRIDE;
-    // the first batch is loaded before the split count is known (indices
-    // clamped inside the workspace; states past the count are discarded), so
-    // the position read and these loads are one round trip
-    float2 ml[ATTN_MERGE_BATCH];
-    float4 v[ATTN_MERGE_BATCH];
+    const uint32_t last = a.max_splits - 1u;
+    float v[NB];
 #pragma unroll
-    for (int j = 0; j < ATTN_MERGE_BATCH; j++) {
-        const uint32_t sp = min(p + P * j, a.max_splits - 1u);
-        ml[j] = *(const float2 *)(hp + (size_t)sp * STRIDE);
-        v[j] = *(const float4 *)(hp + (size_t)sp * STRIDE + 4 + q * 4);
+    for (int j = 0; j < (int)NB; j++) v[j] = hp[(size_t)min(p + P * (uint32_t)j, last) * STRIDE + 4 + d];
+    float m0 = 0.0f, l0 = 0.0f;
+    if (wave == 0) {
+        const uint32_t sp = min((uint32_t)lane, last);
+        m0 = hp[(size_t)sp * STRIDE];
+        l0 = hp[(size_t)sp * STRIDE + 1];
     }
     uint32_t seq = (a.pos_ptr ? (uint32_t)(*a.pos_ptr + 1) : a.seq) + row;
     seq = min(seq, a.chunk * a.max_splits);
     const uint32_t nsplit = (seq + a.chunk - 1) / a.chunk;
     if (nsplit <= 1) return;
-    float M = -3.402823466e38f, L = 0.0f;
-    float4 o = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (uint32_t sp0 = p; sp0 < nsplit; sp0 += P * ATTN_MERGE_BATCH) {
-        if (sp0 != p) {
-#pragma unroll
-            for (int j = 0; j < ATTN_MERGE_BATCH; j++) {
-                const uint32_t sp = min(sp0 + P * j, nsplit - 1u);
-                ml[j] = *(const float2 *)(hp + (size_t)sp * STRIDE);
-                v[j] = *(const float4 *)(hp + (size_t)sp * STRIDE + 4 + q * 4);
-            }
+    if (wave == 0) {
+        float M = (uint32_t)lane < nsplit ? m0 : -3.402823466e38f;
+        for (uint32_t i = (uint32_t)lane + 64u; i < nsplit; i += 64u) M = fmaxf(M, hp[(size_t)i * STRIDE]);
+        M = wave_max(M);
+        float L = 0.0f;
+        for (uint32_t i = (uint32_t)lane; i < nsplit; i += 64u) {
+            const float mi = i == (uint32_t)lane ? m0 : hp[(size_t)i * STRIDE];
+            const float li = i == (uint32_t)lane ? l0 : hp[(size_t)i * STRIDE + 1];
+            const float w = attn_exp2(mi - M);
+            if (i < ATTN_MERGE_BATCH) s_w[i] = w;
+            L = fmaf(li, w, L);
         }
-#pragma unroll
-        for (int j = 0; j < ATTN_MERGE_BATCH; j++) {
-            if (sp0 + P * j >= nsplit) break;
-            const float Mn = fmaxf(M, ml[j].x);
-            const float ea = expf(M - Mn), eb = expf(ml[j].x - Mn);
-            L = fmaf(L, ea, ml[j].y * eb);
-            o.x = fmaf(o.x, ea, v[j].x * eb);
-            o.y = fmaf(o.y, ea, v[j].y * eb);
-            o.z = fmaf(o.z, ea, v[j].z * eb);
-            o.w = fmaf(o.w, ea, v[j].w * eb);
-            M = Mn;
+        L = wave_sum(L);
+        if (lane == 0) {
+            s_L = L;
+            s_M = M;
         }
     }
-    float *me = sh[p][q];
-    me[0] = M; me[1] = L; me[2] = o.x; me[3] = o.y; me[4] = o.z; me[5] = o.w;
+    __syncthreads();
+    float acc = 0.0f;
+    for (uint32_t b = 0; b < nsplit; b += ATTN_MERGE_BATCH) {
+        if (b > 0) {
+#pragma unroll
+            for (int j = 0; j < (int)NB; j++) v[j] = hp[(size_t)min(b + p + P * (uint32_t)j, last) * STRIDE + 4 + d];
+            __syncthreads(); // the previous batch's weights are read
+            if (wave == 0 && b + (uint32_t)lane < nsplit) s_w[lane] = attn_exp2(hp[(size_t)(b + lane) * STRIDE] - s_M);
+            __syncthreads();
+        }
+#pragma unroll
+        for (int j = 0; j < (int)NB; j++) {
+            const uint32_t sp = p + P * (uint32_t)j;
+            if (b + sp < nsplit) acc = fmaf(s_w[sp], v[j], acc);
+        }
+    }
+    if (p > 0) s_part[p][d] = acc;
     __syncthreads();
     if (p != 0) return;
-    for (uint32_t r = 1; r < P; r++) {
-        const float *o2 = sh[r][q];
-        const float Mn = fmaxf(M, o2[0]), ea = expf(M - Mn), eb = expf(o2[0] - Mn);
-        L = fmaf(L, ea, o2[1] * eb);
-        o.x = fmaf(o.x, ea, o2[2] * eb);
-        o.y = fmaf(o.y, ea, o2[3] * eb);
-        o.z = fmaf(o.z, ea, o2[4] * eb);
-        o.w = fmaf(o.w, ea, o2[5] * eb);
-        M = Mn;
-    }
-    float *dst = a.out + (size_t)row * a.out_rs + (size_t)h * HD + q * 4;
-    dst[0] = __fdiv_rn(o.x, L);
-    dst[1] = __fdiv_rn(o.y, L);
-    dst[2] = __fdiv_rn(o.z, L);
-    dst[3] = __fdiv_rn(o.w, L);
-}
-
-// Tokens of one sub-chunk (the K/V rows attn_body holds in registers at once).
-constexpr uint32_t attn_sub_chunk(uint32_t hd, uint32_t elem_bytes)
-{
-    return (256u / (hd * elem_bytes / 16u)) * ((hd == 128u && elem_bytes == 2u) ? 9u : 8u);
+#pragma unroll
+    for (uint32_t r = 1; r < P; r++) acc += s_part[r][d];
+    a.out[(size_t)row * a.out_rs + (size_t)h * HD + d] = __fdiv_rn(acc, s_L);
 }

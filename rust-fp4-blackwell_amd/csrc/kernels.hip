@@ -122,11 +122,16 @@ K256 void rfp4_rope(RopeArgs a) { rope_body(a); }
 K256 void rfp4_rope_append(RopeAppendArgs a) { rope_append_body(a); }
 K256 void rfp4_embed(EmbedArgs a) { embed_body(a); }
 
-// ---- attention
-K256 void rfp4_attn_hd64_f32(AttnArgs a) { attn_body<64, float>(a); }
-K256 void rfp4_attn_hd64_f16(AttnArgs a) { attn_body<64, uint16_t>(a); }
-K256 void rfp4_attn_hd128_f32(AttnArgs a) { attn_body<128, float>(a); }
-K256 void rfp4_attn_hd128_f16(AttnArgs a) { attn_body<128, uint16_t>(a); }
+// ---- attention: rfp4_attn_hd<HD>_<KV type>_g<query heads per KV head, padded to 1/2/4/8>
+#define ATTN_KERNELS(HD, KNAME, KT) \
+    K256 void rfp4_attn_hd##HD##_##KNAME##_g1(AttnArgs a) { attn_body<HD, KT, 1>(a); } \
+    K256 void rfp4_attn_hd##HD##_##KNAME##_g2(AttnArgs a) { attn_body<HD, KT, 2>(a); } \
+    K256 void rfp4_attn_hd##HD##_##KNAME##_g4(AttnArgs a) { attn_body<HD, KT, 4>(a); } \
+    K256 void rfp4_attn_hd##HD##_##KNAME##_g8(AttnArgs a) { attn_body<HD, KT, 8>(a); }
+ATTN_KERNELS(64, f32, float)
+ATTN_KERNELS(64, f16, uint16_t)
+ATTN_KERNELS(128, f32, float)
+ATTN_KERNELS(128, f16, uint16_t)
 K256 void rfp4_attn_merge_hd64(AttnArgs a) { attn_merge_body<64>(a); }
 K256 void rfp4_attn_merge_hd128(AttnArgs a) { attn_merge_body<128>(a); }
 

@@ -456,10 +456,14 @@ namespace rfp4 {
 
 int attn_launch(const AttnArgs &args, int kv_f16, hipStream_t s, uint32_t max_seq_for_grid, uint32_t rows)
 {
-    const char *name;
-    if (args.head_dim == 64) name = kv_f16 ? "rfp4_attn_hd64_f16" : "rfp4_attn_hd64_f32";
-    else if (args.head_dim == 128) name = kv_f16 ? "rfp4_attn_hd128_f16" : "rfp4_attn_hd128_f32";
-    else return set_error(RFP4_E_SHAPE, "attn: head_dim %u unsupported (64 or 128)", args.head_dim);
+    if (args.head_dim != 64 && args.head_dim != 128)
+        return set_error(RFP4_E_SHAPE, "attn: head_dim %u unsupported (64 or 128)", args.head_dim);
+    if (args.n_kv_heads == 0 || args.n_heads % args.n_kv_heads || args.n_heads / args.n_kv_heads > 8)
+        return set_error(RFP4_E_SHAPE, "attn: %u query heads over %u KV heads (group of at most 8)", args.n_heads,
+                         args.n_kv_heads);
+    char name[48];
+    snprintf(name, sizeof name, "rfp4_attn_hd%u_%s_g%u", args.head_dim, kv_f16 ? "f16" : "f32",
+             attn_group_pad(args.n_heads / args.n_kv_heads));
     if (args.chunk == 0) return set_error(RFP4_E_INVALID, "attn: chunk must be positive");
     if (args.cosv && !kv_f16) return set_error(RFP4_E_INVALID, "attn: fused KV append needs an fp16 cache");
     if (rows == 0 || (rows > 1 && args.cosv)) return set_error(RFP4_E_INVALID, "attn: fused append is one row only");
@@ -474,26 +478,27 @@ int attn_launch(const AttnArgs &args, int kv_f16, hipStream_t s, uint32_t max_se
                   dim3(256), s, &a);
 }
 
-uint32_t attn_sub_chunk(uint32_t head_dim, uint32_t elem_bytes)
+uint32_t attn_group_pad(uint32_t group) { return group <= 1u ? 1u : group <= 2u ? 2u : group <= 4u ? 4u : 8u; }
+
+uint32_t attn_sub_chunk(uint32_t head_dim, uint32_t elem_bytes, uint32_t group)
 {
     // tokens per workgroup step (256 threads / lanes per 16-byte-split row)
-    // times the load steps each thread keeps in registers (9 for fp16 rows of
-    // 128, else 8: device/attn.h attn_steps)
+    // times the load steps each thread keeps in registers
     uint32_t lanes_per_row = head_dim * elem_bytes / 16u;
-    uint32_t steps = (head_dim == 128u && elem_bytes == 2u) ? 9u : 8u;
-    return (256u / lanes_per_row) * steps;
+    return (256u / lanes_per_row) * (uint32_t)attn_steps_for((int)head_dim, (int)elem_bytes, (int)attn_group_pad(group));
 }
 
 static thread_local uint32_t t_force_attn_chunk = 0;
 
-uint32_t attn_chunk_for(uint32_t n_kv_heads, uint32_t seq, uint32_t num_cus, uint32_t head_dim, uint32_t elem_bytes)
+uint32_t attn_chunk_for(uint32_t n_kv_heads, uint32_t seq, uint32_t num_cus, uint32_t head_dim, uint32_t elem_bytes,
+                        uint32_t group)
 {
     if (t_force_attn_chunk) return t_force_attn_chunk;
     // At most one (KV head, split) workgroup per CU and at least 64 tokens per
     // split; the chunk is a whole number of workgroup steps and at most one
     // sub-chunk (one pass over registers) unless the context needs more
     // workgroups than CUs, in which case it is exactly one sub-chunk.
-    const uint32_t sub = attn_sub_chunk(head_dim, elem_bytes);
+    const uint32_t sub = attn_sub_chunk(head_dim, elem_bytes, group);
     const uint32_t step = 256u / (head_dim * elem_bytes / 16u);
     uint32_t splits = (seq + 63u) / 64u;
     uint32_t per_head = num_cus / n_kv_heads;
@@ -654,7 +659,7 @@ static int attn_common(hipStream_t s, uint32_t nh, uint32_t nkv, uint32_t hd, ui
     if (((uintptr_t)kc | (uintptr_t)vc) & 15u || (ts * eb) % 16u || (hs * eb) % 16u)
         return set_error(RFP4_E_ALIGN, "attn_decode: K/V rows must start 16-byte aligned (strides %llu, %llu)",
                          (unsigned long long)ts, (unsigned long long)hs);
-    uint32_t chunk = attn_chunk_for(nkv, seq, rt->num_cus, hd, eb);
+    uint32_t chunk = attn_chunk_for(nkv, seq, rt->num_cus, hd, eb, nh / nkv);
     uint32_t splits = (seq + chunk - 1) / chunk;
     if (splits > kAttnMaxSplits)
         return set_error(RFP4_E_CAPACITY, "attn_decode: seq %u needs %u splits of %u tokens (> %u)", seq, splits, chunk,

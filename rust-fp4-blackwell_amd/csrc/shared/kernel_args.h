@@ -212,4 +212,16 @@ typedef struct SelftestArgs {
 
 #ifdef __cplusplus
 }
+
+// Attention: 16-byte row pieces of K (and of V) each thread holds per
+// sub-chunk, for head_dim, KV element bytes and the compile-time query-head
+// group (1, 2, 4, 8).  9 for fp16 rows of 128 with groups up to 4 (144
+// tokens: a 4096-token context takes 29 splits per KV head, and 8 KV heads
+// fit one workgroup per CU); 4 with 8 heads per group (their scores and
+// accumulators take the registers); else 8.  Tokens per sub-chunk: this
+// times 256 / (head_dim * elem_bytes / 16).
+constexpr int attn_steps_for(int head_dim, int elem_bytes, int group)
+{
+    return group == 8 ? 4 : (head_dim == 128 && elem_bytes == 2) ? 9 : 8;
+}
 #endif
