@@ -121,7 +121,8 @@ RFP4_DEV void attn_merge_last(const AttnArgs &a, const float *prow, uint32_t kvh
 {
     constexpr int S = ATTN_INMERGE_MAX_SPLITS, OPT = (GT * HD + 255) / 256; // outputs per thread (max)
     __shared__ uint32_t s_last;
-    __shared__ float s_w[GT][S], s_L[GT];
+    __shared__ __align__(16) float s_w[GT][S];
+    __shared__ float s_L[GT];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t stride = HD + 4;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // this thread's states have landed
@@ -161,10 +162,21 @@ RFP4_DEV void attn_merge_last(const AttnArgs &a, const float *prow, uint32_t kvh
         const uint32_t i = (uint32_t)tid + 256u * (uint32_t)j;
         const uint32_t g = i / HD, d = i % HD;
         if (g >= G) break;
+        float w[S];
+#pragma unroll
+        for (int sp = 0; sp < S; sp += 4) {
+            const float4 w4 = *(const float4 *)&s_w[g][sp];
+            w[sp] = w4.x;
+            w[sp + 1] = w4.y;
+            w[sp + 2] = w4.z;
+            w[sp + 3] = w4.w;
+        }
         float acc = 0.0f;
 #pragma unroll
-        for (int sp = 0; sp < S; sp++)
-            if ((uint32_t)sp < nsplit) acc = fmaf(s_w[g][sp], v[j][sp], acc);
+        for (int sp = 0; sp < S; sp++) {
+            const float t = fmaf(w[sp], v[j][sp], acc);
+            acc = (uint32_t)sp < nsplit ? t : acc;
+        }
         a.out[(size_t)(kvh * G + g) * HD + d] = __fdiv_rn(acc, s_L[g]);
     }
 }
@@ -453,15 +465,16 @@ RFP4_DEV void attn_body(const AttnArgs &a)
 // Every thread issues the value loads of the first batch at once, before the
 // split count is known (indices clamped inside the workspace; values past the
 // count are discarded by select), while wave 0 loads (m_i, l_i), one split
-// per lane, and turns them into M, L and the batch's weights (LDS); the rest
-// is FMAs and one LDS combine of the P partial sums.  Up to ATTN_MERGE_BATCH
-// splits this is one round trip of loads.
+// per lane, and turns them into M, L and the batch's weights, stored in LDS
+// partition-major (split p + P j at p * NB + j) so that a thread reads its NB
+// weights as float4s; the rest is FMAs and one LDS combine of the P partial
+// sums.  Up to ATTN_MERGE_BATCH splits this is one round trip of loads.
 #define ATTN_MERGE_BATCH 64
 template <int HD>
 RFP4_DEV void attn_merge_body(const AttnArgs &a)
 {
     constexpr uint32_t P = 256 / HD, STRIDE = HD + 4, NB = ATTN_MERGE_BATCH / P;
-    __shared__ float s_w[ATTN_MERGE_BATCH];
+    __shared__ __align__(16) float s_w[ATTN_MERGE_BATCH]; // batch split i at (i % P) * NB + i / P
     __shared__ float s_part[P][HD];
     __shared__ float s_L, s_M;
     const uint32_t row = blockIdx.z;
@@ -492,7 +505,7 @@ RFP4_DEV void attn_merge_body(const AttnArgs &a)
             const float mi = i == (uint32_t)lane ? m0 : hp[(size_t)i * STRIDE];
             const float li = i == (uint32_t)lane ? l0 : hp[(size_t)i * STRIDE + 1];
             const float w = attn_exp2(mi - M);
-            if (i < ATTN_MERGE_BATCH) s_w[i] = w;
+            if (i < ATTN_MERGE_BATCH) s_w[(i % P) * NB + i / P] = w;
             L = fmaf(li, w, L);
         }
         L = wave_sum(L);
@@ -508,13 +521,23 @@ RFP4_DEV void attn_merge_body(const AttnArgs &a)
 #pragma unroll
             for (int j = 0; j < (int)NB; j++) v[j] = hp[(size_t)min(b + p + P * (uint32_t)j, last) * STRIDE + 4 + d];
             __syncthreads(); // the previous batch's weights are read
-            if (wave == 0 && b + (uint32_t)lane < nsplit) s_w[lane] = attn_exp2(hp[(size_t)(b + lane) * STRIDE] - s_M);
+            if (wave == 0 && b + (uint32_t)lane < nsplit)
+                s_w[((uint32_t)lane % P) * NB + (uint32_t)lane / P] = attn_exp2(hp[(size_t)(b + lane) * STRIDE] - s_M);
             __syncthreads();
+        }
+        float w[NB];
+#pragma unroll
+        for (int j = 0; j < (int)NB; j += 4) {
+            const float4 w4 = *(const float4 *)&s_w[p * NB + (uint32_t)j];
+            w[j] = w4.x;
+            w[j + 1] = w4.y;
+            w[j + 2] = w4.z;
+            w[j + 3] = w4.w;
         }
 #pragma unroll
         for (int j = 0; j < (int)NB; j++) {
-            const uint32_t sp = p + P * (uint32_t)j;
-            if (b + sp < nsplit) acc = fmaf(s_w[sp], v[j], acc);
+            const float t = fmaf(w[j], v[j], acc); // stale workspace values are never kept
+            acc = b + p + P * (uint32_t)j < nsplit ? t : acc;
         }
     }
     if (p > 0) s_part[p][d] = acc;
