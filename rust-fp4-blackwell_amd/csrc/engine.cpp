@@ -52,13 +52,15 @@ struct llama_engine {
     uint32_t n_best = 0;
     float *attn_part = nullptr;
     uint32_t attn_chunk = 64, attn_max_splits = 1;
-    uint32_t *attn_counters = nullptr; // in-kernel merge of the decode step (null: merge kernel)
+    uint32_t *attn_counters = nullptr; // arrival counters of the in-kernel attention merge (zero between steps)
+    int attn_merge_mode = 0;           // merge policy fixed at creation (rfp4_debug_attn_merge)
     StepState *state = nullptr;
     uint32_t *ids = nullptr, *last_tok = nullptr;
     uint32_t ids_alloc = 0;
     uint32_t embed_bf16 = 0; // embeddings hold bf16 (1) or fp16 (0) bits; norms are fp16
-    hipGraph_t graph = nullptr;
-    hipGraphExec_t graph_exec = nullptr;
+    // one step graph per attention split count (index = splits launched), captured on demand
+    std::vector<hipGraph_t> graphs;
+    std::vector<hipGraphExec_t> graph_execs;
     bool use_graph = true;
     // host mirror of the cursor, for bounds checks
     int64_t h_pos = 0, h_step = 0, h_ids_cap = 0;
@@ -99,7 +101,10 @@ static int validate(const rfp4_model_config &c)
 }
 
 // ---------------------------------------------------------------- step enqueue
-static int enqueue_step(llama_engine *e)
+// The decode step at a position whose context needs `nsplit` attention
+// splits: the attention grid launches exactly those, and up to 8 splits are
+// merged inside the attention kernel (attn_inmerge_mode).
+static int enqueue_step(llama_engine *e, uint32_t nsplit)
 {
     const rfp4_model_config &c = e->c;
     hipStream_t s = e->stream;
@@ -120,8 +125,8 @@ static int enqueue_step(llama_engine *e)
         aa.ts = hd; aa.hs = (uint64_t)e->max_seq_alloc * hd;
         aa.n_heads = c.n_heads; aa.n_kv_heads = c.n_kv_heads; aa.head_dim = hd; aa.seq = 0;
         aa.chunk = e->attn_chunk; aa.max_splits = e->attn_max_splits;
-        aa.counters = e->attn_counters;
-        if ((rc = attn_launch(aa, 1, s, e->attn_chunk * e->attn_max_splits, 1))) return rc;
+        aa.counters = attn_inmerge_mode(e->attn_merge_mode, nsplit) ? e->attn_counters : nullptr;
+        if ((rc = attn_launch(aa, 1, s, e->attn_chunk * nsplit, 1))) return rc;
         GemvArgs oa{w.o_c, w.o_s, e->attn_out, e->x, nullptr, nullptr, c.dim, qd, 0, 0.0f};
         if ((rc = gemv_launch("e8m0", RFP4_EPI_RESIDUAL, oa, s, 0))) return rc;
         GemvArgs ga{w.gu_c, w.gu_s, e->x, e->sw, nullptr, e->norm_ffn + (size_t)l * c.dim, c.ffn, c.dim, c.ffn, c.eps};
@@ -229,28 +234,58 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
     return rc;
 }
 
-static int capture_graph(llama_engine *e)
+static uint32_t splits_at(const llama_engine *e, int64_t pos)
 {
-    int rc = hip_check(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
-    if (rc) return rc;
-    int rc_enq = enqueue_step(e);
-    hipGraph_t g = nullptr;
-    rc = hip_check(hipStreamEndCapture(e->stream, &g), "hipStreamEndCapture");
-    if (rc_enq) {
-        if (g) hipGraphDestroy(g);
-        return rc_enq;
+    const uint64_t ns = ((uint64_t)pos + e->attn_chunk) / e->attn_chunk; // ceil((pos + 1) / chunk)
+    return (uint32_t)(ns < e->attn_max_splits ? ns : e->attn_max_splits);
+}
+
+// The step graph for `nsplit` attention splits (captured once).
+static int step_graph(llama_engine *e, uint32_t nsplit, hipGraphExec_t *out)
+{
+    if (e->graph_execs.size() <= nsplit) {
+        e->graph_execs.resize(nsplit + 1, nullptr);
+        e->graphs.resize(nsplit + 1, nullptr);
     }
-    if (rc) return rc;
-    e->graph = g;
-    return hip_check(hipGraphInstantiate(&e->graph_exec, g, nullptr, nullptr, 0), "hipGraphInstantiate");
+    if (!e->graph_execs[nsplit]) {
+        int rc = hip_check(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+        if (rc) return rc;
+        int rc_enq = enqueue_step(e, nsplit);
+        hipGraph_t g = nullptr;
+        rc = hip_check(hipStreamEndCapture(e->stream, &g), "hipStreamEndCapture");
+        if (rc_enq) {
+            if (g) hipGraphDestroy(g);
+            return rc_enq;
+        }
+        if (rc) return rc;
+        e->graphs[nsplit] = g;
+        rc = hip_check(hipGraphInstantiate(&e->graph_execs[nsplit], g, nullptr, nullptr, 0), "hipGraphInstantiate");
+        if (rc) return rc;
+    }
+    *out = e->graph_execs[nsplit];
+    return RFP4_OK;
+}
+
+// Step graphs for every position in [pos_first, pos_last].
+static int step_graphs_for(llama_engine *e, int64_t pos_first, int64_t pos_last)
+{
+    if (!e->use_graph) return RFP4_OK;
+    hipGraphExec_t g;
+    for (uint32_t ns = splits_at(e, pos_first); ns <= splits_at(e, pos_last); ns++) {
+        int rc = step_graph(e, ns, &g);
+        if (rc) return rc;
+    }
+    return RFP4_OK;
 }
 
 static void engine_free(llama_engine *e)
 {
     if (!e) return;
     if (e->stream) hipStreamSynchronize(e->stream);
-    if (e->graph_exec) hipGraphExecDestroy(e->graph_exec);
-    if (e->graph) hipGraphDestroy(e->graph);
+    for (hipGraphExec_t g : e->graph_execs)
+        if (g) hipGraphExecDestroy(g);
+    for (hipGraph_t g : e->graphs)
+        if (g) hipGraphDestroy(g);
     for (void *p : e->allocs) hipFree(p);
     if (e->stream) hipStreamDestroy(e->stream);
     delete e;
@@ -328,10 +363,9 @@ static int engine_alloc(const rfp4_model_config *cfg, llama_engine **out)
     e->n_best = gemv_blocks(c.vocab, c.dim, RFP4_EPI_ARGMAX);
     if (!rc) rc = dalloc_t(e, &e->best, e->n_best);
     if (!rc) rc = dalloc_t(e, &e->attn_part, (size_t)c.n_heads * e->attn_max_splits * (hd + 4));
-    if (!rc && attn_inmerge(e->attn_max_splits)) {
-        rc = dalloc_t(e, &e->attn_counters, c.n_kv_heads);
-        if (!rc) rc = fill_words(e->attn_counters, c.n_kv_heads, 0u, s);
-    }
+    e->attn_merge_mode = attn_merge_mode();
+    if (!rc) rc = dalloc_t(e, &e->attn_counters, c.n_kv_heads);
+    if (!rc) rc = fill_words(e->attn_counters, c.n_kv_heads, 0u, s);
     if (!rc) rc = dalloc(e, (void **)&e->state, sizeof(StepState));
     e->ids_alloc = c.max_seq + 2;
     if (!rc) rc = dalloc_t(e, &e->ids, e->ids_alloc);
@@ -382,9 +416,8 @@ static int engine_synth(llama_engine *e, uint64_t seed)
 
 static int engine_finish(llama_engine *e)
 {
-    int rc = hip_check(hipStreamSynchronize(e->stream), "hipStreamSynchronize(create)");
-    if (!rc) rc = capture_graph(e);
-    return rc;
+    // step graphs are captured by llama_engine_begin for the positions it can reach
+    return hip_check(hipStreamSynchronize(e->stream), "hipStreamSynchronize(create)");
 }
 
 // ---------------------------------------------------------------- real weights
@@ -619,6 +652,10 @@ int llama_engine_begin(llama_engine *e, const uint32_t *prompt, uint32_t n_promp
     e->h_pos = pos0;
     e->h_step = 0;
     e->h_ids_cap = ids_cap;
+    // the step graphs for every position this generation can reach
+    const int64_t last = std::min<int64_t>((int64_t)pos0 + ids_cap - 2, (int64_t)e->c.max_seq - 1);
+    rc = step_graphs_for(e, pos0, std::max<int64_t>(last, pos0));
+    if (rc) return rc;
     e->armed = true;
     return RFP4_OK;
 }
@@ -634,7 +671,15 @@ int llama_engine_run_steps(llama_engine *e, uint32_t n_steps)
         return set_error(RFP4_E_CAPACITY, "steps exceed the token array (%lld + %u > %lld)", (long long)e->h_step, n_steps,
                          (long long)(e->h_ids_cap - 1));
     for (uint32_t i = 0; i < n_steps; i++) {
-        int rc = e->use_graph ? hip_check(hipGraphLaunch(e->graph_exec, e->stream), "hipGraphLaunch") : enqueue_step(e);
+        const uint32_t ns = splits_at(e, e->h_pos + i);
+        int rc;
+        if (e->use_graph) {
+            hipGraphExec_t g;
+            rc = step_graph(e, ns, &g);
+            if (!rc) rc = hip_check(hipGraphLaunch(g, e->stream), "hipGraphLaunch");
+        } else {
+            rc = enqueue_step(e, ns);
+        }
         if (rc) return rc;
     }
     e->h_pos += n_steps;

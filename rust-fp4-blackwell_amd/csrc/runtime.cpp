@@ -283,6 +283,14 @@ GemvVariant gemv_variant(uint32_t n, uint32_t k, int epi, bool f32scale)
 
 static thread_local int t_attn_merge = 0; // 0 automatic, 1 merge kernel, 2 in-kernel merge where it fits
 
+int attn_merge_mode() { return t_attn_merge; }
+
+bool attn_inmerge_mode(int mode, uint32_t splits)
+{
+    if (splits <= 1 || splits > kAttnInmergeMaxSplits) return false;
+    return mode != 1;
+}
+
 bool attn_inmerge(uint32_t max_splits)
 {
     // In-kernel when the last split's merge is one round of loads (few
@@ -467,9 +475,10 @@ int attn_launch(const AttnArgs &args, int kv_f16, hipStream_t s, uint32_t max_se
     if (args.chunk == 0) return set_error(RFP4_E_INVALID, "attn: chunk must be positive");
     if (args.cosv && !kv_f16) return set_error(RFP4_E_INVALID, "attn: fused KV append needs an fp16 cache");
     if (rows == 0 || (rows > 1 && args.cosv)) return set_error(RFP4_E_INVALID, "attn: fused append is one row only");
-    if (args.counters && (rows != 1 || args.max_splits > kAttnInmergeMaxSplits))
-        return set_error(RFP4_E_INVALID, "attn: the in-kernel merge takes one row and at most %u splits", kAttnInmergeMaxSplits);
     uint32_t splits = (max_seq_for_grid + args.chunk - 1) / args.chunk;
+    if (splits > args.max_splits) return set_error(RFP4_E_INVALID, "attn: %u splits exceed the workspace's %u", splits, args.max_splits);
+    if (args.counters && (rows != 1 || splits > kAttnInmergeMaxSplits))
+        return set_error(RFP4_E_INVALID, "attn: the in-kernel merge takes one row and at most %u splits", kAttnInmergeMaxSplits);
     AttnArgs a = args;
     int rc = launch(name, dim3(a.n_kv_heads, splits, rows), dim3(256), s, &a);
     if (rc || splits <= 1 || a.counters) return rc;

@@ -46,6 +46,8 @@ uint32_t attn_sub_chunk(uint32_t head_dim, uint32_t elem_bytes, uint32_t group);
 // Whether one-row attention with `max_splits` splits merges inside the split
 // kernel (arrival counters) instead of in a second launch.
 bool attn_inmerge(uint32_t max_splits);
+int attn_merge_mode();                           // this thread's rfp4_debug_attn_merge setting
+bool attn_inmerge_mode(int mode, uint32_t splits); // attn_inmerge under an explicit setting
 constexpr uint32_t kAttnInmergeMaxSplits = 8;
 uint32_t attn_chunk_for(uint32_t n_kv_heads, uint32_t seq, uint32_t num_cus, uint32_t head_dim, uint32_t elem_bytes,
                         uint32_t group);
