@@ -248,7 +248,7 @@ RFP4_DEV void attn_body(const AttnArgs &a)
     do {                                                                                        \
         _Pragma("unroll") for (int s_ = 0; s_ < NSTEP; s_++) {                         \
             const uint32_t t_ = min((C) * CAPT + (uint32_t)s_ * TPS + (uint32_t)slot, nt - 1u); \
-            R[s_] = *(const uint4 *)((BASE) + (size_t)(t0 + t_) * a.ts + (size_t)li * EPL);    \
+            R[s_] = load_nt16((BASE) + (size_t)(t0 + t_) * a.ts + (size_t)li * EPL);           \
         }                                                                                       \
     } while (0)
     RFP4_ATTN_LOAD(kr, kc, 0u);

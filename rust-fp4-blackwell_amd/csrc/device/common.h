@@ -8,6 +8,18 @@
 #define RFP4_DEV __device__ __forceinline__
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Non-temporal loads for data read once per launch (weights, KV rows): on
+// MI355X a one-launch stream of 58.7 MB measured 10.4 us with them against
+// 11.1 us with ordinary loads.
+RFP4_DEV uint4 load_nt16(const void *p)
+{
+    const u32x4 v = __builtin_nontemporal_load((const u32x4 *)p);
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+RFP4_DEV uint32_t load_nt_u8(const uint8_t *p) { return __builtin_nontemporal_load(p); }
+RFP4_DEV uint32_t load_nt_u32(const uint32_t *p) { return __builtin_nontemporal_load(p); }
 
 // ---------------------------------------------------------------- wave64 reductions
 // DPP controls (GCN/CDNA encoding).

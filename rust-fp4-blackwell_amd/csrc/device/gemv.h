@@ -128,8 +128,8 @@ RFP4_DEV void stage_x_regs(float *xs, const float4 *xr, const uint2 *wr, uint32_
 template <int SCALE_F32>
 RFP4_DEV uint32_t load_scale_bits(const void *scales, size_t idx)
 {
-    if (SCALE_F32) return ((const uint32_t *)scales)[idx];
-    return ((const uint8_t *)scales)[idx];
+    if (SCALE_F32) return load_nt_u32((const uint32_t *)scales + idx);
+    return load_nt_u8((const uint8_t *)scales + idx);
 }
 
 template <int SCALE_F32>
@@ -210,7 +210,7 @@ RFP4_DEV void gemv_body(const GemvArgs &a)
             const uint32_t cl = min((uint32_t)lane + 64u * (uint32_t)s, clast);
 #pragma unroll
             for (int p = 0; p < NP; p++) {
-                q[s][p] = *(const uint4 *)(rowp[p] + (size_t)cl * 16u);
+                q[s][p] = load_nt16(rowp[p] + (size_t)cl * 16u);
                 sb[s][p] = load_scale_bits<SCALE_F32>(a.scales, srow[p] + cl);
             }
         }
@@ -235,8 +235,8 @@ RFP4_DEV void gemv_body(const GemvArgs &a)
             float sc[NP];
 #pragma unroll
             for (int p = 0; p < NP; p++) {
-                q[p] = *(const uint4 *)(rowp[p] + (size_t)c * 16u);
-                sc[p] = load_scale<SCALE_F32>(a.scales, srow[p] + c);
+                q[p] = load_nt16(rowp[p] + (size_t)c * 16u);
+                sc[p] = scale_from_bits<SCALE_F32>(load_scale_bits<SCALE_F32>(a.scales, srow[p] + c));
             }
             float4 xv[8];
             const float4 *xp = (const float4 *)(xs + (size_t)c * GEMV_XS_CHUNK);
