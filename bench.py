@@ -277,6 +277,7 @@ def main():
     ap.add_argument("--no-tiny", action="store_true", help="skip the TinyLlama-1.1B line")
     ap.add_argument("--no-gemm", action="store_true", help="skip the config-5 batched GEMM figures")
     ap.add_argument("--no-prefill", action="store_true", help="skip the batched prefill figure")
+    ap.add_argument("--prefill-tokens", type=int, default=512, help="prompt length of the batched prefill figure")
     ap.add_argument("--pmc-probe", action="store_true", help="only the launch sequence of the counter runs")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -306,9 +307,9 @@ def main():
     log(f"GEMV path: {path_bytes / 1e9:.3f} GB in {path_ms * 1e3:.1f} us -> {path_gbs:.0f} GB/s; "
         f"gate/up GEMV {gate_ms * 1e3:.2f} us -> {gate_gbs:.0f} GB/s")
     gemm = None if args.no_gemm else gemm_config5(rf, eng, cfg)
-    prefill = None if args.no_prefill else prefill_run(rf, eng, cfg)
+    prefill = None if args.no_prefill else prefill_run(rf, eng, cfg, n=args.prefill_tokens)
     if prefill:
-        log(f"prefill 512: {prefill['ms']} ms, {prefill['tok_s']} tok/s, {prefill['TFLOP_s']} TFLOP/s")
+        log(f"prefill {prefill['tokens']}: {prefill['ms']} ms, {prefill['tok_s']} tok/s, {prefill['TFLOP_s']} TFLOP/s")
     eng.close()
 
     tiny = None

@@ -129,6 +129,15 @@ int attn_decode(rfp4_stream_t stream, uint32_t n_heads, uint32_t n_kv_heads, uin
 int attn_decode_f16(rfp4_stream_t stream, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
                     uint32_t seq, const float *q, const uint16_t *kc, const uint16_t *vc, uint64_t token_stride,
                     uint64_t head_stride, float *out);
+/* Causal attention of `rows` query rows at positions pos0 .. pos0+rows-1 over
+ * fp16 K/V (the rows' own k, v already in the caches): row r is attn_decode_f16
+ * with seq = pos0 + r + 1 (llama_run/src/main.rs:148-242 applied row by row;
+ * the reference feeds a prompt one token at a time, :550-556).  q row r at
+ * q + r*q_row_stride, out row r at out + r*out_row_stride (floats).  fp16
+ * matrix-core operands, f32 accumulation.  No reference counterpart as one call. */
+int attn_prefill_f16(rfp4_stream_t stream, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim, uint32_t pos0,
+                     uint32_t rows, const float *q, uint32_t q_row_stride, const uint16_t *kc, const uint16_t *vc,
+                     uint64_t token_stride, uint64_t head_stride, float *out, uint32_t out_row_stride);
 /* swiglu(n, gate, up, out): llama_run/src/main.rs:244-252 */
 int swiglu(rfp4_stream_t stream, uint32_t n, const float *gate, const float *up, float *out);
 /* residual(n, y, x): x += y, llama_run/src/main.rs:254-261 */
@@ -176,6 +185,10 @@ int rfp4_debug_attn_chunk(uint32_t chunk);
  * split of each KV head inside the attention kernel wherever it can (at most
  * 8 splits).  No reference counterpart. */
 int rfp4_debug_attn_merge(int mode);
+/* Test hook: the batched prefill's attention on this thread: 0 = the
+ * matrix-core prefill kernel, 1 = the decode kernel, one grid row per prompt
+ * row.  No reference counterpart. */
+int rfp4_debug_prefill_attn(int mode);
 /* The tile and K split fp4_gemm would use for this shape (honours the test
  * hook).  No reference counterpart. */
 int rfp4_gemm_plan(uint32_t m, uint32_t n, uint32_t k, int *tile_m, int *tile_n, int *kz);
@@ -221,6 +234,9 @@ int rfp4_selftest_cvt_bf16(rfp4_stream_t stream, uint32_t n, const uint32_t *wor
 /* One v_mfma_f32_16x16x32_bf16 from raw per-lane registers (4 dwords per
  * lane for a and b); out receives 4 accumulator floats per lane. */
 int rfp4_mma_bf16_tile(rfp4_stream_t stream, const uint32_t *a, const uint32_t *b, float *out);
+/* The same with fp16 operands (v_mfma_f32_16x16x32_f16, the prefill
+ * attention's instruction).  Test hook; no reference counterpart. */
+int rfp4_mma_f16_tile(rfp4_stream_t stream, const uint32_t *a, const uint32_t *b, float *out);
 /* Synthetic weight generator used by the engine (rows [r0, r0+nrows)). */
 int rfp4_synth_mx_weight(rfp4_stream_t stream, uint64_t seed, uint64_t stream_id, float sigma, uint64_t k,
                          uint64_t r0, uint64_t nrows, uint8_t *codes, uint8_t *scales);

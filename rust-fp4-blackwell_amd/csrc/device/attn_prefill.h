@@ -1,0 +1,231 @@
+// Causal GQA attention for the batched prefill (gfx950 matrix cores).
+//
+// Semantics as attn.h for every prompt row r (absolute position pos0 + r):
+//   out[r][h] = softmax over t <= pos0 + r of (q_h . k_t) / sqrt(HD), times v_t
+// (llama_run/src/main.rs:148-242 applied row by row), with the prompt's own
+// rows already appended to the fp16 caches.
+//
+// Grid (query tiles, n_kv_heads).  A workgroup takes BQ prompt rows and every
+// query head of one KV head (GT heads, G <= GT real), i.e. NT = (BQ/16) * GT
+// tiles of 16 (row, head) pairs, MT per wave, and walks the keys 0 .. last
+// row's position in blocks of 32: K rows staged in LDS as loaded, V rows
+// staged transposed (dimension-major), both as v_mfma_f32_16x16x32_f16
+// operands read with one 16-byte LDS read per lane:
+//   S (16 x 32) = Q (16 x HD) . K^T        -- A = q as two fp16 terms
+//   online softmax per row (base 2, f32)   -- rows live in 16-lane groups
+//   O (16 x HD) += P (16 x 32) . V         -- A = p as two fp16 terms, through LDS
+// q and p enter as hi + lo (hi = fp16(x), lo = fp16(x - hi): about 2^-22
+// relative, two MFMAs per product; K and V are fp16 already), products exact
+// and f32 accumulation, so the output matches the f32 decode kernel's to
+// about 1e-6: one fp16 rounding of q and p (2^-11) moves enough of the O
+// projection's MXFP4 input codes across rounding boundaries to shift the
+// logits by percent.  Operand
+// layout (pinned by the fp16 layout test): lane l holds A row / B column
+// l % 16 and K = 8 (l / 16) .. +7; accumulator r of lane l is D[4 (l/16) + r][l % 16].
+// The next block's K/V loads are in flight while the current block computes.
+#pragma once
+#include "common.h"
+
+typedef _Float16 pf_f16x8 __attribute__((ext_vector_type(8)));
+typedef float pf_f32x4 __attribute__((ext_vector_type(4)));
+
+#define PF_BK 32   // keys per block
+#define PF_KPAD 8  // fp16 padding of a staged K row (16 consecutive rows -> 16 distinct bank groups)
+#define PF_TPAD 8  // fp16 padding of a transposed V row / a P row
+
+// x -> hi + lo, both fp16 (hi = fp16(x), lo = fp16(x - hi); x - hi is exact)
+RFP4_DEV void pf_split8(const float *v, pf_f16x8 &hi, pf_f16x8 &lo)
+{
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const _Float16 h = (_Float16)v[i];
+        hi[i] = h;
+        lo[i] = (_Float16)(v[i] - (float)h);
+    }
+}
+
+RFP4_DEV float pf_row16_max(float v)
+{
+    v = fmaxf(v, dpp_mov<DPP_QUAD_1032>(v));
+    v = fmaxf(v, dpp_mov<DPP_QUAD_2301>(v));
+    v = fmaxf(v, dpp_mov<DPP_ROW_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_mov<DPP_ROW_MIRROR>(v));
+    return v;
+}
+
+template <int HD, int GT>
+RFP4_DEV void attn_prefill_body(const AttnPrefillArgs &a)
+{
+    const uint32_t pos0 = a.pos0, nrows = a.rows;
+    constexpr int BQ = GT >= 4 ? 16 : 64 / GT;       // prompt rows per workgroup
+    constexpr int NT = (BQ / 16) * GT;               // 16-row tiles per workgroup
+    constexpr int MT = NT / 4;                       // tiles per wave
+    constexpr int KS = HD / 32;                      // K steps of S = Q K^T
+    constexpr int NN = HD / 16;                      // 16-wide column tiles of O
+    constexpr int KROW = HD + PF_KPAD, TROW = PF_BK + PF_TPAD;
+    constexpr int LPK = HD / 8;                      // 16-byte pieces per K/V row
+    constexpr int LD = PF_BK * LPK / 256;            // K (and V) pieces per thread per block
+    static_assert(NT % 4 == 0 && MT >= 1, "tiles per wave");
+    static_assert(LD >= 1 && PF_BK * LPK % 256 == 0, "block load split");
+    __shared__ __align__(16) _Float16 ks[PF_BK][KROW];
+    __shared__ __align__(16) _Float16 vt[HD][TROW];
+    __shared__ __align__(16) _Float16 ps[4][MT][2][16][TROW]; // P hi, lo
+
+    const uint32_t kvh = blockIdx.y, r0 = blockIdx.x * BQ;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t l16 = (uint32_t)lane & 15u, q4 = (uint32_t)lane >> 4;
+    const uint32_t G = a.n_heads / a.n_kv_heads;
+    const uint16_t *kc = a.kc + (size_t)kvh * a.hs;
+    const uint16_t *vc = a.vc + (size_t)kvh * a.hs;
+    // keys of this workgroup: 0 .. position of its last row
+    const uint32_t last_row = min(r0 + (uint32_t)BQ, nrows) - 1u;
+    const uint32_t nk = pos0 + last_row + 1u;
+    const uint32_t nblk = (nk + PF_BK - 1) / PF_BK;
+    const float scale = __fmul_rn(1.4426950408889634f, __fdiv_rn(1.0f, __fsqrt_rn((float)HD))); // log2(e) / sqrt(HD)
+
+    // ---- Q tiles of this wave as fp16 A operands (rows past the prompt or heads past G: zero)
+    pf_f16x8 qa[MT][KS], ql[MT][KS];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) {
+        const uint32_t t = (uint32_t)(wave * MT + mt), g = t % GT, row = r0 + 16u * (t / GT) + l16;
+        const bool in = row < nrows && g < G;
+        const float *qp = a.q + (size_t)min(row, nrows - 1u) * a.q_rs + (size_t)(kvh * G + min(g, G - 1u)) * HD + 8u * q4;
+#pragma unroll
+        for (int k = 0; k < KS; k++) {
+            float v[8];
+            const float4 x0 = *(const float4 *)(qp + 32 * k), x1 = *(const float4 *)(qp + 32 * k + 4);
+            v[0] = x0.x; v[1] = x0.y; v[2] = x0.z; v[3] = x0.w;
+            v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[i] = in ? v[i] : 0.0f;
+            pf_split8(v, qa[mt][k], ql[mt][k]);
+        }
+    }
+
+    pf_f32x4 o[MT][NN];
+    float mrun[MT][4], lrun[MT][4];
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            mrun[mt][r] = -3.402823466e38f;
+            lrun[mt][r] = 0.0f;
+        }
+#pragma unroll
+        for (int n = 0; n < NN; n++) o[mt][n] = {0.0f, 0.0f, 0.0f, 0.0f};
+    }
+
+    // ---- K / V block loads: K piece (key tid / LPK, dims 8 (tid % LPK)), V
+    // piece (key tid % 32, dims 8 (tid / 32)) -- consecutive lanes take
+    // consecutive keys, so the transposed V writes fall on consecutive halves
+    uint4 kr[LD], vr[LD];
+#define RFP4_PF_LOAD(B)                                                                                   \
+    do {                                                                                                  \
+        _Pragma("unroll") for (int j = 0; j < LD; j++) {                                                  \
+            const uint32_t p = (uint32_t)tid + 256u * (uint32_t)j;                                        \
+            const uint32_t kk = min((B) * PF_BK + p / LPK, nk - 1u), kd = 8u * (p % LPK);                 \
+            kr[j] = load_nt16(kc + (size_t)kk * a.ts + kd);                                               \
+            const uint32_t vk = min((B) * PF_BK + p % PF_BK, nk - 1u), vd = 8u * (p / PF_BK);              \
+            vr[j] = load_nt16(vc + (size_t)vk * a.ts + vd);                                               \
+        }                                                                                                 \
+    } while (0)
+    RFP4_PF_LOAD(0u);
+
+    for (uint32_t b = 0; b < nblk; b++) {
+        __syncthreads(); // the previous block's LDS reads are done
+#pragma unroll
+        for (int j = 0; j < LD; j++) {
+            const uint32_t p = (uint32_t)tid + 256u * (uint32_t)j;
+            *(uint4 *)&ks[p / LPK][8u * (p % LPK)] = kr[j];
+            const uint32_t vk = p % PF_BK, vd = 8u * (p / PF_BK);
+            const uint32_t w[4] = {vr[j].x, vr[j].y, vr[j].z, vr[j].w};
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                vt[vd + 2u * i][vk] = __builtin_bit_cast(_Float16, (uint16_t)(w[i] & 0xFFFFu));
+                vt[vd + 2u * i + 1u][vk] = __builtin_bit_cast(_Float16, (uint16_t)(w[i] >> 16));
+            }
+        }
+        __syncthreads();
+        if (b + 1u < nblk) RFP4_PF_LOAD(b + 1u);
+
+#pragma unroll
+        for (int mt = 0; mt < MT; mt++) {
+            const uint32_t t = (uint32_t)(wave * MT + mt);
+            // ---- S = Q K^T for the block's two 16-key halves
+            pf_f32x4 s[2];
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                s[h] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int k = 0; k < KS; k++) {
+                    const pf_f16x8 kb = *(const pf_f16x8 *)&ks[16u * h + l16][32 * k + 8u * q4];
+                    s[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[mt][k], kb, s[h], 0, 0, 0);
+                    s[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[mt][k], kb, s[h], 0, 0, 0);
+                }
+            }
+            // ---- causal mask, online softmax (base 2) per row 4 q4 + r
+            float p[2][4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const uint32_t qrow = r0 + 16u * (t / GT) + 4u * q4 + (uint32_t)r;
+                const uint32_t qpos = pos0 + min(qrow, nrows - 1u);
+                float mx = -3.402823466e38f;
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const uint32_t key = b * PF_BK + 16u * h + l16;
+                    const float v = s[h][r] * scale;
+                    p[h][r] = key <= qpos ? v : -3.402823466e38f;
+                    mx = fmaxf(mx, p[h][r]);
+                }
+                mx = pf_row16_max(mx);
+                const float mnew = fmaxf(mrun[mt][r], mx);
+                const float alpha = __builtin_amdgcn_exp2f(mrun[mt][r] - mnew);
+                mrun[mt][r] = mnew;
+                float ls = 0.0f;
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    p[h][r] = __builtin_amdgcn_exp2f(p[h][r] - mnew);
+                    ls += p[h][r];
+                }
+                lrun[mt][r] = fmaf(lrun[mt][r], alpha, row16_sum(ls));
+#pragma unroll
+                for (int n = 0; n < NN; n++) o[mt][n][r] *= alpha;
+            }
+            // ---- P (hi, lo) to the A layout through LDS (this wave's rows only)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+#pragma unroll
+                for (int h = 0; h < 2; h++) {
+                    const _Float16 ph = (_Float16)p[h][r];
+                    ps[wave][mt][0][4u * q4 + (uint32_t)r][16u * h + l16] = ph;
+                    ps[wave][mt][1][4u * q4 + (uint32_t)r][16u * h + l16] = (_Float16)(p[h][r] - (float)ph);
+                }
+            __builtin_amdgcn_wave_barrier();
+            const pf_f16x8 pa = *(const pf_f16x8 *)&ps[wave][mt][0][l16][8u * q4];
+            const pf_f16x8 pl = *(const pf_f16x8 *)&ps[wave][mt][1][l16][8u * q4];
+            // ---- O += P V
+#pragma unroll
+            for (int n = 0; n < NN; n++) {
+                const pf_f16x8 vb = *(const pf_f16x8 *)&vt[16u * n + l16][8u * q4];
+                o[mt][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, o[mt][n], 0, 0, 0);
+                o[mt][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vb, o[mt][n], 0, 0, 0);
+            }
+        }
+    }
+#undef RFP4_PF_LOAD
+
+    // ---- out[row][head][dim] = O / l for rows in the prompt and heads < G
+#pragma unroll
+    for (int mt = 0; mt < MT; mt++) {
+        const uint32_t t = (uint32_t)(wave * MT + mt), g = t % GT;
+        if (g >= G) continue;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const uint32_t row = r0 + 16u * (t / GT) + 4u * q4 + (uint32_t)r;
+            if (row >= nrows) continue;
+            float *op = a.out + (size_t)row * a.out_rs + (size_t)(kvh * G + g) * HD + l16;
+#pragma unroll
+            for (int n = 0; n < NN; n++) op[16 * n] = __fdiv_rn(o[mt][n][r], lrun[mt][r]);
+        }
+    }
+}

@@ -51,16 +51,23 @@ RFP4_DEV void mma32_tile_body(const MmaTileArgs &a)
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
 
-// One v_mfma_f32_16x16x32_bf16 from raw per-lane registers: a, b hold 4
-// dwords (8 bf16) per lane; out receives the 4 accumulator floats per lane.
+// One v_mfma_f32_16x16x32_bf16 (mode 0) or v_mfma_f32_16x16x32_f16 (mode 1)
+// from raw per-lane registers: a, b hold 4 dwords (8 bf16 / fp16) per lane;
+// out receives the 4 accumulator floats per lane.
 RFP4_DEV void mma_bf16_tile_body(const MmaTileArgs &a)
 {
     const int lane = threadIdx.x & 63;
     uint4 ar = ((const uint4 *)a.a)[lane], br = ((const uint4 *)a.b)[lane];
-    bf16x8_t av = __builtin_bit_cast(bf16x8_t, ar), bv = __builtin_bit_cast(bf16x8_t, br);
     v4f32 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc, 0, 0, 0);
+    if (a.mode == 1) { // fp16 operands: v_mfma_f32_16x16x32_f16
+        const f16x8_t av = __builtin_bit_cast(f16x8_t, ar), bv = __builtin_bit_cast(f16x8_t, br);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, bv, acc, 0, 0, 0);
+    } else {
+        const bf16x8_t av = __builtin_bit_cast(bf16x8_t, ar), bv = __builtin_bit_cast(bf16x8_t, br);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(av, bv, acc, 0, 0, 0);
+    }
 #pragma unroll
     for (int r = 0; r < 4; r++) a.out[lane * 4 + r] = acc[r];
 }

@@ -67,7 +67,7 @@ struct llama_engine {
     bool armed = false;
     // batched prefill workspace (rows of the prompt), grown on demand
     uint32_t pf_cap = 0;
-    float *pf_x = nullptr, *pf_c = nullptr, *pf_a = nullptr, *pf_part = nullptr;
+    float *pf_x = nullptr, *pf_c = nullptr, *pf_a = nullptr, *pf_part = nullptr; // pf_part: decode-kernel test path only
     uint8_t *pf_codes = nullptr, *pf_scales = nullptr;
     uint32_t *pf_ids = nullptr;
 };
@@ -170,7 +170,6 @@ static int prefill_reserve(llama_engine *e, uint32_t n)
     int rc = dalloc_t(e, &e->pf_x, (size_t)cap * c.dim);
     if (!rc) rc = dalloc_t(e, &e->pf_c, (size_t)cap * ncols);
     if (!rc) rc = dalloc_t(e, &e->pf_a, (size_t)cap * qd);
-    if (!rc) rc = dalloc_t(e, &e->pf_part, (size_t)cap * c.n_heads * e->attn_max_splits * (c.head_dim + 4));
     if (!rc) rc = dalloc_t(e, &e->pf_codes, (size_t)cap * kmax / 2);
     if (!rc) rc = dalloc_t(e, &e->pf_scales, (size_t)cap * kmax / 32);
     if (!rc) rc = dalloc_t(e, &e->pf_ids, cap);
@@ -206,13 +205,24 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
         ra.rows = n; ra.row_stride = nqkv; ra.n_heads = c.n_heads; ra.n_kv_heads = c.n_kv_heads;
         ra.head_dim = hd; ra.pos0 = pos0;
         if ((rc = launch("rfp4_rope_kv_rows", dim3(n), dim3(256), s, &ra))) return rc;
-        AttnArgs aa{};
-        aa.q = e->pf_c; aa.q_rs = nqkv; aa.kc = kc; aa.vc = vc; aa.out = e->pf_a; aa.out_rs = qd;
-        aa.part = e->pf_part; aa.pos_ptr = nullptr; aa.seq = pos0 + 1; // row r sees pos0 + r + 1 positions
-        aa.ts = hd; aa.hs = (uint64_t)e->max_seq_alloc * hd;
-        aa.n_heads = c.n_heads; aa.n_kv_heads = c.n_kv_heads; aa.head_dim = hd;
-        aa.chunk = e->attn_chunk; aa.max_splits = e->attn_max_splits;
-        if ((rc = attn_launch(aa, 1, s, pos0 + n, n))) return rc;
+        // causal attention of the prompt rows (row r sees positions 0 .. pos0 + r)
+        if (prefill_attn_mode() == 1) {
+            // test path: the decode kernel, one query row per grid z (split states per row)
+            if (!e->pf_part &&
+                (rc = dalloc_t(e, &e->pf_part, (size_t)e->pf_cap * c.n_heads * e->attn_max_splits * (hd + 4))))
+                return rc;
+            AttnArgs aa{};
+            aa.q = e->pf_c; aa.q_rs = nqkv; aa.kc = kc; aa.vc = vc; aa.out = e->pf_a; aa.out_rs = qd;
+            aa.part = e->pf_part; aa.pos_ptr = nullptr; aa.seq = pos0 + 1;
+            aa.ts = hd; aa.hs = (uint64_t)e->max_seq_alloc * hd;
+            aa.n_heads = c.n_heads; aa.n_kv_heads = c.n_kv_heads; aa.head_dim = hd;
+            aa.chunk = e->attn_chunk; aa.max_splits = e->attn_max_splits;
+            if ((rc = attn_launch(aa, 1, s, pos0 + n, n))) return rc;
+        } else {
+            AttnPrefillArgs pa{e->pf_c, kc, vc, e->pf_a, hd, (uint64_t)e->max_seq_alloc * hd, nqkv, qd,
+                               c.n_heads, c.n_kv_heads, pos0, n};
+            if ((rc = attn_prefill_launch(pa, hd, s))) return rc;
+        }
         if ((rc = mx4_quantize(s, n, qd, e->pf_a, 0, e->pf_codes, e->pf_scales))) return rc;
         if ((rc = fp4_gemm(s, n, c.dim, qd, e->pf_codes, e->pf_scales, w.o_c, w.o_s, e->pf_c))) return rc;
         if ((rc = residual(s, n * c.dim, e->pf_c, e->pf_x))) return rc;

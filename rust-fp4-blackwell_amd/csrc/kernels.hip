@@ -13,6 +13,7 @@
 #include "device/gemm.h"
 #include "device/gemm_skinny.h"
 #include "device/prefill.h"
+#include "device/attn_prefill.h"
 
 #define K256 extern "C" __global__ __launch_bounds__(256)
 #define K1024 extern "C" __global__ __launch_bounds__(1024)
@@ -132,6 +133,13 @@ ATTN_KERNELS(64, f32, float)
 ATTN_KERNELS(64, f16, uint16_t)
 ATTN_KERNELS(128, f32, float)
 ATTN_KERNELS(128, f16, uint16_t)
+#define ATTN_PREFILL_KERNELS(HD) \
+    K256 void rfp4_attn_prefill_hd##HD##_g1(AttnPrefillArgs a) { attn_prefill_body<HD, 1>(a); } \
+    K256 void rfp4_attn_prefill_hd##HD##_g2(AttnPrefillArgs a) { attn_prefill_body<HD, 2>(a); } \
+    K256 void rfp4_attn_prefill_hd##HD##_g4(AttnPrefillArgs a) { attn_prefill_body<HD, 4>(a); } \
+    K256 void rfp4_attn_prefill_hd##HD##_g8(AttnPrefillArgs a) { attn_prefill_body<HD, 8>(a); }
+ATTN_PREFILL_KERNELS(64)
+ATTN_PREFILL_KERNELS(128)
 K256 void rfp4_attn_merge_hd64(AttnArgs a) { attn_merge_body<64>(a); }
 K256 void rfp4_attn_merge_hd128(AttnArgs a) { attn_merge_body<128>(a); }
 

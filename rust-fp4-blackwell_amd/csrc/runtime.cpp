@@ -285,6 +285,9 @@ static thread_local int t_attn_merge = 0; // 0 automatic, 1 merge kernel, 2 in-k
 
 int attn_merge_mode() { return t_attn_merge; }
 
+static thread_local int t_prefill_attn = 0; // 0 matrix-core prefill kernel, 1 one decode-kernel row per prompt row
+int prefill_attn_mode() { return t_prefill_attn; }
+
 bool attn_inmerge_mode(int mode, uint32_t splits)
 {
     if (splits <= 1 || splits > kAttnInmergeMaxSplits) return false;
@@ -450,6 +453,14 @@ extern "C" int rfp4_debug_gemv_waves(int waves)
     return RFP4_OK;
 }
 
+extern "C" int rfp4_debug_prefill_attn(int mode)
+{
+    using namespace rfp4;
+    if (mode != 0 && mode != 1) return set_error(RFP4_E_INVALID, "prefill attention mode must be 0 (matrix cores) or 1 (decode kernel per row)");
+    t_prefill_attn = mode;
+    return RFP4_OK;
+}
+
 extern "C" int rfp4_debug_gemv_variant(int rows_per_wave, int slices)
 {
     using namespace rfp4;
@@ -485,6 +496,22 @@ int attn_launch(const AttnArgs &args, int kv_f16, hipStream_t s, uint32_t max_se
     // the split states are merged by a second launch (stream order, no fence)
     return launch(args.head_dim == 64 ? "rfp4_attn_merge_hd64" : "rfp4_attn_merge_hd128", dim3(a.n_heads, 1, rows),
                   dim3(256), s, &a);
+}
+
+int attn_prefill_launch(const AttnPrefillArgs &a, uint32_t head_dim, hipStream_t s)
+{
+    if (!a.q || !a.kc || !a.vc || !a.out) return set_error(RFP4_E_INVALID, "attn prefill: null pointer");
+    if (head_dim != 64 && head_dim != 128) return set_error(RFP4_E_SHAPE, "attn prefill: head_dim %u (64 or 128)", head_dim);
+    if (a.n_kv_heads == 0 || a.n_heads % a.n_kv_heads || a.n_heads / a.n_kv_heads > 8)
+        return set_error(RFP4_E_SHAPE, "attn prefill: %u query heads over %u KV heads (group of at most 8)", a.n_heads,
+                         a.n_kv_heads);
+    if (a.rows == 0) return RFP4_OK;
+    const uint32_t g = attn_group_pad(a.n_heads / a.n_kv_heads);
+    const uint32_t bq = g >= 4u ? 16u : 64u / g; // prompt rows per workgroup (device/attn_prefill.h)
+    char name[48];
+    snprintf(name, sizeof name, "rfp4_attn_prefill_hd%u_g%u", head_dim, g);
+    AttnPrefillArgs args = a;
+    return launch(name, dim3((a.rows + bq - 1) / bq, a.n_kv_heads), dim3(256), s, &args);
 }
 
 uint32_t attn_group_pad(uint32_t group) { return group <= 1u ? 1u : group <= 2u ? 2u : group <= 4u ? 4u : 8u; }
@@ -696,6 +723,21 @@ int attn_decode_f16(rfp4_stream_t stream, uint32_t n_heads, uint32_t n_kv_heads,
 {
     return attn_common((hipStream_t)stream, n_heads, n_kv_heads, head_dim, seq, q, kc, vc, token_stride, head_stride,
                        out, 1);
+}
+
+int attn_prefill_f16(rfp4_stream_t stream, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim, uint32_t pos0,
+                     uint32_t rows, const float *q, uint32_t q_row_stride, const uint16_t *kc, const uint16_t *vc,
+                     uint64_t token_stride, uint64_t head_stride, float *out, uint32_t out_row_stride)
+{
+    if (!runtime()) return set_error(RFP4_E_NOT_INIT, "rfp4_init has not been called");
+    if (((uintptr_t)q | (uintptr_t)kc | (uintptr_t)vc) & 15u || q_row_stride % 4u || (token_stride * 2u) % 16u)
+        return set_error(RFP4_E_ALIGN, "attn_prefill_f16: q rows and K/V rows must start 16-byte aligned");
+    if (rows && q_row_stride < n_heads * head_dim)
+        return set_error(RFP4_E_SHAPE, "attn_prefill_f16: q row stride %u < %u", q_row_stride, n_heads * head_dim);
+    if (rows && out_row_stride < n_heads * head_dim)
+        return set_error(RFP4_E_SHAPE, "attn_prefill_f16: out row stride %u < %u", out_row_stride, n_heads * head_dim);
+    AttnPrefillArgs a{q, kc, vc, out, token_stride, head_stride, q_row_stride, out_row_stride, n_heads, n_kv_heads, pos0, rows};
+    return attn_prefill_launch(a, head_dim, (hipStream_t)stream);
 }
 
 int swiglu(rfp4_stream_t stream, uint32_t n, const float *gate, const float *up, float *out)
@@ -945,6 +987,13 @@ int rfp4_mma_bf16_tile(rfp4_stream_t stream, const uint32_t *a, const uint32_t *
 {
     if (!a || !b || !out) return set_error(RFP4_E_INVALID, "mma_bf16_tile: null pointer");
     MmaTileArgs args{a, b, nullptr, nullptr, out, 0, 0};
+    return launch("rfp4_mma_bf16_tile", dim3(1), dim3(64), (hipStream_t)stream, &args);
+}
+
+int rfp4_mma_f16_tile(rfp4_stream_t stream, const uint32_t *a, const uint32_t *b, float *out)
+{
+    if (!a || !b || !out) return set_error(RFP4_E_INVALID, "mma_f16_tile: null pointer");
+    MmaTileArgs args{a, b, nullptr, nullptr, out, 1, 0};
     return launch("rfp4_mma_bf16_tile", dim3(1), dim3(64), (hipStream_t)stream, &args);
 }
 

@@ -41,12 +41,15 @@ GemvVariant gemv_variant(uint32_t n, uint32_t k, int epi, bool f32scale);
 int gemv_launch(const char *scale_name, int epi, const GemvArgs &args, hipStream_t s, int r_override);
 uint32_t gemv_blocks(uint32_t n_logical, uint32_t k, int epi);
 int attn_launch(const AttnArgs &args, int kv_f16, hipStream_t s, uint32_t max_seq_for_grid, uint32_t rows);
-uint32_t attn_group_pad(uint32_t group); // compiled query-head group (1, 2, 4, 8) serving `group` heads
+uint32_t attn_group_pad(uint32_t group);
+// Causal prefill attention (device/attn_prefill.h), fp16 caches.
+int attn_prefill_launch(const AttnPrefillArgs &a, uint32_t head_dim, hipStream_t s); // compiled query-head group (1, 2, 4, 8) serving `group` heads
 uint32_t attn_sub_chunk(uint32_t head_dim, uint32_t elem_bytes, uint32_t group);
 // Whether one-row attention with `max_splits` splits merges inside the split
 // kernel (arrival counters) instead of in a second launch.
 bool attn_inmerge(uint32_t max_splits);
 int attn_merge_mode();                           // this thread's rfp4_debug_attn_merge setting
+int prefill_attn_mode();                         // this thread's rfp4_debug_prefill_attn setting
 bool attn_inmerge_mode(int mode, uint32_t splits); // attn_inmerge under an explicit setting
 constexpr uint32_t kAttnInmergeMaxSplits = 8;
 uint32_t attn_chunk_for(uint32_t n_kv_heads, uint32_t seq, uint32_t num_cus, uint32_t head_dim, uint32_t elem_bytes,

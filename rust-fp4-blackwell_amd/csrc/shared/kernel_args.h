@@ -97,6 +97,16 @@ typedef struct AttnArgs {
     uint32_t *counters;
 } AttnArgs;
 
+// Causal attention of the batched prefill (device/attn_prefill.h): prompt
+// row r sits at position pos0 + r and its k, v are already in the caches.
+typedef struct AttnPrefillArgs {
+    const float *q;          // row r: q + r*q_rs, [n_heads][head_dim]
+    const uint16_t *kc, *vc; // fp16 caches: element (t, kvh, d) at t*ts + kvh*hs + d
+    float *out;              // row r: out + r*out_rs, [n_heads][head_dim]
+    uint64_t ts, hs;
+    uint32_t q_rs, out_rs, n_heads, n_kv_heads, pos0, rows;
+} AttnPrefillArgs;
+
 // Batched prefill row kernels (device/prefill.h).
 typedef struct RowsArgs {
     const float *x;          // rmsnorm: rows [rows][k]; swiglu: gate|up rows [rows][2k]

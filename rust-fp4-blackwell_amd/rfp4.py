@@ -77,6 +77,7 @@ _SIGS = {
     "kv_append_f16": (I32, [P, U32, U32, P, P]),
     "attn_decode": (I32, [P, U32, U32, U32, P, P, P, P]),
     "attn_decode_f16": (I32, [P, U32, U32, U32, U32, P, P, P, U64, U64, P]),
+    "attn_prefill_f16": (I32, [P, U32, U32, U32, U32, U32, P, U32, P, P, U64, U64, P, U32]),
     "swiglu": (I32, [P, U32, P, P, P]),
     "residual": (I32, [P, U32, P, P]),
     "argmax": (I32, [P, U32, P, P]),
@@ -92,10 +93,12 @@ _SIGS = {
     "rfp4_debug_gemv_variant": (I32, [I32, I32]),
     "rfp4_debug_gemv_waves": (I32, [I32]),
     "rfp4_debug_attn_merge": (I32, [I32]),
+    "rfp4_debug_prefill_attn": (I32, [I32]),
     "rfp4_debug_gemv_path": (I32, [I32]),
     "rfp4_debug_gemv_fused": (I32, [P, I32, U32, U32, U32, P, P, P, P, F32, P, P, P]),
     "rfp4_selftest_cvt_bf16": (I32, [P, U32, P, P, P]),
     "rfp4_mma_bf16_tile": (I32, [P, P, P, P]),
+    "rfp4_mma_f16_tile": (I32, [P, P, P, P]),
     "rfp4_synth_mx_weight": (I32, [P, U64, U64, F32, U64, U64, U64, P, P]),
     "rfp4_synth_f16": (I32, [P, U64, U64, F32, F32, U64, P]),
     "llama_engine_create": (I32, [C.POINTER(ModelConfig), U64, C.POINTER(P)]),
@@ -337,6 +340,12 @@ def attn_decode(stream, n_heads, n_kv_heads, seq, q, kc, vc, out):
 def attn_decode_f16(stream, n_heads, n_kv_heads, head_dim, seq, q, kc, vc, token_stride, head_stride, out):
     check(load().attn_decode_f16(_s(stream), n_heads, n_kv_heads, head_dim, seq, _p(q), _p(kc), _p(vc),
                                  token_stride, head_stride, _p(out)))
+
+
+def attn_prefill_f16(stream, n_heads, n_kv_heads, head_dim, pos0, rows, q, q_row_stride, kc, vc, token_stride,
+                     head_stride, out, out_row_stride):
+    check(load().attn_prefill_f16(_s(stream), n_heads, n_kv_heads, head_dim, pos0, rows, _p(q), q_row_stride, _p(kc),
+                                  _p(vc), token_stride, head_stride, _p(out), out_row_stride))
 
 
 def swiglu(stream, n, gate, up, out):

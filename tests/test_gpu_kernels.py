@@ -236,6 +236,49 @@ def test_attn_decode_f16_parity(rf, orc, stream, nh, nkv, hd, seq):
     _assert_attn_close(dout.to_host(nh * hd, np.float32, stream), oref)
 
 
+@pytest.mark.parametrize("nh,nkv,hd,pos0,rows", [(32, 8, 128, 0, 40), (32, 4, 64, 0, 100), (8, 8, 64, 17, 70),
+                                                  (16, 8, 128, 300, 33), (32, 8, 128, 4000, 16), (6, 2, 64, 5, 9),
+                                                  (32, 8, 128, 7, 1), (4, 2, 64, 0, 5), (4, 2, 64, 5, 40),
+                                                  (8, 2, 128, 0, 3), (2, 2, 128, 0, 130)])
+def test_attn_prefill_f16(rf, orc, stream, nh, nkv, hd, pos0, rows):
+    """Causal prefill attention on the matrix cores: row r equals the
+    oracle's attn_decode at seq = pos0 + r + 1 over the same fp16 caches,
+    within the decode kernel's bar (q and p enter the fp16 MFMAs as hi + lo
+    fp16 terms, about 2^-22 relative); query-head groups 1, 2, 3 (padded to
+    4), 4 and 8, both head dims."""
+    rng = np.random.default_rng(pos0 * 31 + rows + hd)
+    cap = pos0 + rows + 3
+    q = rng.standard_normal((rows, nh * hd)).astype(np.float32)
+    kc = rng.standard_normal(nkv * cap * hd).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal(nkv * cap * hd).astype(np.float16).view(np.uint16)
+    oref = np.stack([orc.attn_decode(nh, nkv, hd, pos0 + r + 1, q[r], kc, vc, hd, cap * hd) for r in range(rows)])
+    dout = rf.DeviceBuffer.zeroed(rows * nh * hd, np.float32, stream)
+    rf.attn_prefill_f16(stream, nh, nkv, hd, pos0, rows, _dev(rf, q.reshape(-1), stream), nh * hd,
+                        _dev(rf, kc, stream), _dev(rf, vc, stream), hd, cap * hd, dout, nh * hd)
+    got = dout.to_host(rows * nh * hd, np.float32, stream).reshape(rows, nh * hd)
+    _assert_attn_close(got, oref)
+
+
+@pytest.mark.parametrize("nh,nkv,hd,pos0,rows", [(8, 2, 128, 0, 200), (8, 1, 64, 30, 77)])
+def test_attn_prefill_f16_strided(rf, orc, stream, nh, nkv, hd, pos0, rows):
+    """The engine's layout: q rows inside fused QKV rows (row stride
+    (nh + 2 nkv) hd), output rows padded, and a cache head stride past the
+    sequence (the cache's allocated positions)."""
+    rng = np.random.default_rng(rows * 3 + nh)
+    q_rs, out_rs, alloc = (nh + 2 * nkv) * hd, nh * hd + 64, pos0 + rows + 256
+    qkv = rng.standard_normal((rows, q_rs)).astype(np.float32)
+    kc = rng.standard_normal(nkv * alloc * hd).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal(nkv * alloc * hd).astype(np.float16).view(np.uint16)
+    oref = np.stack([orc.attn_decode(nh, nkv, hd, pos0 + r + 1, np.ascontiguousarray(qkv[r, :nh * hd]), kc, vc,
+                                     hd, alloc * hd) for r in range(rows)])
+    dout = rf.DeviceBuffer.zeroed(rows * out_rs, np.float32, stream)
+    rf.attn_prefill_f16(stream, nh, nkv, hd, pos0, rows, _dev(rf, qkv.reshape(-1), stream), q_rs,
+                        _dev(rf, kc, stream), _dev(rf, vc, stream), hd, alloc * hd, dout, out_rs)
+    got = dout.to_host(rows * out_rs, np.float32, stream).reshape(rows, out_rs)
+    _assert_attn_close(got[:, :nh * hd], oref)
+    assert not got[:, nh * hd:].any()   # the row padding is not written
+
+
 def test_swiglu_residual_copy(rf, orc, stream):
     rng = np.random.default_rng(3)
     n = 5632

@@ -4,8 +4,14 @@ same packed weights and seeds.  The reference feeds a prompt token by token
 (llama_run/src/main.rs:550-556); the oracle's prefill restates that loop with
 every projection input quantised by the OCP rules, so the two differ only in
 f32 summation order.  A value that lands within an ulp of an E2M1 rounding
-boundary can take the neighbouring code on one side, so logits and K/V are
-compared normwise (bars below) and greedy tokens exactly."""
+boundary can take the neighbouring code on one side: that changes the K/V of
+its own row in the next layer by a code step (isolated rows; every other row
+stays bit-identical) and, through attention, the logits of later rows by up
+to percent.  So layer 0's K/V (no attention upstream) must match on every
+row, later layers may hold a few such boundary rows (a wrong mask, index or
+stride corrupts most rows), greedy tokens are compared exactly and the
+logits normwise when no row took a boundary code.  The attention kernel
+itself is held to 1e-4 on identical inputs in test_gpu_kernels.py."""
 import numpy as np
 import pytest
 
@@ -16,8 +22,17 @@ TINY = dict(dim=256, n_layers=2, n_heads=4, n_kv_heads=2, head_dim=64, ffn=512, 
 TINY128 = dict(dim=512, n_layers=2, n_heads=8, n_kv_heads=2, head_dim=128, ffn=1024, vocab=2048,
                theta=500000.0, eps=1e-5, max_seq=300)
 
+G8 = dict(dim=256, n_layers=2, n_heads=8, n_kv_heads=1, head_dim=64, ffn=512, vocab=1024,
+          theta=10000.0, eps=1e-5, max_seq=200)    # 8 query heads per KV head
+G1 = dict(dim=256, n_layers=2, n_heads=2, n_kv_heads=2, head_dim=128, ffn=512, vocab=1024,
+          theta=500000.0, eps=1e-5, max_seq=200)   # no grouping
+
 LOGIT_TOL = 2e-2   # max |gpu - oracle| / max |oracle| over the vocabulary
-KV_TOL = 2e-2      # same, per layer, over the prefilled K and V
+KV_TOL = 2e-2      # same, per position, over the prefilled K and V of one layer
+
+
+def _boundary_rows_max(n):
+    return max(1, n // 64)   # positions per layer allowed to hold a neighbouring code
 
 
 def _engine(rf, cfg, seed):
@@ -38,7 +53,23 @@ def _rel(a, b):
     return float(np.max(np.abs(a - b)) / max(np.abs(b).max(), 1e-30))
 
 
-@pytest.mark.parametrize("cfg,n", [(TINY, 1), (TINY, 5), (TINY, 37), (TINY128, 3), (TINY128, 200)])
+def _check_kv(eng, ref, cfg, n_pos):
+    """Per layer, the positions whose K or V differ from the oracle's beyond
+    KV_TOL (normwise against the layer's largest value); returns their total."""
+    total = 0
+    for layer in range(cfg["n_layers"]):
+        kg, vg, kr, vr = _kv(eng, ref, cfg, layer, 0, n_pos)
+        d = np.maximum(np.abs(kg - kr).max(axis=(0, 2)) / max(np.abs(kr).max(), 1e-30),
+                       np.abs(vg - vr).max(axis=(0, 2)) / max(np.abs(vr).max(), 1e-30))
+        bad = np.nonzero(d > KV_TOL)[0]
+        limit = 0 if layer == 0 else _boundary_rows_max(n_pos)
+        assert len(bad) <= limit, f"layer {layer}: positions {bad.tolist()[:16]} differ (max {d.max():.3e})"
+        total += len(bad)
+    return total
+
+
+@pytest.mark.parametrize("cfg,n", [(TINY, 1), (TINY, 5), (TINY, 37), (TINY128, 3), (TINY128, 200), (TINY128, 250), (G8, 70),
+                                   (G1, 130)])
 def test_prefill_matches_oracle(rf, orc, cfg, n):
     seed = 0x5EED + n
     rng = np.random.default_rng(n)
@@ -50,12 +81,9 @@ def test_prefill_matches_oracle(rf, orc, cfg, n):
     rtok, rlog = ref.prefill(prompt, 0, want_logits=True)
     lg = eng.logits()
     top2 = np.sort(rlog)[-2:]
-    assert _rel(lg, rlog) <= LOGIT_TOL, f"logits rel {_rel(lg, rlog):.3e}"
     assert tok == rtok, f"gpu {tok} cpu {rtok} margin {top2[1] - top2[0]:.4g}"
-    for layer in range(cfg["n_layers"]):
-        kg, vg, kr, vr = _kv(eng, ref, cfg, layer, 0, n)
-        assert _rel(kg, kr) <= KV_TOL, f"K layer {layer} rel {_rel(kg, kr):.3e}"
-        assert _rel(vg, vr) <= KV_TOL, f"V layer {layer} rel {_rel(vg, vr):.3e}"
+    if _check_kv(eng, ref, cfg, n) == 0:
+        assert _rel(lg, rlog) <= LOGIT_TOL, f"logits rel {_rel(lg, rlog):.3e}"
     eng.close()
 
 
@@ -77,7 +105,7 @@ def test_prefill_then_decode(rf, orc, cfg):
     eng.close()
 
 
-@pytest.mark.parametrize("cfg", [TINY, TINY128])
+@pytest.mark.parametrize("cfg", [TINY, TINY128, G8, G1])
 def test_prefill_in_chunks(rf, orc, cfg):
     """A chunk prefilled at pos0 > 0 attends to the K/V of an earlier chunk
     (causal offset: row r sees pos0 + r + 1 positions)."""
@@ -89,11 +117,9 @@ def test_prefill_in_chunks(rf, orc, cfg):
     assert eng.prefill(head, 0) == ref.prefill(head, 0)
     tok = eng.prefill(chunk, len(head))
     rtok, rlog = ref.prefill(chunk, len(head), want_logits=True)
-    assert _rel(eng.logits(), rlog) <= LOGIT_TOL
     assert tok == rtok
-    for layer in range(cfg["n_layers"]):
-        kg, vg, kr, vr = _kv(eng, ref, cfg, layer, 0, len(head) + len(chunk))
-        assert _rel(kg, kr) <= KV_TOL and _rel(vg, vr) <= KV_TOL
+    if _check_kv(eng, ref, cfg, len(head) + len(chunk)) == 0:
+        assert _rel(eng.logits(), rlog) <= LOGIT_TOL
     eng.close()
 
 
