@@ -155,7 +155,8 @@ int fp4_mma_allones(rfp4_stream_t stream, float *out);
 int fp4_quantize_absmax(const float *w, uint32_t rows, uint32_t k, uint32_t *packed, float *scales);
 /* OCP MX quantization of rows x k values (f32, or bf16 if src_is_bf16) into
  * E2M1 codes (k/2 bytes per row) and E8M0 scales (k/32 per row).  Same bits
- * as the engine's weight quantizer.  No reference counterpart on the engine
+ * as the engine's weight quantizer; src 16-byte aligned (8 for bf16), codes
+ * 16-byte aligned.  No reference counterpart on the engine
  * path (the reference quantizes with f32 absmax/6 scales on the host,
  * llama_run/src/main.rs:334-376); needed for MXFP4 activations. */
 int mx4_quantize(rfp4_stream_t stream, uint64_t rows, uint64_t k, const void *src, int src_is_bf16,

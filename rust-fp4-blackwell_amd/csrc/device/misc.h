@@ -146,6 +146,37 @@ RFP4_DEV uint32_t quant_block32(const float *v, uint8_t *out16)
     return sbyte;
 }
 
+// quant_block32 spread over 8 consecutive lanes: lane part p = lane & 7 holds
+// values 4p .. 4p+3 of the block in v, and every lane of the group is active.
+// Same shared exponent (the maximum does not depend on the order) and the
+// same element arithmetic; part 0 writes the scale byte, even parts one
+// 32-bit word of the 16 code bytes each.
+RFP4_DEV void quant_block32_x8(float4 v, uint8_t *codes16, uint8_t *scale)
+{
+    const uint32_t p = threadIdx.x & 7u;
+    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+    amax = fmaxf(amax, dpp_mov<DPP_QUAD_1032>(amax));
+    amax = fmaxf(amax, dpp_mov<DPP_QUAD_2301>(amax));
+    amax = fmaxf(amax, dpp_mov<DPP_ROW_HALF_MIRROR>(amax)); // lane i <-> 7 - i: the other quad of the 8
+    int se = 0;
+    uint32_t sbyte = 0;
+    if (amax != 0.0f) {
+        se = floor_log2_pos(amax) - 2;
+        se = se < -127 ? -127 : (se > 127 ? 127 : se);
+        sbyte = (uint32_t)(se + 127);
+    }
+    const float f[4] = {v.x, v.y, v.z, v.w};
+    uint32_t h = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const float sv = amax != 0.0f ? ldexpf(f[i], -se) : f[i];
+        h |= e2m1_rne_code(sv) << (4 * i);
+    }
+    const uint32_t hn = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)h, DPP_QUAD_1032, 0xF, 0xF, false); // part p ^ 1
+    if ((p & 1u) == 0) *(uint32_t *)(codes16 + 2u * p) = h | (hn << 16);
+    if (p == 0) *scale = (uint8_t)sbyte;
+}
+
 // One thread per 32-block of the synthetic weight.
 RFP4_DEV void synth_weight_body(const SynthWeightArgs &a)
 {
@@ -183,17 +214,19 @@ RFP4_DEV void synth_kv_body(const SynthKvArgs &a)
 template <int SRC_BF16>
 RFP4_DEV void quant_mx_body(const QuantMxArgs &a)
 {
-    const uint64_t nb = a.k / 32, total = a.rows * nb;
-    for (uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total; t += (uint64_t)gridDim.x * blockDim.x) {
-        uint64_t r = t / nb, blk = t % nb;
-        float v[32];
-#pragma unroll
-        for (int i = 0; i < 32; i++) {
-            uint64_t idx = r * a.k + blk * 32 + (uint64_t)i;
-            v[i] = SRC_BF16 ? __uint_as_float((uint32_t)((const uint16_t *)a.src)[idx] << 16)
-                            : ((const float *)a.src)[idx];
+    // one float4 (or 4 bf16) per thread and step, 8 threads per 32-block:
+    // k % 32 == 0 makes every 8-lane group lie inside one block of one row
+    const uint64_t total4 = a.rows * a.k / 4u;
+    for (uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; t < total4; t += (uint64_t)gridDim.x * blockDim.x) {
+        float4 v;
+        if (SRC_BF16) {
+            const uint2 b = ((const uint2 *)a.src)[t];
+            v = make_float4(__uint_as_float(b.x << 16), __uint_as_float(b.x & 0xFFFF0000u), __uint_as_float(b.y << 16),
+                            __uint_as_float(b.y & 0xFFFF0000u));
+        } else {
+            v = ((const float4 *)a.src)[t];
         }
-        a.scales[t] = (uint8_t)quant_block32(v, a.packed + (r * a.k + blk * 32) / 2);
+        quant_block32_x8(v, a.packed + (t / 8u) * 16u, a.scales + t / 8u);
     }
 }
 

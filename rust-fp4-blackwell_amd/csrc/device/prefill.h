@@ -19,46 +19,50 @@ RFP4_DEV void embed_rows_body(const RowsArgs &a)
     for (uint32_t i = threadIdx.x; i < a.k; i += blockDim.x) a.y[(size_t)r * a.k + i] = half_bits_to_f32(row[i], a.bf16 != 0);
 }
 
-// grid (rows), dynamic LDS k floats: RMSNorm of row r with fp16 weights, in
-// the order of rmsnorm_body ((x * rms) * w, llama_run/src/main.rs:79-116),
-// then OCP MX quantisation per 32 values.
+// grid (rows): RMSNorm of row r with fp16 weights, in the order of
+// rmsnorm_body ((x * rms) * w, llama_run/src/main.rs:79-116), then OCP MX
+// quantisation per 32 values (8 threads per block, float4 loads).
 RFP4_DEV void rmsnorm_quant_rows_body(const RowsArgs &a)
 {
-    extern __shared__ float yrow[];
     __shared__ float red[16];
-    const uint32_t r = blockIdx.x;
-    const float *x = a.x + (size_t)r * a.k;
+    const uint32_t r = blockIdx.x, k4 = a.k / 4u;
+    const float4 *x = (const float4 *)(a.x + (size_t)r * a.k);
     float ss = 0.0f;
-    for (uint32_t i = threadIdx.x; i < a.k; i += blockDim.x) ss = __fadd_rn(ss, __fmul_rn(x[i], x[i]));
+    for (uint32_t i = threadIdx.x; i < k4; i += blockDim.x) {
+        const float4 v = x[i];
+        ss = __fadd_rn(ss, __fmul_rn(v.x, v.x));
+        ss = __fadd_rn(ss, __fmul_rn(v.y, v.y));
+        ss = __fadd_rn(ss, __fmul_rn(v.z, v.z));
+        ss = __fadd_rn(ss, __fmul_rn(v.w, v.w));
+    }
     const float total = block_sum(ss, red);
     const float rms = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(total, (float)a.k), a.eps)));
-    for (uint32_t i = threadIdx.x; i < a.k; i += blockDim.x)
-        yrow[i] = __fmul_rn(__fmul_rn(x[i], rms), f16_bits_to_f32(a.w[i]));
-    __syncthreads();
-    const uint32_t nb = a.k / 32u;
-    for (uint32_t b = threadIdx.x; b < nb; b += blockDim.x) {
-        float v[32];
-#pragma unroll
-        for (int i = 0; i < 32; i++) v[i] = yrow[b * 32u + (uint32_t)i];
-        a.scales[(size_t)r * nb + b] = (uint8_t)quant_block32(v, a.codes + ((size_t)r * a.k + b * 32u) / 2);
+    const uint2 *w = (const uint2 *)a.w;
+    uint8_t *codes = a.codes + (size_t)r * a.k / 2u, *scales = a.scales + (size_t)r * (a.k / 32u);
+    for (uint32_t i = threadIdx.x; i < k4; i += blockDim.x) { // k % 32 == 0: whole 8-thread groups
+        const float4 v = x[i];
+        const uint2 wb = w[i];
+        const float4 y = make_float4(__fmul_rn(__fmul_rn(v.x, rms), f16_bits_to_f32((uint16_t)(wb.x & 0xFFFFu))),
+                                     __fmul_rn(__fmul_rn(v.y, rms), f16_bits_to_f32((uint16_t)(wb.x >> 16))),
+                                     __fmul_rn(__fmul_rn(v.z, rms), f16_bits_to_f32((uint16_t)(wb.y & 0xFFFFu))),
+                                     __fmul_rn(__fmul_rn(v.w, rms), f16_bits_to_f32((uint16_t)(wb.y >> 16))));
+        quant_block32_x8(y, codes + (i / 8u) * 16u, scales + i / 8u);
     }
 }
 
 // grid (rows): s = silu(gate) * up (llama_run/src/main.rs:244-252) of row r
 // (gate = columns [0, k), up = [k, 2k) of the stacked gate|up output), then
-// OCP MX quantisation per 32 values.
+// OCP MX quantisation per 32 values (8 threads per block, float4 loads).
 RFP4_DEV void swiglu_quant_rows_body(const RowsArgs &a)
 {
-    const uint32_t r = blockIdx.x, nb = a.k / 32u;
-    const float *g = a.x + (size_t)r * 2u * a.k, *u = g + a.k;
-    for (uint32_t b = threadIdx.x; b < nb; b += blockDim.x) {
-        float v[32];
-#pragma unroll
-        for (int i = 0; i < 32; i++) {
-            const uint32_t j = b * 32u + (uint32_t)i;
-            v[i] = __fmul_rn(silu_ref(g[j]), u[j]);
-        }
-        a.scales[(size_t)r * nb + b] = (uint8_t)quant_block32(v, a.codes + ((size_t)r * a.k + b * 32u) / 2);
+    const uint32_t r = blockIdx.x, k4 = a.k / 4u;
+    const float4 *g = (const float4 *)(a.x + (size_t)r * 2u * a.k), *u = g + k4;
+    uint8_t *codes = a.codes + (size_t)r * a.k / 2u, *scales = a.scales + (size_t)r * (a.k / 32u);
+    for (uint32_t i = threadIdx.x; i < k4; i += blockDim.x) { // k % 32 == 0: whole 8-thread groups
+        const float4 gv = g[i], uv = u[i];
+        const float4 y = make_float4(__fmul_rn(silu_ref(gv.x), uv.x), __fmul_rn(silu_ref(gv.y), uv.y),
+                                     __fmul_rn(silu_ref(gv.z), uv.z), __fmul_rn(silu_ref(gv.w), uv.w));
+        quant_block32_x8(y, codes + (i / 8u) * 16u, scales + i / 8u);
     }
 }
 

@@ -197,7 +197,7 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
         RowsArgs na{};
         na.x = e->pf_x; na.w = e->norm_attn + (size_t)l * c.dim; na.codes = e->pf_codes; na.scales = e->pf_scales;
         na.rows = n; na.k = c.dim; na.eps = c.eps;
-        if ((rc = launch("rfp4_rmsnorm_quant_rows", dim3(n), dim3(256), s, &na, c.dim * 4u))) return rc;
+        if ((rc = launch("rfp4_rmsnorm_quant_rows", dim3(n), dim3(256), s, &na))) return rc;
         if ((rc = fp4_gemm(s, n, nqkv, c.dim, e->pf_codes, e->pf_scales, w.qkv_c, w.qkv_s, e->pf_c))) return rc;
         RopeRowsArgs ra{};
         ra.qkv = e->pf_c; ra.cosv = e->cos_tab; ra.sinv = e->sin_tab; ra.kc = kc; ra.vc = vc;
@@ -227,7 +227,7 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
         if ((rc = fp4_gemm(s, n, c.dim, qd, e->pf_codes, e->pf_scales, w.o_c, w.o_s, e->pf_c))) return rc;
         if ((rc = residual(s, n * c.dim, e->pf_c, e->pf_x))) return rc;
         na.w = e->norm_ffn + (size_t)l * c.dim;
-        if ((rc = launch("rfp4_rmsnorm_quant_rows", dim3(n), dim3(256), s, &na, c.dim * 4u))) return rc;
+        if ((rc = launch("rfp4_rmsnorm_quant_rows", dim3(n), dim3(256), s, &na))) return rc;
         if ((rc = fp4_gemm(s, n, 2 * c.ffn, c.dim, e->pf_codes, e->pf_scales, w.gu_c, w.gu_s, e->pf_c))) return rc;
         RowsArgs sa{};
         sa.x = e->pf_c; sa.codes = e->pf_codes; sa.scales = e->pf_scales; sa.rows = n; sa.k = c.ffn;

@@ -811,8 +811,10 @@ int mx4_quantize(rfp4_stream_t stream, uint64_t rows, uint64_t k, const void *sr
     if (!src || !codes || !scales) return set_error(RFP4_E_INVALID, "mx4_quantize: null pointer");
     if (k == 0 || k % 32) return set_error(RFP4_E_SHAPE, "mx4_quantize: k=%llu not a multiple of 32", (unsigned long long)k);
     if (((uintptr_t)codes & 15u) != 0) return set_error(RFP4_E_ALIGN, "mx4_quantize: codes must be 16-byte aligned");
+    if (((uintptr_t)src & (src_is_bf16 ? 7u : 15u)) != 0)
+        return set_error(RFP4_E_ALIGN, "mx4_quantize: src must be %u-byte aligned", src_is_bf16 ? 8u : 16u);
     QuantMxArgs a{src, codes, scales, rows, k};
-    uint64_t blocks = (rows * (k / 32) + 255) / 256;
+    uint64_t blocks = (rows * (k / 4) + 255) / 256; // one thread per 4 values
     if (blocks > 65536) blocks = 65536;
     return launch(src_is_bf16 ? "rfp4_quant_mx_bf16" : "rfp4_quant_mx_f32", dim3((unsigned)blocks), dim3(256),
                   (hipStream_t)stream, &a);

@@ -334,14 +334,21 @@ def test_synth_f16_bit_exact(rf, orc, stream):
     np.testing.assert_array_equal(d.to_host(n, np.uint16, stream), ref)
 
 
+@pytest.mark.parametrize("rows,k", [(64, 512), (37, 96), (7, 32)])
 @pytest.mark.parametrize("bf16", [False, True])
-def test_quantize_bit_exact(rf, orc, stream, bf16):
-    rng = np.random.default_rng(5)
-    rows, k = 64, 512
+def test_quantize_bit_exact(rf, orc, stream, bf16, rows, k):
+    """Eight threads share each 32-block on the device (DPP maximum); codes
+    and scale bytes identical to the oracle's quantizer: zero and -0 blocks,
+    subnormals, exact E2M1 rounding ties, a NaN element, one-block rows."""
+    rng = np.random.default_rng(5 + rows)
     w = (rng.standard_normal((rows, k)) * np.exp(rng.uniform(-20, 20, (rows, 1)))).astype(np.float32)
     w[3, :32] = 0.0                      # all-zero block
     w[4, :32] = np.float32(-0.0)
     w[5, 5] = 1e-41                      # subnormal
+    w[6, :32] = np.tile(np.float32([6, 0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0]), 4)  # amax 6: scale 1, ties
+    w[6, 8:16] *= -1
+    if rows > 20:
+        w[20, 7] = np.nan                 # ignored by the block maximum, saturates to the largest code
     if bf16:
         src = (w.view(np.uint32) >> 16).astype(np.uint16)
         w = (src.astype(np.uint32) << 16).view(np.float32).reshape(rows, k)
