@@ -190,6 +190,9 @@ int rfp4_debug_attn_merge(int mode);
  * matrix-core prefill kernel, 1 = the decode kernel, one grid row per prompt
  * row.  No reference counterpart. */
 int rfp4_debug_prefill_attn(int mode);
+/* Test hook: waves per workgroup of the matrix-core prefill attention on
+ * this thread (0 = automatic, 4 or 8).  No reference counterpart. */
+int rfp4_debug_prefill_waves(int waves);
 /* The tile and K split fp4_gemm would use for this shape (honours the test
  * hook).  No reference counterpart. */
 int rfp4_gemm_plan(uint32_t m, uint32_t n, uint32_t k, int *tile_m, int *tile_n, int *kz);

@@ -5,9 +5,10 @@
 // (llama_run/src/main.rs:148-242 applied row by row), with the prompt's own
 // rows already appended to the fp16 caches.
 //
-// Grid (query tiles, n_kv_heads).  A workgroup takes BQ prompt rows and every
-// query head of one KV head (GT heads, G <= GT real), i.e. NT = (BQ/16) * GT
-// tiles of 16 (row, head) pairs, MT per wave, and walks the keys 0 .. last
+// Grid (query tiles, n_kv_heads).  A workgroup of NW waves takes BQ =
+// max(16, 16 NW / GT) prompt rows and every query head of one KV head (GT
+// heads, G <= GT real), i.e. NT = (BQ/16) * GT tiles of 16 (row, head) pairs,
+// MT = NT / NW per wave, and walks the keys 0 .. last
 // row's position in blocks of 32: K rows staged in LDS as loaded, V rows
 // staged transposed (dimension-major), both as v_mfma_f32_16x16x32_f16
 // operands read with one 16-byte LDS read per lane:
@@ -53,23 +54,25 @@ RFP4_DEV float pf_row16_max(float v)
     return v;
 }
 
-template <int HD, int GT>
+template <int HD, int GT, int NW = 4>
 RFP4_DEV void attn_prefill_body(const AttnPrefillArgs &a)
 {
     const uint32_t pos0 = a.pos0, nrows = a.rows;
-    constexpr int BQ = GT >= 4 ? 16 : 64 / GT;       // prompt rows per workgroup
+    constexpr int BQ = attn_prefill_rows(GT, NW);    // prompt rows per workgroup
     constexpr int NT = (BQ / 16) * GT;               // 16-row tiles per workgroup
-    constexpr int MT = NT / 4;                       // tiles per wave
+    constexpr int MT = NT / NW;                      // tiles per wave
     constexpr int KS = HD / 32;                      // K steps of S = Q K^T
     constexpr int NN = HD / 16;                      // 16-wide column tiles of O
     constexpr int KROW = HD + PF_KPAD, TROW = PF_BK + PF_TPAD;
     constexpr int LPK = HD / 8;                      // 16-byte pieces per K/V row
-    constexpr int LD = PF_BK * LPK / 256;            // K (and V) pieces per thread per block
-    static_assert(NT % 4 == 0 && MT >= 1, "tiles per wave");
-    static_assert(LD >= 1 && PF_BK * LPK % 256 == 0, "block load split");
+    constexpr int T = 64 * NW;                       // threads
+    constexpr int LD = (PF_BK * LPK + T - 1) / T;    // K (and V) pieces per thread per block
+    constexpr bool LFULL = PF_BK * LPK % T == 0;     // every thread loads LD pieces
+    static_assert(NT % NW == 0 && MT >= 1, "tiles per wave");
+    static_assert(LFULL || LD == 1, "block load split");
     __shared__ __align__(16) _Float16 ks[PF_BK][KROW];
     __shared__ __align__(16) _Float16 vt[HD][TROW];
-    __shared__ __align__(16) _Float16 ps[4][MT][2][16][TROW]; // P hi, lo
+    __shared__ __align__(16) _Float16 ps[NW][MT][2][16][TROW]; // P hi, lo
 
     const uint32_t kvh = blockIdx.y, r0 = blockIdx.x * BQ;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -122,7 +125,8 @@ RFP4_DEV void attn_prefill_body(const AttnPrefillArgs &a)
 #define RFP4_PF_LOAD(B)                                                                                   \
     do {                                                                                                  \
         _Pragma("unroll") for (int j = 0; j < LD; j++) {                                                  \
-            const uint32_t p = (uint32_t)tid + 256u * (uint32_t)j;                                        \
+            const uint32_t p = (uint32_t)tid + (uint32_t)T * (uint32_t)j;                                 \
+            if (!LFULL && p >= (uint32_t)(PF_BK * LPK)) break;                                            \
             const uint32_t kk = min((B) * PF_BK + p / LPK, nk - 1u), kd = 8u * (p % LPK);                 \
             kr[j] = load_nt16(kc + (size_t)kk * a.ts + kd);                                               \
             const uint32_t vk = min((B) * PF_BK + p % PF_BK, nk - 1u), vd = 8u * (p / PF_BK);              \
@@ -135,7 +139,8 @@ RFP4_DEV void attn_prefill_body(const AttnPrefillArgs &a)
         __syncthreads(); // the previous block's LDS reads are done
 #pragma unroll
         for (int j = 0; j < LD; j++) {
-            const uint32_t p = (uint32_t)tid + 256u * (uint32_t)j;
+            const uint32_t p = (uint32_t)tid + (uint32_t)T * (uint32_t)j;
+            if (!LFULL && p >= (uint32_t)(PF_BK * LPK)) break;
             *(uint4 *)&ks[p / LPK][8u * (p % LPK)] = kr[j];
             const uint32_t vk = p % PF_BK, vd = 8u * (p / PF_BK);
             const uint32_t w[4] = {vr[j].x, vr[j].y, vr[j].z, vr[j].w};

@@ -16,6 +16,7 @@
 #include "device/attn_prefill.h"
 
 #define K256 extern "C" __global__ __launch_bounds__(256)
+#define K512 extern "C" __global__ __launch_bounds__(512)
 #define K1024 extern "C" __global__ __launch_bounds__(1024)
 
 // ---- GEMV: rfp4_gemv_<scale>_<epilogue>_r<R>_s<NS>
@@ -133,11 +134,16 @@ ATTN_KERNELS(64, f32, float)
 ATTN_KERNELS(64, f16, uint16_t)
 ATTN_KERNELS(128, f32, float)
 ATTN_KERNELS(128, f16, uint16_t)
+// rfp4_attn_prefill_hd<HD>_g<group>_w<waves per workgroup>
 #define ATTN_PREFILL_KERNELS(HD) \
-    K256 void rfp4_attn_prefill_hd##HD##_g1(AttnPrefillArgs a) { attn_prefill_body<HD, 1>(a); } \
-    K256 void rfp4_attn_prefill_hd##HD##_g2(AttnPrefillArgs a) { attn_prefill_body<HD, 2>(a); } \
-    K256 void rfp4_attn_prefill_hd##HD##_g4(AttnPrefillArgs a) { attn_prefill_body<HD, 4>(a); } \
-    K256 void rfp4_attn_prefill_hd##HD##_g8(AttnPrefillArgs a) { attn_prefill_body<HD, 8>(a); }
+    K256 void rfp4_attn_prefill_hd##HD##_g1_w4(AttnPrefillArgs a) { attn_prefill_body<HD, 1, 4>(a); } \
+    K256 void rfp4_attn_prefill_hd##HD##_g2_w4(AttnPrefillArgs a) { attn_prefill_body<HD, 2, 4>(a); } \
+    K256 void rfp4_attn_prefill_hd##HD##_g4_w4(AttnPrefillArgs a) { attn_prefill_body<HD, 4, 4>(a); } \
+    K256 void rfp4_attn_prefill_hd##HD##_g8_w4(AttnPrefillArgs a) { attn_prefill_body<HD, 8, 4>(a); } \
+    K512 void rfp4_attn_prefill_hd##HD##_g1_w8(AttnPrefillArgs a) { attn_prefill_body<HD, 1, 8>(a); } \
+    K512 void rfp4_attn_prefill_hd##HD##_g2_w8(AttnPrefillArgs a) { attn_prefill_body<HD, 2, 8>(a); } \
+    K512 void rfp4_attn_prefill_hd##HD##_g4_w8(AttnPrefillArgs a) { attn_prefill_body<HD, 4, 8>(a); } \
+    K512 void rfp4_attn_prefill_hd##HD##_g8_w8(AttnPrefillArgs a) { attn_prefill_body<HD, 8, 8>(a); }
 ATTN_PREFILL_KERNELS(64)
 ATTN_PREFILL_KERNELS(128)
 K256 void rfp4_attn_merge_hd64(AttnArgs a) { attn_merge_body<64>(a); }

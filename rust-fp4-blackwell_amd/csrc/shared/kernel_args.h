@@ -234,4 +234,11 @@ constexpr int attn_steps_for(int head_dim, int elem_bytes, int group)
 {
     return group == 8 ? 4 : (head_dim == 128 && elem_bytes == 2) ? 9 : 8;
 }
+// Prompt rows per workgroup of the prefill attention with `waves` waves and
+// a query-head group padded to `group`: one 16-row tile per wave when the
+// group allows, at least 16 rows.
+constexpr int attn_prefill_rows(int group, int waves)
+{
+    return 16 * waves / group > 16 ? 16 * waves / group : 16;
+}
 #endif
