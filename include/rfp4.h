@@ -193,6 +193,10 @@ int rfp4_debug_prefill_attn(int mode);
 /* Test hook: waves per workgroup of the matrix-core prefill attention on
  * this thread (0 = automatic, 4 or 8).  No reference counterpart. */
 int rfp4_debug_prefill_waves(int waves);
+/* Test hook: query-tile pairing of the matrix-core prefill attention on this
+ * thread (0 = automatic, 1 = one tile per workgroup, 2 = tiles t and
+ * ntiles-1-t per workgroup).  No reference counterpart. */
+int rfp4_debug_prefill_pairing(int mode);
 /* The tile and K split fp4_gemm would use for this shape (honours the test
  * hook).  No reference counterpart. */
 int rfp4_gemm_plan(uint32_t m, uint32_t n, uint32_t k, int *tile_m, int *tile_n, int *kz);

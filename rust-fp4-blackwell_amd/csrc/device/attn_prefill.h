@@ -54,8 +54,9 @@ RFP4_DEV float pf_row16_max(float v)
     return v;
 }
 
-template <int HD, int GT, int NW = 4>
-RFP4_DEV void attn_prefill_body(const AttnPrefillArgs &a)
+// One query tile: prompt rows r0 .. r0 + BQ of KV head blockIdx.y.
+template <int HD, int GT, int NW>
+RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
 {
     const uint32_t pos0 = a.pos0, nrows = a.rows;
     constexpr int BQ = attn_prefill_rows(GT, NW);    // prompt rows per workgroup
@@ -74,7 +75,7 @@ RFP4_DEV void attn_prefill_body(const AttnPrefillArgs &a)
     __shared__ __align__(16) _Float16 vt[HD][TROW];
     __shared__ __align__(16) _Float16 ps[NW][MT][2][16][TROW]; // P hi, lo
 
-    const uint32_t kvh = blockIdx.y, r0 = blockIdx.x * BQ;
+    const uint32_t kvh = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t l16 = (uint32_t)lane & 15u, q4 = (uint32_t)lane >> 4;
     const uint32_t G = a.n_heads / a.n_kv_heads;
@@ -233,4 +234,18 @@ RFP4_DEV void attn_prefill_body(const AttnPrefillArgs &a)
             for (int n = 0; n < NN; n++) op[16 * n] = __fdiv_rn(o[mt][n][r], lrun[mt][r]);
         }
     }
+}
+
+// Workgroup x of KV head blockIdx.y: query tile x, or, paired, tiles
+// ntiles - 1 - x (the longer causal range, first) and x, so that every
+// workgroup walks ntiles + 1 key ranges' worth of blocks.
+template <int HD, int GT, int NW = 4>
+RFP4_DEV void attn_prefill_body(const AttnPrefillArgs &a)
+{
+    constexpr uint32_t BQ = (uint32_t)attn_prefill_rows(GT, NW);
+    const uint32_t ntiles = (a.rows + BQ - 1u) / BQ, x = blockIdx.x;
+    const uint32_t t0 = a.paired ? ntiles - 1u - x : x;
+    const uint32_t npass = a.paired && x < t0 ? 2u : 1u;
+#pragma nounroll
+    for (uint32_t pass = 0; pass < npass; pass++) attn_prefill_tile<HD, GT, NW>(a, (pass == 0 ? t0 : x) * BQ);
 }

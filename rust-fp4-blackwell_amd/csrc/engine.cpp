@@ -220,7 +220,7 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
             if ((rc = attn_launch(aa, 1, s, pos0 + n, n))) return rc;
         } else {
             AttnPrefillArgs pa{e->pf_c, kc, vc, e->pf_a, hd, (uint64_t)e->max_seq_alloc * hd, nqkv, qd,
-                               c.n_heads, c.n_kv_heads, pos0, n};
+                               c.n_heads, c.n_kv_heads, pos0, n, 0u}; // pairing: chosen by the launcher
             if ((rc = attn_prefill_launch(pa, hd, s))) return rc;
         }
         if ((rc = mx4_quantize(s, n, qd, e->pf_a, 0, e->pf_codes, e->pf_scales))) return rc;

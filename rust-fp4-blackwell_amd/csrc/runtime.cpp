@@ -287,6 +287,7 @@ int attn_merge_mode() { return t_attn_merge; }
 
 static thread_local int t_prefill_attn = 0; // 0 matrix-core prefill kernel, 1 one decode-kernel row per prompt row
 static thread_local int t_prefill_waves = 0; // prefill attention waves per workgroup (0 = automatic)
+static thread_local int t_prefill_pairing = 0; // 0 automatic, 1 one query tile per workgroup, 2 paired tiles
 int prefill_attn_mode() { return t_prefill_attn; }
 
 bool attn_inmerge_mode(int mode, uint32_t splits)
@@ -462,6 +463,14 @@ extern "C" int rfp4_debug_prefill_waves(int waves)
     return RFP4_OK;
 }
 
+extern "C" int rfp4_debug_prefill_pairing(int mode)
+{
+    using namespace rfp4;
+    if (mode < 0 || mode > 2) return set_error(RFP4_E_INVALID, "pairing mode must be 0 (auto), 1 (off) or 2 (on)");
+    t_prefill_pairing = mode;
+    return RFP4_OK;
+}
+
 extern "C" int rfp4_debug_prefill_attn(int mode)
 {
     using namespace rfp4;
@@ -530,10 +539,18 @@ int attn_prefill_launch(const AttnPrefillArgs &a, uint32_t head_dim, hipStream_t
     }
     if (t_prefill_waves) waves = (uint32_t)t_prefill_waves;
     const uint32_t bq = (uint32_t)attn_prefill_rows((int)g, (int)waves); // prompt rows per workgroup
+    const uint32_t ntiles = (a.rows + bq - 1) / bq;
+    // Causal tiles differ in length (tile t walks t + 1 key ranges' worth of
+    // blocks); pairing tile t with ntiles - 1 - t in one workgroup evens them
+    // out wherever the halved grid still gives every CU a workgroup.
+    bool paired = ntiles >= 2 && g_rt && (uint64_t)((ntiles + 1) / 2) * a.n_kv_heads >= (uint64_t)g_rt->num_cus;
+    if (t_prefill_pairing) paired = t_prefill_pairing == 2;
     char name[48];
     snprintf(name, sizeof name, "rfp4_attn_prefill_hd%u_g%u_w%u", head_dim, g, waves);
     AttnPrefillArgs args = a;
-    return launch(name, dim3((a.rows + bq - 1) / bq, a.n_kv_heads), dim3(64u * waves), s, &args);
+    args.paired = paired ? 1u : 0u;
+    const uint32_t gx = paired ? (ntiles + 1) / 2 : ntiles;
+    return launch(name, dim3(gx, a.n_kv_heads), dim3(64u * waves), s, &args);
 }
 
 uint32_t attn_group_pad(uint32_t group) { return group <= 1u ? 1u : group <= 2u ? 2u : group <= 4u ? 4u : 8u; }
@@ -758,7 +775,7 @@ int attn_prefill_f16(rfp4_stream_t stream, uint32_t n_heads, uint32_t n_kv_heads
         return set_error(RFP4_E_SHAPE, "attn_prefill_f16: q row stride %u < %u", q_row_stride, n_heads * head_dim);
     if (rows && out_row_stride < n_heads * head_dim)
         return set_error(RFP4_E_SHAPE, "attn_prefill_f16: out row stride %u < %u", out_row_stride, n_heads * head_dim);
-    AttnPrefillArgs a{q, kc, vc, out, token_stride, head_stride, q_row_stride, out_row_stride, n_heads, n_kv_heads, pos0, rows};
+    AttnPrefillArgs a{q, kc, vc, out, token_stride, head_stride, q_row_stride, out_row_stride, n_heads, n_kv_heads, pos0, rows, 0u};
     return attn_prefill_launch(a, head_dim, (hipStream_t)stream);
 }
 

@@ -105,6 +105,7 @@ typedef struct AttnPrefillArgs {
     float *out;              // row r: out + r*out_rs, [n_heads][head_dim]
     uint64_t ts, hs;
     uint32_t q_rs, out_rs, n_heads, n_kv_heads, pos0, rows;
+    uint32_t paired;         // nonzero: workgroup x takes query tiles ntiles-1-x and x (grid ceil(ntiles/2))
 } AttnPrefillArgs;
 
 // Batched prefill row kernels (device/prefill.h).

@@ -240,13 +240,14 @@ def test_attn_decode_f16_parity(rf, orc, stream, nh, nkv, hd, seq):
                                                   (16, 8, 128, 300, 33), (32, 8, 128, 4000, 16), (6, 2, 64, 5, 9),
                                                   (32, 8, 128, 7, 1), (4, 2, 64, 0, 5), (4, 2, 64, 5, 40),
                                                   (8, 2, 128, 0, 3), (2, 2, 128, 0, 130)])
-@pytest.mark.parametrize("waves", [4, 8])
-def test_attn_prefill_f16(rf, orc, stream, nh, nkv, hd, pos0, rows, waves):
+@pytest.mark.parametrize("waves,pairing", [(4, 1), (8, 1), (4, 2), (8, 2)])
+def test_attn_prefill_f16(rf, orc, stream, nh, nkv, hd, pos0, rows, waves, pairing):
     """Causal prefill attention on the matrix cores: row r equals the
     oracle's attn_decode at seq = pos0 + r + 1 over the same fp16 caches,
     within the decode kernel's bar (q and p enter the fp16 MFMAs as hi + lo
     fp16 terms, about 2^-22 relative); query-head groups 1, 2, 3 (padded to
-    4), 4 and 8, both head dims, 4- and 8-wave workgroups."""
+    4), 4 and 8, both head dims, 4- and 8-wave workgroups, one or two (paired causal)
+    query tiles per workgroup."""
     rng = np.random.default_rng(pos0 * 31 + rows + hd)
     cap = pos0 + rows + 3
     q = rng.standard_normal((rows, nh * hd)).astype(np.float32)
@@ -255,11 +256,13 @@ def test_attn_prefill_f16(rf, orc, stream, nh, nkv, hd, pos0, rows, waves):
     oref = np.stack([orc.attn_decode(nh, nkv, hd, pos0 + r + 1, q[r], kc, vc, hd, cap * hd) for r in range(rows)])
     dout = rf.DeviceBuffer.zeroed(rows * nh * hd, np.float32, stream)
     rf.check(rf.load().rfp4_debug_prefill_waves(waves))
+    rf.check(rf.load().rfp4_debug_prefill_pairing(pairing))
     try:
         rf.attn_prefill_f16(stream, nh, nkv, hd, pos0, rows, _dev(rf, q.reshape(-1), stream), nh * hd,
                             _dev(rf, kc, stream), _dev(rf, vc, stream), hd, cap * hd, dout, nh * hd)
     finally:
         rf.check(rf.load().rfp4_debug_prefill_waves(0))
+        rf.check(rf.load().rfp4_debug_prefill_pairing(0))
     got = dout.to_host(rows * nh * hd, np.float32, stream).reshape(rows, nh * hd)
     _assert_attn_close(got, oref)
 
