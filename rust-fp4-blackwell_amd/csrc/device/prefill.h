@@ -21,7 +21,10 @@ RFP4_DEV void embed_rows_body(const RowsArgs &a)
 
 // grid (rows): RMSNorm of row r with fp16 weights, in the order of
 // rmsnorm_body ((x * rms) * w, llama_run/src/main.rs:79-116), then OCP MX
-// quantisation per 32 values (8 threads per block, float4 loads).
+// quantisation per 32 values (8 threads per block, float4 loads).  With
+// `add`, the layer's residual add comes first: x = x + add
+// (llama_run/src/main.rs:254-261) is stored back and normalised; each
+// thread re-reads only the elements it stored.
 RFP4_DEV void rmsnorm_quant_rows_body(const RowsArgs &a)
 {
     __shared__ float red[16];
@@ -29,7 +32,12 @@ RFP4_DEV void rmsnorm_quant_rows_body(const RowsArgs &a)
     const float4 *x = (const float4 *)(a.x + (size_t)r * a.k);
     float ss = 0.0f;
     for (uint32_t i = threadIdx.x; i < k4; i += blockDim.x) {
-        const float4 v = x[i];
+        float4 v = x[i];
+        if (a.add) {
+            const float4 d = ((const float4 *)(a.add + (size_t)r * a.k))[i];
+            v = make_float4(__fadd_rn(v.x, d.x), __fadd_rn(v.y, d.y), __fadd_rn(v.z, d.z), __fadd_rn(v.w, d.w));
+            ((float4 *)(a.x_out + (size_t)r * a.k))[i] = v;
+        }
         ss = __fadd_rn(ss, __fmul_rn(v.x, v.x));
         ss = __fadd_rn(ss, __fmul_rn(v.y, v.y));
         ss = __fadd_rn(ss, __fmul_rn(v.z, v.z));

@@ -197,6 +197,9 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
         RowsArgs na{};
         na.x = e->pf_x; na.w = e->norm_attn + (size_t)l * c.dim; na.codes = e->pf_codes; na.scales = e->pf_scales;
         na.rows = n; na.k = c.dim; na.eps = c.eps;
+        // layer l > 0: the previous layer's down projection (pf_c) is added into the residual stream here
+        na.add = l > 0 ? e->pf_c : nullptr;
+        na.x_out = e->pf_x;
         if ((rc = launch("rfp4_rmsnorm_quant_rows", dim3(n), dim3(256), s, &na))) return rc;
         if ((rc = fp4_gemm(s, n, nqkv, c.dim, e->pf_codes, e->pf_scales, w.qkv_c, w.qkv_s, e->pf_c))) return rc;
         RopeRowsArgs ra{};
@@ -225,15 +228,16 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
         }
         if ((rc = mx4_quantize(s, n, qd, e->pf_a, 0, e->pf_codes, e->pf_scales))) return rc;
         if ((rc = fp4_gemm(s, n, c.dim, qd, e->pf_codes, e->pf_scales, w.o_c, w.o_s, e->pf_c))) return rc;
-        if ((rc = residual(s, n * c.dim, e->pf_c, e->pf_x))) return rc;
         na.w = e->norm_ffn + (size_t)l * c.dim;
+        na.add = e->pf_c; // x += O projection, then the FFN norm
         if ((rc = launch("rfp4_rmsnorm_quant_rows", dim3(n), dim3(256), s, &na))) return rc;
         if ((rc = fp4_gemm(s, n, 2 * c.ffn, c.dim, e->pf_codes, e->pf_scales, w.gu_c, w.gu_s, e->pf_c))) return rc;
         RowsArgs sa{};
         sa.x = e->pf_c; sa.codes = e->pf_codes; sa.scales = e->pf_scales; sa.rows = n; sa.k = c.ffn;
         if ((rc = launch("rfp4_swiglu_quant_rows", dim3(n), dim3(256), s, &sa))) return rc;
         if ((rc = fp4_gemm(s, n, c.dim, c.ffn, e->pf_codes, e->pf_scales, w.d_c, w.d_s, e->pf_c))) return rc;
-        if ((rc = residual(s, n * c.dim, e->pf_c, e->pf_x))) return rc;
+        // x += down projection: by the next layer's first norm, after the last layer here
+        if (l + 1 == c.n_layers && (rc = residual(s, n * c.dim, e->pf_c, e->pf_x))) return rc;
     }
     // last row: the decode step's final norm + LM head, then argmax
     rc = hip_check(hipMemcpyAsync(e->x, e->pf_x + (size_t)(n - 1) * c.dim, c.dim * sizeof(float),

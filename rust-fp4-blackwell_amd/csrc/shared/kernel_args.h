@@ -119,6 +119,8 @@ typedef struct RowsArgs {
     uint32_t rows, k, vocab;
     float eps;
     uint32_t bf16;           // embed holds bf16 (1) or fp16 (0) bit patterns
+    const float *add;        // rmsnorm: rows added into x first (the layer's residual add), or null
+    float *x_out;            // rmsnorm with add: where x + add is stored (x itself)
 } RowsArgs;
 
 typedef struct RopeRowsArgs {
