@@ -283,7 +283,8 @@ def main():
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path "
-              "(the decode step would shard tensor-parallel; see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "(the decode step would shard tensor-parallel: q|k|v and gate|up by output rows, o and down by "
+              "input columns with one small all-reduce each, attention by KV head). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import rfp4 as rf
