@@ -43,7 +43,9 @@ uint32_t gemv_blocks(uint32_t n_logical, uint32_t k, int epi);
 int attn_launch(const AttnArgs &args, int kv_f16, hipStream_t s, uint32_t max_seq_for_grid, uint32_t rows);
 uint32_t attn_group_pad(uint32_t group);
 // Causal prefill attention (device/attn_prefill.h), fp16 caches.
-int attn_prefill_launch(const AttnPrefillArgs &a, uint32_t head_dim, hipStream_t s); // compiled query-head group (1, 2, 4, 8) serving `group` heads
+int attn_prefill_launch(const AttnPrefillArgs &a, uint32_t head_dim, hipStream_t s);
+// tokens per register sub-chunk of the decode attention with a compiled
+// query-head group (1, 2, 4, 8) serving `group` heads
 uint32_t attn_sub_chunk(uint32_t head_dim, uint32_t elem_bytes, uint32_t group);
 // Whether one-row attention with `max_splits` splits merges inside the split
 // kernel (arrival counters) instead of in a second launch.
