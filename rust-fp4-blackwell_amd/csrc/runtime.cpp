@@ -899,6 +899,7 @@ uint32_t ceil_div(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); 
 // Tile: the largest one that does not waste more than a quarter of its rows
 // on m and still yields a tile per CU; else the smallest such tile, with the
 // K split raised until every CU has a workgroup (bounded by the workspace).
+// Two measured exceptions below: 256x256 at 7/8 fill, and long K split in two.
 GemmPlan gemm_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t num_cus)
 {
     const uint32_t nsuper = k / 256u;
@@ -912,6 +913,15 @@ GemmPlan gemm_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t num_cus)
         return p;
     }
     int pick = t_gemm_tile;
+    if (pick < 0) {
+        // one round of 256x256 tiles over at least 7/8 of the CUs beats two
+        // rounds of 256x128 (one workgroup per CU either way): 8B gate|up at
+        // M = 512 (224 tiles) 50 vs 66 us
+        const GemmTile &t = kGemmTiles[0];
+        const uint64_t nt = (uint64_t)ceil_div(m, t.bm) * ceil_div(n, t.bn);
+        if ((uint64_t)ceil_div(m, t.bm) * t.bm * 4u <= (uint64_t)m * 5u && nt * 8u >= 7ull * num_cus && nt < num_cus)
+            return {0, 1u};
+    }
     for (int i = 0; pick < 0 && i < kGemmNumTiles; i++) {
         const GemmTile &t = kGemmTiles[i];
         if (t.bm > 32u && (uint64_t)ceil_div(m, t.bm) * t.bm * 4u > (uint64_t)m * 5u) continue; // > 25% padding
@@ -919,7 +929,13 @@ GemmPlan gemm_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t num_cus)
     }
     const uint64_t tiles = (uint64_t)ceil_div(m, kGemmTiles[pick].bm) * ceil_div(n, kGemmTiles[pick].bn);
     if (t_gemm_kz > 0) return {pick, std::min<uint32_t>((uint32_t)t_gemm_kz, nsuper)};
-    if (tiles >= num_cus) return {pick, 1u};
+    if (tiles >= num_cus) {
+        // long K at about one workgroup per CU: two K splits let two
+        // workgroups per CU overlap their serial chains of K steps (8B down
+        // at M = 512: 64x128, 56 steps, 51 -> 37 us), if the workspace holds them
+        if (nsuper >= 32u && tiles < 2ull * num_cus && 2ull * m * n <= kGemmPartFloats) return {pick, 2u};
+        return {pick, 1u};
+    }
     // steps per split: as few as reach one workgroup per CU; kz = ceil(nsuper / per) leaves no split empty
     uint32_t per = std::max<uint32_t>(1u, nsuper / ceil_div(num_cus, tiles));
     uint32_t kz = ceil_div(nsuper, per);

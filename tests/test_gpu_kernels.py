@@ -267,6 +267,32 @@ def test_attn_prefill_f16(rf, orc, stream, nh, nkv, hd, pos0, rows, waves, pairi
     _assert_attn_close(got, oref)
 
 
+@pytest.mark.parametrize("nh,nkv,hd,pos0,rows", [(8, 2, 128, 0, 200), (32, 4, 64, 9, 151), (6, 6, 128, 3, 97)])
+def test_attn_prefill_f16_grouping_invariant(rf, stream, nh, nkv, hd, pos0, rows):
+    """Workgroup shape does not change a row's arithmetic: 4- or 8-wave
+    workgroups, one or paired causal tiles give bit-identical outputs (key
+    blocks past a row's position add exact zeros with an exact factor 1)."""
+    rng = np.random.default_rng(rows + hd)
+    cap = pos0 + rows + 3
+    q = rng.standard_normal((rows, nh * hd)).astype(np.float32)
+    kc = rng.standard_normal(nkv * cap * hd).astype(np.float16).view(np.uint16)
+    vc = rng.standard_normal(nkv * cap * hd).astype(np.float16).view(np.uint16)
+    dq, dk, dv = _dev(rf, q.reshape(-1), stream), _dev(rf, kc, stream), _dev(rf, vc, stream)
+    outs = []
+    for waves, pairing in [(4, 1), (8, 1), (4, 2), (8, 2)]:
+        dout = rf.DeviceBuffer.zeroed(rows * nh * hd, np.float32, stream)
+        rf.check(rf.load().rfp4_debug_prefill_waves(waves))
+        rf.check(rf.load().rfp4_debug_prefill_pairing(pairing))
+        try:
+            rf.attn_prefill_f16(stream, nh, nkv, hd, pos0, rows, dq, nh * hd, dk, dv, hd, cap * hd, dout, nh * hd)
+        finally:
+            rf.check(rf.load().rfp4_debug_prefill_waves(0))
+            rf.check(rf.load().rfp4_debug_prefill_pairing(0))
+        outs.append(dout.to_host(rows * nh * hd, np.float32, stream))
+    for o in outs[1:]:
+        np.testing.assert_array_equal(o, outs[0])
+
+
 @pytest.mark.parametrize("nh,nkv,hd,pos0,rows", [(8, 2, 128, 0, 200), (8, 1, 64, 30, 77)])
 def test_attn_prefill_f16_strided(rf, orc, stream, nh, nkv, hd, pos0, rows):
     """The engine's layout: q rows inside fused QKV rows (row stride
