@@ -866,11 +866,12 @@ namespace {
 struct GemmTile {
     uint32_t bm, bn;
     const char *name;
+    uint32_t occ; // workgroups per CU (registers / LDS of the compiled kernel)
 };
 // Compiled tile shapes (kernels.hip GEMM_KERNEL), largest first.
 constexpr GemmTile kGemmTiles[] = {
-    {256, 256, "rfp4_gemm_256x256"}, {256, 128, "rfp4_gemm_256x128"}, {128, 128, "rfp4_gemm_128x128"},
-    {64, 128, "rfp4_gemm_64x128"},   {32, 128, "rfp4_gemm_32x128"},
+    {256, 256, "rfp4_gemm_256x256", 1}, {256, 128, "rfp4_gemm_256x128", 1}, {128, 128, "rfp4_gemm_128x128", 2},
+    {64, 128, "rfp4_gemm_64x128", 3},   {32, 128, "rfp4_gemm_32x128", 3},
 };
 constexpr int kGemmNumTiles = (int)(sizeof(kGemmTiles) / sizeof(kGemmTiles[0]));
 // plan index of the few-row kernel (gemm_skinny.h): 16 * MA activation rows, 16 * NB W rows per workgroup
@@ -913,6 +914,30 @@ GemmPlan gemm_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t num_cus)
         return p;
     }
     int pick = t_gemm_tile;
+    if (pick < 0 && m >= 1024u) {
+        // many rows: the fewest rounds of resident workgroups (tiles over
+        // occupancy x CUs), then the fullest last round, then the most
+        // workgroups per CU.  Measured at M = 2048 (8B prefill): q|k|v 256x256
+        // 49.6 us (vs 60.0 for 256x128), o and down 128x128 29.6 / 82.2 us (vs
+        // 33.2 / 90.2), gate|up 256x256.
+        int best = -1;
+        uint64_t best_rounds = 0;
+        double best_fill = 0.0;
+        for (int i = 0; i < kGemmNumTiles; i++) {
+            const GemmTile &t = kGemmTiles[i];
+            if ((uint64_t)ceil_div(m, t.bm) * t.bm * 4u > (uint64_t)m * 5u) continue; // > 25% padding
+            const uint64_t nt = (uint64_t)ceil_div(m, t.bm) * ceil_div(n, t.bn), slots = (uint64_t)t.occ * num_cus;
+            const uint64_t rounds = (nt + slots - 1) / slots;
+            const double fill = (double)nt / (double)(rounds * slots);
+            const bool better = best < 0 || rounds < best_rounds ||
+                                (rounds == best_rounds && (fill > best_fill + 0.01 ||
+                                                           (fill > best_fill - 0.01 && t.occ > kGemmTiles[best].occ)));
+            if (better) best = i, best_rounds = rounds, best_fill = fill;
+        }
+        // (a grid under half the CUs goes to the K-split rule below)
+        if (best >= 0 && 2ull * ceil_div(m, kGemmTiles[best].bm) * ceil_div(n, kGemmTiles[best].bn) >= num_cus)
+            return {best, 1u};
+    }
     if (pick < 0) {
         // one round of 256x256 tiles over at least 7/8 of the CUs beats two
         // rounds of 256x128 (one workgroup per CU either way): 8B gate|up at
