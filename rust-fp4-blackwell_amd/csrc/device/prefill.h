@@ -9,6 +9,8 @@
 #include "misc.h"
 #include "norm_rope.h"
 
+#define RQ_U 4 // elements per thread whose loads are issued together in the row kernels
+
 // grid (rows): y[r] = widen(embed[ids[r]])  (llama_run/src/main.rs:509-510)
 RFP4_DEV void embed_rows_body(const RowsArgs &a)
 {
@@ -27,50 +29,97 @@ RFP4_DEV void embed_rows_body(const RowsArgs &a)
 // thread re-reads only the elements it stored.
 RFP4_DEV void rmsnorm_quant_rows_body(const RowsArgs &a)
 {
+    // each thread takes elements i, i + T, i + 2T, ... in that order; the
+    // loads of RQ_U consecutive ones are issued before any is used (one
+    // memory round trip per RQ_U instead of per element)
+    constexpr int U = RQ_U;
     __shared__ float red[16];
-    const uint32_t r = blockIdx.x, k4 = a.k / 4u;
+    const uint32_t r = blockIdx.x, k4 = a.k / 4u, T = blockDim.x;
     const float4 *x = (const float4 *)(a.x + (size_t)r * a.k);
+    const float4 *add = a.add ? (const float4 *)(a.add + (size_t)r * a.k) : nullptr;
+    float4 *xo = (float4 *)(a.x_out + (size_t)r * a.k);
     float ss = 0.0f;
-    for (uint32_t i = threadIdx.x; i < k4; i += blockDim.x) {
-        float4 v = x[i];
-        if (a.add) {
-            const float4 d = ((const float4 *)(a.add + (size_t)r * a.k))[i];
-            v = make_float4(__fadd_rn(v.x, d.x), __fadd_rn(v.y, d.y), __fadd_rn(v.z, d.z), __fadd_rn(v.w, d.w));
-            ((float4 *)(a.x_out + (size_t)r * a.k))[i] = v;
+    for (uint32_t i0 = threadIdx.x; i0 < k4; i0 += U * T) {
+        float4 v[U], d[U];
+#pragma unroll
+        for (int j = 0; j < U; j++) {
+            const uint32_t i = i0 + (uint32_t)j * T;
+            if (i < k4) {
+                v[j] = x[i];
+                if (add) d[j] = add[i];
+            }
         }
-        ss = __fadd_rn(ss, __fmul_rn(v.x, v.x));
-        ss = __fadd_rn(ss, __fmul_rn(v.y, v.y));
-        ss = __fadd_rn(ss, __fmul_rn(v.z, v.z));
-        ss = __fadd_rn(ss, __fmul_rn(v.w, v.w));
+#pragma unroll
+        for (int j = 0; j < U; j++) {
+            const uint32_t i = i0 + (uint32_t)j * T;
+            if (i >= k4) break;
+            if (add) {
+                v[j] = make_float4(__fadd_rn(v[j].x, d[j].x), __fadd_rn(v[j].y, d[j].y), __fadd_rn(v[j].z, d[j].z),
+                                   __fadd_rn(v[j].w, d[j].w));
+                xo[i] = v[j];
+            }
+            ss = __fadd_rn(ss, __fmul_rn(v[j].x, v[j].x));
+            ss = __fadd_rn(ss, __fmul_rn(v[j].y, v[j].y));
+            ss = __fadd_rn(ss, __fmul_rn(v[j].z, v[j].z));
+            ss = __fadd_rn(ss, __fmul_rn(v[j].w, v[j].w));
+        }
     }
     const float total = block_sum(ss, red);
     const float rms = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(total, (float)a.k), a.eps)));
     const uint2 *w = (const uint2 *)a.w;
     uint8_t *codes = a.codes + (size_t)r * a.k / 2u, *scales = a.scales + (size_t)r * (a.k / 32u);
-    for (uint32_t i = threadIdx.x; i < k4; i += blockDim.x) { // k % 32 == 0: whole 8-thread groups
-        const float4 v = x[i];
-        const uint2 wb = w[i];
-        const float4 y = make_float4(__fmul_rn(__fmul_rn(v.x, rms), f16_bits_to_f32((uint16_t)(wb.x & 0xFFFFu))),
-                                     __fmul_rn(__fmul_rn(v.y, rms), f16_bits_to_f32((uint16_t)(wb.x >> 16))),
-                                     __fmul_rn(__fmul_rn(v.z, rms), f16_bits_to_f32((uint16_t)(wb.y & 0xFFFFu))),
-                                     __fmul_rn(__fmul_rn(v.w, rms), f16_bits_to_f32((uint16_t)(wb.y >> 16))));
-        quant_block32_x8(y, codes + (i / 8u) * 16u, scales + i / 8u);
+    for (uint32_t i0 = threadIdx.x; i0 < k4; i0 += U * T) { // k % 32 == 0: whole 8-thread groups
+        float4 v[U];
+        uint2 wb[U];
+#pragma unroll
+        for (int j = 0; j < U; j++) {
+            const uint32_t i = i0 + (uint32_t)j * T;
+            if (i < k4) {
+                v[j] = add ? xo[i] : x[i];
+                wb[j] = w[i];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < U; j++) {
+            const uint32_t i = i0 + (uint32_t)j * T;
+            if (i >= k4) break;
+            const float4 y = make_float4(__fmul_rn(__fmul_rn(v[j].x, rms), f16_bits_to_f32((uint16_t)(wb[j].x & 0xFFFFu))),
+                                         __fmul_rn(__fmul_rn(v[j].y, rms), f16_bits_to_f32((uint16_t)(wb[j].x >> 16))),
+                                         __fmul_rn(__fmul_rn(v[j].z, rms), f16_bits_to_f32((uint16_t)(wb[j].y & 0xFFFFu))),
+                                         __fmul_rn(__fmul_rn(v[j].w, rms), f16_bits_to_f32((uint16_t)(wb[j].y >> 16))));
+            quant_block32_x8(y, codes + (i / 8u) * 16u, scales + i / 8u);
+        }
     }
 }
 
 // grid (rows): s = silu(gate) * up (llama_run/src/main.rs:244-252) of row r
 // (gate = columns [0, k), up = [k, 2k) of the stacked gate|up output), then
-// OCP MX quantisation per 32 values (8 threads per block, float4 loads).
+// OCP MX quantisation per 32 values (8 threads per block, float4 loads, the
+// loads of RQ_U consecutive elements of a thread issued together).
 RFP4_DEV void swiglu_quant_rows_body(const RowsArgs &a)
 {
-    const uint32_t r = blockIdx.x, k4 = a.k / 4u;
+    constexpr int U = RQ_U;
+    const uint32_t r = blockIdx.x, k4 = a.k / 4u, T = blockDim.x;
     const float4 *g = (const float4 *)(a.x + (size_t)r * 2u * a.k), *u = g + k4;
     uint8_t *codes = a.codes + (size_t)r * a.k / 2u, *scales = a.scales + (size_t)r * (a.k / 32u);
-    for (uint32_t i = threadIdx.x; i < k4; i += blockDim.x) { // k % 32 == 0: whole 8-thread groups
-        const float4 gv = g[i], uv = u[i];
-        const float4 y = make_float4(__fmul_rn(silu_ref(gv.x), uv.x), __fmul_rn(silu_ref(gv.y), uv.y),
-                                     __fmul_rn(silu_ref(gv.z), uv.z), __fmul_rn(silu_ref(gv.w), uv.w));
-        quant_block32_x8(y, codes + (i / 8u) * 16u, scales + i / 8u);
+    for (uint32_t i0 = threadIdx.x; i0 < k4; i0 += U * T) { // k % 32 == 0: whole 8-thread groups
+        float4 gv[U], uv[U];
+#pragma unroll
+        for (int j = 0; j < U; j++) {
+            const uint32_t i = i0 + (uint32_t)j * T;
+            if (i < k4) {
+                gv[j] = g[i];
+                uv[j] = u[i];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < U; j++) {
+            const uint32_t i = i0 + (uint32_t)j * T;
+            if (i >= k4) break;
+            const float4 y = make_float4(__fmul_rn(silu_ref(gv[j].x), uv[j].x), __fmul_rn(silu_ref(gv[j].y), uv[j].y),
+                                         __fmul_rn(silu_ref(gv[j].z), uv[j].z), __fmul_rn(silu_ref(gv[j].w), uv[j].w));
+            quant_block32_x8(y, codes + (i / 8u) * 16u, scales + i / 8u);
+        }
     }
 }
 
