@@ -54,13 +54,14 @@ def test_shape_errors_need_no_device():
     assert lib.rfp4_debug_gemm_plan(6, 0) == -1
 
 
-@pytest.mark.parametrize("m", [1, 32, 80, 512, 4096])
-@pytest.mark.parametrize("n,k", [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336), (128256, 4096),
-                                 (292, 1024)])
+@pytest.mark.parametrize("m", [1, 32, 80, 512, 2048, 4096])
+@pytest.mark.parametrize("n,k", [(4096, 4096), (1024, 4096), (14336, 4096), (28672, 4096), (4096, 14336),
+                                 (128256, 4096), (292, 1024)])
 def test_gemm_plan_shapes(m, n, k):
     """The automatic GEMM plan (256 CUs without a device): a compiled tile, no
-    empty K split, the split-K partials fit the workspace, and either one
-    workgroup per CU or the K split is at its maximum."""
+    empty K split, the split-K partials fit the workspace, and the CUs covered
+    (at least 7/8 of them, at least half from 1024 rows) unless the K split
+    is at its maximum."""
     tm, tn, kz = rfp4.gemm_plan(m, n, k)
     if m <= 64 and k % 2048 == 0 and n * k <= 1 << 25:   # few-row kernel: no K split
         assert (tm, tn, kz) == (16 if m <= 16 else 32 if m <= 32 else 64, 32 if n >= 64 * 256 else 16, 1)
@@ -71,9 +72,27 @@ def test_gemm_plan_shapes(m, n, k):
     assert 1 <= kz <= nsuper and (kz - 1) * per < nsuper
     assert kz == 1 or kz * m * n <= (8 << 20)
     tiles = -(-m // tm) * -(-n // tn)
-    assert tiles * kz >= 256 or kz == nsuper or (kz + 1) * m * n > (8 << 20)
+    cover = 128 if m >= 1024 else 224
+    assert tiles * kz >= cover or kz == nsuper or (kz + 1) * m * n > (8 << 20)
     if m > 32:
         assert -(-m // tm) * tm <= 1.25 * m or tm == 32   # bounded row padding
+
+
+@pytest.mark.parametrize("m,n,k,plan", [
+    (512, 28672, 4096, (256, 256, 1)),   # one round of 256x256 at 7/8 of the CUs (50 vs 66 us)
+    (512, 4096, 14336, (64, 128, 2)),    # long K split in two (37-49 vs 51-62 us)
+    (512, 14336, 4096, (128, 128, 1)),
+    (512, 6144, 4096, (64, 128, 1)),
+    (2048, 6144, 4096, (256, 256, 1)),   # fewest resident rounds (49.6 vs 60.0 us)
+    (2048, 4096, 4096, (128, 128, 1)),   # (29.6 vs 33.2 us)
+    (2048, 4096, 14336, (128, 128, 1)),  # (82.2 vs 90.2 us)
+    (2048, 28672, 4096, (256, 256, 1)),
+    (32, 28672, 4096, (32, 128, 1)),     # no split at 7/8 of the CUs (17.0 vs 19.7 us)
+])
+def test_gemm_plan_measured_choices(m, n, k, plan):
+    """The planner's choices on the 8B prefill and decode-batch shapes that
+    were measured on MI355X (tile sweeps; times in the comments)."""
+    assert rfp4.gemm_plan(m, n, k) == plan
 
 
 def test_calls_before_init_fail_loudly():
