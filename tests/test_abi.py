@@ -120,3 +120,19 @@ def test_product_does_not_link_or_name_the_oracle():
             text = open(os.path.join(dirpath, f), errors="ignore").read()
             assert "orc_" not in text and "pyoracle" not in text, f
     assert "pyoracle" not in open(os.path.join(PKG, "rfp4.py")).read()
+
+
+def test_test_hooks_validate_arguments():
+    """The thread-local test hooks reject values that name no compiled
+    variant or mode (no device needed) and accept their automatic setting."""
+    lib = rfp4.load()
+    assert lib.rfp4_debug_prefill_waves(6) == -1
+    assert lib.rfp4_debug_prefill_waves(16) == -1
+    assert lib.rfp4_debug_prefill_pairing(3) == -1
+    assert lib.rfp4_debug_prefill_attn(2) == -1
+    assert lib.rfp4_debug_attn_merge(3) == -1
+    assert lib.rfp4_debug_gemv_waves(2) == -1
+    for hook in (lib.rfp4_debug_prefill_waves, lib.rfp4_debug_prefill_pairing, lib.rfp4_debug_prefill_attn,
+                 lib.rfp4_debug_attn_merge, lib.rfp4_debug_gemv_waves):
+        assert hook(0) == 0
+
