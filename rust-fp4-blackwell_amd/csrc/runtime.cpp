@@ -269,12 +269,13 @@ GemvVariant gemv_variant(uint32_t n, uint32_t k, int epi, bool f32scale)
         else if (n >= 65536u && ns_needed <= 2) R = 8;
         else R = 2;
     }
-    // 4 waves per workgroup: 8-wave workgroups (compiled for one-slice
-    // shapes) are faster alone (TinyLlama gate|up 6.18 -> 5.42 us) but slower
-    // inside the decode step (1313 -> 1276 tok/s, fused norm), so only forced
+    // 8 waves per workgroup where compiled (one-slice SwiGLU at R = 1, store
+    // at R = 2: K <= 2048), else 4.  Measured in the TinyLlama decode step:
+    // 1811 -> 1836 tok/s (gate|up, q|k|v and the LM head on 8 waves).
     int W = 4;
     if (t_force_r) R = t_force_r;
     if (t_force_w) W = t_force_w;
+    else if (gemv_has_ns(f32scale, epi, R, ns_needed, 8)) W = 8;
     int ns = gemv_has_ns(f32scale, epi, R, ns_needed, W) ? ns_needed : 0;
     if (t_force_ns >= 0) ns = t_force_ns;
     if (W != 4 && !gemv_has_ns(f32scale, epi, R, ns, W)) W = 4, ns = gemv_has_ns(f32scale, epi, R, ns_needed) ? ns_needed : 0;
