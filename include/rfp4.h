@@ -48,6 +48,13 @@ enum {
 const char *rfp4_last_error(void);
 int rfp4_version(void);
 
+/* Kernels of the embedded gfx950 code object, read from its symbol table (no
+ * device needed): how many, and the name of kernel i.  Test hook: the CPU
+ * tests check that every kernel the host launches is present.  No reference
+ * counterpart. */
+int rfp4_kernel_count(uint32_t *count);
+int rfp4_kernel_name(uint32_t i, char *buf, size_t cap);
+
 /* ------------------------------------------------------------------ runtime
  * Replaces cuda-oxide's context / stream / DeviceBuffer / event API used by
  * the reference (fp4_gemv/src/main.rs:144-150,177-191). */
@@ -218,27 +225,18 @@ int rfp4_debug_gemv_variant(int rows_per_wave, int slices);
  * (0 = automatic, 4 or 8; 8 exists for one-slice SwiGLU at 1 row per wave and
  * store at 2).  No reference counterpart. */
 int rfp4_debug_gemv_waves(int waves);
-/* Test hook: GEMV implementation of later launches on this thread: 0 = auto,
- * 1 = VALU kernel, 2 = bf16 matrix-core kernel (rows_per_wave then means
- * 16-row tiles per wave, slices the super-chunks per wave), 3 = block-scaled
- * MFMA kernel (E2M1 weights x E4M3 planes of x; E8M0 scales, k % 512 == 0,
- * k <= 14336).  No reference counterpart. */
-int rfp4_debug_gemv_path(int path);
 /* Test hook: one GEMV launch with any epilogue (0 store, 1 residual,
  * 2 SwiGLU with gate rows [0, n) and up rows [pair_off, pair_off + n),
- * 3 argmax) and, when norm_w is not null, the RMSNorm of x fused in front:
- * the engine's fused launches, reachable alone.  Argmax needs
+ * 3 argmax), scales of either format (RFP4_SCALE_*: E8M0 bytes or f32) and,
+ * when norm_w is not null, the RMSNorm of x fused in front: the engine's
+ * fused launches, reachable alone.  Argmax needs
  * mx4_gemv_argmax_workspace(n) bytes of workspace.  No reference
  * counterpart. */
-int rfp4_debug_gemv_fused(rfp4_stream_t stream, int epi, uint32_t n, uint32_t k, uint32_t pair_off,
-                          const uint8_t *codes, const uint8_t *scales, const float *x, const uint16_t *norm_w,
+int rfp4_debug_gemv_fused(rfp4_stream_t stream, int epi, int scale_format, uint32_t n, uint32_t k, uint32_t pair_off,
+                          const uint8_t *codes, const void *scales, const float *x, const uint16_t *norm_w,
                           float eps, float *y, void *workspace, uint32_t *best_token);
 /* Hardware E2M1 conversion of n words (8 codes each) to 8n floats. */
 int rfp4_selftest_cvt_fp4(rfp4_stream_t stream, uint32_t n, const uint32_t *words, float *out);
-/* Hardware E2M1 -> bf16 conversion with a per-word f32 scale: out[4i+s] =
- * packed bf16 pair of byte s of words[i] times scales[i]. */
-int rfp4_selftest_cvt_bf16(rfp4_stream_t stream, uint32_t n, const uint32_t *words, const float *scales,
-                           uint32_t *out);
 /* One v_mfma_f32_16x16x32_bf16 from raw per-lane registers (4 dwords per
  * lane for a and b); out receives 4 accumulator floats per lane. */
 int rfp4_mma_bf16_tile(rfp4_stream_t stream, const uint32_t *a, const uint32_t *b, float *out);
@@ -255,17 +253,32 @@ int rfp4_synth_f16(rfp4_stream_t stream, uint64_t seed, uint64_t stream_id, floa
  * The step loop of llama_run / llama_decode (llama_run/src/main.rs:492-570,
  * llama_decode/src/main.rs:428-492) with the model constants of
  * llama_run/src/main.rs:318-332 made a runtime config. */
+/* Per-32 block scales of every projection: OCP E8M0 bytes (the BASELINE
+ * MXFP4 numerics), or the reference engine's f32 scales
+ * (llama_run/src/main.rs:334-376, llama_decode/src/main.rs:307-325). */
+enum { RFP4_SCALE_E8M0 = 0, RFP4_SCALE_F32 = 1 };
+/* KV-cache elements: fp16 (the configs), or f32 as the reference
+ * (llama_run/src/main.rs:388-389). */
+enum { RFP4_KV_F16 = 0, RFP4_KV_F32 = 1 };
+
 typedef struct rfp4_model_config {
     uint32_t dim, n_layers, n_heads, n_kv_heads, head_dim, ffn, vocab, max_seq;
     double theta;
     float eps;
-    uint32_t reserved;
+    uint16_t scale_format; /* RFP4_SCALE_* (0 = E8M0) */
+    uint16_t kv_format;    /* RFP4_KV_* (0 = fp16) */
 } rfp4_model_config;
 
 typedef struct llama_engine llama_engine;
 
-/* Allocates weights (synthetic MXFP4 init from `seed`, generated on the
- * device), fp16 KV caches and workspaces, and captures the step graph. */
+/* Allocates weights, KV caches and workspaces.  Synthetic init from `seed`:
+ *  - E8M0 scales: weights N(0, 0.02^2) quantized by the OCP MX rules,
+ *    embeddings N(0, 0.02^2) fp16, norms 1 + 0.02 N, generated on the device;
+ *  - f32 scales: the reference harness's weights (llama_decode/src/main.rs:
+ *    300-325,369-393: xorshift32 from the low 32 bits of `seed`, per layer
+ *    q, k, v, o, gate, up, down, then the LM head, each its packed words then
+ *    its scales 0.25 + (r % 8) / 32) and its activation vector
+ *    (r % 2001) / 1000 - 1 (:421), norms 1.0; embeddings as for E8M0. */
 int llama_engine_create(const rfp4_model_config *cfg, uint64_t seed, llama_engine **out);
 /* Real weights (the reference's loader, llama_run/src/main.rs:413-460): a
  * safetensors checkpoint with the Llama tensor names (model.layers.N.
@@ -277,6 +290,9 @@ int llama_engine_create(const rfp4_model_config *cfg, uint64_t seed, llama_engin
  * (exact for bf16 gains of magnitude 2^-17 .. 65504, as the reference's f32
  * copies), embeddings as stored when BF16 or F16 (F32 rounded to bf16). */
 int llama_engine_create_from_safetensors(const rfp4_model_config *cfg, const char *path, llama_engine **out);
+/* With cfg.scale_format = RFP4_SCALE_F32 the projections are quantized on the
+ * host by the reference's own packer instead (absmax/6 f32 scales,
+ * fp4_quantize_absmax, llama_run/src/main.rs:334-376). */
 /* Packed-weight cache (no reference counterpart; the reference re-quantizes
  * at every start): the engine's MXFP4 weights, norms and embeddings with its
  * config, written as one file, and an engine rebuilt from such a file with
@@ -292,7 +308,8 @@ int llama_engine_prefill_kv(llama_engine *e, uint64_t seed, uint32_t upto);
 /* forward(tok, pos) -> argmax, blocking: llama_run/src/main.rs:492-536 */
 int llama_decode_step(llama_engine *e, uint32_t tok, uint32_t pos, uint32_t *next);
 /* Batched prefill (no reference counterpart; the reference feeds the prompt
- * token by token, llama_run/src/main.rs:550-556): prompt[0..n) at positions
+ * token by token, llama_run/src/main.rs:550-556), for E8M0 engines with fp16
+ * caches: prompt[0..n) at positions
  * pos0.. through the MXFP4 GEMM, every projection input quantised to MXFP4
  * per 32 along K (OCP rules).  Writes those positions' K/V and returns in
  * *next_token the greedy token after the last one; decoding continues with
@@ -310,7 +327,27 @@ int llama_generate(llama_engine *e, const uint32_t *prompt, uint32_t n_prompt, u
  * replay n steps, read back the produced tokens. */
 int llama_engine_begin(llama_engine *e, const uint32_t *prompt, uint32_t n_prompt, uint32_t pos0,
                        uint32_t ids_cap);
+/* The reference's random-weight decode harness (llama_decode/src/main.rs:
+ * 356-492) on an f32-scale engine made by llama_engine_create: every K/V
+ * position [0, ctx) set to 0.01 (:375-376,388-389), the activation x set to
+ * the harness vector, and the cursor armed at position ctx.  Each following
+ * llama_engine_run_steps step is that harness's decode_step: no embedding
+ * lookup, x carries over from the previous step, and the step's argmax is
+ * written to ids[1 + i] (llama_engine_read_ids).  Graph replays as usual. */
+int llama_engine_begin_harness(llama_engine *e, uint32_t ctx, uint32_t ids_cap);
 int llama_engine_run_steps(llama_engine *e, uint32_t n_steps);
+/* Timing of the step's kernels in place: n_steps more steps (advancing the
+ * cursor exactly like llama_engine_run_steps), launched one by one, each
+ * kernel bracketed by start/stop events taken from its own dispatch
+ * (hipExtModuleLaunchKernel), so a record is the kernel's duration inside the
+ * decode step.  Blocking; up to `cap` records in launch order, `*count` set
+ * to the number of launches.  No reference counterpart (the reference times
+ * whole steps, llama_decode/src/main.rs:486-492). */
+typedef struct rfp4_kernel_time {
+    char name[64];
+    float us;
+} rfp4_kernel_time;
+int llama_engine_time_steps(llama_engine *e, uint32_t n_steps, rfp4_kernel_time *out, uint32_t cap, uint32_t *count);
 int llama_engine_read_ids(llama_engine *e, uint32_t *ids, uint32_t count);
 /* Logits of the last step (vocab floats, blocking). */
 int llama_engine_logits(llama_engine *e, float *host_logits);
@@ -320,7 +357,9 @@ int llama_engine_use_graph(llama_engine *e, int enable);
 /* Device views for parity tests.  proj: 0..6 = q,k,v,o,gate,up,down; layer -1 = LM head. */
 int llama_engine_weight(llama_engine *e, int layer, int proj, const uint8_t **codes, const uint8_t **scales,
                         size_t *code_bytes, size_t *scale_bytes);
-int llama_engine_kv(llama_engine *e, int layer, const uint16_t **k, const uint16_t **v, size_t *count);
+/* K/V caches of a layer, [kv_head][cache positions][head_dim] elements of the
+ * engine's kv_format (fp16 bits or f32); count = elements per cache. */
+int llama_engine_kv(llama_engine *e, int layer, const void **k, const void **v, size_t *count);
 /* Per-token weight and KV bytes the step streams at a given position. */
 uint64_t llama_engine_weight_bytes(const llama_engine *e);
 

@@ -659,16 +659,39 @@ uint32_t orc_argmax(uint32_t n, const float *logits)
 struct orc_model {
     orc_model_config c;
     uint8_t *codes[64][ORC_NPROJ];
-    uint8_t *scales[64][ORC_NPROJ];
+    uint8_t *scales[64][ORC_NPROJ]; /* E8M0 bytes or f32, per scale_format */
     uint16_t *norm_attn[64], *norm_ffn[64], *norm_final;
     uint16_t *embed;
     uint8_t *lm_codes, *lm_scales;
-    uint16_t *kc[64], *vc[64]; /* [kvh][max_seq][hd] */
+    void *kc[64], *vc[64];     /* [kvh][max_seq][hd], fp16 bits or f32 per kv_format */
     int embed_bf16;            /* embeddings hold bf16 (1) or f16 (0) bits; norms are f16 */
     float *cosv, *sinv;
+    float *x0;                 /* the harness's activation vector (f32-scale models) */
     /* scratch */
     float *x, *h, *q, *k, *v, *a, *ao, *g, *u, *sw, *d, *logits, *attn_f32_q, *tmpw;
 };
+
+static size_t scale_bytes(const orc_model_config *c) { return c->scale_format == ORC_SCALE_F32 ? 4u : 1u; }
+static size_t kv_bytes(const orc_model_config *c) { return c->kv_format == ORC_KV_F32 ? 4u : 2u; }
+
+/* y = W.x for one projection of the model, in its scale format. */
+static void model_gemv(const orc_model *m, uint32_t n, uint32_t k, const uint8_t *codes, const uint8_t *scales,
+                       const float *x, float *y)
+{
+    if (m->c.scale_format == ORC_SCALE_F32)
+        orc_gemv_f32scale(n, k, (const uint32_t *)codes, (const float *)scales, x, y);
+    else
+        orc_gemv_e8m0(n, k, codes, scales, x, y);
+}
+
+/* llama_decode/src/main.rs:307-325 (mk_fp4): n*k/8 words, one xorshift32
+ * output each, then n*k/32 scales 0.25 + (r % 8) * 0.03125. */
+static void mk_fp4(uint32_t *s, size_t n, size_t k, uint8_t *codes, float *scales)
+{
+    uint32_t *w = (uint32_t *)codes;
+    for (size_t i = 0; i < n * k / 8; i++) w[i] = orc_xorshift32_next(s);
+    for (size_t i = 0; i < n * (k / 32); i++) scales[i] = 0.25f + (float)(orc_xorshift32_next(s) % 8u) * 0.03125f;
+}
 
 static void proj_shape(const orc_model_config *c, int p, uint32_t *N, uint32_t *K)
 {
@@ -694,40 +717,60 @@ static void proj_shape(const orc_model_config *c, int p, uint32_t *N, uint32_t *
 
 orc_model *orc_model_create(const orc_model_config *cfg, uint64_t seed)
 {
-    if (cfg->n_layers > 64) return NULL;
+    if (cfg->n_layers > 64 || cfg->scale_format > ORC_SCALE_F32 || cfg->kv_format > ORC_KV_F32) return NULL;
     orc_model *m = (orc_model *)calloc(1, sizeof(orc_model));
     m->c = *cfg;
     const orc_model_config *c = cfg;
+    const int f32s = c->scale_format == ORC_SCALE_F32;
+    const size_t sb = scale_bytes(c);
+    uint32_t xs = (uint32_t)seed; /* mk_fp4 stream (f32 scales) */
     for (uint32_t l = 0; l < c->n_layers; l++) {
         for (int p = 0; p < ORC_NPROJ; p++) {
             uint32_t N, K;
             proj_shape(c, p, &N, &K);
             m->codes[l][p] = (uint8_t *)malloc((size_t)N * K / 2);
-            m->scales[l][p] = (uint8_t *)malloc((size_t)N * K / 32);
-            orc_synth_mx_weight(seed, STREAM_W(l, p), 0.02f, K, 0, N, m->codes[l][p], m->scales[l][p]);
+            m->scales[l][p] = (uint8_t *)malloc((size_t)N * K / 32 * sb);
+            if (f32s)
+                mk_fp4(&xs, N, K, m->codes[l][p], (float *)m->scales[l][p]);
+            else
+                orc_synth_mx_weight(seed, STREAM_W(l, p), 0.02f, K, 0, N, m->codes[l][p], m->scales[l][p]);
         }
         m->norm_attn[l] = (uint16_t *)malloc(sizeof(uint16_t) * c->dim);
         m->norm_ffn[l] = (uint16_t *)malloc(sizeof(uint16_t) * c->dim);
-        orc_synth_f16(seed, STREAM_NORM(l, 0), 0.02f, 1.0f, c->dim, m->norm_attn[l]);
-        orc_synth_f16(seed, STREAM_NORM(l, 1), 0.02f, 1.0f, c->dim, m->norm_ffn[l]);
+        if (f32s) {
+            for (uint32_t i = 0; i < c->dim; i++) m->norm_attn[l][i] = m->norm_ffn[l][i] = 0x3C00u; /* 1.0 */
+        } else {
+            orc_synth_f16(seed, STREAM_NORM(l, 0), 0.02f, 1.0f, c->dim, m->norm_attn[l]);
+            orc_synth_f16(seed, STREAM_NORM(l, 1), 0.02f, 1.0f, c->dim, m->norm_ffn[l]);
+        }
         size_t kvn = (size_t)c->n_kv_heads * c->max_seq * c->head_dim;
-        m->kc[l] = (uint16_t *)calloc(kvn, sizeof(uint16_t));
-        m->vc[l] = (uint16_t *)calloc(kvn, sizeof(uint16_t));
+        m->kc[l] = calloc(kvn, kv_bytes(c));
+        m->vc[l] = calloc(kvn, kv_bytes(c));
     }
     m->norm_final = (uint16_t *)malloc(sizeof(uint16_t) * c->dim);
-    orc_synth_f16(seed, STREAM_NORM_FINAL, 0.02f, 1.0f, c->dim, m->norm_final);
+    if (f32s)
+        for (uint32_t i = 0; i < c->dim; i++) m->norm_final[i] = 0x3C00u;
+    else
+        orc_synth_f16(seed, STREAM_NORM_FINAL, 0.02f, 1.0f, c->dim, m->norm_final);
     m->embed = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)c->vocab * c->dim);
     orc_synth_f16(seed, STREAM_EMBED, 0.02f, 0.0f, (size_t)c->vocab * c->dim, m->embed);
     m->lm_codes = (uint8_t *)malloc((size_t)c->vocab * c->dim / 2);
-    m->lm_scales = (uint8_t *)malloc((size_t)c->vocab * c->dim / 32);
-    orc_synth_mx_weight(seed, STREAM_LM, 0.02f, c->dim, 0, c->vocab, m->lm_codes, m->lm_scales);
+    m->lm_scales = (uint8_t *)malloc((size_t)c->vocab * c->dim / 32 * sb);
+    if (f32s)
+        mk_fp4(&xs, c->vocab, c->dim, m->lm_codes, (float *)m->lm_scales);
+    else
+        orc_synth_mx_weight(seed, STREAM_LM, 0.02f, c->dim, 0, c->vocab, m->lm_codes, m->lm_scales);
+    /* the harness's activation vector (llama_decode/src/main.rs:421) */
+    m->x0 = (float *)calloc(c->dim, sizeof(float));
+    if (f32s)
+        for (uint32_t i = 0; i < c->dim; i++) m->x0[i] = (float)(orc_xorshift32_next(&xs) % 2001u) / 1000.0f - 1.0f;
     uint32_t half = c->head_dim / 2;
     m->cosv = (float *)malloc(sizeof(float) * (size_t)c->max_seq * half);
     m->sinv = (float *)malloc(sizeof(float) * (size_t)c->max_seq * half);
     orc_rope_table(c->max_seq, c->head_dim, c->theta, m->cosv, m->sinv);
     uint32_t qd = c->n_heads * c->head_dim, kvd = c->n_kv_heads * c->head_dim;
     uint32_t big = c->dim > qd ? c->dim : qd;
-    m->x = (float *)malloc(sizeof(float) * c->dim);
+    m->x = (float *)calloc(c->dim, sizeof(float));
     m->h = (float *)malloc(sizeof(float) * c->dim);
     m->q = (float *)malloc(sizeof(float) * qd);
     m->k = (float *)malloc(sizeof(float) * kvd);
@@ -762,6 +805,7 @@ void orc_model_destroy(orc_model *m)
     free(m->lm_scales);
     free(m->cosv);
     free(m->sinv);
+    free(m->x0);
     free(m->x); free(m->h); free(m->q); free(m->k); free(m->v); free(m->a); free(m->ao);
     free(m->g); free(m->u); free(m->sw); free(m->d); free(m->logits); free(m->tmpw);
     free(m);
@@ -783,11 +827,11 @@ uint8_t *orc_model_scales(orc_model *m, int layer, int proj, size_t *bytes)
 {
     uint32_t N, K;
     if (layer < 0) {
-        *bytes = (size_t)m->c.vocab * m->c.dim / 32;
+        *bytes = (size_t)m->c.vocab * m->c.dim / 32 * scale_bytes(&m->c);
         return m->lm_scales;
     }
     proj_shape(&m->c, proj, &N, &K);
-    *bytes = (size_t)N * K / 32;
+    *bytes = (size_t)N * K / 32 * scale_bytes(&m->c);
     return m->scales[layer][proj];
 }
 
@@ -804,13 +848,13 @@ uint16_t *orc_model_norm(orc_model *m, int layer, int which, size_t *count)
     return which ? m->norm_ffn[layer] : m->norm_attn[layer];
 }
 
-uint16_t *orc_model_kcache(orc_model *m, int layer, size_t *count)
+void *orc_model_kcache(orc_model *m, int layer, size_t *count)
 {
     *count = (size_t)m->c.n_kv_heads * m->c.max_seq * m->c.head_dim;
     return m->kc[layer];
 }
 
-uint16_t *orc_model_vcache(orc_model *m, int layer, size_t *count)
+void *orc_model_vcache(orc_model *m, int layer, size_t *count)
 {
     *count = (size_t)m->c.n_kv_heads * m->c.max_seq * m->c.head_dim;
     return m->vc[layer];
@@ -829,13 +873,17 @@ static void prefill_layers(void *p, size_t a, size_t b)
     float coef = orc_ih4_coef(0.1f);
     for (size_t l = a; l < b; l++)
         for (int isv = 0; isv < 2; isv++) {
-            uint16_t *dst = isv ? c->m->vc[l] : c->m->kc[l];
+            void *dst = isv ? c->m->vc[l] : c->m->kc[l];
             for (uint32_t t = 0; t < c->upto; t++)
                 for (uint32_t kvh = 0; kvh < cf->n_kv_heads; kvh++)
                     for (uint32_t d = 0; d < cf->head_dim; d++) {
                         uint64_t idx = ((uint64_t)t * cf->n_kv_heads + kvh) * cf->head_dim + d;
                         float v = orc_ih4_normal(orc_mix64(c->seed, STREAM_KV(l, isv), idx), coef);
-                        dst[((size_t)kvh * cf->max_seq + t) * cf->head_dim + d] = orc_f32_to_f16(v);
+                        size_t at = ((size_t)kvh * cf->max_seq + t) * cf->head_dim + d;
+                        if (cf->kv_format == ORC_KV_F32)
+                            ((float *)dst)[at] = v;
+                        else
+                            ((uint16_t *)dst)[at] = orc_f32_to_f16(v);
                     }
         }
 }
@@ -861,46 +909,107 @@ static void widen_embed(const orc_model *m, const uint16_t *src, uint32_t n, flo
 
 void orc_model_set_embed_bf16(orc_model *m, int bf16) { m->embed_bf16 = bf16 ? 1 : 0; }
 
-/* llama_run/src/main.rs:492-536 */
-uint32_t orc_model_step(orc_model *m, uint32_t tok, uint32_t pos, float *logits)
+void orc_model_fill_kv(orc_model *m, float value, uint32_t upto)
+{
+    const orc_model_config *c = &m->c;
+    if (upto > c->max_seq) upto = c->max_seq;
+    const uint16_t h = orc_f32_to_f16(value);
+    for (uint32_t l = 0; l < c->n_layers; l++)
+        for (int isv = 0; isv < 2; isv++) {
+            void *dst = isv ? m->vc[l] : m->kc[l];
+            for (uint32_t kvh = 0; kvh < c->n_kv_heads; kvh++)
+                for (uint32_t t = 0; t < upto; t++)
+                    for (uint32_t d = 0; d < c->head_dim; d++) {
+                        size_t at = ((size_t)kvh * c->max_seq + t) * c->head_dim + d;
+                        if (c->kv_format == ORC_KV_F32)
+                            ((float *)dst)[at] = value;
+                        else
+                            ((uint16_t *)dst)[at] = h;
+                    }
+        }
+}
+
+void orc_model_harness_begin(orc_model *m) { memcpy(m->x, m->x0, sizeof(float) * m->c.dim); }
+
+/* The layers and the LM head of one decode step on the activation m->x
+ * (llama_run/src/main.rs:512-534, llama_decode/src/main.rs:445-466): per
+ * layer rmsnorm -> q, k, v GEMVs -> RoPE of q and k -> K/V append at `pos`
+ * -> attention over pos + 1 positions -> o GEMV -> residual -> rmsnorm ->
+ * gate, up GEMVs -> SwiGLU -> down GEMV -> residual; then the final rmsnorm
+ * and the LM-head GEMV into m->logits. */
+static void model_layers(orc_model *m, uint32_t pos)
 {
     const orc_model_config *c = &m->c;
     uint32_t half = c->head_dim / 2;
     uint32_t qd = c->n_heads * c->head_dim, kvd = c->n_kv_heads * c->head_dim;
-    if (pos >= c->max_seq || tok >= c->vocab) return 0xFFFFFFFFu;
-    widen_embed(m, m->embed + (size_t)tok * c->dim, c->dim, m->x);
     const float *cp = m->cosv + (size_t)pos * half, *sp = m->sinv + (size_t)pos * half;
     for (uint32_t l = 0; l < c->n_layers; l++) {
         widen_f16(m->norm_attn[l], c->dim, m->tmpw);
         orc_rmsnorm(c->dim, c->eps, m->x, m->tmpw, m->h);
-        orc_gemv_e8m0(qd, c->dim, m->codes[l][ORC_WQ], m->scales[l][ORC_WQ], m->h, m->q);
-        orc_gemv_e8m0(kvd, c->dim, m->codes[l][ORC_WK], m->scales[l][ORC_WK], m->h, m->k);
-        orc_gemv_e8m0(kvd, c->dim, m->codes[l][ORC_WV], m->scales[l][ORC_WV], m->h, m->v);
+        model_gemv(m, qd, c->dim, m->codes[l][ORC_WQ], m->scales[l][ORC_WQ], m->h, m->q);
+        model_gemv(m, kvd, c->dim, m->codes[l][ORC_WK], m->scales[l][ORC_WK], m->h, m->k);
+        model_gemv(m, kvd, c->dim, m->codes[l][ORC_WV], m->scales[l][ORC_WV], m->h, m->v);
         orc_rope(c->n_heads, c->head_dim, cp, sp, m->q);
         orc_rope(c->n_kv_heads, c->head_dim, cp, sp, m->k);
         for (uint32_t kvh = 0; kvh < c->n_kv_heads; kvh++)
             for (uint32_t d = 0; d < c->head_dim; d++) {
                 size_t at = ((size_t)kvh * c->max_seq + pos) * c->head_dim + d;
-                m->kc[l][at] = orc_f32_to_f16(m->k[kvh * c->head_dim + d]);
-                m->vc[l][at] = orc_f32_to_f16(m->v[kvh * c->head_dim + d]);
+                if (c->kv_format == ORC_KV_F32) {
+                    ((float *)m->kc[l])[at] = m->k[kvh * c->head_dim + d];
+                    ((float *)m->vc[l])[at] = m->v[kvh * c->head_dim + d];
+                } else {
+                    ((uint16_t *)m->kc[l])[at] = orc_f32_to_f16(m->k[kvh * c->head_dim + d]);
+                    ((uint16_t *)m->vc[l])[at] = orc_f32_to_f16(m->v[kvh * c->head_dim + d]);
+                }
             }
-        orc_attn_decode_f16(c->n_heads, c->n_kv_heads, c->head_dim, pos + 1, m->q, m->kc[l], m->vc[l],
-                            c->head_dim, (size_t)c->max_seq * c->head_dim, m->a);
-        orc_gemv_e8m0(c->dim, qd, m->codes[l][ORC_WO], m->scales[l][ORC_WO], m->a, m->ao);
+        if (c->kv_format == ORC_KV_F32)
+            orc_attn_decode(c->n_heads, c->n_kv_heads, c->head_dim, pos + 1, m->q, (const float *)m->kc[l],
+                            (const float *)m->vc[l], c->head_dim, (size_t)c->max_seq * c->head_dim, m->a);
+        else
+            orc_attn_decode_f16(c->n_heads, c->n_kv_heads, c->head_dim, pos + 1, m->q, (const uint16_t *)m->kc[l],
+                                (const uint16_t *)m->vc[l], c->head_dim, (size_t)c->max_seq * c->head_dim, m->a);
+        model_gemv(m, c->dim, qd, m->codes[l][ORC_WO], m->scales[l][ORC_WO], m->a, m->ao);
         orc_residual(c->dim, m->ao, m->x);
         widen_f16(m->norm_ffn[l], c->dim, m->tmpw);
         orc_rmsnorm(c->dim, c->eps, m->x, m->tmpw, m->h);
-        orc_gemv_e8m0(c->ffn, c->dim, m->codes[l][ORC_WG], m->scales[l][ORC_WG], m->h, m->g);
-        orc_gemv_e8m0(c->ffn, c->dim, m->codes[l][ORC_WU], m->scales[l][ORC_WU], m->h, m->u);
+        model_gemv(m, c->ffn, c->dim, m->codes[l][ORC_WG], m->scales[l][ORC_WG], m->h, m->g);
+        model_gemv(m, c->ffn, c->dim, m->codes[l][ORC_WU], m->scales[l][ORC_WU], m->h, m->u);
         orc_swiglu(c->ffn, m->g, m->u, m->sw);
-        orc_gemv_e8m0(c->dim, c->ffn, m->codes[l][ORC_WD], m->scales[l][ORC_WD], m->sw, m->d);
+        model_gemv(m, c->dim, c->ffn, m->codes[l][ORC_WD], m->scales[l][ORC_WD], m->sw, m->d);
         orc_residual(c->dim, m->d, m->x);
     }
     widen_f16(m->norm_final, c->dim, m->tmpw);
     orc_rmsnorm(c->dim, c->eps, m->x, m->tmpw, m->h);
-    orc_gemv_e8m0(c->vocab, c->dim, m->lm_codes, m->lm_scales, m->h, m->logits);
+    model_gemv(m, c->vocab, c->dim, m->lm_codes, m->lm_scales, m->h, m->logits);
+}
+
+/* llama_run/src/main.rs:492-536 */
+uint32_t orc_model_step(orc_model *m, uint32_t tok, uint32_t pos, float *logits)
+{
+    const orc_model_config *c = &m->c;
+    if (pos >= c->max_seq || tok >= c->vocab) return 0xFFFFFFFFu;
+    widen_embed(m, m->embed + (size_t)tok * c->dim, c->dim, m->x);
+    model_layers(m, pos);
     if (logits) memcpy(logits, m->logits, sizeof(float) * c->vocab);
     return orc_argmax(c->vocab, m->logits);
+}
+
+/* llama_decode/src/main.rs:428-477: the same layers on the carried x; the
+ * host argmax scans from f32::MIN with strict > (:467-476). */
+uint32_t orc_model_step_noembed(orc_model *m, uint32_t pos, float *logits)
+{
+    const orc_model_config *c = &m->c;
+    if (pos >= c->max_seq) return 0xFFFFFFFFu;
+    model_layers(m, pos);
+    if (logits) memcpy(logits, m->logits, sizeof(float) * c->vocab);
+    uint32_t best = 0;
+    float bv = -3.40282347e38f;
+    for (uint32_t i = 0; i < c->vocab; i++)
+        if (m->logits[i] > bv) {
+            bv = m->logits[i];
+            best = i;
+        }
+    return best;
 }
 
 /* Batched prefill with MXFP4 activations (the "next" path of the decode
@@ -931,6 +1040,7 @@ uint32_t orc_model_prefill(orc_model *m, const uint32_t *prompt, uint32_t n, uin
     const uint32_t half = c->head_dim / 2, hd = c->head_dim;
     const uint32_t qd = c->n_heads * hd, kvd = c->n_kv_heads * hd;
     if (n == 0 || pos0 + n > c->max_seq) return 0xFFFFFFFFu;
+    if (c->scale_format != ORC_SCALE_E8M0 || c->kv_format != ORC_KV_F16) return 0xFFFFFFFFu; /* MXFP4 GEMM path */
     for (uint32_t i = 0; i < n; i++)
         if (prompt[i] >= c->vocab) return 0xFFFFFFFFu;
     const uint32_t kmax = c->dim > c->ffn ? (c->dim > qd ? c->dim : qd) : (c->ffn > qd ? c->ffn : qd);
@@ -958,12 +1068,13 @@ uint32_t orc_model_prefill(orc_model *m, const uint32_t *prompt, uint32_t n, uin
             for (uint32_t kvh = 0; kvh < c->n_kv_heads; kvh++)
                 for (uint32_t d = 0; d < hd; d++) {
                     size_t at = ((size_t)kvh * c->max_seq + pos) * hd + d;
-                    m->kc[l][at] = orc_f32_to_f16(Kr[(size_t)i * kvd + kvh * hd + d]);
-                    m->vc[l][at] = orc_f32_to_f16(Vr[(size_t)i * kvd + kvh * hd + d]);
+                    ((uint16_t *)m->kc[l])[at] = orc_f32_to_f16(Kr[(size_t)i * kvd + kvh * hd + d]);
+                    ((uint16_t *)m->vc[l])[at] = orc_f32_to_f16(Vr[(size_t)i * kvd + kvh * hd + d]);
                 }
         }
         for (uint32_t i = 0; i < n; i++)
-            orc_attn_decode_f16(c->n_heads, c->n_kv_heads, hd, pos0 + i + 1, Q + (size_t)i * qd, m->kc[l], m->vc[l], hd,
+            orc_attn_decode_f16(c->n_heads, c->n_kv_heads, hd, pos0 + i + 1, Q + (size_t)i * qd, (const uint16_t *)m->kc[l],
+                                (const uint16_t *)m->vc[l], hd,
                                 (size_t)c->max_seq * hd, A + (size_t)i * qd);
         orc_quant_mx(A, n, qd, hc, hs);
         gemm_rows_f32(n, c->dim, qd, hc, hs, m->codes[l][ORC_WO], m->scales[l][ORC_WO], O);

@@ -132,16 +132,29 @@ typedef struct orc_model_config {
     uint32_t dim, n_layers, n_heads, n_kv_heads, head_dim, ffn, vocab, max_seq;
     double theta;
     float eps;
+    uint16_t scale_format; /* ORC_SCALE_*: per-32 block scales of every projection */
+    uint16_t kv_format;    /* ORC_KV_*: element type of the K/V caches */
 } orc_model_config;
+
+enum { ORC_SCALE_E8M0 = 0, ORC_SCALE_F32 = 1 };
+enum { ORC_KV_F16 = 0, ORC_KV_F32 = 1 };
 
 /* Projection order inside a layer (stream ids for the synthetic init). */
 enum { ORC_WQ = 0, ORC_WK, ORC_WV, ORC_WO, ORC_WG, ORC_WU, ORC_WD, ORC_NPROJ };
 
 typedef struct orc_model orc_model;
 
-/* Allocate a model with synthetic weights generated on the CPU from `seed`
- * (weights sigma 0.02, embeddings sigma 0.02, norms 1 + 0.02*N) -- the same
- * generator the device engine uses, so packed bytes are identical. */
+/* Allocate a model with synthetic weights generated on the CPU from `seed` --
+ * the same generators the device engine uses, so packed bytes are identical.
+ *  - E8M0 scales: weights N(0, 0.02^2) quantized by the OCP MX rules,
+ *    embeddings N(0, 0.02^2) in f16, norms 1 + 0.02*N in f16.
+ *  - f32 scales: the reference harness's mk_fp4 (llama_decode/src/main.rs:
+ *    300-325,369-393): xorshift32 seeded with the low 32 bits of `seed`,
+ *    per layer q, k, v, o, gate, up, down, then the LM head, each as all its
+ *    packed words (uniform codes) followed by all its scales
+ *    0.25 + (r % 8) * 0.03125; then the harness's activation vector
+ *    (r % 2001) / 1000 - 1 (:421).  Norms 1.0 (:381-383,392); embeddings as
+ *    the E8M0 model's (the harness has none). */
 orc_model *orc_model_create(const orc_model_config *cfg, uint64_t seed);
 void orc_model_destroy(orc_model *m);
 /* Embeddings are bf16 bit patterns (a real checkpoint) instead of f16. */
@@ -151,11 +164,22 @@ uint8_t *orc_model_codes(orc_model *m, int layer, int proj, size_t *bytes);
 uint8_t *orc_model_scales(orc_model *m, int layer, int proj, size_t *bytes);
 uint16_t *orc_model_embed(orc_model *m, size_t *count);
 uint16_t *orc_model_norm(orc_model *m, int layer, int which, size_t *count); /* which: 0 attn, 1 ffn; layer=-1 final */
-uint16_t *orc_model_kcache(orc_model *m, int layer, size_t *count);  /* [kvh][max_seq][hd] */
-uint16_t *orc_model_vcache(orc_model *m, int layer, size_t *count);
+/* K/V caches [kvh][max_seq][hd], fp16 bits or f32 per kv_format; count in elements */
+void *orc_model_kcache(orc_model *m, int layer, size_t *count);
+void *orc_model_vcache(orc_model *m, int layer, size_t *count);
 /* Fill positions [0, upto) of every layer's K/V cache with f16(0.1*N) from
  * (seed, stream 0x4B560000 + 2*layer (+1 for V), index (t*NKV+kvh)*HD+d). */
 void orc_model_prefill_kv(orc_model *m, uint64_t seed, uint32_t upto);
+/* The reference harness's context (llama_decode/src/main.rs:375-376,388-389):
+ * positions [0, upto) of every K/V cache set to `value` (rounded to fp16 for
+ * fp16 caches); and its persistent activation x := the vector drawn after the
+ * weights (f32-scale models only, else zeros). */
+void orc_model_fill_kv(orc_model *m, float value, uint32_t upto);
+void orc_model_harness_begin(orc_model *m);
+/* One step of the harness (llama_decode/src/main.rs:428-477): no embedding
+ * lookup, x carries over from the previous step; returns the argmax of the
+ * logits (strict >, first maximum). */
+uint32_t orc_model_step_noembed(orc_model *m, uint32_t pos, float *logits);
 /* One decode step (llama_run/src/main.rs:492-536): token `tok` at position
  * `pos`; writes logits (vocab floats) if non-null; returns the argmax. */
 uint32_t orc_model_step(orc_model *m, uint32_t tok, uint32_t pos, float *logits);

@@ -12,7 +12,8 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "liboracle.so")
+# RFP4_ORACLE_LIB selects another build (the sanitizer build of the CPU tests)
+LIB_PATH = os.environ.get("RFP4_ORACLE_LIB") or os.path.join(HERE, "liboracle.so")
 
 P = C.c_void_p
 U8, U16, U32, U64, I32, F32, F64, SZ = C.c_uint8, C.c_uint16, C.c_uint32, C.c_uint64, C.c_int, C.c_float, C.c_double, C.c_size_t
@@ -22,7 +23,7 @@ class OrcModelConfig(C.Structure):
     _fields_ = [
         ("dim", U32), ("n_layers", U32), ("n_heads", U32), ("n_kv_heads", U32),
         ("head_dim", U32), ("ffn", U32), ("vocab", U32), ("max_seq", U32),
-        ("theta", F64), ("eps", F32),
+        ("theta", F64), ("eps", F32), ("scale_format", U16), ("kv_format", U16),
     ]
 
 
@@ -73,6 +74,9 @@ _SIGS = {
     "orc_model_vcache": (P, [P, I32, C.POINTER(SZ)]),
     "orc_model_prefill_kv": (None, [P, U64, U32]),
     "orc_model_step": (U32, [P, U32, U32, P]),
+    "orc_model_fill_kv": (None, [P, F32, U32]),
+    "orc_model_harness_begin": (None, [P]),
+    "orc_model_step_noembed": (U32, [P, U32, P]),
     "orc_model_generate": (None, [P, P, U32, U32, U32, P, P]),
     "orc_model_prefill": (U32, [P, P, U32, U32, P]),
 }
@@ -259,12 +263,23 @@ def f32_to_f16(v: np.ndarray) -> np.ndarray:
 
 
 # ---------------------------------------------------------------- model
+SCALE_E8M0, SCALE_F32 = 0, 1
+KV_F16, KV_F32 = 0, 1
+
+
 class Model:
+    """The oracle decoder.  cfg may carry scale_format (SCALE_E8M0 or
+    SCALE_F32: the reference's f32 per-32 scales and its mk_fp4 harness init)
+    and kv_format (KV_F16 or KV_F32)."""
+
     def __init__(self, cfg: dict, seed: int):
         self.cfg = dict(cfg)
+        self.scale_format = int(cfg.get("scale_format", SCALE_E8M0))
+        self.kv_format = int(cfg.get("kv_format", KV_F16))
         c = OrcModelConfig(dim=cfg["dim"], n_layers=cfg["n_layers"], n_heads=cfg["n_heads"],
                            n_kv_heads=cfg["n_kv_heads"], head_dim=cfg["head_dim"], ffn=cfg["ffn"],
-                           vocab=cfg["vocab"], max_seq=cfg["max_seq"], theta=cfg["theta"], eps=cfg["eps"])
+                           vocab=cfg["vocab"], max_seq=cfg["max_seq"], theta=cfg["theta"], eps=cfg["eps"],
+                           scale_format=self.scale_format, kv_format=self.kv_format)
         self.h = lib().orc_model_create(C.byref(c), seed)
         if not self.h:
             raise RuntimeError("orc_model_create failed")
@@ -278,7 +293,9 @@ class Model:
         return self._view(lib().orc_model_codes, layer, proj, dtype=np.uint8)
 
     def scales(self, layer, proj):
-        return self._view(lib().orc_model_scales, layer, proj, dtype=np.uint8)
+        """E8M0 bytes, or the f32 scales of a SCALE_F32 model."""
+        b = self._view(lib().orc_model_scales, layer, proj, dtype=np.uint8)
+        return b.view(np.float32) if self.scale_format == SCALE_F32 else b
 
     def embed(self):
         return self._view(lib().orc_model_embed, dtype=np.uint16)
@@ -309,11 +326,28 @@ class Model:
         self.scales(-1, 0)[:] = s.reshape(-1)
         lib().orc_model_set_embed_bf16(self.h, 1 if embed_bf16 else 0)
 
+    def _kv_dtype(self):
+        return np.float32 if self.kv_format == KV_F32 else np.uint16
+
     def kcache(self, layer):
-        return self._view(lib().orc_model_kcache, layer, dtype=np.uint16)
+        return self._view(lib().orc_model_kcache, layer, dtype=self._kv_dtype())
 
     def vcache(self, layer):
-        return self._view(lib().orc_model_vcache, layer, dtype=np.uint16)
+        return self._view(lib().orc_model_vcache, layer, dtype=self._kv_dtype())
+
+    def fill_kv(self, value, upto):
+        lib().orc_model_fill_kv(self.h, value, upto)
+
+    def harness_begin(self, ctx):
+        """llama_decode's context: K/V positions [0, ctx) := 0.01 and x := the
+        harness vector (llama_decode/src/main.rs:375-376,421)."""
+        self.fill_kv(0.01, ctx)
+        lib().orc_model_harness_begin(self.h)
+
+    def step_noembed(self, pos, want_logits=False):
+        logits = np.empty(self.cfg["vocab"], dtype=np.float32) if want_logits else None
+        t = lib().orc_model_step_noembed(self.h, pos, ptr(logits) if want_logits else None)
+        return (t, logits) if want_logits else t
 
     def prefill_kv(self, seed, upto):
         lib().orc_model_prefill_kv(self.h, seed, upto)

@@ -23,7 +23,8 @@
 //
 // Optional fusion (engine): with rope tables given, q and the current token's
 // k are rotated here (llama_run/src/main.rs:517-518) and the split owning
-// position seq-1 appends fp16 k, v to the caches (:519-521); that split uses
+// position seq-1 appends k, v to the caches (:519-521), rounded to the cache's
+// element type (fp16 RNE, or f32 as the reference's copy_into); that split uses
 // the new row directly instead of its own load of the not-yet-written row.
 #pragma once
 #include "common.h"
@@ -40,6 +41,9 @@ RFP4_DEV float attn_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 template <typename KT>
 struct KvTraits;
+// Per KV element type: elements per 16-byte load, widening to f32, the
+// cache's rounding of a new f32 value (fp16: RNE; f32: as is), and the
+// 16-byte load of EPL stored elements.
 template <>
 struct KvTraits<uint16_t> {
     static constexpr int EPL = 8; // elements per 16-byte load
@@ -52,6 +56,12 @@ struct KvTraits<uint16_t> {
             o[2 * i + 1] = f16_bits_to_f32((uint16_t)(w[i] >> 16));
         }
     }
+    RFP4_DEV static uint16_t from_f32(float v) { return f32_to_f16_bits(v); }
+    RFP4_DEV static uint4 pack(const uint16_t *p)
+    {
+        return make_uint4(p[0] | ((uint32_t)p[1] << 16), p[2] | ((uint32_t)p[3] << 16), p[4] | ((uint32_t)p[5] << 16),
+                          p[6] | ((uint32_t)p[7] << 16));
+    }
 };
 template <>
 struct KvTraits<float> {
@@ -62,6 +72,11 @@ struct KvTraits<float> {
         o[1] = __uint_as_float(r.y);
         o[2] = __uint_as_float(r.z);
         o[3] = __uint_as_float(r.w);
+    }
+    RFP4_DEV static float from_f32(float v) { return v; }
+    RFP4_DEV static uint4 pack(const float *p)
+    {
+        return make_uint4(__float_as_uint(p[0]), __float_as_uint(p[1]), __float_as_uint(p[2]), __float_as_uint(p[3]));
     }
 };
 
@@ -197,7 +212,7 @@ RFP4_DEV void attn_body(const AttnArgs &a)
     __shared__ __align__(16) float qs[GT][HD];
     __shared__ __align__(16) float vred[4][GT][HD];
     __shared__ float s_mx[2][4][GT], s_lred[4][GT], s_mfin[GT];
-    __shared__ uint16_t knew[HD], vnew[HD];
+    __shared__ KT knew[HD], vnew[HD];
 
     const uint32_t kvh = blockIdx.x, split = blockIdx.y, row = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -273,11 +288,11 @@ RFP4_DEV void attn_body(const AttnArgs &a)
         // its K/V stream, so no other split waits on them)
         const float *kn = a.k_new + (size_t)kvh * HD, *vn = a.v_new + (size_t)kvh * HD;
         const float kna = kn[tid], knb = kn[tid + HALF], vna = vn[tid], vnb = vn[tid + HALF];
-        uint16_t *kdst = (uint16_t *)a.kc + (size_t)kvh * a.hs + (size_t)pos * a.ts;
-        uint16_t *vdst = (uint16_t *)a.vc + (size_t)kvh * a.hs + (size_t)pos * a.ts;
-        const uint16_t r0 = f32_to_f16_bits(__fsub_rn(__fmul_rn(kna, cs), __fmul_rn(knb, sn)));
-        const uint16_t r1 = f32_to_f16_bits(__fadd_rn(__fmul_rn(knb, cs), __fmul_rn(kna, sn)));
-        const uint16_t w0 = f32_to_f16_bits(vna), w1 = f32_to_f16_bits(vnb);
+        KT *kdst = (KT *)a.kc + (size_t)kvh * a.hs + (size_t)pos * a.ts;
+        KT *vdst = (KT *)a.vc + (size_t)kvh * a.hs + (size_t)pos * a.ts;
+        const KT r0 = KvTraits<KT>::from_f32(__fsub_rn(__fmul_rn(kna, cs), __fmul_rn(knb, sn)));
+        const KT r1 = KvTraits<KT>::from_f32(__fadd_rn(__fmul_rn(knb, cs), __fmul_rn(kna, sn)));
+        const KT w0 = KvTraits<KT>::from_f32(vna), w1 = KvTraits<KT>::from_f32(vnb);
         knew[tid] = r0;
         knew[tid + HALF] = r1;
         vnew[tid] = w0;
@@ -317,12 +332,7 @@ RFP4_DEV void attn_body(const AttnArgs &a)
             const uint32_t tl = pos - t0 - tb;
             if ((uint32_t)slot == tl % TPS) {
                 const uint32_t s = tl / TPS;
-                uint4 kk, vv;
-                const uint16_t *kp = knew + li * EPL, *vp = vnew + li * EPL;
-                kk.x = kp[0] | ((uint32_t)kp[1] << 16); kk.y = kp[2] | ((uint32_t)kp[3] << 16);
-                kk.z = kp[4] | ((uint32_t)kp[5] << 16); kk.w = kp[6] | ((uint32_t)kp[7] << 16);
-                vv.x = vp[0] | ((uint32_t)vp[1] << 16); vv.y = vp[2] | ((uint32_t)vp[3] << 16);
-                vv.z = vp[4] | ((uint32_t)vp[5] << 16); vv.w = vp[6] | ((uint32_t)vp[7] << 16);
+                const uint4 kk = KvTraits<KT>::pack(knew + li * EPL), vv = KvTraits<KT>::pack(vnew + li * EPL);
 #pragma unroll
                 for (int st = 0; st < NSTEP; st++)
                     if ((uint32_t)st == s) {

@@ -206,7 +206,11 @@ RFP4_DEV void synth_kv_body(const SynthKvArgs &a)
     for (uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (uint64_t)gridDim.x * blockDim.x) {
         uint64_t d = i % a.head_dim, r = i / a.head_dim, kvh = r % a.n_kv_heads, t = r / a.n_kv_heads;
         float v = ih4_normal(mix64(a.seed, a.stream, i), a.coef);
-        a.cache[(kvh * a.max_seq + t) * a.head_dim + d] = f32_to_f16_bits(v);
+        const uint64_t at = (kvh * a.max_seq + t) * a.head_dim + d;
+        if (a.kv_f32)
+            ((float *)a.cache)[at] = v;
+        else
+            ((uint16_t *)a.cache)[at] = f32_to_f16_bits(v);
     }
 }
 

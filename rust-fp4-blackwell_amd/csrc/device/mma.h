@@ -72,21 +72,6 @@ RFP4_DEV void mma_bf16_tile_body(const MmaTileArgs &a)
     for (int r = 0; r < 4; r++) a.out[lane * 4 + r] = acc[r];
 }
 
-// Hardware E2M1 -> bf16 conversion with a per-lane f32 scale: out word i*4+s
-// = packed bf16 pair of byte s of in[i], converted with scale[i].
-RFP4_DEV void selftest_cvt_bf16_body(const SelftestArgs &a)
-{
-    uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= a.n) return;
-    uint32_t w = a.in[i];
-    float s = a.scale[i];
-    uint32_t *o = (uint32_t *)a.out + (size_t)i * 4;
-    o[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 0));
-    o[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 1));
-    o[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 2));
-    o[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, s, 3));
-}
-
 // All-ones known answer (fp4_mma/src/main.rs:24-31): A = B = 1.0 (E2M1 0x2)
 // over K = 128 with the A scale 2^-1 (E8M0 0x7E) and B scale 1.0 (0x7F), so
 // every element is 128 * 0.5 = 64.0, the reference's expected value.  Writes

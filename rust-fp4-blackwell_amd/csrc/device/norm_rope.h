@@ -51,34 +51,6 @@ RFP4_DEV void rope_body(const RopeArgs &a)
     rope_pair(a.q + (size_t)head * a.head_dim, j, half, a.cosv[a.cos_base + j], a.sinv[a.cos_base + j]);
 }
 
-// Engine: rotate q and k of the fused qkv vector at position *pos_ptr and
-// append k, v to the fp16 caches ([kvh][max_seq][hd]).  Replaces the rope x2
-// and copy_into x2 launches of llama_run/src/main.rs:517-521.
-RFP4_DEV void rope_append_body(const RopeAppendArgs &a)
-{
-    const uint32_t hd = a.head_dim, half = hd / 2;
-    const int32_t pos = *a.pos_ptr;
-    if (pos < 0 || (uint32_t)pos >= a.max_seq) return;
-    const float *cp = a.cosv + (size_t)pos * half, *sp = a.sinv + (size_t)pos * half;
-    const uint32_t nq = a.n_heads * half, nk = a.n_kv_heads * half, nv = a.n_kv_heads * hd;
-    float *qv = a.qkv, *kv = a.qkv + (size_t)a.n_heads * hd, *vv = kv + (size_t)a.n_kv_heads * hd;
-    for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < nq + nk + nv; i += gridDim.x * blockDim.x) {
-        if (i < nq) {
-            uint32_t h = i / half, j = i % half;
-            rope_pair(qv + (size_t)h * hd, j, half, cp[j], sp[j]);
-        } else if (i < nq + nk) {
-            uint32_t ii = i - nq, h = ii / half, j = ii % half;
-            float *b = kv + (size_t)h * hd;
-            rope_pair(b, j, half, cp[j], sp[j]);
-            size_t at = ((size_t)h * a.max_seq + (size_t)pos) * hd;
-            a.kcache[at + j] = f32_to_f16_bits(b[j]);
-            a.kcache[at + j + half] = f32_to_f16_bits(b[j + half]);
-        } else {
-            uint32_t ii = i - nq - nk, h = ii / hd, d = ii % hd;
-            a.vcache[((size_t)h * a.max_seq + (size_t)pos) * hd + d] = f32_to_f16_bits(vv[ii]);
-        }
-    }
-}
 
 // x[i] = embed[ids[step]][i] (fp16 or bf16 -> f32): llama_run/src/main.rs:509-510,
 // but gathered on the device so no per-token host upload is needed.

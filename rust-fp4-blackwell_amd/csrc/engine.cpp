@@ -3,13 +3,14 @@
 // rebuilt around one HIP graph per token.
 //
 // Device memory per engine:
-//  - weights (MXFP4, row-major codes + E8M0 scales), per layer
+//  - weights (MXFP4, row-major codes + per-32 scales: E8M0 bytes or the
+//    reference's f32, per the config's scale_format), per layer
 //      qkv  [(NH+2*NKV)*HD][DIM]   q, k, v stacked: one GEMV launch
 //      o    [DIM][NH*HD]
 //      gu   [2*FFN][DIM]           gate rows then up rows: one GEMV + SwiGLU
 //      down [DIM][FFN]
 //    plus the LM head [VOCAB][DIM]; embeddings and norms fp16.
-//  - KV caches fp16 [layer][kvh][max_seq_alloc][HD] (head-major, so a split-K
+//  - KV caches fp16 or f32 [layer][kvh][max_seq_alloc][HD] (head-major, so a split-K
 //    attention workgroup streams one contiguous token range).
 //  - a device cursor (position, step) and the token array ids[]; the LM-head
 //    GEMV reduces its argmax per workgroup and the step kernel writes the next
@@ -18,6 +19,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <thread>
 #include <vector>
 
 #include "runtime.h"
@@ -34,8 +36,11 @@ static const uint64_t kStreamNormFinal = 0xAFFFFull;
 static inline uint64_t stream_kv(uint32_t l, uint32_t isv) { return 0x4B560000ull + ((uint64_t)l << 1) + isv; }
 
 struct LayerW {
-    uint8_t *qkv_c, *qkv_s, *o_c, *o_s, *gu_c, *gu_s, *d_c, *d_s;
+    uint8_t *qkv_c, *qkv_s, *o_c, *o_s, *gu_c, *gu_s, *d_c, *d_s; // scales: sb bytes per 32-block
 };
+
+// The engine's GEMV launches, their variants fixed at creation.
+enum { GV_QKV = 0, GV_O, GV_GU, GV_D, GV_LM, GV_N };
 
 struct llama_engine {
     rfp4_model_config c{};
@@ -44,7 +49,13 @@ struct llama_engine {
     std::vector<LayerW> L;
     uint16_t *norm_attn = nullptr, *norm_ffn = nullptr, *norm_final = nullptr, *embed = nullptr;
     uint8_t *lm_c = nullptr, *lm_s = nullptr;
-    uint16_t *kcache = nullptr, *vcache = nullptr;
+    void *kcache = nullptr, *vcache = nullptr;
+    uint32_t sb = 1, kvb = 2;  // bytes per scale (E8M0 1, f32 4) and per KV element (fp16 2, f32 4)
+    const char *sname = "e8m0"; // kernel-name token of the scale format
+    GemvVariant gv[GV_N]{};     // GEMV variants, fixed at creation (the LM head's sizes `best`)
+    float *gemm_part = nullptr; // split-K partials of the prefill GEMMs (kGemmPartFloats)
+    std::vector<float> harness_x; // llama_decode's activation vector (f32-scale synthetic init)
+    bool no_embed = false;        // harness steps: x carries over, no embedding lookup
     uint32_t max_seq_alloc = 0;
     float *cos_tab = nullptr, *sin_tab = nullptr;
     float *x = nullptr, *h = nullptr, *qkv = nullptr, *attn_out = nullptr, *sw = nullptr, *logits = nullptr;
@@ -87,6 +98,14 @@ static int dalloc_t(llama_engine *e, T **p, size_t count)
 
 static uint32_t qdim(const rfp4_model_config &c) { return c.n_heads * c.head_dim; }
 static uint32_t kvdim(const rfp4_model_config &c) { return c.n_kv_heads * c.head_dim; }
+static uint32_t scale_bytes(const rfp4_model_config &c) { return c.scale_format == RFP4_SCALE_F32 ? 4u : 1u; }
+static uint32_t kv_bytes(const rfp4_model_config &c) { return c.kv_format == RFP4_KV_F32 ? 4u : 2u; }
+// Layer l's K (isv 0) or V (1) cache: [kvh][max_seq_alloc][hd] elements.
+static void *kv_layer(const llama_engine *e, uint32_t l, int isv)
+{
+    const size_t per = (size_t)e->c.n_kv_heads * e->max_seq_alloc * e->c.head_dim * e->kvb;
+    return (char *)(isv ? e->vcache : e->kcache) + (size_t)l * per;
+}
 
 static int validate(const rfp4_model_config &c)
 {
@@ -97,6 +116,8 @@ static int validate(const rfp4_model_config &c)
         return set_error(RFP4_E_SHAPE, "n_heads %u / n_kv_heads %u: group must divide and be <= 8", c.n_heads, c.n_kv_heads);
     if (c.dim % 32 || c.ffn % 32 || qdim(c) % 32) return set_error(RFP4_E_SHAPE, "dim, ffn and n_heads*head_dim must be multiples of 32");
     if (c.n_heads > kAttnMaxHeads) return set_error(RFP4_E_SHAPE, "n_heads %u > %u", c.n_heads, kAttnMaxHeads);
+    if (c.scale_format > RFP4_SCALE_F32) return set_error(RFP4_E_INVALID, "scale_format %u unknown", c.scale_format);
+    if (c.kv_format > RFP4_KV_F32) return set_error(RFP4_E_INVALID, "kv_format %u unknown", c.kv_format);
     return RFP4_OK;
 }
 
@@ -110,14 +131,16 @@ static int enqueue_step(llama_engine *e, uint32_t nsplit)
     hipStream_t s = e->stream;
     const uint32_t qd = qdim(c), kvd = kvdim(c), hd = c.head_dim;
     int rc;
-    EmbedArgs ea{e->embed, e->ids, e->state, e->x, c.dim, c.vocab, e->embed_bf16};
-    if ((rc = launch("rfp4_embed", dim3((c.dim + 255) / 256), dim3(256), s, &ea))) return rc;
+    if (!e->no_embed) {
+        EmbedArgs ea{e->embed, e->ids, e->state, e->x, c.dim, c.vocab, e->embed_bf16};
+        if ((rc = launch("rfp4_embed", dim3((c.dim + 255) / 256), dim3(256), s, &ea))) return rc;
+    }
+    const char *sn = e->sname;
     for (uint32_t l = 0; l < c.n_layers; l++) {
         const LayerW &w = e->L[l];
-        uint16_t *kc = e->kcache + (size_t)l * c.n_kv_heads * e->max_seq_alloc * hd;
-        uint16_t *vc = e->vcache + (size_t)l * c.n_kv_heads * e->max_seq_alloc * hd;
+        void *kc = kv_layer(e, l, 0), *vc = kv_layer(e, l, 1);
         GemvArgs qa{w.qkv_c, w.qkv_s, e->x, e->qkv, nullptr, e->norm_attn + (size_t)l * c.dim, qd + 2 * kvd, c.dim, 0, c.eps};
-        if ((rc = gemv_launch("e8m0", RFP4_EPI_STORE, qa, s, 0))) return rc;
+        if ((rc = gemv_launch_v(sn, RFP4_EPI_STORE, qa, s, e->gv[GV_QKV]))) return rc;
         AttnArgs aa{};
         aa.q = e->qkv; aa.kc = kc; aa.vc = vc; aa.out = e->attn_out;
         aa.part = e->attn_part; aa.pos_ptr = &e->state->pos;
@@ -126,16 +149,16 @@ static int enqueue_step(llama_engine *e, uint32_t nsplit)
         aa.n_heads = c.n_heads; aa.n_kv_heads = c.n_kv_heads; aa.head_dim = hd; aa.seq = 0;
         aa.chunk = e->attn_chunk; aa.max_splits = e->attn_max_splits;
         aa.counters = attn_inmerge_mode(e->attn_merge_mode, nsplit) ? e->attn_counters : nullptr;
-        if ((rc = attn_launch(aa, 1, s, e->attn_chunk * nsplit, 1))) return rc;
+        if ((rc = attn_launch(aa, e->kvb == 2 ? 1 : 0, s, e->attn_chunk * nsplit, 1))) return rc;
         GemvArgs oa{w.o_c, w.o_s, e->attn_out, e->x, nullptr, nullptr, c.dim, qd, 0, 0.0f};
-        if ((rc = gemv_launch("e8m0", RFP4_EPI_RESIDUAL, oa, s, 0))) return rc;
+        if ((rc = gemv_launch_v(sn, RFP4_EPI_RESIDUAL, oa, s, e->gv[GV_O]))) return rc;
         GemvArgs ga{w.gu_c, w.gu_s, e->x, e->sw, nullptr, e->norm_ffn + (size_t)l * c.dim, c.ffn, c.dim, c.ffn, c.eps};
-        if ((rc = gemv_launch("e8m0", RFP4_EPI_SWIGLU, ga, s, 0))) return rc;
+        if ((rc = gemv_launch_v(sn, RFP4_EPI_SWIGLU, ga, s, e->gv[GV_GU]))) return rc;
         GemvArgs da{w.d_c, w.d_s, e->sw, e->x, nullptr, nullptr, c.dim, c.ffn, 0, 0.0f};
-        if ((rc = gemv_launch("e8m0", RFP4_EPI_RESIDUAL, da, s, 0))) return rc;
+        if ((rc = gemv_launch_v(sn, RFP4_EPI_RESIDUAL, da, s, e->gv[GV_D]))) return rc;
     }
     GemvArgs la{e->lm_c, e->lm_s, e->x, e->logits, e->best, e->norm_final, c.vocab, c.dim, 0, c.eps};
-    if ((rc = gemv_launch("e8m0", RFP4_EPI_ARGMAX, la, s, 0))) return rc;
+    if ((rc = gemv_launch_v(sn, RFP4_EPI_ARGMAX, la, s, e->gv[GV_LM]))) return rc;
     StepArgs sa{e->best, e->state, e->ids, e->last_tok, e->n_best, 0};
     return launch("rfp4_step", dim3(1), dim3(1024), s, &sa);
 }
@@ -167,7 +190,8 @@ static int prefill_reserve(llama_engine *e, uint32_t n)
     e->pf_cap = 0;
     const size_t kmax = std::max(std::max(c.dim, qd), c.ffn);
     const size_t ncols = std::max(std::max(qd + 2 * kvd, 2 * c.ffn), c.dim);
-    int rc = dalloc_t(e, &e->pf_x, (size_t)cap * c.dim);
+    int rc = e->gemm_part ? RFP4_OK : dalloc_t(e, &e->gemm_part, kGemmPartFloats);
+    if (!rc) rc = dalloc_t(e, &e->pf_x, (size_t)cap * c.dim);
     if (!rc) rc = dalloc_t(e, &e->pf_c, (size_t)cap * ncols);
     if (!rc) rc = dalloc_t(e, &e->pf_a, (size_t)cap * qd);
     if (!rc) rc = dalloc_t(e, &e->pf_codes, (size_t)cap * kmax / 2);
@@ -192,8 +216,7 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
     if ((rc = launch("rfp4_embed_rows", dim3(n), dim3(256), s, &ea))) return rc;
     for (uint32_t l = 0; l < c.n_layers; l++) {
         const LayerW &w = e->L[l];
-        uint16_t *kc = e->kcache + (size_t)l * c.n_kv_heads * e->max_seq_alloc * hd;
-        uint16_t *vc = e->vcache + (size_t)l * c.n_kv_heads * e->max_seq_alloc * hd;
+        uint16_t *kc = (uint16_t *)kv_layer(e, l, 0), *vc = (uint16_t *)kv_layer(e, l, 1); // fp16 (checked by the caller)
         RowsArgs na{};
         na.x = e->pf_x; na.w = e->norm_attn + (size_t)l * c.dim; na.codes = e->pf_codes; na.scales = e->pf_scales;
         na.rows = n; na.k = c.dim; na.eps = c.eps;
@@ -201,7 +224,7 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
         na.add = l > 0 ? e->pf_c : nullptr;
         na.x_out = e->pf_x;
         if ((rc = launch("rfp4_rmsnorm_quant_rows", dim3(n), dim3(256), s, &na))) return rc;
-        if ((rc = fp4_gemm(s, n, nqkv, c.dim, e->pf_codes, e->pf_scales, w.qkv_c, w.qkv_s, e->pf_c))) return rc;
+        if ((rc = gemm_launch(s, n, nqkv, c.dim, e->pf_codes, e->pf_scales, w.qkv_c, w.qkv_s, e->pf_c, e->gemm_part))) return rc;
         RopeRowsArgs ra{};
         ra.qkv = e->pf_c; ra.cosv = e->cos_tab; ra.sinv = e->sin_tab; ra.kc = kc; ra.vc = vc;
         ra.ts = hd; ra.hs = (uint64_t)e->max_seq_alloc * hd;
@@ -227,15 +250,15 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
             if ((rc = attn_prefill_launch(pa, hd, s))) return rc;
         }
         if ((rc = mx4_quantize(s, n, qd, e->pf_a, 0, e->pf_codes, e->pf_scales))) return rc;
-        if ((rc = fp4_gemm(s, n, c.dim, qd, e->pf_codes, e->pf_scales, w.o_c, w.o_s, e->pf_c))) return rc;
+        if ((rc = gemm_launch(s, n, c.dim, qd, e->pf_codes, e->pf_scales, w.o_c, w.o_s, e->pf_c, e->gemm_part))) return rc;
         na.w = e->norm_ffn + (size_t)l * c.dim;
         na.add = e->pf_c; // x += O projection, then the FFN norm
         if ((rc = launch("rfp4_rmsnorm_quant_rows", dim3(n), dim3(256), s, &na))) return rc;
-        if ((rc = fp4_gemm(s, n, 2 * c.ffn, c.dim, e->pf_codes, e->pf_scales, w.gu_c, w.gu_s, e->pf_c))) return rc;
+        if ((rc = gemm_launch(s, n, 2 * c.ffn, c.dim, e->pf_codes, e->pf_scales, w.gu_c, w.gu_s, e->pf_c, e->gemm_part))) return rc;
         RowsArgs sa{};
         sa.x = e->pf_c; sa.codes = e->pf_codes; sa.scales = e->pf_scales; sa.rows = n; sa.k = c.ffn;
         if ((rc = launch("rfp4_swiglu_quant_rows", dim3(n), dim3(256), s, &sa))) return rc;
-        if ((rc = fp4_gemm(s, n, c.dim, c.ffn, e->pf_codes, e->pf_scales, w.d_c, w.d_s, e->pf_c))) return rc;
+        if ((rc = gemm_launch(s, n, c.dim, c.ffn, e->pf_codes, e->pf_scales, w.d_c, w.d_s, e->pf_c, e->gemm_part))) return rc;
         // x += down projection: by the next layer's first norm, after the last layer here
         if (l + 1 == c.n_layers && (rc = residual(s, n * c.dim, e->pf_c, e->pf_x))) return rc;
     }
@@ -243,7 +266,7 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
     rc = hip_check(hipMemcpyAsync(e->x, e->pf_x + (size_t)(n - 1) * c.dim, c.dim * sizeof(float),
                                   hipMemcpyDeviceToDevice, s), "hipMemcpyAsync(prefill row)");
     GemvArgs la{e->lm_c, e->lm_s, e->x, e->logits, nullptr, e->norm_final, c.vocab, c.dim, 0, c.eps};
-    if (!rc) rc = gemv_launch("e8m0", RFP4_EPI_STORE, la, s, 0);
+    if (!rc) rc = gemv_launch(e->sname, RFP4_EPI_STORE, la, s);
     if (!rc) rc = argmax(s, c.vocab, e->logits, e->last_tok);
     return rc;
 }
@@ -292,14 +315,33 @@ static int step_graphs_for(llama_engine *e, int64_t pos_first, int64_t pos_last)
     return RFP4_OK;
 }
 
+// Drop the captured step graphs (the step's launch list changes with the
+// embedding mode); they are captured again on demand.
+static void drop_graphs(llama_engine *e)
+{
+    for (hipGraphExec_t &g : e->graph_execs)
+        if (g) hipGraphExecDestroy(g), g = nullptr;
+    for (hipGraph_t &g : e->graphs)
+        if (g) hipGraphDestroy(g), g = nullptr;
+}
+
+// Embedding lookup per step (llama_run) or a carried activation (the
+// llama_decode harness): switching drops the graphs of the other mode.
+static int set_embed_mode(llama_engine *e, bool no_embed)
+{
+    if (e->no_embed == no_embed) return RFP4_OK;
+    int rc = hip_check(hipStreamSynchronize(e->stream), "hipStreamSynchronize(mode)");
+    if (rc) return rc;
+    drop_graphs(e);
+    e->no_embed = no_embed;
+    return RFP4_OK;
+}
+
 static void engine_free(llama_engine *e)
 {
     if (!e) return;
     if (e->stream) hipStreamSynchronize(e->stream);
-    for (hipGraphExec_t g : e->graph_execs)
-        if (g) hipGraphExecDestroy(g);
-    for (hipGraph_t g : e->graphs)
-        if (g) hipGraphDestroy(g);
+    drop_graphs(e);
     for (void *p : e->allocs) hipFree(p);
     if (e->stream) hipStreamDestroy(e->stream);
     delete e;
@@ -320,6 +362,10 @@ static int engine_alloc(const rfp4_model_config *cfg, llama_engine **out)
     e->c = *cfg;
     const rfp4_model_config &c = e->c;
     const uint32_t qd = qdim(c), kvd = kvdim(c), hd = c.head_dim;
+    e->sb = scale_bytes(c);
+    e->kvb = kv_bytes(c);
+    e->sname = c.scale_format == RFP4_SCALE_F32 ? "f32" : "e8m0";
+    const size_t sb = e->sb;
     rc = hip_check(hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking), "hipStreamCreate");
     // attention split plan over the full cache capacity
     e->attn_chunk = attn_chunk_for(c.n_kv_heads, c.max_seq, rt->num_cus, hd, 2u, c.n_heads / c.n_kv_heads);
@@ -331,25 +377,25 @@ static int engine_alloc(const rfp4_model_config *cfg, llama_engine **out)
         LayerW &w = e->L[l];
         uint32_t nqkv = qd + 2 * kvd;
         rc = dalloc_t(e, &w.qkv_c, (size_t)nqkv * c.dim / 2);
-        if (!rc) rc = dalloc_t(e, &w.qkv_s, (size_t)nqkv * c.dim / 32);
+        if (!rc) rc = dalloc_t(e, &w.qkv_s, (size_t)nqkv * c.dim / 32 * sb);
         if (!rc) rc = dalloc_t(e, &w.o_c, (size_t)c.dim * qd / 2);
-        if (!rc) rc = dalloc_t(e, &w.o_s, (size_t)c.dim * qd / 32);
+        if (!rc) rc = dalloc_t(e, &w.o_s, (size_t)c.dim * qd / 32 * sb);
         if (!rc) rc = dalloc_t(e, &w.gu_c, (size_t)2 * c.ffn * c.dim / 2);
-        if (!rc) rc = dalloc_t(e, &w.gu_s, (size_t)2 * c.ffn * c.dim / 32);
+        if (!rc) rc = dalloc_t(e, &w.gu_s, (size_t)2 * c.ffn * c.dim / 32 * sb);
         if (!rc) rc = dalloc_t(e, &w.d_c, (size_t)c.dim * c.ffn / 2);
-        if (!rc) rc = dalloc_t(e, &w.d_s, (size_t)c.dim * c.ffn / 32);
+        if (!rc) rc = dalloc_t(e, &w.d_s, (size_t)c.dim * c.ffn / 32 * sb);
     }
     if (!rc) rc = dalloc_t(e, &e->norm_attn, (size_t)c.n_layers * c.dim);
     if (!rc) rc = dalloc_t(e, &e->norm_ffn, (size_t)c.n_layers * c.dim);
     if (!rc) rc = dalloc_t(e, &e->norm_final, c.dim);
     if (!rc) rc = dalloc_t(e, &e->embed, (size_t)c.vocab * c.dim);
     if (!rc) rc = dalloc_t(e, &e->lm_c, (size_t)c.vocab * c.dim / 2);
-    if (!rc) rc = dalloc_t(e, &e->lm_s, (size_t)c.vocab * c.dim / 32);
-    size_t kv_elems = (size_t)c.n_layers * c.n_kv_heads * e->max_seq_alloc * hd;
-    if (!rc) rc = dalloc_t(e, &e->kcache, kv_elems);
-    if (!rc) rc = dalloc_t(e, &e->vcache, kv_elems);
-    if (!rc) rc = fill_words((uint32_t *)e->kcache, kv_elems / 2, 0u, s);
-    if (!rc) rc = fill_words((uint32_t *)e->vcache, kv_elems / 2, 0u, s);
+    if (!rc) rc = dalloc_t(e, &e->lm_s, (size_t)c.vocab * c.dim / 32 * sb);
+    const size_t kv_bytes_all = (size_t)c.n_layers * c.n_kv_heads * e->max_seq_alloc * hd * e->kvb;
+    if (!rc) rc = dalloc(e, &e->kcache, kv_bytes_all);
+    if (!rc) rc = dalloc(e, &e->vcache, kv_bytes_all);
+    if (!rc) rc = fill_words((uint32_t *)e->kcache, kv_bytes_all / 4, 0u, s);
+    if (!rc) rc = fill_words((uint32_t *)e->vcache, kv_bytes_all / 4, 0u, s);
     // rotary table in f64 -> f32 (llama_run/src/main.rs:462-471)
     const uint32_t half = hd / 2;
     std::vector<float> cosv((size_t)e->max_seq_alloc * half), sinv((size_t)e->max_seq_alloc * half);
@@ -374,7 +420,15 @@ static int engine_alloc(const rfp4_model_config *cfg, llama_engine **out)
     if (!rc) rc = dalloc_t(e, &e->attn_out, qd);
     if (!rc) rc = dalloc_t(e, &e->sw, c.ffn);
     if (!rc) rc = dalloc_t(e, &e->logits, c.vocab);
-    e->n_best = gemv_blocks(c.vocab, c.dim, RFP4_EPI_ARGMAX);
+    // GEMV variants fixed now: later thread-local overrides cannot change the
+    // LM head's grid, whose per-workgroup keys `best` holds
+    const bool f32s = c.scale_format == RFP4_SCALE_F32;
+    e->gv[GV_QKV] = gemv_variant(qd + 2 * kvd, c.dim, RFP4_EPI_STORE, f32s);
+    e->gv[GV_O] = gemv_variant(c.dim, qd, RFP4_EPI_RESIDUAL, f32s);
+    e->gv[GV_GU] = gemv_variant(c.ffn, c.dim, RFP4_EPI_SWIGLU, f32s);
+    e->gv[GV_D] = gemv_variant(c.dim, c.ffn, RFP4_EPI_RESIDUAL, f32s);
+    e->gv[GV_LM] = gemv_variant(c.vocab, c.dim, RFP4_EPI_ARGMAX, f32s);
+    e->n_best = gemv_grid(c.vocab, e->gv[GV_LM]);
     if (!rc) rc = dalloc_t(e, &e->best, e->n_best);
     if (!rc) rc = dalloc_t(e, &e->attn_part, (size_t)c.n_heads * e->attn_max_splits * (hd + 4));
     e->attn_merge_mode = attn_merge_mode();
@@ -453,13 +507,64 @@ static ProjDst proj_dst(llama_engine *e, uint32_t l, int p)
     LayerW &w = e->L[l];
     switch (p) {
     case 0: return {w.qkv_c, w.qkv_s, qd, c.dim};
-    case 1: return {w.qkv_c + (size_t)qd * c.dim / 2, w.qkv_s + (size_t)qd * c.dim / 32, kvd, c.dim};
-    case 2: return {w.qkv_c + (size_t)(qd + kvd) * c.dim / 2, w.qkv_s + (size_t)(qd + kvd) * c.dim / 32, kvd, c.dim};
+    case 1: return {w.qkv_c + (size_t)qd * c.dim / 2, w.qkv_s + (size_t)qd * c.dim / 32 * e->sb, kvd, c.dim};
+    case 2: return {w.qkv_c + (size_t)(qd + kvd) * c.dim / 2, w.qkv_s + (size_t)(qd + kvd) * c.dim / 32 * e->sb, kvd, c.dim};
     case 3: return {w.o_c, w.o_s, c.dim, qd};
     case 4: return {w.gu_c, w.gu_s, c.ffn, c.dim};
-    case 5: return {w.gu_c + (size_t)c.ffn * c.dim / 2, w.gu_s + (size_t)c.ffn * c.dim / 32, c.ffn, c.dim};
+    case 5: return {w.gu_c + (size_t)c.ffn * c.dim / 2, w.gu_s + (size_t)c.ffn * c.dim / 32 * e->sb, c.ffn, c.dim};
     default: return {w.d_c, w.d_s, c.dim, c.ffn};
     }
+}
+
+// ---------------------------------------------------------------- the reference harness's init
+// xorshift32 13/17/5 (llama_decode/src/main.rs:300-305).
+static inline uint32_t xorshift32(uint32_t *s)
+{
+    uint32_t x = *s;
+    x ^= x << 13;
+    x ^= x >> 17;
+    x ^= x << 5;
+    *s = x;
+    return x;
+}
+
+// mk_fp4 (llama_decode/src/main.rs:307-325): rows*k/8 packed words, one
+// xorshift output each (uniform codes), then rows*k/32 f32 scales
+// 0.25 + (r % 8) * 0.03125, uploaded to the projection's place.
+static int mk_fp4_upload(uint32_t *st, const ProjDst &d)
+{
+    std::vector<uint32_t> w((size_t)d.rows * d.k / 8);
+    for (auto &v : w) v = xorshift32(st);
+    std::vector<float> sc((size_t)d.rows * (d.k / 32));
+    for (auto &v : sc) v = 0.25f + (float)(xorshift32(st) % 8u) * 0.03125f;
+    int rc = hip_check(hipMemcpy(d.codes, w.data(), w.size() * 4, hipMemcpyHostToDevice), "H2D weights");
+    if (!rc) rc = hip_check(hipMemcpy(d.scales, sc.data(), sc.size() * 4, hipMemcpyHostToDevice), "H2D scales");
+    return rc;
+}
+
+// f32-scale synthetic init: the reference harness's weights in its order
+// (llama_decode/src/main.rs:369-393: per layer q, k, v, o, gate, up, down,
+// then the LM head), norms 1.0 (:381-383,392) and the activation vector
+// (r % 2001) / 1000 - 1 drawn after them (:421); embeddings as the E8M0
+// init's (the harness has none).
+static int engine_synth_mk_fp4(llama_engine *e, uint64_t seed)
+{
+    const rfp4_model_config &c = e->c;
+    hipStream_t s = e->stream;
+    uint32_t st = (uint32_t)seed;
+    int rc = RFP4_OK;
+    for (uint32_t l = 0; l < c.n_layers && !rc; l++)
+        for (int p = 0; p < 7 && !rc; p++) rc = mk_fp4_upload(&st, proj_dst(e, l, p));
+    if (!rc) rc = mk_fp4_upload(&st, ProjDst{e->lm_c, e->lm_s, c.vocab, c.dim});
+    e->harness_x.resize(c.dim);
+    for (auto &v : e->harness_x) v = (float)(xorshift32(&st) % 2001u) / 1000.0f - 1.0f;
+    const uint32_t one2 = 0x3C003C00u; // two fp16 1.0
+    if (!rc) rc = fill_words((uint32_t *)e->norm_attn, (size_t)c.n_layers * c.dim / 2, one2, s);
+    if (!rc) rc = fill_words((uint32_t *)e->norm_ffn, (size_t)c.n_layers * c.dim / 2, one2, s);
+    if (!rc) rc = fill_words((uint32_t *)e->norm_final, c.dim / 2, one2, s);
+    if (!rc) rc = rfp4_synth_f16(s, seed, kStreamEmbed, 0.02f, 0.0f, (size_t)c.vocab * c.dim, e->embed);
+    e->embed_bf16 = 0;
+    return rc;
 }
 
 static int st_tensor(const StFile &f, const std::string &name, uint64_t d0, uint64_t d1, const StTensor **out)
@@ -487,6 +592,33 @@ static int load_proj(llama_engine *e, const StFile &f, const StTensor &t, uint8_
     hipStream_t s = e->stream;
     const uint64_t rows = t.shape[0], k = t.shape[1], n = rows * k;
     int rc;
+    if (e->sb == 4) {
+        // the reference's packer (llama_run/src/main.rs:334-376) on the host,
+        // rows split over threads (each row's result is independent of them)
+        std::vector<float> w(n);
+        rc = f.read_f32(t, w.data(), n);
+        if (rc) return rc;
+        std::vector<uint32_t> packed(n / 8);
+        std::vector<float> sc(n / 32);
+        const uint64_t nt = std::max<uint64_t>(1, std::min<uint64_t>(std::min<uint64_t>(16, rows),
+                                                                     std::thread::hardware_concurrency()));
+        std::vector<std::thread> th;
+        std::vector<int> rcs(nt, 0);
+        for (uint64_t i = 0; i < nt; i++) {
+            const uint64_t r0 = rows * i / nt, r1 = rows * (i + 1) / nt;
+            th.emplace_back([&, i, r0, r1] {
+                if (r1 > r0)
+                    rcs[i] = fp4_quantize_absmax(w.data() + r0 * k, (uint32_t)(r1 - r0), (uint32_t)k,
+                                                 packed.data() + r0 * k / 8, sc.data() + r0 * k / 32);
+            });
+        }
+        for (auto &x : th) x.join();
+        for (int r : rcs)
+            if (r) return set_error(RFP4_E_SHAPE, "absmax quantization of %s failed", t.name.c_str());
+        rc = hip_check(hipMemcpy(codes, packed.data(), n / 2, hipMemcpyHostToDevice), "H2D checkpoint codes");
+        if (!rc) rc = hip_check(hipMemcpy(scales, sc.data(), n / 32 * 4, hipMemcpyHostToDevice), "H2D checkpoint scales");
+        return rc;
+    }
     if (t.dtype == "F16") {
         std::vector<float> tmp(n);
         rc = f.read_f32(t, tmp.data(), n);
@@ -577,9 +709,11 @@ static int engine_load_safetensors(llama_engine *e, const char *path)
 
 // ---------------------------------------------------------------- packed cache
 // File: "RFP4PACK", u32 version, u32 embed_bf16, rfp4_model_config, u32 count,
-// then `count` blobs (u64 bytes + bytes) in engine_blobs order.
+// then `count` blobs (u64 bytes + bytes) in engine_blobs order.  Version 2
+// carries the scale and KV formats in the config (version 1 files, written
+// before the formats existed, hold zeros there: E8M0 and fp16).
 static const char kPackMagic[8] = {'R', 'F', 'P', '4', 'P', 'A', 'C', 'K'};
-static const uint32_t kPackVersion = 1;
+static const uint32_t kPackVersion = 2;
 
 static std::vector<std::pair<void *, size_t>> engine_blobs(llama_engine *e)
 {
@@ -589,20 +723,20 @@ static std::vector<std::pair<void *, size_t>> engine_blobs(llama_engine *e)
     for (uint32_t l = 0; l < c.n_layers; l++) {
         LayerW &w = e->L[l];
         b.push_back({w.qkv_c, (size_t)nqkv * c.dim / 2});
-        b.push_back({w.qkv_s, (size_t)nqkv * c.dim / 32});
+        b.push_back({w.qkv_s, (size_t)nqkv * c.dim / 32 * e->sb});
         b.push_back({w.o_c, (size_t)c.dim * qd / 2});
-        b.push_back({w.o_s, (size_t)c.dim * qd / 32});
+        b.push_back({w.o_s, (size_t)c.dim * qd / 32 * e->sb});
         b.push_back({w.gu_c, (size_t)2 * c.ffn * c.dim / 2});
-        b.push_back({w.gu_s, (size_t)2 * c.ffn * c.dim / 32});
+        b.push_back({w.gu_s, (size_t)2 * c.ffn * c.dim / 32 * e->sb});
         b.push_back({w.d_c, (size_t)c.dim * c.ffn / 2});
-        b.push_back({w.d_s, (size_t)c.dim * c.ffn / 32});
+        b.push_back({w.d_s, (size_t)c.dim * c.ffn / 32 * e->sb});
     }
     b.push_back({e->norm_attn, (size_t)c.n_layers * c.dim * 2});
     b.push_back({e->norm_ffn, (size_t)c.n_layers * c.dim * 2});
     b.push_back({e->norm_final, (size_t)c.dim * 2});
     b.push_back({e->embed, (size_t)c.vocab * c.dim * 2});
     b.push_back({e->lm_c, (size_t)c.vocab * c.dim / 2});
-    b.push_back({e->lm_s, (size_t)c.vocab * c.dim / 32});
+    b.push_back({e->lm_s, (size_t)c.vocab * c.dim / 32 * e->sb});
     return b;
 }
 
@@ -613,7 +747,7 @@ int llama_engine_create(const rfp4_model_config *cfg, uint64_t seed, llama_engin
     llama_engine *e = nullptr;
     int rc = engine_alloc(cfg, &e);
     if (rc) return rc;
-    rc = engine_synth(e, seed);
+    rc = e->sb == 4 ? engine_synth_mk_fp4(e, seed) : engine_synth(e, seed);
     if (!rc) rc = engine_finish(e);
     if (rc) {
         engine_free(e);
@@ -637,8 +771,8 @@ int llama_engine_prefill_kv(llama_engine *e, uint64_t seed, uint32_t upto)
     const float coef = ih4_coef(0.1f);
     for (uint32_t l = 0; l < c.n_layers; l++)
         for (uint32_t isv = 0; isv < 2; isv++) {
-            uint16_t *base = (isv ? e->vcache : e->kcache) + (size_t)l * c.n_kv_heads * e->max_seq_alloc * c.head_dim;
-            SynthKvArgs a{base, seed, stream_kv(l, isv), upto, c.n_kv_heads, c.head_dim, e->max_seq_alloc, coef, 0.0f};
+            SynthKvArgs a{kv_layer(e, l, (int)isv), seed, stream_kv(l, isv), upto, c.n_kv_heads, c.head_dim,
+                          e->max_seq_alloc, coef, e->kvb == 4 ? 1u : 0u};
             uint64_t total = (uint64_t)upto * c.n_kv_heads * c.head_dim;
             uint64_t blocks = (total + 255) / 256;
             if (blocks > 65536) blocks = 65536;
@@ -658,6 +792,7 @@ int llama_engine_begin(llama_engine *e, const uint32_t *prompt, uint32_t n_promp
     for (uint32_t i = 0; i < n_prompt; i++)
         if (prompt[i] >= e->c.vocab) return set_error(RFP4_E_INVALID, "prompt token %u >= vocab %u", prompt[i], e->c.vocab);
     int rc = hip_check(hipStreamSynchronize(e->stream), "hipStreamSynchronize(begin)");
+    if (!rc) rc = set_embed_mode(e, false);
     if (rc) return rc;
     rc = hip_check(hipMemcpy(e->ids, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice), "H2D prompt");
     StepState st{(int32_t)pos0, 0, n_prompt, ids_cap};
@@ -669,6 +804,50 @@ int llama_engine_begin(llama_engine *e, const uint32_t *prompt, uint32_t n_promp
     // the step graphs for every position this generation can reach
     const int64_t last = std::min<int64_t>((int64_t)pos0 + ids_cap - 2, (int64_t)e->c.max_seq - 1);
     rc = step_graphs_for(e, pos0, std::max<int64_t>(last, pos0));
+    if (rc) return rc;
+    e->armed = true;
+    return RFP4_OK;
+}
+
+int llama_engine_begin_harness(llama_engine *e, uint32_t ctx, uint32_t ids_cap)
+{
+    if (!e) return set_error(RFP4_E_INVALID, "llama_engine_begin_harness: null engine");
+    const rfp4_model_config &c = e->c;
+    if (e->harness_x.size() != c.dim)
+        return set_error(RFP4_E_INVALID, "the harness needs an f32-scale engine from llama_engine_create");
+    if (ctx >= c.max_seq) return set_error(RFP4_E_KV_OVERFLOW, "context %u >= max_seq %u", ctx, c.max_seq);
+    if (ids_cap < 2 || ids_cap > e->ids_alloc) return set_error(RFP4_E_CAPACITY, "ids capacity %u out of range", ids_cap);
+    int rc = hip_check(hipStreamSynchronize(e->stream), "hipStreamSynchronize(harness)");
+    if (!rc) rc = set_embed_mode(e, true);
+    if (rc) return rc;
+    // every K/V position [0, ctx) := 0.01 (llama_decode/src/main.rs:375-376,388-389)
+    const float v = 0.01f;
+    uint32_t word;
+    if (e->kvb == 4) {
+        std::memcpy(&word, &v, 4);
+    } else {
+        const uint32_t h = f32_to_f16_rne_host(v);
+        word = h | (h << 16);
+    }
+    const size_t head_bytes = (size_t)e->max_seq_alloc * c.head_dim * e->kvb;
+    for (uint32_t l = 0; l < c.n_layers && !rc; l++)
+        for (int isv = 0; isv < 2 && !rc; isv++)
+            for (uint32_t h = 0; h < c.n_kv_heads && !rc; h++)
+                rc = fill_words((uint32_t *)((char *)kv_layer(e, l, isv) + h * head_bytes),
+                                (size_t)ctx * c.head_dim * e->kvb / 4, word, e->stream);
+    if (!rc) rc = hip_check(hipStreamSynchronize(e->stream), "hipStreamSynchronize(harness kv)");
+    // x := the harness vector; the cursor at ctx, ids[1 + i] <- step i's argmax
+    if (!rc) rc = hip_check(hipMemcpy(e->x, e->harness_x.data(), (size_t)c.dim * 4, hipMemcpyHostToDevice), "H2D x");
+    const uint32_t zero = 0;
+    if (!rc) rc = hip_check(hipMemcpy(e->ids, &zero, 4, hipMemcpyHostToDevice), "H2D ids");
+    StepState st{(int32_t)ctx, 0, 1u, ids_cap};
+    if (!rc) rc = hip_check(hipMemcpy(e->state, &st, sizeof st, hipMemcpyHostToDevice), "H2D cursor");
+    if (rc) return rc;
+    e->h_pos = ctx;
+    e->h_step = 0;
+    e->h_ids_cap = ids_cap;
+    const int64_t last = std::min<int64_t>((int64_t)ctx + ids_cap - 2, (int64_t)c.max_seq - 1);
+    rc = step_graphs_for(e, ctx, std::max<int64_t>(last, ctx));
     if (rc) return rc;
     e->armed = true;
     return RFP4_OK;
@@ -696,6 +875,38 @@ int llama_engine_run_steps(llama_engine *e, uint32_t n_steps)
         }
         if (rc) return rc;
     }
+    e->h_pos += n_steps;
+    e->h_step += n_steps;
+    return RFP4_OK;
+}
+
+int llama_engine_time_steps(llama_engine *e, uint32_t n_steps, rfp4_kernel_time *out, uint32_t cap, uint32_t *count)
+{
+    if (!e || !count || (cap && !out)) return set_error(RFP4_E_INVALID, "llama_engine_time_steps: null argument");
+    if (!e->armed) return set_error(RFP4_E_INVALID, "llama_engine_begin has not been called");
+    if (e->h_pos + n_steps > (int64_t)e->c.max_seq)
+        return set_error(RFP4_E_KV_OVERFLOW, "steps would reach position %lld >= max_seq %u", (long long)(e->h_pos + n_steps),
+                         e->c.max_seq);
+    if (e->h_step + n_steps > e->h_ids_cap - 1)
+        return set_error(RFP4_E_CAPACITY, "steps exceed the token array");
+    std::vector<KernelTiming> rec;
+    int rc = RFP4_OK;
+    timing_install(&rec);
+    for (uint32_t i = 0; i < n_steps && !rc; i++) rc = enqueue_step(e, splits_at(e, e->h_pos + i));
+    timing_install(nullptr);
+    if (!rc) rc = hip_check(hipStreamSynchronize(e->stream), "hipStreamSynchronize(timing)");
+    *count = (uint32_t)rec.size();
+    for (size_t i = 0; i < rec.size(); i++) {
+        float ms = 0.0f;
+        if (!rc) rc = hip_check(hipEventElapsedTime(&ms, rec[i].start, rec[i].stop), "hipEventElapsedTime");
+        if (!rc && i < cap) {
+            snprintf(out[i].name, sizeof out[i].name, "%s", rec[i].name);
+            out[i].us = ms * 1000.0f;
+        }
+        hipEventDestroy(rec[i].start);
+        hipEventDestroy(rec[i].stop);
+    }
+    if (rc) return rc;
     e->h_pos += n_steps;
     e->h_step += n_steps;
     return RFP4_OK;
@@ -760,7 +971,7 @@ int llama_engine_weight(llama_engine *e, int layer, int proj, const uint8_t **co
         *codes = e->lm_c;
         *scales = e->lm_s;
         *code_bytes = (size_t)c.vocab * c.dim / 2;
-        *scale_bytes = (size_t)c.vocab * c.dim / 32;
+        *scale_bytes = (size_t)c.vocab * c.dim / 32 * e->sb;
         return RFP4_OK;
     }
     if ((uint32_t)layer >= c.n_layers || proj < 0 || proj > 6) return set_error(RFP4_E_INVALID, "bad layer/proj");
@@ -777,20 +988,19 @@ int llama_engine_weight(llama_engine *e, int layer, int proj, const uint8_t **co
     default: bc = w.d_c; bs = w.d_s; rows = c.dim; K = c.ffn; break;
     }
     *codes = bc + rows_before * K / 2;
-    *scales = bs + rows_before * K / 32;
+    *scales = bs + rows_before * K / 32 * e->sb;
     *code_bytes = rows * K / 2;
-    *scale_bytes = rows * K / 32;
+    *scale_bytes = rows * K / 32 * e->sb;
     return RFP4_OK;
 }
 
-int llama_engine_kv(llama_engine *e, int layer, const uint16_t **k, const uint16_t **v, size_t *count)
+int llama_engine_kv(llama_engine *e, int layer, const void **k, const void **v, size_t *count)
 {
     if (!e || !k || !v || !count) return set_error(RFP4_E_INVALID, "null argument");
     if (layer < 0 || (uint32_t)layer >= e->c.n_layers) return set_error(RFP4_E_INVALID, "bad layer");
-    size_t per = (size_t)e->c.n_kv_heads * e->max_seq_alloc * e->c.head_dim;
-    *k = e->kcache + (size_t)layer * per;
-    *v = e->vcache + (size_t)layer * per;
-    *count = per;
+    *k = kv_layer(e, (uint32_t)layer, 0);
+    *v = kv_layer(e, (uint32_t)layer, 1);
+    *count = (size_t)e->c.n_kv_heads * e->max_seq_alloc * e->c.head_dim;
     return RFP4_OK;
 }
 
@@ -805,6 +1015,8 @@ int llama_engine_prefill(llama_engine *e, const uint32_t *prompt, uint32_t n_pro
                          c.max_seq);
     if (c.dim % 256u || qdim(c) % 256u || c.ffn % 256u)
         return set_error(RFP4_E_SHAPE, "prefill runs on the MXFP4 GEMM: dim, n_heads*head_dim and ffn must be multiples of 256");
+    if (c.scale_format != RFP4_SCALE_E8M0 || c.kv_format != RFP4_KV_F16)
+        return set_error(RFP4_E_SHAPE, "prefill runs on the MXFP4 GEMM: it needs E8M0 weights and fp16 caches");
     for (uint32_t i = 0; i < n_prompt; i++)
         if (prompt[i] >= c.vocab) return set_error(RFP4_E_INVALID, "prompt token %u out of range", prompt[i]);
     int rc = prefill_reserve(e, n_prompt);
@@ -871,13 +1083,14 @@ int llama_engine_load(const char *path, uint32_t max_seq, llama_engine **out)
     uint32_t version = 0, half = 0, count = 0;
     rfp4_model_config cfg{};
     bool ok = fread(magic, 1, 8, fp) == 8 && memcmp(magic, kPackMagic, 8) == 0 && fread(&version, 4, 1, fp) == 1 &&
-              version == kPackVersion && fread(&half, 4, 1, fp) == 1 && half <= 1 &&
+              (version == 1 || version == kPackVersion) && fread(&half, 4, 1, fp) == 1 && half <= 1 &&
               fread(&cfg, sizeof cfg, 1, fp) == 1 && fread(&count, 4, 1, fp) == 1;
     if (!ok) {
         fclose(fp);
         return set_error(RFP4_E_SHAPE, "llama_engine_load: %s is not a packed engine (version %u)", path, kPackVersion);
     }
     cfg.max_seq = max_seq;
+    if (version == 1) cfg.scale_format = cfg.kv_format = 0;
     llama_engine *e = nullptr;
     int rc = engine_alloc(&cfg, &e);
     if (rc) {
@@ -926,7 +1139,7 @@ uint64_t llama_engine_weight_bytes(const llama_engine *e)
     uint64_t per_layer = (uint64_t)(qdim(c) + 2 * kvdim(c)) * c.dim + (uint64_t)c.dim * qdim(c) +
                          3ull * c.ffn * c.dim;
     uint64_t elems = per_layer * c.n_layers + (uint64_t)c.vocab * c.dim;
-    return elems / 2 + elems / 32;
+    return elems / 2 + elems / 32 * e->sb;
 }
 
 } // extern "C"

@@ -4,8 +4,6 @@
 // value (shared/kernel_args.h).
 #include "device/common.h"
 #include "device/gemv.h"
-#include "device/gemv_mfma.h"
-#include "device/gemv_mx.h"
 #include "device/norm_rope.h"
 #include "device/attn.h"
 #include "device/misc.h"
@@ -58,70 +56,32 @@ GEMV_KERNEL_OCC4(e8m0, 0, swiglu, RFP4_EPI_SWIGLU, 4, 0)
 GEMV_KERNEL_OCC4(e8m0, 0, swiglu, RFP4_EPI_SWIGLU, 4, 1)
 GEMV_KERNEL_OCC4(e8m0, 0, swiglu, RFP4_EPI_SWIGLU, 4, 2)
 GEMV_KERNEL(e8m0, 0, swiglu, RFP4_EPI_SWIGLU, 4, 3) // 128 VGPRs would spill
-GEMV_NS_FULL(f32, 1, store, RFP4_EPI_STORE, 4)
-// 8 waves per workgroup for one-slice shapes (K <= 2048), test-selectable:
-// alone faster (TinyLlama gate|up 6.18 -> 5.42 us at 1 row per wave), inside
-// the decode step slower; at K = 4096 and 14336 slower alone too (runtime.cpp
-// gemv_variant).  rfp4_gemv_e8m0_<epilogue>_r<R>_s<NS>_w<W>
-#define GEMV_KERNEL_W(ENAME, EPI, R, NS, W) \
-    extern "C" __global__ __launch_bounds__(64 * W) void rfp4_gemv_e8m0_##ENAME##_r##R##_s##NS##_w##W(GemvArgs a) \
+// f32 per-32 scales (the reference's format, fp4_gemv/src/main.rs:32-92):
+// the variants the planner picks (runtime.cpp gemv_variant)
+GEMV_NS_FULL(f32, 1, store, RFP4_EPI_STORE, 2)
+GEMV_NS_SHORT(f32, 1, store, RFP4_EPI_STORE, 8)
+GEMV_NS_FULL(f32, 1, resid, RFP4_EPI_RESIDUAL, 2)
+GEMV_NS_SHORT(f32, 1, resid, RFP4_EPI_RESIDUAL, 8)
+GEMV_NS_FULL(f32, 1, argmax, RFP4_EPI_ARGMAX, 2)
+GEMV_NS_SHORT(f32, 1, argmax, RFP4_EPI_ARGMAX, 8)
+GEMV_NS_FULL(f32, 1, swiglu, RFP4_EPI_SWIGLU, 1)
+// 8 waves per workgroup for one-slice shapes (K <= 2048), the default there
+// (runtime.cpp gemv_variant): TinyLlama decode 1811 -> 1836 tok/s; at K = 4096
+// and 14336 slower.  rfp4_gemv_<scale>_<epilogue>_r<R>_s<NS>_w<W>
+#define GEMV_KERNEL_W(SNAME, SF32, ENAME, EPI, R, NS, W)                                                         \
+    extern "C" __global__ __launch_bounds__(64 * W) void rfp4_gemv_##SNAME##_##ENAME##_r##R##_s##NS##_w##W(GemvArgs a) \
     {                                                                                                           \
-        gemv_body<0, EPI, R, NS, W>(a);                                                                         \
+        gemv_body<SF32, EPI, R, NS, W>(a);                                                                      \
     }
-GEMV_KERNEL_W(swiglu, RFP4_EPI_SWIGLU, 1, 1, 8)
-GEMV_KERNEL_W(store, RFP4_EPI_STORE, 2, 1, 8)
-
-// ---- block-scaled MFMA GEMV: rfp4_gemvx_<epilogue>_n<NORM>_p<PER>
-// (E2M1 weights straight into v_mfma_scale_f32_16x16x128_f8f6f4, x as E4M3
-// planes; PER = ceil(K / 2048) segments of 512 per wave).  Host selection:
-// runtime.cpp gemv_mx_ok.
-#define GEMVX_KERNEL(ENAME, EPI, NORM, PER) \
-    K256 void rfp4_gemvx_##ENAME##_n##NORM##_p##PER(GemvArgs a) { gemv_mx_body<EPI, NORM, PER>(a); }
-#define GEMVX_PERS(ENAME, EPI, NORM) \
-    GEMVX_KERNEL(ENAME, EPI, NORM, 1) \
-    GEMVX_KERNEL(ENAME, EPI, NORM, 2) \
-    GEMVX_KERNEL(ENAME, EPI, NORM, 3) \
-    GEMVX_KERNEL(ENAME, EPI, NORM, 4) \
-    GEMVX_KERNEL(ENAME, EPI, NORM, 5) \
-    GEMVX_KERNEL(ENAME, EPI, NORM, 6) \
-    GEMVX_KERNEL(ENAME, EPI, NORM, 7)
-GEMVX_PERS(store, RFP4_EPI_STORE, 0)
-GEMVX_PERS(store, RFP4_EPI_STORE, 1)
-GEMVX_PERS(resid, RFP4_EPI_RESIDUAL, 0)
-GEMVX_PERS(swiglu, RFP4_EPI_SWIGLU, 0)
-GEMVX_PERS(swiglu, RFP4_EPI_SWIGLU, 1)
-GEMVX_PERS(argmax, RFP4_EPI_ARGMAX, 0)
-GEMVX_PERS(argmax, RFP4_EPI_ARGMAX, 1)
-
-// ---- MFMA GEMV: rfp4_gemvm_<epilogue>_t<RT>_s<NSC>
-// (RT 16-row tiles per wave, NSC = ceil(K/512) super-chunks per wave issued
-// up front, 0 = loop).  Host selection: runtime.cpp gemv_mfma_has.
-#define GEMVM_KERNEL(ENAME, EPI, RT, NSC) \
-    K256 void rfp4_gemvm_##ENAME##_t##RT##_s##NSC(GemvArgs a) { gemv_mfma_body<EPI, RT, NSC>(a); }
-#define GEMVM_LONG(ENAME, EPI, RT) \
-    GEMVM_KERNEL(ENAME, EPI, RT, 0) \
-    GEMVM_KERNEL(ENAME, EPI, RT, 4) \
-    GEMVM_KERNEL(ENAME, EPI, RT, 8) \
-    GEMVM_KERNEL(ENAME, EPI, RT, 11) \
-    GEMVM_KERNEL(ENAME, EPI, RT, 16) \
-    GEMVM_KERNEL(ENAME, EPI, RT, 28)
-#define GEMVM_SHORT(ENAME, EPI, RT) \
-    GEMVM_KERNEL(ENAME, EPI, RT, 0) \
-    GEMVM_KERNEL(ENAME, EPI, RT, 4) \
-    GEMVM_KERNEL(ENAME, EPI, RT, 8)
-
-GEMVM_LONG(store, RFP4_EPI_STORE, 1)
-GEMVM_SHORT(store, RFP4_EPI_STORE, 2)
-GEMVM_LONG(resid, RFP4_EPI_RESIDUAL, 1)
-GEMVM_SHORT(swiglu, RFP4_EPI_SWIGLU, 1)
-GEMVM_SHORT(argmax, RFP4_EPI_ARGMAX, 1)
-GEMVM_SHORT(argmax, RFP4_EPI_ARGMAX, 2)
+GEMV_KERNEL_W(e8m0, 0, swiglu, RFP4_EPI_SWIGLU, 1, 1, 8)
+GEMV_KERNEL_W(e8m0, 0, store, RFP4_EPI_STORE, 2, 1, 8)
+GEMV_KERNEL_W(f32, 1, swiglu, RFP4_EPI_SWIGLU, 1, 1, 8)
+GEMV_KERNEL_W(f32, 1, store, RFP4_EPI_STORE, 2, 1, 8)
 
 // ---- norm / rope / embed
 K1024 void rfp4_rmsnorm_f32w(RmsnormArgs a) { rmsnorm_body<0>(a); }
 K1024 void rfp4_rmsnorm_f16w(RmsnormArgs a) { rmsnorm_body<1>(a); }
 K256 void rfp4_rope(RopeArgs a) { rope_body(a); }
-K256 void rfp4_rope_append(RopeAppendArgs a) { rope_append_body(a); }
 K256 void rfp4_embed(EmbedArgs a) { embed_body(a); }
 
 // ---- attention: rfp4_attn_hd<HD>_<KV type>_g<query heads per KV head, padded to 1/2/4/8>
@@ -169,7 +129,6 @@ K256 void rfp4_mma16_tile(MmaTileArgs a) { mma16_tile_body(a); }
 K256 void rfp4_mma32_tile(MmaTileArgs a) { mma32_tile_body(a); }
 K256 void rfp4_mma_allones(MmaTileArgs a) { mma_allones_body(a.out); }
 K256 void rfp4_mma_bf16_tile(MmaTileArgs a) { mma_bf16_tile_body(a); }
-K256 void rfp4_selftest_cvt_bf16(SelftestArgs a) { selftest_cvt_bf16_body(a); }
 
 // ---- batched MXFP4 GEMM: rfp4_gemm_<BM>x<BN> (4 waves in WM x WN, wave tile 32FA x 32FB).
 // The host picks among these (runtime.cpp gemm_plan); keep the lists in sync.

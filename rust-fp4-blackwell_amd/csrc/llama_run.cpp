@@ -31,9 +31,9 @@ struct Preset {
 
 // Same shapes as rfp4.py's presets (TinyLlama: llama_run/src/main.rs:318-332).
 const Preset kPresets[] = {
-    {"tinyllama-1.1b", "TinyLlama-1.1B", {2048, 22, 32, 4, 64, 5632, 32000, 0, 10000.0, 1e-5f, 0}},
-    {"llama3-8b", "Llama-3-8B", {4096, 32, 32, 8, 128, 14336, 128256, 0, 500000.0, 1e-5f, 0}},
-    {"llama3.2-1b", "Llama-3.2-1B", {2048, 16, 32, 8, 64, 8192, 128256, 0, 500000.0, 1e-5f, 0}},
+    {"tinyllama-1.1b", "TinyLlama-1.1B", {2048, 22, 32, 4, 64, 5632, 32000, 0, 10000.0, 1e-5f, 0, 0}},
+    {"llama3-8b", "Llama-3-8B", {4096, 32, 32, 8, 128, 14336, 128256, 0, 500000.0, 1e-5f, 0, 0}},
+    {"llama3.2-1b", "Llama-3.2-1B", {2048, 16, 32, 8, 64, 8192, 128256, 0, 500000.0, 1e-5f, 0, 0}},
 };
 
 const uint32_t kMaxSeq = 2048; // MAXSEQ (llama_run/src/main.rs:440)

@@ -3,6 +3,8 @@
 // (include/rfp4.h) over hipModuleLaunchKernel.
 #include "runtime.h"
 
+#include <elf.h>
+
 #include <algorithm>
 #include <cmath>
 #include <cstdarg>
@@ -11,6 +13,16 @@
 #include <mutex>
 #include <string>
 #include <unordered_map>
+#include <vector>
+
+// HIP's launch with start/stop events from the dispatch itself
+// (hip/hip_ext.h; that header also holds device-side templates this g++
+// translation unit cannot compile, so only the declaration is repeated).
+extern "C" hipError_t hipExtModuleLaunchKernel(hipFunction_t f, uint32_t globalWorkSizeX, uint32_t globalWorkSizeY,
+                                               uint32_t globalWorkSizeZ, uint32_t localWorkSizeX,
+                                               uint32_t localWorkSizeY, uint32_t localWorkSizeZ, size_t sharedMemBytes,
+                                               hipStream_t hStream, void **kernelParams, void **extra,
+                                               hipEvent_t startEvent, hipEvent_t stopEvent, uint32_t flags);
 
 extern "C" const unsigned char rfp4_hsaco_start[];
 extern "C" const unsigned char rfp4_hsaco_end[];
@@ -40,23 +52,113 @@ int hip_check(hipError_t e, const char *what)
 
 Runtime *runtime() { return g_rt; }
 
+// Names of every kernel in the embedded code object.  The blob is a clang
+// offload bundle ("__CLANG_OFFLOAD_BUNDLE__", u64 entry count, then per entry
+// u64 offset, u64 size, u64 triple length, triple) whose amdgcn entry is an
+// ELF64 code object; each kernel `k` has a descriptor symbol `k.kd`.  Every
+// offset and size is checked against the blob before it is read.
+static int kernel_names(const unsigned char *blob, size_t len, std::vector<std::string> *out)
+{
+    static const char kMagic[] = "__CLANG_OFFLOAD_BUNDLE__";
+    const size_t mlen = sizeof kMagic - 1;
+    auto rd64 = [&](size_t off, uint64_t *v) {
+        if (off > len || len - off < 8) return false;
+        std::memcpy(v, blob + off, 8);
+        return true;
+    };
+    const unsigned char *elf = nullptr;
+    size_t elf_len = 0;
+    if (len >= mlen && std::memcmp(blob, kMagic, mlen) == 0) {
+        uint64_t n = 0;
+        size_t p = mlen;
+        if (!rd64(p, &n)) return set_error(RFP4_E_HIP, "code object bundle truncated");
+        p += 8;
+        for (uint64_t i = 0; i < n && !elf; i++) {
+            uint64_t off, size, tlen;
+            if (!rd64(p, &off) || !rd64(p + 8, &size) || !rd64(p + 16, &tlen)) return set_error(RFP4_E_HIP, "bundle entry truncated");
+            p += 24;
+            if (tlen > len - std::min(p, len)) return set_error(RFP4_E_HIP, "bundle triple out of range");
+            const std::string triple((const char *)blob + p, (size_t)tlen);
+            p += tlen;
+            if (triple.find("amdgcn") != std::string::npos) {
+                if (off > len || size > len - off) return set_error(RFP4_E_HIP, "bundle entry out of range");
+                elf = blob + off;
+                elf_len = (size_t)size;
+            }
+        }
+    } else {
+        elf = blob;
+        elf_len = len;
+    }
+    if (!elf || elf_len < sizeof(Elf64_Ehdr) || std::memcmp(elf, ELFMAG, SELFMAG) != 0)
+        return set_error(RFP4_E_HIP, "no amdgcn ELF code object in the embedded blob");
+    Elf64_Ehdr eh;
+    std::memcpy(&eh, elf, sizeof eh);
+    if (eh.e_shentsize != sizeof(Elf64_Shdr) || eh.e_shoff > elf_len ||
+        (uint64_t)eh.e_shnum * sizeof(Elf64_Shdr) > elf_len - eh.e_shoff)
+        return set_error(RFP4_E_HIP, "code object section table out of range");
+    auto shdr = [&](uint32_t i) {
+        Elf64_Shdr s;
+        std::memcpy(&s, elf + eh.e_shoff + (size_t)i * sizeof(Elf64_Shdr), sizeof s);
+        return s;
+    };
+    for (uint32_t i = 0; i < eh.e_shnum; i++) {
+        const Elf64_Shdr sh = shdr(i);
+        if (sh.sh_type != SHT_SYMTAB || sh.sh_entsize != sizeof(Elf64_Sym) || sh.sh_link >= eh.e_shnum) continue;
+        const Elf64_Shdr st = shdr(sh.sh_link);
+        if (sh.sh_offset > elf_len || sh.sh_size > elf_len - sh.sh_offset || st.sh_offset > elf_len ||
+            st.sh_size > elf_len - st.sh_offset)
+            return set_error(RFP4_E_HIP, "code object symbol table out of range");
+        const char *strs = (const char *)elf + st.sh_offset;
+        for (uint64_t j = 0; j < sh.sh_size / sizeof(Elf64_Sym); j++) {
+            Elf64_Sym sym;
+            std::memcpy(&sym, elf + sh.sh_offset + j * sizeof(Elf64_Sym), sizeof sym);
+            if (sym.st_name >= st.sh_size) continue;
+            const size_t maxn = (size_t)(st.sh_size - sym.st_name);
+            const size_t nlen = strnlen(strs + sym.st_name, maxn);
+            if (nlen == maxn || nlen < 4) continue; // unterminated or too short for "x.kd"
+            const std::string name(strs + sym.st_name, nlen);
+            if (name.compare(nlen - 3, 3, ".kd") == 0) out->push_back(name.substr(0, nlen - 3));
+        }
+    }
+    if (out->empty()) return set_error(RFP4_E_HIP, "no kernel descriptors in the code object");
+    return RFP4_OK;
+}
+
+// The kernel table is filled once by rfp4_init and read-only afterwards, so
+// launches from several threads (and launches under stream capture) never
+// touch the module or modify the map.
+static thread_local std::vector<KernelTiming> *t_timing = nullptr;
+
+void timing_install(std::vector<KernelTiming> *records) { t_timing = records; }
+
 int launch(const char *name, dim3 grid, dim3 block, hipStream_t s, void *args, unsigned shmem)
 {
     Runtime *rt = g_rt;
     if (!rt) return set_error(RFP4_E_NOT_INIT, "rfp4_init has not been called");
     auto it = rt->fns.find(name);
-    hipFunction_t f = nullptr;
-    if (it == rt->fns.end()) {
-        std::lock_guard<std::mutex> lk(g_mu);
-        hipError_t e = hipModuleGetFunction(&f, rt->module, name);
-        if (e != hipSuccess) return set_error(RFP4_E_HIP, "kernel %s not found: %s", name, hipGetErrorString(e));
-        rt->fns.emplace(name, f);
-    } else {
-        f = it->second;
-    }
+    if (it == rt->fns.end()) return set_error(RFP4_E_HIP, "kernel %s is not in the code object", name);
     if (grid.x == 0 || grid.y == 0 || grid.z == 0) return RFP4_OK; // nothing to do
     void *params[] = {args};
-    return hip_check(hipModuleLaunchKernel(f, grid.x, grid.y, grid.z, block.x, block.y, block.z, shmem, s, params, nullptr),
+    if (t_timing) {
+        KernelTiming k{it->first.c_str(), nullptr, nullptr};
+        int rc = hip_check(hipEventCreate(&k.start), "hipEventCreate");
+        if (!rc) rc = hip_check(hipEventCreate(&k.stop), "hipEventCreate");
+        if (!rc)
+            rc = hip_check(hipExtModuleLaunchKernel(it->second, grid.x * block.x, grid.y * block.y, grid.z * block.z,
+                                                    block.x, block.y, block.z, shmem, s, params, nullptr, k.start,
+                                                    k.stop, 0),
+                           name);
+        if (rc) {
+            if (k.start) hipEventDestroy(k.start);
+            if (k.stop) hipEventDestroy(k.stop);
+            return rc;
+        }
+        t_timing->push_back(k);
+        return RFP4_OK;
+    }
+    return hip_check(hipModuleLaunchKernel(it->second, grid.x, grid.y, grid.z, block.x, block.y, block.z, shmem, s,
+                                           params, nullptr),
                      name);
 }
 
@@ -68,6 +170,27 @@ extern "C" {
 
 const char *rfp4_last_error(void) { return t_err.c_str(); }
 int rfp4_version(void) { return 1; }
+
+int rfp4_kernel_count(uint32_t *count)
+{
+    if (!count) return set_error(RFP4_E_INVALID, "null count");
+    std::vector<std::string> names;
+    int rc = kernel_names(rfp4_hsaco_start, (size_t)(rfp4_hsaco_end - rfp4_hsaco_start), &names);
+    *count = rc ? 0u : (uint32_t)names.size();
+    return rc;
+}
+
+int rfp4_kernel_name(uint32_t i, char *buf, size_t cap)
+{
+    if (!buf || cap == 0) return set_error(RFP4_E_INVALID, "null buffer");
+    std::vector<std::string> names;
+    int rc = kernel_names(rfp4_hsaco_start, (size_t)(rfp4_hsaco_end - rfp4_hsaco_start), &names);
+    if (rc) return rc;
+    if (i >= names.size()) return set_error(RFP4_E_INVALID, "kernel index %u >= %zu", i, names.size());
+    if (names[i].size() + 1 > cap) return set_error(RFP4_E_CAPACITY, "name of kernel %u needs %zu bytes", i, names[i].size() + 1);
+    std::memcpy(buf, names[i].c_str(), names[i].size() + 1);
+    return RFP4_OK;
+}
 
 int rfp4_device_count(int *count)
 {
@@ -100,6 +223,19 @@ int rfp4_init(int device)
     rt->max_lds = (size_t)prop.sharedMemPerBlock;
     rc = hip_check(hipModuleLoadData(&rt->module, rfp4_hsaco_start), "hipModuleLoadData");
     if (rc) {
+        delete rt;
+        return rc;
+    }
+    // every kernel handle now: the table is read-only from here on
+    std::vector<std::string> names;
+    rc = kernel_names(rfp4_hsaco_start, (size_t)(rfp4_hsaco_end - rfp4_hsaco_start), &names);
+    for (size_t i = 0; i < names.size() && !rc; i++) {
+        hipFunction_t f = nullptr;
+        rc = hip_check(hipModuleGetFunction(&f, rt->module, names[i].c_str()), names[i].c_str());
+        if (!rc) rt->fns.emplace(names[i], f);
+    }
+    if (rc) {
+        hipModuleUnload(rt->module);
         delete rt;
         return rc;
     }
@@ -236,19 +372,22 @@ int gemv_check(uint32_t n, uint32_t k, const void *w, const void *sc, const floa
 // Forced variant for tests (0 = automatic); thread-local like the error text.
 static thread_local int t_force_r = 0, t_force_ns = -1, t_force_w = 0;
 
-// Compiled (R, NS) variants; must match the table in kernels.hip.
+// Compiled (R, NS, W) variants; must match the table in kernels.hip.  E8M0
+// scales have every variant the tests force; f32 scales the planner's own.
 static bool gemv_has_ns(bool f32scale, int epi, int R, int ns, int W = 4)
 {
     if (W != 4) // 8-wave workgroups: one-slice SwiGLU at R = 1, store at R = 2
-        return !f32scale && W == 8 && ns == 1 &&
-               ((epi == RFP4_EPI_SWIGLU && R == 1) || (epi == RFP4_EPI_STORE && R == 2));
-    if (ns == 0) return true;
-    bool full = ns == 1 || ns == 2 || ns == 3 || ns == 4 || ns == 7;
-    if (f32scale) return R == 4 && full;
+        return W == 8 && ns == 1 && ((epi == RFP4_EPI_SWIGLU && R == 1) || (epi == RFP4_EPI_STORE && R == 2));
+    const bool full = ns == 0 || ns == 1 || ns == 2 || ns == 3 || ns == 4 || ns == 7;
+    const bool shrt = ns == 0 || ns == 1 || ns == 2;
+    if (f32scale) {
+        if (epi == RFP4_EPI_SWIGLU) return R == 1 && full;
+        return R == 2 ? full : (R == 8 && shrt);
+    }
     if (R == 1) return epi != RFP4_EPI_ARGMAX && full;
     if (R == 2) return full;
-    if (R == 4) return epi == RFP4_EPI_SWIGLU ? (ns >= 1 && ns <= 3) : full;
-    if (R == 8) return epi != RFP4_EPI_SWIGLU && (ns == 1 || ns == 2);
+    if (R == 4) return epi == RFP4_EPI_SWIGLU ? (ns >= 0 && ns <= 3) : full;
+    if (R == 8) return epi != RFP4_EPI_SWIGLU && shrt;
     return false;
 }
 
@@ -259,16 +398,14 @@ static bool gemv_has_ns(bool f32scale, int epi, int R, int ns, int W = 4)
 // 12.7 us vs 12.9-13.6 at R = 2 and 17.3 at R = 4), R = 2 elsewhere (8B down
 // 9.5 us vs 11.1 at R = 4 and 10.6 at R = 1; q|k|v 5.0 vs 5.2-5.4; TinyLlama
 // LM head 7.9-8.1 vs 8.3 at R = 4), R = 8 for very wide matrices with short
-// K (8B LM head).  f32 scales: R = 4 only.
+// K (8B LM head).  The same choices for f32 scales.
 GemvVariant gemv_variant(uint32_t n, uint32_t k, int epi, bool f32scale)
 {
     int ns_needed = (int)((k + 2047u) / 2048u);
-    int R = 4;
-    if (!f32scale) {
-        if (epi == RFP4_EPI_SWIGLU) R = gemv_has_ns(f32scale, epi, 1, ns_needed) ? 1 : 2;
-        else if (n >= 65536u && ns_needed <= 2) R = 8;
-        else R = 2;
-    }
+    int R;
+    if (epi == RFP4_EPI_SWIGLU) R = (f32scale || gemv_has_ns(f32scale, epi, 1, ns_needed)) ? 1 : 2;
+    else if (n >= 65536u && ns_needed <= 2) R = 8;
+    else R = 2;
     // 8 waves per workgroup where compiled (one-slice SwiGLU at R = 1, store
     // at R = 2: K <= 2048), else 4.  Measured in the TinyLlama decode step:
     // 1811 -> 1836 tok/s (gate|up, q|k|v and the LM head on 8 waves).
@@ -305,139 +442,30 @@ bool attn_inmerge(uint32_t max_splits)
     return t_attn_merge != 1;
 }
 
-// Path: 0 = automatic, 1 = VALU kernel, 2 = bf16 MFMA kernel, 3 = block-scaled
-// MFMA kernel (forced paths: tests only).
-static thread_local int t_force_path = 0;
-
-// Block-scaled MFMA kernel (gemv_mx.h): E8M0 weight scales, K in whole
-// 512-value segments, at most 7 segments per wave (K <= 14336) and the E4M3
-// planes of x in LDS.
-constexpr uint32_t kGemvMxPlanes = 6;
-static bool gemv_mx_ok(uint32_t k, bool f32scale)
-{
-    if (f32scale || k % 512u || k > 7u * 2048u) return false;
-    return !g_rt || (size_t)k * kGemvMxPlanes + (k / 32u) * kGemvMxPlanes + 1024u <= g_rt->max_lds;
-}
-
-// The MFMA kernel needs E8M0 scales (folded into the bf16 conversion), K in
-// whole 128-value super-chunks and the three bf16 planes of x in LDS.
-static bool gemv_mfma_ok(uint32_t k, bool f32scale)
-{
-    if (f32scale || k % 128u) return false;
-    return !g_rt || (size_t)k * 6u + 2048u <= g_rt->max_lds;
-}
-
-// Compiled MFMA variants; must match the table in kernels.hip.
-static bool gemv_mfma_has(int epi, int rt, int nsc)
-{
-    bool lng = nsc == 0 || nsc == 4 || nsc == 8 || nsc == 11 || nsc == 16 || nsc == 28;
-    bool sht = nsc == 0 || nsc == 4 || nsc == 8;
-    switch (epi) {
-    case RFP4_EPI_STORE: return rt == 1 ? lng : (rt == 2 && sht);
-    case RFP4_EPI_RESIDUAL: return rt == 1 && lng;
-    case RFP4_EPI_SWIGLU: return rt == 1 && sht;
-    default: return (rt == 1 || rt == 2) && sht;
-    }
-}
-
-struct GemvPlan {
-    bool mfma, mx;
-    int R, NS, W = 4;               // VALU: rows per wave, K slices; MFMA: 16-row tiles, super-chunks per wave
-    uint32_t rows_per_block;
-};
-
-static GemvPlan gemv_plan(uint32_t n, uint32_t k, int epi, bool f32scale)
-{
-    GemvPlan p{};
-    // Measured on MI355X (batch 1, weights streamed from HBM): the VALU
-    // kernel with registers-first staging beats the matrix-core kernel on
-    // every decode shape (e.g. 128256x4096: 50.6 vs 69.5 us), because the
-    // matrix-core path must also convert x into three bf16 planes per
-    // workgroup.  The matrix-core kernel stays selectable (path 2).
-    p.mfma = t_force_path == 2;
-    p.mx = t_force_path == 3;
-    if (p.mx) {
-        p.R = 1;
-        p.NS = (int)((k + 2047u) / 2048u);
-        p.rows_per_block = 16u;
-    } else if (p.mfma) {
-        int rt = ((epi == RFP4_EPI_STORE || epi == RFP4_EPI_ARGMAX) && n >= 65536u) ? 2 : 1;
-        if (t_force_path == 2 && t_force_r) rt = t_force_r;
-        int per_wave = (int)(((k >> 7) + 3u) / 4u);
-        int ns = gemv_mfma_has(epi, rt, per_wave) ? per_wave : 0;
-        if (t_force_path == 2 && t_force_ns >= 0) ns = t_force_ns;
-        p.R = rt;
-        p.NS = ns;
-        p.rows_per_block = 16u * (uint32_t)rt;
-    } else {
-        GemvVariant v = gemv_variant(n, k, epi, f32scale);
-        p.R = v.R;
-        p.NS = v.NS;
-        p.W = v.W;
-        p.rows_per_block = (uint32_t)v.W * (uint32_t)v.R;
-    }
-    return p;
-}
-
-int gemv_launch(const char *scale_name, int epi, const GemvArgs &args, hipStream_t s, int r_override)
+int gemv_launch_v(const char *scale_name, int epi, const GemvArgs &args, hipStream_t s, const GemvVariant &v)
 {
     static const char *epi_names[] = {"store", "resid", "swiglu", "argmax"};
     const bool f32scale = scale_name[0] == 'f';
-    GemvPlan p = gemv_plan(args.n, args.k, epi, f32scale);
+    if (!gemv_has_ns(f32scale, epi, v.R, v.NS, v.W))
+        return set_error(RFP4_E_INVALID, "gemv: no compiled variant R=%d NS=%d W=%d for %s/%s", v.R, v.NS, v.W,
+                         scale_name, epi_names[epi]);
+    if (v.NS > 0 && (uint32_t)v.NS * 2048u < args.k)
+        return set_error(RFP4_E_INVALID, "gemv: NS=%d slices cannot cover k=%u", v.NS, args.k);
     char name[64];
-    unsigned shmem;
-    if (p.mx) {
-        if (!gemv_mx_ok(args.k, f32scale))
-            return set_error(RFP4_E_INVALID, "gemv: block-scaled MFMA path needs E8M0 scales and k %% 512 == 0, "
-                                             "k <= 14336 (k=%u)", args.k);
-        if ((uintptr_t)args.scales % 4u) return set_error(RFP4_E_ALIGN, "gemv: block-scaled MFMA path needs 4-byte aligned scales");
-        if (epi == RFP4_EPI_RESIDUAL && args.norm_w)
-            return set_error(RFP4_E_INVALID, "gemv: no block-scaled MFMA variant of the residual GEMV with a norm");
-        snprintf(name, sizeof name, "rfp4_gemvx_%s_n%d_p%d", epi_names[epi], args.norm_w ? 1 : 0, p.NS);
-        shmem = args.k * kGemvMxPlanes + (args.k / 32u) * kGemvMxPlanes;
-    } else if (p.mfma) {
-        if (!gemv_mfma_ok(args.k, f32scale))
-            return set_error(RFP4_E_INVALID, "gemv: MFMA path needs E8M0 scales and k %% 128 == 0 (k=%u)", args.k);
-        if (!gemv_mfma_has(epi, p.R, p.NS) || (p.NS != 0 && p.NS != (int)(((args.k >> 7) + 3u) / 4u)))
-            return set_error(RFP4_E_INVALID, "gemv: no MFMA variant RT=%d NSC=%d for %s, k=%u", p.R, p.NS,
-                             epi_names[epi], args.k);
-        snprintf(name, sizeof name, "rfp4_gemvm_%s_t%d_s%d", epi_names[epi], p.R, p.NS);
-        shmem = args.k * 6u;
-    } else {
-        if (r_override) p.R = r_override, p.rows_per_block = (uint32_t)p.W * (uint32_t)r_override;
-        if (!gemv_has_ns(f32scale, epi, p.R, p.NS, p.W))
-            return set_error(RFP4_E_INVALID, "gemv: no compiled variant R=%d NS=%d W=%d for %s/%s", p.R, p.NS, p.W,
-                             scale_name, epi_names[epi]);
-        if (p.NS > 0 && (uint32_t)p.NS * 2048u < args.k)
-            return set_error(RFP4_E_INVALID, "gemv: NS=%d slices cannot cover k=%u", p.NS, args.k);
-        if (p.W == 4)
-            snprintf(name, sizeof name, "rfp4_gemv_%s_%s_r%d_s%d", scale_name, epi_names[epi], p.R, p.NS);
-        else
-            snprintf(name, sizeof name, "rfp4_gemv_%s_%s_r%d_s%d_w%d", scale_name, epi_names[epi], p.R, p.NS, p.W);
-        shmem = gemv_lds_bytes(args.k);
-    }
-    uint32_t blocks = (args.n + p.rows_per_block - 1) / p.rows_per_block;
+    if (v.W == 4)
+        snprintf(name, sizeof name, "rfp4_gemv_%s_%s_r%d_s%d", scale_name, epi_names[epi], v.R, v.NS);
+    else
+        snprintf(name, sizeof name, "rfp4_gemv_%s_%s_r%d_s%d_w%d", scale_name, epi_names[epi], v.R, v.NS, v.W);
     GemvArgs a = args;
-    const uint32_t threads = (p.mx || p.mfma) ? 256u : 64u * (uint32_t)p.W;
-    return launch(name, dim3(blocks), dim3(threads), s, &a, shmem);
+    return launch(name, dim3(gemv_grid(args.n, v)), dim3(64u * (uint32_t)v.W), s, &a, gemv_lds_bytes(args.k));
 }
 
-uint32_t gemv_blocks(uint32_t n_logical, uint32_t k, int epi)
+int gemv_launch(const char *scale_name, int epi, const GemvArgs &args, hipStream_t s)
 {
-    GemvPlan p = gemv_plan(n_logical, k, epi, false);
-    return (n_logical + p.rows_per_block - 1) / p.rows_per_block;
+    return gemv_launch_v(scale_name, epi, args, s, gemv_variant(args.n, args.k, epi, scale_name[0] == 'f'));
 }
 
 } // namespace rfp4
-
-extern "C" int rfp4_debug_gemv_path(int path)
-{
-    using namespace rfp4;
-    if (path < 0 || path > 3)
-        return set_error(RFP4_E_INVALID, "path must be 0 (auto), 1 (VALU), 2 (bf16 MFMA) or 3 (block-scaled MFMA)");
-    t_force_path = path;
-    return RFP4_OK;
-}
 
 extern "C" int rfp4_debug_attn_merge(int mode)
 {
@@ -503,7 +531,6 @@ int attn_launch(const AttnArgs &args, int kv_f16, hipStream_t s, uint32_t max_se
     snprintf(name, sizeof name, "rfp4_attn_hd%u_%s_g%u", args.head_dim, kv_f16 ? "f16" : "f32",
              attn_group_pad(args.n_heads / args.n_kv_heads));
     if (args.chunk == 0) return set_error(RFP4_E_INVALID, "attn: chunk must be positive");
-    if (args.cosv && !kv_f16) return set_error(RFP4_E_INVALID, "attn: fused KV append needs an fp16 cache");
     if (rows == 0 || (rows > 1 && args.cosv)) return set_error(RFP4_E_INVALID, "attn: fused append is one row only");
     uint32_t splits = (max_seq_for_grid + args.chunk - 1) / args.chunk;
     if (splits > args.max_splits) return set_error(RFP4_E_INVALID, "attn: %u splits exceed the workspace's %u", splits, args.max_splits);
@@ -597,7 +624,7 @@ int fp4_gemv(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint32_t *w, co
     int rc = gemv_check(n, k, w, scales, x, y);
     if (rc) return rc;
     GemvArgs a{w, scales, x, y, nullptr, nullptr, n, k, 0, 0.0f};
-    return gemv_launch("f32", RFP4_EPI_STORE, a, (hipStream_t)stream, 0);
+    return gemv_launch("f32", RFP4_EPI_STORE, a, (hipStream_t)stream);
 }
 
 int mx4_gemv(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_t *codes, const uint8_t *scales,
@@ -606,7 +633,7 @@ int mx4_gemv(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_t *codes,
     int rc = gemv_check(n, k, codes, scales, x, y);
     if (rc) return rc;
     GemvArgs a{codes, scales, x, y, nullptr, nullptr, n, k, 0, 0.0f};
-    return gemv_launch("e8m0", RFP4_EPI_STORE, a, (hipStream_t)stream, 0);
+    return gemv_launch("e8m0", RFP4_EPI_STORE, a, (hipStream_t)stream);
 }
 
 int mx4_gemv_rmsnorm(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_t *codes, const uint8_t *scales,
@@ -616,7 +643,7 @@ int mx4_gemv_rmsnorm(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_t
     if (rc) return rc;
     if (!norm_w) return set_error(RFP4_E_INVALID, "gemv_rmsnorm: null norm weights");
     GemvArgs a{codes, scales, x, y, nullptr, norm_w, n, k, 0, eps};
-    return gemv_launch("e8m0", RFP4_EPI_STORE, a, (hipStream_t)stream, 0);
+    return gemv_launch("e8m0", RFP4_EPI_STORE, a, (hipStream_t)stream);
 }
 
 int mx4_gemv_residual(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_t *codes, const uint8_t *scales,
@@ -625,7 +652,7 @@ int mx4_gemv_residual(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_
     int rc = gemv_check(n, k, codes, scales, x, x_res);
     if (rc) return rc;
     GemvArgs a{codes, scales, x, x_res, nullptr, nullptr, n, k, 0, 0.0f};
-    return gemv_launch("e8m0", RFP4_EPI_RESIDUAL, a, (hipStream_t)stream, 0);
+    return gemv_launch("e8m0", RFP4_EPI_RESIDUAL, a, (hipStream_t)stream);
 }
 
 int mx4_gemv_swiglu(rfp4_stream_t stream, uint32_t n, uint32_t k, uint32_t pair_off, const uint8_t *codes,
@@ -635,10 +662,29 @@ int mx4_gemv_swiglu(rfp4_stream_t stream, uint32_t n, uint32_t k, uint32_t pair_
     if (rc) return rc;
     if (pair_off < n) return set_error(RFP4_E_SHAPE, "gemv_swiglu: pair_off %u overlaps the %u gate rows", pair_off, n);
     GemvArgs a{codes, scales, x, out, nullptr, nullptr, n, k, pair_off, 0.0f};
-    return gemv_launch("e8m0", RFP4_EPI_SWIGLU, a, (hipStream_t)stream, 0);
+    return gemv_launch("e8m0", RFP4_EPI_SWIGLU, a, (hipStream_t)stream);
 }
 
 size_t mx4_gemv_argmax_workspace(uint32_t n) { return ((size_t)n + 7u) / 8u * 8u + 64u; /* >= one key per 8 rows */ }
+
+// The per-workgroup keys of an argmax GEMV, then the step kernel's reduction
+// on a scratch cursor after the keys (ids_cap = 0: no ids are written).
+static int gemv_argmax_launch(hipStream_t s, const char *sname, const GemvArgs &args, void *workspace,
+                              uint32_t *best_token)
+{
+    const GemvVariant v = gemv_variant(args.n, args.k, RFP4_EPI_ARGMAX, sname[0] == 'f');
+    const uint32_t nb = gemv_grid(args.n, v);
+    if ((size_t)nb * 8u + sizeof(StepState) > mx4_gemv_argmax_workspace(args.n))
+        return set_error(RFP4_E_CAPACITY, "gemv_argmax: %u workgroup keys exceed the workspace of %zu bytes", nb,
+                         mx4_gemv_argmax_workspace(args.n));
+    int rc = gemv_launch_v(sname, RFP4_EPI_ARGMAX, args, s, v);
+    if (rc) return rc;
+    StepState *st = (StepState *)((char *)workspace + (size_t)nb * 8u);
+    rc = fill_words((uint32_t *)st, sizeof(StepState) / 4, 0u, s);
+    if (rc) return rc;
+    StepArgs sa{args.best, st, nullptr, best_token, nb, 0};
+    return launch("rfp4_step", dim3(1), dim3(1024), s, &sa);
+}
 
 int mx4_gemv_argmax(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_t *codes, const uint8_t *scales,
                     const float *x, float *y, void *workspace, uint32_t *best_token)
@@ -646,39 +692,27 @@ int mx4_gemv_argmax(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_t 
     int rc = gemv_check(n, k, codes, scales, x, y);
     if (rc) return rc;
     if (!workspace || !best_token) return set_error(RFP4_E_INVALID, "gemv_argmax: null workspace or output");
-    unsigned long long *best = (unsigned long long *)workspace;
-    GemvArgs a{codes, scales, x, y, best, nullptr, n, k, 0, 0.0f};
-    rc = gemv_launch("e8m0", RFP4_EPI_ARGMAX, a, (hipStream_t)stream, 0);
-    if (rc) return rc;
-    // reduce the per-workgroup keys with the step kernel on a scratch cursor
-    // that lives after the keys (no ids are written: ids_cap = 0).
-    uint32_t nb = gemv_blocks(n, k, RFP4_EPI_ARGMAX);
-    StepState *st = (StepState *)((char *)workspace + (size_t)nb * 8u);
-    rc = fill_words((uint32_t *)st, sizeof(StepState) / 4, 0u, (hipStream_t)stream);
-    if (rc) return rc;
-    StepArgs sa{best, st, nullptr, best_token, nb, 0};
-    return launch("rfp4_step", dim3(1), dim3(1024), (hipStream_t)stream, &sa);
+    GemvArgs a{codes, scales, x, y, (unsigned long long *)workspace, nullptr, n, k, 0, 0.0f};
+    return gemv_argmax_launch((hipStream_t)stream, "e8m0", a, workspace, best_token);
 }
 
-int rfp4_debug_gemv_fused(rfp4_stream_t stream, int epi, uint32_t n, uint32_t k, uint32_t pair_off,
-                          const uint8_t *codes, const uint8_t *scales, const float *x, const uint16_t *norm_w,
+int rfp4_debug_gemv_fused(rfp4_stream_t stream, int epi, int scale_format, uint32_t n, uint32_t k, uint32_t pair_off,
+                          const uint8_t *codes, const void *scales, const float *x, const uint16_t *norm_w,
                           float eps, float *y, void *workspace, uint32_t *best_token)
 {
     int rc = gemv_check(n, k, codes, scales, x, y);
     if (rc) return rc;
     if (epi < RFP4_EPI_STORE || epi > RFP4_EPI_ARGMAX) return set_error(RFP4_E_INVALID, "gemv_fused: bad epilogue %d", epi);
+    if (scale_format != RFP4_SCALE_E8M0 && scale_format != RFP4_SCALE_F32)
+        return set_error(RFP4_E_INVALID, "gemv_fused: bad scale format %d", scale_format);
     if (epi == RFP4_EPI_ARGMAX && (!workspace || !best_token))
         return set_error(RFP4_E_INVALID, "gemv_fused: argmax needs a workspace and an output");
-    unsigned long long *best = (unsigned long long *)workspace;
-    GemvArgs a{codes, scales, x, y, best, norm_w, n, k, pair_off, eps};
-    rc = gemv_launch("e8m0", epi, a, (hipStream_t)stream, 0);
-    if (rc || epi != RFP4_EPI_ARGMAX) return rc;
-    uint32_t nb = gemv_blocks(n, k, RFP4_EPI_ARGMAX);
-    StepState *st = (StepState *)((char *)workspace + (size_t)nb * 8u);
-    rc = fill_words((uint32_t *)st, sizeof(StepState) / 4, 0u, (hipStream_t)stream);
-    if (rc) return rc;
-    StepArgs sa{best, st, nullptr, best_token, nb, 0};
-    return launch("rfp4_step", dim3(1), dim3(1024), (hipStream_t)stream, &sa);
+    if (epi == RFP4_EPI_SWIGLU && pair_off < n)
+        return set_error(RFP4_E_SHAPE, "gemv_fused: pair_off %u overlaps the %u gate rows", pair_off, n);
+    const char *sname = scale_format == RFP4_SCALE_F32 ? "f32" : "e8m0";
+    GemvArgs a{codes, scales, x, y, (unsigned long long *)workspace, norm_w, n, k, pair_off, eps};
+    if (epi == RFP4_EPI_ARGMAX) return gemv_argmax_launch((hipStream_t)stream, sname, a, workspace, best_token);
+    return gemv_launch(sname, epi, a, (hipStream_t)stream);
 }
 
 int rmsnorm(rfp4_stream_t stream, uint32_t dim, float eps, const float *x, const float *weight, float *y)
@@ -980,6 +1014,17 @@ extern "C" {
 int fp4_gemm(rfp4_stream_t stream, uint32_t m, uint32_t n, uint32_t k, const uint8_t *a_codes,
              const uint8_t *a_scales, const uint8_t *w_codes, const uint8_t *w_scales, float *c)
 {
+    return gemm_launch((hipStream_t)stream, m, n, k, a_codes, a_scales, w_codes, w_scales, c,
+                       g_rt ? g_rt->gemm_part : nullptr);
+}
+
+} // extern "C"
+
+namespace rfp4 {
+
+int gemm_launch(hipStream_t stream, uint32_t m, uint32_t n, uint32_t k, const uint8_t *a_codes, const uint8_t *a_scales,
+                const uint8_t *w_codes, const uint8_t *w_scales, float *c, float *part)
+{
     if (!a_codes || !a_scales || !w_codes || !w_scales || !c) return set_error(RFP4_E_INVALID, "fp4_gemm: null pointer");
     if (m == 0 || n == 0 || k == 0) return set_error(RFP4_E_SHAPE, "fp4_gemm: empty shape m=%u n=%u k=%u", m, n, k);
     if (k % 256u) return set_error(RFP4_E_SHAPE, "fp4_gemm: k=%u must be a multiple of 256", k);
@@ -1004,13 +1049,18 @@ int fp4_gemm(rfp4_stream_t stream, uint32_t m, uint32_t n, uint32_t k, const uin
     if (p.kz > 1 && (uint64_t)p.kz * m * n > kGemmPartFloats)
         return set_error(RFP4_E_CAPACITY, "fp4_gemm: split-K partials %u x %u x %u exceed the workspace", p.kz, m, n);
     if (tiles * p.kz > 0x7FFFFFFFull) return set_error(RFP4_E_SHAPE, "fp4_gemm: grid too large");
-    GemmArgs a{a_codes, a_scales, w_codes, w_scales, c, rt->gemm_part, m, n, k, p.kz};
+    if (p.kz > 1 && !part) return set_error(RFP4_E_INVALID, "fp4_gemm: split-K plan without a workspace");
+    GemmArgs a{a_codes, a_scales, w_codes, w_scales, c, part, m, n, k, p.kz};
     int rc = launch(t.name, dim3((unsigned)(tiles * p.kz)), dim3(256), (hipStream_t)stream, &a);
     if (rc || p.kz == 1) return rc;
     const uint64_t n4 = (uint64_t)m * n / 4u;
     return launch("rfp4_gemm_reduce", dim3((unsigned)std::min<uint64_t>((n4 + 255u) / 256u, 8192u)), dim3(256),
                   (hipStream_t)stream, &a);
 }
+
+} // namespace rfp4
+
+extern "C" {
 
 int rfp4_debug_attn_chunk(uint32_t chunk)
 {
@@ -1060,14 +1110,6 @@ int rfp4_selftest_cvt_fp4(rfp4_stream_t stream, uint32_t n, const uint32_t *word
     if (!words || !out) return set_error(RFP4_E_INVALID, "selftest_cvt: null pointer");
     SelftestArgs a{words, out, nullptr, n, 0};
     return launch("rfp4_selftest_cvt", dim3((n + 255) / 256), dim3(256), (hipStream_t)stream, &a);
-}
-
-int rfp4_selftest_cvt_bf16(rfp4_stream_t stream, uint32_t n, const uint32_t *words, const float *scales,
-                           uint32_t *out)
-{
-    if (!words || !scales || !out) return set_error(RFP4_E_INVALID, "selftest_cvt_bf16: null pointer");
-    SelftestArgs a{words, (float *)out, scales, n, 0};
-    return launch("rfp4_selftest_cvt_bf16", dim3((n + 255) / 256), dim3(256), (hipStream_t)stream, &a);
 }
 
 int rfp4_mma_bf16_tile(rfp4_stream_t stream, const uint32_t *a, const uint32_t *b, float *out)

@@ -4,6 +4,7 @@
 
 #include <string>
 #include <unordered_map>
+#include <vector>
 
 #include "../../include/rfp4.h"
 #include "shared/kernel_args.h"
@@ -32,15 +33,32 @@ int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3
 int hip_check(hipError_t e, const char *what);
 int launch(const char *name, dim3 grid, dim3 block, hipStream_t s, void *args, unsigned shmem = 0);
 
+// Per-launch timing: while a record list is installed on this thread, every
+// launch() goes through hipExtModuleLaunchKernel with its own start and stop
+// events, which take the kernel's dispatch timestamps (the interval rocprof
+// reports as its duration).  Eager launches only (not under stream capture).
+struct KernelTiming {
+    const char *name; // a kernel-table key: lives as long as the runtime
+    hipEvent_t start, stop;
+};
+void timing_install(std::vector<KernelTiming> *records); // nullptr = off
+
 int fill_words(uint32_t *p, uint64_t n_words, uint32_t value, hipStream_t s);
 int gemv_check(uint32_t n, uint32_t k, const void *w, const void *sc, const float *x, const float *y);
 struct GemvVariant {
     int R, NS, W; // rows per wave, up-front K slices (0 = loop), waves per workgroup
 };
+// The variant a launch of this shape gets now (honours this thread's
+// rfp4_debug_gemv_* overrides); an engine fixes its variants at creation.
 GemvVariant gemv_variant(uint32_t n, uint32_t k, int epi, bool f32scale);
-int gemv_launch(const char *scale_name, int epi, const GemvArgs &args, hipStream_t s, int r_override);
-uint32_t gemv_blocks(uint32_t n_logical, uint32_t k, int epi);
+inline uint32_t gemv_grid(uint32_t n, const GemvVariant &v) { return (n + (uint32_t)(v.W * v.R) - 1) / (uint32_t)(v.W * v.R); }
+int gemv_launch_v(const char *scale_name, int epi, const GemvArgs &args, hipStream_t s, const GemvVariant &v);
+int gemv_launch(const char *scale_name, int epi, const GemvArgs &args, hipStream_t s);
 int attn_launch(const AttnArgs &args, int kv_f16, hipStream_t s, uint32_t max_seq_for_grid, uint32_t rows);
+// fp4_gemm with the caller's split-K workspace (kGemmPartFloats floats; the
+// engine owns one, so engines on different streams do not share partials).
+int gemm_launch(hipStream_t stream, uint32_t m, uint32_t n, uint32_t k, const uint8_t *a_codes, const uint8_t *a_scales,
+                const uint8_t *w_codes, const uint8_t *w_scales, float *c, float *part);
 uint32_t attn_group_pad(uint32_t group);
 // Causal prefill attention (device/attn_prefill.h), fp16 caches.
 int attn_prefill_launch(const AttnPrefillArgs &a, uint32_t head_dim, hipStream_t s);

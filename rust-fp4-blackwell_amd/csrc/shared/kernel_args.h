@@ -45,15 +45,6 @@ typedef struct RopeArgs {
     uint32_t pad;
 } RopeArgs;
 
-// Fused per-token q/k rotation and fp16 KV append for the engine.
-typedef struct RopeAppendArgs {
-    float *qkv;           // [q: nh*hd][k: nkv*hd][v: nkv*hd]
-    const float *cosv, *sinv;
-    uint16_t *kcache, *vcache; // [kvh][max_seq][hd] fp16
-    const int32_t *pos_ptr;
-    uint32_t n_heads, n_kv_heads, head_dim, max_seq;
-} RopeAppendArgs;
-
 typedef struct CopyArgs {
     const float *src;
     void *dst;
@@ -79,7 +70,7 @@ typedef struct AttnArgs {
     float *out;           // [n_heads][head_dim]
     float *part;          // workspace: [n_heads][max_splits][head_dim + 4] = (m, l, -, -, acc)
     const int32_t *pos_ptr; // if non-null, seq = *pos_ptr + 1
-    // Fused RoPE + fp16 KV append (null cosv = off): q is un-rotated, the
+    // Fused RoPE + KV append (null cosv = off): q is un-rotated, the
     // current token (position seq-1) has un-rotated k_new and v_new
     // ([n_kv_heads][head_dim]); tables are [pos][head_dim/2].
     const float *cosv, *sinv;
@@ -154,12 +145,14 @@ typedef struct SynthF16Args {
     float coef, offset;
 } SynthF16Args;
 
-// Synthetic KV prefill: positions [0, upto) of [kvh][max_seq][hd] fp16 caches.
+// Synthetic KV prefill: positions [0, upto) of [kvh][max_seq][hd] fp16 (or
+// f32) caches.
 typedef struct SynthKvArgs {
-    uint16_t *cache;
+    void *cache;
     uint64_t seed, stream;
     uint32_t upto, n_kv_heads, head_dim, max_seq;
-    float coef, pad;
+    float coef;
+    uint32_t kv_f32;      // nonzero: f32 elements, else fp16 bits
 } SynthKvArgs;
 
 // OCP MX quantization of f32 (or bf16) rows into codes + E8M0.

@@ -18,7 +18,9 @@ import re
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "librfp4.so")
+# RFP4_LIB selects another build of the same library (the sanitizer build of
+# the CPU tests); the default is the in-tree librfp4.so.
+LIB_PATH = os.environ.get("RFP4_LIB") or os.path.join(HERE, "librfp4.so")
 HEADER_PATH = os.path.join(os.path.dirname(HERE), "include", "rfp4.h")
 
 P = C.c_void_p
@@ -35,18 +37,28 @@ class Rfp4Error(RuntimeError):
         self.code = code
 
 
+class KernelTime(C.Structure):
+    _fields_ = [("name", C.c_char * 64), ("us", F32)]
+
+
 class ModelConfig(C.Structure):
     _fields_ = [
         ("dim", U32), ("n_layers", U32), ("n_heads", U32), ("n_kv_heads", U32),
         ("head_dim", U32), ("ffn", U32), ("vocab", U32), ("max_seq", U32),
-        ("theta", C.c_double), ("eps", F32), ("reserved", U32),
+        ("theta", C.c_double), ("eps", F32), ("scale_format", C.c_uint16), ("kv_format", C.c_uint16),
     ]
+
+
+SCALE_E8M0, SCALE_F32 = 0, 1   # RFP4_SCALE_*
+KV_F16, KV_F32 = 0, 1           # RFP4_KV_*
 
 
 # name -> (restype, argtypes)
 _SIGS = {
     "rfp4_last_error": (C.c_char_p, []),
     "rfp4_version": (I32, []),
+    "rfp4_kernel_count": (I32, [C.POINTER(U32)]),
+    "rfp4_kernel_name": (I32, [U32, C.c_char_p, SZ]),
     "rfp4_init": (I32, [I32]),
     "rfp4_device_count": (I32, [C.POINTER(I32)]),
     "rfp4_device_info": (I32, [C.POINTER(I32), C.POINTER(SZ), C.POINTER(I32)]),
@@ -96,9 +108,7 @@ _SIGS = {
     "rfp4_debug_prefill_attn": (I32, [I32]),
     "rfp4_debug_prefill_waves": (I32, [I32]),
     "rfp4_debug_prefill_pairing": (I32, [I32]),
-    "rfp4_debug_gemv_path": (I32, [I32]),
-    "rfp4_debug_gemv_fused": (I32, [P, I32, U32, U32, U32, P, P, P, P, F32, P, P, P]),
-    "rfp4_selftest_cvt_bf16": (I32, [P, U32, P, P, P]),
+    "rfp4_debug_gemv_fused": (I32, [P, I32, I32, U32, U32, U32, P, P, P, P, F32, P, P, P]),
     "rfp4_mma_bf16_tile": (I32, [P, P, P, P]),
     "rfp4_mma_f16_tile": (I32, [P, P, P, P]),
     "rfp4_synth_mx_weight": (I32, [P, U64, U64, F32, U64, U64, U64, P, P]),
@@ -122,7 +132,9 @@ _SIGS = {
     "llama_decode_step": (I32, [P, U32, U32, C.POINTER(U32)]),
     "llama_generate": (I32, [P, P, U32, U32, U32, P]),
     "llama_engine_begin": (I32, [P, P, U32, U32, U32]),
+    "llama_engine_begin_harness": (I32, [P, U32, U32]),
     "llama_engine_run_steps": (I32, [P, U32]),
+    "llama_engine_time_steps": (I32, [P, U32, P, U32, C.POINTER(U32)]),
     "llama_engine_read_ids": (I32, [P, P, U32]),
     "llama_engine_logits": (I32, [P, P]),
     "llama_engine_stream": (P, [P]),
@@ -173,6 +185,19 @@ def init(device: int = 0):
     if not _inited:
         check(load().rfp4_init(device))
         _inited = True
+
+
+def kernel_names() -> list:
+    """Every kernel of the embedded gfx950 code object (no device needed)."""
+    lib = load()
+    n = U32(0)
+    check(lib.rfp4_kernel_count(C.byref(n)))
+    buf = C.create_string_buffer(256)
+    out = []
+    for i in range(n.value):
+        check(lib.rfp4_kernel_name(i, buf, 256))
+        out.append(buf.value.decode())
+    return out
 
 
 def device_count() -> int:
@@ -492,7 +517,7 @@ class SafeTensors:
 
 
 class Engine:
-    """llama_engine: weights, fp16 KV and the captured step graph."""
+    """llama_engine: weights, KV caches and the captured step graphs."""
 
     def __init__(self, cfg: ModelConfig, seed: int, _handle=None):
         init()
@@ -555,8 +580,20 @@ class Engine:
         pr = np.ascontiguousarray(prompt, dtype=np.uint32)
         check(load().llama_engine_begin(self.h, pr.ctypes.data, len(pr), pos0, ids_cap))
 
+    def begin_harness(self, ctx: int, ids_cap: int):
+        """llama_decode's harness (f32-scale engines): context [0, ctx) at 0.01,
+        x = the harness vector; step i's argmax lands in ids[1 + i]."""
+        check(load().llama_engine_begin_harness(self.h, ctx, ids_cap))
+
     def run_steps(self, n: int):
         check(load().llama_engine_run_steps(self.h, n))
+
+    def time_steps(self, n: int, cap: int = 16384) -> list:
+        """n more steps with every kernel timed in place: [(name, us)] in launch order."""
+        buf = (KernelTime * cap)()
+        cnt = U32(0)
+        check(load().llama_engine_time_steps(self.h, n, buf, cap, C.byref(cnt)))
+        return [(buf[i].name.decode(), float(buf[i].us)) for i in range(min(cnt.value, cap))]
 
     def read_ids(self, count: int) -> np.ndarray:
         out = np.zeros(count, dtype=np.uint32)
@@ -582,13 +619,14 @@ class Engine:
         scales = np.empty(sb, dtype=np.uint8)
         check(load().rfp4_d2h(codes.ctypes.data, c, cb, self.stream.h))
         check(load().rfp4_d2h(scales.ctypes.data, s, sb, self.stream.h))
-        return codes, scales
+        return codes, (scales.view(np.float32) if self.cfg.scale_format == SCALE_F32 else scales)
 
     def kv_host(self, layer: int):
         k, v, n = P(), P(), SZ()
         check(load().llama_engine_kv(self.h, layer, C.byref(k), C.byref(v), C.byref(n)))
-        ka = np.empty(n.value, dtype=np.uint16)
-        va = np.empty(n.value, dtype=np.uint16)
+        dt = np.float32 if self.cfg.kv_format == KV_F32 else np.uint16
+        ka = np.empty(n.value, dtype=dt)
+        va = np.empty(n.value, dtype=dt)
         check(load().rfp4_d2h(ka.ctypes.data, k.value, ka.nbytes, self.stream.h))
         check(load().rfp4_d2h(va.ctypes.data, v.value, va.nbytes, self.stream.h))
         return ka, va

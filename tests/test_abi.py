@@ -34,6 +34,45 @@ def test_reference_entry_points_present():
         assert n in rfp4.header_functions()
 
 
+def _bundle_kernel_symbols():
+    """Kernel descriptor symbols of the built code object, read with the LLVM
+    tools (an independent reading of the same file)."""
+    import tempfile
+    hsaco = os.path.join(PKG, "build", "kernels.hsaco")
+    llvm = "/opt/rocm/llvm/bin"
+    if not os.path.exists(hsaco) or not os.path.exists(os.path.join(llvm, "llvm-readelf")):
+        pytest.skip("built code object or LLVM tools not present")
+    with tempfile.TemporaryDirectory() as d:
+        elf = os.path.join(d, "k.elf")
+        r = subprocess.run([os.path.join(llvm, "clang-offload-bundler"), "--unbundle", "--type=o",
+                            "--targets=hipv4-amdgcn-amd-amdhsa--gfx950", f"--input={hsaco}", f"--output={elf}"],
+                           capture_output=True, text=True)
+        if r.returncode:
+            pytest.skip("clang-offload-bundler failed: " + r.stderr[-200:])
+        out = subprocess.run([os.path.join(llvm, "llvm-readelf"), "--syms", elf], capture_output=True,
+                             text=True).stdout
+    return sorted({w[:-3] for w in out.split() if w.endswith(".kd")})
+
+
+def test_kernel_table_matches_the_code_object():
+    """The runtime resolves every kernel handle at init from the embedded code
+    object's symbol table (no lookup, and no map update, after init): its
+    parser agrees with the LLVM tools on the built file, and every kernel the
+    host launches by a literal name is present."""
+    names = rfp4.kernel_names()
+    assert len(names) == len(set(names)) and len(names) > 100
+    assert sorted(names) == _bundle_kernel_symbols()
+    literal = set()
+    for f in ("runtime.cpp", "engine.cpp"):
+        literal |= set(re.findall(r'"(rfp4_[a-z0-9_]+)"', open(os.path.join(PKG, "csrc", f)).read()))
+    missing = sorted(n for n in literal if n not in names)
+    assert not missing, missing
+    for hd in (64, 128):
+        for kv in ("f16", "f32"):
+            for g in (1, 2, 4, 8):
+                assert f"rfp4_attn_hd{hd}_{kv}_g{g}" in names
+
+
 def test_shape_errors_need_no_device():
     lib = rfp4.load()
     p = 0x10000  # never dereferenced: validation fails first
@@ -43,8 +82,6 @@ def test_shape_errors_need_no_device():
     assert lib.fp4_gemv(None, 16, 64, None, p, p, p) == -1         # null pointer
     assert lib.mx4_gemv(None, 16, 64, p + 4, p, p, p) == -6       # misaligned codes
     assert lib.mx4_gemv_swiglu(None, 16, 64, 8, p, p, p, p) == -2  # up rows overlap gate rows
-    assert lib.rfp4_debug_gemv_path(4) == -1
-    assert lib.rfp4_debug_gemv_path(3) == 0 and lib.rfp4_debug_gemv_path(0) == 0
     assert lib.fp4_gemm(None, 32, 4096, 4000, p, p, p, p, p) == -2  # K not a multiple of 256
     assert lib.fp4_gemm(None, 32, 4098, 4096, p, p, p, p, p) == -2  # N not a multiple of 4
     assert lib.fp4_gemm(None, 0, 4096, 4096, p, p, p, p, p) == -2   # M = 0

@@ -17,6 +17,13 @@ def _deq(orc, codes, scales, n, k):
     return v * np.repeat(np.ldexp(1.0, scales.astype(np.int64) - 127).reshape(n, k // 32), 32, axis=1)
 
 
+def _deq_f32(orc, codes, scales, n, k):
+    """E2M1 codes times the reference's f32 per-32 scales (fp4_gemv/src/main.rs:136-142)."""
+    c = orc.unpack(codes).reshape(n, k)
+    v = np.where(c & 8, -1.0, 1.0) * FP4[c & 7]
+    return v * np.repeat(np.asarray(scales, np.float64).reshape(n, k // 32), 32, axis=1)
+
+
 def _f16(a):
     return np.asarray(a).view(np.float16).astype(np.float64)
 
@@ -27,9 +34,11 @@ class NumpyLlama:
         qd, kvd = c["n_heads"] * c["head_dim"], c["n_kv_heads"] * c["head_dim"]
         shapes = [(qd, c["dim"]), (kvd, c["dim"]), (kvd, c["dim"]), (c["dim"], qd),
                   (c["ffn"], c["dim"]), (c["ffn"], c["dim"]), (c["dim"], c["ffn"])]
-        self.W = [[_deq(orc, m.codes(l, p), m.scales(l, p), *shapes[p]) for p in range(7)]
+        self.f32kv = c.get("kv_format", 0) == 1
+        deq = _deq_f32 if c.get("scale_format", 0) == 1 else _deq
+        self.W = [[deq(orc, m.codes(l, p), m.scales(l, p), *shapes[p]) for p in range(7)]
                   for l in range(c["n_layers"])]
-        self.lm = _deq(orc, m.codes(-1, 0), m.scales(-1, 0), c["vocab"], c["dim"])
+        self.lm = deq(orc, m.codes(-1, 0), m.scales(-1, 0), c["vocab"], c["dim"])
         self.emb = _f16(m.embed()).reshape(c["vocab"], c["dim"])
         self.na = [_f16(m.norm(l, 0)) for l in range(c["n_layers"])]
         self.nf = [_f16(m.norm(l, 1)) for l in range(c["n_layers"])]
@@ -51,17 +60,25 @@ class NumpyLlama:
         return np.concatenate([a * cs - b * sn, b * cs + a * sn], axis=1)
 
     def step(self, tok, pos):
+        return self.layers(self.emb[tok].copy(), pos)
+
+    def _kv(self, v):
+        v = v.astype(np.float32)
+        return (v if self.f32kv else v.astype(np.float16)).astype(np.float64)
+
+    def layers(self, x, pos):
+        """The layers and LM head on activation x; returns (argmax, logits)
+        and leaves the final residual stream in self.x."""
         c = self.c
         nh, nkv, hd = c["n_heads"], c["n_kv_heads"], c["head_dim"]
-        x = self.emb[tok].copy()
         for l in range(c["n_layers"]):
             Wq, Wk, Wv, Wo, Wg, Wu, Wd = self.W[l]
             h = self._norm(x, self.na[l])
             q = self._rope(Wq @ h, nh, pos)
             k = self._rope(Wk @ h, nkv, pos)
-            # fp16 KV cache (round to nearest even via numpy's IEEE conversion)
-            self.K[l][pos] = k.astype(np.float32).astype(np.float16).astype(np.float64)
-            self.V[l][pos] = (Wv @ h).reshape(nkv, hd).astype(np.float32).astype(np.float16).astype(np.float64)
+            # fp16 KV cache (round to nearest even via numpy's IEEE conversion), or f32
+            self.K[l][pos] = self._kv(k)
+            self.V[l][pos] = self._kv((Wv @ h).reshape(nkv, hd))
             att = np.zeros((nh, hd))
             for hh in range(nh):
                 g = hh // (nh // nkv)
@@ -72,6 +89,7 @@ class NumpyLlama:
             h = self._norm(x, self.nf[l])
             gate, up = Wg @ h, Wu @ h
             x = x + Wd @ (gate / (1 + np.exp(-gate)) * up)
+        self.x = x
         logits = self.lm @ self._norm(x, self.nfinal)
         return int(np.argmax(logits)), logits
 
@@ -201,4 +219,79 @@ def test_kv_prefill_layout(orc):
     v = orc.lib().orc_ih4_normal(orc.mix64(0x4B56, 0x4B560000 + 2 * 1, idx), coef)
     assert kc[kvh, t, d] == orc.lib().orc_f32_to_f16(v)
     assert not kc[:, 5:].any()
+    m.close()
+
+
+def _xorshift(s, n):
+    """xorshift32 13/17/5 (llama_decode/src/main.rs:300-305) in numpy."""
+    out = np.empty(n, np.uint32)
+    s = np.uint32(s)
+    for i in range(n):
+        s ^= np.uint32(s << np.uint32(13))
+        s ^= np.uint32(s >> np.uint32(17))
+        s ^= np.uint32(s << np.uint32(5))
+        out[i] = s
+    return out, int(s)
+
+
+HCFG = dict(dim=64, n_layers=2, n_heads=4, n_kv_heads=2, head_dim=32, ffn=128, vocab=96,
+            theta=500000.0, eps=1e-5, max_seq=48, scale_format=1, kv_format=1)
+
+
+def test_f32_scale_model_is_mk_fp4(orc):
+    """An f32-scale oracle model holds the reference harness's weights
+    (llama_decode/src/main.rs:307-325,369-393): per layer q, k, v, o, gate,
+    up, down, then the LM head, each all its packed words then all its scales
+    0.25 + (r % 8) * 0.03125, from one xorshift32 stream; norms 1.0."""
+    c = HCFG
+    qd, kvd = c["n_heads"] * c["head_dim"], c["n_kv_heads"] * c["head_dim"]
+    shapes = [(qd, c["dim"]), (kvd, c["dim"]), (kvd, c["dim"]), (c["dim"], qd),
+              (c["ffn"], c["dim"]), (c["ffn"], c["dim"]), (c["dim"], c["ffn"])]
+    m = orc.Model(c, 0xDEADBEEF)
+    st = 0xDEADBEEF
+    for l in range(c["n_layers"]):
+        for p, (n, k) in enumerate(shapes):
+            words, st = _xorshift(st, n * k // 8)
+            r, st = _xorshift(st, n * k // 32)
+            np.testing.assert_array_equal(m.codes(l, p).view(np.uint32), words)
+            np.testing.assert_array_equal(m.scales(l, p), np.float32(0.25) + (r % 8).astype(np.float32) * np.float32(0.03125))
+        assert np.all(m.norm(l, 0) == 0x3C00) and np.all(m.norm(l, 1) == 0x3C00)
+    words, st = _xorshift(st, c["vocab"] * c["dim"] // 8)
+    np.testing.assert_array_equal(m.codes(-1, 0).view(np.uint32), words)
+    assert np.all(m.norm(-1, 0) == 0x3C00)
+    m.close()
+
+
+def test_harness_decode_matches_numpy_llama(orc):
+    """The llama_decode harness (llama_decode/src/main.rs:356-492) on the
+    oracle: f32 scales, f32 K/V with the context [0, P) at 0.01, the
+    activation vector (r % 2001) / 1000 - 1 drawn after the weights, and steps
+    at P, P+1, ... with no embedding (x carries over); against the float64
+    numpy decoder on the same weights."""
+    c = HCFG
+    P = 20
+    m = orc.Model(c, 0xDEADBEEF)
+    ref = NumpyLlama(orc, m, c)
+    # the stream position after the weights: replay the counts
+    qd, kvd = c["n_heads"] * c["head_dim"], c["n_kv_heads"] * c["head_dim"]
+    per_layer = (qd + 2 * kvd) * c["dim"] + c["dim"] * qd + 3 * c["ffn"] * c["dim"]
+    total = per_layer * c["n_layers"] + c["vocab"] * c["dim"]
+    _, st = _xorshift(0xDEADBEEF, total // 8 + total // 32)
+    r, _ = _xorshift(st, c["dim"])
+    x = (r % 2001).astype(np.float32) / np.float32(1000.0) - np.float32(1.0)
+    for l in range(c["n_layers"]):
+        ref.K[l][:P] = np.float32(0.01)
+        ref.V[l][:P] = np.float32(0.01)
+    m.harness_begin(P)
+    x = x.astype(np.float64)
+    for i in range(6):
+        t_orc, lo = m.step_noembed(P + i, want_logits=True)
+        t_np, ln = ref.layers(x, P + i)
+        x = ref.x
+        np.testing.assert_allclose(lo, ln, rtol=1e-4, atol=1e-4 * np.abs(ln).max())
+        srt = np.sort(ln)
+        if srt[-1] - srt[-2] > 1e-3 * np.abs(ln).max():
+            assert t_orc == t_np, i
+    kc = m.kcache(0).reshape(c["n_kv_heads"], c["max_seq"], c["head_dim"])
+    assert kc.dtype == np.float32 and np.all(kc[:, :P] == np.float32(0.01)) and np.any(kc[:, P] != np.float32(0.01))
     m.close()
