@@ -115,13 +115,34 @@ RFP4_DEV float slots_max(float v)
     return xor32_max(v);
 }
 
-// ---- in-kernel merge of the split states (no fence).  Every word another
-// workgroup reads is written and read with agent-scope atomic accesses
-// (global_store / global_load sc1: coherent on their own on gfx950, as the
-// compiler's own release/acquire sequences assume), so publishing them
-// needs only their completion (s_waitcnt vmcnt(0)) before the arrival
-// counter is bumped; no L2 writeback or invalidate.  No workgroup waits for
-// another: the one that arrives last merges, the others exit.
+// ---- in-kernel merge of the split states (no fence).  No workgroup waits
+// for another: the one that arrives last merges, the others exit.
+//
+// HARD REQUIREMENT (gfx950 memory system): this protocol publishes one
+// workgroup's split state to another without a release/acquire pair.  It
+// holds because on gfx950 (a) a relaxed agent-scope atomic store compiles to
+// global_store ... sc1, which writes through the XCD's L2 to the device-
+// coherent level, (b) a relaxed agent-scope atomic load compiles to
+// global_load ... sc1, which misses the non-coherent L2 and reads that level,
+// and (c) s_waitcnt vmcnt(0) returns only after this thread's stores are
+// acknowledged there.  So every state word is stored with agent-scope stores,
+// every thread waits for its own stores (vmcnt(0)), the workgroup
+// synchronises, and only then does one thread bump the KV head's arrival
+// counter (a device-coherent atomic); the workgroup whose increment completes
+// the count has every other split's stores acknowledged before their
+// increments, and its agent-scope loads read them.  These are the cache-bypass
+// semantics the compiler's own agent-scope release/acquire sequences assume
+// on this target, minus the L2 writeback and invalidate (buffer_wbl2 /
+// buffer_inv sc1) that a fence adds: measured at 5.8 us per launch on 264
+// workgroups.  Another target, or a compiler that stops mapping these atomics
+// to sc1 accesses, needs the fence back.  The merge-mode tests compare with
+// the second-kernel merge and repeat the in-kernel merge 20 times (a stale
+// state would change a result).  The in-kernel merge is used up to 8 splits:
+// measured at 29 splits (the 8B context), its atomic and state round trips
+// cost 5.5 us inside the kernel against 4.2 us for the merge kernel.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "the in-kernel attention merge's publication protocol is written for gfx950's sc1 accesses"
+#endif
 RFP4_DEV void attn_store_agent(float *p, float v) { __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 RFP4_DEV float attn_load_agent(const float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 
