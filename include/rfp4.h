@@ -136,6 +136,17 @@ int attn_decode(rfp4_stream_t stream, uint32_t n_heads, uint32_t n_kv_heads, uin
 int attn_decode_f16(rfp4_stream_t stream, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
                     uint32_t seq, const float *q, const uint16_t *kc, const uint16_t *vc, uint64_t token_stride,
                     uint64_t head_stride, float *out);
+/* attn_decode_f16 that allocates nothing.  No counterpart in the reference:
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The split
+ * states live in a static device array of 4 MiB per device (set up by
+ * rfp4_init) instead of the library workspace; shapes whose states exceed it
+ * (n_heads * splits * (head_dim + 4) floats > 2^20) fail with
+ * RFP4_E_CAPACITY.  Splits are always merged by a second kernel.  Every call
+ * on a device shares that array: calls that overlap on one device race. */
+int attn_decode_f16_noalloc(rfp4_stream_t stream, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                            uint32_t seq, const float *q, const uint16_t *kc, const uint16_t *vc,
+                            uint64_t token_stride, uint64_t head_stride, float *out);
 /* Causal attention of `rows` query rows at positions pos0 .. pos0+rows-1 over
  * fp16 K/V (the rows' own k, v already in the caches): row r is attn_decode_f16
  * with seq = pos0 + r + 1 (llama_run/src/main.rs:148-242 applied row by row;

@@ -247,6 +247,8 @@ int rfp4_init(int device)
     // arrival counters of the in-kernel attention merge: zero between calls
     if (!rc) rc = hip_check(hipMalloc((void **)&rt->attn_counters, kAttnMaxHeads * sizeof(uint32_t)), "hipMalloc(attn counters)");
     if (!rc) rc = hip_check(hipMemset(rt->attn_counters, 0, kAttnMaxHeads * sizeof(uint32_t)), "hipMemset(attn counters)");
+    // the allocation-free entry points' scratch on this device (current now)
+    if (!rc) rc = noalloc_setup(device);
     if (!rc) rc = hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize");
     if (rc) {
         hipFree(rt->attn_part);
@@ -755,8 +757,13 @@ int kv_append_f16(rfp4_stream_t stream, uint32_t n, uint32_t off, const float *s
     return launch("rfp4_copy_into_f16", dim3((n + 255) / 256), dim3(256), (hipStream_t)stream, &a);
 }
 
-static int attn_common(hipStream_t s, uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t seq, const float *q,
-                       const void *kc, const void *vc, uint64_t ts, uint64_t hs, float *out, int f16)
+} // extern "C"
+
+namespace rfp4 {
+
+int attn_decode_ws(hipStream_t s, uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t seq, const float *q, const void *kc,
+                   const void *vc, uint64_t ts, uint64_t hs, float *out, int f16, float *part, size_t part_floats,
+                   bool allow_inmerge)
 {
     Runtime *rt = runtime();
     if (!rt) return set_error(RFP4_E_NOT_INIT, "rfp4_init has not been called");
@@ -774,14 +781,32 @@ static int attn_common(hipStream_t s, uint32_t nh, uint32_t nkv, uint32_t hd, ui
     if (splits > kAttnMaxSplits)
         return set_error(RFP4_E_CAPACITY, "attn_decode: seq %u needs %u splits of %u tokens (> %u)", seq, splits, chunk,
                          kAttnMaxSplits);
+    if (splits > 1 && (size_t)nh * splits * (hd + 4) > part_floats)
+        return set_error(RFP4_E_CAPACITY, "attn_decode: %u heads x %u splits x %u floats of split state exceed the "
+                                          "%zu-float workspace", nh, splits, hd + 4, part_floats);
     AttnArgs a{};
     a.q = q; a.kc = kc; a.vc = vc; a.out = out;
-    a.part = rt->attn_part; a.pos_ptr = nullptr;
+    a.part = part; a.pos_ptr = nullptr;
     a.ts = ts; a.hs = hs;
     a.n_heads = nh; a.n_kv_heads = nkv; a.head_dim = hd; a.seq = seq;
     a.chunk = chunk; a.max_splits = splits;
-    if (attn_inmerge(splits)) a.counters = rt->attn_counters;
+    if (allow_inmerge && attn_inmerge(splits)) a.counters = rt->attn_counters;
     return attn_launch(a, f16, s, seq, 1);
+}
+
+} // namespace rfp4
+
+extern "C" {
+
+// The drop-in attention calls share the library's split-state workspace and
+// merge counters: calls that overlap on one device (several streams or
+// threads) race on them.
+static int attn_common(hipStream_t s, uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t seq, const float *q,
+                       const void *kc, const void *vc, uint64_t ts, uint64_t hs, float *out, int f16)
+{
+    Runtime *rt = runtime();
+    return attn_decode_ws(s, nh, nkv, hd, seq, q, kc, vc, ts, hs, out, f16, rt ? rt->attn_part : nullptr,
+                          rt ? rt->attn_part_floats : 0, true);
 }
 
 int attn_decode(rfp4_stream_t stream, uint32_t n_heads, uint32_t n_kv_heads, uint32_t seq, const float *q,

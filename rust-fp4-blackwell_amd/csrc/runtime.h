@@ -55,6 +55,16 @@ inline uint32_t gemv_grid(uint32_t n, const GemvVariant &v) { return (n + (uint3
 int gemv_launch_v(const char *scale_name, int epi, const GemvArgs &args, hipStream_t s, const GemvVariant &v);
 int gemv_launch(const char *scale_name, int epi, const GemvArgs &args, hipStream_t s);
 int attn_launch(const AttnArgs &args, int kv_f16, hipStream_t s, uint32_t max_seq_for_grid, uint32_t rows);
+// One-row attention over caller K/V with split states in `part` (at least
+// n_heads * splits * (head_dim + 4) floats, checked); allow_inmerge = false
+// always merges with the second kernel (no counters, nothing that must start
+// at zero).
+int attn_decode_ws(hipStream_t s, uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t seq, const float *q, const void *kc,
+                   const void *vc, uint64_t ts, uint64_t hs, float *out, int f16, float *part, size_t part_floats,
+                   bool allow_inmerge);
+// Looks up, once per device and with that device current, the address of
+// the allocation-free entry points' static scratch (csrc/noalloc.hip).
+int noalloc_setup(int device);
 // fp4_gemm with the caller's split-K workspace (kGemmPartFloats floats; the
 // engine owns one, so engines on different streams do not share partials).
 int gemm_launch(hipStream_t stream, uint32_t m, uint32_t n, uint32_t k, const uint8_t *a_codes, const uint8_t *a_scales,

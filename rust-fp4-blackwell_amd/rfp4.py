@@ -89,6 +89,7 @@ _SIGS = {
     "kv_append_f16": (I32, [P, U32, U32, P, P]),
     "attn_decode": (I32, [P, U32, U32, U32, P, P, P, P]),
     "attn_decode_f16": (I32, [P, U32, U32, U32, U32, P, P, P, U64, U64, P]),
+    "attn_decode_f16_noalloc": (I32, [P, U32, U32, U32, U32, P, P, P, U64, U64, P]),
     "attn_prefill_f16": (I32, [P, U32, U32, U32, U32, U32, P, U32, P, P, U64, U64, P, U32]),
     "swiglu": (I32, [P, U32, P, P, P]),
     "residual": (I32, [P, U32, P, P]),
