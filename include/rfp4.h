@@ -208,6 +208,14 @@ int rfp4_debug_attn_merge(int mode);
  * matrix-core prefill kernel, 1 = the decode kernel, one grid row per prompt
  * row.  No reference counterpart. */
 int rfp4_debug_prefill_attn(int mode);
+/* Test hook (this thread): llama_engine_prefill stops after one stage and
+ * returns *next_token = UINT32_MAX with that stage's output in its workspace
+ * (llama_engine_prefill_buffers).  after = -1: the embedding rows; 10 * layer
+ * + s: stage s of that layer, s = 0 residual add + RMSNorm + MXFP4 rows, 1 the
+ * q|k|v GEMM, 2 RoPE + fp16 K/V append, 3 causal attention, 4 MXFP4 of the
+ * attention rows, 5 the o GEMM, 6 residual add + RMSNorm + MXFP4 rows, 7 the
+ * gate|up GEMM, 8 SwiGLU + MXFP4 rows, 9 the down GEMM.  -2 = no stop. */
+int rfp4_debug_prefill_stop(int after);
 /* Test hook: waves per workgroup of the matrix-core prefill attention on
  * this thread (0 = automatic, 4 or 8).  No reference counterpart. */
 int rfp4_debug_prefill_waves(int waves);
@@ -371,6 +379,13 @@ int llama_engine_weight(llama_engine *e, int layer, int proj, const uint8_t **co
 /* K/V caches of a layer, [kv_head][cache positions][head_dim] elements of the
  * engine's kv_format (fp16 bits or f32); count = elements per cache. */
 int llama_engine_kv(llama_engine *e, int layer, const void **k, const void **v, size_t *count);
+/* Test hook: the batched prefill's workspace, device pointers valid until a
+ * longer prompt regrows it: x [rows][dim] f32 (the residual stream), MXFP4
+ * activation rows (codes [rows][kmax/2], E8M0 [rows][kmax/32], rows packed
+ * at the stage's K), the GEMM output c [rows][widest projection] f32 and the
+ * attention output a [rows][n_heads*head_dim] f32. */
+int llama_engine_prefill_buffers(llama_engine *e, float **x, uint8_t **codes, uint8_t **scales, float **c, float **a,
+                                 uint32_t *rows_cap);
 /* Per-token weight and KV bytes the step streams at a given position. */
 uint64_t llama_engine_weight_bytes(const llama_engine *e);
 

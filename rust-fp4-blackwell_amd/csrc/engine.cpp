@@ -204,6 +204,9 @@ static int prefill_reserve(llama_engine *e, uint32_t n)
 // The prompt through the MXFP4 GEMM: llama_run/src/main.rs:550-556 feed it
 // token by token; here all n positions of a layer run at once, every
 // projection input quantised to MXFP4 per 32 along K (the GEMM is FP4 x FP4).
+// enqueue_prefill's return when the rfp4_debug_prefill_stop hook ended it early
+constexpr int kPrefillStopped = 1;
+
 static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
 {
     const rfp4_model_config &c = e->c;
@@ -214,6 +217,11 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
     ea.ids = e->pf_ids; ea.embed = e->embed; ea.y = e->pf_x; ea.rows = n; ea.k = c.dim; ea.vocab = c.vocab;
     ea.bf16 = e->embed_bf16;
     if ((rc = launch("rfp4_embed_rows", dim3(n), dim3(256), s, &ea))) return rc;
+    // test hook: stop after stage `stop` (-1: the embedding; 10 * layer + s: stage s of that layer)
+    const int stop = prefill_stop();
+    if (stop == -1) return kPrefillStopped;
+#define RFP4_PF_STAGE(S) \
+    if (stop == (int)(10u * l + (S))) return kPrefillStopped
     for (uint32_t l = 0; l < c.n_layers; l++) {
         const LayerW &w = e->L[l];
         uint16_t *kc = (uint16_t *)kv_layer(e, l, 0), *vc = (uint16_t *)kv_layer(e, l, 1); // fp16 (checked by the caller)
@@ -224,13 +232,16 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
         na.add = l > 0 ? e->pf_c : nullptr;
         na.x_out = e->pf_x;
         if ((rc = launch("rfp4_rmsnorm_quant_rows", dim3(n), dim3(256), s, &na))) return rc;
+        RFP4_PF_STAGE(0);
         if ((rc = gemm_launch(s, n, nqkv, c.dim, e->pf_codes, e->pf_scales, w.qkv_c, w.qkv_s, e->pf_c, e->gemm_part))) return rc;
+        RFP4_PF_STAGE(1);
         RopeRowsArgs ra{};
         ra.qkv = e->pf_c; ra.cosv = e->cos_tab; ra.sinv = e->sin_tab; ra.kc = kc; ra.vc = vc;
         ra.ts = hd; ra.hs = (uint64_t)e->max_seq_alloc * hd;
         ra.rows = n; ra.row_stride = nqkv; ra.n_heads = c.n_heads; ra.n_kv_heads = c.n_kv_heads;
         ra.head_dim = hd; ra.pos0 = pos0;
         if ((rc = launch("rfp4_rope_kv_rows", dim3(n), dim3(256), s, &ra))) return rc;
+        RFP4_PF_STAGE(2);
         // causal attention of the prompt rows (row r sees positions 0 .. pos0 + r)
         if (prefill_attn_mode() == 1) {
             // test path: the decode kernel, one query row per grid z (split states per row)
@@ -249,19 +260,27 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
                                c.n_heads, c.n_kv_heads, pos0, n, 0u}; // pairing: chosen by the launcher
             if ((rc = attn_prefill_launch(pa, hd, s))) return rc;
         }
+        RFP4_PF_STAGE(3);
         if ((rc = mx4_quantize(s, n, qd, e->pf_a, 0, e->pf_codes, e->pf_scales))) return rc;
+        RFP4_PF_STAGE(4);
         if ((rc = gemm_launch(s, n, c.dim, qd, e->pf_codes, e->pf_scales, w.o_c, w.o_s, e->pf_c, e->gemm_part))) return rc;
+        RFP4_PF_STAGE(5);
         na.w = e->norm_ffn + (size_t)l * c.dim;
         na.add = e->pf_c; // x += O projection, then the FFN norm
         if ((rc = launch("rfp4_rmsnorm_quant_rows", dim3(n), dim3(256), s, &na))) return rc;
+        RFP4_PF_STAGE(6);
         if ((rc = gemm_launch(s, n, 2 * c.ffn, c.dim, e->pf_codes, e->pf_scales, w.gu_c, w.gu_s, e->pf_c, e->gemm_part))) return rc;
+        RFP4_PF_STAGE(7);
         RowsArgs sa{};
         sa.x = e->pf_c; sa.codes = e->pf_codes; sa.scales = e->pf_scales; sa.rows = n; sa.k = c.ffn;
         if ((rc = launch("rfp4_swiglu_quant_rows", dim3(n), dim3(256), s, &sa))) return rc;
+        RFP4_PF_STAGE(8);
         if ((rc = gemm_launch(s, n, c.dim, c.ffn, e->pf_codes, e->pf_scales, w.d_c, w.d_s, e->pf_c, e->gemm_part))) return rc;
+        RFP4_PF_STAGE(9);
         // x += down projection: by the next layer's first norm, after the last layer here
         if (l + 1 == c.n_layers && (rc = residual(s, n * c.dim, e->pf_c, e->pf_x))) return rc;
     }
+#undef RFP4_PF_STAGE
     // last row: the decode step's final norm + LM head, then argmax
     rc = hip_check(hipMemcpyAsync(e->x, e->pf_x + (size_t)(n - 1) * c.dim, c.dim * sizeof(float),
                                   hipMemcpyDeviceToDevice, s), "hipMemcpyAsync(prefill row)");
@@ -1024,6 +1043,12 @@ int llama_engine_prefill(llama_engine *e, const uint32_t *prompt, uint32_t n_pro
         rc = hip_check(hipMemcpyAsync(e->pf_ids, prompt, n_prompt * sizeof(uint32_t), hipMemcpyHostToDevice, e->stream),
                        "hipMemcpyAsync(prompt)");
     if (!rc) rc = enqueue_prefill(e, n_prompt, pos0);
+    if (rc == kPrefillStopped) {
+        // stopped by the test hook: the workspace holds that stage's output, no token
+        rc = hip_check(hipStreamSynchronize(e->stream), "hipStreamSynchronize");
+        if (!rc) *next_token = UINT32_MAX;
+        return rc;
+    }
     uint32_t tok = 0;
     if (!rc)
         rc = hip_check(hipMemcpyAsync(&tok, e->last_tok, sizeof(uint32_t), hipMemcpyDeviceToHost, e->stream),
@@ -1031,6 +1056,20 @@ int llama_engine_prefill(llama_engine *e, const uint32_t *prompt, uint32_t n_pro
     if (!rc) rc = hip_check(hipStreamSynchronize(e->stream), "hipStreamSynchronize");
     if (!rc) *next_token = tok;
     return rc;
+}
+
+int llama_engine_prefill_buffers(llama_engine *e, float **x, uint8_t **codes, uint8_t **scales, float **c, float **a,
+                                 uint32_t *rows_cap)
+{
+    if (!e || !x || !codes || !scales || !c || !a || !rows_cap)
+        return set_error(RFP4_E_INVALID, "llama_engine_prefill_buffers: null argument");
+    *x = e->pf_x;
+    *codes = e->pf_codes;
+    *scales = e->pf_scales;
+    *c = e->pf_c;
+    *a = e->pf_a;
+    *rows_cap = e->pf_cap;
+    return RFP4_OK;
 }
 
 int llama_engine_create_from_safetensors(const rfp4_model_config *cfg, const char *path, llama_engine **out)

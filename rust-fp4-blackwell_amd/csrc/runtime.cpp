@@ -429,6 +429,8 @@ static thread_local int t_prefill_attn = 0; // 0 matrix-core prefill kernel, 1 o
 static thread_local int t_prefill_waves = 0; // prefill attention waves per workgroup (0 = automatic)
 static thread_local int t_prefill_pairing = 0; // 0 automatic, 1 one query tile per workgroup, 2 paired tiles
 int prefill_attn_mode() { return t_prefill_attn; }
+static thread_local int t_prefill_stop = -2; // stage after which the batched prefill stops (-2: none)
+int prefill_stop() { return t_prefill_stop; }
 
 bool attn_inmerge_mode(int mode, uint32_t splits)
 {
@@ -499,6 +501,14 @@ extern "C" int rfp4_debug_prefill_pairing(int mode)
     using namespace rfp4;
     if (mode < 0 || mode > 2) return set_error(RFP4_E_INVALID, "pairing mode must be 0 (auto), 1 (off) or 2 (on)");
     t_prefill_pairing = mode;
+    return RFP4_OK;
+}
+
+extern "C" int rfp4_debug_prefill_stop(int after)
+{
+    using namespace rfp4;
+    if (after < -2) return set_error(RFP4_E_INVALID, "prefill stop must be -2 (off), -1 (after the embedding) or 10*layer + stage");
+    t_prefill_stop = after;
     return RFP4_OK;
 }
 

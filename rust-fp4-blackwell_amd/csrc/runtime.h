@@ -80,6 +80,7 @@ uint32_t attn_sub_chunk(uint32_t head_dim, uint32_t elem_bytes, uint32_t group);
 bool attn_inmerge(uint32_t max_splits);
 int attn_merge_mode();                           // this thread's rfp4_debug_attn_merge setting
 int prefill_attn_mode();                         // this thread's rfp4_debug_prefill_attn setting
+int prefill_stop();                              // this thread's rfp4_debug_prefill_stop setting
 bool attn_inmerge_mode(int mode, uint32_t splits); // attn_inmerge under an explicit setting
 constexpr uint32_t kAttnInmergeMaxSplits = 8;
 uint32_t attn_chunk_for(uint32_t n_kv_heads, uint32_t seq, uint32_t num_cus, uint32_t head_dim, uint32_t elem_bytes,

@@ -107,6 +107,7 @@ _SIGS = {
     "rfp4_debug_gemv_waves": (I32, [I32]),
     "rfp4_debug_attn_merge": (I32, [I32]),
     "rfp4_debug_prefill_attn": (I32, [I32]),
+    "rfp4_debug_prefill_stop": (I32, [I32]),
     "rfp4_debug_prefill_waves": (I32, [I32]),
     "rfp4_debug_prefill_pairing": (I32, [I32]),
     "rfp4_debug_gemv_fused": (I32, [P, I32, I32, U32, U32, U32, P, P, P, P, F32, P, P, P]),
@@ -142,6 +143,8 @@ _SIGS = {
     "llama_engine_use_graph": (I32, [P, I32]),
     "llama_engine_weight": (I32, [P, I32, I32, C.POINTER(P), C.POINTER(P), C.POINTER(SZ), C.POINTER(SZ)]),
     "llama_engine_kv": (I32, [P, I32, C.POINTER(P), C.POINTER(P), C.POINTER(SZ)]),
+    "llama_engine_prefill_buffers": (I32, [P, C.POINTER(P), C.POINTER(P), C.POINTER(P), C.POINTER(P), C.POINTER(P),
+                                           C.POINTER(U32)]),
     "llama_engine_weight_bytes": (U64, [P]),
 }
 
@@ -565,6 +568,27 @@ class Engine:
         out = U32(0)
         check(load().llama_engine_prefill(self.h, pr.ctypes.data, len(pr), pos0, C.byref(out)))
         return out.value
+
+    def prefill_stop(self, prompt, pos0: int, after: int):
+        """Test hook: the batched prefill stopped after one stage (-1: the
+        embedding; 10 * layer + s: stage s of that layer); read the stage's
+        output with prefill_buffer."""
+        check(load().rfp4_debug_prefill_stop(after))
+        try:
+            self.prefill(prompt, pos0)
+        finally:
+            check(load().rfp4_debug_prefill_stop(-2))
+
+    def prefill_buffer(self, name: str, shape, dtype=np.float32) -> np.ndarray:
+        """Copy of the prefill workspace buffer `name` (x, codes, scales, c, a), first prod(shape) elements."""
+        ptrs = [P() for _ in range(5)]
+        cap = U32(0)
+        check(load().llama_engine_prefill_buffers(self.h, *[C.byref(q) for q in ptrs], C.byref(cap)))
+        src = dict(zip(("x", "codes", "scales", "c", "a"), ptrs))[name].value
+        out = np.empty(shape, dtype=dtype)
+        check(load().rfp4_d2h(out.ctypes.data, src, out.nbytes, self.stream.h))
+        check(load().rfp4_stream_synchronize(self.stream.h))
+        return out
 
     def decode_step(self, tok: int, pos: int) -> int:
         out = U32(0)
