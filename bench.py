@@ -379,6 +379,34 @@ def decode_run(rf, preset, max_seq, prefill, prompt, warmup, steps):
 TIMED_STEPS = 2  # steps whose kernels are timed one by one after the timed region
 
 
+def persistent_run(rf, eng, steps=32, warmup=2):
+    """The same 8B decode with every layer of a step in one cooperative launch
+    (llama_engine_use_persistent; off by default): the KV cache refilled to
+    PREFILL, `steps` steps timed with stream events, tokens compared with the
+    graph step's run from the same state."""
+    if not eng.persistent_available:
+        return None
+    out = {}
+    for mode in (True, False):
+        eng.use_persistent(mode)
+        eng.prefill_kv(KV_SEED, PREFILL)
+        eng.begin([1], PREFILL, 1 + warmup + steps + 1)
+        eng.run_steps(warmup)
+        e0, e1 = rf.Event(), rf.Event()
+        e0.record(eng.stream)
+        eng.run_steps(steps)
+        e1.record(eng.stream)
+        e1.synchronize()
+        out[mode] = (e0.elapsed_ms(e1), eng.read_ids(1 + warmup + steps))
+    eng.use_persistent(False)
+    ms = out[True][0]
+    return {"tok_s": round(steps / (ms / 1e3), 1), "ms_per_token": round(ms / steps, 4),
+            "graph_tok_s_same_run": round(steps / (out[False][0] / 1e3), 1),
+            "tokens_identical_to_graph": bool(np.array_equal(out[True][1], out[False][1])),
+            "workload": f"Llama-3-8B decode at ctx {PREFILL}, {steps} steps, all layers of a step in one cooperative "
+                        "launch (grid barriers between stages), opt-in"}
+
+
 def step_kernels(eng, preset):
     """Every kernel of TIMED_STEPS more decode steps, each timed by its own
     dispatch events (llama_engine_time_steps): {name: [calls per step, avg us]}."""
@@ -591,6 +619,10 @@ def main():
     log(f"GEMV path alone: {path_bytes / 1e9:.3f} GB in {path_ms * 1e3:.1f} us -> {path_gbs:.0f} GB/s; "
         f"gate/up GEMV {gate_in_us:.2f} us in the step ({gate_in_gbs:.0f} GB/s), {gate_ms * 1e3:.2f} us alone "
         f"({gate_gbs:.0f} GB/s)")
+    persistent = persistent_run(rf, eng)
+    if persistent:
+        log(f"persistent decode (opt-in): {persistent['tok_s']} tok/s vs graph {persistent['graph_tok_s_same_run']} "
+            f"tok/s, tokens identical: {persistent['tokens_identical_to_graph']}")
     gemm = None if args.no_gemm else gemm_config5(rf, eng, cfg)
     prefill = None
     if not args.no_prefill:
@@ -671,6 +703,7 @@ def main():
             "GB_s": round(path_gbs, 1),
             "frac": round(path_gbs / HBM_PEAK_GBS, 4),
         },
+        "persistent_decode": persistent,
         "tinyllama": tiny,
         "llama_decode_harness": harness,
         "gemm_config5": gemm,

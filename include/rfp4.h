@@ -373,6 +373,19 @@ int llama_engine_logits(llama_engine *e, float *host_logits);
 rfp4_stream_t llama_engine_stream(llama_engine *e);
 /* 1 = replay the captured step graph (default), 0 = launch kernels eagerly */
 int llama_engine_use_graph(llama_engine *e, int enable);
+/* Persistent decode: every layer of a step in one cooperative launch (one
+ * workgroup per CU, grid barriers between the stages of a layer), then the
+ * LM head; tokens bit-identical to the graph step past 8 attention splits.
+ * Available where the model has the Llama-3-8B widths (dim 4096, 32/8 heads
+ * of 128, FFN 14336; any layer count and vocabulary) with E8M0 weights and
+ * fp16 caches on a 256-CU device; off by default (the graph step is faster on
+ * MI355X: a grid barrier costs more than the kernel boundary it replaces).
+ * enable = 1 fails with RFP4_E_SHAPE where the shape does not allow it;
+ * llama_engine_persistent tells which step is in use.  No reference
+ * counterpart (the reference launches every kernel, llama_run/src/main.rs:
+ * 492-530). */
+int llama_engine_use_persistent(llama_engine *e, int enable);
+int llama_engine_persistent(const llama_engine *e);
 /* Device views for parity tests.  proj: 0..6 = q,k,v,o,gate,up,down; layer -1 = LM head. */
 int llama_engine_weight(llama_engine *e, int layer, int proj, const uint8_t **codes, const uint8_t **scales,
                         size_t *code_bytes, size_t *scale_bytes);

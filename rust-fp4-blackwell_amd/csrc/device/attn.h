@@ -147,6 +147,8 @@ RFP4_DEV void attn_store_agent(float *p, float v) { __hip_atomic_store(p, v, __A
 RFP4_DEV float attn_load_agent(const float *p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); }
 
 #define ATTN_INMERGE_MAX_SPLITS 8
+// Splits the persistent decode kernel merges in place (one round of loads).
+#define ATTN_PERSIST_MAX_SPLITS 32
 // The last split's merge (at most ATTN_INMERGE_MAX_SPLITS splits): every
 // thread first issues the loads of its outputs' split values (the G x HD
 // outputs, 256 per pass), one wave per query head turns (m_i, l_i) into the
@@ -217,69 +219,249 @@ RFP4_DEV void attn_merge_last(const AttnArgs &a, const float *prow, uint32_t kvh
     }
 }
 
-template <int HD, typename KT, int GT>
-RFP4_DEV void attn_body(const AttnArgs &a)
+// Reads and writes of values that the persistent decode kernel produces and
+// consumes inside one launch (q, the new k and v, split states, outputs) go
+// through agent scope (AG); the stand-alone kernels use plain accesses.
+template <bool AG>
+RFP4_DEV float attn_in(const float *p)
 {
-    constexpr int EPL = KvTraits<KT>::EPL;
-    constexpr int LPT = HD / EPL;          // lanes per token row
-    constexpr int TPS = 256 / LPT;         // tokens per workgroup step
-    constexpr int NSTEP = attn_steps_for(HD, (int)sizeof(KT), GT);
-    constexpr uint32_t CAPT = TPS * NSTEP;  // tokens of one sub-chunk (held in registers)
-    constexpr uint32_t HALF = HD / 2;
-    constexpr int QPT = (GT * (int)HALF + 255) / 256; // q rotation pairs per thread
+    return AG ? attn_load_agent(p) : *p;
+}
+template <bool AG>
+RFP4_DEV void attn_out(float *p, float v)
+{
+    if (AG)
+        attn_store_agent(p, v);
+    else
+        *p = v;
+}
+
+// The last split's merge in the merge kernel's summation order
+// (attn_merge_body), for up to S splits in one round of loads: the
+// persistent decode kernel merges in place and stays bit-identical to the
+// two-launch step.  Output (g, d) sums splits p, p + P, p + 2P, ... (P =
+// 256 / HD) per partial p with one FMA chain each, then the partials in p
+// order, divided by L.
+template <int HD, int GT, int S>
+RFP4_DEV void attn_merge_last_ordered(const AttnArgs &a, const float *prow, uint32_t kvh, uint32_t G, uint32_t nsplit)
+{
+    constexpr int P = 256 / HD, OPT = (GT * HD + 255) / 256, NJ = (S + P - 1) / P;
+    static_assert(S <= 64, "one split per lane");
+    __shared__ uint32_t s_last;
+    __shared__ __align__(16) float s_w[GT][S];
+    __shared__ float s_L[GT];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t stride = HD + 4;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // this thread's states have landed
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(a.counters + kvh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = old + 1u == nsplit ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    if (tid == 0) __hip_atomic_store(a.counters + kvh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); // for the next launch
+    float v[OPT][S];
+#pragma unroll
+    for (int j = 0; j < OPT; j++) {
+        const uint32_t i = (uint32_t)tid + 256u * (uint32_t)j;
+        const uint32_t g = i / HD, d = i % HD;
+        const float *hp = prow + (size_t)(kvh * G + min(g, G - 1u)) * a.max_splits * stride + 4 + d;
+#pragma unroll
+        for (int sp = 0; sp < S; sp++) v[j][sp] = (g < G && (uint32_t)sp < nsplit) ? attn_load_agent(hp + (size_t)sp * stride) : 0.0f;
+    }
+    for (uint32_t g = (uint32_t)wave; g < G; g += 4) {
+        const float *hp = prow + (size_t)(kvh * G + g) * a.max_splits * stride;
+        const bool in = (uint32_t)lane < nsplit;
+        const float m = in ? attn_load_agent(hp + (size_t)lane * stride) : -3.402823466e38f;
+        const float l = in ? attn_load_agent(hp + (size_t)lane * stride + 1) : 0.0f;
+        const float M = wave_max(m);
+        const float w = in ? attn_exp2(m - M) : 0.0f;
+        if ((uint32_t)lane < (uint32_t)S) s_w[g][lane] = w;
+        const float L = wave_sum(fmaf(l, w, 0.0f));
+        if (lane == 0) s_L[g] = L;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < OPT; j++) {
+        const uint32_t i = (uint32_t)tid + 256u * (uint32_t)j;
+        const uint32_t g = i / HD, d = i % HD;
+        if (g >= G) break;
+        float out = 0.0f;
+#pragma unroll
+        for (int p = 0; p < P; p++) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int jj = 0; jj < NJ; jj++) {
+                const int sp = p + P * jj;
+                if (sp < S) {
+                    const float t = fmaf(s_w[g][sp], v[j][sp], acc);
+                    acc = (uint32_t)sp < nsplit ? t : acc;
+                }
+            }
+            out = p == 0 ? acc : out + acc;
+        }
+        attn_store_agent(a.out + (size_t)(kvh * G + g) * HD + d, __fdiv_rn(out, s_L[g]));
+    }
+}
+
+// One split of one KV head: the phases of the attention workgroup.  The
+// stand-alone kernel runs load_q, issue and finish back to back; the
+// persistent decode kernel issues the K/V stream (issue) before the grid
+// barrier that publishes q, then loads q and finishes.
+template <int HD, typename KT, int GT, bool AG>
+struct AttnSplit {
+    static constexpr int EPL = KvTraits<KT>::EPL;
+    static constexpr int LPT = HD / EPL;          // lanes per token row
+    static constexpr int TPS = 256 / LPT;         // tokens per workgroup step
+    static constexpr int NSTEP = attn_steps_for(HD, (int)sizeof(KT), GT);
+    static constexpr uint32_t CAPT = TPS * NSTEP;  // tokens of one sub-chunk (held in registers)
+    static constexpr uint32_t HALF = HD / 2;
+    static constexpr int QPT = (GT * (int)HALF + 255) / 256; // q rotation pairs per thread
     static_assert(LPT >= 4 && LPT <= 32, "row split");
     static_assert(256 % HALF == 0, "a thread's rotation pairs share one table column");
     static_assert(GT == 1 || GT == 2 || GT == 4 || GT == 8, "group");
-    __shared__ __align__(16) float qs[GT][HD];
-    __shared__ __align__(16) float vred[4][GT][HD];
-    __shared__ float s_mx[2][4][GT], s_lred[4][GT], s_mfin[GT];
-    __shared__ KT knew[HD], vnew[HD];
 
-    const uint32_t kvh = blockIdx.x, split = blockIdx.y, row = blockIdx.z;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int li = tid % LPT, slot = tid / LPT;
-    const uint32_t G = a.n_heads / a.n_kv_heads; // <= GT
-    const bool fused = a.cosv != nullptr;
-    const float *qg = a.q + (size_t)row * a.q_rs + (size_t)(kvh * G) * HD;
-
-    // ---- loads that need no position: this thread's q pairs (j, j + HD/2)
-    // of pair index i = tid + 256 m
     float qa[QPT], qb[QPT];
-#pragma unroll
-    for (int m = 0; m < QPT; m++) {
-        const uint32_t i = (uint32_t)tid + 256u * (uint32_t)m;
-        const uint32_t g = i / HALF, j = i % HALF;
-        const bool in = g < G;
-        qa[m] = in ? qg[g * HD + j] : 0.0f;
-        qb[m] = in ? qg[g * HD + j + HALF] : 0.0f;
-    }
-    const uint32_t chunk = a.chunk;
-    uint32_t seq = (a.pos_ptr ? (uint32_t)(*a.pos_ptr + 1) : a.seq) + row;
-    float *orow = a.out + (size_t)row * a.out_rs;
-    float *prow = a.part + (size_t)row * a.n_heads * a.max_splits * (HD + 4);
-    seq = min(seq, chunk * a.max_splits); // never read past the planned splits
-    const uint32_t nsplit = (seq + chunk - 1) / chunk;
-    if (split >= nsplit) return;
-    const uint32_t t0 = split * chunk;
-    const uint32_t nt = min(seq, t0 + chunk) - t0;
-    const uint32_t nsub = (nt + CAPT - 1) / CAPT;
-    const uint32_t pos = seq - 1;
-    const bool owner = fused && (pos >= t0) && (pos < t0 + nt);
-    const KT *kc = (const KT *)a.kc + (size_t)kvh * a.hs;
-    const KT *vc = (const KT *)a.vc + (size_t)kvh * a.hs;
-
-    // ---- rope table column j = tid % (HD/2) at the position, then the K/V stream
-    float cs = 1.0f, sn = 0.0f;
-    if (fused) {
-        const uint32_t j = (uint32_t)tid % HALF;
-        cs = a.cosv[(size_t)pos * HALF + j];
-        sn = a.sinv[(size_t)pos * HALF + j];
-    }
-    // K and V rows of sub-chunk C: token t0 + C*CAPT + s*TPS + slot, lanes split
-    // the row.  Slots past the split re-read its last row (in bounds, finite;
-    // their scores are masked and their p is 0): no branch around the loads,
-    // so the wait for the rope tables below does not wait for this stream.
     uint4 kr[NSTEP], vr[NSTEP];
+    float cs, sn;
+    uint32_t kvh, split, row, G, seq, nsplit, t0, nt, nsub, pos;
+    bool fused, owner;
+    const KT *kc, *vc;
+
+    // This thread's q pairs (j, j + HD/2) of pair index i = tid + 256 m.
+    RFP4_DEV void load_q(const AttnArgs &a, uint32_t kvh_, uint32_t row_)
+    {
+        const int tid = threadIdx.x;
+        kvh = kvh_;
+        row = row_;
+        G = a.n_heads / a.n_kv_heads; // <= GT
+        const float *qg = a.q + (size_t)row * a.q_rs + (size_t)(kvh * G) * HD;
+#pragma unroll
+        for (int m = 0; m < QPT; m++) {
+            const uint32_t i = (uint32_t)tid + 256u * (uint32_t)m;
+            const uint32_t g = i / HALF, j = i % HALF;
+            const bool in = g < G;
+            qa[m] = in ? attn_in<AG>(qg + g * HD + j) : 0.0f;
+            qb[m] = in ? attn_in<AG>(qg + g * HD + j + HALF) : 0.0f;
+        }
+    }
+
+    // Split geometry at sequence length seq_, the rope table column of the
+    // position, and every K/V load of sub-chunk 0.  False: this split is
+    // past the sequence (nothing to do).
+    RFP4_DEV bool issue(const AttnArgs &a, uint32_t kvh_, uint32_t split_, uint32_t row_, uint32_t seq_)
+    {
+        int tid = threadIdx.x;
+        if (AG) asm volatile("" : "+v"(tid)); // the persistent kernel's layer loop: no hoisted addresses
+        const int li = tid % LPT, slot = tid / LPT;
+        kvh = kvh_;
+        split = split_;
+        row = row_;
+        G = a.n_heads / a.n_kv_heads;
+        fused = a.cosv != nullptr;
+        seq = min(seq_, a.chunk * a.max_splits); // never read past the planned splits
+        nsplit = (seq + a.chunk - 1) / a.chunk;
+        if (split >= nsplit) return false;
+        t0 = split * a.chunk;
+        nt = min(seq, t0 + a.chunk) - t0;
+        nsub = (nt + CAPT - 1) / CAPT;
+        pos = seq - 1;
+        owner = fused && (pos >= t0) && (pos < t0 + nt);
+        kc = (const KT *)a.kc + (size_t)kvh * a.hs;
+        vc = (const KT *)a.vc + (size_t)kvh * a.hs;
+        cs = 1.0f;
+        sn = 0.0f;
+        if (fused) {
+            const uint32_t j = (uint32_t)tid % HALF;
+            cs = a.cosv[(size_t)pos * HALF + j];
+            sn = a.sinv[(size_t)pos * HALF + j];
+        }
+        // K and V rows of sub-chunk 0: token t0 + s*TPS + slot, lanes split
+        // the row.  Slots past the split re-read its last row (in bounds,
+        // finite; their scores are masked and their p is 0): no branch around
+        // the loads, so the wait for the rope tables does not wait for them.
+#pragma unroll
+        for (int s_ = 0; s_ < NSTEP; s_++) {
+            const uint32_t t_ = min((uint32_t)s_ * TPS + (uint32_t)slot, nt - 1u);
+            kr[s_] = load_nt16(kc + (size_t)(t0 + t_) * a.ts + (size_t)li * EPL);
+        }
+#pragma unroll
+        for (int s_ = 0; s_ < NSTEP; s_++) {
+            const uint32_t t_ = min((uint32_t)s_ * TPS + (uint32_t)slot, nt - 1u);
+            vr[s_] = load_nt16(vc + (size_t)(t0 + t_) * a.ts + (size_t)li * EPL);
+        }
+        return true;
+    }
+
+    RFP4_DEV void finish(const AttnArgs &a)
+    {
+        __shared__ __align__(16) float qs[GT][HD];
+        __shared__ __align__(16) float vred[4][GT][HD];
+        __shared__ float s_mx[2][4][GT], s_lred[4][GT], s_mfin[GT];
+        __shared__ KT knew[HD], vnew[HD];
+        const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+        const int li = tid % LPT, slot = tid / LPT;
+        float *orow = a.out + (size_t)row * a.out_rs;
+        float *prow = a.part + (size_t)row * a.n_heads * a.max_splits * (HD + 4);
+
+        // ---- q (rotated if fused) into LDS; the owner split appends k, v
+#pragma unroll
+        for (int m = 0; m < QPT; m++) {
+            const uint32_t i = (uint32_t)tid + 256u * (uint32_t)m;
+            if (i >= GT * HALF) break;
+            const uint32_t g = i / HALF, j = i % HALF;
+            float r0 = qa[m], r1 = qb[m];
+            if (fused) {
+                r0 = __fsub_rn(__fmul_rn(qa[m], cs), __fmul_rn(qb[m], sn));
+                r1 = __fadd_rn(__fmul_rn(qb[m], cs), __fmul_rn(qa[m], sn));
+            }
+            qs[g][j] = r0;
+            qs[g][j + HALF] = r1;
+        }
+        if (owner && (uint32_t)tid < HALF) {
+            // the current token's k and v, loaded by the owner split only (after
+            // its K/V stream, so no other split waits on them)
+            const float *kn = a.k_new + (size_t)kvh * HD, *vn = a.v_new + (size_t)kvh * HD;
+            const float kna = attn_in<AG>(kn + tid), knb = attn_in<AG>(kn + tid + HALF);
+            const float vna = attn_in<AG>(vn + tid), vnb = attn_in<AG>(vn + tid + HALF);
+            KT *kdst = (KT *)a.kc + (size_t)kvh * a.hs + (size_t)pos * a.ts;
+            KT *vdst = (KT *)a.vc + (size_t)kvh * a.hs + (size_t)pos * a.ts;
+            const KT r0 = KvTraits<KT>::from_f32(__fsub_rn(__fmul_rn(kna, cs), __fmul_rn(knb, sn)));
+            const KT r1 = KvTraits<KT>::from_f32(__fadd_rn(__fmul_rn(knb, cs), __fmul_rn(kna, sn)));
+            const KT w0 = KvTraits<KT>::from_f32(vna), w1 = KvTraits<KT>::from_f32(vnb);
+            knew[tid] = r0;
+            knew[tid + HALF] = r1;
+            vnew[tid] = w0;
+            vnew[tid + HALF] = w1;
+            kdst[tid] = r0;
+            kdst[tid + HALF] = r1;
+            vdst[tid] = w0;
+            vdst[tid + HALF] = w1;
+        }
+        __syncthreads();
+
+        float qv[GT][EPL];
+#pragma unroll
+        for (int g = 0; g < GT; g++)
+#pragma unroll
+            for (int e = 0; e < EPL; e += 4) {
+                const float4 v4 = *(const float4 *)&qs[g][li * EPL + e];
+                qv[g][e] = v4.x;
+                qv[g][e + 1] = v4.y;
+                qv[g][e + 2] = v4.z;
+                qv[g][e + 3] = v4.w;
+            }
+        const float scale = __fmul_rn(1.4426950408889634f, __fdiv_rn(1.0f, __fsqrt_rn((float)HD))); // log2(e) / sqrt(HD)
+        float acc[GT][EPL], lsum[GT], mrun[GT];
+#pragma unroll
+        for (int g = 0; g < GT; g++) {
+            lsum[g] = 0.0f;
+            mrun[g] = -3.402823466e38f;
+#pragma unroll
+            for (int e = 0; e < EPL; e++) acc[g][e] = 0.0f;
+        }
+
 #define RFP4_ATTN_LOAD(R, BASE, C)                                                              \
     do {                                                                                        \
         _Pragma("unroll") for (int s_ = 0; s_ < NSTEP; s_++) {                         \
@@ -287,202 +469,160 @@ RFP4_DEV void attn_body(const AttnArgs &a)
             R[s_] = load_nt16((BASE) + (size_t)(t0 + t_) * a.ts + (size_t)li * EPL);           \
         }                                                                                       \
     } while (0)
-    RFP4_ATTN_LOAD(kr, kc, 0u);
-    RFP4_ATTN_LOAD(vr, vc, 0u);
-
-    // ---- q (rotated if fused) into LDS; the owner split appends k, v
+        for (uint32_t c = 0; c < nsub; c++) {
+            const uint32_t tb = c * CAPT, ntc = min(CAPT, nt - tb);
+            if (owner && pos - t0 >= tb && pos - t0 < tb + ntc) {
+                // the thread holding position `pos` takes the freshly rotated row
+                const uint32_t tl = pos - t0 - tb;
+                if ((uint32_t)slot == tl % TPS) {
+                    const uint32_t s = tl / TPS;
+                    const uint4 kk = KvTraits<KT>::pack(knew + li * EPL), vv = KvTraits<KT>::pack(vnew + li * EPL);
 #pragma unroll
-    for (int m = 0; m < QPT; m++) {
-        const uint32_t i = (uint32_t)tid + 256u * (uint32_t)m;
-        if (i >= GT * HALF) break;
-        const uint32_t g = i / HALF, j = i % HALF;
-        float r0 = qa[m], r1 = qb[m];
-        if (fused) {
-            r0 = __fsub_rn(__fmul_rn(qa[m], cs), __fmul_rn(qb[m], sn));
-            r1 = __fadd_rn(__fmul_rn(qb[m], cs), __fmul_rn(qa[m], sn));
-        }
-        qs[g][j] = r0;
-        qs[g][j + HALF] = r1;
-    }
-    if (owner && (uint32_t)tid < HALF) {
-        // the current token's k and v, loaded by the owner split only (after
-        // its K/V stream, so no other split waits on them)
-        const float *kn = a.k_new + (size_t)kvh * HD, *vn = a.v_new + (size_t)kvh * HD;
-        const float kna = kn[tid], knb = kn[tid + HALF], vna = vn[tid], vnb = vn[tid + HALF];
-        KT *kdst = (KT *)a.kc + (size_t)kvh * a.hs + (size_t)pos * a.ts;
-        KT *vdst = (KT *)a.vc + (size_t)kvh * a.hs + (size_t)pos * a.ts;
-        const KT r0 = KvTraits<KT>::from_f32(__fsub_rn(__fmul_rn(kna, cs), __fmul_rn(knb, sn)));
-        const KT r1 = KvTraits<KT>::from_f32(__fadd_rn(__fmul_rn(knb, cs), __fmul_rn(kna, sn)));
-        const KT w0 = KvTraits<KT>::from_f32(vna), w1 = KvTraits<KT>::from_f32(vnb);
-        knew[tid] = r0;
-        knew[tid + HALF] = r1;
-        vnew[tid] = w0;
-        vnew[tid + HALF] = w1;
-        kdst[tid] = r0;
-        kdst[tid + HALF] = r1;
-        vdst[tid] = w0;
-        vdst[tid + HALF] = w1;
-    }
-    __syncthreads();
-
-    float qv[GT][EPL];
-#pragma unroll
-    for (int g = 0; g < GT; g++)
-#pragma unroll
-        for (int e = 0; e < EPL; e += 4) {
-            const float4 v4 = *(const float4 *)&qs[g][li * EPL + e];
-            qv[g][e] = v4.x;
-            qv[g][e + 1] = v4.y;
-            qv[g][e + 2] = v4.z;
-            qv[g][e + 3] = v4.w;
-        }
-    const float scale = __fmul_rn(1.4426950408889634f, __fdiv_rn(1.0f, __fsqrt_rn((float)HD))); // log2(e) / sqrt(HD)
-    float acc[GT][EPL], lsum[GT], mrun[GT];
-#pragma unroll
-    for (int g = 0; g < GT; g++) {
-        lsum[g] = 0.0f;
-        mrun[g] = -3.402823466e38f;
-#pragma unroll
-        for (int e = 0; e < EPL; e++) acc[g][e] = 0.0f;
-    }
-
-    for (uint32_t c = 0; c < nsub; c++) {
-        const uint32_t tb = c * CAPT, ntc = min(CAPT, nt - tb);
-        if (owner && pos - t0 >= tb && pos - t0 < tb + ntc) {
-            // the thread holding position `pos` takes the freshly rotated row
-            const uint32_t tl = pos - t0 - tb;
-            if ((uint32_t)slot == tl % TPS) {
-                const uint32_t s = tl / TPS;
-                const uint4 kk = KvTraits<KT>::pack(knew + li * EPL), vv = KvTraits<KT>::pack(vnew + li * EPL);
-#pragma unroll
-                for (int st = 0; st < NSTEP; st++)
-                    if ((uint32_t)st == s) {
-                        kr[st] = kk;
-                        vr[st] = vv;
-                    }
+                    for (int st = 0; st < NSTEP; st++)
+                        if ((uint32_t)st == s) {
+                            kr[st] = kk;
+                            vr[st] = vv;
+                        }
+                }
             }
-        }
 
-        // ---- scores of this sub-chunk (every lane of a row gets its row's
-        //      score), this wave's max per head, then the next sub-chunk's K loads
-        float sc[NSTEP][GT], mloc[GT];
+            // ---- scores of this sub-chunk (every lane of a row gets its row's
+            //      score), this wave's max per head, then the next sub-chunk's K loads
+            float sc[NSTEP][GT], mloc[GT];
 #pragma unroll
-        for (int g = 0; g < GT; g++) mloc[g] = -3.402823466e38f;
+            for (int g = 0; g < GT; g++) mloc[g] = -3.402823466e38f;
 #pragma unroll
-        for (int s = 0; s < NSTEP; s++) {
-            const bool valid = (uint32_t)s * TPS + (uint32_t)slot < ntc;
-            float kf[EPL];
-            KvTraits<KT>::widen(kr[s], kf);
+            for (int s = 0; s < NSTEP; s++) {
+                const bool valid = (uint32_t)s * TPS + (uint32_t)slot < ntc;
+                float kf[EPL];
+                KvTraits<KT>::widen(kr[s], kf);
+#pragma unroll
+                for (int g = 0; g < GT; g++) {
+                    float d = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < EPL; e++) d = fmaf(qv[g][e], kf[e], d);
+                    d = group_sum<LPT>(d) * scale;
+                    sc[s][g] = valid ? d : -3.402823466e38f;
+                    mloc[g] = fmaxf(mloc[g], sc[s][g]);
+                }
+            }
+            if (c + 1 < nsub) RFP4_ATTN_LOAD(kr, kc, c + 1);
+#pragma unroll
+            for (int g = 0; g < GT; g++) mloc[g] = slots_max<LPT>(mloc[g]);
+            if (lane == 0) {
+#pragma unroll
+                for (int g = 0; g < GT; g++) s_mx[c & 1u][wave][g] = mloc[g];
+            }
+            __syncthreads(); // s_mx is double-buffered: the next sub-chunk's writes wait for this barrier's successor
+
+            // ---- online softmax: m' = max(m, max_t s_t), acc and l scaled by
+            //      2^(m - m'), then p_t = 2^(s_t - m'), l += p_t, acc += p_t v_t (base 2)
 #pragma unroll
             for (int g = 0; g < GT; g++) {
-                float d = 0.0f;
+                const float mx = fmaxf(fmaxf(s_mx[c & 1u][0][g], s_mx[c & 1u][1][g]),
+                                       fmaxf(s_mx[c & 1u][2][g], s_mx[c & 1u][3][g]));
+                const float mnew = fmaxf(mrun[g], mx);
+                const float alpha = attn_exp2(mrun[g] - mnew);
+                mrun[g] = mnew;
+                lsum[g] *= alpha;
 #pragma unroll
-                for (int e = 0; e < EPL; e++) d = fmaf(qv[g][e], kf[e], d);
-                d = group_sum<LPT>(d) * scale;
-                sc[s][g] = valid ? d : -3.402823466e38f;
-                mloc[g] = fmaxf(mloc[g], sc[s][g]);
+                for (int e = 0; e < EPL; e++) acc[g][e] *= alpha;
             }
-        }
-        if (c + 1 < nsub) RFP4_ATTN_LOAD(kr, kc, c + 1);
 #pragma unroll
-        for (int g = 0; g < GT; g++) mloc[g] = slots_max<LPT>(mloc[g]);
-        if (lane == 0) {
+            for (int s = 0; s < NSTEP; s++) {
+                const bool valid = (uint32_t)s * TPS + (uint32_t)slot < ntc;
+                float vf[EPL];
+                KvTraits<KT>::widen(vr[s], vf);
 #pragma unroll
-            for (int g = 0; g < GT; g++) s_mx[c & 1u][wave][g] = mloc[g];
-        }
-        __syncthreads(); // s_mx is double-buffered: the next sub-chunk's writes wait for this barrier's successor
-
-        // ---- online softmax: m' = max(m, max_t s_t), acc and l scaled by
-        //      2^(m - m'), then p_t = 2^(s_t - m'), l += p_t, acc += p_t v_t (base 2)
+                for (int g = 0; g < GT; g++) {
+                    const float p = valid ? attn_exp2(sc[s][g] - mrun[g]) : 0.0f;
+                    lsum[g] += p;
 #pragma unroll
-        for (int g = 0; g < GT; g++) {
-            const float mx = fmaxf(fmaxf(s_mx[c & 1u][0][g], s_mx[c & 1u][1][g]),
-                                   fmaxf(s_mx[c & 1u][2][g], s_mx[c & 1u][3][g]));
-            const float mnew = fmaxf(mrun[g], mx);
-            const float alpha = attn_exp2(mrun[g] - mnew);
-            mrun[g] = mnew;
-            lsum[g] *= alpha;
-#pragma unroll
-            for (int e = 0; e < EPL; e++) acc[g][e] *= alpha;
-        }
-#pragma unroll
-        for (int s = 0; s < NSTEP; s++) {
-            const bool valid = (uint32_t)s * TPS + (uint32_t)slot < ntc;
-            float vf[EPL];
-            KvTraits<KT>::widen(vr[s], vf);
-#pragma unroll
-            for (int g = 0; g < GT; g++) {
-                const float p = valid ? attn_exp2(sc[s][g] - mrun[g]) : 0.0f;
-                lsum[g] += p;
-#pragma unroll
-                for (int e = 0; e < EPL; e++) acc[g][e] = fmaf(p, vf[e], acc[g][e]);
+                    for (int e = 0; e < EPL; e++) acc[g][e] = fmaf(p, vf[e], acc[g][e]);
+                }
             }
+            if (c + 1 < nsub) RFP4_ATTN_LOAD(vr, vc, c + 1);
         }
-        if (c + 1 < nsub) RFP4_ATTN_LOAD(vr, vc, c + 1);
-    }
 #undef RFP4_ATTN_LOAD
 
-    // ---- fold the token slots of each wave, then the four waves through LDS
+        // ---- fold the token slots of each wave, then the four waves through LDS
 #pragma unroll
-    for (int g = 0; g < GT; g++) {
-        lsum[g] = slots_sum<LPT>(lsum[g]);
+        for (int g = 0; g < GT; g++) {
+            lsum[g] = slots_sum<LPT>(lsum[g]);
 #pragma unroll
-        for (int e = 0; e < EPL; e++) acc[g][e] = slots_sum<LPT>(acc[g][e]);
-    }
-    if (lane < LPT) {
+            for (int e = 0; e < EPL; e++) acc[g][e] = slots_sum<LPT>(acc[g][e]);
+        }
+        if (lane < LPT) {
 #pragma unroll
-        for (int g = 0; g < GT; g++)
+            for (int g = 0; g < GT; g++)
 #pragma unroll
-            for (int e = 0; e < EPL; e += 4)
-                *(float4 *)&vred[wave][g][li * EPL + e] = make_float4(acc[g][e], acc[g][e + 1], acc[g][e + 2], acc[g][e + 3]);
-    }
-    if (lane == 0) {
+                for (int e = 0; e < EPL; e += 4)
+                    *(float4 *)&vred[wave][g][li * EPL + e] = make_float4(acc[g][e], acc[g][e + 1], acc[g][e + 2], acc[g][e + 3]);
+        }
+        if (lane == 0) {
 #pragma unroll
-        for (int g = 0; g < GT; g++) s_lred[wave][g] = lsum[g];
-    }
-    if (tid == 0) {
+            for (int g = 0; g < GT; g++) s_lred[wave][g] = lsum[g];
+        }
+        if (tid == 0) {
 #pragma unroll
-        for (int g = 0; g < GT; g++) s_mfin[g] = mrun[g];
-    }
-    __syncthreads();
+            for (int g = 0; g < GT; g++) s_mfin[g] = mrun[g];
+        }
+        __syncthreads();
 
-    if (nsplit == 1) {
-        // one split holds the whole sequence: normalise and write the heads' outputs
+        if (nsplit == 1) {
+            // one split holds the whole sequence: normalise and write the heads' outputs
+            for (uint32_t i = tid; i < G * HD; i += blockDim.x) {
+                const uint32_t g = i / HD, d = i % HD;
+                const float v = vred[0][g][d] + vred[1][g][d] + vred[2][g][d] + vred[3][g][d];
+                const float l = (s_lred[0][g] + s_lred[1][g]) + (s_lred[2][g] + s_lred[3][g]);
+                attn_out<AG>(orow + (size_t)(kvh * G + g) * HD + d, __fdiv_rn(v, l));
+            }
+            return;
+        }
+
+        // ---- write this split's partial state: [m, l, -, -, acc[HD]] per (head, split);
+        // the merge kernel launched next on the same stream combines them, or
+        // (counters given) the last split of this KV head to arrive does
+        const uint32_t stride = HD + 4;
+        const bool inmerge = a.counters != nullptr;
         for (uint32_t i = tid; i < G * HD; i += blockDim.x) {
-            const uint32_t g = i / HD, d = i % HD;
-            const float v = vred[0][g][d] + vred[1][g][d] + vred[2][g][d] + vred[3][g][d];
+            uint32_t g = i / HD, d = i % HD;
+            float v = vred[0][g][d] + vred[1][g][d] + vred[2][g][d] + vred[3][g][d];
+            size_t base = ((size_t)(kvh * G + g) * a.max_splits + split) * stride;
             const float l = (s_lred[0][g] + s_lred[1][g]) + (s_lred[2][g] + s_lred[3][g]);
-            orow[(size_t)(kvh * G + g) * HD + d] = __fdiv_rn(v, l);
+            if (inmerge || AG) {
+                attn_store_agent(prow + base + 4 + d, v);
+                if (d == 0) {
+                    attn_store_agent(prow + base, s_mfin[g]);
+                    attn_store_agent(prow + base + 1, l);
+                }
+            } else {
+                prow[base + 4 + d] = v;
+                if (d == 0) {
+                    prow[base] = s_mfin[g];
+                    prow[base + 1] = l;
+                }
+            }
         }
-        return;
+        if (!inmerge) return;
+        if (AG)
+            attn_merge_last_ordered<HD, GT, ATTN_PERSIST_MAX_SPLITS>(a, prow, kvh, G, nsplit);
+        else
+            attn_merge_last<HD, GT>(a, prow, kvh, G, nsplit);
     }
+};
 
-    // ---- write this split's partial state: [m, l, -, -, acc[HD]] per (head, split);
-    // the merge kernel launched next on the same stream combines them, or
-    // (counters given) the last split of this KV head to arrive does
-    const uint32_t stride = HD + 4;
-    const bool inmerge = a.counters != nullptr;
-    for (uint32_t i = tid; i < G * HD; i += blockDim.x) {
-        uint32_t g = i / HD, d = i % HD;
-        float v = vred[0][g][d] + vred[1][g][d] + vred[2][g][d] + vred[3][g][d];
-        size_t base = ((size_t)(kvh * G + g) * a.max_splits + split) * stride;
-        const float l = (s_lred[0][g] + s_lred[1][g]) + (s_lred[2][g] + s_lred[3][g]);
-        if (inmerge) {
-            attn_store_agent(prow + base + 4 + d, v);
-            if (d == 0) {
-                attn_store_agent(prow + base, s_mfin[g]);
-                attn_store_agent(prow + base + 1, l);
-            }
-        } else {
-            prow[base + 4 + d] = v;
-            if (d == 0) {
-                prow[base] = s_mfin[g];
-                prow[base + 1] = l;
-            }
-        }
-    }
-    if (!inmerge) return;
-    attn_merge_last<HD, GT>(a, prow, kvh, G, nsplit);
+template <int HD, typename KT, int GT>
+RFP4_DEV void attn_body(const AttnArgs &a)
+{
+    AttnSplit<HD, KT, GT, false> u;
+    const uint32_t kvh = blockIdx.x, split = blockIdx.y, row = blockIdx.z;
+    // loads that need no position first (q), then the position, the rope
+    // tables and the K/V stream, so the rotation of q overlaps the stream
+    u.load_q(a, kvh, row);
+    const uint32_t seq = (a.pos_ptr ? (uint32_t)(*a.pos_ptr + 1) : a.seq) + row;
+    if (!u.issue(a, kvh, split, row, seq)) return;
+    u.finish(a);
 }
 
 // Merge kernel body: grid (n_heads), launched after attn_body on the same

@@ -81,6 +81,11 @@ struct llama_engine {
     float *pf_x = nullptr, *pf_c = nullptr, *pf_a = nullptr, *pf_part = nullptr; // pf_part: decode-kernel test path only
     uint8_t *pf_codes = nullptr, *pf_scales = nullptr;
     uint32_t *pf_ids = nullptr;
+    // persistent decode (one cooperative launch for all layers of a step)
+    bool persist_ok = false, persist = false; // shape and device allow it / chosen
+    PersistLayer *p_layers = nullptr;       // device copy of the layer table
+    uint32_t *p_flags = nullptr, *p_err = nullptr;
+    uint32_t p_gen = 0, p_grid = 0, p_lds = 0;
 };
 
 static int dalloc(llama_engine *e, void **p, size_t bytes)
@@ -161,6 +166,113 @@ static int enqueue_step(llama_engine *e, uint32_t nsplit)
     if ((rc = gemv_launch_v(sn, RFP4_EPI_ARGMAX, la, s, e->gv[GV_LM]))) return rc;
     StepArgs sa{e->best, e->state, e->ids, e->last_tok, e->n_best, 0};
     return launch("rfp4_step", dim3(1), dim3(1024), s, &sa);
+}
+
+// ---------------------------------------------------------------- persistent decode
+// The shape rfp4_decode_layers_8b is compiled for (device/persist.h
+// PersistShape8B): Llama-3-8B widths at one workgroup of 256 threads per CU on
+// a 256-CU device; any layer count, vocabulary and context whose attention
+// splits fit the grid and the in-place merge.
+static const char *kPersistKernel = "rfp4_decode_layers_8b";
+static const uint32_t kPersistGrid = 256, kPersistMaxSplits = 32;
+
+static uint32_t persist_barriers(const llama_engine *e) { return 5u * e->c.n_layers - 1u; }
+
+static int persist_setup(llama_engine *e)
+{
+    const rfp4_model_config &c = e->c;
+    Runtime *rt = runtime();
+    if (c.dim != 4096 || c.n_heads != 32 || c.n_kv_heads != 8 || c.head_dim != 128 || c.ffn != 14336) return RFP4_OK;
+    if (c.scale_format != RFP4_SCALE_E8M0 || c.kv_format != RFP4_KV_F16) return RFP4_OK;
+    if ((uint32_t)rt->num_cus != kPersistGrid) return RFP4_OK;
+    if (e->attn_max_splits > kPersistMaxSplits || c.n_kv_heads * e->attn_max_splits > kPersistGrid) return RFP4_OK;
+    const uint32_t kmax = std::max(std::max(c.dim, qdim(c)), c.ffn);
+    e->p_lds = gemv_lds_bytes(kmax);
+    int per_cu = 0;
+    int rc = kernel_occupancy(kPersistKernel, 256, e->p_lds, &per_cu);
+    if (rc || per_cu < 1) return rc;
+    std::vector<PersistLayer> tab(c.n_layers);
+    for (uint32_t l = 0; l < c.n_layers; l++) {
+        const LayerW &w = e->L[l];
+        tab[l] = PersistLayer{w.qkv_c, w.qkv_s, w.o_c, w.o_s, w.gu_c, w.gu_s, w.d_c, w.d_s};
+    }
+    rc = dalloc_t(e, &e->p_layers, c.n_layers);
+    if (!rc) rc = hip_check(hipMemcpy(e->p_layers, tab.data(), tab.size() * sizeof(PersistLayer), hipMemcpyHostToDevice),
+                            "H2D layer table");
+    if (!rc) rc = dalloc_t(e, &e->p_flags, kPersistGrid);
+    if (!rc) rc = dalloc_t(e, &e->p_err, 1);
+    if (!rc) rc = fill_words(e->p_flags, kPersistGrid, 0u, e->stream);
+    if (!rc) rc = fill_words(e->p_err, 1, 0u, e->stream);
+    if (rc) return rc;
+    e->p_grid = kPersistGrid;
+    e->persist_ok = true; // available; the graph step stays the default (faster, measured)
+    return RFP4_OK;
+}
+
+// One decode step with every layer in the persistent kernel: embedding,
+// rfp4_decode_layers, LM head + argmax, cursor.
+static int enqueue_step_persist(llama_engine *e)
+{
+    const rfp4_model_config &c = e->c;
+    hipStream_t s = e->stream;
+    int rc;
+    if (!e->no_embed) {
+        EmbedArgs ea{e->embed, e->ids, e->state, e->x, c.dim, c.vocab, e->embed_bf16};
+        if ((rc = launch("rfp4_embed", dim3((c.dim + 255) / 256), dim3(256), s, &ea))) return rc;
+    }
+    if (e->p_gen > 0x40000000u) { // barrier generations restart from zero (stream order: no launch still polls)
+        if ((rc = fill_words(e->p_flags, e->p_grid, 0u, s))) return rc;
+        e->p_gen = 0;
+    }
+    PersistArgs pa{};
+    pa.layers = e->p_layers;
+    pa.norm_attn = e->norm_attn;
+    pa.norm_ffn = e->norm_ffn;
+    pa.kcache = e->kcache;
+    pa.vcache = e->vcache;
+    pa.kv_layer_elems = (uint64_t)c.n_kv_heads * e->max_seq_alloc * c.head_dim;
+    pa.cosv = e->cos_tab;
+    pa.sinv = e->sin_tab;
+    pa.state = e->state;
+    pa.x = e->x;
+    pa.qkv = e->qkv;
+    pa.att = e->attn_out;
+    pa.sw = e->sw;
+    pa.part = e->attn_part;
+    pa.counters = e->attn_counters;
+    pa.flags = e->p_flags;
+    pa.err = e->p_err;
+    pa.n_layers = c.n_layers;
+    pa.dim = c.dim;
+    pa.n_heads = c.n_heads;
+    pa.n_kv_heads = c.n_kv_heads;
+    pa.head_dim = c.head_dim;
+    pa.ffn = c.ffn;
+    pa.max_seq_alloc = e->max_seq_alloc;
+    pa.chunk = e->attn_chunk;
+    pa.max_splits = e->attn_max_splits;
+    pa.gen0 = e->p_gen;
+    pa.spin_limit = 1u << 20;
+    pa.eps = c.eps;
+    if ((rc = launch_coop(kPersistKernel, dim3(e->p_grid), dim3(256), s, &pa, e->p_lds))) return rc;
+    e->p_gen += persist_barriers(e);
+    GemvArgs la{e->lm_c, e->lm_s, e->x, e->logits, e->best, e->norm_final, c.vocab, c.dim, 0, c.eps};
+    if ((rc = gemv_launch_v(e->sname, RFP4_EPI_ARGMAX, la, s, e->gv[GV_LM]))) return rc;
+    StepArgs sa{e->best, e->state, e->ids, e->last_tok, e->n_best, 0};
+    return launch("rfp4_step", dim3(1), dim3(1024), s, &sa);
+}
+
+// A barrier of the persistent kernel that hit its spin limit leaves the
+// error word set: the step's results are not valid.
+static int persist_check(llama_engine *e)
+{
+    if (!e->persist_ok) return RFP4_OK;
+    uint32_t err = 0;
+    int rc = hip_check(hipMemcpyAsync(&err, e->p_err, 4, hipMemcpyDeviceToHost, e->stream), "D2H persist error");
+    if (!rc) rc = hip_check(hipStreamSynchronize(e->stream), "hipStreamSynchronize(persist error)");
+    if (rc) return rc;
+    if (err) return set_error(RFP4_E_HIP, "persistent decode: a grid barrier hit its spin limit (workgroups not co-resident)");
+    return RFP4_OK;
 }
 
 // ---------------------------------------------------------------- batched prefill
@@ -325,7 +437,7 @@ static int step_graph(llama_engine *e, uint32_t nsplit, hipGraphExec_t *out)
 // Step graphs for every position in [pos_first, pos_last].
 static int step_graphs_for(llama_engine *e, int64_t pos_first, int64_t pos_last)
 {
-    if (!e->use_graph) return RFP4_OK;
+    if (!e->use_graph || e->persist) return RFP4_OK;
     hipGraphExec_t g;
     for (uint32_t ns = splits_at(e, pos_first); ns <= splits_at(e, pos_last); ns++) {
         int rc = step_graph(e, ns, &g);
@@ -459,6 +571,7 @@ static int engine_alloc(const rfp4_model_config *cfg, llama_engine **out)
     if (!rc) rc = dalloc_t(e, &e->last_tok, 1);
     if (!rc) rc = fill_words((uint32_t *)e->state, sizeof(StepState) / 4, 0u, s);
     if (!rc) rc = fill_words(e->ids, e->ids_alloc, 0u, s);
+    if (!rc) rc = persist_setup(e);
     if (rc) {
         engine_free(e);
         return rc;
@@ -885,7 +998,9 @@ int llama_engine_run_steps(llama_engine *e, uint32_t n_steps)
     for (uint32_t i = 0; i < n_steps; i++) {
         const uint32_t ns = splits_at(e, e->h_pos + i);
         int rc;
-        if (e->use_graph) {
+        if (e->persist) {
+            rc = enqueue_step_persist(e);
+        } else if (e->use_graph) {
             hipGraphExec_t g;
             rc = step_graph(e, ns, &g);
             if (!rc) rc = hip_check(hipGraphLaunch(g, e->stream), "hipGraphLaunch");
@@ -911,7 +1026,8 @@ int llama_engine_time_steps(llama_engine *e, uint32_t n_steps, rfp4_kernel_time 
     std::vector<KernelTiming> rec;
     int rc = RFP4_OK;
     timing_install(&rec);
-    for (uint32_t i = 0; i < n_steps && !rc; i++) rc = enqueue_step(e, splits_at(e, e->h_pos + i));
+    for (uint32_t i = 0; i < n_steps && !rc; i++)
+        rc = e->persist ? enqueue_step_persist(e) : enqueue_step(e, splits_at(e, e->h_pos + i));
     timing_install(nullptr);
     if (!rc) rc = hip_check(hipStreamSynchronize(e->stream), "hipStreamSynchronize(timing)");
     *count = (uint32_t)rec.size();
@@ -937,7 +1053,8 @@ int llama_engine_read_ids(llama_engine *e, uint32_t *ids, uint32_t count)
     if (count > e->ids_alloc) return set_error(RFP4_E_CAPACITY, "count %u > %u", count, e->ids_alloc);
     int rc = hip_check(hipMemcpyAsync(ids, e->ids, (size_t)count * 4, hipMemcpyDeviceToHost, e->stream), "D2H ids");
     if (rc) return rc;
-    return hip_check(hipStreamSynchronize(e->stream), "hipStreamSynchronize(ids)");
+    rc = hip_check(hipStreamSynchronize(e->stream), "hipStreamSynchronize(ids)");
+    return rc ? rc : persist_check(e);
 }
 
 int llama_generate(llama_engine *e, const uint32_t *prompt, uint32_t n_prompt, uint32_t pos0, uint32_t n_new,
@@ -979,6 +1096,19 @@ int llama_engine_use_graph(llama_engine *e, int enable)
     e->use_graph = enable != 0;
     return RFP4_OK;
 }
+
+int llama_engine_use_persistent(llama_engine *e, int enable)
+{
+    if (!e) return set_error(RFP4_E_INVALID, "null engine");
+    if (enable && !e->persist_ok)
+        return set_error(RFP4_E_SHAPE, "persistent decode needs the Llama-3-8B widths, E8M0 weights, fp16 caches, "
+                                       "a 256-CU device and at most %u attention splits", kPersistMaxSplits);
+    int rc = hip_check(hipStreamSynchronize(e->stream), "hipStreamSynchronize(mode)");
+    if (!rc) e->persist = enable != 0;
+    return rc;
+}
+
+int llama_engine_persistent(const llama_engine *e) { return e && e->persist ? 1 : 0; }
 
 int llama_engine_weight(llama_engine *e, int layer, int proj, const uint8_t **codes, const uint8_t **scales,
                         size_t *code_bytes, size_t *scale_bytes)

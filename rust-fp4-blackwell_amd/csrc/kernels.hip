@@ -12,6 +12,7 @@
 #include "device/gemm_skinny.h"
 #include "device/prefill.h"
 #include "device/attn_prefill.h"
+#include "device/persist.h"
 
 #define K256 extern "C" __global__ __launch_bounds__(256)
 #define K512 extern "C" __global__ __launch_bounds__(512)
@@ -149,6 +150,10 @@ GEMM_SKINNY_KERNEL(32, 2, 1)
 GEMM_SKINNY_KERNEL(32, 2, 2)
 GEMM_SKINNY_KERNEL(64, 4, 1)
 GEMM_SKINNY_KERNEL(64, 4, 2)
+
+// ---- persistent decode of every layer of a step, one workgroup per CU
+// (device/persist.h): rfp4_decode_layers_<shape>
+K256 void rfp4_decode_layers_8b(PersistArgs a) { decode_layers_body<PersistShape8B>(a); }
 
 // ---- batched prefill row kernels (device/prefill.h)
 K256 void rfp4_embed_rows(RowsArgs a) { embed_rows_body(a); }

@@ -162,6 +162,45 @@ int launch(const char *name, dim3 grid, dim3 block, hipStream_t s, void *args, u
                      name);
 }
 
+int launch_coop(const char *name, dim3 grid, dim3 block, hipStream_t s, void *args, unsigned shmem)
+{
+    Runtime *rt = g_rt;
+    if (!rt) return set_error(RFP4_E_NOT_INIT, "rfp4_init has not been called");
+    auto it = rt->fns.find(name);
+    if (it == rt->fns.end()) return set_error(RFP4_E_HIP, "kernel %s is not in the code object", name);
+    void *params[] = {args};
+    KernelTiming k{it->first.c_str(), nullptr, nullptr};
+    int rc = RFP4_OK;
+    if (t_timing) {
+        rc = hip_check(hipEventCreate(&k.start), "hipEventCreate");
+        if (!rc) rc = hip_check(hipEventCreate(&k.stop), "hipEventCreate");
+        if (!rc) rc = hip_check(hipEventRecord(k.start, s), "hipEventRecord");
+    }
+    if (!rc)
+        rc = hip_check(hipModuleLaunchCooperativeKernel(it->second, grid.x, grid.y, grid.z, block.x, block.y, block.z, shmem,
+                                                        s, params),
+                       name);
+    if (t_timing) {
+        if (!rc) rc = hip_check(hipEventRecord(k.stop, s), "hipEventRecord");
+        if (rc) {
+            if (k.start) hipEventDestroy(k.start);
+            if (k.stop) hipEventDestroy(k.stop);
+            return rc;
+        }
+        t_timing->push_back(k);
+    }
+    return rc;
+}
+
+int kernel_occupancy(const char *name, int block, unsigned shmem, int *per_cu)
+{
+    Runtime *rt = g_rt;
+    if (!rt) return set_error(RFP4_E_NOT_INIT, "rfp4_init has not been called");
+    auto it = rt->fns.find(name);
+    if (it == rt->fns.end()) return set_error(RFP4_E_HIP, "kernel %s is not in the code object", name);
+    return hip_check(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(per_cu, it->second, block, shmem), name);
+}
+
 } // namespace rfp4
 
 using namespace rfp4;
@@ -357,7 +396,7 @@ int fill_words(uint32_t *p, uint64_t n_words, uint32_t value, hipStream_t s)
 static bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
 // LDS of the VALU GEMV: x at 36 floats per 32-value chunk (device/gemv.h).
-static uint32_t gemv_lds_bytes(uint32_t k) { return (k / 32u) * 36u * 4u; }
+uint32_t gemv_lds_bytes(uint32_t k) { return (k / 32u) * 36u * 4u; }
 
 int gemv_check(uint32_t n, uint32_t k, const void *w, const void *sc, const float *x, const float *y)
 {

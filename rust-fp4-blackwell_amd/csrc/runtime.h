@@ -32,6 +32,13 @@ Runtime *runtime();
 int set_error(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 int hip_check(hipError_t e, const char *what);
 int launch(const char *name, dim3 grid, dim3 block, hipStream_t s, void *args, unsigned shmem = 0);
+// Cooperative launch (every workgroup resident at once, or an error): for
+// kernels with grid barriers.  Timed like launch() while a record list is
+// installed (events recorded around the launch on the stream).
+int launch_coop(const char *name, dim3 grid, dim3 block, hipStream_t s, void *args, unsigned shmem);
+// Workgroups of `name` with `block` threads and `shmem` dynamic LDS bytes
+// that fit on one CU at once.
+int kernel_occupancy(const char *name, int block, unsigned shmem, int *per_cu);
 
 // Per-launch timing: while a record list is installed on this thread, every
 // launch() goes through hipExtModuleLaunchKernel with its own start and stop
@@ -51,6 +58,9 @@ struct GemvVariant {
 // The variant a launch of this shape gets now (honours this thread's
 // rfp4_debug_gemv_* overrides); an engine fixes its variants at creation.
 GemvVariant gemv_variant(uint32_t n, uint32_t k, int epi, bool f32scale);
+// Dynamic LDS of a GEMV's x staging for reduction length k (36 floats per
+// 32-value chunk, device/gemv.h).
+uint32_t gemv_lds_bytes(uint32_t k);
 inline uint32_t gemv_grid(uint32_t n, const GemvVariant &v) { return (n + (uint32_t)(v.W * v.R) - 1) / (uint32_t)(v.W * v.R); }
 int gemv_launch_v(const char *scale_name, int epi, const GemvArgs &args, hipStream_t s, const GemvVariant &v);
 int gemv_launch(const char *scale_name, int epi, const GemvArgs &args, hipStream_t s);

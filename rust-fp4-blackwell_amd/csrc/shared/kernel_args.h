@@ -201,6 +201,31 @@ typedef struct GemmArgs {
     uint32_t m, n, k, kz;
 } GemmArgs;
 
+// Persistent decode of every layer of one step (device/persist.h): one
+// workgroup per CU, grid barriers between the stages of a layer.
+typedef struct PersistLayer {
+    const uint8_t *qkv_c, *qkv_s, *o_c, *o_s, *gu_c, *gu_s, *d_c, *d_s; // E8M0 MXFP4, as the engine stacks them
+} PersistLayer;
+
+typedef struct PersistArgs {
+    const PersistLayer *layers;           // [n_layers], device memory
+    const uint16_t *norm_attn, *norm_ffn; // fp16 [n_layers][dim]
+    void *kcache, *vcache;                // fp16; layer l starts kv_layer_elems * l elements in
+    uint64_t kv_layer_elems;
+    const float *cosv, *sinv;             // rope tables [pos][head_dim/2]
+    const StepState *state;               // the step's position
+    float *x;                             // residual stream [dim], in and out
+    float *qkv, *att, *sw;                // stage outputs [nq + 2 nkv][hd], [nq][hd], [ffn]
+    float *part;                          // split states [n_heads][max_splits][head_dim + 4]
+    uint32_t *counters;                   // [n_kv_heads] merge arrivals, zero between launches
+    uint32_t *flags;                      // [gridDim.x] barrier generations (monotonic)
+    uint32_t *err;                        // nonzero: a barrier hit its spin limit
+    uint32_t n_layers, dim, n_heads, n_kv_heads, head_dim, ffn;
+    uint32_t max_seq_alloc, chunk, max_splits;
+    uint32_t gen0, spin_limit;            // generation before this launch's first barrier
+    float eps;
+} PersistArgs;
+
 typedef struct MmaTileArgs {
     const uint32_t *a;    // per-lane A registers
     const uint32_t *b;

@@ -143,6 +143,8 @@ _SIGS = {
     "llama_engine_use_graph": (I32, [P, I32]),
     "llama_engine_weight": (I32, [P, I32, I32, C.POINTER(P), C.POINTER(P), C.POINTER(SZ), C.POINTER(SZ)]),
     "llama_engine_kv": (I32, [P, I32, C.POINTER(P), C.POINTER(P), C.POINTER(SZ)]),
+    "llama_engine_use_persistent": (I32, [P, I32]),
+    "llama_engine_persistent": (I32, [P]),
     "llama_engine_prefill_buffers": (I32, [P, C.POINTER(P), C.POINTER(P), C.POINTER(P), C.POINTER(P), C.POINTER(P),
                                            C.POINTER(U32)]),
     "llama_engine_weight_bytes": (U64, [P]),
@@ -632,6 +634,25 @@ class Engine:
 
     def use_graph(self, on: bool):
         check(load().llama_engine_use_graph(self.h, int(on)))
+
+    def use_persistent(self, on: bool):
+        check(load().llama_engine_use_persistent(self.h, int(on)))
+
+    @property
+    def persistent(self) -> bool:
+        return bool(load().llama_engine_persistent(self.h))
+
+    @property
+    def persistent_available(self) -> bool:
+        """True where use_persistent(True) succeeds (the shape it is compiled for)."""
+        if self.persistent:
+            return True
+        try:
+            self.use_persistent(True)
+        except Rfp4Error:
+            return False
+        self.use_persistent(False)
+        return True
 
     def weight(self, layer: int, proj: int):
         c, s, cb, sb = P(), P(), SZ(), SZ()

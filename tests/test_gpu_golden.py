@@ -71,10 +71,12 @@ def test_config2_kernel_fixtures(rf, orc, stream):
     assert (rel > 1e-4).sum() == 0, rel.max()
 
 
-def _engine_tokens(rf, fx):
+def _engine_tokens(rf, fx, persistent=None):
     cfg = dict(fx["config"])
     eng = rf.Engine(rf.model_config(**cfg), fx["seed"])
     try:
+        if persistent is not None:
+            eng.use_persistent(persistent)
         assert _sha(eng.weight_host(-1, 0)[0]) == fx["hashes"]["lm_codes"]
         assert _sha(eng.weight_host(0, 0)[0]) == fx["hashes"]["l0_wq_codes"]
         assert _sha(eng.weight_host(0, 6)[1]) == fx["hashes"]["l0_wd_scales"]
@@ -100,9 +102,11 @@ def test_config3_tinyllama_tokens(rf):
     _check_tokens(_engine_tokens(rf, fx), fx)
 
 
-def test_config4_llama3_8b_tokens(rf):
+@pytest.mark.parametrize("persistent", [True, False])
+def test_config4_llama3_8b_tokens(rf, persistent):
     """Llama-3-8B architecture, random MXFP4 weights, fp16 KV pre-filled to
-    4096 positions, 128 greedy steps from token 1: identical to the oracle."""
+    4096 positions, 128 greedy steps from token 1: identical to the oracle,
+    with the persistent step (one launch for all layers) and the graph step."""
     with open(os.path.join(GOLDEN, "llama3_8b_tokens.json")) as f:
         fx = json.load(f)
-    _check_tokens(_engine_tokens(rf, fx), fx)
+    _check_tokens(_engine_tokens(rf, fx, persistent), fx)
