@@ -251,6 +251,27 @@ def pmc_probe(rf, which):
                       "copy_write_bytes": 4 * COPY_FLOATS}), flush=True)
 
 
+def trace_tiny_eager(rf, steps=64):
+    """The TinyLlama-1.1B decode launched kernel by kernel (no step graph) for
+    a rocprofv3 kernel trace: a 16-token prompt then `steps` greedy steps in
+    the ROCTx range tinyllama_decode_eager.  (Tracing the graph replays of
+    this model aborted inside the runtime's graph launch under the profiler;
+    the untraced graph replays of the same path pass.)"""
+    cfg = rf.model_config("tinyllama-1.1b", max_seq=16 + steps + 8)
+    eng = rf.Engine(cfg, SEED)
+    eng.use_graph(False)
+    prompt = np.random.default_rng(16).integers(0, cfg.vocab, 16).astype(np.uint32)
+    eng.begin(prompt, 0, 16 + steps + 1)
+    eng.run_steps(15)
+    eng.stream.synchronize()
+    with ROCTX.range("tinyllama_decode_eager"):
+        eng.run_steps(steps)
+        eng.stream.synchronize()
+    ids = eng.read_ids(16 + steps)
+    eng.close()
+    print(json.dumps({"trace_probe": "tinyllama_decode_eager", "steps": steps, "last_token": int(ids[-1])}), flush=True)
+
+
 TRAFFIC_JSON = os.path.join(ROOT, "profiles", "decode_llama3-8b_traffic.json")
 
 
@@ -573,6 +594,8 @@ def main():
     ap.add_argument("--no-prefill", action="store_true", help="skip the batched prefill figure")
     ap.add_argument("--prefill-tokens", type=int, default=512, help="prompt length of the batched prefill figure")
     ap.add_argument("--pmc-probe", choices=["decode", "gemm"], help="only the launch sequence of a counter pass")
+    ap.add_argument("--trace-tiny-eager", action="store_true",
+                    help="only the TinyLlama decode launched kernel by kernel (for a kernel trace)")
     ap.add_argument("--summarize-trace", nargs="+", metavar="DIR", help="summarise rocprofv3 kernel traces")
     ap.add_argument("--summarize-pmc", nargs="+", metavar="DIR", help="summarise rocprofv3 counter passes")
     args = ap.parse_args()
@@ -594,6 +617,9 @@ def main():
     rf.init(0)
     if args.pmc_probe:
         pmc_probe(rf, args.pmc_probe)
+        return
+    if args.trace_tiny_eager:
+        trace_tiny_eager(rf)
         return
     # ---- config 4: Llama-3-8B decode at batch 1, ctx 4096
     max_seq = PREFILL + args.warmup + args.steps + TIMED_STEPS + 8
