@@ -132,7 +132,11 @@ int kv_append_f16(rfp4_stream_t stream, uint32_t n, uint32_t off, const float *s
 int attn_decode(rfp4_stream_t stream, uint32_t n_heads, uint32_t n_kv_heads, uint32_t seq, const float *q,
                 const float *kc, const float *vc, float *out);
 /* attn_decode over fp16 K/V with head_dim 64 or 128 and any token / head
- * strides (elements): element (t, kvh, d) at t*token_stride + kvh*head_stride + d. */
+ * strides (elements): element (t, kvh, d) at t*token_stride + kvh*head_stride + d.
+ * attn_decode and attn_decode_f16 keep their split states (and the in-kernel
+ * merge's arrival counters) in one library workspace per device: calls that
+ * overlap on one device (two streams, two threads) race; serialise them on
+ * one stream.  Engines have workspaces of their own. */
 int attn_decode_f16(rfp4_stream_t stream, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
                     uint32_t seq, const float *q, const uint16_t *kc, const uint16_t *vc, uint64_t token_stride,
                     uint64_t head_stride, float *out);
