@@ -208,6 +208,10 @@ int rfp4_debug_attn_chunk(uint32_t chunk);
  * split of each KV head inside the attention kernel wherever it can (at most
  * 8 splits).  No reference counterpart. */
 int rfp4_debug_attn_merge(int mode);
+/* Test hook (this thread): query-head slices per KV head of the decode
+ * attention of engines created afterwards (0 = automatic, 1, 2, 4, 8; a
+ * value that does not divide the group means 1). */
+int rfp4_debug_attn_head_split(int hs);
 /* Test hook: the batched prefill's attention on this thread: 0 = the
  * matrix-core prefill kernel, 1 = the decode kernel, one grid row per prompt
  * row.  No reference counterpart. */

@@ -155,7 +155,7 @@ RFP4_DEV float attn_load_agent(const float *p) { return __hip_atomic_load(p, __A
 // weights 2^(m_i - M) and L, then each output is sum_i w_i acc_i / L with the
 // splits in order.  One round trip of loads.
 template <int HD, int GT>
-RFP4_DEV void attn_merge_last(const AttnArgs &a, const float *prow, uint32_t kvh, uint32_t G, uint32_t nsplit)
+RFP4_DEV void attn_merge_last(const AttnArgs &a, const float *prow, uint32_t cidx, uint32_t hbase, uint32_t G, uint32_t nsplit)
 {
     constexpr int S = ATTN_INMERGE_MAX_SPLITS, OPT = (GT * HD + 255) / 256; // outputs per thread (max)
     __shared__ uint32_t s_last;
@@ -166,25 +166,25 @@ RFP4_DEV void attn_merge_last(const AttnArgs &a, const float *prow, uint32_t kvh
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // this thread's states have landed
     __syncthreads();
     if (tid == 0) {
-        const uint32_t old = __hip_atomic_fetch_add(a.counters + kvh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t old = __hip_atomic_fetch_add(a.counters + cidx, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_last = old + 1u == nsplit ? 1u : 0u;
     }
     __syncthreads();
     if (!s_last) return;
-    if (tid == 0) __hip_atomic_store(a.counters + kvh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); // for the next launch
+    if (tid == 0) __hip_atomic_store(a.counters + cidx, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); // for the next launch
     // split values of this thread's outputs i = tid + 256 j
     float v[OPT][S];
 #pragma unroll
     for (int j = 0; j < OPT; j++) {
         const uint32_t i = (uint32_t)tid + 256u * (uint32_t)j;
         const uint32_t g = i / HD, d = i % HD;
-        const float *hp = prow + (size_t)(kvh * G + min(g, G - 1u)) * a.max_splits * stride + 4 + d;
+        const float *hp = prow + (size_t)(hbase + min(g, G - 1u)) * a.max_splits * stride + 4 + d;
 #pragma unroll
         for (int sp = 0; sp < S; sp++) v[j][sp] = (g < G && (uint32_t)sp < nsplit) ? attn_load_agent(hp + (size_t)sp * stride) : 0.0f;
     }
     // weights per head (one wave per head; lane = split)
     for (uint32_t g = (uint32_t)wave; g < G; g += 4) {
-        const float *hp = prow + (size_t)(kvh * G + g) * a.max_splits * stride;
+        const float *hp = prow + (size_t)(hbase + g) * a.max_splits * stride;
         const bool in = (uint32_t)lane < nsplit;
         const float m = in ? attn_load_agent(hp + (size_t)lane * stride) : -3.402823466e38f;
         const float l = in ? attn_load_agent(hp + (size_t)lane * stride + 1) : 0.0f;
@@ -215,7 +215,7 @@ RFP4_DEV void attn_merge_last(const AttnArgs &a, const float *prow, uint32_t kvh
             const float t = fmaf(w[sp], v[j][sp], acc);
             acc = (uint32_t)sp < nsplit ? t : acc;
         }
-        a.out[(size_t)(kvh * G + g) * HD + d] = __fdiv_rn(acc, s_L[g]);
+        a.out[(size_t)(hbase + g) * HD + d] = __fdiv_rn(acc, s_L[g]);
     }
 }
 
@@ -243,7 +243,8 @@ RFP4_DEV void attn_out(float *p, float v)
 // 256 / HD) per partial p with one FMA chain each, then the partials in p
 // order, divided by L.
 template <int HD, int GT, int S>
-RFP4_DEV void attn_merge_last_ordered(const AttnArgs &a, const float *prow, uint32_t kvh, uint32_t G, uint32_t nsplit)
+RFP4_DEV void attn_merge_last_ordered(const AttnArgs &a, const float *prow, uint32_t cidx, uint32_t hbase, uint32_t G,
+                                      uint32_t nsplit)
 {
     constexpr int P = 256 / HD, OPT = (GT * HD + 255) / 256, NJ = (S + P - 1) / P;
     static_assert(S <= 64, "one split per lane");
@@ -255,23 +256,23 @@ RFP4_DEV void attn_merge_last_ordered(const AttnArgs &a, const float *prow, uint
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // this thread's states have landed
     __syncthreads();
     if (tid == 0) {
-        const uint32_t old = __hip_atomic_fetch_add(a.counters + kvh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t old = __hip_atomic_fetch_add(a.counters + cidx, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         s_last = old + 1u == nsplit ? 1u : 0u;
     }
     __syncthreads();
     if (!s_last) return;
-    if (tid == 0) __hip_atomic_store(a.counters + kvh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); // for the next launch
+    if (tid == 0) __hip_atomic_store(a.counters + cidx, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); // for the next launch
     float v[OPT][S];
 #pragma unroll
     for (int j = 0; j < OPT; j++) {
         const uint32_t i = (uint32_t)tid + 256u * (uint32_t)j;
         const uint32_t g = i / HD, d = i % HD;
-        const float *hp = prow + (size_t)(kvh * G + min(g, G - 1u)) * a.max_splits * stride + 4 + d;
+        const float *hp = prow + (size_t)(hbase + min(g, G - 1u)) * a.max_splits * stride + 4 + d;
 #pragma unroll
         for (int sp = 0; sp < S; sp++) v[j][sp] = (g < G && (uint32_t)sp < nsplit) ? attn_load_agent(hp + (size_t)sp * stride) : 0.0f;
     }
     for (uint32_t g = (uint32_t)wave; g < G; g += 4) {
-        const float *hp = prow + (size_t)(kvh * G + g) * a.max_splits * stride;
+        const float *hp = prow + (size_t)(hbase + g) * a.max_splits * stride;
         const bool in = (uint32_t)lane < nsplit;
         const float m = in ? attn_load_agent(hp + (size_t)lane * stride) : -3.402823466e38f;
         const float l = in ? attn_load_agent(hp + (size_t)lane * stride + 1) : 0.0f;
@@ -301,7 +302,7 @@ RFP4_DEV void attn_merge_last_ordered(const AttnArgs &a, const float *prow, uint
             }
             out = p == 0 ? acc : out + acc;
         }
-        attn_store_agent(a.out + (size_t)(kvh * G + g) * HD + d, __fdiv_rn(out, s_L[g]));
+        attn_store_agent(a.out + (size_t)(hbase + g) * HD + d, __fdiv_rn(out, s_L[g]));
     }
 }
 
@@ -326,17 +327,34 @@ struct AttnSplit {
     uint4 kr[NSTEP], vr[NSTEP];
     float cs, sn;
     uint32_t kvh, split, row, G, seq, nsplit, t0, nt, nsub, pos;
-    bool fused, owner;
+    uint32_t hbase, cidx; // first query head of this workgroup, its merge-counter index
+    bool fused, owner, writer;
+
+    // Workgroup x index -> KV head and query-head slice: with head_split HS,
+    // x = hg * n_kv_heads + kvh takes query heads hg*G .. hg*G + G - 1 of the
+    // KV head's group (G = group / HS); the HS workgroups of one KV head have
+    // indices n_kv_heads apart (the same XCD under round-robin dispatch), and
+    // slice 0 writes the appended K/V row.
+    RFP4_DEV void heads(const AttnArgs &a, uint32_t x)
+    {
+        const uint32_t hs = a.head_split > 1u ? a.head_split : 1u;
+        const uint32_t gfull = a.n_heads / a.n_kv_heads;
+        kvh = x % a.n_kv_heads;
+        const uint32_t hg = x / a.n_kv_heads;
+        G = gfull / hs;
+        hbase = kvh * gfull + hg * G;
+        cidx = x;
+        writer = hg == 0u;
+    }
     const KT *kc, *vc;
 
     // This thread's q pairs (j, j + HD/2) of pair index i = tid + 256 m.
-    RFP4_DEV void load_q(const AttnArgs &a, uint32_t kvh_, uint32_t row_)
+    RFP4_DEV void load_q(const AttnArgs &a, uint32_t x, uint32_t row_)
     {
         const int tid = threadIdx.x;
-        kvh = kvh_;
+        heads(a, x);
         row = row_;
-        G = a.n_heads / a.n_kv_heads; // <= GT
-        const float *qg = a.q + (size_t)row * a.q_rs + (size_t)(kvh * G) * HD;
+        const float *qg = a.q + (size_t)row * a.q_rs + (size_t)hbase * HD;
 #pragma unroll
         for (int m = 0; m < QPT; m++) {
             const uint32_t i = (uint32_t)tid + 256u * (uint32_t)m;
@@ -350,15 +368,14 @@ struct AttnSplit {
     // Split geometry at sequence length seq_, the rope table column of the
     // position, and every K/V load of sub-chunk 0.  False: this split is
     // past the sequence (nothing to do).
-    RFP4_DEV bool issue(const AttnArgs &a, uint32_t kvh_, uint32_t split_, uint32_t row_, uint32_t seq_)
+    RFP4_DEV bool issue(const AttnArgs &a, uint32_t x, uint32_t split_, uint32_t row_, uint32_t seq_)
     {
         int tid = threadIdx.x;
         if (AG) asm volatile("" : "+v"(tid)); // the persistent kernel's layer loop: no hoisted addresses
         const int li = tid % LPT, slot = tid / LPT;
-        kvh = kvh_;
+        heads(a, x);
         split = split_;
         row = row_;
-        G = a.n_heads / a.n_kv_heads;
         fused = a.cosv != nullptr;
         seq = min(seq_, a.chunk * a.max_splits); // never read past the planned splits
         nsplit = (seq + a.chunk - 1) / a.chunk;
@@ -434,10 +451,12 @@ struct AttnSplit {
             knew[tid + HALF] = r1;
             vnew[tid] = w0;
             vnew[tid + HALF] = w1;
-            kdst[tid] = r0;
-            kdst[tid + HALF] = r1;
-            vdst[tid] = w0;
-            vdst[tid + HALF] = w1;
+            if (writer) {
+                kdst[tid] = r0;
+                kdst[tid + HALF] = r1;
+                vdst[tid] = w0;
+                vdst[tid + HALF] = w1;
+            }
         }
         __syncthreads();
 
@@ -575,7 +594,7 @@ struct AttnSplit {
                 const uint32_t g = i / HD, d = i % HD;
                 const float v = vred[0][g][d] + vred[1][g][d] + vred[2][g][d] + vred[3][g][d];
                 const float l = (s_lred[0][g] + s_lred[1][g]) + (s_lred[2][g] + s_lred[3][g]);
-                attn_out<AG>(orow + (size_t)(kvh * G + g) * HD + d, __fdiv_rn(v, l));
+                attn_out<AG>(orow + (size_t)(hbase + g) * HD + d, __fdiv_rn(v, l));
             }
             return;
         }
@@ -588,7 +607,7 @@ struct AttnSplit {
         for (uint32_t i = tid; i < G * HD; i += blockDim.x) {
             uint32_t g = i / HD, d = i % HD;
             float v = vred[0][g][d] + vred[1][g][d] + vred[2][g][d] + vred[3][g][d];
-            size_t base = ((size_t)(kvh * G + g) * a.max_splits + split) * stride;
+            size_t base = ((size_t)(hbase + g) * a.max_splits + split) * stride;
             const float l = (s_lred[0][g] + s_lred[1][g]) + (s_lred[2][g] + s_lred[3][g]);
             if (inmerge || AG) {
                 attn_store_agent(prow + base + 4 + d, v);
@@ -606,9 +625,9 @@ struct AttnSplit {
         }
         if (!inmerge) return;
         if (AG)
-            attn_merge_last_ordered<HD, GT, ATTN_PERSIST_MAX_SPLITS>(a, prow, kvh, G, nsplit);
+            attn_merge_last_ordered<HD, GT, ATTN_PERSIST_MAX_SPLITS>(a, prow, cidx, hbase, G, nsplit);
         else
-            attn_merge_last<HD, GT>(a, prow, kvh, G, nsplit);
+            attn_merge_last<HD, GT>(a, prow, cidx, hbase, G, nsplit);
     }
 };
 
@@ -616,12 +635,12 @@ template <int HD, typename KT, int GT>
 RFP4_DEV void attn_body(const AttnArgs &a)
 {
     AttnSplit<HD, KT, GT, false> u;
-    const uint32_t kvh = blockIdx.x, split = blockIdx.y, row = blockIdx.z;
+    const uint32_t x = blockIdx.x, split = blockIdx.y, row = blockIdx.z; // x: KV head and query-head slice
     // loads that need no position first (q), then the position, the rope
     // tables and the K/V stream, so the rotation of q overlaps the stream
-    u.load_q(a, kvh, row);
+    u.load_q(a, x, row);
     const uint32_t seq = (a.pos_ptr ? (uint32_t)(*a.pos_ptr + 1) : a.seq) + row;
-    if (!u.issue(a, kvh, split, row, seq)) return;
+    if (!u.issue(a, x, split, row, seq)) return;
     u.finish(a);
 }
 

@@ -65,6 +65,7 @@ struct llama_engine {
     uint32_t attn_chunk = 64, attn_max_splits = 1;
     uint32_t *attn_counters = nullptr; // arrival counters of the in-kernel attention merge (zero between steps)
     int attn_merge_mode = 0;           // merge policy fixed at creation (rfp4_debug_attn_merge)
+    uint32_t attn_head_split = 0;      // query-head slices per KV head (0: per grid, attn_head_split_for)
     StepState *state = nullptr;
     uint32_t *ids = nullptr, *last_tok = nullptr;
     uint32_t ids_alloc = 0;
@@ -154,6 +155,7 @@ static int enqueue_step(llama_engine *e, uint32_t nsplit)
         aa.n_heads = c.n_heads; aa.n_kv_heads = c.n_kv_heads; aa.head_dim = hd; aa.seq = 0;
         aa.chunk = e->attn_chunk; aa.max_splits = e->attn_max_splits;
         aa.counters = attn_inmerge_mode(e->attn_merge_mode, nsplit) ? e->attn_counters : nullptr;
+        aa.head_split = e->attn_head_split;
         if ((rc = attn_launch(aa, e->kvb == 2 ? 1 : 0, s, e->attn_chunk * nsplit, 1))) return rc;
         GemvArgs oa{w.o_c, w.o_s, e->attn_out, e->x, nullptr, nullptr, c.dim, qd, 0, 0.0f};
         if ((rc = gemv_launch_v(sn, RFP4_EPI_RESIDUAL, oa, s, e->gv[GV_O]))) return rc;
@@ -563,8 +565,13 @@ static int engine_alloc(const rfp4_model_config *cfg, llama_engine **out)
     if (!rc) rc = dalloc_t(e, &e->best, e->n_best);
     if (!rc) rc = dalloc_t(e, &e->attn_part, (size_t)c.n_heads * e->attn_max_splits * (hd + 4));
     e->attn_merge_mode = attn_merge_mode();
-    if (!rc) rc = dalloc_t(e, &e->attn_counters, c.n_kv_heads);
-    if (!rc) rc = fill_words(e->attn_counters, c.n_kv_heads, 0u, s);
+    {
+        const uint32_t g = c.n_heads / c.n_kv_heads, hs = (uint32_t)attn_head_split_mode();
+        e->attn_head_split = hs == 0u ? 0u : (g % hs == 0u ? hs : 1u);
+    }
+    // one arrival counter per attention workgroup column (KV head x query-head slice)
+    if (!rc) rc = dalloc_t(e, &e->attn_counters, c.n_heads);
+    if (!rc) rc = fill_words(e->attn_counters, c.n_heads, 0u, s);
     if (!rc) rc = dalloc(e, (void **)&e->state, sizeof(StepState));
     e->ids_alloc = c.max_seq + 2;
     if (!rc) rc = dalloc_t(e, &e->ids, e->ids_alloc);

@@ -65,6 +65,9 @@ inline uint32_t gemv_grid(uint32_t n, const GemvVariant &v) { return (n + (uint3
 int gemv_launch_v(const char *scale_name, int epi, const GemvArgs &args, hipStream_t s, const GemvVariant &v);
 int gemv_launch(const char *scale_name, int epi, const GemvArgs &args, hipStream_t s);
 int attn_launch(const AttnArgs &args, int kv_f16, hipStream_t s, uint32_t max_seq_for_grid, uint32_t rows);
+// Query-head slices per KV head for an attention grid of `splits` splits
+// (args.head_split = 0 asks attn_launch for this).
+uint32_t attn_head_split_for(uint32_t n_heads, uint32_t n_kv_heads, uint32_t splits, uint32_t num_cus);
 // One-row attention over caller K/V with split states in `part` (at least
 // n_heads * splits * (head_dim + 4) floats, checked); allow_inmerge = false
 // always merges with the second kernel (no counters, nothing that must start
@@ -90,6 +93,7 @@ uint32_t attn_sub_chunk(uint32_t head_dim, uint32_t elem_bytes, uint32_t group);
 bool attn_inmerge(uint32_t max_splits);
 int attn_merge_mode();                           // this thread's rfp4_debug_attn_merge setting
 int prefill_attn_mode();                         // this thread's rfp4_debug_prefill_attn setting
+int attn_head_split_mode();                      // this thread's rfp4_debug_attn_head_split setting
 int prefill_stop();                              // this thread's rfp4_debug_prefill_stop setting
 bool attn_inmerge_mode(int mode, uint32_t splits); // attn_inmerge under an explicit setting
 constexpr uint32_t kAttnInmergeMaxSplits = 8;

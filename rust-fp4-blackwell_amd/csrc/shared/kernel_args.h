@@ -82,10 +82,13 @@ typedef struct AttnArgs {
     // writes out + r*out_rs, sees seq + r positions (causal), and owns its own
     // workspace slice of n_heads*max_splits*(head_dim+4) floats.  One row: 0, 0.
     uint32_t q_rs, out_rs;
-    // In-kernel merge (one query row): arrival counters per KV head, zero
-    // between launches; the last split of a KV head merges.  Null = the
-    // merge kernel runs after this one.
+    // In-kernel merge (one query row): arrival counters per workgroup column
+    // (KV head x query-head slice), zero between launches; the last split of
+    // a column merges.  Null = the merge kernel runs after this one.
     uint32_t *counters;
+    // Query-head slices per KV head (grid x = head_split * n_kv_heads; 0 or 1:
+    // every workgroup serves the KV head's whole group).
+    uint32_t head_split, pad2;
 } AttnArgs;
 
 // Causal attention of the batched prefill (device/attn_prefill.h): prompt

@@ -117,3 +117,39 @@ def test_engine_attn_merge_modes_tokens(rf, orc, cfg, mode):
     cpu, margins = ref.generate(prompt, 0, 30)
     assert list(gpu) == list(cpu), f"gpu {list(gpu)}\ncpu {list(cpu)}\nmargins {margins}"
     eng.close()
+
+
+G8E = dict(dim=256, n_layers=2, n_heads=8, n_kv_heads=1, head_dim=64, ffn=512, vocab=1024,
+           theta=10000.0, eps=1e-5, max_seq=200)  # 8 query heads per KV head
+
+
+@pytest.mark.parametrize("cfg,slices", [(TINY128, (1, 2, 4)), (G8E, (1, 2, 4, 8))])
+@pytest.mark.parametrize("merge", [1, 2])
+def test_engine_attn_head_slices_bit_identical(rf, orc, cfg, slices, merge):
+    """Query-head slices per KV head (rfp4_debug_attn_head_split): each
+    attention workgroup serves group/slices query heads of its KV head; the
+    per-head arithmetic is unchanged, so tokens and logits are bit-identical
+    for every slice count, with the splits merged by the second kernel (1) or
+    in the attention kernel (2), and the tokens are the oracle's."""
+    seed = 0x51CE
+    prompt = [2, 9, 77, 401, 5, 6, 7]
+    outs = []
+    for hs in slices:
+        rf.check(rf.load().rfp4_debug_attn_head_split(hs))
+        rf.check(rf.load().rfp4_debug_attn_merge(merge))
+        rf.debug_attn_chunk(cfg["max_seq"] // 6 + 1)  # 6 splits over the context
+        try:
+            eng = _engine(rf, cfg, seed)
+        finally:
+            rf.debug_attn_chunk(0)
+            rf.check(rf.load().rfp4_debug_attn_merge(0))
+            rf.check(rf.load().rfp4_debug_attn_head_split(0))
+        toks = eng.generate(prompt, 0, 40)
+        outs.append((np.array(toks), eng.logits()))
+        eng.close()
+    for t, l in outs[1:]:
+        np.testing.assert_array_equal(t, outs[0][0])
+        np.testing.assert_array_equal(l, outs[0][1])
+    ref = orc.Model(cfg, seed)
+    cpu, margins = ref.generate(prompt, 0, 40)
+    assert list(outs[0][0]) == list(cpu), f"gpu {list(outs[0][0])}\ncpu {list(cpu)}\nmargins {margins}"
