@@ -501,7 +501,7 @@ static int engine_alloc(const rfp4_model_config *cfg, llama_engine **out)
     const size_t sb = e->sb;
     rc = hip_check(hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking), "hipStreamCreate");
     // attention split plan over the full cache capacity
-    e->attn_chunk = attn_chunk_for(c.n_kv_heads, c.max_seq, rt->num_cus, hd, 2u, c.n_heads / c.n_kv_heads);
+    e->attn_chunk = attn_chunk_for(c.n_kv_heads, c.max_seq, rt->num_cus, hd, e->kvb, c.n_heads / c.n_kv_heads);
     e->attn_max_splits = (c.max_seq + e->attn_chunk - 1) / e->attn_chunk;
     e->max_seq_alloc = (e->attn_chunk * e->attn_max_splits + 255u) / 256u * 256u;
     hipStream_t s = e->stream;
