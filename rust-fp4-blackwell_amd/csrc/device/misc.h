@@ -82,6 +82,7 @@ RFP4_DEV void step_body(const StepArgs &a)
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     if (lane == 0) red[wave] = best;
     __syncthreads();
+    __shared__ uint32_t s_next;
     if (threadIdx.x == 0) {
         unsigned long long b = red[0];
         for (int w = 1; w < nw; w++) b = red[w] > b ? red[w] : b;
@@ -90,10 +91,20 @@ RFP4_DEV void step_body(const StepArgs &a)
         *a.last_tok = tok;
         uint32_t nxt = (uint32_t)st.step + 1u;
         if (nxt >= st.n_prompt && nxt < st.ids_cap) a.ids[nxt] = tok;
+        // the next step's input token: a prompt token, else this step's argmax
+        s_next = nxt < st.n_prompt ? a.ids[nxt] : tok;
         st.step += 1;
         st.pos += 1;
         *a.state = st;
     }
+    if (!a.embed) return;
+    // the next step's embedding (rfp4_embed's gather, done here so the step
+    // graph has one launch less)
+    __syncthreads();
+    uint32_t t = s_next;
+    if (t >= a.vocab) t = 0;
+    const uint16_t *row = a.embed + (size_t)t * a.dim;
+    for (uint32_t i = threadIdx.x; i < a.dim; i += blockDim.x) a.x[i] = half_bits_to_f32(row[i], a.bf16 != 0);
 }
 
 // ---------------------------------------------------------------- OCP MX block quantizer

@@ -137,10 +137,6 @@ static int enqueue_step(llama_engine *e, uint32_t nsplit)
     hipStream_t s = e->stream;
     const uint32_t qd = qdim(c), kvd = kvdim(c), hd = c.head_dim;
     int rc;
-    if (!e->no_embed) {
-        EmbedArgs ea{e->embed, e->ids, e->state, e->x, c.dim, c.vocab, e->embed_bf16};
-        if ((rc = launch("rfp4_embed", dim3((c.dim + 255) / 256), dim3(256), s, &ea))) return rc;
-    }
     const char *sn = e->sname;
     for (uint32_t l = 0; l < c.n_layers; l++) {
         const LayerW &w = e->L[l];
@@ -166,7 +162,8 @@ static int enqueue_step(llama_engine *e, uint32_t nsplit)
     }
     GemvArgs la{e->lm_c, e->lm_s, e->x, e->logits, e->best, e->norm_final, c.vocab, c.dim, 0, c.eps};
     if ((rc = gemv_launch_v(sn, RFP4_EPI_ARGMAX, la, s, e->gv[GV_LM]))) return rc;
-    StepArgs sa{e->best, e->state, e->ids, e->last_tok, e->n_best, 0};
+    StepArgs sa{e->best, e->state, e->ids, e->last_tok, e->n_best, 0,
+                e->no_embed ? nullptr : e->embed, e->x, c.dim, c.vocab, e->embed_bf16, 0};
     return launch("rfp4_step", dim3(1), dim3(1024), s, &sa);
 }
 
@@ -218,10 +215,6 @@ static int enqueue_step_persist(llama_engine *e)
     const rfp4_model_config &c = e->c;
     hipStream_t s = e->stream;
     int rc;
-    if (!e->no_embed) {
-        EmbedArgs ea{e->embed, e->ids, e->state, e->x, c.dim, c.vocab, e->embed_bf16};
-        if ((rc = launch("rfp4_embed", dim3((c.dim + 255) / 256), dim3(256), s, &ea))) return rc;
-    }
     if (e->p_gen > 0x40000000u) { // barrier generations restart from zero (stream order: no launch still polls)
         if ((rc = fill_words(e->p_flags, e->p_grid, 0u, s))) return rc;
         e->p_gen = 0;
@@ -260,7 +253,8 @@ static int enqueue_step_persist(llama_engine *e)
     e->p_gen += persist_barriers(e);
     GemvArgs la{e->lm_c, e->lm_s, e->x, e->logits, e->best, e->norm_final, c.vocab, c.dim, 0, c.eps};
     if ((rc = gemv_launch_v(e->sname, RFP4_EPI_ARGMAX, la, s, e->gv[GV_LM]))) return rc;
-    StepArgs sa{e->best, e->state, e->ids, e->last_tok, e->n_best, 0};
+    StepArgs sa{e->best, e->state, e->ids, e->last_tok, e->n_best, 0,
+                e->no_embed ? nullptr : e->embed, e->x, c.dim, c.vocab, e->embed_bf16, 0};
     return launch("rfp4_step", dim3(1), dim3(1024), s, &sa);
 }
 
@@ -460,6 +454,15 @@ static void drop_graphs(llama_engine *e)
 
 // Embedding lookup per step (llama_run) or a carried activation (the
 // llama_decode harness): switching drops the graphs of the other mode.
+// The first step's embedding row (later steps' rows are gathered by the
+// previous step's cursor kernel).
+static int embed_first(llama_engine *e)
+{
+    const rfp4_model_config &c = e->c;
+    EmbedArgs ea{e->embed, e->ids, e->state, e->x, c.dim, c.vocab, e->embed_bf16};
+    return launch("rfp4_embed", dim3((c.dim + 255) / 256), dim3(256), e->stream, &ea);
+}
+
 static int set_embed_mode(llama_engine *e, bool no_embed)
 {
     if (e->no_embed == no_embed) return RFP4_OK;
@@ -936,6 +939,7 @@ int llama_engine_begin(llama_engine *e, const uint32_t *prompt, uint32_t n_promp
     rc = hip_check(hipMemcpy(e->ids, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice), "H2D prompt");
     StepState st{(int32_t)pos0, 0, n_prompt, ids_cap};
     if (!rc) rc = hip_check(hipMemcpy(e->state, &st, sizeof st, hipMemcpyHostToDevice), "H2D cursor");
+    if (!rc) rc = embed_first(e);
     if (rc) return rc;
     e->h_pos = pos0;
     e->h_step = 0;

@@ -192,6 +192,11 @@ typedef struct StepArgs {
     uint32_t *ids;
     uint32_t *last_tok;
     uint32_t n_best, pad;
+    // optional (embed non-null): the next step's embedding row into x, as
+    // rfp4_embed would gather it at the start of that step
+    const uint16_t *embed;
+    float *x;
+    uint32_t dim, vocab, bf16, pad2;
 } StepArgs;
 
 // Scaled-MFMA MXFP4 GEMM: C[M][N] = A[M][K] * W[N][K]^T, both MXFP4 (E2M1 +
