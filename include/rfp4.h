@@ -203,10 +203,13 @@ int rfp4_debug_gemm_plan(int tile, int kz);
  * on this thread (0 = automatic).  No reference counterpart. */
 int rfp4_debug_attn_chunk(uint32_t chunk);
 /* Test hook: how later one-row attention launches on this thread (and
- * engines created by it) merge their splits: 0 = automatic (in-kernel up to
- * 8 splits, else a second kernel), 1 = always a second kernel, 2 = the last
- * split of each KV head inside the attention kernel wherever it can (at most
- * 8 splits).  No reference counterpart. */
+ * engines created by it) merge their splits: 0 = automatic (in-kernel by the
+ * last split up to 8 splits; engines: from tagged states up to 32; else a
+ * second kernel), 1 = always a second kernel, 2 = the last split of each KV
+ * head inside the attention kernel wherever it can (at most 8 splits), 3 =
+ * engines only: the first splits of each workgroup column inside the
+ * attention kernel, polling tagged split states (2 to 32 splits; other
+ * launches as 0).  No reference counterpart. */
 int rfp4_debug_attn_merge(int mode);
 /* Test hook (this thread): query-head slices per KV head of the decode
  * attention of engines created afterwards (0 = automatic, 1, 2, 4, 8; a

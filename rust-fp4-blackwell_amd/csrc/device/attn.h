@@ -149,6 +149,11 @@ RFP4_DEV float attn_load_agent(const float *p) { return __hip_atomic_load(p, __A
 #define ATTN_INMERGE_MAX_SPLITS 8
 // Splits the persistent decode kernel merges in place (one round of loads).
 #define ATTN_PERSIST_MAX_SPLITS 32
+// Splits per batch of the merge kernel's loads.
+#define ATTN_MERGE_BATCH 64
+// Splits of the tagged in-kernel merge (at most ATTN_MERGE_BATCH: the merge
+// kernel's summation order is one batch).
+#define ATTN_TAG_MAX_SPLITS 32
 // The last split's merge (at most ATTN_INMERGE_MAX_SPLITS splits): every
 // thread first issues the loads of its outputs' split values (the G x HD
 // outputs, 256 per pass), one wave per query head turns (m_i, l_i) into the
@@ -217,6 +222,134 @@ RFP4_DEV void attn_merge_last(const AttnArgs &a, const float *prow, uint32_t cid
         }
         a.out[(size_t)(hbase + g) * HD + d] = __fdiv_rn(acc, s_L[g]);
     }
+}
+
+// ---- tagged in-kernel merge (engine decode, one query row, at most
+// ATTN_TAG_MAX_SPLITS splits): no arrival counter and no wait for store
+// acknowledgements.  Every word of a split state is one 64-bit relaxed
+// atomic holding the float's bits and a tag, the launch's sequence length,
+// which differs between the steps of a generation (the engine clears the
+// per-layer workspace before a generation starts, so no word of an earlier
+// one carries a current tag).  A load that returns the tag returns the value
+// stored with it (a single atomic object), so the merging workgroup polls
+// every word it needs until it carries the tag, with no ordering between
+// words and no fence.  In the language memory model this rests only on the
+// coherence of each atomic object and on relaxed stores becoming visible in
+// finite time.  Split g of a workgroup column merges its query head g (and
+// g + nsplit, ... below G) after finishing its own split; at most n_heads
+// workgroups wait, each only for workgroups that never wait, so the launch
+// completes whenever the device holds n_heads + 1 of them at once.  A poll
+// that reaches the spin limit writes NaN outputs and sets *err.  The sums
+// follow the merge kernel's order (attn_merge_body), so the outputs are
+// bit-identical to the two-launch step.
+#define ATTN_TAG_SPIN_LIMIT (1u << 20)
+RFP4_DEV void attn_store_tagged(unsigned long long *p, float v, uint32_t tag)
+{
+    __hip_atomic_store(p, ((unsigned long long)tag << 32) | __float_as_uint(v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+RFP4_DEV unsigned long long attn_load_tagged(const unsigned long long *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+RFP4_DEV bool attn_tag_ok(unsigned long long w, uint32_t tag) { return (uint32_t)(w >> 32) == tag; }
+RFP4_DEV float attn_tag_val(unsigned long long w) { return __uint_as_float((uint32_t)w); }
+
+// Merge of one query head: hp = its first state word, out = its HD outputs.
+// Wave 0 first polls (m, l) of split `lane` until every split has published
+// them (small polls, no traffic against the splits still streaming K/V), then
+// thread (d = tid % HD, p = tid / HD) loads the acc words of splits p, p + P,
+// ... (P = 256 / HD) and reloads any that do not carry the tag yet.
+// Measured against polling every word from the start (Llama-3-8B, 29 splits):
+// 10.4 against 10.8 us per launch.
+template <int HD>
+RFP4_DEV void attn_merge_tagged(const AttnArgs &a, const unsigned long long *hp, float *out, uint32_t nsplit, uint32_t tag)
+{
+    constexpr uint32_t P = 256 / HD, STRIDE = HD + 4, NB = ATTN_TAG_MAX_SPLITS / P;
+    static_assert(ATTN_TAG_MAX_SPLITS <= ATTN_MERGE_BATCH && ATTN_TAG_MAX_SPLITS <= 64, "one batch, one split per lane");
+    __shared__ __align__(16) float t_w[ATTN_TAG_MAX_SPLITS]; // split i at (i % P) * NB + i / P
+    __shared__ float t_part[P][HD];
+    __shared__ float t_L;
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid)); // no per-lane address of the merge is hoisted above the split's loop
+    const int lane = tid & 63, wave = tid >> 6;
+    const uint32_t d = (uint32_t)tid % HD, p = (uint32_t)tid / HD;
+    __syncthreads(); // a previous head's merge in this workgroup has read t_w and t_part
+    // (m, l) of every split first (wave 0, one split per lane), then the acc words
+    const bool ml = wave == 0 && (uint32_t)lane < nsplit;
+    unsigned long long mw = 0ull, lw = 0ull;
+    bool timeout = false;
+    if (wave == 0) {
+        if (ml) {
+            mw = attn_load_tagged(hp + (size_t)lane * STRIDE);
+            lw = attn_load_tagged(hp + (size_t)lane * STRIDE + 1);
+        }
+        for (uint32_t spin = 0;; spin++) {
+            const bool stale = ml && !(attn_tag_ok(mw, tag) && attn_tag_ok(lw, tag));
+            if (!__any(stale)) break;
+            if (spin >= ATTN_TAG_SPIN_LIMIT) {
+                timeout = true;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+            if (ml && !attn_tag_ok(mw, tag)) mw = attn_load_tagged(hp + (size_t)lane * STRIDE);
+            if (ml && !attn_tag_ok(lw, tag)) lw = attn_load_tagged(hp + (size_t)lane * STRIDE + 1);
+        }
+    }
+    __syncthreads();
+    unsigned long long v[NB];
+#pragma unroll
+    for (int j = 0; j < (int)NB; j++) {
+        const uint32_t sp = p + P * (uint32_t)j;
+        v[j] = sp < nsplit ? attn_load_tagged(hp + (size_t)sp * STRIDE + 4 + d) : 0ull;
+    }
+    for (uint32_t spin = 0;; spin++) {
+        bool stale = false;
+#pragma unroll
+        for (int j = 0; j < (int)NB; j++) stale = stale || (p + P * (uint32_t)j < nsplit && !attn_tag_ok(v[j], tag));
+        if (!stale) break;
+        if (spin >= ATTN_TAG_SPIN_LIMIT) {
+            timeout = true;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int j = 0; j < (int)NB; j++) {
+            const uint32_t sp = p + P * (uint32_t)j;
+            if (sp < nsplit && !attn_tag_ok(v[j], tag)) v[j] = attn_load_tagged(hp + (size_t)sp * STRIDE + 4 + d);
+        }
+    }
+    if (wave == 0) {
+        const float m = ml ? attn_tag_val(mw) : -3.402823466e38f;
+        const float M = wave_max(m);
+        const float w = ml ? attn_exp2(m - M) : 0.0f;
+        if (ml) t_w[((uint32_t)lane % P) * NB + (uint32_t)lane / P] = w;
+        const float L = wave_sum(ml ? fmaf(attn_tag_val(lw), w, 0.0f) : 0.0f);
+        if (lane == 0) t_L = L;
+    }
+    const bool bad = __syncthreads_or(timeout);
+    float w[NB];
+#pragma unroll
+    for (int j = 0; j < (int)NB; j += 4) {
+        const float4 w4 = *(const float4 *)&t_w[p * NB + (uint32_t)j];
+        w[j] = w4.x;
+        w[j + 1] = w4.y;
+        w[j + 2] = w4.z;
+        w[j + 3] = w4.w;
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < (int)NB; j++) {
+        const float t = fmaf(w[j], attn_tag_val(v[j]), acc);
+        acc = p + P * (uint32_t)j < nsplit ? t : acc;
+    }
+    if (p > 0) t_part[p][d] = acc;
+    __syncthreads();
+    if (p == 0) {
+#pragma unroll
+        for (uint32_t r = 1; r < P; r++) acc += t_part[r][d];
+        out[d] = bad ? __builtin_nanf("") : __fdiv_rn(acc, t_L);
+    }
+    if (bad && tid == 0 && a.err) __hip_atomic_store(a.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // Reads and writes of values that the persistent decode kernel produces and
@@ -309,8 +442,11 @@ RFP4_DEV void attn_merge_last_ordered(const AttnArgs &a, const float *prow, uint
 // One split of one KV head: the phases of the attention workgroup.  The
 // stand-alone kernel runs load_q, issue and finish back to back; the
 // persistent decode kernel issues the K/V stream (issue) before the grid
-// barrier that publishes q, then loads q and finishes.
-template <int HD, typename KT, int GT, bool AG>
+// barrier that publishes q, then loads q and finishes.  TAG: the split
+// states go to the tagged workspace and are merged by the first splits of
+// each workgroup column (kernels of their own: the merge's registers stay out
+// of the other kernels' allocation).
+template <int HD, typename KT, int GT, bool AG, bool TAG = false>
 struct AttnSplit {
     static constexpr int EPL = KvTraits<KT>::EPL;
     static constexpr int LPT = HD / EPL;          // lanes per token row
@@ -601,8 +737,27 @@ struct AttnSplit {
 
         // ---- write this split's partial state: [m, l, -, -, acc[HD]] per (head, split);
         // the merge kernel launched next on the same stream combines them, or
-        // (counters given) the last split of this KV head to arrive does
+        // (counters given) the last split of this KV head to arrive does, or
+        // (tagged workspace given) the first splits of the column do
         const uint32_t stride = HD + 4;
+        if (TAG) {
+            const uint32_t tag = seq;
+            for (uint32_t i = tid; i < G * HD; i += blockDim.x) {
+                const uint32_t g = i / HD, d = i % HD;
+                const float v = vred[0][g][d] + vred[1][g][d] + vred[2][g][d] + vred[3][g][d];
+                const float l = (s_lred[0][g] + s_lred[1][g]) + (s_lred[2][g] + s_lred[3][g]);
+                unsigned long long *tp = a.tagged + ((size_t)(hbase + g) * a.tag_splits + split) * stride;
+                attn_store_tagged(tp + 4 + d, v, tag);
+                if (d == 0) {
+                    attn_store_tagged(tp, s_mfin[g], tag);
+                    attn_store_tagged(tp + 1, l, tag);
+                }
+            }
+            for (uint32_t g = split; g < G; g += nsplit)
+                attn_merge_tagged<HD>(a, a.tagged + (size_t)(hbase + g) * a.tag_splits * stride, orow + (size_t)(hbase + g) * HD,
+                                      nsplit, tag);
+            return;
+        }
         const bool inmerge = a.counters != nullptr;
         for (uint32_t i = tid; i < G * HD; i += blockDim.x) {
             uint32_t g = i / HD, d = i % HD;
@@ -631,10 +786,10 @@ struct AttnSplit {
     }
 };
 
-template <int HD, typename KT, int GT>
+template <int HD, typename KT, int GT, bool TAG = false>
 RFP4_DEV void attn_body(const AttnArgs &a)
 {
-    AttnSplit<HD, KT, GT, false> u;
+    AttnSplit<HD, KT, GT, false, TAG> u;
     const uint32_t x = blockIdx.x, split = blockIdx.y, row = blockIdx.z; // x: KV head and query-head slice
     // loads that need no position first (q), then the position, the rope
     // tables and the K/V stream, so the rotation of q overlaps the stream
@@ -659,7 +814,6 @@ RFP4_DEV void attn_body(const AttnArgs &a)
 // partition-major (split p + P j at p * NB + j) so that a thread reads its NB
 // weights as float4s; the rest is FMAs and one LDS combine of the P partial
 // sums.  Up to ATTN_MERGE_BATCH splits this is one round trip of loads.
-#define ATTN_MERGE_BATCH 64
 template <int HD>
 RFP4_DEV void attn_merge_body(const AttnArgs &a)
 {

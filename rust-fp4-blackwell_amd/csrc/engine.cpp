@@ -65,6 +65,11 @@ struct llama_engine {
     uint32_t attn_chunk = 64, attn_max_splits = 1;
     uint32_t *attn_counters = nullptr; // arrival counters of the in-kernel attention merge (zero between steps)
     int attn_merge_mode = 0;           // merge policy fixed at creation (rfp4_debug_attn_merge)
+    // tagged attention merge: per layer [n_heads][attn_tag_splits][head_dim + 4] 64-bit words,
+    // cleared before each generation (tags are sequence lengths)
+    unsigned long long *attn_tagged = nullptr;
+    uint32_t attn_tag_splits = 0;
+    size_t attn_tag_layer = 0; // words per layer
     uint32_t attn_head_split = 0;      // query-head slices per KV head (0: per grid, attn_head_split_for)
     StepState *state = nullptr;
     uint32_t *ids = nullptr, *last_tok = nullptr;
@@ -85,7 +90,8 @@ struct llama_engine {
     // persistent decode (one cooperative launch for all layers of a step)
     bool persist_ok = false, persist = false; // shape and device allow it / chosen
     PersistLayer *p_layers = nullptr;       // device copy of the layer table
-    uint32_t *p_flags = nullptr, *p_err = nullptr;
+    uint32_t *p_flags = nullptr;
+    uint32_t *p_err = nullptr; // set by a device-side wait that hit its spin limit (grid barrier, tagged merge)
     uint32_t p_gen = 0, p_grid = 0, p_lds = 0;
 };
 
@@ -150,7 +156,13 @@ static int enqueue_step(llama_engine *e, uint32_t nsplit)
         aa.ts = hd; aa.hs = (uint64_t)e->max_seq_alloc * hd;
         aa.n_heads = c.n_heads; aa.n_kv_heads = c.n_kv_heads; aa.head_dim = hd; aa.seq = 0;
         aa.chunk = e->attn_chunk; aa.max_splits = e->attn_max_splits;
-        aa.counters = attn_inmerge_mode(e->attn_merge_mode, nsplit) ? e->attn_counters : nullptr;
+        if (e->attn_tagged && attn_tagged_mode(e->attn_merge_mode, nsplit)) {
+            aa.tagged = e->attn_tagged + (size_t)l * e->attn_tag_layer;
+            aa.tag_splits = e->attn_tag_splits;
+            aa.err = e->p_err;
+        } else {
+            aa.counters = attn_inmerge_mode(e->attn_merge_mode, nsplit) ? e->attn_counters : nullptr;
+        }
         aa.head_split = e->attn_head_split;
         if ((rc = attn_launch(aa, e->kvb == 2 ? 1 : 0, s, e->attn_chunk * nsplit, 1))) return rc;
         GemvArgs oa{w.o_c, w.o_s, e->attn_out, e->x, nullptr, nullptr, c.dim, qd, 0, 0.0f};
@@ -199,9 +211,7 @@ static int persist_setup(llama_engine *e)
     if (!rc) rc = hip_check(hipMemcpy(e->p_layers, tab.data(), tab.size() * sizeof(PersistLayer), hipMemcpyHostToDevice),
                             "H2D layer table");
     if (!rc) rc = dalloc_t(e, &e->p_flags, kPersistGrid);
-    if (!rc) rc = dalloc_t(e, &e->p_err, 1);
     if (!rc) rc = fill_words(e->p_flags, kPersistGrid, 0u, e->stream);
-    if (!rc) rc = fill_words(e->p_err, 1, 0u, e->stream);
     if (rc) return rc;
     e->p_grid = kPersistGrid;
     e->persist_ok = true; // available; the graph step stays the default (faster, measured)
@@ -258,17 +268,28 @@ static int enqueue_step_persist(llama_engine *e)
     return launch("rfp4_step", dim3(1), dim3(1024), s, &sa);
 }
 
-// A barrier of the persistent kernel that hit its spin limit leaves the
-// error word set: the step's results are not valid.
-static int persist_check(llama_engine *e)
+// A grid barrier of the persistent kernel or a tagged attention merge that
+// hit its spin limit leaves the error word set: the steps' results are not
+// valid.
+static int wait_check(llama_engine *e)
 {
-    if (!e->persist_ok) return RFP4_OK;
+    if (!e->persist_ok && !e->attn_tagged) return RFP4_OK;
     uint32_t err = 0;
-    int rc = hip_check(hipMemcpyAsync(&err, e->p_err, 4, hipMemcpyDeviceToHost, e->stream), "D2H persist error");
-    if (!rc) rc = hip_check(hipStreamSynchronize(e->stream), "hipStreamSynchronize(persist error)");
+    int rc = hip_check(hipMemcpyAsync(&err, e->p_err, 4, hipMemcpyDeviceToHost, e->stream), "D2H wait error");
+    if (!rc) rc = hip_check(hipStreamSynchronize(e->stream), "hipStreamSynchronize(wait error)");
     if (rc) return rc;
-    if (err) return set_error(RFP4_E_HIP, "persistent decode: a grid barrier hit its spin limit (workgroups not co-resident)");
+    if (err)
+        return set_error(RFP4_E_HIP, "decode: a device-side wait hit its spin limit (persistent grid barrier or tagged "
+                                     "attention merge: workgroups not co-resident)");
     return RFP4_OK;
+}
+
+// Before a generation: no word of the tagged merge workspace may carry a tag
+// (sequence length) that this generation's steps will use.
+static int tag_clear(llama_engine *e)
+{
+    if (!e->attn_tagged) return RFP4_OK;
+    return fill_words((uint32_t *)e->attn_tagged, e->attn_tag_layer * e->c.n_layers * 2, 0u, e->stream);
 }
 
 // ---------------------------------------------------------------- batched prefill
@@ -575,6 +596,14 @@ static int engine_alloc(const rfp4_model_config *cfg, llama_engine **out)
     // one arrival counter per attention workgroup column (KV head x query-head slice)
     if (!rc) rc = dalloc_t(e, &e->attn_counters, c.n_heads);
     if (!rc) rc = fill_words(e->attn_counters, c.n_heads, 0u, s);
+    if (e->attn_max_splits > 1) {
+        e->attn_tag_splits = std::min(e->attn_max_splits, kAttnTagMaxSplits);
+        e->attn_tag_layer = (size_t)c.n_heads * e->attn_tag_splits * (hd + 4);
+        if (!rc) rc = dalloc_t(e, &e->attn_tagged, e->attn_tag_layer * c.n_layers);
+        if (!rc) rc = tag_clear(e);
+    }
+    if (!rc) rc = dalloc_t(e, &e->p_err, 1);
+    if (!rc) rc = fill_words(e->p_err, 1, 0u, s);
     if (!rc) rc = dalloc(e, (void **)&e->state, sizeof(StepState));
     e->ids_alloc = c.max_seq + 2;
     if (!rc) rc = dalloc_t(e, &e->ids, e->ids_alloc);
@@ -939,6 +968,7 @@ int llama_engine_begin(llama_engine *e, const uint32_t *prompt, uint32_t n_promp
     rc = hip_check(hipMemcpy(e->ids, prompt, (size_t)n_prompt * 4, hipMemcpyHostToDevice), "H2D prompt");
     StepState st{(int32_t)pos0, 0, n_prompt, ids_cap};
     if (!rc) rc = hip_check(hipMemcpy(e->state, &st, sizeof st, hipMemcpyHostToDevice), "H2D cursor");
+    if (!rc) rc = tag_clear(e);
     if (!rc) rc = embed_first(e);
     if (rc) return rc;
     e->h_pos = pos0;
@@ -985,6 +1015,7 @@ int llama_engine_begin_harness(llama_engine *e, uint32_t ctx, uint32_t ids_cap)
     if (!rc) rc = hip_check(hipMemcpy(e->ids, &zero, 4, hipMemcpyHostToDevice), "H2D ids");
     StepState st{(int32_t)ctx, 0, 1u, ids_cap};
     if (!rc) rc = hip_check(hipMemcpy(e->state, &st, sizeof st, hipMemcpyHostToDevice), "H2D cursor");
+    if (!rc) rc = tag_clear(e);
     if (rc) return rc;
     e->h_pos = ctx;
     e->h_step = 0;
@@ -1065,7 +1096,7 @@ int llama_engine_read_ids(llama_engine *e, uint32_t *ids, uint32_t count)
     int rc = hip_check(hipMemcpyAsync(ids, e->ids, (size_t)count * 4, hipMemcpyDeviceToHost, e->stream), "D2H ids");
     if (rc) return rc;
     rc = hip_check(hipStreamSynchronize(e->stream), "hipStreamSynchronize(ids)");
-    return rc ? rc : persist_check(e);
+    return rc ? rc : wait_check(e);
 }
 
 int llama_generate(llama_engine *e, const uint32_t *prompt, uint32_t n_prompt, uint32_t pos0, uint32_t n_new,

@@ -85,12 +85,16 @@ K1024 void rfp4_rmsnorm_f16w(RmsnormArgs a) { rmsnorm_body<1>(a); }
 K256 void rfp4_rope(RopeArgs a) { rope_body(a); }
 K256 void rfp4_embed(EmbedArgs a) { embed_body(a); }
 
-// ---- attention: rfp4_attn_hd<HD>_<KV type>_g<query heads per KV head, padded to 1/2/4/8>
+// ---- attention: rfp4_attn_hd<HD>_<KV type>_g<query heads per KV head, padded to 1/2/4/8>[_t: tagged merge]
 #define ATTN_KERNELS(HD, KNAME, KT) \
     K256 void rfp4_attn_hd##HD##_##KNAME##_g1(AttnArgs a) { attn_body<HD, KT, 1>(a); } \
     K256 void rfp4_attn_hd##HD##_##KNAME##_g2(AttnArgs a) { attn_body<HD, KT, 2>(a); } \
     K256 void rfp4_attn_hd##HD##_##KNAME##_g4(AttnArgs a) { attn_body<HD, KT, 4>(a); } \
-    K256 void rfp4_attn_hd##HD##_##KNAME##_g8(AttnArgs a) { attn_body<HD, KT, 8>(a); }
+    K256 void rfp4_attn_hd##HD##_##KNAME##_g8(AttnArgs a) { attn_body<HD, KT, 8>(a); } \
+    K256 void rfp4_attn_hd##HD##_##KNAME##_g1_t(AttnArgs a) { attn_body<HD, KT, 1, true>(a); } \
+    K256 void rfp4_attn_hd##HD##_##KNAME##_g2_t(AttnArgs a) { attn_body<HD, KT, 2, true>(a); } \
+    K256 void rfp4_attn_hd##HD##_##KNAME##_g4_t(AttnArgs a) { attn_body<HD, KT, 4, true>(a); } \
+    K256 void rfp4_attn_hd##HD##_##KNAME##_g8_t(AttnArgs a) { attn_body<HD, KT, 8, true>(a); }
 ATTN_KERNELS(64, f32, float)
 ATTN_KERNELS(64, f16, uint16_t)
 ATTN_KERNELS(128, f32, float)

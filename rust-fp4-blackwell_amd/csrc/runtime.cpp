@@ -460,7 +460,7 @@ GemvVariant gemv_variant(uint32_t n, uint32_t k, int epi, bool f32scale)
     return GemvVariant{R, ns, W};
 }
 
-static thread_local int t_attn_merge = 0; // 0 automatic, 1 merge kernel, 2 in-kernel merge where it fits
+static thread_local int t_attn_merge = 0; // 0 automatic, 1 merge kernel, 2 in-kernel merge where it fits, 3 tagged (engines)
 
 int attn_merge_mode() { return t_attn_merge; }
 
@@ -478,6 +478,16 @@ bool attn_inmerge_mode(int mode, uint32_t splits)
 {
     if (splits <= 1 || splits > kAttnInmergeMaxSplits) return false;
     return mode != 1;
+}
+
+bool attn_tagged_mode(int mode, uint32_t splits)
+{
+    // Automatic: above the last-arriver merge's splits.  Measured (graph step,
+    // tok/s, merge kernel -> tagged): TinyLlama at context 1500 1835 -> 1886,
+    // Llama-3.2-1B at 1200 2261 -> 2330, Llama-3-8B at 4096 (29 splits)
+    // 672 -> 674.
+    if (splits <= 1 || splits > kAttnTagMaxSplits) return false;
+    return mode == 3 || (mode == 0 && splits > kAttnInmergeMaxSplits);
 }
 
 bool attn_inmerge(uint32_t max_splits)
@@ -525,7 +535,8 @@ extern "C" int rfp4_debug_attn_head_split(int hs)
 extern "C" int rfp4_debug_attn_merge(int mode)
 {
     using namespace rfp4;
-    if (mode < 0 || mode > 2) return set_error(RFP4_E_INVALID, "merge mode must be 0 (auto), 1 (merge kernel) or 2 (in-kernel)");
+    if (mode < 0 || mode > 3)
+        return set_error(RFP4_E_INVALID, "merge mode must be 0 (auto), 1 (merge kernel), 2 (in-kernel) or 3 (tagged)");
     t_attn_merge = mode;
     return RFP4_OK;
 }
@@ -615,17 +626,20 @@ int attn_launch(const AttnArgs &args, int kv_f16, hipStream_t s, uint32_t max_se
         return set_error(RFP4_E_INVALID, "attn: head split %u does not divide the group of %u", hs,
                          args.n_heads / args.n_kv_heads);
     char name[48];
-    snprintf(name, sizeof name, "rfp4_attn_hd%u_%s_g%u", args.head_dim, kv_f16 ? "f16" : "f32",
-             attn_group_pad(args.n_heads / args.n_kv_heads / hs));
+    snprintf(name, sizeof name, "rfp4_attn_hd%u_%s_g%u%s", args.head_dim, kv_f16 ? "f16" : "f32",
+             attn_group_pad(args.n_heads / args.n_kv_heads / hs), args.tagged ? "_t" : "");
     if (rows == 0 || (rows > 1 && args.cosv)) return set_error(RFP4_E_INVALID, "attn: fused append is one row only");
     uint32_t splits = (max_seq_for_grid + args.chunk - 1) / args.chunk;
     if (splits > args.max_splits) return set_error(RFP4_E_INVALID, "attn: %u splits exceed the workspace's %u", splits, args.max_splits);
     if (args.counters && (rows != 1 || splits > kAttnInmergeMaxSplits))
         return set_error(RFP4_E_INVALID, "attn: the in-kernel merge takes one row and at most %u splits", kAttnInmergeMaxSplits);
+    if (args.tagged && (rows != 1 || args.counters || splits > args.tag_splits || args.tag_splits > kAttnTagMaxSplits))
+        return set_error(RFP4_E_INVALID, "attn: the tagged merge takes one row and at most %u splits (workspace: %u)",
+                         kAttnTagMaxSplits, args.tag_splits);
     AttnArgs a = args;
     a.head_split = hs;
     int rc = launch(name, dim3(a.n_kv_heads * hs, splits, rows), dim3(256), s, &a);
-    if (rc || splits <= 1 || a.counters) return rc;
+    if (rc || splits <= 1 || a.counters || a.tagged) return rc;
     // the split states are merged by a second launch (stream order, no fence)
     return launch(args.head_dim == 64 ? "rfp4_attn_merge_hd64" : "rfp4_attn_merge_hd128", dim3(a.n_heads, 1, rows),
                   dim3(256), s, &a);

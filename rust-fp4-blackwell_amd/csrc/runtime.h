@@ -97,6 +97,11 @@ int attn_head_split_mode();                      // this thread's rfp4_debug_att
 int prefill_stop();                              // this thread's rfp4_debug_prefill_stop setting
 bool attn_inmerge_mode(int mode, uint32_t splits); // attn_inmerge under an explicit setting
 constexpr uint32_t kAttnInmergeMaxSplits = 8;
+// Whether an engine's one-row attention with `splits` splits uses the tagged
+// in-kernel merge (a per-layer tagged workspace of at most kAttnTagMaxSplits
+// splits per head, cleared before each generation).
+bool attn_tagged_mode(int mode, uint32_t splits);
+constexpr uint32_t kAttnTagMaxSplits = 32; // ATTN_TAG_MAX_SPLITS (device/attn.h)
 uint32_t attn_chunk_for(uint32_t n_kv_heads, uint32_t seq, uint32_t num_cus, uint32_t head_dim, uint32_t elem_bytes,
                         uint32_t group);
 

@@ -89,6 +89,16 @@ typedef struct AttnArgs {
     // Query-head slices per KV head (grid x = head_split * n_kv_heads; 0 or 1:
     // every workgroup serves the KV head's whole group).
     uint32_t head_split, pad2;
+    // Tagged in-kernel merge (engine decode, one query row, splits <=
+    // tag_splits <= 64; null = off): split states as 64-bit words (float bits
+    // | tag << 32, tag = the launch's sequence length), word (h, split, i) at
+    // (h * tag_splits + split) * (head_dim + 4) + i, i = 0 m, 1 l, 4 + d acc.
+    // The workspace must hold no word tagged with a sequence length this
+    // launch could use before its first launch of a generation (the engine
+    // clears it).  err: set to 1 if a merge hit its spin limit.
+    unsigned long long *tagged;
+    uint32_t *err;
+    uint32_t tag_splits, pad3;
 } AttnArgs;
 
 // Causal attention of the batched prefill (device/attn_prefill.h): prompt

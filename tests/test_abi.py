@@ -167,7 +167,7 @@ def test_test_hooks_validate_arguments():
     assert lib.rfp4_debug_prefill_waves(16) == -1
     assert lib.rfp4_debug_prefill_pairing(3) == -1
     assert lib.rfp4_debug_prefill_attn(2) == -1
-    assert lib.rfp4_debug_attn_merge(3) == -1
+    assert lib.rfp4_debug_attn_merge(4) == -1
     assert lib.rfp4_debug_gemv_waves(2) == -1
     for hook in (lib.rfp4_debug_prefill_waves, lib.rfp4_debug_prefill_pairing, lib.rfp4_debug_prefill_attn,
                  lib.rfp4_debug_attn_merge, lib.rfp4_debug_gemv_waves):

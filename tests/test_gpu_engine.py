@@ -98,11 +98,12 @@ def test_engine_errors(rf):
 
 
 @pytest.mark.parametrize("cfg", [TINY, TINY128])
-@pytest.mark.parametrize("mode", [1, 2])
+@pytest.mark.parametrize("mode", [1, 2, 3])
 def test_engine_attn_merge_modes_tokens(rf, orc, cfg, mode):
     """The decode step with the attention splits merged by a second kernel
-    (mode 1) and inside the attention kernel (mode 2): the same greedy tokens
-    as the oracle over a context that needs several splits."""
+    (mode 1), inside the attention kernel by the last split (mode 2) or by
+    the first splits polling tagged states (mode 3): the same greedy tokens as
+    the oracle over a context that needs several splits."""
     seed = 0x1A2B
     rf.check(rf.load().rfp4_debug_attn_merge(mode))
     rf.debug_attn_chunk(cfg["max_seq"] // 6 + 1)  # 6 splits over the context
@@ -124,13 +125,14 @@ G8E = dict(dim=256, n_layers=2, n_heads=8, n_kv_heads=1, head_dim=64, ffn=512, v
 
 
 @pytest.mark.parametrize("cfg,slices", [(TINY128, (1, 2, 4)), (G8E, (1, 2, 4, 8))])
-@pytest.mark.parametrize("merge", [1, 2])
+@pytest.mark.parametrize("merge", [1, 2, 3])
 def test_engine_attn_head_slices_bit_identical(rf, orc, cfg, slices, merge):
     """Query-head slices per KV head (rfp4_debug_attn_head_split): each
     attention workgroup serves group/slices query heads of its KV head; the
     per-head arithmetic is unchanged, so tokens and logits are bit-identical
-    for every slice count, with the splits merged by the second kernel (1) or
-    in the attention kernel (2), and the tokens are the oracle's."""
+    for every slice count, with the splits merged by the second kernel (1), in
+    the attention kernel by the last split (2) or from tagged states (3), and
+    the tokens are the oracle's."""
     seed = 0x51CE
     prompt = [2, 9, 77, 401, 5, 6, 7]
     outs = []
@@ -153,3 +155,45 @@ def test_engine_attn_head_slices_bit_identical(rf, orc, cfg, slices, merge):
     ref = orc.Model(cfg, seed)
     cpu, margins = ref.generate(prompt, 0, 40)
     assert list(outs[0][0]) == list(cpu), f"gpu {list(outs[0][0])}\ncpu {list(cpu)}\nmargins {margins}"
+
+
+def _merge_engine(rf, cfg, seed, mode, chunk):
+    rf.check(rf.load().rfp4_debug_attn_merge(mode))
+    rf.debug_attn_chunk(chunk)
+    try:
+        return _engine(rf, cfg, seed)
+    finally:
+        rf.debug_attn_chunk(0)
+        rf.check(rf.load().rfp4_debug_attn_merge(0))
+
+
+@pytest.mark.parametrize("cfg", [dict(TINY128, max_seq=400), dict(G8E, max_seq=400)])
+def test_engine_tagged_merge_bit_identical(rf, orc, cfg):
+    """The tagged in-kernel merge (mode 3) sums in the merge kernel's order:
+    tokens and logits bit-identical to mode 1 over contexts of 1 to 30 splits
+    (10-token splits), and past the tagged merge's 32 splits (up to 34: the
+    merge kernel takes over).  A second generation on the same engine at the same
+    positions (the workspace then holds the first one's states under the
+    same tags until the engine clears it) gives the oracle's tokens for its
+    own prompt, and repeating the first prompt repeats its logits."""
+    seed = 0x7A66
+    chunk = 10
+    ref = orc.Model(cfg, seed)
+    p1, p2 = [2, 9, 77, 401, 5, 6, 7], [13, 600, 3, 3, 250]
+    n1 = min(cfg["max_seq"] - len(p1) - 1, 330)
+    a = _merge_engine(rf, cfg, seed, 1, chunk)
+    b = _merge_engine(rf, cfg, seed, 3, chunk)
+    ta, tb = a.generate(p1, 0, n1), b.generate(p1, 0, n1)
+    la, lb = a.logits(), b.logits()
+    np.testing.assert_array_equal(np.array(ta), np.array(tb))
+    np.testing.assert_array_equal(la, lb)
+    # second generation at the same positions, another prompt
+    t2 = b.generate(p2, 0, 40)
+    cpu2, margins = ref.generate(p2, 0, 40)
+    assert list(t2) == list(cpu2), f"gpu {list(t2)}\ncpu {list(cpu2)}\nmargins {margins}"
+    np.testing.assert_array_equal(np.array(b.generate(p1, 0, n1)), np.array(ta))
+    np.testing.assert_array_equal(b.logits(), lb)
+    cpu1, margins = ref.generate(p1, 0, 40)
+    assert list(ta[:40]) == list(cpu1), f"gpu {list(ta[:40])}\ncpu {list(cpu1)}\nmargins {margins}"
+    a.close()
+    b.close()
