@@ -574,8 +574,10 @@ def gemv_step_table(cfg, kern):
         out[r] = {"kernel": role[r], "bytes": b, "us": us,
                   "GB_s": round(b / us / 1e3, 1) if us else None, "frac": round(b / us / 1e3 / HBM_PEAK_GBS, 4) if us else None}
     per_tok_us = sum(kern[k][0] * kern[k][1] for k in names)
-    per_tok_b = cfg.n_layers * sum(gemv_bytes(n, k) + adj for r, (n, k, adj) in shapes.items() if r != "lm_head") + \
-        gemv_bytes(cfg.vocab, cfg.dim)
+    # roles with a GEMV launch of their own (the q|k|v GEMV may be fused with
+    # the attention into one launch, rfp4_qkva_*: not a GEMV-only time)
+    per_tok_b = cfg.n_layers * sum(gemv_bytes(n, k) + adj for r, (n, k, adj) in shapes.items()
+                                   if r != "lm_head" and r in role) + gemv_bytes(cfg.vocab, cfg.dim)
     return out, {"bytes_per_token": per_tok_b, "us_per_token": round(per_tok_us, 2),
                  "GB_s": round(per_tok_b / per_tok_us / 1e3, 1), "frac": round(per_tok_b / per_tok_us / 1e3 / HBM_PEAK_GBS, 4)}
 
@@ -631,9 +633,17 @@ def main():
         f"weights {weight_bytes / 1e9:.3f} GB -> {weight_bytes / ms_step / 1e6:.0f} GB/s effective")
     kern = step_kernels(eng, "llama3-8b")
     gemv_roles, gemv_in_step = gemv_step_table(cfg, kern)
+    # attention (+ its merge kernel) per layer; where the engine fuses the
+    # q|k|v GEMV and the attention into one launch (rfp4_qkva_*), that launch
+    fused = any(k.startswith("rfp4_qkva_") for k in kern)
     attn_us = sum(v[0] * v[1] for k, v in kern.items() if k.startswith("rfp4_attn_")) / cfg.n_layers
+    qkva_us = sum(v[0] * v[1] for k, v in kern.items()
+                  if k.startswith("rfp4_qkva_") or (fused and k.startswith("rfp4_attn_merge"))) / cfg.n_layers
     log("in-step kernels (us): " + ", ".join(f"{k} {v[1]}" for k, v in sorted(kern.items(), key=lambda kv: -kv[1][0] * kv[1][1])))
-    log(f"attention + merge per layer {attn_us:.2f} us; GEMV path in the step {gemv_in_step['GB_s']} GB/s")
+    if fused:
+        log(f"q|k|v GEMV + attention (one launch) per layer {qkva_us:.2f} us; GEMV path in the step {gemv_in_step['GB_s']} GB/s")
+    else:
+        log(f"attention + merge per layer {attn_us:.2f} us; GEMV path in the step {gemv_in_step['GB_s']} GB/s")
 
     with ROCTX.range("gemv_path_isolated"):
         path_bytes, path_ms, gate_bytes, gate_ms = gemv_path(rf, eng, cfg)
@@ -721,7 +731,8 @@ def main():
                          "frac": round(gate_gbs / HBM_PEAK_GBS, 4)},
         },
         "step_kernels_us": {k: v[1] for k, v in kern.items()},
-        "attention_us_per_layer": round(attn_us, 3),
+        "attention_us_per_layer": None if fused else round(attn_us, 3),
+        "qkv_attention_fused_us_per_layer": round(qkva_us, 3) if fused else None,
         "gemv_in_step": dict(gemv_in_step, roles=gemv_roles),
         "gemv_path": {
             "bytes_per_token": path_bytes,

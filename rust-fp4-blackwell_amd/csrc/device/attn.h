@@ -445,8 +445,10 @@ RFP4_DEV void attn_merge_last_ordered(const AttnArgs &a, const float *prow, uint
 // barrier that publishes q, then loads q and finishes.  TAG: the split
 // states go to the tagged workspace and are merged by the first splits of
 // each workgroup column (kernels of their own: the merge's registers stay out
-// of the other kernels' allocation).
-template <int HD, typename KT, int GT, bool AG, bool TAG = false>
+// of the other kernels' allocation).  QT: q and the current token's k and v
+// come as tagged words from the q|k|v GEMV of the same launch (fused kernel,
+// device/qkva.h): load_q_tagged after issue, in place of load_q.
+template <int HD, typename KT, int GT, bool AG, bool TAG = false, bool QT = false>
 struct AttnSplit {
     static constexpr int EPL = KvTraits<KT>::EPL;
     static constexpr int LPT = HD / EPL;          // lanes per token row
@@ -483,6 +485,77 @@ struct AttnSplit {
         writer = hg == 0u;
     }
     const KT *kc, *vc;
+    float tkv[4]; // QT, owner split, tid < HD/2: k[tid], k[tid + HD/2], v[tid], v[tid + HD/2] of the current token
+
+    // QT: this thread's q pairs (as load_q) and, in the split owning the
+    // current position, the current token's k and v, from words tagged with
+    // `tag` (the launch's sequence length).  After issue (owner known).
+    // Every word is polled until it carries the tag; each word read with the
+    // tag is the value stored with it (one 64-bit atomic object), so no fence
+    // or counter is needed.  A poll past ATTN_TAG_SPIN_LIMIT spins sets *err
+    // (the results are then invalid, and the engine reports it).
+    RFP4_DEV void load_q_tagged(const AttnArgs &a, uint32_t tag)
+    {
+        const int tid = threadIdx.x;
+        const unsigned long long *qg = a.qkv_t + (size_t)hbase * HD;
+        const unsigned long long *kn = a.qkv_t + (size_t)(a.n_heads + kvh) * HD;
+        const unsigned long long *vn = a.qkv_t + (size_t)(a.n_heads + a.n_kv_heads + kvh) * HD;
+        const bool kv = owner && (uint32_t)tid < HALF;
+        unsigned long long wa[QPT], wb[QPT], wk[4];
+#pragma unroll
+        for (int m = 0; m < QPT; m++) {
+            const uint32_t i = (uint32_t)tid + 256u * (uint32_t)m;
+            const uint32_t g = i / HALF, j = i % HALF;
+            const bool in = g < G;
+            wa[m] = in ? attn_load_tagged(qg + g * HD + j) : 0ull;
+            wb[m] = in ? attn_load_tagged(qg + g * HD + j + HALF) : 0ull;
+        }
+        if (kv) {
+            wk[0] = attn_load_tagged(kn + tid);
+            wk[1] = attn_load_tagged(kn + tid + HALF);
+            wk[2] = attn_load_tagged(vn + tid);
+            wk[3] = attn_load_tagged(vn + tid + HALF);
+        }
+        bool timeout = false;
+        for (uint32_t spin = 0;; spin++) {
+            bool stale = false;
+#pragma unroll
+            for (int m = 0; m < QPT; m++) {
+                const bool in = (uint32_t)tid + 256u * (uint32_t)m < G * HALF;
+                stale = stale || (in && !(attn_tag_ok(wa[m], tag) && attn_tag_ok(wb[m], tag)));
+            }
+            if (kv)
+#pragma unroll
+                for (int r = 0; r < 4; r++) stale = stale || !attn_tag_ok(wk[r], tag);
+            if (!__syncthreads_or(stale)) break;
+            if (spin >= ATTN_TAG_SPIN_LIMIT) {
+                timeout = true;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int m = 0; m < QPT; m++) {
+                const uint32_t i = (uint32_t)tid + 256u * (uint32_t)m;
+                const uint32_t g = i / HALF, j = i % HALF;
+                if (g < G && !attn_tag_ok(wa[m], tag)) wa[m] = attn_load_tagged(qg + g * HD + j);
+                if (g < G && !attn_tag_ok(wb[m], tag)) wb[m] = attn_load_tagged(qg + g * HD + j + HALF);
+            }
+            if (kv) {
+                if (!attn_tag_ok(wk[0], tag)) wk[0] = attn_load_tagged(kn + tid);
+                if (!attn_tag_ok(wk[1], tag)) wk[1] = attn_load_tagged(kn + tid + HALF);
+                if (!attn_tag_ok(wk[2], tag)) wk[2] = attn_load_tagged(vn + tid);
+                if (!attn_tag_ok(wk[3], tag)) wk[3] = attn_load_tagged(vn + tid + HALF);
+            }
+        }
+#pragma unroll
+        for (int m = 0; m < QPT; m++) {
+            qa[m] = attn_tag_val(wa[m]);
+            qb[m] = attn_tag_val(wb[m]);
+        }
+#pragma unroll
+        for (int r = 0; r < 4; r++) tkv[r] = kv ? attn_tag_val(wk[r]) : 0.0f;
+        if (timeout && tid == 0 && a.err) __hip_atomic_store(a.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
 
     // This thread's q pairs (j, j + HD/2) of pair index i = tid + 256 m.
     RFP4_DEV void load_q(const AttnArgs &a, uint32_t x, uint32_t row_)
@@ -575,9 +648,19 @@ struct AttnSplit {
         if (owner && (uint32_t)tid < HALF) {
             // the current token's k and v, loaded by the owner split only (after
             // its K/V stream, so no other split waits on them)
-            const float *kn = a.k_new + (size_t)kvh * HD, *vn = a.v_new + (size_t)kvh * HD;
-            const float kna = attn_in<AG>(kn + tid), knb = attn_in<AG>(kn + tid + HALF);
-            const float vna = attn_in<AG>(vn + tid), vnb = attn_in<AG>(vn + tid + HALF);
+            float kna, knb, vna, vnb;
+            if (QT) {
+                kna = tkv[0];
+                knb = tkv[1];
+                vna = tkv[2];
+                vnb = tkv[3];
+            } else {
+                const float *kn = a.k_new + (size_t)kvh * HD, *vn = a.v_new + (size_t)kvh * HD;
+                kna = attn_in<AG>(kn + tid);
+                knb = attn_in<AG>(kn + tid + HALF);
+                vna = attn_in<AG>(vn + tid);
+                vnb = attn_in<AG>(vn + tid + HALF);
+            }
             KT *kdst = (KT *)a.kc + (size_t)kvh * a.hs + (size_t)pos * a.ts;
             KT *vdst = (KT *)a.vc + (size_t)kvh * a.hs + (size_t)pos * a.ts;
             const KT r0 = KvTraits<KT>::from_f32(__fsub_rn(__fmul_rn(kna, cs), __fmul_rn(knb, sn)));

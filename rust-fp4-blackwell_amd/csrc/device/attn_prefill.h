@@ -27,32 +27,9 @@
 #pragma once
 #include "common.h"
 
-typedef _Float16 pf_f16x8 __attribute__((ext_vector_type(8)));
-typedef float pf_f32x4 __attribute__((ext_vector_type(4)));
-
 #define PF_BK 32   // keys per block
 #define PF_KPAD 8  // fp16 padding of a staged K row (16 consecutive rows -> 16 distinct bank groups)
 #define PF_TPAD 8  // fp16 padding of a transposed V row / a P row
-
-// x -> hi + lo, both fp16 (hi = fp16(x), lo = fp16(x - hi); x - hi is exact)
-RFP4_DEV void pf_split8(const float *v, pf_f16x8 &hi, pf_f16x8 &lo)
-{
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        const _Float16 h = (_Float16)v[i];
-        hi[i] = h;
-        lo[i] = (_Float16)(v[i] - (float)h);
-    }
-}
-
-RFP4_DEV float pf_row16_max(float v)
-{
-    v = fmaxf(v, dpp_mov<DPP_QUAD_1032>(v));
-    v = fmaxf(v, dpp_mov<DPP_QUAD_2301>(v));
-    v = fmaxf(v, dpp_mov<DPP_ROW_HALF_MIRROR>(v));
-    v = fmaxf(v, dpp_mov<DPP_ROW_MIRROR>(v));
-    return v;
-}
 
 // One query tile: prompt rows r0 .. r0 + BQ of KV head blockIdx.y.
 template <int HD, int GT, int NW>
@@ -88,7 +65,7 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
     const float scale = __fmul_rn(1.4426950408889634f, __fdiv_rn(1.0f, __fsqrt_rn((float)HD))); // log2(e) / sqrt(HD)
 
     // ---- Q tiles of this wave as fp16 A operands (rows past the prompt or heads past G: zero)
-    pf_f16x8 qa[MT][KS], ql[MT][KS];
+    f16x8 qa[MT][KS], ql[MT][KS];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
         const uint32_t t = (uint32_t)(wave * MT + mt), g = t % GT, row = r0 + 16u * (t / GT) + l16;
@@ -102,11 +79,11 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
             v[4] = x1.x; v[5] = x1.y; v[6] = x1.z; v[7] = x1.w;
 #pragma unroll
             for (int i = 0; i < 8; i++) v[i] = in ? v[i] : 0.0f;
-            pf_split8(v, qa[mt][k], ql[mt][k]);
+            split_hi_lo8(v, qa[mt][k], ql[mt][k]);
         }
     }
 
-    pf_f32x4 o[MT][NN];
+    f32x4 o[MT][NN];
     float mrun[MT][4], lrun[MT][4];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
@@ -158,13 +135,13 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
         for (int mt = 0; mt < MT; mt++) {
             const uint32_t t = (uint32_t)(wave * MT + mt);
             // ---- S = Q K^T for the block's two 16-key halves
-            pf_f32x4 s[2];
+            f32x4 s[2];
 #pragma unroll
             for (int h = 0; h < 2; h++) {
                 s[h] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int k = 0; k < KS; k++) {
-                    const pf_f16x8 kb = *(const pf_f16x8 *)&ks[16u * h + l16][32 * k + 8u * q4];
+                    const f16x8 kb = *(const f16x8 *)&ks[16u * h + l16][32 * k + 8u * q4];
                     s[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[mt][k], kb, s[h], 0, 0, 0);
                     s[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[mt][k], kb, s[h], 0, 0, 0);
                 }
@@ -183,7 +160,7 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
                     p[h][r] = key <= qpos ? v : -3.402823466e38f;
                     mx = fmaxf(mx, p[h][r]);
                 }
-                mx = pf_row16_max(mx);
+                mx = row16_max(mx);
                 const float mnew = fmaxf(mrun[mt][r], mx);
                 const float alpha = __builtin_amdgcn_exp2f(mrun[mt][r] - mnew);
                 mrun[mt][r] = mnew;
@@ -207,12 +184,12 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
                     ps[wave][mt][1][4u * q4 + (uint32_t)r][16u * h + l16] = (_Float16)(p[h][r] - (float)ph);
                 }
             __builtin_amdgcn_wave_barrier();
-            const pf_f16x8 pa = *(const pf_f16x8 *)&ps[wave][mt][0][l16][8u * q4];
-            const pf_f16x8 pl = *(const pf_f16x8 *)&ps[wave][mt][1][l16][8u * q4];
+            const f16x8 pa = *(const f16x8 *)&ps[wave][mt][0][l16][8u * q4];
+            const f16x8 pl = *(const f16x8 *)&ps[wave][mt][1][l16][8u * q4];
             // ---- O += P V
 #pragma unroll
             for (int n = 0; n < NN; n++) {
-                const pf_f16x8 vb = *(const pf_f16x8 *)&vt[16u * n + l16][8u * q4];
+                const f16x8 vb = *(const f16x8 *)&vt[16u * n + l16][8u * q4];
                 o[mt][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, o[mt][n], 0, 0, 0);
                 o[mt][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vb, o[mt][n], 0, 0, 0);
             }

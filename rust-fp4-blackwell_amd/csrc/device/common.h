@@ -75,6 +75,16 @@ RFP4_DEV float xor32_max(float v)
     return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
 }
 
+// Max over the 16 lanes of each DPP row; every lane of the row gets it.
+RFP4_DEV float row16_max(float v)
+{
+    v = fmaxf(v, dpp_mov<DPP_QUAD_1032>(v));
+    v = fmaxf(v, dpp_mov<DPP_QUAD_2301>(v));
+    v = fmaxf(v, dpp_mov<DPP_ROW_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_mov<DPP_ROW_MIRROR>(v));
+    return v;
+}
+
 // Sum over all 64 lanes; every lane gets the total.
 RFP4_DEV float wave_sum(float v)
 {
@@ -89,6 +99,25 @@ RFP4_DEV float wave_max(float v)
     v = fmaxf(v, dpp_mov<DPP_ROW_HALF_MIRROR>(v));
     v = fmaxf(v, dpp_mov<DPP_ROW_MIRROR>(v));
     return xor32_max(xor16_max(v));
+}
+
+// ---------------------------------------------------------------- fp16 matrix-core operands
+// v_mfma_f32_16x16x32_f16 operands: lane l holds A row / B column l % 16 and
+// K = 8 (l / 16) .. +7; accumulator r of lane l is D[4 (l / 16) + r][l % 16]
+// (pinned by the fp16 layout test).
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// x -> hi + lo, both fp16 (hi = fp16(x), lo = fp16(x - hi); x - hi is exact):
+// about 2^-22 relative with two matrix-core products per operand
+RFP4_DEV void split_hi_lo8(const float *v, f16x8 &hi, f16x8 &lo)
+{
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const _Float16 h = (_Float16)v[i];
+        hi[i] = h;
+        lo[i] = (_Float16)(v[i] - (float)h);
+    }
 }
 
 // ---------------------------------------------------------------- E2M1 / E8M0

@@ -71,6 +71,14 @@ struct llama_engine {
     uint32_t attn_tag_splits = 0;
     size_t attn_tag_layer = 0; // words per layer
     uint32_t attn_head_split = 0;      // query-head slices per KV head (0: per grid, attn_head_split_for)
+    // fused q|k|v GEMV + attention launch (device/qkva.h): rows per wave of its
+    // GEMV tiles (0 = no fused kernel for this shape), its tagged q|k|v words
+    // (one region per layer: the tag is the step's sequence length, so a
+    // layer must not see another layer's words of the same step; cleared with
+    // the tagged merge workspace), the policy fixed at creation
+    uint32_t qkva_R = 0;
+    unsigned long long *qkv_t = nullptr;
+    int qkva_mode = 0; // 0 = fused wherever the grid fits the device, 1 = two launches
     StepState *state = nullptr;
     uint32_t *ids = nullptr, *last_tok = nullptr;
     uint32_t ids_alloc = 0;
@@ -134,9 +142,41 @@ static int validate(const rfp4_model_config &c)
 }
 
 // ---------------------------------------------------------------- step enqueue
+// The fused q|k|v GEMV + attention launch (device/qkva.h) of a step with
+// `nsplit` attention splits: kernel name, query-head slices, GEMV tiles,
+// attention workgroups and grid.  False where the engine has no fused kernel
+// for its shape, the policy says two launches, or the grid does not fit the
+// device at once (the attention workgroups wait for the GEMV tiles' words,
+// so every workgroup must be resident).
+struct QkvaPlan {
+    char name[48];
+    uint32_t hs, n_tiles, n_attn, grid;
+};
+
+static bool qkva_plan(const llama_engine *e, uint32_t nsplit, bool tagged, QkvaPlan *pl)
+{
+    const rfp4_model_config &c = e->c;
+    if (!e->qkva_R || e->qkva_mode == 1) return false;
+    Runtime *rt = runtime();
+    const uint32_t G = c.n_heads / c.n_kv_heads;
+    const uint32_t hs = e->attn_head_split ? e->attn_head_split
+                                           : attn_head_split_for(c.n_heads, c.n_kv_heads, nsplit, (uint32_t)rt->num_cus);
+    if (hs == 0 || G % hs) return false;
+    snprintf(pl->name, sizeof pl->name, "rfp4_qkva_hd%u_g%u%s", c.head_dim, attn_group_pad(G / hs), tagged ? "_t" : "");
+    const uint32_t rows = qdim(c) + 2u * kvdim(c), per_tile = 4u * e->qkva_R;
+    pl->hs = hs;
+    pl->n_tiles = (rows + per_tile - 1u) / per_tile;
+    pl->n_attn = c.n_kv_heads * hs * nsplit;
+    pl->grid = std::max(pl->n_tiles, pl->n_attn);
+    int per_cu = 0;
+    if (kernel_occupancy(pl->name, 256, gemv_lds_bytes(c.dim), &per_cu) || per_cu < 1) return false;
+    return (uint64_t)per_cu * (uint64_t)rt->num_cus >= pl->grid;
+}
+
 // The decode step at a position whose context needs `nsplit` attention
 // splits: the attention grid launches exactly those, and up to 8 splits are
-// merged inside the attention kernel (attn_inmerge_mode).
+// merged inside the attention kernel (attn_inmerge_mode).  Where the fused
+// kernel applies, the q|k|v GEMV and the attention are one launch.
 static int enqueue_step(llama_engine *e, uint32_t nsplit)
 {
     const rfp4_model_config &c = e->c;
@@ -148,7 +188,6 @@ static int enqueue_step(llama_engine *e, uint32_t nsplit)
         const LayerW &w = e->L[l];
         void *kc = kv_layer(e, l, 0), *vc = kv_layer(e, l, 1);
         GemvArgs qa{w.qkv_c, w.qkv_s, e->x, e->qkv, nullptr, e->norm_attn + (size_t)l * c.dim, qd + 2 * kvd, c.dim, 0, c.eps};
-        if ((rc = gemv_launch_v(sn, RFP4_EPI_STORE, qa, s, e->gv[GV_QKV]))) return rc;
         AttnArgs aa{};
         aa.q = e->qkv; aa.kc = kc; aa.vc = vc; aa.out = e->attn_out;
         aa.part = e->attn_part; aa.pos_ptr = &e->state->pos;
@@ -164,7 +203,21 @@ static int enqueue_step(llama_engine *e, uint32_t nsplit)
             aa.counters = attn_inmerge_mode(e->attn_merge_mode, nsplit) ? e->attn_counters : nullptr;
         }
         aa.head_split = e->attn_head_split;
-        if ((rc = attn_launch(aa, e->kvb == 2 ? 1 : 0, s, e->attn_chunk * nsplit, 1))) return rc;
+        QkvaPlan pl;
+        if (qkva_plan(e, nsplit, aa.tagged != nullptr, &pl)) {
+            unsigned long long *yt = e->qkv_t + (size_t)l * (qd + 2 * kvd);
+            QkvaArgs fa{qa, aa, yt, pl.n_tiles, pl.n_attn};
+            fa.a.head_split = pl.hs;
+            fa.a.qkv_t = yt;
+            if ((rc = launch(pl.name, dim3(pl.grid), dim3(256), s, &fa, gemv_lds_bytes(c.dim)))) return rc;
+            // more splits than either in-kernel merge takes: the merge kernel
+            if (nsplit > 1 && !aa.counters && !aa.tagged &&
+                (rc = launch(hd == 64 ? "rfp4_attn_merge_hd64" : "rfp4_attn_merge_hd128", dim3(c.n_heads), dim3(256), s, &aa)))
+                return rc;
+        } else {
+            if ((rc = gemv_launch_v(sn, RFP4_EPI_STORE, qa, s, e->gv[GV_QKV]))) return rc;
+            if ((rc = attn_launch(aa, e->kvb == 2 ? 1 : 0, s, e->attn_chunk * nsplit, 1))) return rc;
+        }
         GemvArgs oa{w.o_c, w.o_s, e->attn_out, e->x, nullptr, nullptr, c.dim, qd, 0, 0.0f};
         if ((rc = gemv_launch_v(sn, RFP4_EPI_RESIDUAL, oa, s, e->gv[GV_O]))) return rc;
         GemvArgs ga{w.gu_c, w.gu_s, e->x, e->sw, nullptr, e->norm_ffn + (size_t)l * c.dim, c.ffn, c.dim, c.ffn, c.eps};
@@ -288,7 +341,10 @@ static int wait_check(llama_engine *e)
 // (sequence length) that this generation's steps will use.
 static int tag_clear(llama_engine *e)
 {
-    if (!e->attn_tagged) return RFP4_OK;
+    int rc = RFP4_OK;
+    if (e->qkv_t)
+        rc = fill_words((uint32_t *)e->qkv_t, (size_t)e->c.n_layers * (qdim(e->c) + 2u * kvdim(e->c)) * 2u, 0u, e->stream);
+    if (rc || !e->attn_tagged) return rc;
     return fill_words((uint32_t *)e->attn_tagged, e->attn_tag_layer * e->c.n_layers * 2, 0u, e->stream);
 }
 
@@ -586,6 +642,16 @@ static int engine_alloc(const rfp4_model_config *cfg, llama_engine **out)
     e->gv[GV_D] = gemv_variant(c.dim, c.ffn, RFP4_EPI_RESIDUAL, f32s);
     e->gv[GV_LM] = gemv_variant(c.vocab, c.dim, RFP4_EPI_ARGMAX, f32s);
     e->n_best = gemv_grid(c.vocab, e->gv[GV_LM]);
+    // the fused q|k|v GEMV + attention kernels (kernels.hip QKVA_KERNELS):
+    // E8M0 weights and fp16 caches, with the q|k|v GEMV variant whose RMS
+    // order the fused tile reproduces (bit-identical outputs)
+    e->qkva_mode = qkva_mode();
+    if (!f32s && c.kv_format == RFP4_KV_F16) {
+        const GemvVariant &v = e->gv[GV_QKV];
+        if (c.head_dim == 64 && c.dim == 2048 && v.R == 2 && v.NS == 1 && v.W == 8) e->qkva_R = 2;
+        if (c.head_dim == 128 && c.dim == 4096 && v.R == 2 && v.NS == 2 && v.W == 4) e->qkva_R = 4;
+    }
+    if (!rc && e->qkva_R) rc = dalloc_t(e, &e->qkv_t, (size_t)c.n_layers * (qd + 2 * kvd));
     if (!rc) rc = dalloc_t(e, &e->best, e->n_best);
     if (!rc) rc = dalloc_t(e, &e->attn_part, (size_t)c.n_heads * e->attn_max_splits * (hd + 4));
     e->attn_merge_mode = attn_merge_mode();
@@ -602,6 +668,7 @@ static int engine_alloc(const rfp4_model_config *cfg, llama_engine **out)
         if (!rc) rc = dalloc_t(e, &e->attn_tagged, e->attn_tag_layer * c.n_layers);
         if (!rc) rc = tag_clear(e);
     }
+    if (!rc) rc = tag_clear(e);
     if (!rc) rc = dalloc_t(e, &e->p_err, 1);
     if (!rc) rc = fill_words(e->p_err, 1, 0u, s);
     if (!rc) rc = dalloc(e, (void **)&e->state, sizeof(StepState));

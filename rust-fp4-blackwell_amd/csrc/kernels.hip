@@ -13,6 +13,7 @@
 #include "device/prefill.h"
 #include "device/attn_prefill.h"
 #include "device/persist.h"
+#include "device/qkva.h"
 
 #define K256 extern "C" __global__ __launch_bounds__(256)
 #define K512 extern "C" __global__ __launch_bounds__(512)
@@ -111,6 +112,21 @@ ATTN_KERNELS(128, f16, uint16_t)
     K512 void rfp4_attn_prefill_hd##HD##_g8_w8(AttnPrefillArgs a) { attn_prefill_body<HD, 8, 8>(a); }
 ATTN_PREFILL_KERNELS(64)
 ATTN_PREFILL_KERNELS(128)
+// ---- fused q|k|v GEMV + attention: rfp4_qkva_hd<HD>_g<group>[_t: tagged merge]
+// (device/qkva.h).  HD 64 with K = 2048 (one slice, R = 2, the 8-wave GEMV's
+// RMS order); HD 128 with K = 4096 (two slices, R = 4, the 4-wave order).
+// The host checks the engine's shape against these (engine.cpp qkva_plan).
+#define QKVA_KERNELS(HD, NS, R, WREF) \
+    K256 void rfp4_qkva_hd##HD##_g1(QkvaArgs a) { qkva_body<HD, 1, false, NS, R, WREF>(a); } \
+    K256 void rfp4_qkva_hd##HD##_g2(QkvaArgs a) { qkva_body<HD, 2, false, NS, R, WREF>(a); } \
+    K256 void rfp4_qkva_hd##HD##_g4(QkvaArgs a) { qkva_body<HD, 4, false, NS, R, WREF>(a); } \
+    K256 void rfp4_qkva_hd##HD##_g8(QkvaArgs a) { qkva_body<HD, 8, false, NS, R, WREF>(a); } \
+    K256 void rfp4_qkva_hd##HD##_g1_t(QkvaArgs a) { qkva_body<HD, 1, true, NS, R, WREF>(a); } \
+    K256 void rfp4_qkva_hd##HD##_g2_t(QkvaArgs a) { qkva_body<HD, 2, true, NS, R, WREF>(a); } \
+    K256 void rfp4_qkva_hd##HD##_g4_t(QkvaArgs a) { qkva_body<HD, 4, true, NS, R, WREF>(a); } \
+    K256 void rfp4_qkva_hd##HD##_g8_t(QkvaArgs a) { qkva_body<HD, 8, true, NS, R, WREF>(a); }
+QKVA_KERNELS(64, 1, 2, 8)
+QKVA_KERNELS(128, 2, 4, 4)
 K256 void rfp4_attn_merge_hd64(AttnArgs a) { attn_merge_body<64>(a); }
 K256 void rfp4_attn_merge_hd128(AttnArgs a) { attn_merge_body<128>(a); }
 

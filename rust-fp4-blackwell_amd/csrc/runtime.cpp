@@ -467,6 +467,9 @@ int attn_merge_mode() { return t_attn_merge; }
 static thread_local int t_attn_head_split = 0; // query-head slices per KV head for new engines (0 = automatic)
 int attn_head_split_mode() { return t_attn_head_split; }
 
+static thread_local int t_qkva = 0; // engines created on this thread: 0 fused q|k|v GEMV + attention where it fits, 1 two launches
+int qkva_mode() { return t_qkva; }
+
 static thread_local int t_prefill_attn = 0; // 0 matrix-core prefill kernel, 1 one decode-kernel row per prompt row
 static thread_local int t_prefill_waves = 0; // prefill attention waves per workgroup (0 = automatic)
 static thread_local int t_prefill_pairing = 0; // 0 automatic, 1 one query tile per workgroup, 2 paired tiles
@@ -529,6 +532,14 @@ extern "C" int rfp4_debug_attn_head_split(int hs)
     if (hs != 0 && hs != 1 && hs != 2 && hs != 4 && hs != 8)
         return set_error(RFP4_E_INVALID, "head split must be 0 (automatic), 1, 2, 4 or 8");
     t_attn_head_split = hs;
+    return RFP4_OK;
+}
+
+extern "C" int rfp4_debug_qkv_attn(int mode)
+{
+    using namespace rfp4;
+    if (mode != 0 && mode != 1) return set_error(RFP4_E_INVALID, "q|k|v + attention mode must be 0 (fused) or 1 (two launches)");
+    t_qkva = mode;
     return RFP4_OK;
 }
 

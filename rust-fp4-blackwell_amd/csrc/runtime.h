@@ -94,6 +94,7 @@ bool attn_inmerge(uint32_t max_splits);
 int attn_merge_mode();                           // this thread's rfp4_debug_attn_merge setting
 int prefill_attn_mode();                         // this thread's rfp4_debug_prefill_attn setting
 int attn_head_split_mode();                      // this thread's rfp4_debug_attn_head_split setting
+int qkva_mode();                                 // this thread's rfp4_debug_qkv_attn setting
 int prefill_stop();                              // this thread's rfp4_debug_prefill_stop setting
 bool attn_inmerge_mode(int mode, uint32_t splits); // attn_inmerge under an explicit setting
 constexpr uint32_t kAttnInmergeMaxSplits = 8;

@@ -99,7 +99,26 @@ typedef struct AttnArgs {
     unsigned long long *tagged;
     uint32_t *err;
     uint32_t tag_splits, pad3;
+    // Fused q|k|v GEMV (one row; null = off): q, the current token's k and
+    // v as 64-bit words (float bits | tag << 32, tag = the launch's sequence
+    // length), [n_heads + 2 n_kv_heads][head_dim], stored by the GEMV
+    // workgroups of the same launch and polled by the attention workgroups.
+    // No other launch of the same sequence length may have written these
+    // words (the engine keeps one region per layer and clears them before
+    // each generation).
+    const unsigned long long *qkv_t;
 } AttnArgs;
+
+// Fused q|k|v GEMV + decode attention (device/qkva.h): workgroup b takes GEMV
+// tile b (b < n_tiles; 4R consecutive rows, RMSNorm fused) and attention
+// workgroup b (b < n_attn; KV head x query-head slice = b % (n_kv_heads *
+// head_split), split = b / (n_kv_heads * head_split)).
+typedef struct QkvaArgs {
+    GemvArgs g;               // the q|k|v GEMV (g.y unused: outputs go to yt)
+    AttnArgs a;               // the attention; a.qkv_t = yt
+    unsigned long long *yt;   // tagged q|k|v outputs, [n_heads + 2 n_kv_heads][head_dim]
+    uint32_t n_tiles, n_attn;
+} QkvaArgs;
 
 // Causal attention of the batched prefill (device/attn_prefill.h): prompt
 // row r sits at position pos0 + r and its k, v are already in the caches.
