@@ -212,11 +212,12 @@ int rfp4_debug_attn_chunk(uint32_t chunk);
  * launches as 0).  No reference counterpart. */
 int rfp4_debug_attn_merge(int mode);
 /* Test hook (this thread): the q|k|v GEMV and the decode attention of
- * engines created afterwards: 0 = one fused launch per layer wherever the
- * engine's shape has a fused kernel and its grid fits the device (the
- * default), 1 = two launches.  Outputs are bit-identical either way.  No
- * reference counterpart (the reference launches them apart,
- * llama_run/src/main.rs:513-529). */
+ * engines created afterwards: 0 = one fused launch per layer for steps whose
+ * attention is one split, where the engine's shape has a fused kernel and
+ * its grid fits the device (the default: faster there, measured), 1 = two
+ * launches, 2 = fused at every split count where the grid fits.  Outputs are
+ * bit-identical in every mode.  No reference counterpart (the reference
+ * launches them apart, llama_run/src/main.rs:513-529). */
 int rfp4_debug_qkv_attn(int mode);
 /* Test hook (this thread): query-head slices per KV head of the decode
  * attention of engines created afterwards (0 = automatic, 1, 2, 4, 8; a

@@ -78,7 +78,7 @@ struct llama_engine {
     // the tagged merge workspace), the policy fixed at creation
     uint32_t qkva_R = 0;
     unsigned long long *qkv_t = nullptr;
-    int qkva_mode = 0; // 0 = fused wherever the grid fits the device, 1 = two launches
+    int qkva_mode = 0; // 0 = fused for one-split steps, 1 = two launches, 2 = fused wherever the grid fits
     StepState *state = nullptr;
     uint32_t *ids = nullptr, *last_tok = nullptr;
     uint32_t ids_alloc = 0;
@@ -147,7 +147,14 @@ static int validate(const rfp4_model_config &c)
 // attention workgroups and grid.  False where the engine has no fused kernel
 // for its shape, the policy says two launches, or the grid does not fit the
 // device at once (the attention workgroups wait for the GEMV tiles' words,
-// so every workgroup must be resident).
+// so every workgroup must be resident).  The default policy fuses one-split
+// steps only.  Measured (graph replays, tok/s, separate -> fused): TinyLlama
+// at context 16-270 2235 -> 2304, at 300 2083 -> 2121, at 1000 (16 splits)
+// 1909 -> 1891; Llama-3-8B at context 16 779 -> 791, at 1000 (16 splits)
+// 730 -> 735, at 4096 (29 splits) 668 -> 656: with many splits the GEMV
+// tiles and the K/V stream share the launch's bandwidth and the attention
+// starts only after the last tile, which costs more than the kernel
+// boundary saves.
 struct QkvaPlan {
     char name[48];
     uint32_t hs, n_tiles, n_attn, grid;
@@ -156,7 +163,7 @@ struct QkvaPlan {
 static bool qkva_plan(const llama_engine *e, uint32_t nsplit, bool tagged, QkvaPlan *pl)
 {
     const rfp4_model_config &c = e->c;
-    if (!e->qkva_R || e->qkva_mode == 1) return false;
+    if (!e->qkva_R || e->qkva_mode == 1 || (e->qkva_mode == 0 && nsplit > 1)) return false;
     Runtime *rt = runtime();
     const uint32_t G = c.n_heads / c.n_kv_heads;
     const uint32_t hs = e->attn_head_split ? e->attn_head_split

@@ -467,7 +467,7 @@ int attn_merge_mode() { return t_attn_merge; }
 static thread_local int t_attn_head_split = 0; // query-head slices per KV head for new engines (0 = automatic)
 int attn_head_split_mode() { return t_attn_head_split; }
 
-static thread_local int t_qkva = 0; // engines created on this thread: 0 fused q|k|v GEMV + attention where it fits, 1 two launches
+static thread_local int t_qkva = 0; // engines created on this thread: 0 fused q|k|v GEMV + attention for one-split steps, 1 two launches, 2 fused wherever it fits
 int qkva_mode() { return t_qkva; }
 
 static thread_local int t_prefill_attn = 0; // 0 matrix-core prefill kernel, 1 one decode-kernel row per prompt row
@@ -538,7 +538,9 @@ extern "C" int rfp4_debug_attn_head_split(int hs)
 extern "C" int rfp4_debug_qkv_attn(int mode)
 {
     using namespace rfp4;
-    if (mode != 0 && mode != 1) return set_error(RFP4_E_INVALID, "q|k|v + attention mode must be 0 (fused) or 1 (two launches)");
+    if (mode < 0 || mode > 2)
+        return set_error(RFP4_E_INVALID, "q|k|v + attention mode must be 0 (fused for one split), 1 (two launches) or 2 "
+                                         "(fused wherever the grid fits)");
     t_qkva = mode;
     return RFP4_OK;
 }

@@ -4,8 +4,9 @@ llama_run/src/main.rs:513-529.  Its outputs are computed with the two
 launches' arithmetic, so tokens and logits must be bit-identical to an
 engine made with the fusion off (rfp4_debug_qkv_attn(1)), in every merge
 regime of the attention splits (one split, the last-arriver merge up to 8,
-tagged states up to 32, the merge kernel beyond) and every query-head slice
-count, and the tokens must be the oracle's."""
+tagged states up to 32, the merge kernel beyond; mode 2 fuses at every split
+count, the default only one-split steps) and every query-head slice count,
+and the tokens must be the oracle's."""
 import numpy as np
 import pytest
 
@@ -21,7 +22,7 @@ W128 = dict(dim=4096, n_layers=2, n_heads=32, n_kv_heads=8, head_dim=128, ffn=51
 
 def _engine(rf, cfg, seed, fused, chunk=0, slices=0):
     c = {k: v for k, v in cfg.items() if k != "max_seq"}
-    rf.check(rf.load().rfp4_debug_qkv_attn(0 if fused else 1))
+    rf.check(rf.load().rfp4_debug_qkv_attn(2 if fused else 1))
     rf.check(rf.load().rfp4_debug_attn_head_split(slices))
     rf.debug_attn_chunk(chunk)
     try:
@@ -121,3 +122,23 @@ def test_fused_eager_equals_graph(rf):
     np.testing.assert_array_equal(g.generate(prompt, 0, 40), tg)
     np.testing.assert_array_equal(g.logits(), lg)
     g.close()
+
+
+@pytest.mark.parametrize("cfg", [W64, W128], ids=["hd64", "hd128"])
+def test_default_policy_fuses_one_split_steps(rf, cfg):
+    """The default engine fuses the q|k|v GEMV and the attention for steps
+    whose attention is one split and keeps two launches past that."""
+    c = {k: v for k, v in cfg.items() if k != "max_seq"}
+    rf.debug_attn_chunk(30)
+    try:
+        e = rf.Engine(rf.model_config(max_seq=cfg["max_seq"], **c), 0x5151)
+    finally:
+        rf.debug_attn_chunk(0)
+    prompt = [2, 9, 77]
+    e.begin(prompt, 0, 8)
+    one = [n for n, _ in e.time_steps(1)]
+    e.begin(prompt, 200, 8)  # 7 splits of 30 tokens
+    many = [n for n, _ in e.time_steps(1)]
+    assert any(n.startswith("rfp4_qkva") for n in one), one
+    assert not any(n.startswith("rfp4_qkva") for n in many), many
+    e.close()
