@@ -195,9 +195,10 @@ int fp4_gemm(rfp4_stream_t stream, uint32_t m, uint32_t n, uint32_t k, const uin
              const uint8_t *a_scales, const uint8_t *w_codes, const uint8_t *w_scales, float *c);
 /* Test hook: force the GEMM tile (index into the compiled list, largest
  * first: 256x256, 256x128, 128x128, 64x128, 32x128, then 5 = the few-row
- * kernel for m <= 64 and k % 2048 == 0; -1 = automatic) and K split
- * (0 = automatic; tiled kernels only) of later fp4_gemm calls on this
- * thread.  No reference counterpart. */
+ * kernel for m <= 64 and k a multiple of 512 up to 16384; -1 = automatic)
+ * and K split (0 = automatic; for the few-row kernel: W fragments of 16 rows
+ * per workgroup, 1, 2 or 4) of later fp4_gemm calls on this thread.  No
+ * reference counterpart. */
 int rfp4_debug_gemm_plan(int tile, int kz);
 /* Test hook: tokens per split of later attn_decode / attn_decode_f16 calls
  * on this thread (0 = automatic).  No reference counterpart. */

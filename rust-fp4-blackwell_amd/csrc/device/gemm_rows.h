@@ -1,0 +1,134 @@
+// MXFP4 GEMM for few activation rows (M <= 16 MB, the batched-decode case),
+// streamed like the decode GEMV: C[M][N] = A[M][K] . W[N][K]^T, A and W
+// MXFP4 (E2M1 codes two per byte, low nibble first; E8M0 per 32 along K),
+// C f32.  Semantics as gemm.h (trackb/fp4_scale_test.cu:37 taken to M x N x K).
+//
+// MFMA: v_mfma_scale_f32_16x16x128_f8f6f4 with the W rows as the A operand
+// and the activation rows as the B operand, so D[i][j] = sum_k W[n0 + i][k]
+// A[16 mb + j][k]: lane l holds operand row l % 16 and the K values
+// 32 (l / 16) .. +31 of the 128-wide tile with that block's scale byte, and
+// D register r of lane l is D[4 (l / 16) + r][l % 16] (pinned by the 16x16
+// layout test).  K advances in segments of 512 values (256 bytes per row):
+// MFMA t (0..3) of a segment takes bytes 64 t + 16 q .. +15 of it (values
+// 128 t + 32 q .. +31, E8M0 block 4 t + q) in lane (r, q = l / 16), in W and
+// A alike, so each load instruction reads 64 contiguous bytes of 16 rows and
+// one 16-byte load per lane brings a row's 16 scale bytes of the segment.
+//
+// Workgroup: one block of 16 NF W rows (NF fragments, which share every
+// activation load) and all of K; its NW <= 8 waves (blockDim / 64) take the K
+// segments w, w + NW, ... (at most SEG each), with every load of a wave (W,
+// the activation rows, their scales) issued before its first MFMA, like the
+// GEMV's slices.  The NW partial 16 NF x 16 MB tiles are summed through LDS
+// in wave order.  Each weight byte is read once; the activations (M x K/2
+// bytes) are re-read by every workgroup from the L2, 1/NF of the W bytes per
+// activation row fragment.
+#pragma once
+#include "common.h"
+#include "mma.h"
+
+template <int MB, int SEG, int NF>
+RFP4_DEV void gemm_rows_body(const GemmArgs &g)
+{
+    __shared__ __align__(16) float red[8][NF * MB][4][64];
+    const uint32_t lane = threadIdx.x & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const uint32_t nw = blockDim.x >> 6;
+    const uint32_t r16 = lane & 15u, q = lane >> 4;
+    const uint32_t n0 = blockIdx.x * 16u * NF;
+    const uint32_t kbytes = g.k >> 1, nblk = g.k >> 5, nseg = g.k >> 9;
+
+    const uint8_t *wc[NF], *wsc[NF];
+#pragma unroll
+    for (int f = 0; f < NF; f++) {
+        const uint32_t wrow = min(n0 + 16u * f + r16, g.n - 1u); // clamp: loads stay in bounds
+        wc[f] = g.w_codes + (size_t)wrow * kbytes + q * 16u;
+        wsc[f] = g.w_scales + (size_t)wrow * nblk;
+    }
+    const uint8_t *ac[MB], *asc[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) {
+        const uint32_t arow = min(16u * mb + r16, g.m - 1u);
+        ac[mb] = g.a_codes + (size_t)arow * kbytes + q * 16u;
+        asc[mb] = g.a_scales + (size_t)arow * nblk;
+    }
+
+    // every load of this wave's segments first
+    uint4 wv[SEG][NF][4], av[SEG][MB][4], wsv[SEG][NF], asv[SEG][MB];
+#pragma unroll
+    for (int s = 0; s < SEG; s++) {
+        const uint32_t seg = wave + nw * (uint32_t)s;
+        if (seg >= nseg) break;
+#pragma unroll
+        for (int f = 0; f < NF; f++) {
+#pragma unroll
+            for (int t = 0; t < 4; t++) wv[s][f][t] = *(const uint4 *)(wc[f] + (size_t)seg * 256u + t * 64u);
+            wsv[s][f] = *(const uint4 *)(wsc[f] + (size_t)seg * 16u);
+        }
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++) {
+#pragma unroll
+            for (int t = 0; t < 4; t++) av[s][mb][t] = *(const uint4 *)(ac[mb] + (size_t)seg * 256u + t * 64u);
+            asv[s][mb] = *(const uint4 *)(asc[mb] + (size_t)seg * 16u);
+        }
+    }
+
+    v4f32 acc[NF][MB];
+#pragma unroll
+    for (int f = 0; f < NF; f++)
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++) acc[f][mb] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < SEG; s++) {
+        const uint32_t seg = wave + nw * (uint32_t)s;
+        if (seg >= nseg) break;
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+#pragma unroll
+            for (int f = 0; f < NF; f++) {
+                const uint4 w = wv[s][f][t];
+                const v8i32 w8 = {(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
+                const uint32_t sws[4] = {wsv[s][f].x, wsv[s][f].y, wsv[s][f].z, wsv[s][f].w};
+                const int sw = (int)((sws[t] >> (8u * q)) & 0xFFu); // block 4 t + q
+#pragma unroll
+                for (int mb = 0; mb < MB; mb++) {
+                    const uint4 a = av[s][mb][t];
+                    const v8i32 a8 = {(int)a.x, (int)a.y, (int)a.z, (int)a.w, 0, 0, 0, 0};
+                    const uint32_t sas[4] = {asv[s][mb].x, asv[s][mb].y, asv[s][mb].z, asv[s][mb].w};
+                    const int sa = (int)((sas[t] >> (8u * q)) & 0xFFu);
+                    acc[f][mb] = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(w8, a8, acc[f][mb], MX_FMT_FP4, MX_FMT_FP4,
+                                                                                  0, sw, 0, sa);
+                }
+            }
+        }
+    }
+
+    // ---- the waves' partial tiles summed in wave order; lane (r16, q) of
+    // tile (f, mb) stores C[16 mb + r16][n0 + 16 f + 4 q .. +3]
+#pragma unroll
+    for (int f = 0; f < NF; f++)
+#pragma unroll
+        for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) red[wave][f * MB + mb][r][lane] = acc[f][mb][r];
+    __syncthreads();
+    for (uint32_t fm = wave; fm < (uint32_t)(NF * MB); fm += nw) {
+        const uint32_t f = fm / MB, mb = fm % MB;
+        float v[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            float sum = red[0][fm][r][lane];
+            for (uint32_t w = 1; w < nw; w++) sum = __fadd_rn(sum, red[w][fm][r][lane]);
+            v[r] = sum;
+        }
+        const uint32_t row = 16u * mb + r16, col = n0 + 16u * f + 4u * q;
+        if (row >= g.m) continue;
+        float *cp = g.c + (size_t)row * g.n + col;
+        if (col + 3u < g.n && (g.n & 3u) == 0u) {
+            *(float4 *)cp = make_float4(v[0], v[1], v[2], v[3]);
+        } else {
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                if (col + (uint32_t)r < g.n) cp[r] = v[r];
+        }
+    }
+}

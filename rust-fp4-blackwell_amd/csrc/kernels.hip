@@ -9,7 +9,7 @@
 #include "device/misc.h"
 #include "device/mma.h"
 #include "device/gemm.h"
-#include "device/gemm_skinny.h"
+#include "device/gemm_rows.h"
 #include "device/prefill.h"
 #include "device/attn_prefill.h"
 #include "device/persist.h"
@@ -161,15 +161,24 @@ GEMM_KERNEL(128, 128, 2, 2, 2, 2)
 GEMM_KERNEL(256, 128, 2, 2, 4, 2)
 GEMM_KERNEL(256, 256, 2, 2, 4, 4)
 K256 void rfp4_gemm_reduce(GemmArgs a) { gemm_reduce_body(a); }
-// few activation rows (M <= 16, 32, 64) x 16 or 32 W rows per workgroup
-#define GEMM_SKINNY_KERNEL(M, MA, NB) \
-    K256 void rfp4_gemm_skinny_m##M##_n##NB(GemmArgs a) { gemm_skinny_body<MA, NB>(a); }
-GEMM_SKINNY_KERNEL(16, 1, 1)
-GEMM_SKINNY_KERNEL(16, 1, 2)
-GEMM_SKINNY_KERNEL(32, 2, 1)
-GEMM_SKINNY_KERNEL(32, 2, 2)
-GEMM_SKINNY_KERNEL(64, 4, 1)
-GEMM_SKINNY_KERNEL(64, 4, 2)
+// few activation rows (M <= 16 MB) x 16 NF W rows per workgroup, up to 8
+// waves of up to SEG K segments of 512 each (device/gemm_rows.h):
+// rfp4_gemm_rows_m<16 MB>_s<SEG>_f<NF>, the combinations whose loads fit the
+// registers (runtime.cpp gemm_rows_has); keep the two lists in sync.
+#define GEMM_ROWS_KERNEL(M, MB, SEG, NF) \
+    K512 void rfp4_gemm_rows_m##M##_s##SEG##_f##NF(GemmArgs a) { gemm_rows_body<MB, SEG, NF>(a); }
+#define GEMM_ROWS_SMALL_M(M, MB) \
+    GEMM_ROWS_KERNEL(M, MB, 1, 1) \
+    GEMM_ROWS_KERNEL(M, MB, 1, 2) \
+    GEMM_ROWS_KERNEL(M, MB, 1, 4) \
+    GEMM_ROWS_KERNEL(M, MB, 2, 1) \
+    GEMM_ROWS_KERNEL(M, MB, 2, 2) \
+    GEMM_ROWS_KERNEL(M, MB, 4, 1)
+GEMM_ROWS_SMALL_M(16, 1)
+GEMM_ROWS_SMALL_M(32, 2)
+GEMM_ROWS_KERNEL(64, 4, 1, 1)
+GEMM_ROWS_KERNEL(64, 4, 1, 2)
+GEMM_ROWS_KERNEL(64, 4, 2, 1)
 
 // ---- persistent decode of every layer of a step, one workgroup per CU
 // (device/persist.h): rfp4_decode_layers_<shape>

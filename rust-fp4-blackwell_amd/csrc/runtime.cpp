@@ -1054,25 +1054,51 @@ constexpr GemmTile kGemmTiles[] = {
     {64, 128, "rfp4_gemm_64x128", 3},   {32, 128, "rfp4_gemm_32x128", 3},
 };
 constexpr int kGemmNumTiles = (int)(sizeof(kGemmTiles) / sizeof(kGemmTiles[0]));
-// plan index of the few-row kernel (gemm_skinny.h): 16 * MA activation rows, 16 * NB W rows per workgroup
+// plan index of the few-row kernel (gemm_rows.h): 16 * MA activation rows,
+// 16 W rows per workgroup, at most SEG (nb) K segments of 512 per wave
 constexpr int kGemmSkinny = kGemmNumTiles;
 thread_local int t_gemm_tile = -1, t_gemm_kz = 0;
 
 struct GemmPlan {
     int tile;
     uint32_t kz;
-    int ma = 0, nb = 0; // skinny plan only
+    int ma = 0, nb = 0; // few-row plan only: activation fragments, K segments per wave
 };
 
-bool gemm_skinny_ok(uint32_t m, uint32_t k) { return m <= 64u && k % 2048u == 0u; }
-// Measured on MI355X at m = 32: the few-row kernel wins while W is small
-// (4096x4096: 6.2 vs 9.0 us for the tiled kernel with its split-K reduce);
-// on larger W its 16-row workgroups re-read A at twice the W bytes and the
-// tiled kernel, which shares A through LDS across 128 W rows, is faster
-// (14336x4096: 11.9 vs 17.1 us).
+// The few-row kernel: at most 64 activation rows, K a multiple of 512 in at
+// most 8 waves of up to 4 segments (2 for 64 rows).
+bool gemm_skinny_ok(uint32_t m, uint32_t k)
+{
+    return m <= 64u && k % 512u == 0u && k / 512u <= (m <= 32u ? 32u : 16u);
+}
+// Measured on MI355X at m = 32 (us, few-row kernel with 1 / 2 / 4 W
+// fragments per workgroup, tiled 32x128): 4096x4096 6.75 / 7.96 / 10.25,
+// 10.20; 6144x4096 10.01 / 8.18 / 10.37, 11.50; 14336x4096 16.91 / 12.71 /
+// 10.86, 13.28; 28672x4096 31.22 / 26.06 / 20.55, 21.54; 4096x14336 14.61
+// (one fragment), 15.42; 128256x4096 127.35 / 91.91 / 72.90, 68.41.  The
+// tiled kernel, which shares each activation load over 128 W rows, wins only
+// on very wide W.
 bool gemm_skinny_pays(uint32_t m, uint32_t n, uint32_t k)
 {
-    return gemm_skinny_ok(m, k) && (uint64_t)n * k <= (1ull << 25);
+    return gemm_skinny_ok(m, k) && m <= 32u && n < 65536u;
+}
+// K segments per wave: the K segments over at most 8 waves
+uint32_t gemm_rows_seg(uint32_t k) { return k / 512u <= 8u ? 1u : (k / 512u <= 16u ? 2u : 4u); }
+// the compiled few-row variants (kernels.hip GEMM_ROWS_KERNEL): fragments
+// of 16 activation rows, K segments per wave, fragments of 16 W rows
+bool gemm_rows_has(int mb, int seg, int nf)
+{
+    if (mb <= 2) return (seg == 1 && (nf == 1 || nf == 2 || nf == 4)) || (seg == 2 && (nf == 1 || nf == 2)) || (seg == 4 && nf == 1);
+    return (seg <= 2 && nf == 1) || (seg == 1 && nf == 2);
+}
+// W fragments per workgroup: the most (4, 2, 1) that still give three CUs in
+// four a workgroup (each workgroup shares its activation loads over its W
+// rows; measured above)
+int gemm_rows_nf(int mb, int seg, uint32_t n, uint32_t num_cus)
+{
+    for (int nf = 4; nf > 1; nf /= 2)
+        if (gemm_rows_has(mb, seg, nf) && 4ull * ((n + 16u * nf - 1u) / (16u * nf)) >= 3ull * num_cus) return nf;
+    return 1;
 }
 
 uint32_t ceil_div(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
@@ -1085,12 +1111,13 @@ GemmPlan gemm_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t num_cus)
 {
     const uint32_t nsuper = k / 256u;
     if (t_gemm_tile == kGemmSkinny || (t_gemm_tile < 0 && gemm_skinny_pays(m, n, k))) {
-        // few activation rows: stream W like a GEMV; two W fragments per
-        // workgroup (half the activation re-reads) once that still leaves
-        // two workgroups per CU
+        // few activation rows: stream W like a GEMV, 16 NF W rows per
+        // workgroup (kz: NF, a forced plan may set it)
         GemmPlan p{kGemmSkinny, 1u};
         p.ma = m <= 16u ? 1 : (m <= 32u ? 2 : 4);
-        p.nb = (uint64_t)n >= 64ull * num_cus ? 2 : 1;
+        p.nb = (int)gemm_rows_seg(k);
+        p.kz = t_gemm_tile == kGemmSkinny && t_gemm_kz > 0 ? (uint32_t)t_gemm_kz
+                                                            : (uint32_t)gemm_rows_nf(p.ma, p.nb, n, num_cus);
         return p;
     }
     int pick = t_gemm_tile;
@@ -1183,11 +1210,15 @@ int gemm_launch(hipStream_t stream, uint32_t m, uint32_t n, uint32_t k, const ui
     GemmPlan p = gemm_plan(m, n, k, (uint32_t)rt->num_cus);
     if (p.tile == kGemmSkinny) {
         if (!gemm_skinny_ok(m, k))
-            return set_error(RFP4_E_SHAPE, "fp4_gemm: the few-row kernel needs m <= 64 and k %% 2048 == 0 (m=%u k=%u)", m, k);
+            return set_error(RFP4_E_SHAPE, "fp4_gemm: the few-row kernel needs m <= 64 and k a multiple of 512 up to 32768 "
+                                           "(m=%u k=%u)", m, k);
+        if (!gemm_rows_has(p.ma, p.nb, (int)p.kz))
+            return set_error(RFP4_E_INVALID, "fp4_gemm: no few-row variant with %d W fragments for m=%u k=%u", (int)p.kz, m, k);
         char name[48];
-        snprintf(name, sizeof name, "rfp4_gemm_skinny_m%d_n%d", 16 * p.ma, p.nb);
+        snprintf(name, sizeof name, "rfp4_gemm_rows_m%d_s%d_f%u", 16 * p.ma, p.nb, p.kz);
+        const uint32_t waves = ceil_div(k / 512u, (uint32_t)p.nb);
         GemmArgs a{a_codes, a_scales, w_codes, w_scales, c, nullptr, m, n, k, 1u};
-        return launch(name, dim3(ceil_div(n, 16u * (uint32_t)p.nb)), dim3(256), (hipStream_t)stream, &a);
+        return launch(name, dim3(ceil_div(n, 16u * p.kz)), dim3(64u * waves), (hipStream_t)stream, &a);
     }
     const GemmTile &t = kGemmTiles[p.tile];
     const uint64_t tiles = (uint64_t)ceil_div(m, t.bm) * ceil_div(n, t.bn);
@@ -1229,7 +1260,7 @@ int rfp4_gemm_plan(uint32_t m, uint32_t n, uint32_t k, int *tile_m, int *tile_n,
     if (k == 0 || k % 256u || m == 0 || n == 0) return set_error(RFP4_E_SHAPE, "gemm_plan: bad shape");
     GemmPlan p = gemm_plan(m, n, k, cus);
     if (tile_m) *tile_m = p.tile == kGemmSkinny ? 16 * p.ma : (int)kGemmTiles[p.tile].bm;
-    if (tile_n) *tile_n = p.tile == kGemmSkinny ? 16 * p.nb : (int)kGemmTiles[p.tile].bn;
+    if (tile_n) *tile_n = p.tile == kGemmSkinny ? 16 * (int)p.kz : (int)kGemmTiles[p.tile].bn;
     if (kz) *kz = (int)p.kz;
     return RFP4_OK;
 }

@@ -80,29 +80,60 @@ def test_gemm_every_tile_and_split(rf, orc, stream, forced_plan, tile, kz):
 
 
 @pytest.mark.parametrize("m", [1, 7, 16, 17, 32, 33, 64])
-@pytest.mark.parametrize("n,k", [(4, 2048), (292, 2048), (1040, 6144)])
+@pytest.mark.parametrize("n,k", [(4, 2048), (292, 2048), (1040, 6144), (36, 512), (100, 5632), (60, 14336), (20, 16384)])
 def test_gemm_few_rows_kernel(rf, orc, stream, forced_plan, m, n, k):
-    """The few-row kernel (m <= 64, k % 2048 == 0: 16/32/64-row activation
-    fragments, 16 or 32 W rows per workgroup, K in wave quarters) on ragged
-    m and n, forced and automatic, against the oracle."""
+    """The few-row kernel (m <= 64, k a multiple of 512 up to 16384: 16/32/64
+    activation rows per fragment, K segments of 512 over up to 8 waves, 1, 2
+    or 4 per wave (64 rows: up to 2): k = 512 one wave, 5632 eleven segments
+    over six waves of two, 14336 and 16384 over seven and eight waves of
+    four) on ragged m and n, forced and automatic (m <= 32), against the
+    oracle."""
+    if m > 32 and k > 8192:
+        pytest.skip("64-row fragments take k <= 8192")
     ac, asc = _uniform_mx(orc, m, k, 61 + m)
     wc, wsc = _uniform_mx(orc, n, k, 71 + n)
     c64, absc = orc.gemm_mx_f64(m, n, k, ac, asc, wc, wsc)
-    for plan in ((5, 0), (-1, 0)):   # forced, and automatic (these shapes are small enough)
+    plans = ((5, 0), (-1, 0)) if m <= 32 else ((5, 0),)
+    for plan in plans:
         forced_plan(*plan)
         tm, tn, kz = rf.gemm_plan(m, n, k)
-        assert tm == (16 if m <= 16 else 32 if m <= 32 else 64) and kz == 1
+        assert tm == (16 if m <= 16 else 32 if m <= 32 else 64) and tn == 16 * kz and kz == 1
         c = _gemm(rf, stream, m, n, k, ac, asc, wc, wsc)
         _assert_gemm_close(c, c64, absc)
+        c2 = _gemm(rf, stream, m, n, k, ac, asc, wc, wsc)
+        np.testing.assert_array_equal(c.view(np.uint32), c2.view(np.uint32))  # deterministic
 
 
-def test_gemm_few_rows_two_w_fragments(rf, orc, stream, forced_plan):
-    """Wide N takes 32 W rows per workgroup; a ragged last workgroup."""
-    m, n, k = 32, 16400, 2048
+# every compiled few-row variant: (activation fragments, K segments per wave, W fragments)
+ROWS_VARIANTS = [(mb, seg, nf) for mb in (1, 2) for seg, nf in ((1, 1), (1, 2), (1, 4), (2, 1), (2, 2), (4, 1))] + \
+    [(4, 1, 1), (4, 1, 2), (4, 2, 1)]
+
+
+@pytest.mark.parametrize("mb,seg,nf", ROWS_VARIANTS)
+def test_gemm_few_rows_every_variant(rf, orc, stream, forced_plan, mb, seg, nf):
+    """Each few-row variant, forced through its W-fragment count, on ragged m
+    (16 mb - 3 rows), n (a ragged last workgroup) and a K whose segment count
+    needs its segments per wave."""
+    m = 16 * mb - 3
+    k = 512 * (8 * seg - 3 if seg > 1 else 5)
+    n = 16 * nf * 3 + 4
+    ac, asc = _uniform_mx(orc, m, k, 91 + mb)
+    wc, wsc = _uniform_mx(orc, n, k, 95 + nf)
+    forced_plan(5, nf)
+    assert rf.gemm_plan(m, n, k) == (16 * mb, 16 * nf, nf)
+    c = _gemm(rf, stream, m, n, k, ac, asc, wc, wsc)
+    c64, absc = orc.gemm_mx_f64(m, n, k, ac, asc, wc, wsc)
+    _assert_gemm_close(c, c64, absc)
+
+
+def test_gemm_few_rows_wide_n(rf, orc, stream, forced_plan):
+    """Wide N takes 2 or 4 W fragments per workgroup (here 4: 257 workgroups
+    of 64 rows) with a ragged last workgroup."""
+    m, n, k = 32, 16396, 2048
     ac, asc = _uniform_mx(orc, m, k, 81)
     wc, wsc = _uniform_mx(orc, n, k, 82)
     forced_plan(5, 0)
-    assert rf.gemm_plan(m, n, k) == (32, 32, 1)
+    assert rf.gemm_plan(m, n, k) == (32, 64, 4)
     c = _gemm(rf, stream, m, n, k, ac, asc, wc, wsc)
     cols = np.unique(np.concatenate([np.arange(48), n - 48 + np.arange(48),
                                      np.random.default_rng(1).choice(n, 400, replace=False)]))
