@@ -435,17 +435,26 @@ static bool gemv_has_ns(bool f32scale, int epi, int R, int ns, int W = 4)
 // Rows per wave R and up-front K-slices NS for a GEMV launch.  NS = K/2048
 // rounded up whenever compiled (all loads in flight at once), else the slice
 // loop.  Measured on MI355X with x in conflict-free LDS (weights streamed
-// from HBM, 8B / TinyLlama shapes): R = 1 for the SwiGLU pair (8B gate|up
-// 12.7 us vs 12.9-13.6 at R = 2 and 17.3 at R = 4), R = 2 elsewhere (8B down
-// 9.5 us vs 11.1 at R = 4 and 10.6 at R = 1; q|k|v 5.0 vs 5.2-5.4; TinyLlama
-// LM head 7.9-8.1 vs 8.3 at R = 4), R = 8 for very wide matrices with short
-// K (8B LM head).  The same choices for f32 scales.
+// from HBM, 8B / TinyLlama shapes): for the SwiGLU pair R = 1 at one slice
+// (TinyLlama gate|up on 8 waves 4.56 us) and R = 2 from two slices up with
+// E8M0 scales (8B gate|up 12.3 us vs 13.1 at R = 1 alone; in the 8B decode
+// step at context 4096, 688 -> 700 tok/s), R = 2 elsewhere (8B down 9.5 us
+// vs 11.1 at R = 4 and 10.6 at R = 1; q|k|v 5.0 vs 5.2-5.4; TinyLlama LM head
+// 7.9-8.1 vs 8.3 at R = 4), except R = 1 for residual GEMVs of at most 2048
+// rows (twice the workgroups of R = 2 where R = 2 gives one per CU; decode
+// step, three engines of each interleaved: TinyLlama 2272 -> 2304 tok/s,
+// Llama-3.2-1B 2774 -> 2777), R = 8 for very wide matrices with short K (8B
+// LM head).
+// With f32 scales (their compiled set): R = 1 for SwiGLU, R = 2 for every
+// residual GEMV, the rest as E8M0.
 GemvVariant gemv_variant(uint32_t n, uint32_t k, int epi, bool f32scale)
 {
     int ns_needed = (int)((k + 2047u) / 2048u);
     int R;
-    if (epi == RFP4_EPI_SWIGLU) R = (f32scale || gemv_has_ns(f32scale, epi, 1, ns_needed)) ? 1 : 2;
+    if (epi == RFP4_EPI_SWIGLU)
+        R = f32scale || (ns_needed == 1 && gemv_has_ns(f32scale, epi, 1, ns_needed)) ? 1 : 2;
     else if (n >= 65536u && ns_needed <= 2) R = 8;
+    else if (epi == RFP4_EPI_RESIDUAL && n <= 2048u && !f32scale) R = 1;
     else R = 2;
     // 8 waves per workgroup where compiled (one-slice SwiGLU at R = 1, store
     // at R = 2: K <= 2048), else 4.  Measured in the TinyLlama decode step:
