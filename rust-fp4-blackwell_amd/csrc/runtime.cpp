@@ -1080,16 +1080,17 @@ bool gemm_skinny_ok(uint32_t m, uint32_t k)
 {
     return m <= 64u && k % 512u == 0u && k / 512u <= (m <= 32u ? 32u : 16u);
 }
-// Measured on MI355X at m = 32 (us, few-row kernel with 1 / 2 / 4 W
-// fragments per workgroup, tiled 32x128): 4096x4096 6.75 / 7.96 / 10.25,
-// 10.20; 6144x4096 10.01 / 8.18 / 10.37, 11.50; 14336x4096 16.91 / 12.71 /
-// 10.86, 13.28; 28672x4096 31.22 / 26.06 / 20.55, 21.54; 4096x14336 14.61
-// (one fragment), 15.42; 128256x4096 127.35 / 91.91 / 72.90, 68.41.  The
-// tiled kernel, which shares each activation load over 128 W rows, wins only
-// on very wide W.
+// Measured on MI355X at m = 32 (us, HIP events; few-row kernel with 1 / 2 / 4
+// W fragments per workgroup, then the tiled 32x128): 4096x4096 5.81 / 6.62 /
+// 9.11, 10.11; 6144x4096 7.87 / 6.93 / 9.20, 11.60; 28672x4096 23.91 / 20.25
+// / 17.70, 21.49; 4096x14336 14.52 (one fragment), 15.03; 128256x4096 90.19 /
+// 69.90 / 62.49, 68.38.  At m = 16 the 128256x4096 LM head 56.90 (4
+// fragments) against 64.78 tiled.  The few-row kernel wins at every shape up
+// to 32 rows.
 bool gemm_skinny_pays(uint32_t m, uint32_t n, uint32_t k)
 {
-    return gemm_skinny_ok(m, k) && m <= 32u && n < 65536u;
+    (void)n;
+    return gemm_skinny_ok(m, k) && m <= 32u;
 }
 // K segments per wave: the K segments over at most 8 waves
 uint32_t gemm_rows_seg(uint32_t k) { return k / 512u <= 8u ? 1u : (k / 512u <= 16u ? 2u : 4u); }

@@ -100,7 +100,7 @@ def test_gemm_plan_shapes(m, n, k):
     (at least 7/8 of them, at least half from 1024 rows) unless the K split
     is at its maximum."""
     tm, tn, kz = rfp4.gemm_plan(m, n, k)
-    if m <= 32 and k % 512 == 0 and n < 65536:   # few-row kernel: kz = W fragments per workgroup
+    if m <= 32 and k % 512 == 0:   # few-row kernel: kz = W fragments per workgroup
         nf = next(f for f in (4, 2, 1) if f == 1 or (4 * -(-n // (16 * f)) >= 3 * 256 and k <= (4096 if f == 4 else 8192)))
         assert (tm, tn, kz) == (16 if m <= 16 else 32, 16 * nf, nf)
         return
@@ -125,10 +125,10 @@ def test_gemm_plan_shapes(m, n, k):
     (2048, 4096, 4096, (128, 128, 1)),   # (29.6 vs 33.2 us)
     (2048, 4096, 14336, (128, 128, 1)),  # (82.2 vs 90.2 us)
     (2048, 28672, 4096, (256, 256, 1)),
-    (32, 28672, 4096, (32, 64, 4)),      # few rows, 4 W fragments (20.6 us vs 21.5 tiled)
-    (32, 6144, 4096, (32, 32, 2)),       # few rows, 2 W fragments (8.2 vs 10.0 with one)
-    (32, 4096, 14336, (32, 16, 1)),      # few rows, 4 segments per wave (14.6 vs 15.4 tiled)
-    (32, 128256, 4096, (32, 128, 1)),    # very wide: tiled (68.4 vs 72.9 us)
+    (32, 28672, 4096, (32, 64, 4)),      # few rows, 4 W fragments (17.7 us vs 21.5 tiled)
+    (32, 6144, 4096, (32, 32, 2)),       # few rows, 2 W fragments (6.9 vs 7.9 with one)
+    (32, 4096, 14336, (32, 16, 1)),      # few rows, 4 segments per wave (14.5 vs 15.0 tiled)
+    (32, 128256, 4096, (32, 64, 4)),     # very wide, 4 W fragments (62.5 vs 68.4 us tiled)
 ])
 def test_gemm_plan_measured_choices(m, n, k, plan):
     """The planner's choices on the 8B prefill and decode-batch shapes that
