@@ -1083,8 +1083,8 @@ bool gemm_skinny_ok(uint32_t m, uint32_t k)
 // Measured on MI355X at m = 32 (us, HIP events; few-row kernel with 1 / 2 / 4
 // W fragments per workgroup, then the tiled 32x128): 4096x4096 5.81 / 6.62 /
 // 9.11, 10.11; 6144x4096 7.87 / 6.93 / 9.20, 11.60; 28672x4096 23.91 / 20.25
-// / 17.70, 21.49; 4096x14336 14.52 (one fragment), 15.03; 128256x4096 90.19 /
-// 69.90 / 62.49, 68.38.  At m = 16 the 128256x4096 LM head 56.90 (4
+// / 17.70, 21.49; 4096x14336 11.66 (one fragment), 15.35; 128256x4096 91.74
+// / 69.10 / 62.66, 68.67.  At m = 16 the 128256x4096 LM head 56.90 (4
 // fragments) against 64.78 tiled.  The few-row kernel wins at every shape up
 // to 32 rows.
 bool gemm_skinny_pays(uint32_t m, uint32_t n, uint32_t k)
