@@ -200,6 +200,11 @@ int fp4_gemm(rfp4_stream_t stream, uint32_t m, uint32_t n, uint32_t k, const uin
  * per workgroup, 1, 2 or 4) of later fp4_gemm calls on this thread.  No
  * reference counterpart. */
 int rfp4_debug_gemm_plan(int tile, int kz);
+/* Test hook (this thread): DMA stages of the tiled MXFP4 GEMM's K pipeline
+ * (0 = the planner's choice, 2 = double buffer, 3 or 4 = that many stages
+ * where a kernel is compiled for the tile; others fail at launch).  No
+ * reference counterpart. */
+int rfp4_debug_gemm_stages(int nst);
 /* Test hook: tokens per split of later attn_decode / attn_decode_f16 calls
  * on this thread (0 = automatic).  No reference counterpart. */
 int rfp4_debug_attn_chunk(uint32_t chunk);

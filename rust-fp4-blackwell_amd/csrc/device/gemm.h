@@ -41,15 +41,30 @@ typedef __attribute__((address_space(1))) void rfp4_glb_void;
 // keeps the fragment reads of 8 (and of 16) consecutive rows on distinct banks.
 RFP4_DEV uint32_t gemm_swz(uint32_t r) { return (r ^ (r >> 3)) & 7u; }
 
-template <int WM, int WN, int FA, int FB>
+// Wait until at most n steps' DMAs of this wave are in flight (C DMA
+// instructions per step; n < 4): they complete in issue order.
+template <uint32_t C>
+RFP4_DEV void gemm_wait_steps(uint32_t n)
+{
+    static_assert(3u * C < 64u, "vmcnt field");
+#define RFP4_VMCNT(V) (((V) & 0xFu) | (((V) >> 4) << 14) | (0x7u << 4) | (0xFu << 8))
+    if (n == 0u) __builtin_amdgcn_s_waitcnt(RFP4_VMCNT(0u));
+    else if (n == 1u) __builtin_amdgcn_s_waitcnt(RFP4_VMCNT(C));
+    else if (n == 2u) __builtin_amdgcn_s_waitcnt(RFP4_VMCNT(2u * C));
+    else __builtin_amdgcn_s_waitcnt(RFP4_VMCNT(3u * C));
+#undef RFP4_VMCNT
+}
+
+template <int WM, int WN, int FA, int FB, int NST = 2>
 RFP4_DEV void gemm_body(const GemmArgs &g)
 {
     static_assert(WM * WN == 4, "4 waves");
+    static_assert(NST >= 2 && NST <= 4, "stages");
     constexpr uint32_t BM = 32u * FA * WM, BN = 32u * FB * WN, R = BM + BN;
     constexpr uint32_t NJ = R / 32u;                 // 8-row code blocks per wave per step (1 KB each)
     constexpr uint32_t NSB = (R / 32u + 3u) / 4u;    // 32-row scale blocks per wave per step (256 B each)
     constexpr uint32_t SC0 = R * 128u, STAGE = R * 128u + R * 8u;
-    __shared__ __attribute__((aligned(1024))) uint8_t lds_raw[2 * STAGE];
+    __shared__ __attribute__((aligned(1024))) uint8_t lds_raw[NST * STAGE];
     rfp4_lds_u8 *lds = (rfp4_lds_u8 *)lds_raw;
 
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
@@ -91,9 +106,12 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
         rfp4_lds_u8 *st_ = lds + (BUF) * STAGE;                                                            \
         _Pragma("unroll") for (uint32_t j = 0; j < NJ; j++) __builtin_amdgcn_global_load_lds(              \
             (rfp4_glb_void *)(src[j] + (size_t)(S) * 128u), st_ + 1024u * (wave + 4u * j), 16, 0, 0);     \
-        _Pragma("unroll") for (uint32_t b = 0; b < NSB; b++) if (wave + 4u * b < R / 32u)                  \
-            __builtin_amdgcn_global_load_lds((rfp4_glb_void *)(ssrc[b] + (size_t)(S) * 8u),                \
-                                             st_ + SC0 + 256u * (wave + 4u * b), 4, 0, 0);                 \
+        _Pragma("unroll") for (uint32_t b = 0; b < NSB; b++) {                                             \
+            const uint32_t bb = (NST > 2 && wave + 4u * b >= R / 32u) ? 0u : b; /* uniform count: again block 0 */ \
+            if (NST > 2 || wave + 4u * b < R / 32u)                                                        \
+                __builtin_amdgcn_global_load_lds((rfp4_glb_void *)(ssrc[bb] + (size_t)(S) * 8u),           \
+                                                 st_ + SC0 + 256u * (wave + 4u * bb), 4, 0, 0);            \
+        }                                                                                                  \
     } while (0)
 
     v16f32 acc[FA][FB];
@@ -119,11 +137,29 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
         bsw[fb] = gemm_swz(r);
     }
 
-    if (s0 < s1) RFP4_GEMM_DMA(s0, 0u);
-    __builtin_amdgcn_s_waitcnt(0x0f70); // vmcnt(0): this wave's DMA has landed in LDS
-    __syncthreads();
+    // the first NST - 1 steps in flight, then wait for the first
+    constexpr uint32_t C = NJ + NSB; // DMA instructions per step and wave (NST > 2: uniform)
+    uint32_t issued = 0;
+#pragma unroll
+    for (uint32_t k = 0; k + 1u < (uint32_t)NST; k++)
+        if (s0 + k < s1) {
+            RFP4_GEMM_DMA(s0 + k, k);
+            issued++;
+        }
+    if (NST == 2) {
+        __builtin_amdgcn_s_waitcnt(0x0f70); // vmcnt(0): this wave's DMA has landed in LDS
+        __syncthreads();
+    } else {
+        // a bare barrier: __syncthreads' release fence would wait for every
+        // DMA in flight (vmcnt(0)); each wave has waited for its own copies
+        // of the first step, and LDS is coherent inside the CU
+        gemm_wait_steps<C>(issued > 0u ? issued - 1u : 0u);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    }
     for (uint32_t s = s0; s < s1; s++) {
-        const uint32_t cur = (s - s0) & 1u;
+        const uint32_t cur = (s - s0) % (uint32_t)NST;
         const rfp4_lds_u8 *st = lds + cur * STAGE;
         // all operands of the step into registers first, then the next step's DMA, then the MFMAs
         u32x4 av[4][FA], bv[4][FB];
@@ -144,7 +180,7 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
                 bv[t][fb] = *(const __attribute__((address_space(3))) u32x4 *)(st + boff[fb] +
                                                                                 (((4u * h + t) ^ bsw[fb]) << 4));
         }
-        if (s + 1u < s1) RFP4_GEMM_DMA(s + 1u, cur ^ 1u);
+        if (s + (uint32_t)NST - 1u < s1) RFP4_GEMM_DMA(s + (uint32_t)NST - 1u, (cur + (uint32_t)NST - 1u) % (uint32_t)NST);
 #pragma unroll
         for (uint32_t t = 0; t < 4; t++) {
 #pragma unroll
@@ -163,8 +199,20 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
         }
         // the wait for the next step's DMA goes after every MFMA of this step
         __builtin_amdgcn_sched_barrier(0);
-        __builtin_amdgcn_s_waitcnt(0x0f70); // vmcnt(0)
-        __syncthreads();
+        if (NST == 2) {
+            __builtin_amdgcn_s_waitcnt(0x0f70); // vmcnt(0)
+            __syncthreads();
+        } else {
+            if (s + 1u < s1) {
+                const uint32_t last = min(s + (uint32_t)NST - 1u, s1 - 1u); // the last step whose DMA is out
+                gemm_wait_steps<C>(last - (s + 1u));
+            }
+            // this wave's operand reads of step s returned before its MFMAs:
+            // the buffer the next DMA overwrites is free after the barrier
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+        }
     }
 #undef RFP4_GEMM_DMA
 

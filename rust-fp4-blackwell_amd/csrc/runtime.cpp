@@ -1067,12 +1067,18 @@ constexpr int kGemmNumTiles = (int)(sizeof(kGemmTiles) / sizeof(kGemmTiles[0]));
 // 16 W rows per workgroup, at most SEG (nb) K segments of 512 per wave
 constexpr int kGemmSkinny = kGemmNumTiles;
 thread_local int t_gemm_tile = -1, t_gemm_kz = 0;
+thread_local int t_gemm_stages = 0; // DMA stages of the tiled GEMM (0 / 2: double buffer; 3, 4 where compiled)
 
 struct GemmPlan {
     int tile;
     uint32_t kz;
     int ma = 0, nb = 0; // few-row plan only: activation fragments, K segments per wave
+    int nst = 2;        // tiled plans: DMA stages of the K pipeline (kernels.hip GEMM_KERNEL_P above 2)
 };
+
+// The deepest K pipeline compiled for a tile (kernels.hip GEMM_KERNEL_P): 4
+// stages for 32x128 and 64x128, 3 for 128x128, else double buffering.
+int gemm_deep_stages(int tile) { return tile == 3 || tile == 4 ? 4 : tile == 2 ? 3 : 2; }
 
 // The few-row kernel: at most 64 activation rows, K a multiple of 512 in at
 // most 8 waves of up to 4 segments (2 for 64 rows).
@@ -1117,7 +1123,7 @@ uint32_t ceil_div(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); 
 // on m and still yields a tile per CU; else the smallest such tile, with the
 // K split raised until every CU has a workgroup (bounded by the workspace).
 // Two measured exceptions below: 256x256 at 7/8 fill, and long K split in two.
-GemmPlan gemm_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t num_cus)
+static GemmPlan gemm_plan_tile(uint32_t m, uint32_t n, uint32_t k, uint32_t num_cus)
 {
     const uint32_t nsuper = k / 256u;
     if (t_gemm_tile == kGemmSkinny || (t_gemm_tile < 0 && gemm_skinny_pays(m, n, k))) {
@@ -1179,7 +1185,17 @@ GemmPlan gemm_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t num_cus)
         // long K at about one workgroup per CU: two K splits let two
         // workgroups per CU overlap their serial chains of K steps (8B down
         // at M = 512: 64x128, 56 steps, 51 -> 37 us), if the workspace holds them
-        if (nsuper >= 32u && tiles < 2ull * num_cus && 2ull * m * n <= kGemmPartFloats) return {pick, 2u};
+        if (nsuper >= 32u && tiles < 2ull * num_cus && 2ull * m * n <= kGemmPartFloats) {
+            // or the next tile up in two splits as one round with a deeper
+            // pipeline (8B down at M = 512: 128x128 in two splits, 3 stages,
+            // 35.5 us against 48-50 for 64x128 in two)
+            const GemmTile &u = kGemmTiles[2];
+            const uint64_t tu = (uint64_t)ceil_div(m, u.bm) * ceil_div(n, u.bn);
+            if (pick == 3 && (uint64_t)ceil_div(m, u.bm) * u.bm * 4u <= (uint64_t)m * 5u && 2u * tu <= num_cus &&
+                8u * 2u * tu >= 7ull * num_cus)
+                return {2, 2u};
+            return {pick, 2u};
+        }
         return {pick, 1u};
     }
     // steps per split: as few as reach one workgroup per CU; kz = ceil(nsuper / per) leaves no split empty
@@ -1187,6 +1203,24 @@ GemmPlan gemm_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t num_cus)
     uint32_t kz = ceil_div(nsuper, per);
     while (kz > 1 && (uint64_t)kz * m * n > kGemmPartFloats) kz = ceil_div(nsuper, ++per);
     return {pick, kz};
+}
+
+// The tile and K split, then the K pipeline: where the grid is one round of
+// one workgroup per CU (tiles x splits <= CUs), the deepest compiled one;
+// else double buffering (a deeper ring leaves fewer workgroups per CU).
+// Measured at M = 512 (us, 2 / 3 / 4 stages): 4096x4096 64x128 17.5 / 14.4
+// / 13.9; 1024x4096 32x128 in two splits 12.2 / - / 10.9; 6144x4096 64x128
+// (384 tiles) 19.6 / 21.4 / 24.6; 14336x4096 128x128 (448 tiles) 36.2 /
+// 39.5; 4096x14336 128x128 in two splits 45.3 / 35.5.  Same MFMA sequence at
+// any depth: bit-identical outputs.
+GemmPlan gemm_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t num_cus)
+{
+    GemmPlan p = gemm_plan_tile(m, n, k, num_cus);
+    if (p.tile == kGemmSkinny) return p;
+    const uint64_t grid = (uint64_t)ceil_div(m, kGemmTiles[p.tile].bm) * ceil_div(n, kGemmTiles[p.tile].bn) * p.kz;
+    p.nst = grid <= num_cus ? gemm_deep_stages(p.tile) : 2;
+    if (t_gemm_stages) p.nst = t_gemm_stages;
+    return p;
 }
 
 } // namespace
@@ -1237,7 +1271,13 @@ int gemm_launch(hipStream_t stream, uint32_t m, uint32_t n, uint32_t k, const ui
     if (tiles * p.kz > 0x7FFFFFFFull) return set_error(RFP4_E_SHAPE, "fp4_gemm: grid too large");
     if (p.kz > 1 && !part) return set_error(RFP4_E_INVALID, "fp4_gemm: split-K plan without a workspace");
     GemmArgs a{a_codes, a_scales, w_codes, w_scales, c, part, m, n, k, p.kz};
-    int rc = launch(t.name, dim3((unsigned)(tiles * p.kz)), dim3(256), (hipStream_t)stream, &a);
+    char pname[48];
+    const char *kname = t.name;
+    if (p.nst >= 3) { // a deeper DMA pipeline (kernels.hip GEMM_KERNEL_P)
+        snprintf(pname, sizeof pname, "%s_p%d", t.name, p.nst);
+        kname = pname;
+    }
+    int rc = launch(kname, dim3((unsigned)(tiles * p.kz)), dim3(256), (hipStream_t)stream, &a);
     if (rc || p.kz == 1) return rc;
     const uint64_t n4 = (uint64_t)m * n / 4u;
     return launch("rfp4_gemm_reduce", dim3((unsigned)std::min<uint64_t>((n4 + 255u) / 256u, 8192u)), dim3(256),
@@ -1251,6 +1291,13 @@ extern "C" {
 int rfp4_debug_attn_chunk(uint32_t chunk)
 {
     t_force_attn_chunk = chunk;
+    return RFP4_OK;
+}
+
+int rfp4_debug_gemm_stages(int nst)
+{
+    if (nst != 0 && (nst < 2 || nst > 4)) return set_error(RFP4_E_INVALID, "GEMM stages must be 0 (auto), 2, 3 or 4");
+    t_gemm_stages = nst;
     return RFP4_OK;
 }
 
