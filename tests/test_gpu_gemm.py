@@ -233,3 +233,40 @@ def test_gemm_config5_prefill512(rf, orc, stream, n, k):
     cols = np.unique(np.concatenate([np.arange(32), n - 32 + np.arange(32),
                                      rng.choice(n, min(n, 960), replace=False)]))
     _config5_case(rf, orc, stream, 512, n, k, sample_rows=rows, sample_cols=cols)
+
+
+# tiles with deeper K pipelines compiled (kernels.hip GEMM_KERNEL_P): tile index -> stages
+DEEP = {1: (3,), 2: (3,), 3: (3, 4), 4: (4,)}
+
+
+@pytest.mark.parametrize("tile", sorted(DEEP))
+@pytest.mark.parametrize("kz", [1, 3])
+def test_gemm_deep_pipelines_bit_identical(rf, orc, stream, forced_plan, tile, kz):
+    """Every deeper DMA pipeline of a tile gives the double-buffered result
+    bit for bit (same MFMA sequence), on ragged m and n, K splits included,
+    with K step counts below and above the pipeline depth (k = 512: 2 steps;
+    k = 2816: 11), and stays within the bar against the oracle."""
+    m, n = 200, 900
+    lib = rf.load()
+    for k in (512, 2816):
+        ac, asc = _uniform_mx(orc, m, k, 41 + k)
+        wc, wsc = _uniform_mx(orc, n, k, 43 + k)
+        forced_plan(tile, kz)
+        try:
+            rf.check(lib.rfp4_debug_gemm_stages(2))
+            c2 = _gemm(rf, stream, m, n, k, ac, asc, wc, wsc)
+            for nst in DEEP[tile]:
+                rf.check(lib.rfp4_debug_gemm_stages(nst))
+                cd = _gemm(rf, stream, m, n, k, ac, asc, wc, wsc)
+                np.testing.assert_array_equal(c2.view(np.uint32), cd.view(np.uint32), err_msg=f"k {k} stages {nst}")
+        finally:
+            rf.check(lib.rfp4_debug_gemm_stages(0))
+        c64, absc = orc.gemm_mx_f64(m, n, k, ac, asc, wc, wsc)
+        _assert_gemm_close(c2, c64, absc)
+
+
+def test_gemm_stage_hook_rejects_bad_values(rf):
+    lib = rf.load()
+    assert lib.rfp4_debug_gemm_stages(1) == -1
+    assert lib.rfp4_debug_gemm_stages(5) == -1
+    rf.check(lib.rfp4_debug_gemm_stages(0))
