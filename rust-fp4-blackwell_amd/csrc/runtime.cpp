@@ -443,8 +443,9 @@ static bool gemv_has_ns(bool f32scale, int epi, int R, int ns, int W = 4)
 // 7.9-8.1 vs 8.3 at R = 4), except R = 1 for residual GEMVs of at most 2048
 // rows (twice the workgroups of R = 2 where R = 2 gives one per CU; decode
 // step, three engines of each interleaved: TinyLlama 2272 -> 2304 tok/s,
-// Llama-3.2-1B 2774 -> 2777), R = 8 for very wide matrices with short K (8B
-// LM head).
+// Llama-3.2-1B 2774 -> 2777), R = 8 for wide matrices with short K (the LM
+// heads: Llama-3.2-1B at R = 2 2683-2716 against 2774-2795 tok/s, TinyLlama's
+// 32000 rows 2270-2292 at R = 2 against 2303-2307).
 // With f32 scales (their compiled set): R = 1 for SwiGLU, R = 2 for every
 // residual GEMV, the rest as E8M0.
 GemvVariant gemv_variant(uint32_t n, uint32_t k, int epi, bool f32scale)
@@ -453,7 +454,7 @@ GemvVariant gemv_variant(uint32_t n, uint32_t k, int epi, bool f32scale)
     int R;
     if (epi == RFP4_EPI_SWIGLU)
         R = f32scale || (ns_needed == 1 && gemv_has_ns(f32scale, epi, 1, ns_needed)) ? 1 : 2;
-    else if (n >= 65536u && ns_needed <= 2) R = 8;
+    else if (n >= 16384u && ns_needed <= 2) R = 8;
     else if (epi == RFP4_EPI_RESIDUAL && n <= 2048u && !f32scale) R = 1;
     else R = 2;
     // 8 waves per workgroup where compiled (one-slice SwiGLU at R = 1, store
