@@ -18,10 +18,15 @@
 // Workgroup: 4 waves in a WM x WN grid, wave tile (32 FA) x (32 FB), block
 // tile BM x BN.  Each K step (BM + BN rows of 128 code bytes and 8 scale
 // bytes) is copied global -> LDS by the DMA path (global_load_lds, no
-// staging registers), double buffered: a wave reads all its operands of step
-// s from LDS, issues the DMA of step s+1 into the other buffer, then runs the
-// step's MFMAs while the copy is in flight; one barrier per step.  Code rows
-// are 128 bytes with the 16-byte chunks XOR-swizzled by row (gemm_swz).
+// staging registers) into a ring of NST stage buffers: a wave reads all its
+// operands of step s from LDS, issues the DMA of step s + NST - 1 into the
+// buffer step s - 1 used, then runs the step's MFMAs while the copies are in
+// flight; one barrier per step.  NST = 2 (double buffering) waits for all of
+// the wave's copies (vmcnt(0)) before the barrier; deeper rings wait only for
+// step s + 1's copies (every wave issues the same number per step, so the
+// count is a constant) and use a bare s_barrier, since __syncthreads' release
+// fence would make the compiler wait for every copy in flight.  Code rows are
+// 128 bytes with the 16-byte chunks XOR-swizzled by row (gemm_swz).
 //
 // Grid: one dimension, tiles ordered m fastest, then n, then the K split z;
 // the linear id is first remapped so that each XCD (id % 8 at dispatch) gets
