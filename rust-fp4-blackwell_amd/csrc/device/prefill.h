@@ -92,22 +92,27 @@ RFP4_DEV void rmsnorm_quant_rows_body(const RowsArgs &a)
     }
 }
 
-// grid (rows): s = silu(gate) * up (llama_run/src/main.rs:244-252) of row r
-// (gate = columns [0, k), up = [k, 2k) of the stacked gate|up output), then
-// OCP MX quantisation per 32 values (8 threads per block, float4 loads, the
-// loads of RQ_U consecutive elements of a thread issued together).
+// grid (rows, parts): s = silu(gate) * up (llama_run/src/main.rs:244-252) of
+// row r (gate = columns [0, k), up = [k, 2k) of the stacked gate|up output),
+// then OCP MX quantisation per 32 values (8 threads per block, float4 loads,
+// the loads of RQ_U consecutive elements of a thread issued together).  Part
+// p of the row takes the float4 range [p * per, (p + 1) * per), per a whole
+// number of 32-value blocks: several workgroups per row keep more waves in
+// flight for the exponentials and divisions.
 RFP4_DEV void swiglu_quant_rows_body(const RowsArgs &a)
 {
     constexpr int U = RQ_U;
     const uint32_t r = blockIdx.x, k4 = a.k / 4u, T = blockDim.x;
+    const uint32_t per = (k4 / 8u + gridDim.y - 1u) / gridDim.y * 8u;
+    const uint32_t lo = blockIdx.y * per, hi = min(k4, lo + per);
     const float4 *g = (const float4 *)(a.x + (size_t)r * 2u * a.k), *u = g + k4;
     uint8_t *codes = a.codes + (size_t)r * a.k / 2u, *scales = a.scales + (size_t)r * (a.k / 32u);
-    for (uint32_t i0 = threadIdx.x; i0 < k4; i0 += U * T) { // k % 32 == 0: whole 8-thread groups
+    for (uint32_t i0 = lo + threadIdx.x; i0 < hi; i0 += U * T) { // k % 32 == 0: whole 8-thread groups
         float4 gv[U], uv[U];
 #pragma unroll
         for (int j = 0; j < U; j++) {
             const uint32_t i = i0 + (uint32_t)j * T;
-            if (i < k4) {
+            if (i < hi) {
                 gv[j] = g[i];
                 uv[j] = u[i];
             }
@@ -115,7 +120,7 @@ RFP4_DEV void swiglu_quant_rows_body(const RowsArgs &a)
 #pragma unroll
         for (int j = 0; j < U; j++) {
             const uint32_t i = i0 + (uint32_t)j * T;
-            if (i >= k4) break;
+            if (i >= hi) break;
             const float4 y = make_float4(__fmul_rn(silu_ref(gv[j].x), uv[j].x), __fmul_rn(silu_ref(gv[j].y), uv[j].y),
                                          __fmul_rn(silu_ref(gv[j].z), uv[j].z), __fmul_rn(silu_ref(gv[j].w), uv[j].w));
             quant_block32_x8(y, codes + (i / 8u) * 16u, scales + i / 8u);
