@@ -38,7 +38,53 @@ RFP4_DEV void rmsnorm_quant_rows_body(const RowsArgs &a)
     const float4 *x = (const float4 *)(a.x + (size_t)r * a.k);
     const float4 *add = a.add ? (const float4 *)(a.add + (size_t)r * a.k) : nullptr;
     float4 *xo = (float4 *)(a.x_out + (size_t)r * a.k);
+    const uint2 *w = (const uint2 *)a.w;
+    uint8_t *codes = a.codes + (size_t)r * a.k / 2u, *scales = a.scales + (size_t)r * (a.k / 32u);
     float ss = 0.0f;
+    if (k4 <= (uint32_t)U * T) {
+        // the whole row in registers (one pass of U elements per thread): x,
+        // the added row and the norm weights loaded together, the sum, then
+        // the scaled values quantised without reloading anything; the same
+        // operations in the same order as the two-pass loop below
+        float4 v[U], d[U];
+        uint2 wb[U];
+#pragma unroll
+        for (int j = 0; j < U; j++) {
+            const uint32_t i = threadIdx.x + (uint32_t)j * T;
+            if (i < k4) {
+                v[j] = x[i];
+                if (add) d[j] = add[i];
+                wb[j] = w[i];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < U; j++) {
+            const uint32_t i = threadIdx.x + (uint32_t)j * T;
+            if (i >= k4) break;
+            if (add) {
+                v[j] = make_float4(__fadd_rn(v[j].x, d[j].x), __fadd_rn(v[j].y, d[j].y), __fadd_rn(v[j].z, d[j].z),
+                                   __fadd_rn(v[j].w, d[j].w));
+                xo[i] = v[j];
+            }
+            ss = __fadd_rn(ss, __fmul_rn(v[j].x, v[j].x));
+            ss = __fadd_rn(ss, __fmul_rn(v[j].y, v[j].y));
+            ss = __fadd_rn(ss, __fmul_rn(v[j].z, v[j].z));
+            ss = __fadd_rn(ss, __fmul_rn(v[j].w, v[j].w));
+        }
+        const float total = block_sum(ss, red);
+        const float rms = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(total, (float)a.k), a.eps)));
+#pragma unroll
+        for (int j = 0; j < U; j++) {
+            const uint32_t i = threadIdx.x + (uint32_t)j * T;
+            if (i >= k4) break;
+            const float4 y = make_float4(__fmul_rn(__fmul_rn(v[j].x, rms), f16_bits_to_f32((uint16_t)(wb[j].x & 0xFFFFu))),
+                                         __fmul_rn(__fmul_rn(v[j].y, rms), f16_bits_to_f32((uint16_t)(wb[j].x >> 16))),
+                                         __fmul_rn(__fmul_rn(v[j].z, rms), f16_bits_to_f32((uint16_t)(wb[j].y & 0xFFFFu))),
+                                         __fmul_rn(__fmul_rn(v[j].w, rms), f16_bits_to_f32((uint16_t)(wb[j].y >> 16))));
+            quant_block32_x8(y, codes + (i / 8u) * 16u, scales + i / 8u);
+        }
+        return;
+    }
     for (uint32_t i0 = threadIdx.x; i0 < k4; i0 += U * T) {
         float4 v[U], d[U];
 #pragma unroll
@@ -66,8 +112,6 @@ RFP4_DEV void rmsnorm_quant_rows_body(const RowsArgs &a)
     }
     const float total = block_sum(ss, red);
     const float rms = __fdiv_rn(1.0f, __fsqrt_rn(__fadd_rn(__fdiv_rn(total, (float)a.k), a.eps)));
-    const uint2 *w = (const uint2 *)a.w;
-    uint8_t *codes = a.codes + (size_t)r * a.k / 2u, *scales = a.scales + (size_t)r * (a.k / 32u);
     for (uint32_t i0 = threadIdx.x; i0 < k4; i0 += U * T) { // k % 32 == 0: whole 8-thread groups
         float4 v[U];
         uint2 wb[U];
