@@ -120,7 +120,8 @@ def test_gemm_plan_shapes(m, n, k):
     (512, 28672, 4096, (256, 256, 1)),   # one round of 256x256 at 7/8 of the CUs (50 vs 66 us)
     (512, 4096, 14336, (128, 128, 2)),   # long K: one round of 128x128 in two splits, 3 stages (35.5 vs 48-50 us)
     (512, 14336, 4096, (256, 128, 1)),   # one round of 256x128, 3 stages (31.6 vs 37.8 us for 128x128)
-    (512, 6144, 4096, (64, 128, 1)),
+    (512, 6144, 4096, (128, 128, 1)),   # one round of 128x128 over 3/4 of the CUs, 3 stages (18.3 vs 19.2 us)
+    (128, 28672, 4096, (128, 128, 1)),  # the same rule (23.2 vs 29.8 us)
     (2048, 6144, 4096, (256, 256, 1)),   # fewest resident rounds (49.6 vs 60.0 us)
     (2048, 4096, 4096, (128, 128, 1)),   # (29.6 vs 33.2 us)
     (2048, 4096, 14336, (128, 128, 1)),  # (82.2 vs 90.2 us)
