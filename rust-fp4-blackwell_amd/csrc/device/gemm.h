@@ -35,6 +35,7 @@
 // kernel launched next sums the kz planes in z order, so the result does not
 // depend on the order the workgroups ran in.
 #pragma once
+#include <type_traits>
 #include "common.h"
 #include "mma.h"
 
@@ -163,7 +164,9 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
         __builtin_amdgcn_s_barrier();
         asm volatile("" ::: "memory");
     }
-    for (uint32_t s = s0; s < s1; s++) {
+    // one K step; FULL: a step with NST - 1 steps of DMA still to issue
+    auto step = [&](uint32_t s, auto full_c) {
+        constexpr bool FULL = decltype(full_c)::value;
         const uint32_t cur = (s - s0) % (uint32_t)NST;
         const rfp4_lds_u8 *st = lds + cur * STAGE;
         // all operands of the step into registers first, then the next step's DMA, then the MFMAs
@@ -185,7 +188,7 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
                 bv[t][fb] = *(const __attribute__((address_space(3))) u32x4 *)(st + boff[fb] +
                                                                                 (((4u * h + t) ^ bsw[fb]) << 4));
         }
-        if (s + (uint32_t)NST - 1u < s1) RFP4_GEMM_DMA(s + (uint32_t)NST - 1u, (cur + (uint32_t)NST - 1u) % (uint32_t)NST);
+        if (FULL || s + (uint32_t)NST - 1u < s1) RFP4_GEMM_DMA(s + (uint32_t)NST - 1u, (cur + (uint32_t)NST - 1u) % (uint32_t)NST);
 #pragma unroll
         for (uint32_t t = 0; t < 4; t++) {
 #pragma unroll
@@ -208,7 +211,9 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
             __builtin_amdgcn_s_waitcnt(0x0f70); // vmcnt(0)
             __syncthreads();
         } else {
-            if (s + 1u < s1) {
+            if (FULL) {
+                gemm_wait_steps<C>((uint32_t)NST - 2u);
+            } else if (s + 1u < s1) {
                 const uint32_t last = min(s + (uint32_t)NST - 1u, s1 - 1u); // the last step whose DMA is out
                 gemm_wait_steps<C>(last - (s + 1u));
             }
@@ -218,7 +223,15 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
             __builtin_amdgcn_s_barrier();
             asm volatile("" ::: "memory");
         }
-    }
+    };
+    // Deeper rings run the steps with a full lookahead in a loop of their
+    // own: its wait count is a constant, so the step is one basic block and
+    // the MFMAs stay ahead of the wait (with the wait's branches in the
+    // loop the compiler sank them below it, serialising MFMA and copies).
+    uint32_t s = s0;
+    if constexpr (NST > 2)
+        for (; s + (uint32_t)NST - 1u < s1; s++) step(s, std::integral_constant<bool, true>());
+    for (; s < s1; s++) step(s, std::integral_constant<bool, false>());
 #undef RFP4_GEMM_DMA
 
     // ---- epilogue: accumulator r of lane l is C[8 (r/4) + 4 (l/32) + r%4][l%32] of its fragment
