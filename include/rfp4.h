@@ -205,6 +205,11 @@ int rfp4_debug_gemm_plan(int tile, int kz);
  * where a kernel is compiled for the tile; others fail at launch).  No
  * reference counterpart. */
 int rfp4_debug_gemm_stages(int nst);
+/* Test hook (this thread): 1 = every split-K sum of later fp4_gemm calls in
+ * the reduce kernel launched after the GEMM; 0 = two-way splits summed inside
+ * the GEMM launch by the last split of each tile (the default; the same
+ * sums).  No reference counterpart. */
+int rfp4_debug_gemm_reduce_kernel(int on);
 /* Test hook: tokens per split of later attn_decode / attn_decode_f16 calls
  * on this thread (0 = automatic).  No reference counterpart. */
 int rfp4_debug_attn_chunk(uint32_t chunk);

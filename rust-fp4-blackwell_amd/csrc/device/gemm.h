@@ -61,6 +61,77 @@ RFP4_DEV void gemm_wait_steps(uint32_t n)
 #undef RFP4_VMCNT
 }
 
+// Two-way split-K sum inside the launch (kz = 2): each split stores its
+// partial tile to part[z] with agent-scope stores, waits for them, and bumps
+// the tile's arrival counter; the split whose increment completes the count
+// reads the other plane with agent-scope loads and writes c = part[0] +
+// part[1] (its own plane from registers), the reduce kernel's sums bit for
+// bit, then resets the counter for the next launch.  No split waits for
+// another.  Publication without a fence: on gfx950 a relaxed agent-scope
+// store is a write-through global_store ... sc1, s_waitcnt vmcnt(0) returns
+// once it is acknowledged at the device-coherent level, and a relaxed
+// agent-scope load (global_load ... sc1) reads that level; the attention
+// merge (device/attn.h) relies on the same three facts.
+#if defined(__HIP_DEVICE_COMPILE__) && !defined(__gfx950__)
+#error "the in-launch split-K sum's publication protocol is written for gfx950's sc1 accesses"
+#endif
+template <int FA, int FB>
+RFP4_DEV void gemm_splitk_last(const GemmArgs &g, const v16f32 (&acc)[FA][FB], uint32_t m0, uint32_t n0, uint32_t r32,
+                               uint32_t h, uint32_t z, uint32_t tile)
+{
+    __shared__ uint32_t s_last;
+    const size_t plane = (size_t)g.m * g.n;
+    float *mine = g.part + (size_t)z * plane;
+#pragma unroll
+    for (int fa = 0; fa < FA; fa++)
+#pragma unroll
+        for (int fb = 0; fb < FB; fb++) {
+            const uint32_t col = n0 + 32u * fb + r32;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const uint32_t row = m0 + 32u * fa + 8u * (uint32_t)(r / 4) + 4u * h + (uint32_t)(r % 4);
+                if (row < g.m && col < g.n)
+                    __hip_atomic_store(mine + (size_t)row * g.n + col, acc[fa][fb][r], __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); // this thread's partial is acknowledged
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t old = __hip_atomic_fetch_add(g.counters + tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        s_last = old + 1u == g.kz ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    if (threadIdx.x == 0) __hip_atomic_store(g.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // every load of the other plane first (one round trip), then the sums
+    const float *other = g.part + (size_t)(1u - z) * plane;
+    float o[FA][FB][16];
+#pragma unroll
+    for (int fa = 0; fa < FA; fa++)
+#pragma unroll
+        for (int fb = 0; fb < FB; fb++) {
+            const uint32_t col = min(n0 + 32u * fb + r32, g.n - 1u);
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const uint32_t row = min(m0 + 32u * fa + 8u * (uint32_t)(r / 4) + 4u * h + (uint32_t)(r % 4), g.m - 1u);
+                o[fa][fb][r] = __hip_atomic_load(other + (size_t)row * g.n + col, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+#pragma unroll
+    for (int fa = 0; fa < FA; fa++)
+#pragma unroll
+        for (int fb = 0; fb < FB; fb++) {
+            const uint32_t col = n0 + 32u * fb + r32;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const uint32_t row = m0 + 32u * fa + 8u * (uint32_t)(r / 4) + 4u * h + (uint32_t)(r % 4);
+                const float v = z == 0u ? __fadd_rn(acc[fa][fb][r], o[fa][fb][r]) : __fadd_rn(o[fa][fb][r], acc[fa][fb][r]);
+                if (row < g.m && col < g.n) g.c[(size_t)row * g.n + col] = v;
+            }
+        }
+}
+
 template <int WM, int WN, int FA, int FB, int NST = 2>
 RFP4_DEV void gemm_body(const GemmArgs &g)
 {
@@ -235,8 +306,16 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
 #undef RFP4_GEMM_DMA
 
     // ---- epilogue: accumulator r of lane l is C[8 (r/4) + 4 (l/32) + r%4][l%32] of its fragment
-    float *dst = g.kz > 1u ? g.part + (size_t)z * g.m * g.n : g.c;
     const uint32_t m0 = mt * BM + wm * (32u * FA), n0 = nt * BN + wn * (32u * FB);
+    // (up to 256x128: the other plane's values fit the registers beside the
+    // accumulators; the host passes no counters for larger tiles)
+    if constexpr (FA * FB <= 8) {
+        if (g.kz == 2u && g.counters) {
+            gemm_splitk_last<FA, FB>(g, acc, m0, n0, r32, h, z, mt + mt_n * nt);
+            return;
+        }
+    }
+    float *dst = g.kz > 1u ? g.part + (size_t)z * g.m * g.n : g.c;
 #pragma unroll
     for (int fa = 0; fa < FA; fa++)
 #pragma unroll

@@ -53,7 +53,7 @@ struct llama_engine {
     uint32_t sb = 1, kvb = 2;  // bytes per scale (E8M0 1, f32 4) and per KV element (fp16 2, f32 4)
     const char *sname = "e8m0"; // kernel-name token of the scale format
     GemvVariant gv[GV_N]{};     // GEMV variants, fixed at creation (the LM head's sizes `best`)
-    float *gemm_part = nullptr; // split-K partials of the prefill GEMMs (kGemmPartFloats)
+    float *gemm_part = nullptr; // split-K workspace of the prefill GEMMs (kGemmWorkspaceWords, counters zeroed)
     std::vector<float> harness_x; // llama_decode's activation vector (f32-scale synthetic init)
     bool no_embed = false;        // harness steps: x carries over, no embedding lookup
     uint32_t max_seq_alloc = 0;
@@ -382,7 +382,11 @@ static int prefill_reserve(llama_engine *e, uint32_t n)
     e->pf_cap = 0;
     const size_t kmax = std::max(std::max(c.dim, qd), c.ffn);
     const size_t ncols = std::max(std::max(qd + 2 * kvd, 2 * c.ffn), c.dim);
-    int rc = e->gemm_part ? RFP4_OK : dalloc_t(e, &e->gemm_part, kGemmPartFloats);
+    int rc = RFP4_OK;
+    if (!e->gemm_part) {
+        rc = dalloc_t(e, &e->gemm_part, kGemmWorkspaceWords);
+        if (!rc) rc = fill_words((uint32_t *)(e->gemm_part + kGemmPartFloats), kGemmCounters, 0u, e->stream);
+    }
     if (!rc) rc = dalloc_t(e, &e->pf_x, (size_t)cap * c.dim);
     if (!rc) rc = dalloc_t(e, &e->pf_c, (size_t)cap * ncols);
     if (!rc) rc = dalloc_t(e, &e->pf_a, (size_t)cap * qd);

@@ -282,7 +282,9 @@ int rfp4_init(int device)
     rt->attn_part_floats = (size_t)kAttnMaxHeads * kAttnMaxSplits * (128 + 4); // [m, l, -, -, acc[hd]]
     rc = hip_check(hipMalloc((void **)&rt->attn_part, rt->attn_part_floats * sizeof(float)), "hipMalloc(attn workspace)");
     // split-K workspace of fp4_gemm
-    if (!rc) rc = hip_check(hipMalloc((void **)&rt->gemm_part, kGemmPartFloats * sizeof(float)), "hipMalloc(gemm workspace)");
+    if (!rc) rc = hip_check(hipMalloc((void **)&rt->gemm_part, kGemmWorkspaceWords * sizeof(float)), "hipMalloc(gemm workspace)");
+    if (!rc)
+        rc = hip_check(hipMemset(rt->gemm_part + kGemmPartFloats, 0, kGemmCounters * sizeof(uint32_t)), "hipMemset(gemm counters)");
     // arrival counters of the in-kernel attention merge: zero between calls
     if (!rc) rc = hip_check(hipMalloc((void **)&rt->attn_counters, kAttnMaxHeads * sizeof(uint32_t)), "hipMalloc(attn counters)");
     if (!rc) rc = hip_check(hipMemset(rt->attn_counters, 0, kAttnMaxHeads * sizeof(uint32_t)), "hipMemset(attn counters)");
@@ -1068,6 +1070,7 @@ constexpr int kGemmNumTiles = (int)(sizeof(kGemmTiles) / sizeof(kGemmTiles[0]));
 // 16 W rows per workgroup, at most SEG (nb) K segments of 512 per wave
 constexpr int kGemmSkinny = kGemmNumTiles;
 thread_local int t_gemm_tile = -1, t_gemm_kz = 0;
+thread_local int t_gemm_reduce_kernel = 0; // 1: split-K sums always in the reduce kernel
 thread_local int t_gemm_stages = 0; // DMA stages of the tiled GEMM (0 / 2: double buffer; 3, 4 where compiled)
 
 struct GemmPlan {
@@ -1287,7 +1290,12 @@ int gemm_launch(hipStream_t stream, uint32_t m, uint32_t n, uint32_t k, const ui
         return set_error(RFP4_E_CAPACITY, "fp4_gemm: split-K partials %u x %u x %u exceed the workspace", p.kz, m, n);
     if (tiles * p.kz > 0x7FFFFFFFull) return set_error(RFP4_E_SHAPE, "fp4_gemm: grid too large");
     if (p.kz > 1 && !part) return set_error(RFP4_E_INVALID, "fp4_gemm: split-K plan without a workspace");
-    GemmArgs a{a_codes, a_scales, w_codes, w_scales, c, part, m, n, k, p.kz};
+    // two-way splits sum in the launch (the last split of a tile to arrive),
+    // others in the reduce kernel launched next (also tiles above 256x128,
+    // whose kernels have no registers for the other plane)
+    uint32_t *counters = p.kz == 2u && t.bm * t.bn <= 256u * 128u && tiles <= kGemmCounters && !t_gemm_reduce_kernel
+                             ? (uint32_t *)(part + kGemmPartFloats) : nullptr;
+    GemmArgs a{a_codes, a_scales, w_codes, w_scales, c, part, m, n, k, p.kz, counters};
     char pname[48];
     const char *kname = t.name;
     if (p.nst >= 3) { // a deeper DMA pipeline (kernels.hip GEMM_KERNEL_P)
@@ -1295,7 +1303,7 @@ int gemm_launch(hipStream_t stream, uint32_t m, uint32_t n, uint32_t k, const ui
         kname = pname;
     }
     int rc = launch(kname, dim3((unsigned)(tiles * p.kz)), dim3(256), (hipStream_t)stream, &a);
-    if (rc || p.kz == 1) return rc;
+    if (rc || p.kz == 1 || counters) return rc;
     const uint64_t n4 = (uint64_t)m * n / 4u;
     return launch("rfp4_gemm_reduce", dim3((unsigned)std::min<uint64_t>((n4 + 255u) / 256u, 8192u)), dim3(256),
                   (hipStream_t)stream, &a);
@@ -1308,6 +1316,13 @@ extern "C" {
 int rfp4_debug_attn_chunk(uint32_t chunk)
 {
     t_force_attn_chunk = chunk;
+    return RFP4_OK;
+}
+
+int rfp4_debug_gemm_reduce_kernel(int on)
+{
+    if (on != 0 && on != 1) return set_error(RFP4_E_INVALID, "GEMM reduce mode must be 0 (auto) or 1 (reduce kernel)");
+    t_gemm_reduce_kernel = on;
     return RFP4_OK;
 }
 

@@ -15,6 +15,11 @@ constexpr uint32_t kAttnMaxHeads = 128;
 constexpr uint32_t kAttnMaxSplits = 512;
 
 constexpr size_t kGemmPartFloats = (size_t)8 << 20; // 32 MiB
+// A split-K workspace is kGemmPartFloats floats of partial planes followed by
+// kGemmCounters arrival counters (zero between launches) for the two-way
+// splits that sum inside the launch.
+constexpr uint32_t kGemmCounters = 16384;
+constexpr size_t kGemmWorkspaceWords = kGemmPartFloats + kGemmCounters;
 
 struct Runtime {
     int device = 0;
@@ -23,7 +28,7 @@ struct Runtime {
     std::unordered_map<std::string, hipFunction_t> fns;
     float *attn_part = nullptr;       // default split-K workspace of attn_decode
     size_t attn_part_floats = 0;
-    float *gemm_part = nullptr;       // split-K partials of fp4_gemm (kGemmPartFloats)
+    float *gemm_part = nullptr;       // split-K workspace of fp4_gemm (kGemmWorkspaceWords)
     uint32_t *attn_counters = nullptr; // in-kernel attention merge (kAttnMaxHeads words, zero between calls)
     size_t max_lds = 65536;           // LDS bytes per workgroup
 };
@@ -78,7 +83,8 @@ int attn_decode_ws(hipStream_t s, uint32_t nh, uint32_t nkv, uint32_t hd, uint32
 // Looks up, once per device and with that device current, the address of
 // the allocation-free entry points' static scratch (csrc/noalloc.hip).
 int noalloc_setup(int device);
-// fp4_gemm with the caller's split-K workspace (kGemmPartFloats floats; the
+// fp4_gemm with the caller's split-K workspace (kGemmWorkspaceWords words, the
+// counters zeroed; the
 // engine owns one, so engines on different streams do not share partials).
 int gemm_launch(hipStream_t stream, uint32_t m, uint32_t n, uint32_t k, const uint8_t *a_codes, const uint8_t *a_scales,
                 const uint8_t *w_codes, const uint8_t *w_scales, float *c, float *part);

@@ -236,6 +236,10 @@ typedef struct GemmArgs {
     float *c;                            // [m][n]
     float *part;                         // [kz][m][n] split-K partials (kz > 1)
     uint32_t m, n, k, kz;
+    // kz > 1: arrival counter per output tile (zero between launches); the
+    // last split of a tile to arrive sums the planes.  Null: the reduce
+    // kernel launched next sums them.
+    uint32_t *counters;
 } GemmArgs;
 
 // Persistent decode of every layer of one step (device/persist.h): one

@@ -265,6 +265,46 @@ def test_gemm_deep_pipelines_bit_identical(rf, orc, stream, forced_plan, tile, k
         _assert_gemm_close(c2, c64, absc)
 
 
+@pytest.mark.parametrize("tile", range(len(TILES)))
+def test_gemm_two_way_split_summed_in_launch(rf, orc, stream, forced_plan, tile):
+    """Two-way K splits summed inside the launch (the last split of each tile
+    adds the other's plane) give the reduce kernel's result bit for bit, on
+    ragged m and n, with one and with several K steps per split, over
+    repeated calls with a smaller shape in between (a counter left non-zero
+    or a stale plane would change a result), and within the bar against the
+    oracle."""
+    lib = rf.load()
+    cases = [(200, 900, 512), (200, 900, 2816), (33, 132, 1024)]
+    data = {}
+    for m, n, k in cases:
+        ac, asc = _uniform_mx(orc, m, k, 81 + k + m)
+        wc, wsc = _uniform_mx(orc, n, k, 83 + k + n)
+        data[(m, n, k)] = (ac, asc, wc, wsc)
+    forced_plan(tile, 2)
+    try:
+        ref = {}
+        rf.check(lib.rfp4_debug_gemm_reduce_kernel(1))
+        for key, d in data.items():
+            ref[key] = _gemm(rf, stream, *key, *d)
+        rf.check(lib.rfp4_debug_gemm_reduce_kernel(0))
+        for rep in range(4):
+            for key, d in data.items():
+                got = _gemm(rf, stream, *key, *d)
+                np.testing.assert_array_equal(ref[key].view(np.uint32), got.view(np.uint32), err_msg=f"{key} rep {rep}")
+    finally:
+        rf.check(lib.rfp4_debug_gemm_reduce_kernel(0))
+    for key, (ac, asc, wc, wsc) in data.items():
+        c64, absc = orc.gemm_mx_f64(*key, ac, asc, wc, wsc)
+        _assert_gemm_close(ref[key], c64, absc)
+
+
+def test_gemm_reduce_hook_rejects_bad_values(rf):
+    lib = rf.load()
+    assert lib.rfp4_debug_gemm_reduce_kernel(2) == -1
+    assert lib.rfp4_debug_gemm_reduce_kernel(-1) == -1
+    rf.check(lib.rfp4_debug_gemm_reduce_kernel(0))
+
+
 def test_gemm_stage_hook_rejects_bad_values(rf):
     lib = rf.load()
     assert lib.rfp4_debug_gemm_stages(1) == -1
