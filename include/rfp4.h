@@ -271,8 +271,9 @@ int rfp4_mma_tile32(rfp4_stream_t stream, const uint32_t *a, const uint32_t *b, 
  * 0, -1 = automatic).  No reference counterpart. */
 int rfp4_debug_gemv_variant(int rows_per_wave, int slices);
 /* Test hook: waves per workgroup of later VALU GEMV launches on this thread
- * (0 = automatic, 4 or 8; 8 exists for one-slice SwiGLU at 1 row per wave and
- * store at 2).  No reference counterpart. */
+ * (0 = automatic, 4 or 8; 8 exists for one-slice SwiGLU at 1 row per wave,
+ * store at 2, and the residual epilogue at 1 row per wave with one or three
+ * slices).  No reference counterpart. */
 int rfp4_debug_gemv_waves(int waves);
 /* Test hook: one GEMV launch with any epilogue (0 store, 1 residual,
  * 2 SwiGLU with gate rows [0, n) and up rows [pair_off, pair_off + n),

@@ -67,9 +67,11 @@ GEMV_NS_SHORT(f32, 1, resid, RFP4_EPI_RESIDUAL, 8)
 GEMV_NS_FULL(f32, 1, argmax, RFP4_EPI_ARGMAX, 2)
 GEMV_NS_SHORT(f32, 1, argmax, RFP4_EPI_ARGMAX, 8)
 GEMV_NS_FULL(f32, 1, swiglu, RFP4_EPI_SWIGLU, 1)
-// 8 waves per workgroup for one-slice shapes (K <= 2048), the default there
-// (runtime.cpp gemv_variant): TinyLlama decode 1811 -> 1836 tok/s; at K = 4096
-// and 14336 slower.  rfp4_gemv_<scale>_<epilogue>_r<R>_s<NS>_w<W>
+// 8 waves per workgroup for one-slice shapes (K <= 2048) and the 1-row
+// residual GEMVs of one and three slices, the default there (runtime.cpp
+// gemv_variant): TinyLlama decode 1811 -> 1836 tok/s, then 2307 -> 2338 with
+// the residual ones; at K = 4096 and 14336 slower (8B down at 1 row per wave
+// on 8 waves: 686 -> 661 tok/s).  rfp4_gemv_<scale>_<epilogue>_r<R>_s<NS>_w<W>
 #define GEMV_KERNEL_W(SNAME, SF32, ENAME, EPI, R, NS, W)                                                         \
     extern "C" __global__ __launch_bounds__(64 * W) void rfp4_gemv_##SNAME##_##ENAME##_r##R##_s##NS##_w##W(GemvArgs a) \
     {                                                                                                           \
@@ -79,6 +81,8 @@ GEMV_KERNEL_W(e8m0, 0, swiglu, RFP4_EPI_SWIGLU, 1, 1, 8)
 GEMV_KERNEL_W(e8m0, 0, store, RFP4_EPI_STORE, 2, 1, 8)
 GEMV_KERNEL_W(f32, 1, swiglu, RFP4_EPI_SWIGLU, 1, 1, 8)
 GEMV_KERNEL_W(f32, 1, store, RFP4_EPI_STORE, 2, 1, 8)
+GEMV_KERNEL_W(e8m0, 0, resid, RFP4_EPI_RESIDUAL, 1, 1, 8)
+GEMV_KERNEL_W(e8m0, 0, resid, RFP4_EPI_RESIDUAL, 1, 3, 8)
 
 // ---- norm / rope / embed
 K1024 void rfp4_rmsnorm_f32w(RmsnormArgs a) { rmsnorm_body<0>(a); }

@@ -419,8 +419,9 @@ static thread_local int t_force_r = 0, t_force_ns = -1, t_force_w = 0;
 // scales have every variant the tests force; f32 scales the planner's own.
 static bool gemv_has_ns(bool f32scale, int epi, int R, int ns, int W = 4)
 {
-    if (W != 4) // 8-wave workgroups: one-slice SwiGLU at R = 1, store at R = 2
-        return W == 8 && ns == 1 && ((epi == RFP4_EPI_SWIGLU && R == 1) || (epi == RFP4_EPI_STORE && R == 2));
+    if (W != 4) // 8-wave workgroups: one-slice SwiGLU at R = 1, store at R = 2, residual at R = 1 of 1 or 3 slices
+        return (W == 8 && ns == 1 && ((epi == RFP4_EPI_SWIGLU && R == 1) || (epi == RFP4_EPI_STORE && R == 2))) ||
+               (W == 8 && !f32scale && epi == RFP4_EPI_RESIDUAL && R == 1 && (ns == 1 || ns == 3));
     const bool full = ns == 0 || ns == 1 || ns == 2 || ns == 3 || ns == 4 || ns == 7;
     const bool shrt = ns == 0 || ns == 1 || ns == 2;
     if (f32scale) {
@@ -460,8 +461,9 @@ GemvVariant gemv_variant(uint32_t n, uint32_t k, int epi, bool f32scale)
     else if (epi == RFP4_EPI_RESIDUAL && n <= 2048u && !f32scale) R = 1;
     else R = 2;
     // 8 waves per workgroup where compiled (one-slice SwiGLU at R = 1, store
-    // at R = 2: K <= 2048), else 4.  Measured in the TinyLlama decode step:
-    // 1811 -> 1836 tok/s (gate|up, q|k|v and the LM head on 8 waves).
+    // at R = 2: K <= 2048; residual at R = 1 of one or three slices), else 4.
+    // Measured in the TinyLlama decode step: 1811 -> 1836 tok/s (gate|up,
+    // q|k|v and the LM head on 8 waves), 2307 -> 2338 (o and down on 8 waves).
     int W = 4;
     if (t_force_r) R = t_force_r;
     if (t_force_w) W = t_force_w;

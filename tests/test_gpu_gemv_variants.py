@@ -99,11 +99,13 @@ def test_gemv_fused_rmsnorm(rf, orc, stream, n, k):
     assert (reference_rel_err(got, f64) > 1e-2).sum() == 0
 
 
-@pytest.mark.parametrize("epi,r", [("swiglu", 1), ("store", 2)])
-@pytest.mark.parametrize("n,k", [(67, 512), (300, 2048), (5632, 2048)])
-def test_gemv_eight_wave_variants(rf, orc, stream, epi, r, n, k):
-    """8 waves per workgroup (one K slice), forced; and the automatic choice
-    on the same shape."""
+@pytest.mark.parametrize("epi,r,ns", [("swiglu", 1, 1), ("store", 2, 1), ("resid", 1, 1), ("resid", 1, 3)])
+@pytest.mark.parametrize("n,k", [(67, 512), (300, 2048), (5632, 2048), (2048, 5632)])
+def test_gemv_eight_wave_variants(rf, orc, stream, epi, r, ns, n, k):
+    """8 waves per workgroup (one K slice; three for the residual at 1 row
+    per wave), forced; and the automatic choice on the same shape."""
+    if (k + 2047) // 2048 > ns:
+        pytest.skip("k needs more slices than the variant issues")
     codes, scales, x = _config1(orc, 2 * n, k, seed=n + k + r)
     dc, ds, dx = _dev(rf, codes, stream), _dev(rf, scales, stream), _dev(rf, x, stream)
     full = orc.gemv_e8m0(2 * n, k, codes, scales, x)
@@ -112,7 +114,7 @@ def test_gemv_eight_wave_variants(rf, orc, stream, epi, r, n, k):
     try:
         for forced in (True, False):
             if forced:
-                _force(rf, r, 1)
+                _force(rf, r, ns)
                 rf.check(rf.load().rfp4_debug_gemv_waves(8))
             got, best = _run_epi(rf, stream, epi, n, k, dc, ds, dx, base)
             _check_epi(orc, epi, got, best, n, full, f64, absf, base, f"{epi} R={r} W=8 k={k} forced={forced}")
