@@ -169,15 +169,22 @@ static bool qkva_plan(const llama_engine *e, uint32_t nsplit, bool tagged, QkvaP
     const uint32_t hs = e->attn_head_split ? e->attn_head_split
                                            : attn_head_split_for(c.n_heads, c.n_kv_heads, nsplit, (uint32_t)rt->num_cus);
     if (hs == 0 || G % hs) return false;
-    snprintf(pl->name, sizeof pl->name, "rfp4_qkva_hd%u_g%u%s", c.head_dim, attn_group_pad(G / hs), tagged ? "_t" : "");
-    const uint32_t rows = qdim(c) + 2u * kvdim(c), per_tile = 4u * e->qkva_R;
+    const uint32_t rows = qdim(c) + 2u * kvdim(c);
     pl->hs = hs;
-    pl->n_tiles = (rows + per_tile - 1u) / per_tile;
     pl->n_attn = c.n_kv_heads * hs * nsplit;
-    pl->grid = std::max(pl->n_tiles, pl->n_attn);
-    int per_cu = 0;
-    if (kernel_occupancy(pl->name, 256, gemv_lds_bytes(c.dim), &per_cu) || per_cu < 1) return false;
-    return (uint64_t)per_cu * (uint64_t)rt->num_cus >= pl->grid;
+    // 1 row per wave first where compiled (HD 64), then the engine's rows per
+    // wave: the first whose whole grid fits the device at once
+    for (uint32_t R : {1u, e->qkva_R}) {
+        if (R == 1u && c.head_dim != 64) continue;
+        snprintf(pl->name, sizeof pl->name, "rfp4_qkva_hd%u_g%u%s%s", c.head_dim, attn_group_pad(G / hs), tagged ? "_t" : "",
+                 R == 1u && e->qkva_R != 1u ? "_r1" : "");
+        pl->n_tiles = (rows + 4u * R - 1u) / (4u * R);
+        pl->grid = std::max(pl->n_tiles, pl->n_attn);
+        int per_cu = 0;
+        if (kernel_occupancy(pl->name, 256, gemv_lds_bytes(c.dim), &per_cu) || per_cu < 1) continue;
+        if ((uint64_t)per_cu * (uint64_t)rt->num_cus >= pl->grid) return true;
+    }
+    return false;
 }
 
 // The decode step at a position whose context needs `nsplit` attention

@@ -117,20 +117,24 @@ ATTN_KERNELS(128, f16, uint16_t)
 ATTN_PREFILL_KERNELS(64)
 ATTN_PREFILL_KERNELS(128)
 // ---- fused q|k|v GEMV + attention: rfp4_qkva_hd<HD>_g<group>[_t: tagged merge]
-// (device/qkva.h).  HD 64 with K = 2048 (one slice, R = 2, the 8-wave GEMV's
-// RMS order); HD 128 with K = 4096 (two slices, R = 4, the 4-wave order).
+// (device/qkva.h).  HD 64 with K = 2048 (one slice, R = 2 or 1 (_r1), the
+// 8-wave GEMV's RMS order); HD 128 with K = 4096 (two slices, R = 4, the
+// 4-wave order).
 // The host checks the engine's shape against these (engine.cpp qkva_plan).
-#define QKVA_KERNELS(HD, NS, R, WREF) \
-    K256 void rfp4_qkva_hd##HD##_g1(QkvaArgs a) { qkva_body<HD, 1, false, NS, R, WREF>(a); } \
-    K256 void rfp4_qkva_hd##HD##_g2(QkvaArgs a) { qkva_body<HD, 2, false, NS, R, WREF>(a); } \
-    K256 void rfp4_qkva_hd##HD##_g4(QkvaArgs a) { qkva_body<HD, 4, false, NS, R, WREF>(a); } \
-    K256 void rfp4_qkva_hd##HD##_g8(QkvaArgs a) { qkva_body<HD, 8, false, NS, R, WREF>(a); } \
-    K256 void rfp4_qkva_hd##HD##_g1_t(QkvaArgs a) { qkva_body<HD, 1, true, NS, R, WREF>(a); } \
-    K256 void rfp4_qkva_hd##HD##_g2_t(QkvaArgs a) { qkva_body<HD, 2, true, NS, R, WREF>(a); } \
-    K256 void rfp4_qkva_hd##HD##_g4_t(QkvaArgs a) { qkva_body<HD, 4, true, NS, R, WREF>(a); } \
-    K256 void rfp4_qkva_hd##HD##_g8_t(QkvaArgs a) { qkva_body<HD, 8, true, NS, R, WREF>(a); }
-QKVA_KERNELS(64, 1, 2, 8)
-QKVA_KERNELS(128, 2, 4, 4)
+#define QKVA_KERNELS(HD, NS, R, WREF, SFX) \
+    K256 void rfp4_qkva_hd##HD##_g1##SFX(QkvaArgs a) { qkva_body<HD, 1, false, NS, R, WREF>(a); } \
+    K256 void rfp4_qkva_hd##HD##_g2##SFX(QkvaArgs a) { qkva_body<HD, 2, false, NS, R, WREF>(a); } \
+    K256 void rfp4_qkva_hd##HD##_g4##SFX(QkvaArgs a) { qkva_body<HD, 4, false, NS, R, WREF>(a); } \
+    K256 void rfp4_qkva_hd##HD##_g8##SFX(QkvaArgs a) { qkva_body<HD, 8, false, NS, R, WREF>(a); } \
+    K256 void rfp4_qkva_hd##HD##_g1_t##SFX(QkvaArgs a) { qkva_body<HD, 1, true, NS, R, WREF>(a); } \
+    K256 void rfp4_qkva_hd##HD##_g2_t##SFX(QkvaArgs a) { qkva_body<HD, 2, true, NS, R, WREF>(a); } \
+    K256 void rfp4_qkva_hd##HD##_g4_t##SFX(QkvaArgs a) { qkva_body<HD, 4, true, NS, R, WREF>(a); } \
+    K256 void rfp4_qkva_hd##HD##_g8_t##SFX(QkvaArgs a) { qkva_body<HD, 8, true, NS, R, WREF>(a); }
+QKVA_KERNELS(64, 1, 2, 8, )
+QKVA_KERNELS(128, 2, 4, 4, )
+// HD 64 with 1 row per wave (twice the GEMV tiles), used where its grid
+// still fits the device at once: TinyLlama decode 2306 -> 2334 tok/s
+QKVA_KERNELS(64, 1, 1, 8, _r1)
 K256 void rfp4_attn_merge_hd64(AttnArgs a) { attn_merge_body<64>(a); }
 K256 void rfp4_attn_merge_hd128(AttnArgs a) { attn_merge_body<128>(a); }
 
