@@ -507,6 +507,84 @@ def cpu_baseline(threads, steps, steps_one):
     return steps / dt, dt, steps_one / dt1, dt1, t_setup
 
 
+def _timed(fn, min_s=0.25, max_reps=64):
+    """Seconds per call of fn: repeated until min_s has passed (at least once)."""
+    fn()
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        dt = time.perf_counter() - t0
+        if dt >= min_s or n >= max_reps:
+            return dt / n
+
+
+def cpu_legs(threads, tiny_steps=256, tiny_steps_one=4, tiny_gpu_ids=None):
+    """The rest of the CPU baseline, on the same host cores:
+    - GEMV (the reference's k-order loop, fp4_gemv/src/main.rs:130-143, E8M0
+      scales) at config 1 and the Llama-3-8B per-layer shapes: GB/s of the
+      algorithmic bytes, on `threads` threads and on one;
+    - the batched GEMM's closed form (trackb/fp4_scale_test.cu:37 over M x N x K,
+      float64 accumulation: the oracle's checker) at M = 32, GFLOP/s;
+    - TinyLlama-1.1B decode (config 3): the bench's 16-token prompt fed token by
+      token, then `tiny_steps` greedy steps timed on `threads` threads and
+      `tiny_steps_one` more on one (llama_run/src/main.rs:492-536); the tokens
+      are compared with the GPU run's when given."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import pyoracle
+
+    out = {}
+    rng = np.random.default_rng(0xC0)
+    gemv = {}
+    for name, n, k in (("config1_2048x2048", 2048, 2048), ("8b_qkv_6144x4096", 6144, 4096),
+                       ("8b_o_4096x4096", 4096, 4096), ("8b_gate_up_28672x4096", 28672, 4096),
+                       ("8b_down_4096x14336", 4096, 14336)):
+        codes = rng.integers(0, 256, n * k // 2, dtype=np.uint8)
+        scales = rng.integers(121, 130, n * k // 32, dtype=np.uint8)  # 2^-6 .. 2^2, config 1's range
+        x = rng.standard_normal(k).astype(np.float32)
+        row = {"bytes": gemv_bytes(n, k)}
+        for th, key in ((threads, "all"), (1, "one_thread")):
+            pyoracle.set_threads(th)
+            sec = _timed(lambda: pyoracle.gemv_e8m0(n, k, codes, scales, x), min_s=0.2)
+            row[key] = {"ms": round(sec * 1e3, 3), "GB_s": round(gemv_bytes(n, k) / sec / 1e9, 2)}
+        gemv[name] = row
+    out["gemv"] = gemv
+    m, n, k = 32, 4096, 4096
+    ac = rng.integers(0, 256, m * k // 2, dtype=np.uint8)
+    asc = rng.integers(121, 130, m * k // 32, dtype=np.uint8)
+    wc = rng.integers(0, 256, n * k // 2, dtype=np.uint8)
+    wsc = rng.integers(121, 130, n * k // 32, dtype=np.uint8)
+    pyoracle.set_threads(threads)
+    sec = _timed(lambda: pyoracle.gemm_mx_f64(m, n, k, ac, asc, wc, wsc), min_s=0.5, max_reps=4)
+    out["gemm_m32"] = {"shape": f"{m}x{n}x{k}", "ms": round(sec * 1e3, 2), "GFLOP_s": round(2.0 * m * n * k / sec / 1e9, 2),
+                       "cores": threads, "accumulate": "f64 (the closed form of trackb/fp4_scale_test.cu:37)"}
+    cfg = dict(dim=2048, n_layers=22, n_heads=32, n_kv_heads=4, head_dim=64, ffn=5632, vocab=32000, theta=10000.0,
+               eps=1e-5, max_seq=16 + tiny_steps + tiny_steps_one + 2)
+    prompt = np.random.default_rng(16).integers(0, 32000, 16).astype(np.uint32)
+    mdl = pyoracle.Model(cfg, SEED)
+    tok = 0
+    for i, t in enumerate(prompt):
+        tok = mdl.step(int(t), i)
+    ids = [tok]
+    t0 = time.perf_counter()
+    for i in range(tiny_steps - 1):
+        ids.append(mdl.step(ids[-1], 16 + i))
+    dt = time.perf_counter() - t0
+    pyoracle.set_threads(1)
+    t0 = time.perf_counter()
+    for i in range(tiny_steps_one):
+        ids.append(mdl.step(ids[-1], 16 + tiny_steps - 1 + i))
+    dt1 = time.perf_counter() - t0
+    mdl.close()
+    out["tinyllama"] = {"tok_s": round((tiny_steps - 1) / dt, 3), "cores": threads,
+                        "one_thread": {"tok_s": round(tiny_steps_one / dt1, 3), "steps": tiny_steps_one},
+                        "steps": tiny_steps,
+                        "tokens_identical_to_gpu": (bool(np.array_equal(np.array(ids[:tiny_steps], np.uint32),
+                                                                        tiny_gpu_ids[:tiny_steps]))
+                                                    if tiny_gpu_ids is not None else None)}
+    return out
+
+
 # llama_decode/src/main.rs:289-298,357-360: the reference's random-weight
 # decode harness, 221.6 tok/s on an RTX 5070 Ti (main.tex:208)
 HARNESS_P, HARNESS_WARM, HARNESS_GEN = 512, 4, 32
@@ -588,8 +666,10 @@ def main():
     ap.add_argument("--steps", type=int, default=128)
     ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--cpu-steps", type=int, default=16, help="decode steps of the CPU oracle on all threads")
-    ap.add_argument("--cpu-steps-one", type=int, default=1, help="decode steps of the CPU oracle on one thread")
+    ap.add_argument("--cpu-steps", type=int, default=8, help="decode steps of the CPU oracle on all threads")
+    ap.add_argument("--cpu-steps-one", type=int, default=4, help="decode steps of the CPU oracle on one thread")
+    ap.add_argument("--no-persistent", action="store_true",
+                    help="skip the opt-in persistent step (its cooperative launch; taken out of profiler runs)")
     ap.add_argument("--no-tiny", action="store_true", help="skip the TinyLlama-1.1B line")
     ap.add_argument("--no-harness", action="store_true", help="skip the llama_decode harness line")
     ap.add_argument("--no-gemm", action="store_true", help="skip the config-5 batched GEMM figures")
@@ -655,7 +735,7 @@ def main():
     log(f"GEMV path alone: {path_bytes / 1e9:.3f} GB in {path_ms * 1e3:.1f} us -> {path_gbs:.0f} GB/s; "
         f"gate/up GEMV {gate_in_us:.2f} us in the step ({gate_in_gbs:.0f} GB/s), {gate_ms * 1e3:.2f} us alone "
         f"({gate_gbs:.0f} GB/s)")
-    persistent = persistent_run(rf, eng)
+    persistent = None if args.no_persistent else persistent_run(rf, eng)
     if persistent:
         log(f"persistent decode (opt-in): {persistent['tok_s']} tok/s vs graph {persistent['graph_tok_s_same_run']} "
             f"tok/s, tokens identical: {persistent['tokens_identical_to_graph']}")
@@ -667,11 +747,12 @@ def main():
         log(f"prefill {prefill['tokens']}: {prefill['ms']} ms, {prefill['tok_s']} tok/s, {prefill['TFLOP_s']} TFLOP/s")
     eng.close()
 
-    tiny = None
+    tiny, tiny_ids = None, None
     if not args.no_tiny:
         r = np.random.default_rng(16).integers(0, 32000, 16).astype(np.uint32)
         teng, tcfg, tms, twall, tids = decode_run(rf, "tinyllama-1.1b", 16 + 256 + TIMED_STEPS + 8, 0, r, 0, 256)
         tkern = step_kernels(teng, "tinyllama-1.1b")
+        tiny_ids = tids[16:16 + 256]
         tiny = {"tok_s": round(256 / (tms / 1e3), 1), "ms_per_token": round(tms / 256, 4),
                 "step_kernels_us": {k: v[1] for k, v in tkern.items()},
                 "workload": "TinyLlama-1.1B arch, 16-token prompt, 256 greedy steps"}
@@ -696,6 +777,12 @@ def main():
                          f"setup {t_setup:.1f} s untimed"}
         log(f"cpu oracle: {tok_all:.3f} tok/s on {threads} threads, {tok_one:.3f} tok/s on 1 ({cpu_model()}, nproc "
             f"{os.cpu_count()})")
+        legs = cpu_legs(threads, tiny_gpu_ids=tiny_ids)
+        cpu.update(legs)
+        log("cpu oracle GEMV GB/s (all / 1 thread): " + ", ".join(
+            f"{k} {v['all']['GB_s']}/{v['one_thread']['GB_s']}" for k, v in legs["gemv"].items()) +
+            f"; GEMM M=32 {legs['gemm_m32']['GFLOP_s']} GFLOP/s; TinyLlama {legs['tinyllama']['tok_s']} tok/s "
+            f"({legs['tinyllama']['one_thread']['tok_s']} on 1), tokens = GPU: {legs['tinyllama']['tokens_identical_to_gpu']}")
 
     out = {
         "metric": METRIC,

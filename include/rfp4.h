@@ -43,6 +43,9 @@ enum {
     RFP4_E_ALIGN = -6,       /* pointer not 16-byte aligned where required */
     RFP4_E_HIP = -7,         /* HIP runtime error, see rfp4_last_error() */
     RFP4_E_NO_DEVICE = -8,
+    RFP4_E_WAIT = -9,        /* a device-side wait of a decode step hit its spin limit
+                                (workgroups not co-resident): that generation's tokens
+                                are invalid; the next llama_engine_begin* clears it */
 };
 
 const char *rfp4_last_error(void);
@@ -60,6 +63,14 @@ int rfp4_kernel_name(uint32_t i, char *buf, size_t cap);
  * the reference (fp4_gemv/src/main.rs:144-150,177-191). */
 /* CudaContext::new(device) + kernels::load(&ctx): llama_run/src/main.rs:432,488 */
 int rfp4_init(int device);
+/* Releases every HIP object the library holds: waits for the device,
+ * destroys every engine still alive (its step graphs, stream and memory),
+ * frees the runtime's workspaces and unloads the code object.  Call it before
+ * the host program exits (the Python binding registers it with atexit);
+ * rfp4_init may be called again afterwards.  Caller-owned buffers, streams
+ * and events stay the caller's to free.  No reference counterpart (the
+ * reference's RAII drops free its objects at the end of main). */
+int rfp4_shutdown(void);
 int rfp4_device_count(int *count);
 /* Compute units, LDS bytes per workgroup and peak clock of the initialised device. */
 int rfp4_device_info(int *num_cus, size_t *lds_per_block, int *clock_khz);
@@ -102,7 +113,11 @@ int mx4_gemv(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_t *codes,
  *                     (fp4_gemv gate/up + swiglu, :526-528)
  *  mx4_gemv_argmax:   y = W.x and *best_token = argmax(y) with the
  *                     reference's tie rule (fp4_gemv lm_head + argmax, :533-534);
- *                     workspace: ceil(n/16)*8 bytes (mx4_gemv_argmax_workspace). */
+ *                     workspace: at least mx4_gemv_argmax_workspace(n) =
+ *                     round_up(n, 8) + 64 bytes, 8-byte aligned (one 8-byte key
+ *                     per workgroup, then a 16-byte cursor).  The library cannot
+ *                     see the caller's allocation: a smaller buffer is written
+ *                     out of bounds, so size it with that function. */
 /* rmsnorm + fp4_gemv (llama_run/src/main.rs:513-514 fused): y = W.(x*rms*w_norm),
  * rms = 1/sqrt(sum(x^2)/k + eps), fp16 norm weights. */
 int mx4_gemv_rmsnorm(rfp4_stream_t stream, uint32_t n, uint32_t k, const uint8_t *codes, const uint8_t *scales,
@@ -195,7 +210,8 @@ int fp4_gemm(rfp4_stream_t stream, uint32_t m, uint32_t n, uint32_t k, const uin
              const uint8_t *a_scales, const uint8_t *w_codes, const uint8_t *w_scales, float *c);
 /* Test hook: force the GEMM tile (index into the compiled list, largest
  * first: 256x256, 256x128, 128x128, 64x128, 32x128, then 5 = the few-row
- * kernel for m <= 64 and k a multiple of 512 up to 16384; -1 = automatic)
+ * kernel for k a multiple of 512, up to 16384 for m <= 32 and up to 8192
+ * for m <= 64; -1 = automatic)
  * and K split (0 = automatic; for the few-row kernel: W fragments of 16 rows
  * per workgroup, 1, 2 or 4) of later fp4_gemm calls on this thread.  No
  * reference counterpart. */

@@ -467,6 +467,7 @@ struct AttnSplit {
     uint32_t kvh, split, row, G, seq, nsplit, t0, nt, nsub, pos;
     uint32_t hbase, cidx; // first query head of this workgroup, its merge-counter index
     bool fused, owner, writer;
+    bool q_timeout = false; // QT: a poll of q|k|v hit its spin limit (NaN q, no K/V append)
 
     // Workgroup x index -> KV head and query-head slice: with head_split HS,
     // x = hg * n_kv_heads + kvh takes query heads hg*G .. hg*G + G - 1 of the
@@ -493,7 +494,8 @@ struct AttnSplit {
     // Every word is polled until it carries the tag; each word read with the
     // tag is the value stored with it (one 64-bit atomic object), so no fence
     // or counter is needed.  A poll past ATTN_TAG_SPIN_LIMIT spins sets *err
-    // (the results are then invalid, and the engine reports it).
+    // (the engine reports it), makes q and the current token's k, v NaN (so
+    // the outputs are NaN) and keeps the split from appending to the cache.
     RFP4_DEV void load_q_tagged(const AttnArgs &a, uint32_t tag)
     {
         const int tid = threadIdx.x;
@@ -547,13 +549,15 @@ struct AttnSplit {
                 if (!attn_tag_ok(wk[3], tag)) wk[3] = attn_load_tagged(vn + tid + HALF);
             }
         }
+        const float nan = __uint_as_float(0x7FC00000u);
 #pragma unroll
         for (int m = 0; m < QPT; m++) {
-            qa[m] = attn_tag_val(wa[m]);
-            qb[m] = attn_tag_val(wb[m]);
+            qa[m] = timeout ? nan : attn_tag_val(wa[m]);
+            qb[m] = timeout ? nan : attn_tag_val(wb[m]);
         }
 #pragma unroll
-        for (int r = 0; r < 4; r++) tkv[r] = kv ? attn_tag_val(wk[r]) : 0.0f;
+        for (int r = 0; r < 4; r++) tkv[r] = timeout ? nan : (kv ? attn_tag_val(wk[r]) : 0.0f);
+        q_timeout = timeout;
         if (timeout && tid == 0 && a.err) __hip_atomic_store(a.err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 
@@ -670,7 +674,7 @@ struct AttnSplit {
             knew[tid + HALF] = r1;
             vnew[tid] = w0;
             vnew[tid + HALF] = w1;
-            if (writer) {
+            if (writer && !q_timeout) {
                 kdst[tid] = r0;
                 kdst[tid + HALF] = r1;
                 vdst[tid] = w0;

@@ -161,7 +161,10 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
     // ---- DMA sources.  Code block j of this wave covers tile rows 8 (wave + 4 j) .. +7; lane l
     // fetches logical chunk (l & 7) ^ swz(row) of row 8 (wave + 4 j) + l / 8, which the DMA writes
     // to physical chunk l & 7.  Scale block b of this wave covers rows 32 (wave + 4 b) .. +31; lane l
-    // fetches bytes 4 (l & 1) .. +3 of row 32 (wave + 4 b) + l / 2.
+    // fetches bytes 4 (l / 32) .. +3 of row 32 (wave + 4 b) + l % 32, so a block is stored as two
+    // planes of 32 words (the step's scale bytes 0-3, then 4-7, of each row): the 32 lanes of one
+    // half-wave read 32 consecutive words, free of bank conflicts (row-major 8-byte rows put
+    // rows r and r + 16 on one bank).
     const uint8_t *src[NJ];
 #pragma unroll
     for (uint32_t j = 0; j < NJ; j++) {
@@ -173,10 +176,10 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
     const uint8_t *ssrc[NSB];
 #pragma unroll
     for (uint32_t b = 0; b < NSB; b++) {
-        const uint32_t row = min(32u * (wave + 4u * b) + (lane >> 1), R - 1u);
+        const uint32_t row = min(32u * (wave + 4u * b) + (lane & 31u), R - 1u);
         const uint8_t *base = row < BM ? g.a_scales + (size_t)min(mt * BM + row, g.m - 1u) * nblk
                                        : g.w_scales + (size_t)min(nt * BN + (row - BM), g.n - 1u) * nblk;
-        ssrc[b] = base + (lane & 1u) * 4u;
+        ssrc[b] = base + (lane >> 5) * 4u;
     }
 #define RFP4_GEMM_DMA(S, BUF)                                                                              \
     do {                                                                                                   \
@@ -199,19 +202,21 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[fa][fb][r] = 0.0f;
 
-    // fragment rows of this lane and their swizzles
-    uint32_t aoff[FA], boff[FB], asw[FA], bsw[FB];
+    // fragment rows of this lane, their swizzles and scale words (plane h of the row's block)
+    uint32_t aoff[FA], boff[FB], asw[FA], bsw[FB], asc[FA], bsc[FB];
 #pragma unroll
     for (int fa = 0; fa < FA; fa++) {
         const uint32_t r = wm * (32u * FA) + 32u * fa + r32;
         aoff[fa] = r * 128u;
         asw[fa] = gemm_swz(r);
+        asc[fa] = SC0 + 256u * (r >> 5) + 128u * h + 4u * (r & 31u);
     }
 #pragma unroll
     for (int fb = 0; fb < FB; fb++) {
         const uint32_t r = BM + wn * (32u * FB) + 32u * fb + r32;
         boff[fb] = r * 128u;
         bsw[fb] = gemm_swz(r);
+        bsc[fb] = SC0 + 256u * (r >> 5) + 128u * h + 4u * (r & 31u);
     }
 
     // the first NST - 1 steps in flight, then wait for the first
@@ -245,7 +250,7 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
         uint32_t sa[FA], sb[FB];
 #pragma unroll
         for (int fa = 0; fa < FA; fa++) {
-            sa[fa] = *(const __attribute__((address_space(3))) uint32_t *)(st + SC0 + (aoff[fa] >> 4) + h * 4u);
+            sa[fa] = *(const __attribute__((address_space(3))) uint32_t *)(st + asc[fa]);
 #pragma unroll
             for (uint32_t t = 0; t < 4; t++)
                 av[t][fa] = *(const __attribute__((address_space(3))) u32x4 *)(st + aoff[fa] +
@@ -253,7 +258,7 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
         }
 #pragma unroll
         for (int fb = 0; fb < FB; fb++) {
-            sb[fb] = *(const __attribute__((address_space(3))) uint32_t *)(st + SC0 + (boff[fb] >> 4) + h * 4u);
+            sb[fb] = *(const __attribute__((address_space(3))) uint32_t *)(st + bsc[fb]);
 #pragma unroll
             for (uint32_t t = 0; t < 4; t++)
                 bv[t][fb] = *(const __attribute__((address_space(3))) u32x4 *)(st + boff[fb] +

@@ -19,7 +19,9 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <thread>
+#include <unordered_set>
 #include <vector>
 
 #include "runtime.h"
@@ -209,10 +211,10 @@ static int enqueue_step(llama_engine *e, uint32_t nsplit)
         aa.ts = hd; aa.hs = (uint64_t)e->max_seq_alloc * hd;
         aa.n_heads = c.n_heads; aa.n_kv_heads = c.n_kv_heads; aa.head_dim = hd; aa.seq = 0;
         aa.chunk = e->attn_chunk; aa.max_splits = e->attn_max_splits;
+        aa.err = e->p_err; // every device-side wait (tagged merge, fused q|k|v poll) reports here
         if (e->attn_tagged && attn_tagged_mode(e->attn_merge_mode, nsplit)) {
             aa.tagged = e->attn_tagged + (size_t)l * e->attn_tag_layer;
             aa.tag_splits = e->attn_tag_splits;
-            aa.err = e->p_err;
         } else {
             aa.counters = attn_inmerge_mode(e->attn_merge_mode, nsplit) ? e->attn_counters : nullptr;
         }
@@ -335,19 +337,21 @@ static int enqueue_step_persist(llama_engine *e)
     return launch("rfp4_step", dim3(1), dim3(1024), s, &sa);
 }
 
-// A grid barrier of the persistent kernel or a tagged attention merge that
-// hit its spin limit leaves the error word set: the steps' results are not
-// valid.
+// A grid barrier of the persistent kernel, a tagged attention merge or the
+// fused q|k|v + attention launch's poll that hit its spin limit leaves the
+// error word set: the generation's results are not valid.  The word is
+// cleared when the next generation begins (llama_engine_begin*).
 static int wait_check(llama_engine *e)
 {
-    if (!e->persist_ok && !e->attn_tagged) return RFP4_OK;
+    if (!e->persist_ok && !e->attn_tagged && !e->qkva_R) return RFP4_OK;
     uint32_t err = 0;
     int rc = hip_check(hipMemcpyAsync(&err, e->p_err, 4, hipMemcpyDeviceToHost, e->stream), "D2H wait error");
     if (!rc) rc = hip_check(hipStreamSynchronize(e->stream), "hipStreamSynchronize(wait error)");
     if (rc) return rc;
     if (err)
-        return set_error(RFP4_E_HIP, "decode: a device-side wait hit its spin limit (persistent grid barrier or tagged "
-                                     "attention merge: workgroups not co-resident)");
+        return set_error(RFP4_E_WAIT, "decode: a device-side wait hit its spin limit (persistent grid barrier, tagged "
+                                      "attention merge or fused q|k|v poll: workgroups not co-resident); the "
+                                      "generation's tokens are invalid");
     return RFP4_OK;
 }
 
@@ -570,14 +574,44 @@ static int set_embed_mode(llama_engine *e, bool no_embed)
     return RFP4_OK;
 }
 
+// Engines handed out by the creation calls and not yet destroyed: a stale or
+// foreign handle given to llama_engine_destroy is refused, and
+// rfp4_shutdown destroys whatever is left.
+static std::mutex g_engines_mu;
+static std::unordered_set<llama_engine *> g_engines;
+
+static void engine_register(llama_engine *e)
+{
+    std::lock_guard<std::mutex> lk(g_engines_mu);
+    g_engines.insert(e);
+}
+
+static bool engine_unregister(llama_engine *e)
+{
+    std::lock_guard<std::mutex> lk(g_engines_mu);
+    return g_engines.erase(e) != 0;
+}
+
 static void engine_free(llama_engine *e)
 {
     if (!e) return;
+    engine_unregister(e);
     if (e->stream) hipStreamSynchronize(e->stream);
     drop_graphs(e);
     for (void *p : e->allocs) hipFree(p);
     if (e->stream) hipStreamDestroy(e->stream);
     delete e;
+}
+
+size_t rfp4::engines_destroy_all()
+{
+    std::vector<llama_engine *> live;
+    {
+        std::lock_guard<std::mutex> lk(g_engines_mu);
+        live.assign(g_engines.begin(), g_engines.end());
+    }
+    for (llama_engine *e : live) engine_free(e);
+    return live.size();
 }
 
 // ---------------------------------------------------------------- creation
@@ -1011,12 +1045,15 @@ int llama_engine_create(const rfp4_model_config *cfg, uint64_t seed, llama_engin
         engine_free(e);
         return rc;
     }
+    engine_register(e);
     *out = e;
     return RFP4_OK;
 }
 
 int llama_engine_destroy(llama_engine *e)
 {
+    if (!e) return RFP4_OK;
+    if (!engine_unregister(e)) return set_error(RFP4_E_INVALID, "llama_engine_destroy: not a live engine");
     engine_free(e);
     return RFP4_OK;
 }
@@ -1056,6 +1093,7 @@ int llama_engine_begin(llama_engine *e, const uint32_t *prompt, uint32_t n_promp
     StepState st{(int32_t)pos0, 0, n_prompt, ids_cap};
     if (!rc) rc = hip_check(hipMemcpy(e->state, &st, sizeof st, hipMemcpyHostToDevice), "H2D cursor");
     if (!rc) rc = tag_clear(e);
+    if (!rc) rc = fill_words(e->p_err, 1, 0u, e->stream); // a new generation: no wait has failed yet
     if (!rc) rc = embed_first(e);
     if (rc) return rc;
     e->h_pos = pos0;
@@ -1103,6 +1141,7 @@ int llama_engine_begin_harness(llama_engine *e, uint32_t ctx, uint32_t ids_cap)
     StepState st{(int32_t)ctx, 0, 1u, ids_cap};
     if (!rc) rc = hip_check(hipMemcpy(e->state, &st, sizeof st, hipMemcpyHostToDevice), "H2D cursor");
     if (!rc) rc = tag_clear(e);
+    if (!rc) rc = fill_words(e->p_err, 1, 0u, e->stream); // a new generation: no wait has failed yet
     if (rc) return rc;
     e->h_pos = ctx;
     e->h_step = 0;
@@ -1173,7 +1212,7 @@ int llama_engine_time_steps(llama_engine *e, uint32_t n_steps, rfp4_kernel_time 
     if (rc) return rc;
     e->h_pos += n_steps;
     e->h_step += n_steps;
-    return RFP4_OK;
+    return wait_check(e);
 }
 
 int llama_engine_read_ids(llama_engine *e, uint32_t *ids, uint32_t count)
@@ -1343,6 +1382,7 @@ int llama_engine_create_from_safetensors(const rfp4_model_config *cfg, const cha
         engine_free(e);
         return rc;
     }
+    engine_register(e);
     *out = e;
     return RFP4_OK;
 }
@@ -1418,6 +1458,7 @@ int llama_engine_load(const char *path, uint32_t max_seq, llama_engine **out)
         engine_free(e);
         return rc;
     }
+    engine_register(e);
     *out = e;
     return RFP4_OK;
 }

@@ -170,5 +170,7 @@ int main(int argc, char **argv)
                timed / dt, timed, P);
     printf("✓ decode `tok decode <output ids>` to read the text\n");
     llama_engine_destroy(e);
+    // every HIP object of the library released before main returns
+    if (rfp4_shutdown()) return fail("rfp4_shutdown");
     return 0;
 }

@@ -303,6 +303,31 @@ int rfp4_init(int device)
     return RFP4_OK;
 }
 
+// Every HIP object the library holds, released in dependency order: the
+// work of every stream, the engines (step graphs, their streams and device
+// memory), the runtime's workspaces and the code object.  A host program
+// calls it before it returns from main, so that no graph, stream, module or
+// allocation of this library is left for the HIP runtime's exit-time
+// teardown (which runs after tools such as rocprofv3 have finalized).
+int rfp4_shutdown(void)
+{
+    std::lock_guard<std::mutex> lk(g_mu);
+    Runtime *rt = g_rt;
+    if (!rt) return RFP4_OK;
+    int rc = hip_check(hipDeviceSynchronize(), "hipDeviceSynchronize(shutdown)");
+    engines_destroy_all();
+    auto keep = [&rc](int r) {
+        if (!rc) rc = r;
+    };
+    keep(hip_check(hipFree(rt->attn_part), "hipFree(attn workspace)"));
+    keep(hip_check(hipFree(rt->gemm_part), "hipFree(gemm workspace)"));
+    keep(hip_check(hipFree(rt->attn_counters), "hipFree(attn counters)"));
+    keep(hip_check(hipModuleUnload(rt->module), "hipModuleUnload"));
+    g_rt = nullptr;
+    delete rt;
+    return rc;
+}
+
 int rfp4_device_info(int *num_cus, size_t *lds_per_block, int *clock_khz)
 {
     if (!g_rt) return set_error(RFP4_E_NOT_INIT, "rfp4_init has not been called");
@@ -1276,8 +1301,8 @@ int gemm_launch(hipStream_t stream, uint32_t m, uint32_t n, uint32_t k, const ui
     GemmPlan p = gemm_plan(m, n, k, (uint32_t)rt->num_cus);
     if (p.tile == kGemmSkinny) {
         if (!gemm_skinny_ok(m, k))
-            return set_error(RFP4_E_SHAPE, "fp4_gemm: the few-row kernel needs m <= 64 and k a multiple of 512 up to 32768 "
-                                           "(m=%u k=%u)", m, k);
+            return set_error(RFP4_E_SHAPE, "fp4_gemm: the few-row kernel needs k a multiple of 512, up to 16384 for "
+                                           "m <= 32 and up to 8192 for m <= 64 (m=%u k=%u)", m, k);
         if (!gemm_rows_has(p.ma, p.nb, (int)p.kz))
             return set_error(RFP4_E_INVALID, "fp4_gemm: no few-row variant with %d W fragments for m=%u k=%u", (int)p.kz, m, k);
         char name[48];

@@ -80,6 +80,8 @@ uint32_t attn_head_split_for(uint32_t n_heads, uint32_t n_kv_heads, uint32_t spl
 int attn_decode_ws(hipStream_t s, uint32_t nh, uint32_t nkv, uint32_t hd, uint32_t seq, const float *q, const void *kc,
                    const void *vc, uint64_t ts, uint64_t hs, float *out, int f16, float *part, size_t part_floats,
                    bool allow_inmerge);
+// Destroys every engine still alive (rfp4_shutdown); returns how many.
+size_t engines_destroy_all();
 // Looks up, once per device and with that device current, the address of
 // the allocation-free entry points' static scratch (csrc/noalloc.hip).
 int noalloc_setup(int device);

@@ -11,9 +11,11 @@ present, the calls fail loudly.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes as C
 import os
 import re
+import weakref
 
 import numpy as np
 
@@ -60,6 +62,7 @@ _SIGS = {
     "rfp4_kernel_count": (I32, [C.POINTER(U32)]),
     "rfp4_kernel_name": (I32, [U32, C.c_char_p, SZ]),
     "rfp4_init": (I32, [I32]),
+    "rfp4_shutdown": (I32, []),
     "rfp4_device_count": (I32, [C.POINTER(I32)]),
     "rfp4_device_info": (I32, [C.POINTER(I32), C.POINTER(SZ), C.POINTER(I32)]),
     "rfp4_stream_create": (I32, [C.POINTER(P)]),
@@ -187,14 +190,40 @@ def check(rc: int):
 
 
 _inited = False
+_atexit_registered = False
+# Objects that own a library or HIP resource (engines, device buffers, events,
+# owned streams), released by shutdown() if still alive.
+_live = weakref.WeakSet()
 
 
 def init(device: int = 0):
-    """CudaContext::new(0) + kernels::load (llama_run/src/main.rs:432,488)."""
-    global _inited
+    """CudaContext::new(0) + kernels::load (llama_run/src/main.rs:432,488).
+    Registers shutdown() to run at interpreter exit."""
+    global _inited, _atexit_registered
     if not _inited:
         check(load().rfp4_init(device))
         _inited = True
+        if not _atexit_registered:
+            atexit.register(shutdown)
+            _atexit_registered = True
+
+
+def shutdown():
+    """Release every resource held through the library, then the library's
+    own (rfp4_shutdown): engines first (step graphs, their streams and memory),
+    then device buffers, events and owned streams.  Runs at interpreter exit,
+    before the HIP runtime's own teardown; the released objects' later
+    free/close calls are no-ops.  init() may be called again afterwards."""
+    global _inited
+    if not _inited:
+        return
+    live = list(_live)
+    for kind in (Engine, DeviceBuffer, Event, Stream):
+        for o in live:
+            if isinstance(o, kind):
+                o._release()
+    _inited = False
+    check(load().rfp4_shutdown())
 
 
 def kernel_names() -> list:
@@ -223,6 +252,7 @@ class Stream:
             check(load().rfp4_stream_create(C.byref(h)))
             self.h = h.value
             self._own = True
+            _live.add(self)
         else:
             self.h = handle
             self._own = False
@@ -235,6 +265,14 @@ class Stream:
             load().rfp4_stream_destroy(self.h)
             self.h = None
 
+    _release = destroy
+
+    def __del__(self):
+        try:
+            self.destroy()
+        except Exception:
+            pass
+
 
 class DeviceBuffer:
     """Device allocation (reference DeviceBuffer<T>)."""
@@ -245,6 +283,7 @@ class DeviceBuffer:
         p = P()
         check(load().rfp4_malloc(C.byref(p), max(self.nbytes, 16)))
         self.ptr = p.value
+        _live.add(self)
 
     @classmethod
     def from_host(cls, arr: np.ndarray, stream: Stream | None = None):
@@ -278,6 +317,8 @@ class DeviceBuffer:
             load().rfp4_free(self.ptr)
             self.ptr = None
 
+    _release = free
+
     def __del__(self):
         try:
             self.free()
@@ -290,6 +331,7 @@ class Event:
         h = P()
         check(load().rfp4_event_create(C.byref(h)))
         self.h = h.value
+        _live.add(self)
 
     def record(self, stream: Stream | None = None):
         check(load().rfp4_event_record(self.h, stream.h if stream else None))
@@ -302,9 +344,16 @@ class Event:
         check(load().rfp4_event_elapsed_ms(C.byref(ms), self.h, end.h))
         return ms.value
 
+    def destroy(self):
+        if self.h:
+            load().rfp4_event_destroy(self.h)
+            self.h = None
+
+    _release = destroy
+
     def __del__(self):
         try:
-            load().rfp4_event_destroy(self.h)
+            self.destroy()
         except Exception:
             pass
 
@@ -538,6 +587,7 @@ class Engine:
             _handle = h.value
         self.h = _handle
         self.stream = Stream(load().llama_engine_stream(self.h))
+        _live.add(self)
 
     @classmethod
     def from_safetensors(cls, cfg: ModelConfig, path: str) -> "Engine":
@@ -688,6 +738,8 @@ class Engine:
         if self.h:
             load().llama_engine_destroy(self.h)
             self.h = None
+
+    _release = close
 
     def __del__(self):
         try:

@@ -37,6 +37,23 @@ def _run_epi(rf, stream, epi, n, k, dc, ds, dx, base):
     return got, (int(best.to_host(1, np.uint32, stream)[0]) if best is not None else None)
 
 
+def _activation_like(orc, n, k, codes, scales, x, epi):
+    """x scaled by a power of two (W.x scales exactly) so that the SwiGLU
+    gates have the magnitudes of a real activation (RMS about 3, most |g| < 10)
+    instead of config 1's hundreds, where silu saturates."""
+    if epi != "swiglu":
+        return x
+    g = orc.gemv_e8m0(n, k, codes, scales, x)[:n // 2]
+    e = int(np.round(np.log2(3.0 / max(float(np.sqrt(np.mean(g.astype(np.float64) ** 2))), 1e-30))))
+    return (x * np.float32(2.0 ** e)).astype(np.float32)
+
+
+def _assert_gates_unsaturated(f64, n):
+    g = f64[:n]
+    assert np.mean(np.abs(g) < 10.0) >= 0.5, "gates mostly saturated"
+    assert np.mean(np.abs(g) < 1.0) >= 0.1, "no gates in silu's curved range"
+
+
 def _check_epi(orc, epi, got, best, n, full, f64, absf, base, tag):
     if epi in ("store", "argmax"):
         _assert_gemv_close(got, full[:n], f64[:n], absf[:n])
@@ -59,9 +76,12 @@ def _check_epi(orc, epi, got, best, n, full, f64, absf, base, tag):
 def test_gemv_all_variants(rf, orc, stream, epi, k):
     n = 67  # not a multiple of any workgroup row count
     codes, scales, x = _config1(orc, 2 * n, k, seed=k + len(epi))
+    x = _activation_like(orc, 2 * n, k, codes, scales, x, epi)
     dc, ds, dx = _dev(rf, codes, stream), _dev(rf, scales, stream), _dev(rf, x, stream)
     full = orc.gemv_e8m0(2 * n, k, codes, scales, x)
     f64, absf = orc.gemv_e8m0_f64(2 * n, k, codes, scales, x)
+    if epi == "swiglu":
+        _assert_gates_unsaturated(f64, n)
     need = (k + 2047) // 2048
     base = np.linspace(-1, 1, n).astype(np.float32)
     ran = 0
@@ -107,9 +127,12 @@ def test_gemv_eight_wave_variants(rf, orc, stream, epi, r, ns, n, k):
     if (k + 2047) // 2048 > ns:
         pytest.skip("k needs more slices than the variant issues")
     codes, scales, x = _config1(orc, 2 * n, k, seed=n + k + r)
+    x = _activation_like(orc, 2 * n, k, codes, scales, x, epi)
     dc, ds, dx = _dev(rf, codes, stream), _dev(rf, scales, stream), _dev(rf, x, stream)
     full = orc.gemv_e8m0(2 * n, k, codes, scales, x)
     f64, absf = orc.gemv_e8m0_f64(2 * n, k, codes, scales, x)
+    if epi == "swiglu":
+        _assert_gates_unsaturated(f64, n)
     base = np.linspace(-1, 1, n).astype(np.float32)
     try:
         for forced in (True, False):

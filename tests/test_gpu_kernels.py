@@ -191,6 +191,32 @@ def test_rope_parity(rf, orc, stream, heads, hd, theta, pos):
     np.testing.assert_array_equal(got, qref)  # no fused multiply-add: bit-identical
 
 
+@pytest.mark.parametrize("heads", [32, 4])
+def test_rope_config2_position_sweep(rf, orc, stream, heads):
+    """q 32x64 and k 4x64, theta 10000, every position
+    0..2047 (one launch per position over its own copy of the vector),
+    bit-identical to the oracle's rotation with the engine's table."""
+    hd, theta, npos = 64, 10000.0, 2048
+    half = hd // 2
+    r, _ = orc.xorshift32(0x13579BDF + heads, heads * hd)
+    q = (((r % 2001).astype(np.float32) - 1000.0) / 500.0).astype(np.float32)
+    cos_t, sin_t = orc.rope_table(npos, hd, theta)
+    dq = _dev(rf, np.tile(q, npos), stream)
+    dcos, dsin = _dev(rf, cos_t, stream), _dev(rf, sin_t, stream)
+    for pos in range(npos):
+        rf.rope(stream, heads, hd, pos * half, dcos, dsin, dq.ptr + pos * heads * hd * 4)
+    got = dq.to_host(npos * heads * hd, np.float32, stream).reshape(npos, heads * hd)
+    for pos in range(npos):
+        qref = orc.rope(q, heads, hd, cos_t[pos * half:(pos + 1) * half], sin_t[pos * half:(pos + 1) * half])
+        np.testing.assert_array_equal(got[pos], qref, err_msg=f"position {pos}")
+    # position 0 is the identity; every pair keeps its norm to f32 rounding
+    np.testing.assert_array_equal(got[0], q)
+    pairs = got.reshape(npos, heads, 2, half).astype(np.float64)
+    q2 = q.reshape(heads, 2, half).astype(np.float64)
+    np.testing.assert_allclose(np.hypot(pairs[:, :, 0], pairs[:, :, 1]),
+                               np.broadcast_to(np.hypot(q2[:, 0], q2[:, 1]), (npos, heads, half)), rtol=1e-6)
+
+
 def _assert_attn_close(got, ref):
     """Attention bar: the reference's per-element relative error 1e-4
     (llama_attn_decode/src/main.rs:203-204, |d| / max(|ref|, 1e-3)) plus a
