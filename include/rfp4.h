@@ -446,6 +446,16 @@ int llama_engine_kv(llama_engine *e, int layer, const void **k, const void **v, 
  * attention output a [rows][n_heads*head_dim] f32. */
 int llama_engine_prefill_buffers(llama_engine *e, float **x, uint8_t **codes, uint8_t **scales, float **c, float **a,
                                  uint32_t *rows_cap);
+/* Test hook of the decode step's device-side waits (no reference
+ * counterpart): for a step with `nsplit` attention splits, *err_wired = 1 if
+ * every layer's attention (plain, tagged merge or fused q|k|v poll) reports
+ * a spin-limit hit to the engine's error word, *fused = 1 if that step runs
+ * the fused q|k|v + attention launch, *checked = 1 if llama_engine_read_ids
+ * and llama_engine_time_steps read the word for this engine.  set_err = 1
+ * then sets the word as a timed-out wait would (no kernel is launched), so
+ * that the next read returns RFP4_E_WAIT until llama_engine_begin* clears
+ * it. */
+int rfp4_debug_engine_wait(llama_engine *e, int set_err, uint32_t nsplit, int *err_wired, int *checked, int *fused);
 /* Per-token weight and KV bytes the step streams at a given position. */
 uint64_t llama_engine_weight_bytes(const llama_engine *e);
 

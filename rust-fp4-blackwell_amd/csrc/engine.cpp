@@ -189,6 +189,31 @@ static bool qkva_plan(const llama_engine *e, uint32_t nsplit, bool tagged, QkvaP
     return false;
 }
 
+// Layer l's attention arguments in a decode step with `nsplit` splits: the
+// merge by arrival counters (up to 8 splits), by tagged states (9-32) or by
+// the merge kernel; every device-side wait of the step reports to p_err.
+static AttnArgs step_attn_args(const llama_engine *e, uint32_t l, uint32_t nsplit)
+{
+    const rfp4_model_config &c = e->c;
+    const uint32_t qd = qdim(c), kvd = kvdim(c), hd = c.head_dim;
+    AttnArgs aa{};
+    aa.q = e->qkv; aa.kc = kv_layer(e, l, 0); aa.vc = kv_layer(e, l, 1); aa.out = e->attn_out;
+    aa.part = e->attn_part; aa.pos_ptr = &e->state->pos;
+    aa.cosv = e->cos_tab; aa.sinv = e->sin_tab; aa.k_new = e->qkv + qd; aa.v_new = e->qkv + qd + kvd;
+    aa.ts = hd; aa.hs = (uint64_t)e->max_seq_alloc * hd;
+    aa.n_heads = c.n_heads; aa.n_kv_heads = c.n_kv_heads; aa.head_dim = hd; aa.seq = 0;
+    aa.chunk = e->attn_chunk; aa.max_splits = e->attn_max_splits;
+    aa.err = e->p_err; // every device-side wait (tagged merge, fused q|k|v poll) reports here
+    if (e->attn_tagged && attn_tagged_mode(e->attn_merge_mode, nsplit)) {
+        aa.tagged = e->attn_tagged + (size_t)l * e->attn_tag_layer;
+        aa.tag_splits = e->attn_tag_splits;
+    } else {
+        aa.counters = attn_inmerge_mode(e->attn_merge_mode, nsplit) ? e->attn_counters : nullptr;
+    }
+    aa.head_split = e->attn_head_split;
+    return aa;
+}
+
 // The decode step at a position whose context needs `nsplit` attention
 // splits: the attention grid launches exactly those, and up to 8 splits are
 // merged inside the attention kernel (attn_inmerge_mode).  Where the fused
@@ -202,23 +227,8 @@ static int enqueue_step(llama_engine *e, uint32_t nsplit)
     const char *sn = e->sname;
     for (uint32_t l = 0; l < c.n_layers; l++) {
         const LayerW &w = e->L[l];
-        void *kc = kv_layer(e, l, 0), *vc = kv_layer(e, l, 1);
         GemvArgs qa{w.qkv_c, w.qkv_s, e->x, e->qkv, nullptr, e->norm_attn + (size_t)l * c.dim, qd + 2 * kvd, c.dim, 0, c.eps};
-        AttnArgs aa{};
-        aa.q = e->qkv; aa.kc = kc; aa.vc = vc; aa.out = e->attn_out;
-        aa.part = e->attn_part; aa.pos_ptr = &e->state->pos;
-        aa.cosv = e->cos_tab; aa.sinv = e->sin_tab; aa.k_new = e->qkv + qd; aa.v_new = e->qkv + qd + kvd;
-        aa.ts = hd; aa.hs = (uint64_t)e->max_seq_alloc * hd;
-        aa.n_heads = c.n_heads; aa.n_kv_heads = c.n_kv_heads; aa.head_dim = hd; aa.seq = 0;
-        aa.chunk = e->attn_chunk; aa.max_splits = e->attn_max_splits;
-        aa.err = e->p_err; // every device-side wait (tagged merge, fused q|k|v poll) reports here
-        if (e->attn_tagged && attn_tagged_mode(e->attn_merge_mode, nsplit)) {
-            aa.tagged = e->attn_tagged + (size_t)l * e->attn_tag_layer;
-            aa.tag_splits = e->attn_tag_splits;
-        } else {
-            aa.counters = attn_inmerge_mode(e->attn_merge_mode, nsplit) ? e->attn_counters : nullptr;
-        }
-        aa.head_split = e->attn_head_split;
+        AttnArgs aa = step_attn_args(e, l, nsplit);
         QkvaPlan pl;
         if (qkva_plan(e, nsplit, aa.tagged != nullptr, &pl)) {
             unsigned long long *yt = e->qkv_t + (size_t)l * (qd + 2 * kvd);
@@ -1257,6 +1267,26 @@ int llama_engine_logits(llama_engine *e, float *host_logits)
 }
 
 rfp4_stream_t llama_engine_stream(llama_engine *e) { return e ? (rfp4_stream_t)e->stream : nullptr; }
+
+int rfp4_debug_engine_wait(llama_engine *e, int set_err, uint32_t nsplit, int *err_wired, int *checked, int *fused)
+{
+    if (!e || !err_wired || !checked || !fused) return set_error(RFP4_E_INVALID, "rfp4_debug_engine_wait: null argument");
+    if (nsplit == 0 || nsplit > e->attn_max_splits)
+        return set_error(RFP4_E_INVALID, "rfp4_debug_engine_wait: %u splits (1..%u)", nsplit, e->attn_max_splits);
+    int wired = 1;
+    for (uint32_t l = 0; l < e->c.n_layers; l++) wired &= step_attn_args(e, l, nsplit).err == e->p_err ? 1 : 0;
+    *err_wired = wired;
+    QkvaPlan pl;
+    const AttnArgs a0 = step_attn_args(e, 0, nsplit);
+    *fused = qkva_plan(e, nsplit, a0.tagged != nullptr, &pl) ? 1 : 0;
+    *checked = (e->persist_ok || e->attn_tagged || e->qkva_R) ? 1 : 0;
+    if (set_err) {
+        int rc = fill_words(e->p_err, 1, 1u, e->stream);
+        if (!rc) rc = hip_check(hipStreamSynchronize(e->stream), "hipStreamSynchronize(debug wait)");
+        return rc;
+    }
+    return RFP4_OK;
+}
 
 int llama_engine_use_graph(llama_engine *e, int enable)
 {

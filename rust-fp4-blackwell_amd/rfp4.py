@@ -155,6 +155,7 @@ _SIGS = {
     "llama_engine_prefill_buffers": (I32, [P, C.POINTER(P), C.POINTER(P), C.POINTER(P), C.POINTER(P), C.POINTER(P),
                                            C.POINTER(U32)]),
     "llama_engine_weight_bytes": (U64, [P]),
+    "rfp4_debug_engine_wait": (I32, [P, I32, U32, C.POINTER(I32), C.POINTER(I32), C.POINTER(I32)]),
 }
 
 _lib = None
@@ -730,6 +731,13 @@ class Engine:
         check(load().rfp4_d2h(ka.ctypes.data, k.value, ka.nbytes, self.stream.h))
         check(load().rfp4_d2h(va.ctypes.data, v.value, va.nbytes, self.stream.h))
         return ka, va
+
+    def debug_wait(self, nsplit: int, set_error: bool = False) -> dict:
+        """Test hook: whether the step's device-side waits report to the
+        engine's error word (and, with set_error, set that word)."""
+        w, c, f = I32(0), I32(0), I32(0)
+        check(load().rfp4_debug_engine_wait(self.h, int(set_error), nsplit, C.byref(w), C.byref(c), C.byref(f)))
+        return {"err_wired": bool(w.value), "checked": bool(c.value), "fused": bool(f.value)}
 
     def weight_bytes(self) -> int:
         return int(load().llama_engine_weight_bytes(self.h))

@@ -142,3 +142,34 @@ def test_default_policy_fuses_one_split_steps(rf, cfg):
     assert any(n.startswith("rfp4_qkva") for n in one), one
     assert not any(n.startswith("rfp4_qkva") for n in many), many
     e.close()
+
+
+@pytest.mark.parametrize("cfg", [W64, W128], ids=["hd64", "hd128"])
+def test_device_wait_error_reported_and_cleared(rf, cfg):
+    """Every device-side wait of the step reports to the engine's error word:
+    the fused launch's q|k|v poll at one split (where no tagged merge runs),
+    the tagged merge past 8 splits, and the plain split kernel.  The word is
+    set from the host (no kernel times out): the next read of the tokens
+    fails with RFP4_E_WAIT, also from llama_engine_time_steps, and the next
+    generation starts clean."""
+    RFP4_E_WAIT = -9
+    eng = _engine(rf, cfg, 0x9A12, fused=True, chunk=12)
+    one = eng.debug_wait(1)
+    assert one["fused"] and one["err_wired"] and one["checked"], one
+    for ns in (2, 9, 20):
+        w = eng.debug_wait(ns)
+        assert w["err_wired"] and w["checked"], (ns, w)
+    prompt = [3, 17, 200, 999]
+    ref = eng.generate(prompt, 0, 8)
+    eng.begin(prompt, 0, len(prompt) + 8)
+    eng.run_steps(len(prompt) + 2)
+    eng.debug_wait(1, set_error=True)
+    with pytest.raises(rf.Rfp4Error) as ei:
+        eng.read_ids(len(prompt) + 3)
+    assert ei.value.code == RFP4_E_WAIT
+    with pytest.raises(rf.Rfp4Error) as ei:
+        eng.time_steps(1)
+    assert ei.value.code == RFP4_E_WAIT
+    # a new generation clears the word and reproduces the tokens
+    np.testing.assert_array_equal(eng.generate(prompt, 0, 8), ref)
+    eng.close()
