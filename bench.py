@@ -181,7 +181,8 @@ def gemm_config5(rf, eng, cfg, reps=2, m_list=(32, 512), stack=True):
             gbs = (n * k * 17 // 32 + m * k * 17 // 32 + 4 * m * n) / (ms * 1e-3) / 1e9
             tm, tn, kz = rf.gemm_plan(m, n, k)
             res[name] = {"us": round(ms * 1e3, 2), "TFLOP_s": round(tf, 1), "frac_fp4_peak": round(tf / FP4_PEAK_TFLOPS, 4),
-                         "GB_s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "tile": f"{tm}x{tn}/kz{kz}"}
+                         "GB_s": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "tile": f"{tm}x{tn}/kz{kz}",
+                         "kernel": rf.gemm_plan_kernel(m, n, k)}
         if not stack:
             out[f"m{m}"] = {"shapes": res}
             continue

@@ -272,6 +272,9 @@ int rfp4_debug_prefill_pairing(int mode);
 /* The tile and K split fp4_gemm would use for this shape (honours the test
  * hook).  No reference counterpart. */
 int rfp4_gemm_plan(uint32_t m, uint32_t n, uint32_t k, int *tile_m, int *tile_n, int *kz);
+/* The kernel fp4_gemm would launch for this shape, with its K split
+ * ("<kernel>/kz<splits>"; the few-row kernel's name carries its plan). */
+int rfp4_gemm_plan_kernel(uint32_t m, uint32_t n, uint32_t k, char *buf, size_t cap);
 
 /* ------------------------------------------------------------------ test hooks
  * Raw single-tile MFMA (layout pinning, the role of trackb/fp4_mapping_test.cu

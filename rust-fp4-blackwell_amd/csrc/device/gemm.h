@@ -132,6 +132,27 @@ RFP4_DEV void gemm_splitk_last(const GemmArgs &g, const v16f32 (&acc)[FA][FB], u
         }
 }
 
+// LDS reads in inline asm (see gemm_body's step) and the wait for them.
+RFP4_DEV void gemm_lds_rd16(u32x4 &dst, uint32_t addr) { asm volatile("ds_read_b128 %0, %1" : "=v"(dst) : "v"(addr)); }
+RFP4_DEV void gemm_lds_rd4(uint32_t &dst, uint32_t addr) { asm volatile("ds_read_b32 %0, %1" : "=v"(dst) : "v"(addr)); }
+// Wait until MFMA group t's fragments (and the scales, read first) have
+// returned: at most the 4 (FA + FB) reads per group of groups t + 1 .. 3 may
+// be outstanding (a count above 15 waits for 15).  The values are tied to the
+// wait, so every use is ordered after it.
+template <int FA, int FB>
+RFP4_DEV void gemm_lds_wait_group(uint32_t t, u32x4 (&a)[FA], u32x4 (&b)[FB], uint32_t (&sa)[FA], uint32_t (&sb)[FB])
+{
+    constexpr int G = FA + FB;
+    if (t == 0u) asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(3 * G < 15 ? 3 * G : 15));
+    else if (t == 1u) asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(2 * G < 15 ? 2 * G : 15));
+    else if (t == 2u) asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(G < 15 ? G : 15));
+    else asm volatile("s_waitcnt lgkmcnt(0)");
+#pragma unroll
+    for (int i = 0; i < FA; i++) asm volatile("" : "+v"(a[i]), "+v"(sa[i]));
+#pragma unroll
+    for (int i = 0; i < FB; i++) asm volatile("" : "+v"(b[i]), "+v"(sb[i]));
+}
+
 template <int WM, int WN, int FA, int FB, int NST = 2>
 RFP4_DEV void gemm_body(const GemmArgs &g)
 {
@@ -245,28 +266,34 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
         constexpr bool FULL = decltype(full_c)::value;
         const uint32_t cur = (s - s0) % (uint32_t)NST;
         const rfp4_lds_u8 *st = lds + cur * STAGE;
-        // all operands of the step into registers first, then the next step's DMA, then the MFMAs
+        // all operands of the step into registers first (scales, then MFMA t's
+        // fragments for t = 0..3), then the next step's DMA, then the MFMAs.
+        // The reads are inline asm: the compiler treats every LDS read after an
+        // LDS DMA as a possible alias of it and would wait for every DMA in
+        // flight (vmcnt(0)) before the first read, so the steps of lookahead
+        // of the deeper rings would be waited for one step later anyway.  The
+        // stage read here is complete (the wait and barrier before this
+        // step); each MFMA group waits for its own reads (LDS reads return in
+        // order) with the fragments tied to the wait.
+        const uint32_t stb = (uint32_t)(uintptr_t)st;
         u32x4 av[4][FA], bv[4][FB];
         uint32_t sa[FA], sb[FB];
 #pragma unroll
-        for (int fa = 0; fa < FA; fa++) {
-            sa[fa] = *(const __attribute__((address_space(3))) uint32_t *)(st + asc[fa]);
+        for (int fa = 0; fa < FA; fa++) gemm_lds_rd4(sa[fa], stb + asc[fa]);
 #pragma unroll
-            for (uint32_t t = 0; t < 4; t++)
-                av[t][fa] = *(const __attribute__((address_space(3))) u32x4 *)(st + aoff[fa] +
-                                                                                (((4u * h + t) ^ asw[fa]) << 4));
-        }
+        for (int fb = 0; fb < FB; fb++) gemm_lds_rd4(sb[fb], stb + bsc[fb]);
 #pragma unroll
-        for (int fb = 0; fb < FB; fb++) {
-            sb[fb] = *(const __attribute__((address_space(3))) uint32_t *)(st + bsc[fb]);
+        for (uint32_t t = 0; t < 4; t++) {
 #pragma unroll
-            for (uint32_t t = 0; t < 4; t++)
-                bv[t][fb] = *(const __attribute__((address_space(3))) u32x4 *)(st + boff[fb] +
-                                                                                (((4u * h + t) ^ bsw[fb]) << 4));
+            for (int fa = 0; fa < FA; fa++) gemm_lds_rd16(av[t][fa], stb + aoff[fa] + (((4u * h + t) ^ asw[fa]) << 4));
+#pragma unroll
+            for (int fb = 0; fb < FB; fb++) gemm_lds_rd16(bv[t][fb], stb + boff[fb] + (((4u * h + t) ^ bsw[fb]) << 4));
         }
         if (FULL || s + (uint32_t)NST - 1u < s1) RFP4_GEMM_DMA(s + (uint32_t)NST - 1u, (cur + (uint32_t)NST - 1u) % (uint32_t)NST);
 #pragma unroll
         for (uint32_t t = 0; t < 4; t++) {
+            // at most the reads of MFMA groups t + 1 .. 3 outstanding (lgkmcnt saturates at 15)
+            gemm_lds_wait_group<FA, FB>(t, av[t], bv[t], sa, sb);
 #pragma unroll
             for (int fa = 0; fa < FA; fa++) {
                 const v8i32 a8 = {(int)av[t][fa].x, (int)av[t][fa].y, (int)av[t][fa].z, (int)av[t][fa].w, 0, 0, 0, 0};

@@ -1107,6 +1107,7 @@ struct GemmPlan {
     int nst = 2;        // tiled plans: DMA stages of the K pipeline (kernels.hip GEMM_KERNEL_P above 2)
 };
 
+
 // The deepest K pipeline compiled for a tile (kernels.hip GEMM_KERNEL_P): 4
 // stages for 32x128 and 64x128, 3 for 128x128 and 256x128, else double
 // buffering.
@@ -1375,11 +1376,32 @@ int rfp4_gemm_plan(uint32_t m, uint32_t n, uint32_t k, int *tile_m, int *tile_n,
     const uint32_t cus = rt ? (uint32_t)rt->num_cus : 256u;
     if (k == 0 || k % 256u || m == 0 || n == 0) return set_error(RFP4_E_SHAPE, "gemm_plan: bad shape");
     GemmPlan p = gemm_plan(m, n, k, cus);
-    if (tile_m) *tile_m = p.tile == kGemmSkinny ? 16 * p.ma : (int)kGemmTiles[p.tile].bm;
-    if (tile_n) *tile_n = p.tile == kGemmSkinny ? 16 * (int)p.kz : (int)kGemmTiles[p.tile].bn;
+    const GemmTile *t = p.tile == kGemmSkinny ? nullptr : &kGemmTiles[p.tile];
+    if (tile_m) *tile_m = t ? (int)t->bm : 16 * p.ma;
+    if (tile_n) *tile_n = t ? (int)t->bn : 16 * (int)p.kz;
     if (kz) *kz = (int)p.kz;
     return RFP4_OK;
 }
+
+int rfp4_gemm_plan_kernel(uint32_t m, uint32_t n, uint32_t k, char *buf, size_t cap)
+{
+    Runtime *rt = g_rt;
+    const uint32_t cus = rt ? (uint32_t)rt->num_cus : 256u;
+    if (!buf || cap == 0) return set_error(RFP4_E_INVALID, "gemm_plan_kernel: null buffer");
+    if (k == 0 || k % 256u || m == 0 || n == 0) return set_error(RFP4_E_SHAPE, "gemm_plan_kernel: bad shape");
+    GemmPlan p = gemm_plan(m, n, k, cus);
+    char name[64];
+    if (p.tile == kGemmSkinny)
+        snprintf(name, sizeof name, "rfp4_gemm_rows_m%d_s%d_f%u", 16 * p.ma, p.nb, p.kz);
+    else if (p.nst >= 3)
+        snprintf(name, sizeof name, "%s_p%d/kz%u", kGemmTiles[p.tile].name, p.nst, p.kz);
+    else
+        snprintf(name, sizeof name, "%s/kz%u", kGemmTiles[p.tile].name, p.kz);
+    if (strlen(name) + 1 > cap) return set_error(RFP4_E_CAPACITY, "gemm_plan_kernel: %zu bytes needed", strlen(name) + 1);
+    memcpy(buf, name, strlen(name) + 1);
+    return RFP4_OK;
+}
+
 
 int rfp4_mma_tile16(rfp4_stream_t stream, const uint32_t *a, const uint32_t *b, const uint32_t *sa,
                     const uint32_t *sb, float *out)

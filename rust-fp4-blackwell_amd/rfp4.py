@@ -103,6 +103,7 @@ _SIGS = {
     "rfp4_debug_gemm_plan": (I32, [I32, I32]),
     "rfp4_debug_attn_chunk": (I32, [U32]),
     "rfp4_gemm_plan": (I32, [U32, U32, U32, P, P, P]),
+    "rfp4_gemm_plan_kernel": (I32, [U32, U32, U32, C.c_char_p, SZ]),
     "rfp4_mma_tile16": (I32, [P, P, P, P, P, P]),
     "rfp4_mma_tile32": (I32, [P, P, P, P, P, P]),
     "rfp4_selftest_cvt_fp4": (I32, [P, U32, P, P]),
@@ -472,6 +473,13 @@ def gemm_plan(m, n, k):
     tm, tn, kz = C.c_int(), C.c_int(), C.c_int()
     check(load().rfp4_gemm_plan(m, n, k, C.byref(tm), C.byref(tn), C.byref(kz)))
     return tm.value, tn.value, kz.value
+
+
+def gemm_plan_kernel(m, n, k) -> str:
+    """The kernel (and K split) fp4_gemm launches for this shape."""
+    buf = C.create_string_buffer(96)
+    check(load().rfp4_gemm_plan_kernel(m, n, k, buf, 96))
+    return buf.value.decode()
 
 
 def mma_tile16(stream, a, b, sa, sb, out):
