@@ -123,6 +123,47 @@ RFP4_DEV void stage_x_regs(float *xs, const float4 *xr, const uint2 *wr, uint32_
     __syncthreads();
 }
 
+// x (and the fp16 norm weights) for stage_x_regs, XV float4 per thread of T
+// (element 4*(tid + T*v) + j).  issue() sends the loads with no per-element
+// branch (the index clamped into range; the norm weights behind one uniform
+// branch), so nothing separates them from the caller's weight loads that
+// follow; settle(), after those are issued, zeroes what lies past K through a
+// mask the compiler cannot see through (else it turns the selects back into
+// branches around the loads).  Measured on the 8B gate|up GEMV with its fused
+// norm: 13.7-13.9 -> 13.3-13.4 us per launch, values unchanged.
+template <int XV, uint32_t T>
+struct XRegs {
+    float4 xr[XV];
+    uint2 wr[XV];
+
+    RFP4_DEV void issue(const float *x, const uint16_t *norm_w, uint32_t k)
+    {
+        const uint32_t k4 = k >> 2;
+#pragma unroll
+        for (int v = 0; v < XV; v++) xr[v] = ((const float4 *)x)[min(threadIdx.x + T * (uint32_t)v, k4 - 1u)];
+        if (norm_w) {
+#pragma unroll
+            for (int v = 0; v < XV; v++) wr[v] = ((const uint2 *)norm_w)[min(threadIdx.x + T * (uint32_t)v, k4 - 1u)];
+        } else {
+#pragma unroll
+            for (int v = 0; v < XV; v++) wr[v] = make_uint2(0, 0);
+        }
+    }
+
+    RFP4_DEV void settle(uint32_t k)
+    {
+        const uint32_t k4 = k >> 2;
+#pragma unroll
+        for (int v = 0; v < XV; v++) {
+            uint32_t m = threadIdx.x + T * (uint32_t)v < k4 ? 0xFFFFFFFFu : 0u;
+            asm volatile("" : "+v"(m));
+            xr[v] = make_float4(__uint_as_float(__float_as_uint(xr[v].x) & m), __uint_as_float(__float_as_uint(xr[v].y) & m),
+                                __uint_as_float(__float_as_uint(xr[v].z) & m), __uint_as_float(__float_as_uint(xr[v].w) & m));
+            wr[v] = make_uint2(wr[v].x & m, wr[v].y & m);
+        }
+    }
+};
+
 // Raw scale bits now, value at use: keeps the loads free of dependent ALU
 // work so they can all be in flight together.
 template <int SCALE_F32>
@@ -193,16 +234,9 @@ RFP4_DEV void gemv_body(const GemvArgs &a)
         // for the weights (vmcnt retires in issue order).  A lane past the
         // last chunk re-reads the last chunk (in bounds) and gets scale 0.
         constexpr int XV = NS > 0 ? (512 * NS + (int)T - 1) / (int)T : 1; // float4 of x per thread: K <= 2048 * NS
-        float4 xr[XV];
-        uint2 wr[XV];
-        const bool norm = a.norm_w != nullptr;
-#pragma unroll
-        for (int v = 0; v < XV; v++) {
-            const uint32_t i4 = threadIdx.x + T * (uint32_t)v;
-            const bool in = i4 < (a.k >> 2);
-            xr[v] = in ? ((const float4 *)a.x)[i4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            wr[v] = (in && norm) ? ((const uint2 *)a.norm_w)[i4] : make_uint2(0, 0);
-        }
+        XRegs<XV, T> xg;
+        xg.issue(a.x, a.norm_w, a.k);
+        __builtin_amdgcn_sched_barrier(0); // x before the weight stream
         uint4 q[NS > 0 ? NS : 1][NP];
         uint32_t sb[NS > 0 ? NS : 1][NP];
 #pragma unroll
@@ -214,7 +248,8 @@ RFP4_DEV void gemv_body(const GemvArgs &a)
                 sb[s][p] = load_scale_bits<SCALE_F32>(a.scales, srow[p] + cl);
             }
         }
-        stage_x_regs<XV, W>(xs, xr, wr, a.k, norm, a.eps);
+        xg.settle(a.k);
+        stage_x_regs<XV, W>(xs, xg.xr, xg.wr, a.k, a.norm_w != nullptr, a.eps);
 #pragma unroll
         for (int s = 0; s < NS; s++) {
             const uint32_t c = (uint32_t)lane + 64u * (uint32_t)s;

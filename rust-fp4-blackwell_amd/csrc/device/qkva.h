@@ -84,8 +84,7 @@ RFP4_DEV void stage_x_regs_w8(float *xs, const float4 *xr, const uint2 *wr, uint
 template <int NS, int R, int WREF>
 struct QkvTile {
     static constexpr int XV = 2 * NS; // float4 of x per thread (256 threads)
-    float4 xr[XV];
-    uint2 wr[XV];
+    XRegs<XV, 256u> xg;
     uint4 q[NS][R];
     uint32_t sb[NS][R];
     uint32_t lrow0;
@@ -96,14 +95,8 @@ struct QkvTile {
         lrow0 = (tile * 4u + (uint32_t)wave) * (uint32_t)R;
         const uint32_t nchunk = a.k >> 5, clast = nchunk - 1u;
         const size_t rowbytes = (size_t)(a.k >> 1);
-        const bool norm = a.norm_w != nullptr;
-#pragma unroll
-        for (int v = 0; v < XV; v++) {
-            const uint32_t i4 = threadIdx.x + 256u * (uint32_t)v;
-            const bool in = i4 < (a.k >> 2);
-            xr[v] = in ? ((const float4 *)a.x)[i4] : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            wr[v] = (in && norm) ? ((const uint2 *)a.norm_w)[i4] : make_uint2(0, 0);
-        }
+        xg.issue(a.x, a.norm_w, a.k);
+        __builtin_amdgcn_sched_barrier(0); // x before the weight stream
 #pragma unroll
         for (int s = 0; s < NS; s++) {
             const uint32_t cl = min((uint32_t)lane + 64u * (uint32_t)s, clast);
@@ -122,10 +115,11 @@ struct QkvTile {
         extern __shared__ float xs[];
         const int lane = threadIdx.x & 63;
         const uint32_t nchunk = a.k >> 5, clast = nchunk - 1u;
+        xg.settle(a.k);
         if (WREF == 8)
-            stage_x_regs_w8<XV>(xs, xr, wr, a.k, a.norm_w != nullptr, a.eps);
+            stage_x_regs_w8<XV>(xs, xg.xr, xg.wr, a.k, a.norm_w != nullptr, a.eps);
         else
-            stage_x_regs<XV, 4>(xs, xr, wr, a.k, a.norm_w != nullptr, a.eps);
+            stage_x_regs<XV, 4>(xs, xg.xr, xg.wr, a.k, a.norm_w != nullptr, a.eps);
         float acc[R];
 #pragma unroll
         for (int p = 0; p < R; p++) acc[p] = 0.0f;
