@@ -52,6 +52,7 @@ class ModelConfig(C.Structure):
 
 
 SCALE_E8M0, SCALE_F32 = 0, 1   # RFP4_SCALE_*
+EPI_STORE, EPI_RESIDUAL, EPI_SWIGLU, EPI_ARGMAX = 0, 1, 2, 3  # epilogues of rfp4_debug_gemv_fused
 KV_F16, KV_F32 = 0, 1           # RFP4_KV_*
 
 

@@ -111,3 +111,33 @@ def test_llama_run_contract_matches_oracle(rf, orc, tmp_path):
     p, out = _parse(r.stdout)
     assert p == prompt and out == want
     ref.close()
+
+
+LLAMA_RUN_ASAN = os.path.join(PKG, "llama_run_asan")
+
+
+@pytest.mark.gpu
+def test_llama_run_graph_replays_under_host_asan(tmp_path):
+    """The engine's host code under AddressSanitizer + UBSan (llama_run_asan
+    over librfp4_asan.so; the gfx950 code object is the same): synthetic
+    TinyLlama weights, the prompt, then greedy steps replayed as step graphs
+    (capture, instantiation, replays with the device cursor, engine and
+    runtime teardown through rfp4_shutdown).  No sanitizer report, and the
+    tokens equal the plain build's."""
+    if not os.path.exists(LLAMA_RUN_ASAN):
+        pytest.skip("sanitizer build not present (make -C rust-fp4-blackwell_amd llama_run_asan)")
+    base = dict(os.environ, RFP4_SEED="7", RFP4_MAX_NEW="48", RFP4_EOS="100000")
+    # the harness may preload a library ahead of the ASan runtime; leaks of the
+    # HIP runtime at exit are not this library's
+    san = dict(base, ASAN_OPTIONS="verify_asan_link_order=0:detect_leaks=0:abort_on_error=0",
+               UBSAN_OPTIONS="halt_on_error=1:print_stacktrace=1")
+    prompt = ["1", "15043", "2787"]
+    print("llama_run (plain) TinyLlama synthetic", flush=True)
+    r0 = subprocess.run([LLAMA_RUN] + prompt, capture_output=True, text=True, env=base, timeout=300)
+    assert r0.returncode == 0, r0.stderr
+    print("llama_run_asan TinyLlama synthetic", flush=True)
+    r1 = subprocess.run([LLAMA_RUN_ASAN] + prompt, capture_output=True, text=True, env=san, timeout=300)
+    assert "AddressSanitizer" not in r1.stderr and "runtime error" not in r1.stderr, r1.stderr[-4000:]
+    assert r1.returncode == 0, r1.stderr[-4000:]
+    assert _parse(r1.stdout) == _parse(r0.stdout)
+    assert len(_parse(r0.stdout)[1]) == 48
