@@ -157,29 +157,34 @@ def gemm_config5(rf, eng, cfg, reps=2, m_list=(32, 512), stack=True):
     for k in sorted({cfg.dim, qd, cfg.ffn}):
         a16 = rf.DeviceBuffer.from_host(_bf16_normal(rng, 512, k), s)
         ac, asc = rf.DeviceBuffer(512 * k // 2), rf.DeviceBuffer(512 * k // 32)
-        rf.mx4_quantize(s, 512, k, a16, True, ac, asc)
-        acts[k] = (a16, ac, asc)
+        ast = rf.DeviceBuffer(rf.mx4_scales_tiled_bytes(512, k))
+        rf.mx4_quantize_tiled(s, 512, k, a16, True, ac, asc, ast)
+        acts[k] = (a16, ac, asc, ast)
     c = rf.DeviceBuffer(512 * max(cfg.vocab, 2 * cfg.ffn) * 4)
     L = cfg.n_layers
-    w = {p: [eng.weight(l, p)[:2] for l in range(L)] for p in (0, 3, 4, 6)}
-    lm = eng.weight(-1, 0)[:2]
+    # weight views (codes, row-major scales, step-blocked scales) of projection p of every layer
+    wv = lambda l, p: (*eng.weight(l, p)[:2], eng.weight_scales_tiled(l, p)[0])
+    w = {p: [wv(l, p) for l in range(L)] for p in (0, 1, 3, 4, 6)}
+    lm = wv(-1, 0)
     # config-5 shapes: (name, N, K, weight views rotating over layers)
     shapes = [
         ("4096x4096", cfg.dim, qd, w[3]),
-        ("1024x4096", kvd, cfg.dim, [(wc + qd * cfg.dim // 2, ws + qd * cfg.dim // 32) for wc, ws in w[0]]),
+        ("1024x4096", kvd, cfg.dim, w[1]),
         ("14336x4096", cfg.ffn, cfg.dim, w[4]),
         ("4096x14336", cfg.dim, cfg.ffn, w[6]),
         ("128256x4096", cfg.vocab, cfg.dim, [lm]),
     ]
+    # the stack's q|k|v and gate|up are the stacked matrices: views of projections 0 and 4 widened
     layers = [(qd + 2 * kvd, cfg.dim, w[0]), (cfg.dim, qd, w[3]), (2 * cfg.ffn, cfg.dim, w[4]),
               (cfg.dim, cfg.ffn, w[6])]
+    gemm = lambda m, n, k, a, wc, ws, wst: rf.fp4_gemm_tiled(s, m, n, k, a[1], a[2], a[3], wc, ws, wst, c)
     out = {}
     for m in m_list:
         res = {}
         for name, n, k, views in shapes:
-            _, ac, asc = acts[k]
+            a = acts[k]
             nl = len(views)
-            calls = [lambda wc=wc, ws=ws: rf.fp4_gemm(s, m, n, k, ac, asc, wc, ws, c) for wc, ws in views]
+            calls = [lambda wc=wc, ws=ws, wst=wst: gemm(m, n, k, a, wc, ws, wst) for wc, ws, wst in views]
             if reps == 0:
                 with ROCTX.range(f"gemm_m{m}_{name}"):
                     calls[0]()
@@ -198,29 +203,36 @@ def gemm_config5(rf, eng, cfg, reps=2, m_list=(32, 512), stack=True):
             out[f"m{m}"] = {"shapes": res}
             continue
         flops = 0.0
-        calls = []
+        calls, dropin = [], []
         for l in range(L):
             for n, k, views in layers:
-                _, ac, asc = acts[k]
-                wc, ws = views[l]
-                calls.append(lambda n=n, k=k, ac=ac, asc=asc, wc=wc, ws=ws: rf.fp4_gemm(s, m, n, k, ac, asc, wc, ws, c))
+                a = acts[k]
+                wc, ws, wst = views[l]
+                calls.append(lambda n=n, k=k, a=a, wc=wc, ws=ws, wst=wst: gemm(m, n, k, a, wc, ws, wst))
+                dropin.append(lambda n=n, k=k, a=a, wc=wc, ws=ws: rf.fp4_gemm(s, m, n, k, a[1], a[2], wc, ws, c))
                 flops += 2.0 * m * n * k
-        calls.append(lambda: rf.fp4_gemm(s, m, cfg.vocab, cfg.dim, acts[cfg.dim][1], acts[cfg.dim][2], lm[0], lm[1], c))
+        calls.append(lambda: gemm(m, cfg.vocab, cfg.dim, acts[cfg.dim], *lm))
+        dropin.append(lambda: rf.fp4_gemm(s, m, cfg.vocab, cfg.dim, acts[cfg.dim][1], acts[cfg.dim][2], lm[0], lm[1], c))
         flops += 2.0 * m * cfg.vocab * cfg.dim
         ms = time_launches(rf, s, lambda: [f() for f in calls], reps)
         tf = flops / (ms * 1e-3) / 1e12
+        # the drop-in fp4_gemm (row-major scales only: the tiled kernels' step-blocked copies made per call)
+        ms_dropin = time_launches(rf, s, lambda: [f() for f in dropin], reps) if m > 32 else ms
         qms = time_launches(rf, s, lambda: rf.mx4_quantize(s, m, cfg.dim, acts[cfg.dim][0], True, acts[cfg.dim][1],
                                                            acts[cfg.dim][2]), 20)
         out[f"m{m}"] = {"stack_us": round(ms * 1e3, 1), "stack_TFLOP": round(flops / 1e12, 4),
                         "stack_TFLOP_s": round(tf, 1), "stack_frac_fp4_peak": round(tf / FP4_PEAK_TFLOPS, 4),
+                        "stack_us_dropin_fp4_gemm": round(ms_dropin * 1e3, 1),
                         "quantize_us_k4096": round(qms * 1e3, 2), "shapes": res}
         log(f"gemm M={m}: stack {ms * 1e3:.0f} us, {tf:.0f} TFLOP/s ({100 * tf / FP4_PEAK_TFLOPS:.1f}% of FP4 peak); "
             + ", ".join(f"{k} {v['us']}us {v['TFLOP_s']}TF" for k, v in res.items()))
-    for a16, ac, asc in acts.values():
-        a16.free(), ac.free(), asc.free()
+    for a16, ac, asc, ast in acts.values():
+        a16.free(), ac.free(), asc.free(), ast.free()
     c.free()
     out["workload"] = ("Llama-3-8B projections as MXFP4 GEMMs, bf16 activations ~N(0,1) quantized to MXFP4 per 32 "
-                       "along K; stack = 32 layers x (qkv, o, gate+up, down) + LM head")
+                       "along K; stack = 32 layers x (qkv, o, gate+up, down) + LM head; fp4_gemm_tiled with the "
+                       "engine's step-blocked weight scales (stack_us_dropin_fp4_gemm: fp4_gemm, which makes them "
+                       "per call)")
     out["peak_TFLOP_s"] = FP4_PEAK_TFLOPS
     return out
 

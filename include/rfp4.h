@@ -205,9 +205,40 @@ int mx4_quantize(rfp4_stream_t stream, uint64_t rows, uint64_t k, const void *sr
  * single m16n8k64 block-scaled tile (fp4_mma/src/main.rs:18-54) and its CPU
  * closed form D = sum_k A SFA B SFB (trackb/fp4_scale_test.cu:37); this is
  * that contraction at M x N x K.  Split-K shapes use a library workspace:
- * calls that overlap on one device race. */
+ * calls that overlap on one device race.  The tiled kernels (more than 32
+ * activation rows) read the scales in a step-blocked layout (below), which
+ * this entry point makes first in a library workspace of 64 MiB (one more
+ * launch; shapes whose copies exceed it fail with RFP4_E_CAPACITY: use
+ * fp4_gemm_tiled). */
 int fp4_gemm(rfp4_stream_t stream, uint32_t m, uint32_t n, uint32_t k, const uint8_t *a_codes,
              const uint8_t *a_scales, const uint8_t *w_codes, const uint8_t *w_scales, float *c);
+/* Step-blocked copy of [rows][k/32] E8M0 scales (k % 256 == 0): for each
+ * 32-row block and each K step of 256 values, 256 contiguous bytes holding,
+ * for h = 0, 1 and rows r = 0..31, the step's scale bytes 4h .. 4h + 3 of the
+ * block's row r; ceil(rows/32) blocks, rows past `rows` zero.  It is the
+ * tiled GEMM's LDS layout, so each K step of a 32-row block is one 256-byte
+ * copy instead of 32 row-strided 8-byte pieces.  No reference counterpart
+ * (the reference has no GEMM, main.tex:228).  mx4_scales_tiled_bytes: its
+ * size; mx4_scales_tile: makes it on the device (both pointers 4-byte
+ * aligned). */
+size_t mx4_scales_tiled_bytes(uint32_t rows, uint32_t k);
+int mx4_scales_tile(rfp4_stream_t stream, uint32_t rows, uint32_t k, const uint8_t *scales, uint8_t *scales_tiled);
+/* mx4_quantize that also writes the step-blocked copy of the scales
+ * (k % 256 == 0; the bytes of its rows only: the padding rows of a last
+ * partial block are left as they are, which the GEMM never reads into an
+ * output it stores).  No reference counterpart. */
+int mx4_quantize_tiled(rfp4_stream_t stream, uint64_t rows, uint64_t k, const void *src, int src_is_bf16,
+                       uint8_t *codes, uint8_t *scales, uint8_t *scales_tiled);
+/* fp4_gemm with the operands' step-blocked scales supplied as well (made by
+ * mx4_scales_tile or mx4_quantize_tiled, or an engine's, see
+ * llama_engine_weight_scales_tiled): no copy is made, so the call adds no
+ * launch and has no workspace limit beyond fp4_gemm's split-K one.  The
+ * few-row kernel (m <= 32) reads the row-major scales, the tiled kernels the
+ * step-blocked ones; both must describe the same scales.  Same results as
+ * fp4_gemm, bit for bit.  No reference counterpart (see fp4_gemm). */
+int fp4_gemm_tiled(rfp4_stream_t stream, uint32_t m, uint32_t n, uint32_t k, const uint8_t *a_codes,
+                   const uint8_t *a_scales, const uint8_t *a_scales_tiled, const uint8_t *w_codes,
+                   const uint8_t *w_scales, const uint8_t *w_scales_tiled, float *c);
 /* Test hook: force the GEMM tile (index into the compiled list, largest
  * first: 256x256, 256x128, 128x128, 64x128, 32x128, then 5 = the few-row
  * kernel for k a multiple of 512, up to 16384 for m <= 32 and up to 8192
@@ -439,6 +470,12 @@ int llama_engine_persistent(const llama_engine *e);
 /* Device views for parity tests.  proj: 0..6 = q,k,v,o,gate,up,down; layer -1 = LM head. */
 int llama_engine_weight(llama_engine *e, int layer, int proj, const uint8_t **codes, const uint8_t **scales,
                         size_t *code_bytes, size_t *scale_bytes);
+/* The step-blocked copy of the same weight's scales (mx4_scales_tile's
+ * layout), which engines that can prefill hold for the tiled GEMM
+ * (fp4_gemm_tiled); RFP4_E_SHAPE for other engines.  No reference
+ * counterpart. */
+int llama_engine_weight_scales_tiled(llama_engine *e, int layer, int proj, const uint8_t **scales_tiled,
+                                     size_t *bytes);
 /* K/V caches of a layer, [kv_head][cache positions][head_dim] elements of the
  * engine's kv_format (fp16 bits or f32); count = elements per cache. */
 int llama_engine_kv(llama_engine *e, int layer, const void **k, const void **v, size_t *count);

@@ -18,7 +18,14 @@
 // Workgroup: 4 waves in a WM x WN grid, wave tile (32 FA) x (32 FB), block
 // tile BM x BN.  Each K step (BM + BN rows of 128 code bytes and 8 scale
 // bytes) is copied global -> LDS by the DMA path (global_load_lds, no
-// staging registers) into a ring of NST stage buffers: a wave reads all its
+// staging registers) into a ring of NST stage buffers.  The scales come from
+// the step-blocked copies (GemmArgs::a_st, w_st): a 32-row block's 8 bytes
+// per row of one step are 256 contiguous bytes, copied as they are into the
+// stage's two 32-word planes.  From the row-major [rows][k/32] scales each
+// step would touch one cache line per row for 8 bytes, as many L2 requests as
+// the code bytes need (measured on the DMA stream alone, M = 512: 64x128
+// tiles 7.8 us without scales, 12.3 us with row-major scales, 8.4 us with
+// step-blocked ones).  A wave reads all its
 // operands of step s from LDS, issues the DMA of step s + NST - 1 into the
 // buffer step s - 1 used, then runs the step's MFMAs while the copies are in
 // flight; one barrier per step.  NST = 2 (double buffering) waits for all of
@@ -175,17 +182,16 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
     const uint32_t lg = (L < q * 8u) ? (L & 7u) * q + (L >> 3) : L;
     const uint32_t mt_n = (g.m + BM - 1u) / BM, nt_n = (g.n + BN - 1u) / BN;
     const uint32_t mt = lg % mt_n, rest = lg / mt_n, nt = rest % nt_n, z = rest / nt_n;
-    const uint32_t kbytes = g.k >> 1, nblk = g.k >> 5, nsuper = g.k >> 8;
+    const uint32_t kbytes = g.k >> 1, nsuper = g.k >> 8;
     const uint32_t per = (nsuper + g.kz - 1u) / g.kz;
     const uint32_t s0 = min(nsuper, z * per), s1 = min(nsuper, s0 + per);
 
     // ---- DMA sources.  Code block j of this wave covers tile rows 8 (wave + 4 j) .. +7; lane l
     // fetches logical chunk (l & 7) ^ swz(row) of row 8 (wave + 4 j) + l / 8, which the DMA writes
-    // to physical chunk l & 7.  Scale block b of this wave covers rows 32 (wave + 4 b) .. +31; lane l
-    // fetches bytes 4 (l / 32) .. +3 of row 32 (wave + 4 b) + l % 32, so a block is stored as two
-    // planes of 32 words (the step's scale bytes 0-3, then 4-7, of each row): the 32 lanes of one
-    // half-wave read 32 consecutive words, free of bank conflicts (row-major 8-byte rows put
-    // rows r and r + 16 on one bank).
+    // to physical chunk l & 7.  A stage holds each 32-row scale block as two planes of 32 words (the
+    // step's scale bytes 0-3, then 4-7, of each row; the step-blocked layout as it is): the 32 lanes
+    // of one half-wave read 32 consecutive words, free of bank conflicts (row-major 8-byte rows
+    // would put rows r and r + 16 on one bank).
     const uint8_t *src[NJ];
 #pragma unroll
     for (uint32_t j = 0; j < NJ; j++) {
@@ -194,13 +200,17 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
         if (row < BM) src[j] = g.a_codes + (size_t)min(mt * BM + row, g.m - 1u) * kbytes + qq * 16u;
         else src[j] = g.w_codes + (size_t)min(nt * BN + (row - BM), g.n - 1u) * kbytes + qq * 16u;
     }
+    // Scale block b of this wave covers tile rows 32 (wave + 4 b) .. +31: the
+    // step-blocked block of those rows (clamped to the last block, so that
+    // every copy stays in bounds), lane l's word at byte 4 l of the step
     const uint8_t *ssrc[NSB];
 #pragma unroll
     for (uint32_t b = 0; b < NSB; b++) {
-        const uint32_t row = min(32u * (wave + 4u * b) + (lane & 31u), R - 1u);
-        const uint8_t *base = row < BM ? g.a_scales + (size_t)min(mt * BM + row, g.m - 1u) * nblk
-                                       : g.w_scales + (size_t)min(nt * BN + (row - BM), g.n - 1u) * nblk;
-        ssrc[b] = base + (lane >> 5) * 4u;
+        const uint32_t tb = min(wave + 4u * b, R / 32u - 1u);
+        const uint8_t *base = tb < BM / 32u
+                                  ? g.a_st + (size_t)min(mt * (BM / 32u) + tb, (g.m - 1u) >> 5) * nsuper * 256u
+                                  : g.w_st + (size_t)min(nt * (BN / 32u) + (tb - BM / 32u), (g.n - 1u) >> 5) * nsuper * 256u;
+        ssrc[b] = base + lane * 4u;
     }
 #define RFP4_GEMM_DMA(S, BUF)                                                                              \
     do {                                                                                                   \
@@ -210,7 +220,7 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
         _Pragma("unroll") for (uint32_t b = 0; b < NSB; b++) {                                             \
             const uint32_t bb = (NST > 2 && wave + 4u * b >= R / 32u) ? 0u : b; /* uniform count: again block 0 */ \
             if (NST > 2 || wave + 4u * b < R / 32u)                                                        \
-                __builtin_amdgcn_global_load_lds((rfp4_glb_void *)(ssrc[bb] + (size_t)(S) * 8u),           \
+                __builtin_amdgcn_global_load_lds((rfp4_glb_void *)(ssrc[bb] + (size_t)(S) * 256u),           \
                                                  st_ + SC0 + 256u * (wave + 4u * bb), 4, 0, 0);            \
         }                                                                                                  \
     } while (0)
@@ -377,5 +387,27 @@ RFP4_DEV void gemm_reduce_body(const GemmArgs &g)
             sum.w = __fadd_rn(sum.w, p.w);
         }
         ((float4 *)g.c)[e] = sum;
+    }
+}
+
+// Row-major E8M0 scales -> the step-blocked layout (GemmArgs::a_st): one
+// thread per output word, matrix 0's words first; word l of (row block rb,
+// step s) is bytes 8 s + 4 (l / 32) .. +3 of row 32 rb + l % 32 (zero past
+// the last row).
+RFP4_DEV void scales_tile_body(const ScaleTileArgs &a)
+{
+    const uint32_t nsuper = a.k >> 8, nblk = a.k >> 5;
+    const uint64_t w0 = (uint64_t)((a.rows[0] + 31u) >> 5) * nsuper * 64u;
+    const uint64_t words = w0 + (uint64_t)((a.rows[1] + 31u) >> 5) * nsuper * 64u;
+    for (uint64_t t = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; t < words; t += (uint64_t)gridDim.x * blockDim.x) {
+        const uint32_t mtx = t < w0 ? 0u : 1u;
+        const uint64_t w = t - (mtx ? w0 : 0u);
+        const uint32_t l = (uint32_t)(w & 63u);
+        const uint64_t bs = w >> 6;
+        const uint32_t st = (uint32_t)(bs % nsuper), rb = (uint32_t)(bs / nsuper);
+        const uint32_t row = 32u * rb + (l & 31u);
+        uint32_t v = 0u;
+        if (row < a.rows[mtx]) v = *(const uint32_t *)(a.src[mtx] + (size_t)row * nblk + 8u * st + 4u * (l >> 5));
+        ((uint32_t *)a.dst[mtx])[w] = v;
     }
 }

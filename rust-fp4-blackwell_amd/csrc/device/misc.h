@@ -157,12 +157,22 @@ RFP4_DEV uint32_t quant_block32(const float *v, uint8_t *out16)
     return sbyte;
 }
 
+// Byte offset of scale block `blk` (32 values along K) of row `row` in the
+// step-blocked layout the tiled GEMM reads (GemmArgs::a_st): per 32-row block
+// and K step of 256 values, 256 bytes holding, for h = 0, 1 and rows
+// r = 0..31, the step's blocks 4h .. 4h + 3 of row r.
+RFP4_DEV size_t mx_st_offset(uint32_t row, uint32_t blk, uint32_t nsuper)
+{
+    return ((size_t)(row >> 5) * nsuper + (blk >> 3)) * 256u + 128u * ((blk >> 2) & 1u) + 4u * (row & 31u) + (blk & 3u);
+}
+
 // quant_block32 spread over 8 consecutive lanes: lane part p = lane & 7 holds
 // values 4p .. 4p+3 of the block in v, and every lane of the group is active.
 // Same shared exponent (the maximum does not depend on the order) and the
-// same element arithmetic; part 0 writes the scale byte, even parts one
+// same element arithmetic; part 0 writes the scale byte (and, where scale_t
+// is not null, the same byte there: the step-blocked copy), even parts one
 // 32-bit word of the 16 code bytes each.
-RFP4_DEV void quant_block32_x8(float4 v, uint8_t *codes16, uint8_t *scale)
+RFP4_DEV void quant_block32_x8(float4 v, uint8_t *codes16, uint8_t *scale, uint8_t *scale_t = nullptr)
 {
     const uint32_t p = threadIdx.x & 7u;
     float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
@@ -185,7 +195,10 @@ RFP4_DEV void quant_block32_x8(float4 v, uint8_t *codes16, uint8_t *scale)
     }
     const uint32_t hn = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)h, DPP_QUAD_1032, 0xF, 0xF, false); // part p ^ 1
     if ((p & 1u) == 0) *(uint32_t *)(codes16 + 2u * p) = h | (hn << 16);
-    if (p == 0) *scale = (uint8_t)sbyte;
+    if (p == 0) {
+        *scale = (uint8_t)sbyte;
+        if (scale_t) *scale_t = (uint8_t)sbyte;
+    }
 }
 
 // One thread per 32-block of the synthetic weight.
@@ -241,7 +254,12 @@ RFP4_DEV void quant_mx_body(const QuantMxArgs &a)
         } else {
             v = ((const float4 *)a.src)[t];
         }
-        quant_block32_x8(v, a.packed + (t / 8u) * 16u, a.scales + t / 8u);
+        uint8_t *st = nullptr;
+        if (a.scales_t) {
+            const uint64_t k4 = a.k / 4u, row = t / k4;
+            st = a.scales_t + mx_st_offset((uint32_t)row, (uint32_t)((t - row * k4) / 8u), (uint32_t)(a.k >> 8));
+        }
+        quant_block32_x8(v, a.packed + (t / 8u) * 16u, a.scales + t / 8u, st);
     }
 }
 

@@ -81,7 +81,8 @@ RFP4_DEV void rmsnorm_quant_rows_body(const RowsArgs &a)
                                          __fmul_rn(__fmul_rn(v[j].y, rms), f16_bits_to_f32((uint16_t)(wb[j].x >> 16))),
                                          __fmul_rn(__fmul_rn(v[j].z, rms), f16_bits_to_f32((uint16_t)(wb[j].y & 0xFFFFu))),
                                          __fmul_rn(__fmul_rn(v[j].w, rms), f16_bits_to_f32((uint16_t)(wb[j].y >> 16))));
-            quant_block32_x8(y, codes + (i / 8u) * 16u, scales + i / 8u);
+            quant_block32_x8(y, codes + (i / 8u) * 16u, scales + i / 8u,
+                             a.scales_t ? a.scales_t + mx_st_offset(r, i / 8u, a.k >> 8) : nullptr);
         }
         return;
     }
@@ -131,7 +132,8 @@ RFP4_DEV void rmsnorm_quant_rows_body(const RowsArgs &a)
                                          __fmul_rn(__fmul_rn(v[j].y, rms), f16_bits_to_f32((uint16_t)(wb[j].x >> 16))),
                                          __fmul_rn(__fmul_rn(v[j].z, rms), f16_bits_to_f32((uint16_t)(wb[j].y & 0xFFFFu))),
                                          __fmul_rn(__fmul_rn(v[j].w, rms), f16_bits_to_f32((uint16_t)(wb[j].y >> 16))));
-            quant_block32_x8(y, codes + (i / 8u) * 16u, scales + i / 8u);
+            quant_block32_x8(y, codes + (i / 8u) * 16u, scales + i / 8u,
+                             a.scales_t ? a.scales_t + mx_st_offset(r, i / 8u, a.k >> 8) : nullptr);
         }
     }
 }
@@ -167,7 +169,8 @@ RFP4_DEV void swiglu_quant_rows_body(const RowsArgs &a)
             if (i >= hi) break;
             const float4 y = make_float4(__fmul_rn(silu_ref(gv[j].x), uv[j].x), __fmul_rn(silu_ref(gv[j].y), uv[j].y),
                                          __fmul_rn(silu_ref(gv[j].z), uv[j].z), __fmul_rn(silu_ref(gv[j].w), uv[j].w));
-            quant_block32_x8(y, codes + (i / 8u) * 16u, scales + i / 8u);
+            quant_block32_x8(y, codes + (i / 8u) * 16u, scales + i / 8u,
+                             a.scales_t ? a.scales_t + mx_st_offset(r, i / 8u, a.k >> 8) : nullptr);
         }
     }
 }

@@ -39,6 +39,9 @@ static inline uint64_t stream_kv(uint32_t l, uint32_t isv) { return 0x4B560000ul
 
 struct LayerW {
     uint8_t *qkv_c, *qkv_s, *o_c, *o_s, *gu_c, *gu_s, *d_c, *d_s; // scales: sb bytes per 32-block
+    // the E8M0 scales again, step-blocked for the prefill's tiled GEMM
+    // (GemmArgs::w_st; engines that can prefill, else null)
+    uint8_t *qkv_st = nullptr, *o_st = nullptr, *gu_st = nullptr, *d_st = nullptr;
 };
 
 // The engine's GEMV launches, their variants fixed at creation.
@@ -50,7 +53,7 @@ struct llama_engine {
     std::vector<void *> allocs;
     std::vector<LayerW> L;
     uint16_t *norm_attn = nullptr, *norm_ffn = nullptr, *norm_final = nullptr, *embed = nullptr;
-    uint8_t *lm_c = nullptr, *lm_s = nullptr;
+    uint8_t *lm_c = nullptr, *lm_s = nullptr, *lm_st = nullptr;
     void *kcache = nullptr, *vcache = nullptr;
     uint32_t sb = 1, kvb = 2;  // bytes per scale (E8M0 1, f32 4) and per KV element (fp16 2, f32 4)
     const char *sname = "e8m0"; // kernel-name token of the scale format
@@ -96,6 +99,7 @@ struct llama_engine {
     uint32_t pf_cap = 0;
     float *pf_x = nullptr, *pf_c = nullptr, *pf_a = nullptr, *pf_part = nullptr; // pf_part: decode-kernel test path only
     uint8_t *pf_codes = nullptr, *pf_scales = nullptr;
+    uint8_t *pf_scales_t = nullptr; // the activation scales step-blocked, written beside pf_scales
     uint32_t *pf_ids = nullptr;
     // persistent decode (one cooperative launch for all layers of a step)
     bool persist_ok = false, persist = false; // shape and device allow it / chosen
@@ -127,6 +131,14 @@ static void *kv_layer(const llama_engine *e, uint32_t l, int isv)
 {
     const size_t per = (size_t)e->c.n_kv_heads * e->max_seq_alloc * e->c.head_dim * e->kvb;
     return (char *)(isv ? e->vcache : e->kcache) + (size_t)l * per;
+}
+
+// Whether the engine can prefill (llama_engine_prefill's shape and format
+// conditions): only then does it hold step-blocked weight scales.
+static bool prefill_shape_ok(const rfp4_model_config &c)
+{
+    return c.dim % 256u == 0 && qdim(c) % 256u == 0 && c.ffn % 256u == 0 && c.scale_format == RFP4_SCALE_E8M0 &&
+           c.kv_format == RFP4_KV_F16;
 }
 
 static int validate(const rfp4_model_config &c)
@@ -396,9 +408,9 @@ static int prefill_reserve(llama_engine *e, uint32_t n)
     const uint32_t cap = (n + 255u) / 256u * 256u;
     hipStreamSynchronize(e->stream);
     dfree(e, e->pf_x); dfree(e, e->pf_c); dfree(e, e->pf_a); dfree(e, e->pf_part);
-    dfree(e, e->pf_codes); dfree(e, e->pf_scales); dfree(e, e->pf_ids);
+    dfree(e, e->pf_codes); dfree(e, e->pf_scales); dfree(e, e->pf_scales_t); dfree(e, e->pf_ids);
     e->pf_x = e->pf_c = e->pf_a = e->pf_part = nullptr;
-    e->pf_codes = e->pf_scales = nullptr;
+    e->pf_codes = e->pf_scales = e->pf_scales_t = nullptr;
     e->pf_ids = nullptr;
     e->pf_cap = 0;
     const size_t kmax = std::max(std::max(c.dim, qd), c.ffn);
@@ -413,6 +425,7 @@ static int prefill_reserve(llama_engine *e, uint32_t n)
     if (!rc) rc = dalloc_t(e, &e->pf_a, (size_t)cap * qd);
     if (!rc) rc = dalloc_t(e, &e->pf_codes, (size_t)cap * kmax / 2);
     if (!rc) rc = dalloc_t(e, &e->pf_scales, (size_t)cap * kmax / 32);
+    if (!rc) rc = dalloc_t(e, &e->pf_scales_t, scales_tiled_bytes(cap, (uint32_t)kmax));
     if (!rc) rc = dalloc_t(e, &e->pf_ids, cap);
     if (!rc) e->pf_cap = cap;
     return rc;
@@ -444,13 +457,14 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
         uint16_t *kc = (uint16_t *)kv_layer(e, l, 0), *vc = (uint16_t *)kv_layer(e, l, 1); // fp16 (checked by the caller)
         RowsArgs na{};
         na.x = e->pf_x; na.w = e->norm_attn + (size_t)l * c.dim; na.codes = e->pf_codes; na.scales = e->pf_scales;
-        na.rows = n; na.k = c.dim; na.eps = c.eps;
+        na.scales_t = e->pf_scales_t; na.rows = n; na.k = c.dim; na.eps = c.eps;
         // layer l > 0: the previous layer's down projection (pf_c) is added into the residual stream here
         na.add = l > 0 ? e->pf_c : nullptr;
         na.x_out = e->pf_x;
         if ((rc = launch("rfp4_rmsnorm_quant_rows", dim3(n), dim3(256), s, &na))) return rc;
         RFP4_PF_STAGE(0);
-        if ((rc = gemm_launch(s, n, nqkv, c.dim, e->pf_codes, e->pf_scales, w.qkv_c, w.qkv_s, e->pf_c, e->gemm_part))) return rc;
+        if ((rc = gemm_launch(s, n, nqkv, c.dim, e->pf_codes, e->pf_scales, e->pf_scales_t, w.qkv_c, w.qkv_s, w.qkv_st,
+                              e->pf_c, e->gemm_part))) return rc;
         RFP4_PF_STAGE(1);
         RopeRowsArgs ra{};
         ra.qkv = e->pf_c; ra.cosv = e->cos_tab; ra.sinv = e->sin_tab; ra.kc = kc; ra.vc = vc;
@@ -478,23 +492,27 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
             if ((rc = attn_prefill_launch(pa, hd, s))) return rc;
         }
         RFP4_PF_STAGE(3);
-        if ((rc = mx4_quantize(s, n, qd, e->pf_a, 0, e->pf_codes, e->pf_scales))) return rc;
+        if ((rc = mx4_quantize_st(s, n, qd, e->pf_a, 0, e->pf_codes, e->pf_scales, e->pf_scales_t))) return rc;
         RFP4_PF_STAGE(4);
-        if ((rc = gemm_launch(s, n, c.dim, qd, e->pf_codes, e->pf_scales, w.o_c, w.o_s, e->pf_c, e->gemm_part))) return rc;
+        if ((rc = gemm_launch(s, n, c.dim, qd, e->pf_codes, e->pf_scales, e->pf_scales_t, w.o_c, w.o_s, w.o_st, e->pf_c,
+                              e->gemm_part))) return rc;
         RFP4_PF_STAGE(5);
         na.w = e->norm_ffn + (size_t)l * c.dim;
         na.add = e->pf_c; // x += O projection, then the FFN norm
         if ((rc = launch("rfp4_rmsnorm_quant_rows", dim3(n), dim3(256), s, &na))) return rc;
         RFP4_PF_STAGE(6);
-        if ((rc = gemm_launch(s, n, 2 * c.ffn, c.dim, e->pf_codes, e->pf_scales, w.gu_c, w.gu_s, e->pf_c, e->gemm_part))) return rc;
+        if ((rc = gemm_launch(s, n, 2 * c.ffn, c.dim, e->pf_codes, e->pf_scales, e->pf_scales_t, w.gu_c, w.gu_s, w.gu_st,
+                              e->pf_c, e->gemm_part))) return rc;
         RFP4_PF_STAGE(7);
         RowsArgs sa{};
-        sa.x = e->pf_c; sa.codes = e->pf_codes; sa.scales = e->pf_scales; sa.rows = n; sa.k = c.ffn;
+        sa.x = e->pf_c; sa.codes = e->pf_codes; sa.scales = e->pf_scales; sa.scales_t = e->pf_scales_t;
+        sa.rows = n; sa.k = c.ffn;
         // parts of about 1024 float4 per row (measured: 8B 512 rows x 14336)
         if ((rc = launch("rfp4_swiglu_quant_rows", dim3(n, std::max(1u, (c.ffn / 4u + 1023u) / 1024u)), dim3(256), s, &sa)))
             return rc;
         RFP4_PF_STAGE(8);
-        if ((rc = gemm_launch(s, n, c.dim, c.ffn, e->pf_codes, e->pf_scales, w.d_c, w.d_s, e->pf_c, e->gemm_part))) return rc;
+        if ((rc = gemm_launch(s, n, c.dim, c.ffn, e->pf_codes, e->pf_scales, e->pf_scales_t, w.d_c, w.d_s, w.d_st, e->pf_c,
+                              e->gemm_part))) return rc;
         RFP4_PF_STAGE(9);
         // x += down projection: by the next layer's first norm, after the last layer here
         if (l + 1 == c.n_layers && (rc = residual(s, n * c.dim, e->pf_c, e->pf_x))) return rc;
@@ -668,6 +686,17 @@ static int engine_alloc(const rfp4_model_config *cfg, llama_engine **out)
     if (!rc) rc = dalloc_t(e, &e->embed, (size_t)c.vocab * c.dim);
     if (!rc) rc = dalloc_t(e, &e->lm_c, (size_t)c.vocab * c.dim / 2);
     if (!rc) rc = dalloc_t(e, &e->lm_s, (size_t)c.vocab * c.dim / 32 * sb);
+    // step-blocked E8M0 scales for the prefill's tiled GEMM (made by engine_finish)
+    if (prefill_shape_ok(c)) {
+        for (uint32_t l = 0; l < c.n_layers && !rc; l++) {
+            LayerW &w = e->L[l];
+            rc = dalloc_t(e, &w.qkv_st, scales_tiled_bytes(qd + 2 * kvd, c.dim));
+            if (!rc) rc = dalloc_t(e, &w.o_st, scales_tiled_bytes(c.dim, qd));
+            if (!rc) rc = dalloc_t(e, &w.gu_st, scales_tiled_bytes(2 * c.ffn, c.dim));
+            if (!rc) rc = dalloc_t(e, &w.d_st, scales_tiled_bytes(c.dim, c.ffn));
+        }
+        if (!rc) rc = dalloc_t(e, &e->lm_st, scales_tiled_bytes(c.vocab, c.dim));
+    }
     const size_t kv_bytes_all = (size_t)c.n_layers * c.n_kv_heads * e->max_seq_alloc * hd * e->kvb;
     if (!rc) rc = dalloc(e, &e->kcache, kv_bytes_all);
     if (!rc) rc = dalloc(e, &e->vcache, kv_bytes_all);
@@ -786,8 +815,22 @@ static int engine_synth(llama_engine *e, uint64_t seed)
 
 static int engine_finish(llama_engine *e)
 {
+    // the weights are final: their step-blocked scale copies (engines that can prefill)
+    const rfp4_model_config &c = e->c;
+    const uint32_t qd = qdim(c), kvd = kvdim(c);
+    int rc = RFP4_OK;
+    if (e->lm_st) {
+        for (uint32_t l = 0; l < c.n_layers && !rc; l++) {
+            const LayerW &w = e->L[l];
+            rc = scales_tile_launch(e->stream, c.dim, w.qkv_s, w.qkv_st, qd + 2 * kvd, w.gu_s, w.gu_st, 2 * c.ffn);
+            if (!rc) rc = scales_tile_launch(e->stream, qd, w.o_s, w.o_st, c.dim, nullptr, nullptr, 0u);
+            if (!rc) rc = scales_tile_launch(e->stream, c.ffn, w.d_s, w.d_st, c.dim, nullptr, nullptr, 0u);
+        }
+        if (!rc) rc = scales_tile_launch(e->stream, c.dim, e->lm_s, e->lm_st, c.vocab, nullptr, nullptr, 0u);
+    }
     // step graphs are captured by llama_engine_begin for the positions it can reach
-    return hip_check(hipStreamSynchronize(e->stream), "hipStreamSynchronize(create)");
+    if (!rc) rc = hip_check(hipStreamSynchronize(e->stream), "hipStreamSynchronize(create)");
+    return rc;
 }
 
 // ---------------------------------------------------------------- real weights
@@ -1338,6 +1381,37 @@ int llama_engine_weight(llama_engine *e, int layer, int proj, const uint8_t **co
     *scales = bs + rows_before * K / 32 * e->sb;
     *code_bytes = rows * K / 2;
     *scale_bytes = rows * K / 32 * e->sb;
+    return RFP4_OK;
+}
+
+int llama_engine_weight_scales_tiled(llama_engine *e, int layer, int proj, const uint8_t **scales_tiled,
+                                     size_t *bytes)
+{
+    if (!e || !scales_tiled || !bytes) return set_error(RFP4_E_INVALID, "null argument");
+    if (!e->lm_st) return set_error(RFP4_E_SHAPE, "llama_engine_weight_scales_tiled: the engine cannot prefill, so holds none");
+    const rfp4_model_config &c = e->c;
+    const uint32_t qd = qdim(c), kvd = kvdim(c);
+    if (layer < 0) {
+        *scales_tiled = e->lm_st;
+        *bytes = scales_tiled_bytes(c.vocab, c.dim);
+        return RFP4_OK;
+    }
+    if ((uint32_t)layer >= c.n_layers || proj < 0 || proj > 6) return set_error(RFP4_E_INVALID, "bad layer/proj");
+    const LayerW &w = e->L[layer];
+    // stacked matrices: every part starts on a 32-row block (qd, kvd, ffn are multiples of 256)
+    size_t rows_before = 0, rows = 0, K = c.dim;
+    const uint8_t *bs = nullptr;
+    switch (proj) {
+    case 0: bs = w.qkv_st; rows = qd; break;
+    case 1: bs = w.qkv_st; rows_before = qd; rows = kvd; break;
+    case 2: bs = w.qkv_st; rows_before = qd + kvd; rows = kvd; break;
+    case 3: bs = w.o_st; rows = c.dim; K = qd; break;
+    case 4: bs = w.gu_st; rows = c.ffn; break;
+    case 5: bs = w.gu_st; rows_before = c.ffn; rows = c.ffn; break;
+    default: bs = w.d_st; rows = c.dim; K = c.ffn; break;
+    }
+    *scales_tiled = bs + rows_before * K / 32;
+    *bytes = scales_tiled_bytes((uint32_t)rows, (uint32_t)K);
     return RFP4_OK;
 }
 

@@ -178,6 +178,8 @@ GEMM_KERNEL_P(64, 128, 2, 2, 1, 2, 3)
 GEMM_KERNEL_P(128, 128, 2, 2, 2, 2, 3)
 GEMM_KERNEL_P(256, 128, 2, 2, 4, 2, 3)
 K256 void rfp4_gemm_reduce(GemmArgs a) { gemm_reduce_body(a); }
+// row-major E8M0 scales -> the step-blocked copy the tiled kernels read
+K256 void rfp4_scales_tile(ScaleTileArgs a) { scales_tile_body(a); }
 // few activation rows (M <= 16 MB) x 16 NF W rows per workgroup, up to 8
 // waves of up to SEG K segments of 512 each (device/gemm_rows.h):
 // rfp4_gemm_rows_m<16 MB>_s<SEG>_f<NF>, the combinations whose loads fit the

@@ -285,6 +285,7 @@ int rfp4_init(int device)
     if (!rc) rc = hip_check(hipMalloc((void **)&rt->gemm_part, kGemmWorkspaceWords * sizeof(float)), "hipMalloc(gemm workspace)");
     if (!rc)
         rc = hip_check(hipMemset(rt->gemm_part + kGemmPartFloats, 0, kGemmCounters * sizeof(uint32_t)), "hipMemset(gemm counters)");
+    if (!rc) rc = hip_check(hipMalloc((void **)&rt->gemm_st, kGemmStBytes), "hipMalloc(gemm scale workspace)");
     // arrival counters of the in-kernel attention merge: zero between calls
     if (!rc) rc = hip_check(hipMalloc((void **)&rt->attn_counters, kAttnMaxHeads * sizeof(uint32_t)), "hipMalloc(attn counters)");
     if (!rc) rc = hip_check(hipMemset(rt->attn_counters, 0, kAttnMaxHeads * sizeof(uint32_t)), "hipMemset(attn counters)");
@@ -294,6 +295,7 @@ int rfp4_init(int device)
     if (rc) {
         hipFree(rt->attn_part);
         hipFree(rt->gemm_part);
+        hipFree(rt->gemm_st);
         hipFree(rt->attn_counters);
         hipModuleUnload(rt->module);
         delete rt;
@@ -321,6 +323,7 @@ int rfp4_shutdown(void)
     };
     keep(hip_check(hipFree(rt->attn_part), "hipFree(attn workspace)"));
     keep(hip_check(hipFree(rt->gemm_part), "hipFree(gemm workspace)"));
+    keep(hip_check(hipFree(rt->gemm_st), "hipFree(gemm scale workspace)"));
     keep(hip_check(hipFree(rt->attn_counters), "hipFree(attn counters)"));
     keep(hip_check(hipModuleUnload(rt->module), "hipModuleUnload"));
     g_rt = nullptr;
@@ -1066,19 +1069,57 @@ int fp4_quantize_absmax(const float *w, uint32_t rows, uint32_t k, uint32_t *pac
 int mx4_quantize(rfp4_stream_t stream, uint64_t rows, uint64_t k, const void *src, int src_is_bf16, uint8_t *codes,
                  uint8_t *scales)
 {
-    if (!src || !codes || !scales) return set_error(RFP4_E_INVALID, "mx4_quantize: null pointer");
-    if (k == 0 || k % 32) return set_error(RFP4_E_SHAPE, "mx4_quantize: k=%llu not a multiple of 32", (unsigned long long)k);
-    if (((uintptr_t)codes & 15u) != 0) return set_error(RFP4_E_ALIGN, "mx4_quantize: codes must be 16-byte aligned");
-    if (((uintptr_t)src & (src_is_bf16 ? 7u : 15u)) != 0)
-        return set_error(RFP4_E_ALIGN, "mx4_quantize: src must be %u-byte aligned", src_is_bf16 ? 8u : 16u);
-    QuantMxArgs a{src, codes, scales, rows, k};
-    uint64_t blocks = (rows * (k / 4) + 255) / 256; // one thread per 4 values
-    if (blocks > 65536) blocks = 65536;
-    return launch(src_is_bf16 ? "rfp4_quant_mx_bf16" : "rfp4_quant_mx_f32", dim3((unsigned)blocks), dim3(256),
-                  (hipStream_t)stream, &a);
+    return mx4_quantize_st((hipStream_t)stream, rows, k, src, src_is_bf16, codes, scales, nullptr);
+}
+
+int mx4_quantize_tiled(rfp4_stream_t stream, uint64_t rows, uint64_t k, const void *src, int src_is_bf16,
+                       uint8_t *codes, uint8_t *scales, uint8_t *scales_tiled)
+{
+    if (!scales_tiled) return set_error(RFP4_E_INVALID, "mx4_quantize_tiled: null pointer");
+    return mx4_quantize_st((hipStream_t)stream, rows, k, src, src_is_bf16, codes, scales, scales_tiled);
+}
+
+size_t mx4_scales_tiled_bytes(uint32_t rows, uint32_t k) { return scales_tiled_bytes(rows, k); }
+
+int mx4_scales_tile(rfp4_stream_t stream, uint32_t rows, uint32_t k, const uint8_t *scales, uint8_t *scales_tiled)
+{
+    if (!scales || !scales_tiled) return set_error(RFP4_E_INVALID, "mx4_scales_tile: null pointer");
+    if (rows == 0 || k == 0 || k % 256u) return set_error(RFP4_E_SHAPE, "mx4_scales_tile: rows=%u k=%u (k a multiple of 256)", rows, k);
+    if (((uintptr_t)scales | (uintptr_t)scales_tiled) & 3u) return set_error(RFP4_E_ALIGN, "mx4_scales_tile: 4-byte alignment");
+    return scales_tile_launch((hipStream_t)stream, k, scales, scales_tiled, rows, nullptr, nullptr, 0u);
 }
 
 } // extern "C"
+
+namespace rfp4 {
+
+int mx4_quantize_st(hipStream_t stream, uint64_t rows, uint64_t k, const void *src, int src_is_bf16, uint8_t *codes,
+                    uint8_t *scales, uint8_t *scales_t)
+{
+    if (!src || !codes || !scales) return set_error(RFP4_E_INVALID, "mx4_quantize: null pointer");
+    if (k == 0 || k % 32) return set_error(RFP4_E_SHAPE, "mx4_quantize: k=%llu not a multiple of 32", (unsigned long long)k);
+    if (scales_t && (k % 256u || rows > 0xFFFFFFFFull))
+        return set_error(RFP4_E_SHAPE, "mx4_quantize: the step-blocked scales need k a multiple of 256 (k=%llu)",
+                         (unsigned long long)k);
+    if (((uintptr_t)codes & 15u) != 0) return set_error(RFP4_E_ALIGN, "mx4_quantize: codes must be 16-byte aligned");
+    if (((uintptr_t)src & (src_is_bf16 ? 7u : 15u)) != 0)
+        return set_error(RFP4_E_ALIGN, "mx4_quantize: src must be %u-byte aligned", src_is_bf16 ? 8u : 16u);
+    QuantMxArgs a{src, codes, scales, rows, k, scales_t};
+    uint64_t blocks = (rows * (k / 4) + 255) / 256; // one thread per 4 values
+    if (blocks > 65536) blocks = 65536;
+    return launch(src_is_bf16 ? "rfp4_quant_mx_bf16" : "rfp4_quant_mx_f32", dim3((unsigned)blocks), dim3(256), stream, &a);
+}
+
+int scales_tile_launch(hipStream_t s, uint32_t k, const uint8_t *src0, uint8_t *dst0, uint32_t rows0,
+                       const uint8_t *src1, uint8_t *dst1, uint32_t rows1)
+{
+    ScaleTileArgs a{{src0, src1}, {dst0, dst1}, {rows0, rows1}, k};
+    const uint64_t words = (scales_tiled_bytes(rows0, k) + scales_tiled_bytes(rows1, k)) / 4u;
+    const uint64_t blocks = std::min<uint64_t>((words + 255u) / 256u, 8192u);
+    return launch("rfp4_scales_tile", dim3((unsigned)std::max<uint64_t>(blocks, 1u)), dim3(256), s, &a);
+}
+
+} // namespace rfp4
 
 namespace {
 
@@ -1278,8 +1319,19 @@ extern "C" {
 int fp4_gemm(rfp4_stream_t stream, uint32_t m, uint32_t n, uint32_t k, const uint8_t *a_codes,
              const uint8_t *a_scales, const uint8_t *w_codes, const uint8_t *w_scales, float *c)
 {
-    return gemm_launch((hipStream_t)stream, m, n, k, a_codes, a_scales, w_codes, w_scales, c,
+    return gemm_launch((hipStream_t)stream, m, n, k, a_codes, a_scales, nullptr, w_codes, w_scales, nullptr, c,
                        g_rt ? g_rt->gemm_part : nullptr);
+}
+
+int fp4_gemm_tiled(rfp4_stream_t stream, uint32_t m, uint32_t n, uint32_t k, const uint8_t *a_codes,
+                   const uint8_t *a_scales, const uint8_t *a_scales_tiled, const uint8_t *w_codes,
+                   const uint8_t *w_scales, const uint8_t *w_scales_tiled, float *c)
+{
+    if (!a_scales_tiled || !w_scales_tiled) return set_error(RFP4_E_INVALID, "fp4_gemm_tiled: null step-blocked scales");
+    if (((uintptr_t)a_scales_tiled | (uintptr_t)w_scales_tiled) & 3u)
+        return set_error(RFP4_E_ALIGN, "fp4_gemm_tiled: step-blocked scales must be 4-byte aligned");
+    return gemm_launch((hipStream_t)stream, m, n, k, a_codes, a_scales, a_scales_tiled, w_codes, w_scales,
+                       w_scales_tiled, c, g_rt ? g_rt->gemm_part : nullptr);
 }
 
 } // extern "C"
@@ -1287,7 +1339,8 @@ int fp4_gemm(rfp4_stream_t stream, uint32_t m, uint32_t n, uint32_t k, const uin
 namespace rfp4 {
 
 int gemm_launch(hipStream_t stream, uint32_t m, uint32_t n, uint32_t k, const uint8_t *a_codes, const uint8_t *a_scales,
-                const uint8_t *w_codes, const uint8_t *w_scales, float *c, float *part)
+                const uint8_t *a_st, const uint8_t *w_codes, const uint8_t *w_scales, const uint8_t *w_st, float *c,
+                float *part)
 {
     if (!a_codes || !a_scales || !w_codes || !w_scales || !c) return set_error(RFP4_E_INVALID, "fp4_gemm: null pointer");
     if (m == 0 || n == 0 || k == 0) return set_error(RFP4_E_SHAPE, "fp4_gemm: empty shape m=%u n=%u k=%u", m, n, k);
@@ -1318,12 +1371,24 @@ int gemm_launch(hipStream_t stream, uint32_t m, uint32_t n, uint32_t k, const ui
         return set_error(RFP4_E_CAPACITY, "fp4_gemm: split-K partials %u x %u x %u exceed the workspace", p.kz, m, n);
     if (tiles * p.kz > 0x7FFFFFFFull) return set_error(RFP4_E_SHAPE, "fp4_gemm: grid too large");
     if (p.kz > 1 && !part) return set_error(RFP4_E_INVALID, "fp4_gemm: split-K plan without a workspace");
+    if (!a_st || !w_st) {
+        // the step-blocked scale copies the tiled kernels read, made here (stream-ordered before the GEMM)
+        const size_t abytes = (scales_tiled_bytes(m, k) + 255u) / 256u * 256u, wbytes = scales_tiled_bytes(n, k);
+        if (abytes + wbytes > kGemmStBytes)
+            return set_error(RFP4_E_CAPACITY, "fp4_gemm: step-blocked scales of %u + %u rows x k=%u exceed the %zu-byte "
+                                              "workspace (pass them to fp4_gemm_tiled)", m, n, k, kGemmStBytes);
+        uint8_t *ast = rt->gemm_st, *wst = rt->gemm_st + abytes;
+        const int rc = scales_tile_launch(stream, k, a_scales, ast, m, w_scales, wst, n);
+        if (rc) return rc;
+        a_st = ast;
+        w_st = wst;
+    }
     // two-way splits sum in the launch (the last split of a tile to arrive),
     // others in the reduce kernel launched next (also tiles above 256x128,
     // whose kernels have no registers for the other plane)
     uint32_t *counters = p.kz == 2u && t.bm * t.bn <= 256u * 128u && tiles <= kGemmCounters && !t_gemm_reduce_kernel
                              ? (uint32_t *)(part + kGemmPartFloats) : nullptr;
-    GemmArgs a{a_codes, a_scales, w_codes, w_scales, c, part, m, n, k, p.kz, counters};
+    GemmArgs a{a_codes, a_scales, w_codes, w_scales, c, part, m, n, k, p.kz, counters, a_st, w_st};
     char pname[48];
     const char *kname = t.name;
     if (p.nst >= 3) { // a deeper DMA pipeline (kernels.hip GEMM_KERNEL_P)

@@ -20,6 +20,9 @@ constexpr size_t kGemmPartFloats = (size_t)8 << 20; // 32 MiB
 // splits that sum inside the launch.
 constexpr uint32_t kGemmCounters = 16384;
 constexpr size_t kGemmWorkspaceWords = kGemmPartFloats + kGemmCounters;
+// Step-blocked scale copies the drop-in fp4_gemm makes for the tiled kernels
+// when the caller passes only row-major scales (A's, then W's).
+constexpr size_t kGemmStBytes = (size_t)64 << 20;
 
 struct Runtime {
     int device = 0;
@@ -29,6 +32,7 @@ struct Runtime {
     float *attn_part = nullptr;       // default split-K workspace of attn_decode
     size_t attn_part_floats = 0;
     float *gemm_part = nullptr;       // split-K workspace of fp4_gemm (kGemmWorkspaceWords)
+    uint8_t *gemm_st = nullptr;       // step-blocked scales of fp4_gemm's operands (kGemmStBytes)
     uint32_t *attn_counters = nullptr; // in-kernel attention merge (kAttnMaxHeads words, zero between calls)
     size_t max_lds = 65536;           // LDS bytes per workgroup
 };
@@ -86,10 +90,21 @@ size_t engines_destroy_all();
 // the allocation-free entry points' static scratch (csrc/noalloc.hip).
 int noalloc_setup(int device);
 // fp4_gemm with the caller's split-K workspace (kGemmWorkspaceWords words, the
-// counters zeroed; the
-// engine owns one, so engines on different streams do not share partials).
+// counters zeroed; the engine owns one, so engines on different streams do
+// not share partials).  a_st / w_st: the step-blocked copies of the scales
+// (device/gemm.h); where either is null and the plan is a tiled kernel, both
+// are made first in the runtime's workspace (one more launch).
 int gemm_launch(hipStream_t stream, uint32_t m, uint32_t n, uint32_t k, const uint8_t *a_codes, const uint8_t *a_scales,
-                const uint8_t *w_codes, const uint8_t *w_scales, float *c, float *part);
+                const uint8_t *a_st, const uint8_t *w_codes, const uint8_t *w_scales, const uint8_t *w_st, float *c,
+                float *part);
+// Bytes of the step-blocked copy of [rows][k/32] E8M0 scales.
+inline size_t scales_tiled_bytes(uint32_t rows, uint32_t k) { return (size_t)((rows + 31u) / 32u) * 32u * (k / 32u); }
+// Row-major scales of one or two matrices (rows1 = 0: one) into step-blocked copies, k % 256 == 0.
+int scales_tile_launch(hipStream_t s, uint32_t k, const uint8_t *src0, uint8_t *dst0, uint32_t rows0,
+                       const uint8_t *src1, uint8_t *dst1, uint32_t rows1);
+// mx4_quantize that also writes the step-blocked copy of the scales (null: none; k % 256 == 0 otherwise).
+int mx4_quantize_st(hipStream_t stream, uint64_t rows, uint64_t k, const void *src, int src_is_bf16, uint8_t *codes,
+                    uint8_t *scales, uint8_t *scales_t);
 uint32_t attn_group_pad(uint32_t group);
 // Causal prefill attention (device/attn_prefill.h), fp16 caches.
 int attn_prefill_launch(const AttnPrefillArgs &a, uint32_t head_dim, hipStream_t s);

@@ -144,6 +144,7 @@ typedef struct RowsArgs {
     uint32_t bf16;           // embed holds bf16 (1) or fp16 (0) bit patterns
     const float *add;        // rmsnorm: rows added into x first (the layer's residual add), or null
     float *x_out;            // rmsnorm with add: where x + add is stored (x itself)
+    uint8_t *scales_t;       // rmsnorm, swiglu: the scales step-blocked as well (GemmArgs), or null
 } RowsArgs;
 
 typedef struct RopeRowsArgs {
@@ -192,6 +193,7 @@ typedef struct QuantMxArgs {
     const void *src;      // f32 or bf16, rows x K
     uint8_t *packed, *scales;
     uint64_t rows, k;
+    uint8_t *scales_t;    // the scales step-blocked as well (GemmArgs; k % 256 == 0), or null
 } QuantMxArgs;
 
 // Device-resident decode cursor: lets one captured step graph replay for
@@ -240,7 +242,21 @@ typedef struct GemmArgs {
     // last split of a tile to arrive sums the planes.  Null: the reduce
     // kernel launched next sums them.
     uint32_t *counters;
+    // the same scales step-blocked (the tiled kernels read only these, the
+    // few-row kernels only the row-major ones): per 32-row block and K step
+    // of 256 values, 256 contiguous bytes, for h = 0, 1 and rows r = 0..31
+    // the step's scale bytes 4h .. 4h + 3 of the block's row r
+    const uint8_t *a_st, *w_st;
 } GemmArgs;
+
+// Row-major E8M0 scales [rows][k/32] -> the step-blocked layout of GemmArgs
+// (ceil(rows/32) blocks; rows past `rows` hold zero bytes), for up to two
+// matrices of the same k in one launch (rows[1] = 0: one).
+typedef struct ScaleTileArgs {
+    const uint8_t *src[2];
+    uint8_t *dst[2];
+    uint32_t rows[2], k;
+} ScaleTileArgs;
 
 // Persistent decode of every layer of one step (device/persist.h): one
 // workgroup per CU, grid barriers between the stages of a layer.

@@ -101,6 +101,10 @@ _SIGS = {
     "fp4_mma_allones": (I32, [P, P]),
     "mx4_quantize": (I32, [P, U64, U64, P, I32, P, P]),
     "fp4_gemm": (I32, [P, U32, U32, U32, P, P, P, P, P]),
+    "fp4_gemm_tiled": (I32, [P, U32, U32, U32, P, P, P, P, P, P, P]),
+    "mx4_scales_tiled_bytes": (SZ, [U32, U32]),
+    "mx4_scales_tile": (I32, [P, U32, U32, P, P]),
+    "mx4_quantize_tiled": (I32, [P, U64, U64, P, I32, P, P, P]),
     "rfp4_debug_gemm_plan": (I32, [I32, I32]),
     "rfp4_debug_attn_chunk": (I32, [U32]),
     "rfp4_gemm_plan": (I32, [U32, U32, U32, P, P, P]),
@@ -151,6 +155,7 @@ _SIGS = {
     "llama_engine_stream": (P, [P]),
     "llama_engine_use_graph": (I32, [P, I32]),
     "llama_engine_weight": (I32, [P, I32, I32, C.POINTER(P), C.POINTER(P), C.POINTER(SZ), C.POINTER(SZ)]),
+    "llama_engine_weight_scales_tiled": (I32, [P, I32, I32, C.POINTER(P), C.POINTER(SZ)]),
     "llama_engine_kv": (I32, [P, I32, C.POINTER(P), C.POINTER(P), C.POINTER(SZ)]),
     "llama_engine_use_persistent": (I32, [P, I32]),
     "llama_engine_persistent": (I32, [P]),
@@ -461,6 +466,25 @@ def fp4_gemm(stream, m, n, k, a_codes, a_scales, w_codes, w_scales, c):
     check(load().fp4_gemm(_s(stream), m, n, k, _p(a_codes), _p(a_scales), _p(w_codes), _p(w_scales), _p(c)))
 
 
+def fp4_gemm_tiled(stream, m, n, k, a_codes, a_scales, a_scales_tiled, w_codes, w_scales, w_scales_tiled, c):
+    """fp4_gemm with the step-blocked scale copies supplied (no tiling launch)."""
+    check(load().fp4_gemm_tiled(_s(stream), m, n, k, _p(a_codes), _p(a_scales), _p(a_scales_tiled), _p(w_codes),
+                                _p(w_scales), _p(w_scales_tiled), _p(c)))
+
+
+def mx4_scales_tiled_bytes(rows, k) -> int:
+    return int(load().mx4_scales_tiled_bytes(rows, k))
+
+
+def mx4_scales_tile(stream, rows, k, scales, scales_tiled):
+    check(load().mx4_scales_tile(_s(stream), rows, k, _p(scales), _p(scales_tiled)))
+
+
+def mx4_quantize_tiled(stream, rows, k, src, src_is_bf16, codes, scales, scales_tiled):
+    check(load().mx4_quantize_tiled(_s(stream), rows, k, _p(src), int(src_is_bf16), _p(codes), _p(scales),
+                                    _p(scales_tiled)))
+
+
 def debug_attn_chunk(chunk=0):
     check(load().rfp4_debug_attn_chunk(chunk))
 
@@ -722,6 +746,12 @@ class Engine:
         c, s, cb, sb = P(), P(), SZ(), SZ()
         check(load().llama_engine_weight(self.h, layer, proj, C.byref(c), C.byref(s), C.byref(cb), C.byref(sb)))
         return c.value, s.value, cb.value, sb.value
+
+    def weight_scales_tiled(self, layer: int, proj: int):
+        """(device pointer, bytes) of the weight's step-blocked scale copy."""
+        p, n = C.c_void_p(), SZ(0)
+        check(load().llama_engine_weight_scales_tiled(self.h, layer, proj, C.byref(p), C.byref(n)))
+        return p.value, n.value
 
     def weight_host(self, layer: int, proj: int):
         c, s, cb, sb = self.weight(layer, proj)

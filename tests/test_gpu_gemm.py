@@ -310,3 +310,83 @@ def test_gemm_stage_hook_rejects_bad_values(rf):
     assert lib.rfp4_debug_gemm_stages(1) == -1
     assert lib.rfp4_debug_gemm_stages(5) == -1
     rf.check(lib.rfp4_debug_gemm_stages(0))
+
+
+# ---------------------------------------------------------------- step-blocked scales
+def tile_scales_np(sc, rows, k):
+    """The step-blocked layout (include/rfp4.h, mx4_scales_tile): for row block
+    rb, K step s, half h, row r and byte j, scale block 8 s + 4 h + j of row
+    32 rb + r; rows past `rows` zero."""
+    nb = (rows + 31) // 32
+    pad = np.zeros((nb * 32, k // 32), np.uint8)
+    pad[:rows] = np.asarray(sc, np.uint8).reshape(rows, k // 32)
+    t = pad.reshape(nb, 32, k // 256, 2, 4)           # rb, r, s, h, j
+    return np.ascontiguousarray(t.transpose(0, 2, 3, 1, 4)).reshape(-1)  # rb, s, h, r, j
+
+
+def test_tile_scales_np_layout():
+    """The restatement against hand-placed bytes: row 33's scale block 13 of a
+    k = 512 matrix (step 1, half 1, byte 1) sits in block 1 at
+    (1 * 2 + 1) * 256 + 128 + 4 * 1 + 1."""
+    sc = np.zeros((40, 16), np.uint8)
+    sc[33, 13] = 7
+    t = tile_scales_np(sc, 40, 512)
+    assert t.size == 64 * 16
+    assert np.flatnonzero(t).tolist() == [(1 * 2 + 1) * 256 + 128 + 4 + 1] and t.max() == 7
+
+
+@pytest.mark.parametrize("rows,k", [(1, 256), (33, 256), (80, 1024), (292, 768), (4096, 4096)])
+def test_scales_tile_layout(rf, stream, rows, k):
+    sc = np.random.default_rng(rows + k).integers(0, 256, rows * k // 32, dtype=np.uint8)
+    nbytes = rf.mx4_scales_tiled_bytes(rows, k)
+    assert nbytes == (rows + 31) // 32 * 32 * k // 32
+    dt = rf.DeviceBuffer(nbytes)
+    rf.mx4_scales_tile(stream, rows, k, _dev(rf, sc, stream), dt)
+    np.testing.assert_array_equal(dt.to_host(nbytes, np.uint8, stream), tile_scales_np(sc, rows, k))
+
+
+@pytest.mark.parametrize("bf16", [True, False])
+def test_quantize_tiled_writes_both_layouts(rf, stream, bf16):
+    """mx4_quantize_tiled: the codes and row-major scales of mx4_quantize, bit
+    for bit, plus their step-blocked copy."""
+    rows, k = 37, 1280
+    if bf16:
+        src = _bf16_normal(rows, k, 3)
+    else:
+        src = np.random.default_rng(3).standard_normal((rows, k), dtype=np.float32)
+    ds = _dev(rf, src, stream)
+    c0, s0 = rf.DeviceBuffer(rows * k // 2), rf.DeviceBuffer(rows * k // 32)
+    c1, s1 = rf.DeviceBuffer(rows * k // 2), rf.DeviceBuffer(rows * k // 32)
+    st = rf.DeviceBuffer(rf.mx4_scales_tiled_bytes(rows, k))
+    rf.mx4_quantize(stream, rows, k, ds, bf16, c0, s0)
+    rf.mx4_quantize_tiled(stream, rows, k, ds, bf16, c1, s1, st)
+    sc = s0.to_host(rows * k // 32, np.uint8, stream)
+    np.testing.assert_array_equal(c1.to_host(rows * k // 2, np.uint8, stream), c0.to_host(rows * k // 2, np.uint8, stream))
+    np.testing.assert_array_equal(s1.to_host(rows * k // 32, np.uint8, stream), sc)
+    # the quantizer writes the blocks of its rows only (rows 37-63 of the last block are left as they were)
+    valid = tile_scales_np(np.ones(rows * k // 32, np.uint8), rows, k) == 1
+    got = st.to_host(st.nbytes, np.uint8, stream)
+    np.testing.assert_array_equal(got[valid], tile_scales_np(sc, rows, k)[valid])
+    with pytest.raises(rf.Rfp4Error):
+        rf.mx4_quantize_tiled(stream, rows, 1056, ds, bf16, c1, s1, st)  # k not a multiple of 256
+
+
+@pytest.mark.parametrize("tile", list(range(len(TILES))) + [5])
+def test_gemm_tiled_entry_bit_identical(rf, orc, stream, forced_plan, tile):
+    """fp4_gemm_tiled with the caller's step-blocked scales equals fp4_gemm
+    (which makes them itself) bit for bit, on every tiled kernel and the
+    few-row kernel (which reads the row-major scales), and the oracle."""
+    m, n, k = (80, 292, 1024) if tile < 5 else (16, 292, 1024)
+    ac, asc = _uniform_mx(orc, m, k, 21)
+    wc, wsc = _uniform_mx(orc, n, k, 22)
+    d = [_dev(rf, t, stream) for t in (ac, asc, wc, wsc)]
+    ast = _dev(rf, tile_scales_np(asc, m, k), stream)
+    wst = _dev(rf, tile_scales_np(wsc, n, k), stream)
+    forced_plan(tile, 1 if tile < 5 else 2)
+    c0 = _gemm(rf, stream, m, n, k, *d)
+    dc = rf.DeviceBuffer(m * n * 4)
+    rf.fp4_gemm_tiled(stream, m, n, k, d[0], d[1], ast, d[2], d[3], wst, dc)
+    c1 = dc.to_host(m * n, np.float32, stream).reshape(m, n)
+    np.testing.assert_array_equal(c1.view(np.uint32), c0.view(np.uint32))
+    c64, absc = orc.gemm_mx_f64(m, n, k, ac, asc, wc, wsc)
+    _assert_gemm_close(c1, c64, absc)

@@ -170,3 +170,33 @@ def test_prefill_errors(rf):
         eng.prefill([1, 2], 0)
     assert e.value.code == -2
     eng.close()
+
+
+def test_engine_step_blocked_weight_scales(rf):
+    """An engine that can prefill holds each projection's E8M0 scales again in
+    the step-blocked layout the tiled GEMM reads: equal to mx4_scales_tile of
+    its row-major scales (stacked parts included); engines that cannot
+    prefill hold none."""
+    from test_gpu_gemm import tile_scales_np
+
+    eng = _engine(rf, TINY128, 77)
+    cfg = TINY128
+    qd, kvd = cfg["n_heads"] * cfg["head_dim"], cfg["n_kv_heads"] * cfg["head_dim"]
+    shapes = {0: (qd, cfg["dim"]), 1: (kvd, cfg["dim"]), 2: (kvd, cfg["dim"]), 3: (cfg["dim"], qd),
+              4: (cfg["ffn"], cfg["dim"]), 5: (cfg["ffn"], cfg["dim"]), 6: (cfg["dim"], cfg["ffn"])}
+    views = [(l, p) for l in range(cfg["n_layers"]) for p in range(7)] + [(-1, 0)]
+    for layer, proj in views:
+        rows, k = (cfg["vocab"], cfg["dim"]) if layer < 0 else shapes[proj]
+        _, sc = eng.weight_host(layer, proj)
+        ptr, nbytes = eng.weight_scales_tiled(layer, proj)
+        assert nbytes == rows * k // 32
+        got = np.empty(nbytes, np.uint8)
+        rf.check(rf.load().rfp4_d2h(got.ctypes.data, ptr, nbytes, eng.stream.h))
+        eng.stream.synchronize()
+        np.testing.assert_array_equal(got, tile_scales_np(sc, rows, k), err_msg=f"layer {layer} proj {proj}")
+    eng.close()
+    c = {k: v for k, v in TINY.items() if k != "max_seq"}
+    eng = rf.Engine(rf.model_config(max_seq=TINY["max_seq"], kv_format=1, **c), 1)  # f32 caches: no prefill
+    with pytest.raises(rf.Rfp4Error):
+        eng.weight_scales_tiled(0, 0)
+    eng.close()
