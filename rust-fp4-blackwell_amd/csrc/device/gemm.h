@@ -160,7 +160,33 @@ RFP4_DEV void gemm_lds_wait_group(uint32_t t, u32x4 (&a)[FA], u32x4 (&b)[FB], ui
     for (int i = 0; i < FB; i++) asm volatile("" : "+v"(b[i]), "+v"(sb[i]));
 }
 
-template <int WM, int WN, int FA, int FB, int NST = 2>
+// The operands of one K step in registers (PIPE), and the wait for their
+// reads with every register tied to it.
+template <int FA, int FB>
+struct GemmOps {
+    u32x4 av[4][FA], bv[4][FB];
+    uint32_t sa[FA], sb[FB];
+};
+template <int FA, int FB>
+RFP4_DEV void gemm_lds_wait_all(GemmOps<FA, FB> &o)
+{
+    asm volatile("s_waitcnt lgkmcnt(0)");
+#pragma unroll
+    for (int t = 0; t < 4; t++) {
+#pragma unroll
+        for (int i = 0; i < FA; i++) asm volatile("" : "+v"(o.av[t][i]));
+#pragma unroll
+        for (int i = 0; i < FB; i++) asm volatile("" : "+v"(o.bv[t][i]));
+    }
+#pragma unroll
+    for (int i = 0; i < FA; i++) asm volatile("" : "+v"(o.sa[i]));
+#pragma unroll
+    for (int i = 0; i < FB; i++) asm volatile("" : "+v"(o.sb[i]));
+}
+
+// PIPE: next step's LDS reads overlap this step's MFMAs (two register sets
+// of operands); without it the reads and MFMAs of a step run back to back.
+template <int WM, int WN, int FA, int FB, int NST = 2, bool PIPE = false>
 RFP4_DEV void gemm_body(const GemmArgs &g)
 {
     static_assert(WM * WN == 4, "4 waves");
@@ -185,6 +211,18 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
     const uint32_t kbytes = g.k >> 1, nsuper = g.k >> 8;
     const uint32_t per = (nsuper + g.kz - 1u) / g.kz;
     const uint32_t s0 = min(nsuper, z * per), s1 = min(nsuper, s0 + per);
+    // K steps in a rotated order: the workgroup's i-th step copies and
+    // multiplies step s0 + (i + rot) % (s1 - s0), rot spread over the W
+    // tiles, so that the workgroups of a launch do not all stream the same K
+    // offset of their rows at once (DMA stream alone at M = 512: 256x128
+    // tiles 15.9 -> 14.8 us, 256x256 25.2 -> 21.6 us).  The sum over K runs
+    // in that order, which depends on the column tile only: an output row
+    // gets the same sums in whichever row tile it sits (batch invariance).
+    const uint32_t nsteps = s1 - s0, rot = nsteps ? (nt * 5u) % nsteps : 0u;
+    auto kstep = [&](uint32_t i) {
+        const uint32_t t = i - s0 + rot;
+        return s0 + (t >= nsteps ? t - nsteps : t);
+    };
 
     // ---- DMA sources.  Code block j of this wave covers tile rows 8 (wave + 4 j) .. +7; lane l
     // fetches logical chunk (l & 7) ^ swz(row) of row 8 (wave + 4 j) + l / 8, which the DMA writes
@@ -216,11 +254,11 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
     do {                                                                                                   \
         rfp4_lds_u8 *st_ = lds + (BUF) * STAGE;                                                            \
         _Pragma("unroll") for (uint32_t j = 0; j < NJ; j++) __builtin_amdgcn_global_load_lds(              \
-            (rfp4_glb_void *)(src[j] + (size_t)(S) * 128u), st_ + 1024u * (wave + 4u * j), 16, 0, 0);     \
+            (rfp4_glb_void *)(src[j] + (size_t)kstep(S) * 128u), st_ + 1024u * (wave + 4u * j), 16, 0, 0); \
         _Pragma("unroll") for (uint32_t b = 0; b < NSB; b++) {                                             \
-            const uint32_t bb = (NST > 2 && wave + 4u * b >= R / 32u) ? 0u : b; /* uniform count: again block 0 */ \
-            if (NST > 2 || wave + 4u * b < R / 32u)                                                        \
-                __builtin_amdgcn_global_load_lds((rfp4_glb_void *)(ssrc[bb] + (size_t)(S) * 256u),           \
+            const uint32_t bb = ((NST > 2 || PIPE) && wave + 4u * b >= R / 32u) ? 0u : b; /* uniform count: again block 0 */ \
+            if (NST > 2 || PIPE || wave + 4u * b < R / 32u)                                                \
+                __builtin_amdgcn_global_load_lds((rfp4_glb_void *)(ssrc[bb] + (size_t)kstep(S) * 256u),    \
                                                  st_ + SC0 + 256u * (wave + 4u * bb), 4, 0, 0);            \
         }                                                                                                  \
     } while (0)
@@ -250,8 +288,10 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
         bsc[fb] = SC0 + 256u * (r >> 5) + 128u * h + 4u * (r & 31u);
     }
 
-    // the first NST - 1 steps in flight, then wait for the first
     constexpr uint32_t C = NJ + NSB; // DMA instructions per step and wave (NST > 2: uniform)
+    uint32_t s = s0;
+    if constexpr (!PIPE) {
+    // the first NST - 1 steps in flight, then wait for the first
     uint32_t issued = 0;
 #pragma unroll
     for (uint32_t k = 0; k + 1u < (uint32_t)NST; k++)
@@ -341,10 +381,102 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
     // own: its wait count is a constant, so the step is one basic block and
     // the MFMAs stay ahead of the wait (with the wait's branches in the
     // loop the compiler sank them below it, serialising MFMA and copies).
-    uint32_t s = s0;
     if constexpr (NST > 2)
         for (; s + (uint32_t)NST - 1u < s1; s++) step(s, std::integral_constant<bool, true>());
     for (; s < s1; s++) step(s, std::integral_constant<bool, false>());
+    } else {
+    // ---- PIPE: the operands of step s + 1 are read from LDS into a second
+    // register set while step s's MFMAs run.  Step s: wait for step s + 1's
+    // DMA and the barrier (after it every wave's copies of s + 1 are in LDS
+    // and every wave's reads of stage s, waited for at the end of step
+    // s - 1, are done), the DMA of step s + NST into stage s's buffer, the
+    // reads of step s + 1, the MFMAs of step s (registers complete), then
+    // the wait for the reads, with the registers tied to it so that no use or
+    // copy of them moves above it.  NST stages give NST - 1 steps of DMA
+    // lookahead.  The MFMA sequence is the same as above (bit-identical).
+    GemmOps<FA, FB> o0, o1;
+    auto reads = [&](uint32_t rs, GemmOps<FA, FB> &o) {
+        const uint32_t stb = (uint32_t)(uintptr_t)(lds + ((rs - s0) % (uint32_t)NST) * STAGE);
+#pragma unroll
+        for (int fa = 0; fa < FA; fa++) gemm_lds_rd4(o.sa[fa], stb + asc[fa]);
+#pragma unroll
+        for (int fb = 0; fb < FB; fb++) gemm_lds_rd4(o.sb[fb], stb + bsc[fb]);
+#pragma unroll
+        for (uint32_t t = 0; t < 4; t++) {
+#pragma unroll
+            for (int fa = 0; fa < FA; fa++) gemm_lds_rd16(o.av[t][fa], stb + aoff[fa] + (((4u * h + t) ^ asw[fa]) << 4));
+#pragma unroll
+            for (int fb = 0; fb < FB; fb++) gemm_lds_rd16(o.bv[t][fb], stb + boff[fb] + (((4u * h + t) ^ bsw[fb]) << 4));
+        }
+    };
+    auto mfmas = [&](const GemmOps<FA, FB> &o) {
+#pragma unroll
+        for (uint32_t t = 0; t < 4; t++)
+#pragma unroll
+            for (int fa = 0; fa < FA; fa++) {
+                const v8i32 a8 = {(int)o.av[t][fa].x, (int)o.av[t][fa].y, (int)o.av[t][fa].z, (int)o.av[t][fa].w, 0, 0, 0, 0};
+                const int sca = (int)((o.sa[fa] >> (8u * t)) & 0xFFu);
+#pragma unroll
+                for (int fb = 0; fb < FB; fb++) {
+                    const v8i32 b8 = {(int)o.bv[t][fb].x, (int)o.bv[t][fb].y, (int)o.bv[t][fb].z, (int)o.bv[t][fb].w,
+                                      0, 0, 0, 0};
+                    const int scb = (int)((o.sb[fb] >> (8u * t)) & 0xFFu);
+                    acc[fa][fb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, acc[fa][fb], MX_FMT_FP4,
+                                                                                  MX_FMT_FP4, 0, sca, 0, scb);
+                }
+            }
+    };
+    auto bar = [&]() {
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
+    // prologue: the first NST steps in flight (one per stage), step s0 landed, its reads
+    uint32_t issued = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < (uint32_t)NST; k++)
+        if (s0 + k < s1) {
+            RFP4_GEMM_DMA(s0 + k, k);
+            issued++;
+        }
+    gemm_wait_steps<C>(issued > 0u ? min(issued - 1u, 3u) : 0u);
+    bar();
+    if (s0 < s1) {
+        reads(s0, o0);
+        gemm_lds_wait_all<FA, FB>(o0);
+    }
+    // a step whose successor exists and whose DMA (step s + NST) is issued:
+    // the wait counts are constants
+    auto step_full = [&](uint32_t fs, GemmOps<FA, FB> &cur, GemmOps<FA, FB> &nxt) {
+        gemm_wait_steps<C>((uint32_t)NST - 2u);
+        bar();
+        RFP4_GEMM_DMA(fs + (uint32_t)NST, (fs - s0) % (uint32_t)NST);
+        reads(fs + 1u, nxt);
+        mfmas(cur);
+        __builtin_amdgcn_sched_barrier(0);
+        gemm_lds_wait_all<FA, FB>(nxt);
+    };
+    auto step_tail = [&](uint32_t ts, GemmOps<FA, FB> &cur, GemmOps<FA, FB> &nxt) {
+        if (ts + 1u < s1) {
+            const uint32_t last = min(ts + (uint32_t)NST - 1u, s1 - 1u); // the last step whose DMA is out
+            gemm_wait_steps<C>(last - (ts + 1u));
+            bar();
+            if (ts + (uint32_t)NST < s1) RFP4_GEMM_DMA(ts + (uint32_t)NST, (ts - s0) % (uint32_t)NST);
+            reads(ts + 1u, nxt);
+        }
+        mfmas(cur);
+        __builtin_amdgcn_sched_barrier(0);
+        if (ts + 1u < s1) gemm_lds_wait_all<FA, FB>(nxt);
+    };
+    for (; s + (uint32_t)NST + 1u < s1; s += 2u) {
+        step_full(s, o0, o1);
+        step_full(s + 1u, o1, o0);
+    }
+    for (; s < s1; s += 2u) { // s - s0 is even here: o0 holds step s
+        step_tail(s, o0, o1);
+        if (s + 1u < s1) step_tail(s + 1u, o1, o0);
+    }
+    }
 #undef RFP4_GEMM_DMA
 
     // ---- epilogue: accumulator r of lane l is C[8 (r/4) + 4 (l/32) + r%4][l%32] of its fragment
@@ -366,7 +498,8 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const uint32_t row = m0 + 32u * fa + 8u * (uint32_t)(r / 4) + 4u * h + (uint32_t)(r % 4);
-                if (row < g.m && col < g.n) dst[(size_t)row * g.n + col] = acc[fa][fb][r];
+                // non-temporal: C is written once and read by the next launch
+                if (row < g.m && col < g.n) __builtin_nontemporal_store(acc[fa][fb][r], dst + (size_t)row * g.n + col);
             }
         }
 }

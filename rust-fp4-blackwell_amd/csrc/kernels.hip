@@ -161,8 +161,12 @@ K256 void rfp4_mma_bf16_tile(MmaTileArgs a) { mma_bf16_tile_body(a); }
 
 // ---- batched MXFP4 GEMM: rfp4_gemm_<BM>x<BN> (4 waves in WM x WN, wave tile 32FA x 32FB).
 // The host picks among these (runtime.cpp gemm_plan); keep the lists in sync.
+// Tiles whose two register sets of operands fit beside the accumulators run
+// the pipelined K loop (the next step's LDS reads under this step's MFMAs);
+// the 256x256 tile (8 fragments per wave) keeps the serial one.
+#define GEMM_PIPE(FA, FB) ((FA) + (FB) <= 6)
 #define GEMM_KERNEL(BM, BN, WM, WN, FA, FB) \
-    K256 void rfp4_gemm_##BM##x##BN(GemmArgs a) { gemm_body<WM, WN, FA, FB>(a); }
+    K256 void rfp4_gemm_##BM##x##BN(GemmArgs a) { gemm_body<WM, WN, FA, FB, 2, GEMM_PIPE(FA, FB)>(a); }
 GEMM_KERNEL(32, 128, 1, 4, 1, 1)
 GEMM_KERNEL(64, 128, 2, 2, 1, 2)
 GEMM_KERNEL(128, 128, 2, 2, 2, 2)
@@ -171,7 +175,7 @@ GEMM_KERNEL(256, 256, 2, 2, 4, 4)
 // deeper DMA pipelines (NST stages, NST - 1 steps of lookahead) for the
 // small tiles: rfp4_gemm_<BM>x<BN>_p<NST>
 #define GEMM_KERNEL_P(BM, BN, WM, WN, FA, FB, NST) \
-    K256 void rfp4_gemm_##BM##x##BN##_p##NST(GemmArgs a) { gemm_body<WM, WN, FA, FB, NST>(a); }
+    K256 void rfp4_gemm_##BM##x##BN##_p##NST(GemmArgs a) { gemm_body<WM, WN, FA, FB, NST, GEMM_PIPE(FA, FB)>(a); }
 GEMM_KERNEL_P(32, 128, 1, 4, 1, 1, 4)
 GEMM_KERNEL_P(64, 128, 2, 2, 1, 2, 4)
 GEMM_KERNEL_P(64, 128, 2, 2, 1, 2, 3)
