@@ -447,13 +447,66 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
     }
     // a step whose successor exists and whose DMA (step s + NST) is issued:
     // the wait counts are constants
+    // One wave issues its DMA, LDS reads and MFMAs in program order, and a
+    // DMA instruction waits at issue while the CU's memory path is busy (about
+    // 60 cycles each, measured), an LDS read while the LDS is: issued back to
+    // back the three phases of a 256x128 step took 0.38 + 0.27 + 0.47 us.
+    // So the step's DMA and reads go between its MFMAs (MFMA i, then memory
+    // instructions i NMEM / NM .. (i + 1) NMEM / NM - 1, alternating DMA and
+    // reads), each group pinned by a scheduling barrier; an MFMA runs in its
+    // pipe while the next instructions wait to issue.  Each accumulator's
+    // MFMAs keep their order (t = 0..3), so the sums are unchanged.
+    constexpr int NM = 4 * FA * FB, ND = (int)C, NR = 5 * (FA + FB), NMEM = ND + NR;
+    auto mem_op = [&](int j, uint32_t dstep, uint32_t dbuf, uint32_t rstb, GemmOps<FA, FB> &o) {
+        // merged order: DMA 0, read 0, DMA 1, read 1, ..., then the rest of the longer list
+        const int pairs = ND < NR ? ND : NR;
+        int d = -1, r = -1;
+        if (j < 2 * pairs) (j & 1) ? (r = j >> 1) : (d = j >> 1);
+        else if (ND > NR) d = j - pairs;
+        else r = j - pairs;
+        if (d >= 0) {
+            rfp4_lds_u8 *st_ = lds + dbuf * STAGE;
+            if (d < (int)NJ) {
+                __builtin_amdgcn_global_load_lds((rfp4_glb_void *)(src[d] + (size_t)kstep(dstep) * 128u),
+                                                 st_ + 1024u * (wave + 4u * (uint32_t)d), 16, 0, 0);
+            } else {
+                const uint32_t b = (uint32_t)d - NJ;
+                const uint32_t bb = wave + 4u * b >= R / 32u ? 0u : b; // uniform count: again block 0
+                __builtin_amdgcn_global_load_lds((rfp4_glb_void *)(ssrc[bb] + (size_t)kstep(dstep) * 256u),
+                                                 st_ + SC0 + 256u * (wave + 4u * bb), 4, 0, 0);
+            }
+        }
+        if (r >= 0) {
+            if (r < FA) gemm_lds_rd4(o.sa[r], rstb + asc[r]);
+            else if (r < FA + FB) gemm_lds_rd4(o.sb[r - FA], rstb + bsc[r - FA]);
+            else {
+                const int q = r - FA - FB, t = q / (FA + FB), f = q % (FA + FB);
+                if (f < FA) gemm_lds_rd16(o.av[t][f], rstb + aoff[f] + (((4u * h + (uint32_t)t) ^ asw[f]) << 4));
+                else gemm_lds_rd16(o.bv[t][f - FA], rstb + boff[f - FA] + (((4u * h + (uint32_t)t) ^ bsw[f - FA]) << 4));
+            }
+        }
+    };
     auto step_full = [&](uint32_t fs, GemmOps<FA, FB> &cur, GemmOps<FA, FB> &nxt) {
         gemm_wait_steps<C>((uint32_t)NST - 2u);
         bar();
-        RFP4_GEMM_DMA(fs + (uint32_t)NST, (fs - s0) % (uint32_t)NST);
-        reads(fs + 1u, nxt);
-        mfmas(cur);
+        const uint32_t dbuf = (fs - s0) % (uint32_t)NST;
+        const uint32_t rstb = (uint32_t)(uintptr_t)(lds + ((fs + 1u - s0) % (uint32_t)NST) * STAGE);
         __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < NM; i++) {
+            const int t = i / (FA * FB), fa = (i / FB) % FA, fb = i % FB;
+            const v8i32 a8 = {(int)cur.av[t][fa].x, (int)cur.av[t][fa].y, (int)cur.av[t][fa].z, (int)cur.av[t][fa].w,
+                              0, 0, 0, 0};
+            const v8i32 b8 = {(int)cur.bv[t][fb].x, (int)cur.bv[t][fb].y, (int)cur.bv[t][fb].z, (int)cur.bv[t][fb].w,
+                              0, 0, 0, 0};
+            const int sca = (int)((cur.sa[fa] >> (8u * (uint32_t)t)) & 0xFFu);
+            const int scb = (int)((cur.sb[fb] >> (8u * (uint32_t)t)) & 0xFFu);
+            acc[fa][fb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, acc[fa][fb], MX_FMT_FP4, MX_FMT_FP4,
+                                                                          0, sca, 0, scb);
+#pragma unroll
+            for (int j = i * NMEM / NM; j < (i + 1) * NMEM / NM; j++) mem_op(j, fs + (uint32_t)NST, dbuf, rstb, nxt);
+            __builtin_amdgcn_sched_barrier(0);
+        }
         gemm_lds_wait_all<FA, FB>(nxt);
     };
     auto step_tail = [&](uint32_t ts, GemmOps<FA, FB> &cur, GemmOps<FA, FB> &nxt) {
