@@ -10,6 +10,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <atomic>
 #include <mutex>
 #include <string>
 #include <unordered_map>
@@ -1129,11 +1130,25 @@ struct GemmTile {
     uint32_t occ; // workgroups per CU (registers / LDS of the compiled kernel)
 };
 // Compiled tile shapes (kernels.hip GEMM_KERNEL), largest first.
+// (occ: workgroups per CU of the double-buffered kernel as this build compiles
+// it, used when no runtime is initialised; gemm_occ asks the runtime)
 constexpr GemmTile kGemmTiles[] = {
-    {256, 256, "rfp4_gemm_256x256", 1}, {256, 128, "rfp4_gemm_256x128", 1}, {128, 128, "rfp4_gemm_128x128", 2},
-    {64, 128, "rfp4_gemm_64x128", 3},   {32, 128, "rfp4_gemm_32x128", 3},
+    {256, 256, "rfp4_gemm_256x256", 1}, {256, 128, "rfp4_gemm_256x128", 1}, {128, 128, "rfp4_gemm_128x128", 1},
+    {64, 128, "rfp4_gemm_64x128", 2},   {32, 128, "rfp4_gemm_32x128", 3},
 };
 constexpr int kGemmNumTiles = (int)(sizeof(kGemmTiles) / sizeof(kGemmTiles[0]));
+// Workgroups of tile i's double-buffered kernel that fit one CU (registers
+// and LDS of the compiled code object), asked once per process.
+uint32_t gemm_occ(int i)
+{
+    static std::atomic<uint32_t> occ[kGemmNumTiles];
+    uint32_t v = occ[i].load(std::memory_order_relaxed);
+    if (v) return v;
+    int per_cu = 0;
+    if (!g_rt || kernel_occupancy(kGemmTiles[i].name, 256, 0, &per_cu) || per_cu <= 0) return kGemmTiles[i].occ;
+    occ[i].store((uint32_t)per_cu, std::memory_order_relaxed);
+    return (uint32_t)per_cu;
+}
 // plan index of the few-row kernel (gemm_rows.h): 16 * MA activation rows,
 // 16 W rows per workgroup, at most SEG (nb) K segments of 512 per wave
 constexpr int kGemmSkinny = kGemmNumTiles;
@@ -1149,10 +1164,14 @@ struct GemmPlan {
 };
 
 
-// The deepest K pipeline compiled for a tile (kernels.hip GEMM_KERNEL_P): 4
-// stages for 32x128 and 64x128, 3 for 128x128 and 256x128, else double
-// buffering.
-int gemm_deep_stages(int tile) { return tile == 3 || tile == 4 ? 4 : tile == 1 || tile == 2 ? 3 : 2; }
+// The K pipeline for a grid of one round of one workgroup per CU: 4 stages
+// for 32x128 and 64x128, 3 for 128x128; 256x128, whose pipelined K loop
+// already reads the next step under this step's MFMAs, keeps double
+// buffering (14336x4096 at M = 512: 25.4 vs 29.2 us with 3 stages); 256x256
+// has one.  (128x128 alone measured about 6 % faster double-buffered, but
+// 3 stages inside the 8B layer sequence of the config-5 stack: 3518-3530 vs
+// 3593-3614 us, same process.)
+int gemm_deep_stages(int tile) { return tile == 3 || tile == 4 ? 4 : tile == 2 ? 3 : 2; }
 
 // The few-row kernel: at most 64 activation rows, K a multiple of 512 in at
 // most 8 waves of up to 4 segments (2 for 64 rows).
@@ -1223,12 +1242,12 @@ static GemmPlan gemm_plan_tile(uint32_t m, uint32_t n, uint32_t k, uint32_t num_
         for (int i = 0; i < kGemmNumTiles; i++) {
             const GemmTile &t = kGemmTiles[i];
             if ((uint64_t)ceil_div(m, t.bm) * t.bm * 4u > (uint64_t)m * 5u) continue; // > 25% padding
-            const uint64_t nt = (uint64_t)ceil_div(m, t.bm) * ceil_div(n, t.bn), slots = (uint64_t)t.occ * num_cus;
+            const uint64_t nt = (uint64_t)ceil_div(m, t.bm) * ceil_div(n, t.bn), slots = (uint64_t)gemm_occ(i) * num_cus;
             const uint64_t rounds = (nt + slots - 1) / slots;
             const double fill = (double)nt / (double)(rounds * slots);
             const bool better = best < 0 || rounds < best_rounds ||
                                 (rounds == best_rounds && (fill > best_fill + 0.01 ||
-                                                           (fill > best_fill - 0.01 && t.occ > kGemmTiles[best].occ)));
+                                                           (fill > best_fill - 0.01 && gemm_occ(i) > gemm_occ(best))));
             if (better) best = i, best_rounds = rounds, best_fill = fill;
         }
         // (a grid under half the CUs goes to the K-split rule below)
@@ -1243,17 +1262,18 @@ static GemmPlan gemm_plan_tile(uint32_t m, uint32_t n, uint32_t k, uint32_t num_
         const uint64_t nt = (uint64_t)ceil_div(m, t.bm) * ceil_div(n, t.bn);
         if ((uint64_t)ceil_div(m, t.bm) * t.bm * 4u <= (uint64_t)m * 5u && nt * 8u >= 7ull * num_cus && nt < num_cus)
             return {0, 1u};
-        // likewise one round of 256x128 tiles (which then take the 3-stage
-        // pipeline) over two rounds of 128x128: 14336x4096 at M = 512 31.6
-        // vs 37.8 us
+        // likewise one round of 256x128 tiles over two rounds of 128x128:
+        // 14336x4096 at M = 512 25.4 us (double-buffered, pipelined loop)
+        // against 32.8; 28672x4096 at M = 256 26.4 against 34.0
         const GemmTile &t1 = kGemmTiles[1];
         const uint64_t nt1 = (uint64_t)ceil_div(m, t1.bm) * ceil_div(n, t1.bn);
         if ((uint64_t)ceil_div(m, t1.bm) * t1.bm * 4u <= (uint64_t)m * 5u && nt1 * 8u >= 7ull * num_cus && nt1 < num_cus)
             return {1, 1u};
-        // and one round of 128x128 tiles over at least 3/4 of the CUs (3
-        // stages) over 64x128 tiles past one per CU: 6144x4096 at M = 512
-        // 18.3 vs 19.2 us, 28672x4096 at M = 128 23.2 vs 29.8, 4096x14336
-        // at M = 768 50.9 vs 63.7
+        // and one round of 128x128 tiles over at least 3/4 of the CUs over
+        // 64x128 tiles past one per CU: alone about equal (6144x4096 at M =
+        // 512 15.9-16.2 vs 14.9-15.2 us), but inside the 8B layer sequence
+        // of the config-5 stack the q|k|v shape on 128x128 saves about 2 us
+        // per layer (stack 3587 vs 3656-3670 us, same process)
         const GemmTile &t2 = kGemmTiles[2];
         const uint64_t nt2 = (uint64_t)ceil_div(m, t2.bm) * ceil_div(n, t2.bn);
         if ((uint64_t)ceil_div(m, t2.bm) * t2.bm * 4u <= (uint64_t)m * 5u && nt2 * 4u >= 3ull * num_cus && nt2 < num_cus)
@@ -1266,18 +1286,18 @@ static GemmPlan gemm_plan_tile(uint32_t m, uint32_t n, uint32_t k, uint32_t num_
     }
     const uint64_t tiles = (uint64_t)ceil_div(m, kGemmTiles[pick].bm) * ceil_div(n, kGemmTiles[pick].bn);
     if (t_gemm_kz > 0) return {pick, std::min<uint32_t>((uint32_t)t_gemm_kz, nsuper)};
-    // at least 7/8 of the CUs covered: no K split (its partial sums and the
-    // reduce cost more than the idle eighth: 8B gate|up at M = 32, 224 tiles,
-    // 17.0 vs 19.7 us split in two)
-    if (tiles * 8u >= 7ull * num_cus && tiles < num_cus) return {pick, 1u};
     if (tiles >= num_cus) {
         // long K at about one workgroup per CU: two K splits let two
         // workgroups per CU overlap their serial chains of K steps (8B down
-        // at M = 512: 64x128, 56 steps, 51 -> 37 us), if the workspace holds them
+        // at M = 512: 64x128, 56 steps, 51 -> 37 us before the pipelined
+        // loop), if the workspace holds them
         if (nsuper >= 32u && tiles < 2ull * num_cus && 2ull * m * n <= kGemmPartFloats) {
             // or the next tile up in two splits as one round with a deeper
             // pipeline (8B down at M = 512: 128x128 in two splits, 3 stages,
-            // 35.5 us against 48-50 for 64x128 in two)
+            // 35.5 us against 48-50 for 64x128 in two before the pipelined
+            // loop; since, alone, 29-33 us against 28 for 64x128 unsplit with
+            // 4 stages, but inside the config-5 stack's layer sequence the
+            // split plan stays ahead)
             const GemmTile &u = kGemmTiles[2];
             const uint64_t tu = (uint64_t)ceil_div(m, u.bm) * ceil_div(n, u.bn);
             if (pick == 3 && (uint64_t)ceil_div(m, u.bm) * u.bm * 4u <= (uint64_t)m * 5u && 2u * tu <= num_cus &&
@@ -1287,6 +1307,12 @@ static GemmPlan gemm_plan_tile(uint32_t m, uint32_t n, uint32_t k, uint32_t num_
         }
         return {pick, 1u};
     }
+    // short K over at least half the CUs: no split either (its partial sums
+    // cost more than the idle CUs: 6144x4096 at M = 128, 192 tiles of 32x128,
+    // 8.2 vs 11.1 us split in two; 4096x4096 at M = 128, 128 tiles, 8.0 vs
+    // 9.9; 8B gate|up at M = 32, 224 tiles, 17.0 vs 19.7)
+    if (nsuper < 32u && 2u * tiles >= num_cus) return {pick, 1u};
+    if (tiles * 8u >= 7ull * num_cus) return {pick, 1u};
     // steps per split: as few as reach one workgroup per CU; kz = ceil(nsuper / per) leaves no split empty
     uint32_t per = std::max<uint32_t>(1u, nsuper / ceil_div(num_cus, tiles));
     uint32_t kz = ceil_div(nsuper, per);

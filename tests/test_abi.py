@@ -97,7 +97,8 @@ def test_shape_errors_need_no_device():
 def test_gemm_plan_shapes(m, n, k):
     """The automatic GEMM plan (256 CUs without a device): a compiled tile, no
     empty K split, the split-K partials fit the workspace, and the CUs covered
-    (at least 7/8 of them, at least half from 1024 rows) unless the K split
+    (at least 7/8 of them; at least half from 1024 rows or with a short K,
+    under 32 steps, which runs unsplit from half the CUs) unless the K split
     is at its maximum."""
     tm, tn, kz = rfp4.gemm_plan(m, n, k)
     if m <= 32 and k % 512 == 0:   # few-row kernel: kz = W fragments per workgroup
@@ -110,21 +111,23 @@ def test_gemm_plan_shapes(m, n, k):
     assert 1 <= kz <= nsuper and (kz - 1) * per < nsuper
     assert kz == 1 or kz * m * n <= (8 << 20)
     tiles = -(-m // tm) * -(-n // tn)
-    cover = 128 if m >= 1024 else 224
+    cover = 128 if m >= 1024 or nsuper < 32 else 224
     assert tiles * kz >= cover or kz == nsuper or (kz + 1) * m * n > (8 << 20)
     if m > 32:
         assert -(-m // tm) * tm <= 1.25 * m or tm == 32   # bounded row padding
 
 
 @pytest.mark.parametrize("m,n,k,plan", [
-    (512, 28672, 4096, (256, 256, 1)),   # one round of 256x256 at 7/8 of the CUs (50 vs 66 us)
-    (512, 4096, 14336, (128, 128, 2)),   # long K: one round of 128x128 in two splits, 3 stages (35.5 vs 48-50 us)
-    (512, 14336, 4096, (256, 128, 1)),   # one round of 256x128, 3 stages (31.6 vs 37.8 us for 128x128)
-    (512, 6144, 4096, (128, 128, 1)),   # one round of 128x128 over 3/4 of the CUs, 3 stages (18.3 vs 19.2 us)
-    (128, 28672, 4096, (128, 128, 1)),  # the same rule (23.2 vs 29.8 us)
-    (2048, 6144, 4096, (256, 256, 1)),   # fewest resident rounds (49.6 vs 60.0 us)
-    (2048, 4096, 4096, (128, 128, 1)),   # (29.6 vs 33.2 us)
-    (2048, 4096, 14336, (128, 128, 1)),  # (82.2 vs 90.2 us)
+    (512, 28672, 4096, (256, 256, 1)),   # one round of 256x256 at 7/8 of the CUs (47.9 us, best of the sweep)
+    (512, 4096, 14336, (128, 128, 2)),   # long K: one round of 128x128 in two splits, 3 stages (ahead inside the stack)
+    (512, 14336, 4096, (256, 128, 1)),   # one round of 256x128, double-buffered (25.4 vs 29.2 us with 3 stages)
+    (512, 6144, 4096, (128, 128, 1)),    # one round of 128x128 over 3/4 of the CUs (in the stack, 2 us per layer less than 64x128)
+    (128, 28672, 4096, (128, 128, 1)),   # the same rule (18.5 vs 18.8 us for 64x128)
+    (128, 6144, 4096, (32, 128, 1)),     # short K over 3/4 of the CUs unsplit (8.2 vs 11.1 us in two splits)
+    (256, 28672, 4096, (256, 128, 1)),   # one round of 256x128 (26.4 vs 34.0 us for 128x128)
+    (2048, 6144, 4096, (256, 256, 1)),   # fewest resident rounds (49.7 us, within 2 % of the best)
+    (2048, 4096, 4096, (256, 128, 1)),   # (27.3 vs 34.0 us for 128x128)
+    (2048, 4096, 14336, (256, 128, 1)),  # (77.7 vs 92.1 us for 128x128)
     (2048, 28672, 4096, (256, 256, 1)),
     (32, 28672, 4096, (32, 64, 4)),      # few rows, 4 W fragments (17.7 us vs 21.5 tiled)
     (32, 6144, 4096, (32, 32, 2)),       # few rows, 2 W fragments (6.9 vs 7.9 with one)
