@@ -252,6 +252,13 @@ int rfp4_debug_gemm_plan(int tile, int kz);
  * where a kernel is compiled for the tile; others fail at launch).  No
  * reference counterpart. */
 int rfp4_debug_gemm_stages(int nst);
+/* Test hook (this thread): the 8-wave ping-pong kernels of the 256x256 and
+ * 256x128 tiles (two waves per SIMD, one running MFMAs while the other issues
+ * the next copies and LDS reads; bit-identical to the 4-wave kernels): 0 =
+ * the planner's choice, 1 = 4-wave kernels only, 2 = ping-pong wherever the
+ * plan picks one of those tiles and the matrices' codes stay under 4 GiB.  No
+ * reference counterpart. */
+int rfp4_debug_gemm_pp(int mode);
 /* Test hook (this thread): 1 = every split-K sum of later fp4_gemm calls in
  * the reduce kernel launched after the GEMM; 0 = two-way splits summed inside
  * the GEMM launch by the last split of each tile (the default; the same

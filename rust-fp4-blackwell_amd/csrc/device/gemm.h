@@ -557,6 +557,233 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
         }
 }
 
+// Ping-pong tiled GEMM: 8 waves, two per SIMD, in two groups.  Group g of
+// the workgroup (g = wave >> 2; waves w and w + 4 share SIMD w % 4) computes
+// tile rows 32 FA g .. +32 FA - 1, wave w % 4 of it the columns 32 FB (w % 4)
+// .. +32 FB - 1; block tile BM = 64 FA by BN = 128 FB, the same stage layout
+// and DMA sources as gemm_body.  A K step runs as two halves (MFMA groups
+// t = 0, 1 and t = 2, 3), each a memory phase (group 0 only: this half's
+// share of the next step's DMA; both: the half's operand reads from LDS,
+// waited for) and a compute phase (MFMAs only), one workgroup barrier after
+// each phase.  Group 1 starts one barrier late, so on every SIMD one wave
+// computes while the other issues its copies and reads: the DMA instructions
+// that wait at issue no longer hold back the MFMAs.  Barrier events E_0,
+// E_1, ...: group 0's memory phase of half-step q (q = 2 (s - s0) + half)
+// runs between E_2q and E_2q+1, its compute phase until E_2q+2; group 1's
+// phases one event later.  Stage s is complete at E_4(s - s0) (group 0 waits
+// for its DMA at the end of the compute phase of half-step 2 (s - s0) - 1);
+// group 1 finishes reading stage s - 1 before E_4(s - s0), after which group
+// 0 copies step s + 1 into that buffer (the weight rows in half 0, the
+// activation rows in half 1).
+// Both groups pass the same number of barriers (group 1 one extra at the
+// start, group 0 one at the end).  Every accumulator receives its MFMAs in
+// gemm_body's order (steps in the rotated order, t = 0..3), so C is
+// bit-identical to gemm_body's.  No split-K sum in the launch (kz > 1 writes
+// the partial planes for the reduce kernel).
+template <int FA, int FB>
+RFP4_DEV void gemm_pp_body(const GemmArgs &g)
+{
+    constexpr uint32_t BM = 64u * FA, BN = 128u * FB, R = BM + BN;
+    constexpr uint32_t NJ = R / 32u;                 // 8-row code blocks per group-0 wave per step
+    constexpr uint32_t NSB = (R / 32u + 3u) / 4u;    // 32-row scale blocks per group-0 wave per step
+    static_assert(R % 128u == 0u, "every group-0 wave copies the same number of blocks");
+    constexpr uint32_t SC0 = R * 128u, STAGE = R * 128u + R * 8u;
+    __shared__ __attribute__((aligned(1024))) uint8_t lds_raw[2 * STAGE];
+    rfp4_lds_u8 *lds = (rfp4_lds_u8 *)lds_raw;
+
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t grp = wave >> 2, wv = wave & 3u;
+    const uint32_t r32 = lane & 31u, h = lane >> 5;
+
+    const uint32_t total = gridDim.x, L = blockIdx.x, q = total >> 3;
+    const uint32_t lg = (L < q * 8u) ? (L & 7u) * q + (L >> 3) : L;
+    const uint32_t mt_n = (g.m + BM - 1u) / BM, nt_n = (g.n + BN - 1u) / BN;
+    const uint32_t mt = lg % mt_n, rest = lg / mt_n, nt = rest % nt_n, z = rest / nt_n;
+    const uint32_t kbytes = g.k >> 1, nsuper = g.k >> 8;
+    const uint32_t per = (nsuper + g.kz - 1u) / g.kz;
+    const uint32_t s0 = min(nsuper, z * per), s1 = min(nsuper, s0 + per);
+    const uint32_t nsteps = s1 - s0, rot = nsteps ? (nt * 5u) % nsteps : 0u;
+    auto kstep = [&](uint32_t i) {
+        const uint32_t t = i - s0 + rot;
+        return s0 + (t >= nsteps ? t - nsteps : t);
+    };
+
+    // DMA of a group-0 wave: half 0 the weight rows of step S, half 1 the
+    // activation rows.  Sources are 32-bit offsets from the matrix bases (the
+    // host keeps each matrix's codes and step-blocked scales under 4 GiB),
+    // formed at each copy from the lane index, made opaque per call: kept
+    // across the loop they would not fit beside the accumulators.
+    auto dma = [&](uint32_t S, uint32_t buf, int half) {
+        rfp4_lds_u8 *st = lds + buf * STAGE;
+        const size_t ko = (size_t)kstep(S) * 128u, so = (size_t)kstep(S) * 256u;
+        uint32_t ln = lane;
+        asm volatile("" : "+v"(ln));
+#pragma unroll
+        for (uint32_t j = 0; j < NJ; j++) {
+            const bool is_a = 8u * (4u * j) < BM; // rows 8 (wv + 4 j) .. +7 < BM for every wv
+            if (is_a != (half == 1)) continue;
+            const uint32_t row = 8u * (wv + 4u * j) + (ln >> 3);
+            const uint32_t qq = (ln & 7u) ^ gemm_swz(row);
+            const uint32_t off = is_a ? min(mt * BM + row, g.m - 1u) * kbytes + qq * 16u
+                                      : min(nt * BN + (row - BM), g.n - 1u) * kbytes + qq * 16u;
+            __builtin_amdgcn_global_load_lds((rfp4_glb_void *)((is_a ? g.a_codes : g.w_codes) + ko + off),
+                                             st + 1024u * (wv + 4u * j), 16, 0, 0);
+        }
+#pragma unroll
+        for (uint32_t b = 0; b < NSB; b++) {
+            const bool is_a = 4u * b < BM / 32u; // block wv + 4 b < BM / 32 for every wv
+            if (is_a != (half == 1)) continue;
+            const uint32_t tb = wv + 4u * b;
+            const uint32_t blk = is_a ? min(mt * (BM / 32u) + tb, (g.m - 1u) >> 5)
+                                      : min(nt * (BN / 32u) + (tb - BM / 32u), (g.n - 1u) >> 5);
+            __builtin_amdgcn_global_load_lds((rfp4_glb_void *)((is_a ? g.a_st : g.w_st) + so + blk * nsuper * 256u + ln * 4u),
+                                             st + SC0 + 256u * tb, 4, 0, 0);
+        }
+    };
+
+    v16f32 acc[FA][FB];
+#pragma unroll
+    for (int fa = 0; fa < FA; fa++)
+#pragma unroll
+        for (int fb = 0; fb < FB; fb++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[fa][fb][r] = 0.0f;
+
+    // fragment rows of this lane: the row's offset with its swizzled chunk
+    // of t = 0, and its scale word (plane h of the row's block)
+    uint32_t aoff[FA], boff[FB], asc[FA], bsc[FB];
+#pragma unroll
+    for (int fa = 0; fa < FA; fa++) {
+        const uint32_t r = grp * (32u * FA) + 32u * fa + r32;
+        aoff[fa] = r * 128u + (((4u * h) ^ gemm_swz(r)) << 4);
+        asc[fa] = SC0 + 256u * (r >> 5) + 128u * h + 4u * (r & 31u);
+    }
+#pragma unroll
+    for (int fb = 0; fb < FB; fb++) {
+        const uint32_t r = BM + wv * (32u * FB) + 32u * fb + r32;
+        boff[fb] = r * 128u + (((4u * h) ^ gemm_swz(r)) << 4);
+        bsc[fb] = SC0 + 256u * (r >> 5) + 128u * h + 4u * (r & 31u);
+    }
+
+    u32x4 av[2][FA], bv[2][FB];
+    uint32_t sa[FA], sb[FB];
+    auto bar = [&]() {
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+    };
+    // memory phase of (step S, half): this half's operand reads of stage S
+    // (the scale words in half 0), then the wait for them with every register
+    // tied to it
+    auto reads = [&](uint32_t S, int half) {
+        uint32_t stb = (uint32_t)(uintptr_t)(lds + ((S - s0) & 1u) * STAGE);
+        // opaque to the compiler, so that the 4 (FA + FB) read addresses are
+        // formed here (one XOR each) rather than kept in registers across the loop
+        asm volatile("" : "+v"(stb));
+        if (half == 0) {
+#pragma unroll
+            for (int fa = 0; fa < FA; fa++) gemm_lds_rd4(sa[fa], stb + asc[fa]);
+#pragma unroll
+            for (int fb = 0; fb < FB; fb++) gemm_lds_rd4(sb[fb], stb + bsc[fb]);
+        }
+        // stage bases are 1 KB aligned and rows 128 bytes, so the chunk
+        // offset ((4 h + t) ^ swz) << 4 = (4 h ^ swz) << 4 ^ t << 4 is ORed in
+#pragma unroll
+        for (uint32_t u = 0; u < 2; u++) {
+            const uint32_t t = 2u * (uint32_t)half + u;
+#pragma unroll
+            for (int fa = 0; fa < FA; fa++) gemm_lds_rd16(av[u][fa], (stb + aoff[fa]) ^ (t << 4));
+#pragma unroll
+            for (int fb = 0; fb < FB; fb++) gemm_lds_rd16(bv[u][fb], (stb + boff[fb]) ^ (t << 4));
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)");
+#pragma unroll
+        for (uint32_t u = 0; u < 2; u++) {
+#pragma unroll
+            for (int fa = 0; fa < FA; fa++) asm volatile("" : "+v"(av[u][fa]));
+#pragma unroll
+            for (int fb = 0; fb < FB; fb++) asm volatile("" : "+v"(bv[u][fb]));
+        }
+#pragma unroll
+        for (int fa = 0; fa < FA; fa++) asm volatile("" : "+v"(sa[fa]));
+#pragma unroll
+        for (int fb = 0; fb < FB; fb++) asm volatile("" : "+v"(sb[fb]));
+    };
+    // MFMA group t takes byte t of each scale word (the instruction's
+    // scale byte select), so no byte is extracted into a register of its own
+    auto mfma_t = [&](uint32_t u, auto t_c) {
+        constexpr int T = decltype(t_c)::value;
+#pragma unroll
+        for (int fa = 0; fa < FA; fa++) {
+            const v8i32 a8 = {(int)av[u][fa].x, (int)av[u][fa].y, (int)av[u][fa].z, (int)av[u][fa].w, 0, 0, 0, 0};
+#pragma unroll
+            for (int fb = 0; fb < FB; fb++) {
+                const v8i32 b8 = {(int)bv[u][fb].x, (int)bv[u][fb].y, (int)bv[u][fb].z, (int)bv[u][fb].w, 0, 0, 0, 0};
+                acc[fa][fb] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a8, b8, acc[fa][fb], MX_FMT_FP4, MX_FMT_FP4,
+                                                                              T, (int)sa[fa], T, (int)sb[fb]);
+            }
+        }
+    };
+    // a half's MFMAs, then every accumulator tied to an empty volatile asm:
+    // MFMAs have no side effects, and without the tie the compiler sinks
+    // them below the barrier that ends the compute phase
+    auto mfmas = [&](int half) {
+        if (half == 0) {
+            mfma_t(0u, std::integral_constant<int, 0>());
+            mfma_t(1u, std::integral_constant<int, 1>());
+        } else {
+            mfma_t(0u, std::integral_constant<int, 2>());
+            mfma_t(1u, std::integral_constant<int, 3>());
+        }
+#pragma unroll
+        for (int fa = 0; fa < FA; fa++)
+#pragma unroll
+            for (int fb = 0; fb < FB; fb++) asm volatile("" : "+v"(acc[fa][fb]));
+    };
+
+    // prologue: group 0 copies step s0 and waits for it (E_0 makes it visible)
+    if (grp == 0u && s0 < s1) {
+        dma(s0, 0u, 0);
+        dma(s0, 0u, 1);
+        __builtin_amdgcn_s_waitcnt(0x0f70); // vmcnt(0)
+    }
+    bar();
+    if (grp == 1u) bar(); // group 1 one phase behind
+    for (uint32_t s = s0; s < s1; s++) {
+        const uint32_t nbuf = ((s - s0) & 1u) ^ 1u;
+        const bool more = s + 1u < s1;
+#pragma unroll
+        for (int half = 0; half < 2; half++) {
+            __builtin_amdgcn_sched_barrier(0);
+            if (grp == 0u && more) dma(s + 1u, nbuf, half);
+            reads(s, half);
+            __builtin_amdgcn_sched_barrier(0);
+            bar();
+            __builtin_amdgcn_sched_barrier(0);
+            mfmas(half);
+            __builtin_amdgcn_sched_barrier(0);
+            if (half == 1 && grp == 0u && more) __builtin_amdgcn_s_waitcnt(0x0f70); // step s + 1 landed
+            bar();
+        }
+    }
+    if (grp == 0u) bar(); // the barrier count of group 1
+
+    const uint32_t m0 = mt * BM + grp * (32u * FA), n0 = nt * BN + wv * (32u * FB);
+    float *dst = g.kz > 1u ? g.part + (size_t)z * g.m * g.n : g.c;
+#pragma unroll
+    for (int fa = 0; fa < FA; fa++)
+#pragma unroll
+        for (int fb = 0; fb < FB; fb++) {
+            const uint32_t col = n0 + 32u * fb + r32;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const uint32_t row = m0 + 32u * fa + 8u * (uint32_t)(r / 4) + 4u * h + (uint32_t)(r % 4);
+                if (row < g.m && col < g.n) __builtin_nontemporal_store(acc[fa][fb][r], dst + (size_t)row * g.n + col);
+            }
+        }
+}
+
 // Split-K sum: c = part[0] + part[1] + ... + part[kz-1] in that order (the
 // launch after the GEMM on the same stream, so no cross-workgroup ordering is
 // needed).  Four floats per thread.

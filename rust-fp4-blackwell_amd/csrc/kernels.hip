@@ -181,6 +181,12 @@ GEMM_KERNEL_P(64, 128, 2, 2, 1, 2, 4)
 GEMM_KERNEL_P(64, 128, 2, 2, 1, 2, 3)
 GEMM_KERNEL_P(128, 128, 2, 2, 2, 2, 3)
 GEMM_KERNEL_P(256, 128, 2, 2, 4, 2, 3)
+// 8-wave ping-pong tiles (two waves per SIMD, one computing while the other
+// copies and reads): rfp4_gemm_<BM>x<BN>_pp, wave tile 32FA x 32FB
+#define GEMM_KERNEL_PP(BM, BN, FA, FB) \
+    K512 void rfp4_gemm_##BM##x##BN##_pp(GemmArgs a) { gemm_pp_body<FA, FB>(a); }
+GEMM_KERNEL_PP(256, 256, 4, 2)
+GEMM_KERNEL_PP(256, 128, 4, 1)
 K256 void rfp4_gemm_reduce(GemmArgs a) { gemm_reduce_body(a); }
 // row-major E8M0 scales -> the step-blocked copy the tiled kernels read
 K256 void rfp4_scales_tile(ScaleTileArgs a) { scales_tile_body(a); }

@@ -1155,6 +1155,7 @@ constexpr int kGemmSkinny = kGemmNumTiles;
 thread_local int t_gemm_tile = -1, t_gemm_kz = 0;
 thread_local int t_gemm_reduce_kernel = 0; // 1: split-K sums always in the reduce kernel
 thread_local int t_gemm_stages = 0; // DMA stages of the tiled GEMM (0 / 2: double buffer; 3, 4 where compiled)
+thread_local int t_gemm_pp = 0;     // 0: automatic, 1: 4-wave kernels only, 2: ping-pong wherever compiled
 
 struct GemmPlan {
     int tile;
@@ -1338,6 +1339,18 @@ GemmPlan gemm_plan(uint32_t m, uint32_t n, uint32_t k, uint32_t num_cus)
     return p;
 }
 
+// The 8-wave ping-pong kernel (rfp4_gemm_<tile>_pp) for a plan of the
+// 256x256 or 256x128 tile: compiled for those two, and its DMA sources are
+// 32-bit offsets from the matrix bases, so each matrix's codes stay under
+// 4 GiB.
+bool gemm_use_pp(const GemmPlan &p, uint32_t m, uint32_t n, uint32_t k)
+{
+    if (p.tile != 0 && p.tile != 1) return false;
+    if ((uint64_t)m * k / 2u >= (1ull << 32) || (uint64_t)n * k / 2u >= (1ull << 32)) return false;
+    if (t_gemm_pp) return t_gemm_pp == 2;
+    return p.tile == 0; // 256x256 (M = 512: gate|up 47.0 -> 43.2 us, LM head 208.9 -> 193.6 us); 256x128 is slower
+}
+
 } // namespace
 
 extern "C" {
@@ -1411,17 +1424,22 @@ int gemm_launch(hipStream_t stream, uint32_t m, uint32_t n, uint32_t k, const ui
     }
     // two-way splits sum in the launch (the last split of a tile to arrive),
     // others in the reduce kernel launched next (also tiles above 256x128,
-    // whose kernels have no registers for the other plane)
-    uint32_t *counters = p.kz == 2u && t.bm * t.bn <= 256u * 128u && tiles <= kGemmCounters && !t_gemm_reduce_kernel
+    // whose kernels have no registers for the other plane, and the ping-pong
+    // kernels)
+    const bool pp = gemm_use_pp(p, m, n, k);
+    uint32_t *counters = p.kz == 2u && t.bm * t.bn <= 256u * 128u && tiles <= kGemmCounters && !t_gemm_reduce_kernel && !pp
                              ? (uint32_t *)(part + kGemmPartFloats) : nullptr;
     GemmArgs a{a_codes, a_scales, w_codes, w_scales, c, part, m, n, k, p.kz, counters, a_st, w_st};
     char pname[48];
     const char *kname = t.name;
-    if (p.nst >= 3) { // a deeper DMA pipeline (kernels.hip GEMM_KERNEL_P)
+    if (pp) { // 8 waves, two per SIMD (kernels.hip GEMM_KERNEL_PP)
+        snprintf(pname, sizeof pname, "%s_pp", t.name);
+        kname = pname;
+    } else if (p.nst >= 3) { // a deeper DMA pipeline (kernels.hip GEMM_KERNEL_P)
         snprintf(pname, sizeof pname, "%s_p%d", t.name, p.nst);
         kname = pname;
     }
-    int rc = launch(kname, dim3((unsigned)(tiles * p.kz)), dim3(256), (hipStream_t)stream, &a);
+    int rc = launch(kname, dim3((unsigned)(tiles * p.kz)), dim3(pp ? 512 : 256), (hipStream_t)stream, &a);
     if (rc || p.kz == 1 || counters) return rc;
     const uint64_t n4 = (uint64_t)m * n / 4u;
     return launch("rfp4_gemm_reduce", dim3((unsigned)std::min<uint64_t>((n4 + 255u) / 256u, 8192u)), dim3(256),
@@ -1449,6 +1467,13 @@ int rfp4_debug_gemm_stages(int nst)
 {
     if (nst != 0 && (nst < 2 || nst > 4)) return set_error(RFP4_E_INVALID, "GEMM stages must be 0 (auto), 2, 3 or 4");
     t_gemm_stages = nst;
+    return RFP4_OK;
+}
+
+int rfp4_debug_gemm_pp(int mode)
+{
+    if (mode < 0 || mode > 2) return set_error(RFP4_E_INVALID, "GEMM ping-pong mode must be 0 (auto), 1 (off) or 2 (on)");
+    t_gemm_pp = mode;
     return RFP4_OK;
 }
 
@@ -1484,6 +1509,8 @@ int rfp4_gemm_plan_kernel(uint32_t m, uint32_t n, uint32_t k, char *buf, size_t 
     char name[64];
     if (p.tile == kGemmSkinny)
         snprintf(name, sizeof name, "rfp4_gemm_rows_m%d_s%d_f%u", 16 * p.ma, p.nb, p.kz);
+    else if (gemm_use_pp(p, m, n, k))
+        snprintf(name, sizeof name, "%s_pp/kz%u", kGemmTiles[p.tile].name, p.kz);
     else if (p.nst >= 3)
         snprintf(name, sizeof name, "%s_p%d/kz%u", kGemmTiles[p.tile].name, p.nst, p.kz);
     else

@@ -120,6 +120,7 @@ _SIGS = {
     "rfp4_debug_attn_head_split": (I32, [I32]),
     "rfp4_debug_qkv_attn": (I32, [I32]),
     "rfp4_debug_gemm_stages": (I32, [I32]),
+    "rfp4_debug_gemm_pp": (I32, [I32]),
     "rfp4_debug_gemm_reduce_kernel": (I32, [I32]),
     "rfp4_debug_prefill_waves": (I32, [I32]),
     "rfp4_debug_prefill_pairing": (I32, [I32]),

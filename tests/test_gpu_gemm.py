@@ -298,6 +298,42 @@ def test_gemm_two_way_split_summed_in_launch(rf, orc, stream, forced_plan, tile)
         _assert_gemm_close(ref[key], c64, absc)
 
 
+@pytest.mark.parametrize("tile", [0, 1])
+@pytest.mark.parametrize("kz", [1, 3])
+def test_gemm_ping_pong_bit_identical(rf, orc, stream, forced_plan, tile, kz):
+    """The 8-wave ping-pong kernels of the 256x256 and 256x128 tiles give the
+    4-wave kernels' results bit for bit (each accumulator gets the same MFMA
+    sequence; the scale byte comes from the instruction's byte select), on
+    ragged m and n (the second wave group's rows partly or wholly past m), with
+    1, 2 and 11 K steps and K splits (the reduce kernel sums them), and stay
+    within the bar against the oracle."""
+    lib = rf.load()
+    for m, n, k in ((200, 900, 256), (200, 900, 512), (100, 900, 2816), (512, 1024, 4096)):
+        ac, asc = _uniform_mx(orc, m, k, 61 + k + m)
+        wc, wsc = _uniform_mx(orc, n, k, 63 + k + n)
+        forced_plan(tile, kz)
+        try:
+            rf.check(lib.rfp4_debug_gemm_pp(1))
+            c4 = _gemm(rf, stream, m, n, k, ac, asc, wc, wsc)
+            rf.check(lib.rfp4_debug_gemm_pp(2))
+            cp = _gemm(rf, stream, m, n, k, ac, asc, wc, wsc)
+            cp2 = _gemm(rf, stream, m, n, k, ac, asc, wc, wsc)
+        finally:
+            rf.check(lib.rfp4_debug_gemm_pp(0))
+        np.testing.assert_array_equal(c4.view(np.uint32), cp.view(np.uint32), err_msg=f"{m}x{n}x{k}")
+        np.testing.assert_array_equal(cp.view(np.uint32), cp2.view(np.uint32), err_msg=f"{m}x{n}x{k} repeat")
+        if m * n * k <= 200 * 900 * 2816:
+            c64, absc = orc.gemm_mx_f64(m, n, k, ac, asc, wc, wsc)
+            _assert_gemm_close(cp, c64, absc)
+
+
+def test_gemm_pp_hook_rejects_bad_values(rf):
+    lib = rf.load()
+    assert lib.rfp4_debug_gemm_pp(3) == -1
+    assert lib.rfp4_debug_gemm_pp(-1) == -1
+    rf.check(lib.rfp4_debug_gemm_pp(0))
+
+
 def test_gemm_reduce_hook_rejects_bad_values(rf):
     lib = rf.load()
     assert lib.rfp4_debug_gemm_reduce_kernel(2) == -1
