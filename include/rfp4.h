@@ -288,6 +288,13 @@ int rfp4_debug_qkv_attn(int mode);
  * attention of engines created afterwards (0 = automatic, 1, 2, 4, 8; a
  * value that does not divide the group means 1). */
 int rfp4_debug_attn_head_split(int hs);
+/* Test hook (this thread): the gate|up projection of the batched prefill:
+ * 0 = SwiGLU and the MXFP4 rows of its output in the GEMM's epilogue where the
+ * GEMM's plan is the 256x256 ping-pong tile (no f32 gate|up output is
+ * written; the sums within f32 rounding of the plain GEMM's), 1 = the GEMM,
+ * then the SwiGLU + MXFP4 row kernel.  No reference counterpart (the
+ * reference has no batched prefill). */
+int rfp4_debug_prefill_swiglu(int mode);
 /* Test hook: the batched prefill's attention on this thread: 0 = the
  * matrix-core prefill kernel, 1 = the decode kernel, one grid row per prompt
  * row.  No reference counterpart. */

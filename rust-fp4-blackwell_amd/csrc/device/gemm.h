@@ -45,6 +45,8 @@
 #include <type_traits>
 #include "common.h"
 #include "mma.h"
+#include "misc.h"
+#include "gemv.h"
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) uint8_t rfp4_lds_u8;
@@ -580,7 +582,20 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
 // gemm_body's order (steps in the rotated order, t = 0..3), so C is
 // bit-identical to gemm_body's.  No split-K sum in the launch (kz > 1 writes
 // the partial planes for the reduce kernel).
-template <int FA, int FB>
+//
+// SWQ (the prefill's gate|up projection, GemmArgs::q_codes): the tile's W
+// rows are the gate rows and the up rows of 128 output columns (column tile
+// nt: gate 128 nt .. +127 in tile columns 0-127, up pair_off + 128 nt .. in
+// 128-255), so waves 0, 1 of each group hold gate columns and waves 2, 3 the
+// matching up columns.  After the loop the accumulators go through LDS (free
+// by then), one wave group at a time, and every thread forms y = silu(g) * u
+// for one 32-column block of one row with the row kernel's arithmetic and
+// quantizes it (quant_block32: the row quantizer's bytes for the same
+// values).  The K steps run in the order rotated for this tile's nt, so the
+// sums are those of a GEMM whose column tiles are these pairs: within f32
+// rounding of the plain GEMM's (whose gate and up columns sit in different
+// tiles), not bit-identical to them.
+template <int FA, int FB, bool SWQ = false>
 RFP4_DEV void gemm_pp_body(const GemmArgs &g)
 {
     constexpr uint32_t BM = 64u * FA, BN = 128u * FB, R = BM + BN;
@@ -625,8 +640,10 @@ RFP4_DEV void gemm_pp_body(const GemmArgs &g)
             if (is_a != (half == 1)) continue;
             const uint32_t row = 8u * (wv + 4u * j) + (ln >> 3);
             const uint32_t qq = (ln & 7u) ^ gemm_swz(row);
+            uint32_t wrow = nt * BN + (row - BM);
+            if (SWQ) wrow = (row - BM < BN / 2u ? 0u : g.pair_off - BN / 2u) + nt * (BN / 2u) + (row - BM);
             const uint32_t off = is_a ? min(mt * BM + row, g.m - 1u) * kbytes + qq * 16u
-                                      : min(nt * BN + (row - BM), g.n - 1u) * kbytes + qq * 16u;
+                                      : min(wrow, g.n - 1u) * kbytes + qq * 16u;
             __builtin_amdgcn_global_load_lds((rfp4_glb_void *)((is_a ? g.a_codes : g.w_codes) + ko + off),
                                              st + 1024u * (wv + 4u * j), 16, 0, 0);
         }
@@ -635,8 +652,10 @@ RFP4_DEV void gemm_pp_body(const GemmArgs &g)
             const bool is_a = 4u * b < BM / 32u; // block wv + 4 b < BM / 32 for every wv
             if (is_a != (half == 1)) continue;
             const uint32_t tb = wv + 4u * b;
-            const uint32_t blk = is_a ? min(mt * (BM / 32u) + tb, (g.m - 1u) >> 5)
-                                      : min(nt * (BN / 32u) + (tb - BM / 32u), (g.n - 1u) >> 5);
+            uint32_t wblk = nt * (BN / 32u) + (tb - BM / 32u);
+            if (SWQ)
+                wblk = (tb - BM / 32u < BN / 64u ? 0u : (g.pair_off - BN / 2u) >> 5) + nt * (BN / 64u) + (tb - BM / 32u);
+            const uint32_t blk = is_a ? min(mt * (BM / 32u) + tb, (g.m - 1u) >> 5) : min(wblk, (g.n - 1u) >> 5);
             __builtin_amdgcn_global_load_lds((rfp4_glb_void *)((is_a ? g.a_st : g.w_st) + so + blk * nsuper * 256u + ln * 4u),
                                              st + SC0 + 256u * tb, 4, 0, 0);
         }
@@ -768,6 +787,56 @@ RFP4_DEV void gemm_pp_body(const GemmArgs &g)
         }
     }
     if (grp == 0u) bar(); // the barrier count of group 1
+
+    if constexpr (SWQ) {
+        // Every wave is past its last LDS read: the stages are free.  Two
+        // passes, one per group: the group's waves put their accumulators in
+        // LDS as a [128 rows][gate 128 | up 128] tile (constant register
+        // indices), then each of the 512 threads takes one block of 32 output
+        // columns of one row (row t % 128, block t / 128: consecutive lanes on
+        // consecutive rows, distinct banks with the padded row) and quantizes
+        // it whole (quant_block32: no cross-lane step, no register array
+        // indexed at run time, which would put the accumulators in scratch).
+        constexpr uint32_t GR = 32u * FA, GLD = BN + 4u; // rows per group; floats per LDS row (padded)
+        static_assert(GR * GLD * 4u <= 2u * STAGE && BN == 256u && GR * 4u == 512u, "a group's tile in the stages");
+        float *tl = (float *)lds_raw;
+        const uint32_t nblk = g.pair_off >> 5, nsup = g.pair_off >> 8;
+        for (uint32_t pass = 0; pass < 2u; pass++) {
+            __syncthreads(); // the previous pass's readers (or the loop's last LDS reads) are done
+            if (grp == pass) {
+#pragma unroll
+                for (int fa = 0; fa < FA; fa++)
+#pragma unroll
+                    for (int fb = 0; fb < FB; fb++)
+#pragma unroll
+                        for (int r = 0; r < 16; r++) {
+                            const uint32_t rl = 32u * fa + 8u * (uint32_t)(r / 4) + 4u * h + (uint32_t)(r % 4);
+                            tl[rl * GLD + wv * (32u * FB) + 32u * fb + r32] = acc[fa][fb][r];
+                        }
+            }
+            __syncthreads();
+            const uint32_t rl = tid & (GR - 1u), bl = tid / GR;
+            const uint32_t row = mt * BM + pass * GR + rl, blk = nt * (BN / 64u) + bl;
+            const float4 *gp = (const float4 *)(tl + rl * GLD + 32u * bl), *up = (const float4 *)(tl + rl * GLD + BN / 2u + 32u * bl);
+            float y[32];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float4 gv = gp[i], uv = up[i];
+                y[4 * i] = __fmul_rn(silu_ref(gv.x), uv.x);
+                y[4 * i + 1] = __fmul_rn(silu_ref(gv.y), uv.y);
+                y[4 * i + 2] = __fmul_rn(silu_ref(gv.z), uv.z);
+                y[4 * i + 3] = __fmul_rn(silu_ref(gv.w), uv.w);
+            }
+            uint4 q16;
+            const uint32_t sbyte = quant_block32(y, (uint8_t *)&q16);
+            if (row < g.m) {
+                *(uint4 *)(g.q_codes + (size_t)row * (g.pair_off >> 1) + (size_t)blk * 16u) = q16;
+                g.q_scales[(size_t)row * nblk + blk] = (uint8_t)sbyte;
+                if (g.q_scales_t) g.q_scales_t[mx_st_offset(row, blk, nsup)] = (uint8_t)sbyte;
+            }
+        }
+        return;
+    }
 
     const uint32_t m0 = mt * BM + grp * (32u * FA), n0 = nt * BN + wv * (32u * FB);
     float *dst = g.kz > 1u ? g.part + (size_t)z * g.m * g.n : g.c;

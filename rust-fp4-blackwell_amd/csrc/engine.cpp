@@ -100,6 +100,11 @@ struct llama_engine {
     float *pf_x = nullptr, *pf_c = nullptr, *pf_a = nullptr, *pf_part = nullptr; // pf_part: decode-kernel test path only
     uint8_t *pf_codes = nullptr, *pf_scales = nullptr;
     uint8_t *pf_scales_t = nullptr; // the activation scales step-blocked, written beside pf_scales
+    // the SwiGLU rows' MXFP4 (the down projection's input) where the gate|up
+    // GEMM's epilogue writes them: not pf_codes, which that GEMM is reading;
+    // pf_q_alt: the last MXFP4 rows written are these (prefill buffer hook)
+    uint8_t *pf_codes2 = nullptr, *pf_scales2 = nullptr, *pf_scales_t2 = nullptr;
+    bool pf_q_alt = false;
     uint32_t *pf_ids = nullptr;
     // persistent decode (one cooperative launch for all layers of a step)
     bool persist_ok = false, persist = false; // shape and device allow it / chosen
@@ -409,8 +414,10 @@ static int prefill_reserve(llama_engine *e, uint32_t n)
     hipStreamSynchronize(e->stream);
     dfree(e, e->pf_x); dfree(e, e->pf_c); dfree(e, e->pf_a); dfree(e, e->pf_part);
     dfree(e, e->pf_codes); dfree(e, e->pf_scales); dfree(e, e->pf_scales_t); dfree(e, e->pf_ids);
+    dfree(e, e->pf_codes2); dfree(e, e->pf_scales2); dfree(e, e->pf_scales_t2);
     e->pf_x = e->pf_c = e->pf_a = e->pf_part = nullptr;
     e->pf_codes = e->pf_scales = e->pf_scales_t = nullptr;
+    e->pf_codes2 = e->pf_scales2 = e->pf_scales_t2 = nullptr;
     e->pf_ids = nullptr;
     e->pf_cap = 0;
     const size_t kmax = std::max(std::max(c.dim, qd), c.ffn);
@@ -426,6 +433,9 @@ static int prefill_reserve(llama_engine *e, uint32_t n)
     if (!rc) rc = dalloc_t(e, &e->pf_codes, (size_t)cap * kmax / 2);
     if (!rc) rc = dalloc_t(e, &e->pf_scales, (size_t)cap * kmax / 32);
     if (!rc) rc = dalloc_t(e, &e->pf_scales_t, scales_tiled_bytes(cap, (uint32_t)kmax));
+    if (!rc) rc = dalloc_t(e, &e->pf_codes2, (size_t)cap * c.ffn / 2);
+    if (!rc) rc = dalloc_t(e, &e->pf_scales2, (size_t)cap * c.ffn / 32);
+    if (!rc) rc = dalloc_t(e, &e->pf_scales_t2, scales_tiled_bytes(cap, c.ffn));
     if (!rc) rc = dalloc_t(e, &e->pf_ids, cap);
     if (!rc) e->pf_cap = cap;
     return rc;
@@ -443,6 +453,7 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
     hipStream_t s = e->stream;
     const uint32_t qd = qdim(c), kvd = kvdim(c), hd = c.head_dim, nqkv = qd + 2 * kvd;
     int rc;
+    e->pf_q_alt = false;
     RowsArgs ea{};
     ea.ids = e->pf_ids; ea.embed = e->embed; ea.y = e->pf_x; ea.rows = n; ea.k = c.dim; ea.vocab = c.vocab;
     ea.bf16 = e->embed_bf16;
@@ -462,6 +473,7 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
         na.add = l > 0 ? e->pf_c : nullptr;
         na.x_out = e->pf_x;
         if ((rc = launch("rfp4_rmsnorm_quant_rows", dim3(n), dim3(256), s, &na))) return rc;
+        e->pf_q_alt = false;
         RFP4_PF_STAGE(0);
         if ((rc = gemm_launch(s, n, nqkv, c.dim, e->pf_codes, e->pf_scales, e->pf_scales_t, w.qkv_c, w.qkv_s, w.qkv_st,
                               e->pf_c, e->gemm_part))) return rc;
@@ -493,6 +505,7 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
         }
         RFP4_PF_STAGE(3);
         if ((rc = mx4_quantize_st(s, n, qd, e->pf_a, 0, e->pf_codes, e->pf_scales, e->pf_scales_t))) return rc;
+        e->pf_q_alt = false;
         RFP4_PF_STAGE(4);
         if ((rc = gemm_launch(s, n, c.dim, qd, e->pf_codes, e->pf_scales, e->pf_scales_t, w.o_c, w.o_s, w.o_st, e->pf_c,
                               e->gemm_part))) return rc;
@@ -500,19 +513,31 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
         na.w = e->norm_ffn + (size_t)l * c.dim;
         na.add = e->pf_c; // x += O projection, then the FFN norm
         if ((rc = launch("rfp4_rmsnorm_quant_rows", dim3(n), dim3(256), s, &na))) return rc;
+        e->pf_q_alt = false;
         RFP4_PF_STAGE(6);
-        if ((rc = gemm_launch(s, n, 2 * c.ffn, c.dim, e->pf_codes, e->pf_scales, e->pf_scales_t, w.gu_c, w.gu_s, w.gu_st,
-                              e->pf_c, e->gemm_part))) return rc;
-        RFP4_PF_STAGE(7);
-        RowsArgs sa{};
-        sa.x = e->pf_c; sa.codes = e->pf_codes; sa.scales = e->pf_scales; sa.scales_t = e->pf_scales_t;
-        sa.rows = n; sa.k = c.ffn;
-        // parts of about 1024 float4 per row (measured: 8B 512 rows x 14336)
-        if ((rc = launch("rfp4_swiglu_quant_rows", dim3(n, std::max(1u, (c.ffn / 4u + 1023u) / 1024u)), dim3(256), s, &sa)))
-            return rc;
+        // gate|up: SwiGLU and the MXFP4 rows of its output in the GEMM's
+        // epilogue where the plan is the 256x256 ping-pong tile (no f32
+        // gate|up output; not when the stage test hook wants that output)
+        if (stop != (int)(10u * l + 7u) && prefill_swiglu_mode() == 0 && gemm_swiglu_ok(n, c.ffn, c.dim)) {
+            if ((rc = gemm_swiglu_launch(s, n, c.ffn, c.dim, e->pf_codes, e->pf_scales, e->pf_scales_t, w.gu_c, w.gu_s,
+                                         w.gu_st, e->pf_codes2, e->pf_scales2, e->pf_scales_t2))) return rc;
+            e->pf_q_alt = true;
+        } else {
+            if ((rc = gemm_launch(s, n, 2 * c.ffn, c.dim, e->pf_codes, e->pf_scales, e->pf_scales_t, w.gu_c, w.gu_s,
+                                  w.gu_st, e->pf_c, e->gemm_part))) return rc;
+            RFP4_PF_STAGE(7);
+            RowsArgs sa{};
+            sa.x = e->pf_c; sa.codes = e->pf_codes; sa.scales = e->pf_scales; sa.scales_t = e->pf_scales_t;
+            sa.rows = n; sa.k = c.ffn;
+            // parts of about 1024 float4 per row (measured: 8B 512 rows x 14336)
+            if ((rc = launch("rfp4_swiglu_quant_rows", dim3(n, std::max(1u, (c.ffn / 4u + 1023u) / 1024u)), dim3(256), s,
+                             &sa)))
+                return rc;
+        }
         RFP4_PF_STAGE(8);
-        if ((rc = gemm_launch(s, n, c.dim, c.ffn, e->pf_codes, e->pf_scales, e->pf_scales_t, w.d_c, w.d_s, w.d_st, e->pf_c,
-                              e->gemm_part))) return rc;
+        uint8_t *dc = e->pf_q_alt ? e->pf_codes2 : e->pf_codes, *ds = e->pf_q_alt ? e->pf_scales2 : e->pf_scales;
+        uint8_t *dst_ = e->pf_q_alt ? e->pf_scales_t2 : e->pf_scales_t;
+        if ((rc = gemm_launch(s, n, c.dim, c.ffn, dc, ds, dst_, w.d_c, w.d_s, w.d_st, e->pf_c, e->gemm_part))) return rc;
         RFP4_PF_STAGE(9);
         // x += down projection: by the next layer's first norm, after the last layer here
         if (l + 1 == c.n_layers && (rc = residual(s, n * c.dim, e->pf_c, e->pf_x))) return rc;
@@ -1466,8 +1491,8 @@ int llama_engine_prefill_buffers(llama_engine *e, float **x, uint8_t **codes, ui
     if (!e || !x || !codes || !scales || !c || !a || !rows_cap)
         return set_error(RFP4_E_INVALID, "llama_engine_prefill_buffers: null argument");
     *x = e->pf_x;
-    *codes = e->pf_codes;
-    *scales = e->pf_scales;
+    *codes = e->pf_q_alt ? e->pf_codes2 : e->pf_codes; // the MXFP4 rows written last
+    *scales = e->pf_q_alt ? e->pf_scales2 : e->pf_scales;
     *c = e->pf_c;
     *a = e->pf_a;
     *rows_cap = e->pf_cap;

@@ -187,6 +187,9 @@ GEMM_KERNEL_P(256, 128, 2, 2, 4, 2, 3)
     K512 void rfp4_gemm_##BM##x##BN##_pp(GemmArgs a) { gemm_pp_body<FA, FB>(a); }
 GEMM_KERNEL_PP(256, 256, 4, 2)
 GEMM_KERNEL_PP(256, 128, 4, 1)
+// the prefill's gate|up projection with SwiGLU and the MXFP4 rows of its
+// output in the epilogue (GemmArgs::q_codes)
+K512 void rfp4_gemm_256x256_ppsw(GemmArgs a) { gemm_pp_body<4, 2, true>(a); }
 K256 void rfp4_gemm_reduce(GemmArgs a) { gemm_reduce_body(a); }
 // row-major E8M0 scales -> the step-blocked copy the tiled kernels read
 K256 void rfp4_scales_tile(ScaleTileArgs a) { scales_tile_body(a); }

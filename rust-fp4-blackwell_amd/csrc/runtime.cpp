@@ -519,6 +519,8 @@ static thread_local int t_prefill_pairing = 0; // 0 automatic, 1 one query tile 
 int prefill_attn_mode() { return t_prefill_attn; }
 static thread_local int t_prefill_stop = -2; // stage after which the batched prefill stops (-2: none)
 int prefill_stop() { return t_prefill_stop; }
+static thread_local int t_prefill_swiglu = 0; // 0: SwiGLU + MXFP4 in the gate|up GEMM's epilogue where it applies, 1: the row kernel
+int prefill_swiglu_mode() { return t_prefill_swiglu; }
 
 bool attn_inmerge_mode(int mode, uint32_t splits)
 {
@@ -627,6 +629,15 @@ extern "C" int rfp4_debug_prefill_stop(int after)
     using namespace rfp4;
     if (after < -2) return set_error(RFP4_E_INVALID, "prefill stop must be -2 (off), -1 (after the embedding) or 10*layer + stage");
     t_prefill_stop = after;
+    return RFP4_OK;
+}
+
+extern "C" int rfp4_debug_prefill_swiglu(int mode)
+{
+    using namespace rfp4;
+    if (mode != 0 && mode != 1)
+        return set_error(RFP4_E_INVALID, "prefill SwiGLU mode must be 0 (in the gate|up GEMM where it applies) or 1 (row kernel)");
+    t_prefill_swiglu = mode;
     return RFP4_OK;
 }
 
@@ -1444,6 +1455,30 @@ int gemm_launch(hipStream_t stream, uint32_t m, uint32_t n, uint32_t k, const ui
     const uint64_t n4 = (uint64_t)m * n / 4u;
     return launch("rfp4_gemm_reduce", dim3((unsigned)std::min<uint64_t>((n4 + 255u) / 256u, 8192u)), dim3(256),
                   (hipStream_t)stream, &a);
+}
+
+bool gemm_swiglu_ok(uint32_t m, uint32_t ffn, uint32_t k)
+{
+    Runtime *rt = g_rt;
+    if (!rt || m == 0 || ffn == 0 || ffn % 256u || k == 0 || k % 256u) return false;
+    const GemmPlan p = gemm_plan(m, 2u * ffn, k, (uint32_t)rt->num_cus);
+    return p.tile == 0 && p.kz == 1u && gemm_use_pp(p, m, 2u * ffn, k);
+}
+
+int gemm_swiglu_launch(hipStream_t stream, uint32_t m, uint32_t ffn, uint32_t k, const uint8_t *a_codes,
+                       const uint8_t *a_scales, const uint8_t *a_st, const uint8_t *w_codes, const uint8_t *w_scales,
+                       const uint8_t *w_st, uint8_t *q_codes, uint8_t *q_scales, uint8_t *q_scales_t)
+{
+    if (!a_codes || !a_st || !w_codes || !w_st || !q_codes || !q_scales)
+        return set_error(RFP4_E_INVALID, "gemm_swiglu: null pointer");
+    if (((uintptr_t)a_codes | (uintptr_t)w_codes) & 15u || ((uintptr_t)q_codes | (uintptr_t)a_st | (uintptr_t)w_st) & 3u)
+        return set_error(RFP4_E_ALIGN, "gemm_swiglu: misaligned codes or scales");
+    if (!gemm_swiglu_ok(m, ffn, k))
+        return set_error(RFP4_E_SHAPE, "gemm_swiglu: the plan of %u x %u x %u is not the 256x256 ping-pong tile", m, 2u * ffn, k);
+    GemmArgs a{a_codes, a_scales, w_codes, w_scales, nullptr, nullptr, m, 2u * ffn, k, 1u, nullptr, a_st, w_st,
+               q_codes, q_scales, q_scales_t, ffn, 0u};
+    const uint64_t tiles = (uint64_t)((m + 255u) / 256u) * (ffn / 128u);
+    return launch("rfp4_gemm_256x256_ppsw", dim3((unsigned)tiles), dim3(512), stream, &a);
 }
 
 } // namespace rfp4

@@ -97,6 +97,16 @@ int noalloc_setup(int device);
 int gemm_launch(hipStream_t stream, uint32_t m, uint32_t n, uint32_t k, const uint8_t *a_codes, const uint8_t *a_scales,
                 const uint8_t *a_st, const uint8_t *w_codes, const uint8_t *w_scales, const uint8_t *w_st, float *c,
                 float *part);
+// The gate|up projection of the prefill with SwiGLU and the MXFP4 rows of its
+// output in the GEMM's epilogue (rfp4_gemm_256x256_ppsw): m rows of K = k,
+// W = [gate; up] of 2 ffn rows; y = silu(gate) * up quantized per 32 into
+// q_codes [m][ffn/2], q_scales [m][ffn/32] and q_scales_t (step-blocked).
+// gemm_swiglu_ok: whether the plan of the plain GEMM (m, 2 ffn, k) is that
+// kernel's tile (256x256 ping-pong, no K split) and ffn a multiple of 256.
+bool gemm_swiglu_ok(uint32_t m, uint32_t ffn, uint32_t k);
+int gemm_swiglu_launch(hipStream_t stream, uint32_t m, uint32_t ffn, uint32_t k, const uint8_t *a_codes,
+                       const uint8_t *a_scales, const uint8_t *a_st, const uint8_t *w_codes, const uint8_t *w_scales,
+                       const uint8_t *w_st, uint8_t *q_codes, uint8_t *q_scales, uint8_t *q_scales_t);
 // Bytes of the step-blocked copy of [rows][k/32] E8M0 scales.
 inline size_t scales_tiled_bytes(uint32_t rows, uint32_t k) { return (size_t)((rows + 31u) / 32u) * 32u * (k / 32u); }
 // Row-major scales of one or two matrices (rows1 = 0: one) into step-blocked copies, k % 256 == 0.
@@ -119,6 +129,7 @@ int prefill_attn_mode();                         // this thread's rfp4_debug_pre
 int attn_head_split_mode();                      // this thread's rfp4_debug_attn_head_split setting
 int qkva_mode();                                 // this thread's rfp4_debug_qkv_attn setting
 int prefill_stop();                              // this thread's rfp4_debug_prefill_stop setting
+int prefill_swiglu_mode();                       // this thread's rfp4_debug_prefill_swiglu setting
 bool attn_inmerge_mode(int mode, uint32_t splits); // attn_inmerge under an explicit setting
 constexpr uint32_t kAttnInmergeMaxSplits = 8;
 // Whether an engine's one-row attention with `splits` splits uses the tagged

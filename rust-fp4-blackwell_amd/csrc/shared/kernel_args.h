@@ -247,6 +247,15 @@ typedef struct GemmArgs {
     // of 256 values, 256 contiguous bytes, for h = 0, 1 and rows r = 0..31
     // the step's scale bytes 4h .. 4h + 3 of the block's row r
     const uint8_t *a_st, *w_st;
+    // SwiGLU + MXFP4 epilogue (the 256x256 ping-pong kernel _ppsw only, kz =
+    // 1, n = 2 pair_off): the W rows of column tile nt are gate rows 128 nt ..
+    // +127 and up rows pair_off + 128 nt .. +127; the tile writes y = silu(gate)
+    // * up for its 128 columns of the pair_off wide output, quantized per 32
+    // along it by the row quantizer's rules: q_codes [m][pair_off/2], q_scales
+    // [m][pair_off/32] and, if not null, q_scales_t (step-blocked over K =
+    // pair_off).  c is not written.
+    uint8_t *q_codes, *q_scales, *q_scales_t;
+    uint32_t pair_off, pad;
 } GemmArgs;
 
 // Row-major E8M0 scales [rows][k/32] -> the step-blocked layout of GemmArgs

@@ -200,3 +200,40 @@ def test_engine_step_blocked_weight_scales(rf):
     with pytest.raises(rf.Rfp4Error):
         eng.weight_scales_tiled(0, 0)
     eng.close()
+
+
+def test_prefill_swiglu_in_gemm_epilogue(rf, orc):
+    """Llama-3-8B widths, 450 prompt rows (the second 256-row tile ragged):
+    the gate|up GEMM's plan is the 256x256 ping-pong tile, so SwiGLU and the
+    MXFP4 rows of its output come from the GEMM's epilogue.  Every stage on
+    identical inputs within its bar (the SwiGLU rows against the exact values
+    of the plain GEMM's output, which the stage hook stopped after the GEMM
+    still writes), and against the GEMM + row kernel path (rfp4_debug_prefill_
+    swiglu(1)): the same scale bytes and codes but where the two f32 sums lie
+    at a rounding boundary (their K orders differ), and the same next token."""
+    cfg, seed, n = W8B, 0x5A1F, 450
+    assert rf.gemm_plan_kernel(n, 2 * cfg["ffn"], cfg["dim"]).startswith("rfp4_gemm_256x256_pp/kz1")
+    prompt = np.random.default_rng(450).integers(0, cfg["vocab"], n, dtype=np.uint32)
+    print("prefill at 8B widths, 450 rows, SwiGLU in the gate|up epilogue", flush=True)
+    eng = _engine(rf, cfg, seed)
+    ref = orc.Model(cfg, seed)
+    tok = check_prefill_stages(rf, orc, eng, ref, cfg, prompt, 0)
+    ffn = cfg["ffn"]
+    rows = {}
+    lib = rf.load()
+    try:
+        for mode in (0, 1):
+            rf.check(lib.rfp4_debug_prefill_swiglu(mode))
+            eng.prefill_stop(prompt, 0, 18)  # layer 1's SwiGLU rows
+            rows[mode] = (eng.prefill_buffer("codes", (n, ffn // 2), np.uint8),
+                          eng.prefill_buffer("scales", (n, ffn // 32), np.uint8))
+            rows[mode] += (eng.prefill(prompt, 0),)
+    finally:
+        rf.check(lib.rfp4_debug_prefill_swiglu(0))
+    (cf, sf, tf), (cu, su, tu) = rows[0], rows[1]
+    assert tf == tu == tok
+    off_s = np.count_nonzero(sf != su)
+    off_c = np.count_nonzero(cf != cu)
+    assert off_s <= n * ffn // 32 // 10000 and off_c <= n * ffn // 2 // 10000, (off_s, off_c)
+    eng.close()
+    ref.close()
