@@ -295,6 +295,12 @@ int rfp4_debug_attn_head_split(int hs);
  * then the SwiGLU + MXFP4 row kernel.  No reference counterpart (the
  * reference has no batched prefill). */
 int rfp4_debug_prefill_swiglu(int mode);
+/* Test hook (this thread): the q|k|v projection of the batched prefill:
+ * 0 = RoPE and the fp16 K/V cache rows in the GEMM's epilogue where the
+ * GEMM's plan has that kernel (128x128 tile, or 256x256 ping-pong; heads of
+ * 64 or 128; bit-identical to mode 1), 1 = the GEMM, then the RoPE + K/V row
+ * kernel.  No reference counterpart (the reference has no batched prefill). */
+int rfp4_debug_prefill_rope(int mode);
 /* Test hook: the batched prefill's attention on this thread: 0 = the
  * matrix-core prefill kernel, 1 = the decode kernel, one grid row per prompt
  * row.  No reference counterpart. */

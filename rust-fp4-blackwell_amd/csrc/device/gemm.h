@@ -141,6 +141,112 @@ RFP4_DEV void gemm_splitk_last(const GemmArgs &g, const v16f32 (&acc)[FA][FB], u
         }
 }
 
+// RoPE + K/V cache epilogue of the prefill's q|k|v projection
+// (GemmArgs::rope_cos; rope_kv_rows_body's result in the GEMM's launch).
+// Heads are rope_hd = 64 or 128 columns, a divisor of the tile width, so a
+// head lies in one tile and a 32-column fragment in one head: whether a
+// fragment is q, k or v, and which half of its head, is the same for every
+// lane.  The partner of head column j < half is j + half and the other way
+// round: tile column c ^ half, which is the same lane and accumulator
+// register of the wave that covers that column (half >= 32).  The waves of
+// a workgroup put FS row fragments (fa0 .. fa0 + FS - 1) of their
+// accumulators in LDS, slot xw, fragment-native (gemm_rope_put: consecutive
+// lanes, consecutive words), and each then reads its own values and its
+// partners' from there (gemm_rope_store).  The rotation is rope_pair's,
+// each product and sum rounded in the same order, and C's sums are those of
+// the same GEMM without the epilogue: the result is bit-identical to the
+// GEMM followed by rope_kv_rows_body.
+template <int FA, int FB, int FS>
+RFP4_DEV void gemm_rope_put(float *xl, uint32_t xw, const v16f32 (&acc)[FA][FB], int fa0, uint32_t lane)
+{
+#pragma unroll
+    for (int fs = 0; fs < FS; fs++)
+#pragma unroll
+        for (int fb = 0; fb < FB; fb++)
+#pragma unroll
+            for (int r = 0; r < 16; r++)
+                xl[(((xw * FS + fs) * FB + fb) * 16u + (uint32_t)r) * 64u + lane] = acc[fa0 + fs][fb][r];
+}
+
+// The FS x FB fragments put from row fragment fa0 on: xw0 is the slot of
+// the wave's first column wave (its set holds the same rows), wn its column
+// index in the set (columns from tile column 32 FB wn; slot xw0 + wn), m0
+// its first row (of row fragment 0), nt0 the tile's first column.  UB
+// fragments per batch: the batch's cos and sin loads are issued, then one
+// wait, then its LDS reads (own and partner values), rotations and stores,
+// with no global load behind a store (gfx9 counts stores in vmcnt: a wait
+// for a load issued after a store waits for the store's write too).
+template <int FS, int FB, int UB>
+RFP4_DEV void gemm_rope_store(const GemmArgs &g, const float *xl, uint32_t xw0, uint32_t wn, uint32_t m0, int fa0,
+                              uint32_t nt0, uint32_t lane)
+{
+    constexpr int NU = FS * FB;
+    static_assert(NU % UB == 0, "whole batches");
+    const uint32_t r32 = lane & 31u, h = lane >> 5;
+    const uint32_t hd = g.rope_hd, half = hd >> 1, qk = g.rope_q + g.rope_kv;
+    const float *__restrict__ cosv = g.rope_cos;
+    const float *__restrict__ sinv = g.rope_sin;
+    // fragment u = fs * FB + fb: its tile column and first row
+    auto frag = [&](uint32_t u, uint32_t &col0, uint32_t &rbase) {
+        col0 = nt0 + wn * (32u * FB) + 32u * (u % FB);
+        rbase = m0 + 32u * ((uint32_t)fa0 + u / FB) + 4u * h;
+    };
+#pragma unroll 1
+    for (uint32_t u0 = 0; u0 < (uint32_t)NU; u0 += UB) {
+        float cv[UB][16], sv[UB][16];
+#pragma unroll
+        for (int i = 0; i < UB; i++) {
+            uint32_t col0, rbase;
+            frag(u0 + i, col0, rbase);
+            const uint32_t j = (col0 + r32) & (half - 1u);
+            if (col0 < qk) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const uint32_t row = min(rbase + 8u * (uint32_t)(r / 4) + (uint32_t)(r % 4), g.m - 1u);
+                    const size_t t = (size_t)(g.rope_pos0 + row) * half + j;
+                    cv[i][r] = cosv[t];
+                    sv[i][r] = sinv[t];
+                }
+            }
+        }
+        __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): the batch's cos and sin
+#pragma unroll
+        for (int i = 0; i < UB; i++) {
+            const uint32_t u = u0 + i, fs = u / FB, fb = u % FB;
+            uint32_t col0, rbase;
+            frag(u, col0, rbase);
+            const uint32_t col = col0 + r32, tc = col0 - nt0, pc = tc ^ half;
+            const uint32_t pw = pc / (32u * FB), pfb = (pc >> 5) % (uint32_t)FB;
+            const float *op = xl + ((((xw0 + wn) * FS + fs) * FB + fb) * 16u) * 64u + lane;
+            const float *pp = xl + ((((xw0 + pw) * FS + fs) * FB + pfb) * 16u) * 64u + lane;
+            float v[16];
+#pragma unroll
+            for (int r = 0; r < 16; r++) v[r] = op[(uint32_t)r * 64u];
+            if (col0 < qk) {
+                if ((col0 & (hd - 1u)) < half) {
+#pragma unroll
+                    for (int r = 0; r < 16; r++)
+                        v[r] = __fsub_rn(__fmul_rn(v[r], cv[i][r]), __fmul_rn(pp[(uint32_t)r * 64u], sv[i][r]));
+                } else {
+#pragma unroll
+                    for (int r = 0; r < 16; r++)
+                        v[r] = __fadd_rn(__fmul_rn(v[r], cv[i][r]), __fmul_rn(pp[(uint32_t)r * 64u], sv[i][r]));
+                }
+            }
+            const bool kv = col0 >= g.rope_q, is_v = col0 >= qk;
+            const uint32_t kcol = col - g.rope_q - (is_v ? g.rope_kv : 0u); // k or v columns only
+            uint16_t *cache = (is_v ? g.vc : g.kc) + (size_t)(kcol / hd) * g.kv_hs + (kcol & (hd - 1u));
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const uint32_t row = rbase + 8u * (uint32_t)(r / 4) + (uint32_t)(r % 4);
+                if (row >= g.m || col >= g.n) continue;
+                __builtin_nontemporal_store(v[r], g.c + (size_t)row * g.n + col);
+                if (kv) cache[(size_t)(g.rope_pos0 + row) * g.kv_ts] = f32_to_f16_bits(v[r]);
+            }
+        }
+    }
+}
+
 // LDS reads in inline asm (see gemm_body's step) and the wait for them.
 RFP4_DEV void gemm_lds_rd16(u32x4 &dst, uint32_t addr) { asm volatile("ds_read_b128 %0, %1" : "=v"(dst) : "v"(addr)); }
 RFP4_DEV void gemm_lds_rd4(uint32_t &dst, uint32_t addr) { asm volatile("ds_read_b32 %0, %1" : "=v"(dst) : "v"(addr)); }
@@ -188,7 +294,7 @@ RFP4_DEV void gemm_lds_wait_all(GemmOps<FA, FB> &o)
 
 // PIPE: next step's LDS reads overlap this step's MFMAs (two register sets
 // of operands); without it the reads and MFMAs of a step run back to back.
-template <int WM, int WN, int FA, int FB, int NST = 2, bool PIPE = false>
+template <int WM, int WN, int FA, int FB, int NST = 2, bool PIPE = false, bool ROPE = false>
 RFP4_DEV void gemm_body(const GemmArgs &g)
 {
     static_assert(WM * WN == 4, "4 waves");
@@ -536,6 +642,17 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
 
     // ---- epilogue: accumulator r of lane l is C[8 (r/4) + 4 (l/32) + r%4][l%32] of its fragment
     const uint32_t m0 = mt * BM + wm * (32u * FA), n0 = nt * BN + wn * (32u * FB);
+    if constexpr (ROPE) {
+        // the 4 waves' accumulators in the stages (free after the loop's last
+        // LDS reads), slot = wave; a wave's partners sit in its row of waves
+        static_assert(4u * FA * FB * 16u * 64u * 4u <= NST * STAGE, "the accumulators in the stages");
+        float *xl = (float *)lds_raw;
+        __syncthreads();
+        gemm_rope_put<FA, FB, FA>(xl, wave, acc, 0, lane);
+        __syncthreads();
+        gemm_rope_store<FA, FB, FA * FB>(g, xl, wm * WN, wn, m0, 0, nt * BN, lane);
+        return;
+    }
     // (up to 256x128: the other plane's values fit the registers beside the
     // accumulators; the host passes no counters for larger tiles)
     if constexpr (FA * FB <= 8) {
@@ -595,9 +712,12 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
 // sums are those of a GEMM whose column tiles are these pairs: within f32
 // rounding of the plain GEMM's (whose gate and up columns sit in different
 // tiles), not bit-identical to them.
-template <int FA, int FB, bool SWQ = false>
+// EPI: 0 C only, 1 the SwiGLU + MXFP4 epilogue (SWQ), 2 the RoPE + K/V
+// cache epilogue (gemm_rope_store; two passes, one per wave group)
+template <int FA, int FB, int EPI = 0>
 RFP4_DEV void gemm_pp_body(const GemmArgs &g)
 {
+    constexpr bool SWQ = EPI == 1;
     constexpr uint32_t BM = 64u * FA, BN = 128u * FB, R = BM + BN;
     constexpr uint32_t NJ = R / 32u;                 // 8-row code blocks per group-0 wave per step
     constexpr uint32_t NSB = (R / 32u + 3u) / 4u;    // 32-row scale blocks per group-0 wave per step
@@ -839,6 +959,21 @@ RFP4_DEV void gemm_pp_body(const GemmArgs &g)
     }
 
     const uint32_t m0 = mt * BM + grp * (32u * FA), n0 = nt * BN + wv * (32u * FB);
+    if constexpr (EPI == 2) {
+        // two passes over halves of the row fragments, all 8 waves in each
+        // (slot = wave; a group's 4 waves hold the same rows)
+        constexpr int FS = FA / 2;
+        static_assert(FA % 2 == 0 && 8u * FS * FB * 16u * 64u * 4u <= 2u * STAGE, "half the accumulators in the stages");
+        float *xl = (float *)lds_raw;
+#pragma unroll
+        for (int pass = 0; pass < 2; pass++) {
+            __syncthreads(); // the previous pass's readers (or the loop's last LDS reads) are done
+            gemm_rope_put<FA, FB, FS>(xl, wave, acc, FS * pass, lane);
+            __syncthreads();
+            gemm_rope_store<FS, FB, 2>(g, xl, 4u * grp, wv, m0, FS * pass, nt * BN, lane);
+        }
+        return;
+    }
     float *dst = g.kz > 1u ? g.part + (size_t)z * g.m * g.n : g.c;
 #pragma unroll
     for (int fa = 0; fa < FA; fa++)

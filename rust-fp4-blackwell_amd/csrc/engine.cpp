@@ -475,15 +475,25 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
         if ((rc = launch("rfp4_rmsnorm_quant_rows", dim3(n), dim3(256), s, &na))) return rc;
         e->pf_q_alt = false;
         RFP4_PF_STAGE(0);
-        if ((rc = gemm_launch(s, n, nqkv, c.dim, e->pf_codes, e->pf_scales, e->pf_scales_t, w.qkv_c, w.qkv_s, w.qkv_st,
-                              e->pf_c, e->gemm_part))) return rc;
-        RFP4_PF_STAGE(1);
-        RopeRowsArgs ra{};
-        ra.qkv = e->pf_c; ra.cosv = e->cos_tab; ra.sinv = e->sin_tab; ra.kc = kc; ra.vc = vc;
-        ra.ts = hd; ra.hs = (uint64_t)e->max_seq_alloc * hd;
-        ra.rows = n; ra.row_stride = nqkv; ra.n_heads = c.n_heads; ra.n_kv_heads = c.n_kv_heads;
-        ra.head_dim = hd; ra.pos0 = pos0;
-        if ((rc = launch("rfp4_rope_kv_rows", dim3(n), dim3(256), s, &ra))) return rc;
+        // q|k|v: RoPE and the fp16 K/V cache rows in the GEMM's epilogue
+        // where the plan has that kernel (bit-identical to the row kernel
+        // after the GEMM; not when the stage test hook wants the GEMM's output)
+        const uint64_t kv_hs = (uint64_t)e->max_seq_alloc * hd;
+        if (stop != (int)(10u * l + 1u) && prefill_rope_mode() == 0 && gemm_rope_ok(n, nqkv, c.dim, hd)) {
+            const GemmRope gr{e->cos_tab, e->sin_tab, kc, vc, hd, kv_hs, pos0, qd, kvd, hd};
+            if ((rc = gemm_rope_launch(s, n, nqkv, c.dim, e->pf_codes, e->pf_scales, e->pf_scales_t, w.qkv_c, w.qkv_s,
+                                       w.qkv_st, e->pf_c, gr))) return rc;
+        } else {
+            if ((rc = gemm_launch(s, n, nqkv, c.dim, e->pf_codes, e->pf_scales, e->pf_scales_t, w.qkv_c, w.qkv_s,
+                                  w.qkv_st, e->pf_c, e->gemm_part))) return rc;
+            RFP4_PF_STAGE(1);
+            RopeRowsArgs ra{};
+            ra.qkv = e->pf_c; ra.cosv = e->cos_tab; ra.sinv = e->sin_tab; ra.kc = kc; ra.vc = vc;
+            ra.ts = hd; ra.hs = kv_hs;
+            ra.rows = n; ra.row_stride = nqkv; ra.n_heads = c.n_heads; ra.n_kv_heads = c.n_kv_heads;
+            ra.head_dim = hd; ra.pos0 = pos0;
+            if ((rc = launch("rfp4_rope_kv_rows", dim3(n), dim3(256), s, &ra))) return rc;
+        }
         RFP4_PF_STAGE(2);
         // causal attention of the prompt rows (row r sees positions 0 .. pos0 + r)
         if (prefill_attn_mode() == 1) {

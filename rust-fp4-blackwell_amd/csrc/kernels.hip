@@ -189,7 +189,13 @@ GEMM_KERNEL_PP(256, 256, 4, 2)
 GEMM_KERNEL_PP(256, 128, 4, 1)
 // the prefill's gate|up projection with SwiGLU and the MXFP4 rows of its
 // output in the epilogue (GemmArgs::q_codes)
-K512 void rfp4_gemm_256x256_ppsw(GemmArgs a) { gemm_pp_body<4, 2, true>(a); }
+K512 void rfp4_gemm_256x256_ppsw(GemmArgs a) { gemm_pp_body<4, 2, 1>(a); }
+// the prefill's q|k|v projection with RoPE and the fp16 K/V cache rows in
+// the epilogue (GemmArgs::rope_cos): the plans of that shape at 512 and
+// 2048 prompt rows
+K256 void rfp4_gemm_128x128_rope(GemmArgs a) { gemm_body<2, 2, 2, 2, 2, GEMM_PIPE(2, 2), true>(a); }
+K256 void rfp4_gemm_128x128_p3_rope(GemmArgs a) { gemm_body<2, 2, 2, 2, 3, GEMM_PIPE(2, 2), true>(a); }
+K512 void rfp4_gemm_256x256_pp_rope(GemmArgs a) { gemm_pp_body<4, 2, 2>(a); }
 K256 void rfp4_gemm_reduce(GemmArgs a) { gemm_reduce_body(a); }
 // row-major E8M0 scales -> the step-blocked copy the tiled kernels read
 K256 void rfp4_scales_tile(ScaleTileArgs a) { scales_tile_body(a); }

@@ -521,6 +521,8 @@ static thread_local int t_prefill_stop = -2; // stage after which the batched pr
 int prefill_stop() { return t_prefill_stop; }
 static thread_local int t_prefill_swiglu = 0; // 0: SwiGLU + MXFP4 in the gate|up GEMM's epilogue where it applies, 1: the row kernel
 int prefill_swiglu_mode() { return t_prefill_swiglu; }
+static thread_local int t_prefill_rope = 0; // 0: RoPE + K/V cache rows in the q|k|v GEMM's epilogue where it applies, 1: the row kernel
+int prefill_rope_mode() { return t_prefill_rope; }
 
 bool attn_inmerge_mode(int mode, uint32_t splits)
 {
@@ -638,6 +640,15 @@ extern "C" int rfp4_debug_prefill_swiglu(int mode)
     if (mode != 0 && mode != 1)
         return set_error(RFP4_E_INVALID, "prefill SwiGLU mode must be 0 (in the gate|up GEMM where it applies) or 1 (row kernel)");
     t_prefill_swiglu = mode;
+    return RFP4_OK;
+}
+
+extern "C" int rfp4_debug_prefill_rope(int mode)
+{
+    using namespace rfp4;
+    if (mode != 0 && mode != 1)
+        return set_error(RFP4_E_INVALID, "prefill RoPE mode must be 0 (in the q|k|v GEMM where it applies) or 1 (row kernel)");
+    t_prefill_rope = mode;
     return RFP4_OK;
 }
 
@@ -1479,6 +1490,50 @@ int gemm_swiglu_launch(hipStream_t stream, uint32_t m, uint32_t ffn, uint32_t k,
                q_codes, q_scales, q_scales_t, ffn, 0u};
     const uint64_t tiles = (uint64_t)((m + 255u) / 256u) * (ffn / 128u);
     return launch("rfp4_gemm_256x256_ppsw", dim3((unsigned)tiles), dim3(512), stream, &a);
+}
+
+// The _rope kernel for the plan of (m, n, k): the 128x128 tile with 2 or 3
+// stages, the 256x256 ping-pong tile, no K split (name null: none).
+struct RopeKernel {
+    const char *name;
+    int tile;
+    unsigned threads;
+};
+static RopeKernel gemm_rope_kernel(uint32_t m, uint32_t n, uint32_t k)
+{
+    Runtime *rt = g_rt;
+    if (!rt || m == 0 || n == 0 || k == 0 || k % 256u) return {nullptr, 0, 0};
+    const GemmPlan p = gemm_plan(m, n, k, (uint32_t)rt->num_cus);
+    if (p.tile == kGemmSkinny || p.kz != 1u) return {nullptr, 0, 0};
+    const bool pp = gemm_use_pp(p, m, n, k);
+    if (p.tile == 0 && pp) return {"rfp4_gemm_256x256_pp_rope", 0, 512u};
+    if (p.tile == 2 && !pp && p.nst == 2) return {"rfp4_gemm_128x128_rope", 2, 256u};
+    if (p.tile == 2 && !pp && p.nst == 3) return {"rfp4_gemm_128x128_p3_rope", 2, 256u};
+    return {nullptr, 0, 0};
+}
+
+bool gemm_rope_ok(uint32_t m, uint32_t n, uint32_t k, uint32_t hd)
+{
+    return (hd == 64u || hd == 128u) && n % hd == 0u && gemm_rope_kernel(m, n, k).name != nullptr;
+}
+
+int gemm_rope_launch(hipStream_t stream, uint32_t m, uint32_t n, uint32_t k, const uint8_t *a_codes,
+                     const uint8_t *a_scales, const uint8_t *a_st, const uint8_t *w_codes, const uint8_t *w_scales,
+                     const uint8_t *w_st, float *c, const GemmRope &r)
+{
+    if (!a_codes || !a_st || !w_codes || !w_st || !c || !r.cosv || !r.sinv || !r.kc || !r.vc)
+        return set_error(RFP4_E_INVALID, "gemm_rope: null pointer");
+    if (((uintptr_t)a_codes | (uintptr_t)w_codes | (uintptr_t)c) & 15u || ((uintptr_t)a_st | (uintptr_t)w_st) & 3u)
+        return set_error(RFP4_E_ALIGN, "gemm_rope: misaligned codes, scales or output");
+    if (!gemm_rope_ok(m, n, k, r.hd) || r.q % r.hd || r.kv % r.hd || n != r.q + 2u * r.kv)
+        return set_error(RFP4_E_SHAPE, "gemm_rope: no RoPE epilogue for %u x %u x %u with heads of %u (q %u, kv %u)", m,
+                         n, k, r.hd, r.q, r.kv);
+    const RopeKernel rk = gemm_rope_kernel(m, n, k);
+    const GemmTile &t = kGemmTiles[rk.tile];
+    GemmArgs a{a_codes, a_scales, w_codes, w_scales, c, nullptr, m, n, k, 1u, nullptr, a_st, w_st,
+               nullptr, nullptr, nullptr, 0u, 0u, r.cosv, r.sinv, r.kc, r.vc, r.ts, r.hs, r.pos0, r.q, r.kv, r.hd};
+    const uint64_t tiles = (uint64_t)ceil_div(m, t.bm) * ceil_div(n, t.bn);
+    return launch(rk.name, dim3((unsigned)tiles), dim3(rk.threads), stream, &a);
 }
 
 } // namespace rfp4

@@ -107,6 +107,24 @@ bool gemm_swiglu_ok(uint32_t m, uint32_t ffn, uint32_t k);
 int gemm_swiglu_launch(hipStream_t stream, uint32_t m, uint32_t ffn, uint32_t k, const uint8_t *a_codes,
                        const uint8_t *a_scales, const uint8_t *a_st, const uint8_t *w_codes, const uint8_t *w_scales,
                        const uint8_t *w_st, uint8_t *q_codes, uint8_t *q_scales, uint8_t *q_scales_t);
+// The prefill's q|k|v projection with RoPE and the fp16 K/V cache rows in
+// the GEMM's epilogue (the _rope kernels; GemmArgs::rope_cos): m rows of
+// K = k into n = q + 2 kv columns of c, heads hd wide, row r at position
+// pos0 + r, cache element (pos, kv head, d) at pos * ts + head * hs + d.
+// gemm_rope_ok: whether the plan of the plain GEMM (m, n, k) is a tile with
+// that epilogue compiled (128x128 with 2 or 3 stages, 256x256 ping-pong; no
+// K split) and hd 64 or 128; its output is then bit-identical to the GEMM
+// followed by the RoPE + K/V row kernel.
+struct GemmRope {
+    const float *cosv, *sinv;
+    uint16_t *kc, *vc;
+    uint64_t ts, hs;
+    uint32_t pos0, q, kv, hd;
+};
+bool gemm_rope_ok(uint32_t m, uint32_t n, uint32_t k, uint32_t hd);
+int gemm_rope_launch(hipStream_t stream, uint32_t m, uint32_t n, uint32_t k, const uint8_t *a_codes,
+                     const uint8_t *a_scales, const uint8_t *a_st, const uint8_t *w_codes, const uint8_t *w_scales,
+                     const uint8_t *w_st, float *c, const GemmRope &r);
 // Bytes of the step-blocked copy of [rows][k/32] E8M0 scales.
 inline size_t scales_tiled_bytes(uint32_t rows, uint32_t k) { return (size_t)((rows + 31u) / 32u) * 32u * (k / 32u); }
 // Row-major scales of one or two matrices (rows1 = 0: one) into step-blocked copies, k % 256 == 0.
@@ -130,6 +148,7 @@ int attn_head_split_mode();                      // this thread's rfp4_debug_att
 int qkva_mode();                                 // this thread's rfp4_debug_qkv_attn setting
 int prefill_stop();                              // this thread's rfp4_debug_prefill_stop setting
 int prefill_swiglu_mode();                       // this thread's rfp4_debug_prefill_swiglu setting
+int prefill_rope_mode();                         // this thread's rfp4_debug_prefill_rope setting
 bool attn_inmerge_mode(int mode, uint32_t splits); // attn_inmerge under an explicit setting
 constexpr uint32_t kAttnInmergeMaxSplits = 8;
 // Whether an engine's one-row attention with `splits` splits uses the tagged

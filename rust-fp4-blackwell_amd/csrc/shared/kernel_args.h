@@ -256,6 +256,17 @@ typedef struct GemmArgs {
     // pair_off).  c is not written.
     uint8_t *q_codes, *q_scales, *q_scales_t;
     uint32_t pair_off, pad;
+    // RoPE + K/V cache epilogue (the _rope kernels only, kz = 1): the output
+    // columns are rope_q / rope_hd q heads, then rope_kv / rope_hd k heads,
+    // then as many v heads, rope_hd (64 or 128) wide; row r is position
+    // rope_pos0 + r.  The tile rotates the q and k columns by rope_cos /
+    // rope_sin ([pos][rope_hd / 2]), writes rotated q, k and plain v to c,
+    // and k (rotated) and v as fp16 into kc / vc: element (pos, kv head, d)
+    // at pos * kv_ts + head * kv_hs + d.
+    const float *rope_cos, *rope_sin;
+    uint16_t *kc, *vc;
+    uint64_t kv_ts, kv_hs;
+    uint32_t rope_pos0, rope_q, rope_kv, rope_hd;
 } GemmArgs;
 
 // Row-major E8M0 scales [rows][k/32] -> the step-blocked layout of GemmArgs

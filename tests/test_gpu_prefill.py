@@ -237,3 +237,62 @@ def test_prefill_swiglu_in_gemm_epilogue(rf, orc):
     assert off_s <= n * ffn // 32 // 10000 and off_c <= n * ffn // 2 // 10000, (off_s, off_c)
     eng.close()
     ref.close()
+
+
+@pytest.mark.parametrize("cfg,n,pos0,tile,nst,plan", [
+    (TINY, 37, 0, 2, 2, "rfp4_gemm_128x128/kz1"),             # heads of 64
+    (TINY128, 250, 0, 2, 3, "rfp4_gemm_128x128_p3/kz1"),      # heads of 128, ragged rows
+    (TINY128, 200, 0, 0, 0, "rfp4_gemm_256x256_pp/kz1"),
+    (G8, 70, 5, 0, 0, "rfp4_gemm_256x256_pp/kz1"),            # 640 columns: a ragged column tile; pos0 > 0
+])
+def test_prefill_rope_in_gemm_epilogue(rf, orc, cfg, n, pos0, tile, nst, plan):
+    """RoPE and the fp16 K/V cache rows in the q|k|v GEMM's epilogue
+    (rfp4_gemm_128x128_rope, _128x128_p3_rope, _256x256_pp_rope), each reached
+    by a forced plan, heads of 64 and 128: the staged check (stage 2 compares
+    the rotated q and the fp16 K/V rows bit for bit with the oracle's RoPE of
+    the GEMM's own output, which the stop after stage 1 takes from the plain
+    GEMM), and against the GEMM + row kernel path (rfp4_debug_prefill_rope(1)):
+    identical q|k|v rows and caches after stage 2 of every layer, and the same
+    next token."""
+    seed = 0x20BE + n
+    hd, dim = cfg["head_dim"], cfg["dim"]
+    nqkv = (cfg["n_heads"] + 2 * cfg["n_kv_heads"]) * hd
+    rng = np.random.default_rng(n + 1000 * tile)
+    head = [int(t) for t in rng.integers(0, cfg["vocab"], pos0)]
+    prompt = rng.integers(0, cfg["vocab"], n, dtype=np.uint32)
+    print(f"prefill RoPE epilogue: dim={dim} head_dim={hd} n={n} pos0={pos0} plan {plan}", flush=True)
+    lib = rf.load()
+    eng = _engine(rf, cfg, seed)
+    ref = orc.Model(cfg, seed)
+    got = {}
+    try:
+        rf.debug_gemm_plan(tile, 1)
+        rf.check(lib.rfp4_debug_gemm_stages(nst))
+        assert rf.gemm_plan_kernel(n, nqkv, dim) == plan
+        if pos0:
+            assert eng.prefill(head, 0) == ref.prefill(head, 0)
+        tok = check_prefill_stages(rf, orc, eng, ref, cfg, prompt, pos0)
+        for mode in (0, 1):
+            rf.check(lib.rfp4_debug_prefill_rope(mode))
+            outs = []
+            for l in range(cfg["n_layers"]):
+                eng.prefill_stop(prompt, pos0, 10 * l + 2)
+                outs.append(eng.prefill_buffer("c", (n, nqkv)))
+                outs.extend(eng.kv_host(l))
+            got[mode] = (outs, eng.prefill(prompt, pos0))
+    finally:
+        rf.check(lib.rfp4_debug_prefill_rope(0))
+        rf.check(lib.rfp4_debug_gemm_stages(0))
+        rf.debug_gemm_plan(-1, 0)
+    for i, (a, b) in enumerate(zip(got[0][0], got[1][0])):
+        np.testing.assert_array_equal(a, b, err_msg=f"output {i} (layer {i // 3}: q|k|v rows, k cache, v cache)")
+    assert got[0][1] == got[1][1] == tok
+    eng.close()
+    ref.close()
+
+
+def test_prefill_rope_hook_rejects_bad_values(rf):
+    lib = rf.load()
+    assert lib.rfp4_debug_prefill_rope(2) == -1
+    assert lib.rfp4_debug_prefill_rope(-1) == -1
+    rf.check(lib.rfp4_debug_prefill_rope(0))

@@ -19,7 +19,7 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HSACO = os.path.join(ROOT, "rust-fp4-blackwell_amd", "build", "kernels.hsaco")
 LLVM = "/opt/rocm/llvm/bin"
-TILED = re.compile(r"^rfp4_gemm_\d+x\d+(_p\d|_pp|_ppsw)?$")
+TILED = re.compile(r"^rfp4_gemm_\d+x\d+(_p\d|_pp|_ppsw)?(_rope)?$")
 
 
 def _regs(text):
