@@ -23,7 +23,7 @@
 // logits by percent.  Operand
 // layout (pinned by the fp16 layout test): lane l holds A row / B column
 // l % 16 and K = 8 (l / 16) .. +7; accumulator r of lane l is D[4 (l/16) + r][l % 16].
-// The next block's K/V loads are in flight while the current block computes.
+// The next two blocks' K/V loads are in flight while the current block computes.
 #pragma once
 #include "common.h"
 
@@ -98,39 +98,54 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
 
     // ---- K / V block loads: K piece (key tid / LPK, dims 8 (tid % LPK)), V
     // piece (key tid % 32, dims 8 (tid / 32)) -- consecutive lanes take
-    // consecutive keys, so the transposed V writes fall on consecutive halves
-    uint4 kr[LD], vr[LD];
-#define RFP4_PF_LOAD(B)                                                                                   \
+    // consecutive keys, so the transposed V writes fall on consecutive halves.
+    // Cached loads (each key row is read by every query tile of its KV head),
+    // two register sets: block b + 2's loads are issued when block b's data
+    // has gone to LDS, so each load has two blocks' compute to land.
+    // (each set one 8-word vector value per operand, piece j in words 4j ..
+    // 4j + 3: vectors stay in registers where the two sets' code is merged)
+    static_assert(LD <= 2, "at most two 16-byte pieces per thread and block");
+    typedef uint32_t pf_u32x8 __attribute__((ext_vector_type(8)));
+    pf_u32x8 kr0, vr0, kr1, vr1;
+#define RFP4_PF_LOAD(B, KR, VR)                                                                           \
     do {                                                                                                  \
+        _Pragma("unroll") for (int j = 0; j < LD; j++) {                                                  \
+            /* threads past the block's pieces load the last one again (unused) */                        \
+            const uint32_t p = min((uint32_t)tid + (uint32_t)T * (uint32_t)j, (uint32_t)(PF_BK * LPK) - 1u); \
+            const uint32_t kk = min((B) * PF_BK + p / LPK, nk - 1u), kd = 8u * (p % LPK);                 \
+            const uint32_t vk = min((B) * PF_BK + p % PF_BK, nk - 1u), vd = 8u * (p / PF_BK);              \
+            const u32x4 kx = *(const u32x4 *)(kc + (size_t)kk * a.ts + kd);                               \
+            const u32x4 vx = *(const u32x4 *)(vc + (size_t)vk * a.ts + vd);                               \
+            if (j == 0) { KR.lo = kx; VR.lo = vx; } else { KR.hi = kx; VR.hi = vx; }                      \
+        }                                                                                                 \
+    } while (0)
+    // block b's K rows and transposed V rows into LDS, then block b + 2's loads into the same registers
+#define RFP4_PF_STAGE(b, KR, VR)                                                                          \
+    do {                                                                                                  \
+        __syncthreads(); /* the previous block's LDS reads are done */                                    \
         _Pragma("unroll") for (int j = 0; j < LD; j++) {                                                  \
             const uint32_t p = (uint32_t)tid + (uint32_t)T * (uint32_t)j;                                 \
             if (!LFULL && p >= (uint32_t)(PF_BK * LPK)) break;                                            \
-            const uint32_t kk = min((B) * PF_BK + p / LPK, nk - 1u), kd = 8u * (p % LPK);                 \
-            kr[j] = load_nt16(kc + (size_t)kk * a.ts + kd);                                               \
-            const uint32_t vk = min((B) * PF_BK + p % PF_BK, nk - 1u), vd = 8u * (p / PF_BK);              \
-            vr[j] = load_nt16(vc + (size_t)vk * a.ts + vd);                                               \
+            const u32x4 kx = j == 0 ? KR.lo : KR.hi, vx = j == 0 ? VR.lo : VR.hi;                          \
+            *(u32x4 *)&ks[p / LPK][8u * (p % LPK)] = kx;                                                  \
+            const uint32_t vk = p % PF_BK, vd = 8u * (p / PF_BK);                                          \
+            _Pragma("unroll") for (int i = 0; i < 4; i++) {                                               \
+                vt[vd + 2u * i][vk] = __builtin_bit_cast(_Float16, (uint16_t)(vx[i] & 0xFFFFu));          \
+                vt[vd + 2u * i + 1u][vk] = __builtin_bit_cast(_Float16, (uint16_t)(vx[i] >> 16));         \
+            }                                                                                             \
         }                                                                                                 \
+        __syncthreads();                                                                                  \
+        RFP4_PF_LOAD((b) + 2u, KR, VR);                                                                   \
     } while (0)
-    RFP4_PF_LOAD(0u);
+    // Every load is issued on every path (keys clamped to the last one, so a
+    // block past the end re-reads it): the compiler's wait for a set then
+    // counts exactly the other set's loads behind it, where paths with and
+    // without a load would make it wait for both sets.
+    RFP4_PF_LOAD(0u, kr0, vr0);
+    RFP4_PF_LOAD(1u, kr1, vr1);
 
-    for (uint32_t b = 0; b < nblk; b++) {
-        __syncthreads(); // the previous block's LDS reads are done
-#pragma unroll
-        for (int j = 0; j < LD; j++) {
-            const uint32_t p = (uint32_t)tid + (uint32_t)T * (uint32_t)j;
-            if (!LFULL && p >= (uint32_t)(PF_BK * LPK)) break;
-            *(uint4 *)&ks[p / LPK][8u * (p % LPK)] = kr[j];
-            const uint32_t vk = p % PF_BK, vd = 8u * (p / PF_BK);
-            const uint32_t w[4] = {vr[j].x, vr[j].y, vr[j].z, vr[j].w};
-#pragma unroll
-            for (int i = 0; i < 4; i++) {
-                vt[vd + 2u * i][vk] = __builtin_bit_cast(_Float16, (uint16_t)(w[i] & 0xFFFFu));
-                vt[vd + 2u * i + 1u][vk] = __builtin_bit_cast(_Float16, (uint16_t)(w[i] >> 16));
-            }
-        }
-        __syncthreads();
-        if (b + 1u < nblk) RFP4_PF_LOAD(b + 1u);
-
+    // the block's scores, softmax and P V from the staged K / V
+    auto block = [&](uint32_t b) {
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
             const uint32_t t = (uint32_t)(wave * MT + mt);
@@ -194,7 +209,19 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
                 o[mt][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vb, o[mt][n], 0, 0, 0);
             }
         }
+    };
+    uint32_t b = 0;
+    for (; b + 1u < nblk; b += 2u) {
+        RFP4_PF_STAGE(b, kr0, vr0);
+        block(b);
+        RFP4_PF_STAGE(b + 1u, kr1, vr1);
+        block(b + 1u);
     }
+    if (b < nblk) {
+        RFP4_PF_STAGE(b, kr0, vr0);
+        block(b);
+    }
+#undef RFP4_PF_STAGE
 #undef RFP4_PF_LOAD
 
     // ---- out[row][head][dim] = O / l for rows in the prompt and heads < G
