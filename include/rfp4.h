@@ -170,8 +170,10 @@ int attn_decode_f16_noalloc(rfp4_stream_t stream, uint32_t n_heads, uint32_t n_k
  * fp16 K/V (the rows' own k, v already in the caches): row r is attn_decode_f16
  * with seq = pos0 + r + 1 (llama_run/src/main.rs:148-242 applied row by row;
  * the reference feeds a prompt one token at a time, :550-556).  q row r at
- * q + r*q_row_stride, out row r at out + r*out_row_stride (floats).  fp16
- * matrix-core operands, f32 accumulation.  No reference counterpart as one call. */
+ * q + r*q_row_stride, out row r at out + r*out_row_stride (floats); q, out and
+ * the K/V rows 16-byte aligned (row strides multiples of 4 floats / 8 halves),
+ * else RFP4_E_ALIGN.  fp16 matrix-core operands, f32 accumulation.  No
+ * reference counterpart as one call. */
 int attn_prefill_f16(rfp4_stream_t stream, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim, uint32_t pos0,
                      uint32_t rows, const float *q, uint32_t q_row_stride, const uint16_t *kc, const uint16_t *vc,
                      uint64_t token_stride, uint64_t head_stride, float *out, uint32_t out_row_stride);

@@ -10,11 +10,17 @@
 // heads, G <= GT real), i.e. NT = (BQ/16) * GT tiles of 16 (row, head) pairs,
 // MT = NT / NW per wave, and walks the keys 0 .. last
 // row's position in blocks of 32: K rows staged in LDS as loaded, V rows
-// staged transposed (dimension-major), both as v_mfma_f32_16x16x32_f16
-// operands read with one 16-byte LDS read per lane:
-//   S (16 x 32) = Q (16 x HD) . K^T        -- A = q as two fp16 terms
-//   online softmax per row (base 2, f32)   -- rows live in 16-lane groups
-//   O (16 x HD) += P (16 x 32) . V         -- A = p as two fp16 terms, through LDS
+// staged transposed (dimension-major), as v_mfma_f32_16x16x32_f16 operands,
+// every product transposed so that the scores' accumulator is the next
+// product's operand as it lies in the registers:
+//   S^T (32 x 16) = K (32 x HD) . Q^T         -- B = q as two fp16 terms
+//   online softmax per row (base 2, f32)      -- a row lives in the 4 lanes
+//                                                l % 16 = row of the wave
+//   O^T (HD x 16) += V^T (HD x 32) . P^T      -- B = p as two fp16 terms
+// Lane (q4 = l / 16, row l % 16) holds the scores of keys 4 q4 .. +3 and
+// 16 + 4 q4 .. +3 of a block, which are the 8 K values of its P^T operand;
+// the V^T operand takes the same 8 keys of each dimension (two 8-byte reads of
+// the transposed V rows), so P never leaves the registers.
 // q and p enter as hi + lo (hi = fp16(x), lo = fp16(x - hi): about 2^-22
 // relative, two MFMAs per product; K and V are fp16 already), products exact
 // and f32 accumulation, so the output matches the f32 decode kernel's to
@@ -29,7 +35,7 @@
 
 #define PF_BK 32   // keys per block
 #define PF_KPAD 8  // fp16 padding of a staged K row (16 consecutive rows -> 16 distinct bank groups)
-#define PF_TPAD 8  // fp16 padding of a transposed V row / a P row
+#define PF_TPAD 8  // fp16 padding of a transposed V row
 
 // One query tile: prompt rows r0 .. r0 + BQ of KV head blockIdx.y.
 template <int HD, int GT, int NW>
@@ -50,7 +56,6 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
     static_assert(LFULL || LD == 1, "block load split");
     __shared__ __align__(16) _Float16 ks[PF_BK][KROW];
     __shared__ __align__(16) _Float16 vt[HD][TROW];
-    __shared__ __align__(16) _Float16 ps[NW][MT][2][16][TROW]; // P hi, lo
 
     const uint32_t kvh = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -83,15 +88,14 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
         }
     }
 
+    // O^T tile n: accumulator r of lane l is dimension 16 n + 4 q4 + r of row l16;
+    // the running max and sum are the lane's row's
     f32x4 o[MT][NN];
-    float mrun[MT][4], lrun[MT][4];
+    float mrun[MT], lrun[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            mrun[mt][r] = -3.402823466e38f;
-            lrun[mt][r] = 0.0f;
-        }
+        mrun[mt] = -3.402823466e38f;
+        lrun[mt] = 0.0f;
 #pragma unroll
         for (int n = 0; n < NN; n++) o[mt][n] = {0.0f, 0.0f, 0.0f, 0.0f};
     }
@@ -149,64 +153,58 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
             const uint32_t t = (uint32_t)(wave * MT + mt);
-            // ---- S = Q K^T for the block's two 16-key halves
+            // ---- S^T = K Q^T for the block's two 16-key halves: accumulator r
+            // of lane l is key 16 h + 4 q4 + r of row l16
             f32x4 s[2];
 #pragma unroll
             for (int h = 0; h < 2; h++) {
                 s[h] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int k = 0; k < KS; k++) {
-                    const f16x8 kb = *(const f16x8 *)&ks[16u * h + l16][32 * k + 8u * q4];
-                    s[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qa[mt][k], kb, s[h], 0, 0, 0);
-                    s[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[mt][k], kb, s[h], 0, 0, 0);
+                    const f16x8 ka = *(const f16x8 *)&ks[16u * h + l16][32 * k + 8u * q4];
+                    s[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qa[mt][k], s[h], 0, 0, 0);
+                    s[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[mt][k], s[h], 0, 0, 0);
                 }
             }
-            // ---- causal mask, online softmax (base 2) per row 4 q4 + r
-            float p[2][4];
+            // ---- causal mask, online softmax (base 2) of the lane's row
+            const uint32_t qrow = r0 + 16u * (t / GT) + l16;
+            const uint32_t qpos = pos0 + min(qrow, nrows - 1u);
+            float p[8];
+            float mx = -3.402823466e38f;
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const uint32_t qrow = r0 + 16u * (t / GT) + 4u * q4 + (uint32_t)r;
-                const uint32_t qpos = pos0 + min(qrow, nrows - 1u);
-                float mx = -3.402823466e38f;
+            for (int h = 0; h < 2; h++)
 #pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    const uint32_t key = b * PF_BK + 16u * h + l16;
+                for (int r = 0; r < 4; r++) {
+                    const uint32_t key = b * PF_BK + 16u * h + 4u * q4 + (uint32_t)r;
                     const float v = s[h][r] * scale;
-                    p[h][r] = key <= qpos ? v : -3.402823466e38f;
-                    mx = fmaxf(mx, p[h][r]);
+                    p[4 * h + r] = key <= qpos ? v : -3.402823466e38f;
+                    mx = fmaxf(mx, p[4 * h + r]);
                 }
-                mx = row16_max(mx);
-                const float mnew = fmaxf(mrun[mt][r], mx);
-                const float alpha = __builtin_amdgcn_exp2f(mrun[mt][r] - mnew);
-                mrun[mt][r] = mnew;
-                float ls = 0.0f;
+            mx = xor32_max(xor16_max(mx));
+            const float mnew = fmaxf(mrun[mt], mx);
+            const float alpha = __builtin_amdgcn_exp2f(mrun[mt] - mnew);
+            mrun[mt] = mnew;
+            float ls = 0.0f;
 #pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    p[h][r] = __builtin_amdgcn_exp2f(p[h][r] - mnew);
-                    ls += p[h][r];
-                }
-                lrun[mt][r] = fmaf(lrun[mt][r], alpha, row16_sum(ls));
-#pragma unroll
-                for (int n = 0; n < NN; n++) o[mt][n][r] *= alpha;
+            for (int i = 0; i < 8; i++) {
+                p[i] = __builtin_amdgcn_exp2f(p[i] - mnew);
+                ls += p[i];
             }
-            // ---- P (hi, lo) to the A layout through LDS (this wave's rows only)
+            lrun[mt] = fmaf(lrun[mt], alpha, xor32_sum(xor16_sum(ls)));
 #pragma unroll
-            for (int r = 0; r < 4; r++)
-#pragma unroll
-                for (int h = 0; h < 2; h++) {
-                    const _Float16 ph = (_Float16)p[h][r];
-                    ps[wave][mt][0][4u * q4 + (uint32_t)r][16u * h + l16] = ph;
-                    ps[wave][mt][1][4u * q4 + (uint32_t)r][16u * h + l16] = (_Float16)(p[h][r] - (float)ph);
-                }
-            __builtin_amdgcn_wave_barrier();
-            const f16x8 pa = *(const f16x8 *)&ps[wave][mt][0][l16][8u * q4];
-            const f16x8 pl = *(const f16x8 *)&ps[wave][mt][1][l16][8u * q4];
-            // ---- O += P V
+            for (int n = 0; n < NN; n++) o[mt][n] *= alpha;
+            // ---- P^T as hi + lo operands, straight from the registers
+            f16x8 pb, pl;
+            split_hi_lo8(p, pb, pl);
+            // ---- O^T += V^T P^T: dimension row 16 n + l16, the lane's 8 keys
 #pragma unroll
             for (int n = 0; n < NN; n++) {
-                const f16x8 vb = *(const f16x8 *)&vt[16u * n + l16][8u * q4];
-                o[mt][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, o[mt][n], 0, 0, 0);
-                o[mt][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vb, o[mt][n], 0, 0, 0);
+                const _Float16 *vrow = &vt[16u * n + l16][4u * q4];
+                typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+                const f16x4 v0 = *(const f16x4 *)vrow, v1 = *(const f16x4 *)(vrow + 16);
+                const f16x8 va = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                o[mt][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb, o[mt][n], 0, 0, 0);
+                o[mt][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl, o[mt][n], 0, 0, 0);
             }
         }
     };
@@ -225,18 +223,17 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
 #undef RFP4_PF_LOAD
 
     // ---- out[row][head][dim] = O / l for rows in the prompt and heads < G
+    // (lane: row l16, dimensions 16 n + 4 q4 .. +3 of each tile n)
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
         const uint32_t t = (uint32_t)(wave * MT + mt), g = t % GT;
-        if (g >= G) continue;
+        const uint32_t row = r0 + 16u * (t / GT) + l16;
+        if (g >= G || row >= nrows) continue;
+        float *op = a.out + (size_t)row * a.out_rs + (size_t)(kvh * G + g) * HD + 4u * q4;
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const uint32_t row = r0 + 16u * (t / GT) + 4u * q4 + (uint32_t)r;
-            if (row >= nrows) continue;
-            float *op = a.out + (size_t)row * a.out_rs + (size_t)(kvh * G + g) * HD + l16;
-#pragma unroll
-            for (int n = 0; n < NN; n++) op[16 * n] = __fdiv_rn(o[mt][n][r], lrun[mt][r]);
-        }
+        for (int n = 0; n < NN; n++)
+            *(float4 *)(op + 16 * n) = make_float4(__fdiv_rn(o[mt][n][0], lrun[mt]), __fdiv_rn(o[mt][n][1], lrun[mt]),
+                                                   __fdiv_rn(o[mt][n][2], lrun[mt]), __fdiv_rn(o[mt][n][3], lrun[mt]));
     }
 }
 

@@ -1016,6 +1016,8 @@ int attn_prefill_f16(rfp4_stream_t stream, uint32_t n_heads, uint32_t n_kv_heads
     if (!runtime()) return set_error(RFP4_E_NOT_INIT, "rfp4_init has not been called");
     if (((uintptr_t)q | (uintptr_t)kc | (uintptr_t)vc) & 15u || q_row_stride % 4u || (token_stride * 2u) % 16u)
         return set_error(RFP4_E_ALIGN, "attn_prefill_f16: q rows and K/V rows must start 16-byte aligned");
+    if ((uintptr_t)out & 15u || out_row_stride % 4u)
+        return set_error(RFP4_E_ALIGN, "attn_prefill_f16: out rows must start 16-byte aligned");
     if (rows && q_row_stride < n_heads * head_dim)
         return set_error(RFP4_E_SHAPE, "attn_prefill_f16: q row stride %u < %u", q_row_stride, n_heads * head_dim);
     if (rows && out_row_stride < n_heads * head_dim)

@@ -337,6 +337,11 @@ def test_attn_prefill_f16_strided(rf, orc, stream, nh, nkv, hd, pos0, rows):
     got = dout.to_host(rows * out_rs, np.float32, stream).reshape(rows, out_rs)
     _assert_attn_close(got[:, :nh * hd], oref)
     assert not got[:, nh * hd:].any()   # the row padding is not written
+    # output rows must start 16-byte aligned (the kernel stores 4 floats at once)
+    with pytest.raises(rf.Rfp4Error) as e:
+        rf.attn_prefill_f16(stream, nh, nkv, hd, pos0, rows, _dev(rf, qkv.reshape(-1), stream), q_rs,
+                            _dev(rf, kc, stream), _dev(rf, vc, stream), hd, alloc * hd, dout, out_rs - 2)
+    assert e.value.code == -6
 
 
 def test_swiglu_residual_copy(rf, orc, stream):
