@@ -9,7 +9,7 @@
 // max(16, 16 NW / GT) prompt rows and every query head of one KV head (GT
 // heads, G <= GT real), i.e. NT = (BQ/16) * GT tiles of 16 (row, head) pairs,
 // MT = NT / NW per wave, and walks the keys 0 .. last
-// row's position in blocks of 32: K rows staged in LDS as loaded, V rows
+// row's position in blocks of 64 keys (head dim 64) or 32 (128): K rows staged in LDS as loaded, V rows
 // staged transposed (dimension-major), as v_mfma_f32_16x16x32_f16 operands,
 // every product transposed so that the scores' accumulator is the next
 // product's operand as it lies in the registers:
@@ -18,9 +18,10 @@
 //                                                l % 16 = row of the wave
 //   O^T (HD x 16) += V^T (HD x 32) . P^T      -- B = p as two fp16 terms
 // Lane (q4 = l / 16, row l % 16) holds the scores of keys 4 q4 .. +3 and
-// 16 + 4 q4 .. +3 of a block, which are the 8 K values of its P^T operand;
-// the V^T operand takes the same 8 keys of each dimension (two 8-byte reads of
-// the transposed V rows), so P never leaves the registers.
+// 16 + 4 q4 .. +3 of each 32-key half of a block, which are the 8 K values
+// of its P^T operand for that half; the V^T operand takes the same 8 keys of
+// each dimension (two 8-byte reads of the transposed V rows), so P never
+// leaves the registers.
 // q and p enter as hi + lo (hi = fp16(x), lo = fp16(x - hi): about 2^-22
 // relative, two MFMAs per product; K and V are fp16 already), products exact
 // and f32 accumulation, so the output matches the f32 decode kernel's to
@@ -33,7 +34,6 @@
 #pragma once
 #include "common.h"
 
-#define PF_BK 32   // keys per block
 #define PF_KPAD 8  // fp16 padding of a staged K row (16 consecutive rows -> 16 distinct bank groups)
 #define PF_TPAD 8  // fp16 padding of a transposed V row
 
@@ -47,6 +47,9 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
     constexpr int MT = NT / NW;                      // tiles per wave
     constexpr int KS = HD / 32;                      // K steps of S = Q K^T
     constexpr int NN = HD / 16;                      // 16-wide column tiles of O
+    // keys per block: 64 for head dim 64, 32 for 128 (measured: 8B 2048-row
+    // kernel 96.4 us with 32, 103.2 with 64; TinyLlama 41.2 -> 37.8 us)
+    constexpr int PF_BK = HD == 64 ? 64 : 32;
     constexpr int KROW = HD + PF_KPAD, TROW = PF_BK + PF_TPAD;
     constexpr int LPK = HD / 8;                      // 16-byte pieces per K/V row
     constexpr int T = 64 * NW;                       // threads
@@ -101,16 +104,16 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
     }
 
     // ---- K / V block loads: K piece (key tid / LPK, dims 8 (tid % LPK)), V
-    // piece (key tid % 32, dims 8 (tid / 32)) -- consecutive lanes take
+    // piece (key tid % PF_BK, dims 8 (tid / PF_BK)) -- consecutive lanes take
     // consecutive keys, so the transposed V writes fall on consecutive halves.
     // Cached loads (each key row is read by every query tile of its KV head),
     // two register sets: block b + 2's loads are issued when block b's data
     // has gone to LDS, so each load has two blocks' compute to land.
     // (each set one 8-word vector value per operand, piece j in words 4j ..
     // 4j + 3: vectors stay in registers where the two sets' code is merged)
-    static_assert(LD <= 2, "at most two 16-byte pieces per thread and block");
-    typedef uint32_t pf_u32x8 __attribute__((ext_vector_type(8)));
-    pf_u32x8 kr0, vr0, kr1, vr1;
+    static_assert(LD == 1 || LD == 2 || LD == 4, "16-byte pieces per thread and block");
+    typedef uint32_t pf_vec __attribute__((ext_vector_type(4 * LD)));
+    pf_vec kr0, vr0, kr1, vr1;
 #define RFP4_PF_LOAD(B, KR, VR)                                                                           \
     do {                                                                                                  \
         _Pragma("unroll") for (int j = 0; j < LD; j++) {                                                  \
@@ -120,7 +123,10 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
             const uint32_t vk = min((B) * PF_BK + p % PF_BK, nk - 1u), vd = 8u * (p / PF_BK);              \
             const u32x4 kx = *(const u32x4 *)(kc + (size_t)kk * a.ts + kd);                               \
             const u32x4 vx = *(const u32x4 *)(vc + (size_t)vk * a.ts + vd);                               \
-            if (j == 0) { KR.lo = kx; VR.lo = vx; } else { KR.hi = kx; VR.hi = vx; }                      \
+            _Pragma("unroll") for (int i = 0; i < 4; i++) {                                               \
+                KR[4 * j + i] = kx[i];                                                                    \
+                VR[4 * j + i] = vx[i];                                                                    \
+            }                                                                                             \
         }                                                                                                 \
     } while (0)
     // block b's K rows and transposed V rows into LDS, then block b + 2's loads into the same registers
@@ -130,7 +136,8 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
         _Pragma("unroll") for (int j = 0; j < LD; j++) {                                                  \
             const uint32_t p = (uint32_t)tid + (uint32_t)T * (uint32_t)j;                                 \
             if (!LFULL && p >= (uint32_t)(PF_BK * LPK)) break;                                            \
-            const u32x4 kx = j == 0 ? KR.lo : KR.hi, vx = j == 0 ? VR.lo : VR.hi;                          \
+            const u32x4 kx = {KR[4 * j], KR[4 * j + 1], KR[4 * j + 2], KR[4 * j + 3]};                    \
+            const u32x4 vx = {VR[4 * j], VR[4 * j + 1], VR[4 * j + 2], VR[4 * j + 3]};                    \
             *(u32x4 *)&ks[p / LPK][8u * (p % LPK)] = kx;                                                  \
             const uint32_t vk = p % PF_BK, vd = 8u * (p / PF_BK);                                          \
             _Pragma("unroll") for (int i = 0; i < 4; i++) {                                               \
@@ -153,11 +160,12 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
             const uint32_t t = (uint32_t)(wave * MT + mt);
-            // ---- S^T = K Q^T for the block's two 16-key halves: accumulator r
+            // ---- S^T = K Q^T for the block's 16-key quarters h: accumulator r
             // of lane l is key 16 h + 4 q4 + r of row l16
-            f32x4 s[2];
+            constexpr int NQ = PF_BK / 16;
+            f32x4 s[NQ];
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
+            for (int h = 0; h < NQ; h++) {
                 s[h] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int k = 0; k < KS; k++) {
@@ -169,10 +177,10 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
             // ---- causal mask, online softmax (base 2) of the lane's row
             const uint32_t qrow = r0 + 16u * (t / GT) + l16;
             const uint32_t qpos = pos0 + min(qrow, nrows - 1u);
-            float p[8];
+            float p[4 * NQ];
             float mx = -3.402823466e38f;
 #pragma unroll
-            for (int h = 0; h < 2; h++)
+            for (int h = 0; h < NQ; h++)
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const uint32_t key = b * PF_BK + 16u * h + 4u * q4 + (uint32_t)r;
@@ -186,25 +194,29 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
             mrun[mt] = mnew;
             float ls = 0.0f;
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
+            for (int i = 0; i < 4 * NQ; i++) {
                 p[i] = __builtin_amdgcn_exp2f(p[i] - mnew);
                 ls += p[i];
             }
             lrun[mt] = fmaf(lrun[mt], alpha, xor32_sum(xor16_sum(ls)));
 #pragma unroll
             for (int n = 0; n < NN; n++) o[mt][n] *= alpha;
-            // ---- P^T as hi + lo operands, straight from the registers
-            f16x8 pb, pl;
-            split_hi_lo8(p, pb, pl);
-            // ---- O^T += V^T P^T: dimension row 16 n + l16, the lane's 8 keys
+            // ---- O^T += V^T P^T per 32-key chunk c (quarters 2c, 2c + 1): P^T as
+            // hi + lo operands straight from the registers; V^T dimension row
+            // 16 n + l16 at the lane's 8 keys of the chunk
 #pragma unroll
-            for (int n = 0; n < NN; n++) {
-                const _Float16 *vrow = &vt[16u * n + l16][4u * q4];
-                typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-                const f16x4 v0 = *(const f16x4 *)vrow, v1 = *(const f16x4 *)(vrow + 16);
-                const f16x8 va = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-                o[mt][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb, o[mt][n], 0, 0, 0);
-                o[mt][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl, o[mt][n], 0, 0, 0);
+            for (int c = 0; c < NQ / 2; c++) {
+                f16x8 pb, pl;
+                split_hi_lo8(p + 8 * c, pb, pl);
+#pragma unroll
+                for (int n = 0; n < NN; n++) {
+                    const _Float16 *vrow = &vt[16u * n + l16][32u * c + 4u * q4];
+                    typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+                    const f16x4 v0 = *(const f16x4 *)vrow, v1 = *(const f16x4 *)(vrow + 16);
+                    const f16x8 va = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+                    o[mt][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pb, o[mt][n], 0, 0, 0);
+                    o[mt][n] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va, pl, o[mt][n], 0, 0, 0);
+                }
             }
         }
     };
