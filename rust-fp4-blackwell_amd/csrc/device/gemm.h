@@ -113,9 +113,10 @@ RFP4_DEV void gemm_splitk_last(const GemmArgs &g, const v16f32 (&acc)[FA][FB], u
     __syncthreads();
     if (!s_last) return;
     if (threadIdx.x == 0) __hip_atomic_store(g.counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // every load of the other plane first (one round trip), then the sums
+    // every load of the other plane (and, with c_add, of c) first (one round
+    // trip), then the sums
     const float *other = g.part + (size_t)(1u - z) * plane;
-    float o[FA][FB][16];
+    float o[FA][FB][16], cv[FA][FB][16];
 #pragma unroll
     for (int fa = 0; fa < FA; fa++)
 #pragma unroll
@@ -125,6 +126,7 @@ RFP4_DEV void gemm_splitk_last(const GemmArgs &g, const v16f32 (&acc)[FA][FB], u
             for (int r = 0; r < 16; r++) {
                 const uint32_t row = min(m0 + 32u * fa + 8u * (uint32_t)(r / 4) + 4u * h + (uint32_t)(r % 4), g.m - 1u);
                 o[fa][fb][r] = __hip_atomic_load(other + (size_t)row * g.n + col, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (g.c_add) cv[fa][fb][r] = g.c[(size_t)row * g.n + col];
             }
         }
 #pragma unroll
@@ -135,8 +137,68 @@ RFP4_DEV void gemm_splitk_last(const GemmArgs &g, const v16f32 (&acc)[FA][FB], u
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const uint32_t row = m0 + 32u * fa + 8u * (uint32_t)(r / 4) + 4u * h + (uint32_t)(r % 4);
-                const float v = z == 0u ? __fadd_rn(acc[fa][fb][r], o[fa][fb][r]) : __fadd_rn(o[fa][fb][r], acc[fa][fb][r]);
+                float v = z == 0u ? __fadd_rn(acc[fa][fb][r], o[fa][fb][r]) : __fadd_rn(o[fa][fb][r], acc[fa][fb][r]);
+                if (g.c_add) v = __fadd_rn(cv[fa][fb][r], v);
                 if (row < g.m && col < g.n) g.c[(size_t)row * g.n + col] = v;
+            }
+        }
+}
+
+// The plain epilogue: the wave's accumulators (tile rows m0 .., columns n0
+// ..) into dst, or, with c_add (kz = 1), added to dst: for FAB row
+// fragments at a time every element of dst is loaded first, then one wait,
+// then the sums and stores (a load issued behind a store would also wait
+// for that store: one batch where the registers hold the whole tile).
+// FAB = 0: no accumulating path compiled (the host does not ask it of that
+// kernel).
+template <int FA, int FB, int FAB>
+RFP4_DEV void gemm_store_c(const GemmArgs &g, const v16f32 (&acc)[FA][FB], float *dst, uint32_t m0, uint32_t n0,
+                           uint32_t r32, uint32_t h)
+{
+    static_assert(FAB == 0 || FA % FAB == 0, "whole batches");
+    if constexpr (FAB > 0) if (g.c_add && g.kz == 1u) {
+#pragma unroll
+        for (int f0 = 0; f0 < FA; f0 += FAB) {
+            float cv[FAB][FB][16];
+#pragma unroll
+            for (int i = 0; i < FAB; i++)
+#pragma unroll
+                for (int fb = 0; fb < FB; fb++) {
+                    const uint32_t col = min(n0 + 32u * fb + r32, g.n - 1u);
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const uint32_t row =
+                            min(m0 + 32u * (f0 + i) + 8u * (uint32_t)(r / 4) + 4u * h + (uint32_t)(r % 4), g.m - 1u);
+                        cv[i][fb][r] = dst[(size_t)row * g.n + col];
+                    }
+                }
+            __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): the batch's c
+#pragma unroll
+            for (int i = 0; i < FAB; i++)
+#pragma unroll
+                for (int fb = 0; fb < FB; fb++) {
+                    const uint32_t col = n0 + 32u * fb + r32;
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const uint32_t row = m0 + 32u * (f0 + i) + 8u * (uint32_t)(r / 4) + 4u * h + (uint32_t)(r % 4);
+                        if (row < g.m && col < g.n)
+                            __builtin_nontemporal_store(__fadd_rn(cv[i][fb][r], acc[f0 + i][fb][r]),
+                                                        dst + (size_t)row * g.n + col);
+                    }
+                }
+        }
+        return;
+    }
+#pragma unroll
+    for (int fa = 0; fa < FA; fa++)
+#pragma unroll
+        for (int fb = 0; fb < FB; fb++) {
+            const uint32_t col = n0 + 32u * fb + r32;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const uint32_t row = m0 + 32u * fa + 8u * (uint32_t)(r / 4) + 4u * h + (uint32_t)(r % 4);
+                // non-temporal: C is written once and read by the next launch
+                if (row < g.m && col < g.n) __builtin_nontemporal_store(acc[fa][fb][r], dst + (size_t)row * g.n + col);
             }
         }
 }
@@ -661,19 +723,9 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
             return;
         }
     }
-    float *dst = g.kz > 1u ? g.part + (size_t)z * g.m * g.n : g.c;
-#pragma unroll
-    for (int fa = 0; fa < FA; fa++)
-#pragma unroll
-        for (int fb = 0; fb < FB; fb++) {
-            const uint32_t col = n0 + 32u * fb + r32;
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const uint32_t row = m0 + 32u * fa + 8u * (uint32_t)(r / 4) + 4u * h + (uint32_t)(r % 4);
-                // non-temporal: C is written once and read by the next launch
-                if (row < g.m && col < g.n) __builtin_nontemporal_store(acc[fa][fb][r], dst + (size_t)row * g.n + col);
-            }
-        }
+    // (c_add: the tiles up to 256x128, one batch; the 4-wave 256x256 tile
+    // has no registers for it)
+    gemm_store_c<FA, FB, FA * FB <= 8 ? FA : 0>(g, acc, g.kz > 1u ? g.part + (size_t)z * g.m * g.n : g.c, m0, n0, r32, h);
 }
 
 // Ping-pong tiled GEMM: 8 waves, two per SIMD, in two groups.  Group g of
@@ -974,18 +1026,7 @@ RFP4_DEV void gemm_pp_body(const GemmArgs &g)
         }
         return;
     }
-    float *dst = g.kz > 1u ? g.part + (size_t)z * g.m * g.n : g.c;
-#pragma unroll
-    for (int fa = 0; fa < FA; fa++)
-#pragma unroll
-        for (int fb = 0; fb < FB; fb++) {
-            const uint32_t col = n0 + 32u * fb + r32;
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const uint32_t row = m0 + 32u * fa + 8u * (uint32_t)(r / 4) + 4u * h + (uint32_t)(r % 4);
-                if (row < g.m && col < g.n) __builtin_nontemporal_store(acc[fa][fb][r], dst + (size_t)row * g.n + col);
-            }
-        }
+    gemm_store_c<FA, FB, 1>(g, acc, g.kz > 1u ? g.part + (size_t)z * g.m * g.n : g.c, m0, n0, r32, h);
 }
 
 // Split-K sum: c = part[0] + part[1] + ... + part[kz-1] in that order (the
@@ -1002,6 +1043,10 @@ RFP4_DEV void gemm_reduce_body(const GemmArgs &g)
             sum.y = __fadd_rn(sum.y, p.y);
             sum.z = __fadd_rn(sum.z, p.z);
             sum.w = __fadd_rn(sum.w, p.w);
+        }
+        if (g.c_add) {
+            const float4 c = ((const float4 *)g.c)[e];
+            sum = make_float4(__fadd_rn(c.x, sum.x), __fadd_rn(c.y, sum.y), __fadd_rn(c.z, sum.z), __fadd_rn(c.w, sum.w));
         }
         ((float4 *)g.c)[e] = sum;
     }

@@ -463,6 +463,8 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
     if (stop == -1) return kPrefillStopped;
 #define RFP4_PF_STAGE(S) \
     if (stop == (int)(10u * l + (S))) return kPrefillStopped
+    // the down projection added into x by its GEMM (else left in pf_c for the next norm to add)
+    bool down_in_x = false;
     for (uint32_t l = 0; l < c.n_layers; l++) {
         const LayerW &w = e->L[l];
         uint16_t *kc = (uint16_t *)kv_layer(e, l, 0), *vc = (uint16_t *)kv_layer(e, l, 1); // fp16 (checked by the caller)
@@ -470,7 +472,8 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
         na.x = e->pf_x; na.w = e->norm_attn + (size_t)l * c.dim; na.codes = e->pf_codes; na.scales = e->pf_scales;
         na.scales_t = e->pf_scales_t; na.rows = n; na.k = c.dim; na.eps = c.eps;
         // layer l > 0: the previous layer's down projection (pf_c) is added into the residual stream here
-        na.add = l > 0 ? e->pf_c : nullptr;
+        // (unless its GEMM added it into x)
+        na.add = l > 0 && !down_in_x ? e->pf_c : nullptr;
         na.x_out = e->pf_x;
         if ((rc = launch("rfp4_rmsnorm_quant_rows", dim3(n), dim3(256), s, &na))) return rc;
         e->pf_q_alt = false;
@@ -517,11 +520,14 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
         if ((rc = mx4_quantize_st(s, n, qd, e->pf_a, 0, e->pf_codes, e->pf_scales, e->pf_scales_t))) return rc;
         e->pf_q_alt = false;
         RFP4_PF_STAGE(4);
-        if ((rc = gemm_launch(s, n, c.dim, qd, e->pf_codes, e->pf_scales, e->pf_scales_t, w.o_c, w.o_s, w.o_st, e->pf_c,
-                              e->gemm_part))) return rc;
+        // o: x += O projection in the GEMM's epilogue (the residual add's
+        // arithmetic; not when the stage test hook wants the GEMM's output)
+        const bool o_in_x = stop != (int)(10u * l + 5u) && gemm_accumulate_ok(n, c.dim, qd);
+        if ((rc = gemm_launch(s, n, c.dim, qd, e->pf_codes, e->pf_scales, e->pf_scales_t, w.o_c, w.o_s, w.o_st,
+                              o_in_x ? e->pf_x : e->pf_c, e->gemm_part, o_in_x))) return rc;
         RFP4_PF_STAGE(5);
         na.w = e->norm_ffn + (size_t)l * c.dim;
-        na.add = e->pf_c; // x += O projection, then the FFN norm
+        na.add = o_in_x ? nullptr : e->pf_c; // x += O projection (unless added already), then the FFN norm
         if ((rc = launch("rfp4_rmsnorm_quant_rows", dim3(n), dim3(256), s, &na))) return rc;
         e->pf_q_alt = false;
         RFP4_PF_STAGE(6);
@@ -547,10 +553,12 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
         RFP4_PF_STAGE(8);
         uint8_t *dc = e->pf_q_alt ? e->pf_codes2 : e->pf_codes, *ds = e->pf_q_alt ? e->pf_scales2 : e->pf_scales;
         uint8_t *dst_ = e->pf_q_alt ? e->pf_scales_t2 : e->pf_scales_t;
-        if ((rc = gemm_launch(s, n, c.dim, c.ffn, dc, ds, dst_, w.d_c, w.d_s, w.d_st, e->pf_c, e->gemm_part))) return rc;
+        down_in_x = stop != (int)(10u * l + 9u) && gemm_accumulate_ok(n, c.dim, c.ffn);
+        if ((rc = gemm_launch(s, n, c.dim, c.ffn, dc, ds, dst_, w.d_c, w.d_s, w.d_st, down_in_x ? e->pf_x : e->pf_c,
+                              e->gemm_part, down_in_x))) return rc;
         RFP4_PF_STAGE(9);
-        // x += down projection: by the next layer's first norm, after the last layer here
-        if (l + 1 == c.n_layers && (rc = residual(s, n * c.dim, e->pf_c, e->pf_x))) return rc;
+        // x += down projection: in its GEMM, else by the next layer's first norm, after the last layer here
+        if (l + 1 == c.n_layers && !down_in_x && (rc = residual(s, n * c.dim, e->pf_c, e->pf_x))) return rc;
     }
 #undef RFP4_PF_STAGE
     // last row: the decode step's final norm + LM head, then argmax

@@ -1401,9 +1401,19 @@ int fp4_gemm_tiled(rfp4_stream_t stream, uint32_t m, uint32_t n, uint32_t k, con
 
 namespace rfp4 {
 
+// Where the plan's kernel has the accumulating epilogue: the tiled kernels
+// but the 4-wave 256x256 one (the ping-pong 256x256 kernel has it).
+bool gemm_accumulate_ok(uint32_t m, uint32_t n, uint32_t k)
+{
+    Runtime *rt = g_rt;
+    if (!rt || !m || !n || !k || k % 256u) return false;
+    const GemmPlan p = gemm_plan(m, n, k, (uint32_t)rt->num_cus);
+    return p.tile != kGemmSkinny && (p.tile != 0 || gemm_use_pp(p, m, n, k));
+}
+
 int gemm_launch(hipStream_t stream, uint32_t m, uint32_t n, uint32_t k, const uint8_t *a_codes, const uint8_t *a_scales,
                 const uint8_t *a_st, const uint8_t *w_codes, const uint8_t *w_scales, const uint8_t *w_st, float *c,
-                float *part)
+                float *part, bool accumulate)
 {
     if (!a_codes || !a_scales || !w_codes || !w_scales || !c) return set_error(RFP4_E_INVALID, "fp4_gemm: null pointer");
     if (m == 0 || n == 0 || k == 0) return set_error(RFP4_E_SHAPE, "fp4_gemm: empty shape m=%u n=%u k=%u", m, n, k);
@@ -1417,6 +1427,7 @@ int gemm_launch(hipStream_t stream, uint32_t m, uint32_t n, uint32_t k, const ui
     if (!rt) return set_error(RFP4_E_NOT_INIT, "rfp4_init has not been called");
     GemmPlan p = gemm_plan(m, n, k, (uint32_t)rt->num_cus);
     if (p.tile == kGemmSkinny) {
+        if (accumulate) return set_error(RFP4_E_INVALID, "fp4_gemm: no accumulating few-row kernel (m=%u)", m);
         if (!gemm_skinny_ok(m, k))
             return set_error(RFP4_E_SHAPE, "fp4_gemm: the few-row kernel needs k a multiple of 512, up to 16384 for "
                                            "m <= 32 and up to 8192 for m <= 64 (m=%u k=%u)", m, k);
@@ -1451,9 +1462,12 @@ int gemm_launch(hipStream_t stream, uint32_t m, uint32_t n, uint32_t k, const ui
     // whose kernels have no registers for the other plane, and the ping-pong
     // kernels)
     const bool pp = gemm_use_pp(p, m, n, k);
+    if (accumulate && p.tile == 0 && !pp)
+        return set_error(RFP4_E_INVALID, "fp4_gemm: no accumulating 4-wave 256x256 kernel (the ping-pong one has it)");
     uint32_t *counters = p.kz == 2u && t.bm * t.bn <= 256u * 128u && tiles <= kGemmCounters && !t_gemm_reduce_kernel && !pp
                              ? (uint32_t *)(part + kGemmPartFloats) : nullptr;
     GemmArgs a{a_codes, a_scales, w_codes, w_scales, c, part, m, n, k, p.kz, counters, a_st, w_st};
+    a.c_add = accumulate ? 1u : 0u;
     char pname[48];
     const char *kname = t.name;
     if (pp) { // 8 waves, two per SIMD (kernels.hip GEMM_KERNEL_PP)

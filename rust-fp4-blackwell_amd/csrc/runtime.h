@@ -93,10 +93,14 @@ int noalloc_setup(int device);
 // counters zeroed; the engine owns one, so engines on different streams do
 // not share partials).  a_st / w_st: the step-blocked copies of the scales
 // (device/gemm.h); where either is null and the plan is a tiled kernel, both
-// are made first in the runtime's workspace (one more launch).
+// are made first in the runtime's workspace (one more launch).  accumulate:
+// c += the product (each element one f32 addition of c and the sum, as a
+// residual add after the GEMM would make it); tiled plans only
+// (gemm_accumulate_ok).
 int gemm_launch(hipStream_t stream, uint32_t m, uint32_t n, uint32_t k, const uint8_t *a_codes, const uint8_t *a_scales,
                 const uint8_t *a_st, const uint8_t *w_codes, const uint8_t *w_scales, const uint8_t *w_st, float *c,
-                float *part);
+                float *part, bool accumulate = false);
+bool gemm_accumulate_ok(uint32_t m, uint32_t n, uint32_t k);
 // The gate|up projection of the prefill with SwiGLU and the MXFP4 rows of its
 // output in the GEMM's epilogue (rfp4_gemm_256x256_ppsw): m rows of K = k,
 // W = [gate; up] of 2 ffn rows; y = silu(gate) * up quantized per 32 into

@@ -255,7 +255,11 @@ typedef struct GemmArgs {
     // [m][pair_off/32] and, if not null, q_scales_t (step-blocked over K =
     // pair_off).  c is not written.
     uint8_t *q_codes, *q_scales, *q_scales_t;
-    uint32_t pair_off, pad;
+    uint32_t pair_off;
+    // nonzero: c += A . W^T (each element c + the sum, one rounding, as a
+    // residual add after the plain GEMM; the plain epilogues, the split-K sums
+    // and the reduce kernel), not with the SwiGLU or RoPE epilogues
+    uint32_t c_add;
     // RoPE + K/V cache epilogue (the _rope kernels only, kz = 1): the output
     // columns are rope_q / rope_hd q heads, then rope_kv / rope_hd k heads,
     // then as many v heads, rope_hd (64 or 128) wide; row r is position

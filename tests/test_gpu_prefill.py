@@ -296,3 +296,32 @@ def test_prefill_rope_hook_rejects_bad_values(rf):
     assert lib.rfp4_debug_prefill_rope(2) == -1
     assert lib.rfp4_debug_prefill_rope(-1) == -1
     rf.check(lib.rfp4_debug_prefill_rope(0))
+
+
+@pytest.mark.parametrize("tile,kz,reduce_kernel", [(2, 2, 0), (2, 2, 1), (1, 3, 0), (3, 1, 0), (0, 1, 0)])
+def test_prefill_residual_in_gemm_epilogue(rf, orc, tile, kz, reduce_kernel):
+    """x += o and x += down in the o and down GEMMs' epilogues (GemmArgs::
+    c_add) under forced plans: two K splits summed inside the launch, the
+    same summed by the reduce kernel, three splits, one split, the ping-pong
+    256x256 tile.  The staged check compares x after each residual add (stage
+    6, and stage 0 of the next layer) bit for bit with x + the plain GEMM's
+    output (the stop after stage 5 or 9 takes the plain GEMM), and the next
+    token with the oracle's prefill."""
+    cfg, n, seed = TINY128, 200, 0xADD0 + 10 * tile + kz
+    prompt = np.random.default_rng(seed).integers(0, cfg["vocab"], n, dtype=np.uint32)
+    print(f"prefill residual epilogue: tile {tile} kz {kz} reduce kernel {reduce_kernel}", flush=True)
+    lib = rf.load()
+    eng = _engine(rf, cfg, seed)
+    ref = orc.Model(cfg, seed)
+    try:
+        rf.debug_gemm_plan(tile, kz)
+        rf.check(lib.rfp4_debug_gemm_reduce_kernel(reduce_kernel))
+        tok = check_prefill_stages(rf, orc, eng, ref, cfg, prompt, 0)
+    finally:
+        rf.check(lib.rfp4_debug_gemm_reduce_kernel(0))
+        rf.debug_gemm_plan(-1, 0)
+    rtok, rlog = ref.prefill(prompt, 0, want_logits=True)
+    top2 = np.sort(rlog)[-2:]
+    assert tok == rtok, f"gpu {tok} cpu {rtok} margin {top2[1] - top2[0]:.4g}"
+    eng.close()
+    ref.close()
