@@ -303,6 +303,11 @@ int rfp4_debug_prefill_swiglu(int mode);
  * 64 or 128; bit-identical to mode 1), 1 = the GEMM, then the RoPE + K/V row
  * kernel.  No reference counterpart (the reference has no batched prefill). */
 int rfp4_debug_prefill_rope(int mode);
+/* Test hook (this thread): the batched prefill's attention rows: 0 =
+ * quantized to MXFP4 in the attention kernel's epilogue (the row quantizer's
+ * bytes; no f32 rows written), 1 = f32 rows, then the row quantizer.  No
+ * reference counterpart. */
+int rfp4_debug_prefill_attn_quant(int mode);
 /* Test hook: the batched prefill's attention on this thread: 0 = the
  * matrix-core prefill kernel, 1 = the decode kernel, one grid row per prompt
  * row.  No reference counterpart. */

@@ -33,12 +33,16 @@
 // The next two blocks' K/V loads are in flight while the current block computes.
 #pragma once
 #include "common.h"
+#include "misc.h"
 
 #define PF_KPAD 8  // fp16 padding of a staged K row (16 consecutive rows -> 16 distinct bank groups)
 #define PF_TPAD 8  // fp16 padding of a transposed V row
 
-// One query tile: prompt rows r0 .. r0 + BQ of KV head blockIdx.y.
-template <int HD, int GT, int NW>
+// One query tile: prompt rows r0 .. r0 + BQ of KV head blockIdx.y.  QO: the
+// kernel variant that can quantize its output rows (AttnPrefillArgs::q_codes;
+// a separate instantiation: the epilogue's code changes how the compiler
+// schedules the main loop's LDS reads in the same function).
+template <int HD, int GT, int NW, bool QO>
 RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
 {
     const uint32_t pos0 = a.pos0, nrows = a.rows;
@@ -239,20 +243,66 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
 #pragma unroll
     for (int mt = 0; mt < MT; mt++) {
         const uint32_t t = (uint32_t)(wave * MT + mt), g = t % GT;
-        const uint32_t row = r0 + 16u * (t / GT) + l16;
-        if (g >= G || row >= nrows) continue;
-        float *op = a.out + (size_t)row * a.out_rs + (size_t)(kvh * G + g) * HD + 4u * q4;
+        if (g >= G) continue; // the same for the whole wave
+        const uint32_t row = r0 + 16u * (t / GT) + l16, head = kvh * G + g;
+        if (a.out && row < nrows) {
+            float *op = a.out + (size_t)row * a.out_rs + (size_t)head * HD + 4u * q4;
 #pragma unroll
-        for (int n = 0; n < NN; n++)
-            *(float4 *)(op + 16 * n) = make_float4(__fdiv_rn(o[mt][n][0], lrun[mt]), __fdiv_rn(o[mt][n][1], lrun[mt]),
-                                                   __fdiv_rn(o[mt][n][2], lrun[mt]), __fdiv_rn(o[mt][n][3], lrun[mt]));
+            for (int n = 0; n < NN; n++)
+                *(float4 *)(op + 16 * n) = make_float4(__fdiv_rn(o[mt][n][0], lrun[mt]), __fdiv_rn(o[mt][n][1], lrun[mt]),
+                                                       __fdiv_rn(o[mt][n][2], lrun[mt]), __fdiv_rn(o[mt][n][3], lrun[mt]));
+        }
+        if (QO && a.q_codes) {
+            // MXFP4 per 32 dimensions (quant_block32's arithmetic): block b of
+            // the head is tiles 2b, 2b + 1, i.e. this lane's 8 values and those
+            // of lanes ^16, ^32, ^48 (the same row); the maximum first over all
+            // four, then each lane codes its two runs of 4 dimensions.  One
+            // block at a time, each value formed as the f32 rows would hold it.
+            const uint32_t qd = a.n_heads * HD, qd32 = qd / 32u;
+#pragma unroll
+            for (int b = 0; b < HD / 32; b++) {
+                float y[8];
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    y[r] = __fdiv_rn(o[mt][2 * b][r], lrun[mt]);
+                    y[4 + r] = __fdiv_rn(o[mt][2 * b + 1][r], lrun[mt]);
+                }
+                float amax = 0.0f;
+#pragma unroll
+                for (int i = 0; i < 8; i++) amax = fmaxf(amax, fabsf(y[i]));
+                amax = xor32_max(xor16_max(amax));
+                int se = 0;
+                uint32_t sbyte = 0;
+                if (amax != 0.0f) {
+                    se = floor_log2_pos(amax) - 2;
+                    se = se < -127 ? -127 : (se > 127 ? 127 : se);
+                    sbyte = (uint32_t)(se + 127);
+                }
+                uint32_t lo = 0, hi = 0;
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    lo |= e2m1_rne_code(amax != 0.0f ? ldexpf(y[r], -se) : y[r]) << (4 * r);
+                    hi |= e2m1_rne_code(amax != 0.0f ? ldexpf(y[4 + r], -se) : y[4 + r]) << (4 * r);
+                }
+                if (row < nrows) {
+                    uint8_t *cp = a.q_codes + (size_t)row * (qd / 2u) + (size_t)head * (HD / 2) + 16u * b + 2u * q4;
+                    *(uint16_t *)cp = (uint16_t)lo;
+                    *(uint16_t *)(cp + 8) = (uint16_t)hi;
+                    if (q4 == 0u) {
+                        const uint32_t blk = head * (HD / 32) + (uint32_t)b;
+                        a.q_scales[(size_t)row * qd32 + blk] = (uint8_t)sbyte;
+                        if (a.q_scales_t) a.q_scales_t[mx_st_offset(row, blk, qd / 256u)] = (uint8_t)sbyte;
+                    }
+                }
+            }
+        }
     }
 }
 
 // Workgroup x of KV head blockIdx.y: query tile x, or, paired, tiles
 // ntiles - 1 - x (the longer causal range, first) and x, so that every
 // workgroup walks ntiles + 1 key ranges' worth of blocks.
-template <int HD, int GT, int NW = 4>
+template <int HD, int GT, int NW = 4, bool QO = false>
 RFP4_DEV void attn_prefill_body(const AttnPrefillArgs &a)
 {
     constexpr uint32_t BQ = (uint32_t)attn_prefill_rows(GT, NW);
@@ -260,5 +310,5 @@ RFP4_DEV void attn_prefill_body(const AttnPrefillArgs &a)
     const uint32_t t0 = a.paired ? ntiles - 1u - x : x;
     const uint32_t npass = a.paired && x < t0 ? 2u : 1u;
 #pragma nounroll
-    for (uint32_t pass = 0; pass < npass; pass++) attn_prefill_tile<HD, GT, NW>(a, (pass == 0 ? t0 : x) * BQ);
+    for (uint32_t pass = 0; pass < npass; pass++) attn_prefill_tile<HD, GT, NW, QO>(a, (pass == 0 ? t0 : x) * BQ);
 }

@@ -499,6 +499,7 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
         }
         RFP4_PF_STAGE(2);
         // causal attention of the prompt rows (row r sees positions 0 .. pos0 + r)
+        bool attn_q = false; // quantized by the attention kernel itself
         if (prefill_attn_mode() == 1) {
             // test path: the decode kernel, one query row per grid z (split states per row)
             if (!e->pf_part &&
@@ -512,12 +513,21 @@ static int enqueue_prefill(llama_engine *e, uint32_t n, uint32_t pos0)
             aa.chunk = e->attn_chunk; aa.max_splits = e->attn_max_splits;
             if ((rc = attn_launch(aa, 1, s, pos0 + n, n))) return rc;
         } else {
-            AttnPrefillArgs pa{e->pf_c, kc, vc, e->pf_a, hd, (uint64_t)e->max_seq_alloc * hd, nqkv, qd,
+            // the attention rows quantized to MXFP4 in the kernel's epilogue
+            // (the row quantizer's bytes; no f32 rows), unless the stage test
+            // hook wants the f32 rows
+            attn_q = stop != (int)(10u * l + 3u) && prefill_attn_quant_mode() == 0;
+            AttnPrefillArgs pa{e->pf_c, kc, vc, attn_q ? nullptr : e->pf_a, hd, (uint64_t)e->max_seq_alloc * hd, nqkv, qd,
                                c.n_heads, c.n_kv_heads, pos0, n, 0u}; // pairing: chosen by the launcher
+            if (attn_q) {
+                pa.q_codes = e->pf_codes;
+                pa.q_scales = e->pf_scales;
+                pa.q_scales_t = e->pf_scales_t;
+            }
             if ((rc = attn_prefill_launch(pa, hd, s))) return rc;
         }
         RFP4_PF_STAGE(3);
-        if ((rc = mx4_quantize_st(s, n, qd, e->pf_a, 0, e->pf_codes, e->pf_scales, e->pf_scales_t))) return rc;
+        if (!attn_q && (rc = mx4_quantize_st(s, n, qd, e->pf_a, 0, e->pf_codes, e->pf_scales, e->pf_scales_t))) return rc;
         e->pf_q_alt = false;
         RFP4_PF_STAGE(4);
         // o: x += O projection in the GEMM's epilogue (the residual add's

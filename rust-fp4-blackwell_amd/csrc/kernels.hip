@@ -104,7 +104,9 @@ ATTN_KERNELS(64, f32, float)
 ATTN_KERNELS(64, f16, uint16_t)
 ATTN_KERNELS(128, f32, float)
 ATTN_KERNELS(128, f16, uint16_t)
-// rfp4_attn_prefill_hd<HD>_g<group>_w<waves per workgroup>
+// rfp4_attn_prefill_hd<HD>_g<group>_w<waves per workgroup>[_q: the output
+// rows quantized to MXFP4 as well, AttnPrefillArgs::q_codes]
+#define K512Q extern "C" __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 #define ATTN_PREFILL_KERNELS(HD) \
     K256 void rfp4_attn_prefill_hd##HD##_g1_w4(AttnPrefillArgs a) { attn_prefill_body<HD, 1, 4>(a); } \
     K256 void rfp4_attn_prefill_hd##HD##_g2_w4(AttnPrefillArgs a) { attn_prefill_body<HD, 2, 4>(a); } \
@@ -113,7 +115,15 @@ ATTN_KERNELS(128, f16, uint16_t)
     K512 void rfp4_attn_prefill_hd##HD##_g1_w8(AttnPrefillArgs a) { attn_prefill_body<HD, 1, 8>(a); } \
     K512 void rfp4_attn_prefill_hd##HD##_g2_w8(AttnPrefillArgs a) { attn_prefill_body<HD, 2, 8>(a); } \
     K512 void rfp4_attn_prefill_hd##HD##_g4_w8(AttnPrefillArgs a) { attn_prefill_body<HD, 4, 8>(a); } \
-    K512 void rfp4_attn_prefill_hd##HD##_g8_w8(AttnPrefillArgs a) { attn_prefill_body<HD, 8, 8>(a); }
+    K512 void rfp4_attn_prefill_hd##HD##_g8_w8(AttnPrefillArgs a) { attn_prefill_body<HD, 8, 8>(a); } \
+    K256 void rfp4_attn_prefill_hd##HD##_g1_w4_q(AttnPrefillArgs a) { attn_prefill_body<HD, 1, 4, true>(a); } \
+    K256 void rfp4_attn_prefill_hd##HD##_g2_w4_q(AttnPrefillArgs a) { attn_prefill_body<HD, 2, 4, true>(a); } \
+    K256 void rfp4_attn_prefill_hd##HD##_g4_w4_q(AttnPrefillArgs a) { attn_prefill_body<HD, 4, 4, true>(a); } \
+    K256 void rfp4_attn_prefill_hd##HD##_g8_w4_q(AttnPrefillArgs a) { attn_prefill_body<HD, 8, 4, true>(a); } \
+    K512Q void rfp4_attn_prefill_hd##HD##_g1_w8_q(AttnPrefillArgs a) { attn_prefill_body<HD, 1, 8, true>(a); } \
+    K512Q void rfp4_attn_prefill_hd##HD##_g2_w8_q(AttnPrefillArgs a) { attn_prefill_body<HD, 2, 8, true>(a); } \
+    K512Q void rfp4_attn_prefill_hd##HD##_g4_w8_q(AttnPrefillArgs a) { attn_prefill_body<HD, 4, 8, true>(a); } \
+    K512Q void rfp4_attn_prefill_hd##HD##_g8_w8_q(AttnPrefillArgs a) { attn_prefill_body<HD, 8, 8, true>(a); }
 ATTN_PREFILL_KERNELS(64)
 ATTN_PREFILL_KERNELS(128)
 // ---- fused q|k|v GEMV + attention: rfp4_qkva_hd<HD>_g<group>[_t: tagged merge]

@@ -523,6 +523,8 @@ static thread_local int t_prefill_swiglu = 0; // 0: SwiGLU + MXFP4 in the gate|u
 int prefill_swiglu_mode() { return t_prefill_swiglu; }
 static thread_local int t_prefill_rope = 0; // 0: RoPE + K/V cache rows in the q|k|v GEMM's epilogue where it applies, 1: the row kernel
 int prefill_rope_mode() { return t_prefill_rope; }
+static thread_local int t_prefill_attn_quant = 0; // 0: the attention rows quantized by the attention kernel, 1: by the row quantizer
+int prefill_attn_quant_mode() { return t_prefill_attn_quant; }
 
 bool attn_inmerge_mode(int mode, uint32_t splits)
 {
@@ -652,6 +654,15 @@ extern "C" int rfp4_debug_prefill_rope(int mode)
     return RFP4_OK;
 }
 
+extern "C" int rfp4_debug_prefill_attn_quant(int mode)
+{
+    using namespace rfp4;
+    if (mode != 0 && mode != 1)
+        return set_error(RFP4_E_INVALID, "prefill attention quantization mode must be 0 (in the attention kernel) or 1 (row quantizer)");
+    t_prefill_attn_quant = mode;
+    return RFP4_OK;
+}
+
 extern "C" int rfp4_debug_prefill_attn(int mode)
 {
     using namespace rfp4;
@@ -725,7 +736,10 @@ int attn_launch(const AttnArgs &args, int kv_f16, hipStream_t s, uint32_t max_se
 
 int attn_prefill_launch(const AttnPrefillArgs &a, uint32_t head_dim, hipStream_t s)
 {
-    if (!a.q || !a.kc || !a.vc || !a.out) return set_error(RFP4_E_INVALID, "attn prefill: null pointer");
+    if (!a.q || !a.kc || !a.vc || (!a.out && !a.q_codes)) return set_error(RFP4_E_INVALID, "attn prefill: null pointer");
+    if (a.q_codes && (!a.q_scales || (a.q_scales_t && (a.n_heads * head_dim) % 256u)))
+        return set_error(RFP4_E_INVALID, "attn prefill: quantized output needs scales (and n_heads * head_dim %% 256 == 0 "
+                                         "for the step-blocked copy)");
     if (head_dim != 64 && head_dim != 128) return set_error(RFP4_E_SHAPE, "attn prefill: head_dim %u (64 or 128)", head_dim);
     if (a.n_kv_heads == 0 || a.n_heads % a.n_kv_heads || a.n_heads / a.n_kv_heads > 8)
         return set_error(RFP4_E_SHAPE, "attn prefill: %u query heads over %u KV heads (group of at most 8)", a.n_heads,
@@ -753,7 +767,7 @@ int attn_prefill_launch(const AttnPrefillArgs &a, uint32_t head_dim, hipStream_t
     bool paired = ntiles >= 2 && g_rt && (uint64_t)((ntiles + 1) / 2) * a.n_kv_heads >= (uint64_t)g_rt->num_cus;
     if (t_prefill_pairing) paired = t_prefill_pairing == 2;
     char name[48];
-    snprintf(name, sizeof name, "rfp4_attn_prefill_hd%u_g%u_w%u", head_dim, g, waves);
+    snprintf(name, sizeof name, "rfp4_attn_prefill_hd%u_g%u_w%u%s", head_dim, g, waves, a.q_codes ? "_q" : "");
     AttnPrefillArgs args = a;
     args.paired = paired ? 1u : 0u;
     const uint32_t gx = paired ? (ntiles + 1) / 2 : ntiles;

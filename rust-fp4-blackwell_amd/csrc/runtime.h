@@ -153,6 +153,7 @@ int qkva_mode();                                 // this thread's rfp4_debug_qkv
 int prefill_stop();                              // this thread's rfp4_debug_prefill_stop setting
 int prefill_swiglu_mode();                       // this thread's rfp4_debug_prefill_swiglu setting
 int prefill_rope_mode();                         // this thread's rfp4_debug_prefill_rope setting
+int prefill_attn_quant_mode();                   // this thread's rfp4_debug_prefill_attn_quant setting
 bool attn_inmerge_mode(int mode, uint32_t splits); // attn_inmerge under an explicit setting
 constexpr uint32_t kAttnInmergeMaxSplits = 8;
 // Whether an engine's one-row attention with `splits` splits uses the tagged

@@ -129,6 +129,12 @@ typedef struct AttnPrefillArgs {
     uint64_t ts, hs;
     uint32_t q_rs, out_rs, n_heads, n_kv_heads, pos0, rows;
     uint32_t paired;         // nonzero: workgroup x takes query tiles ntiles-1-x and x (grid ceil(ntiles/2))
+    // Optional (null = off): the output rows quantized to MXFP4 per 32 as the
+    // row quantizer does it, codes [rows][n_heads*head_dim/2], scales
+    // [rows][n_heads*head_dim/32] and, if not null, their step-blocked copy
+    // (GemmArgs::a_st; n_heads*head_dim a multiple of 256).  out may then be
+    // null (no f32 rows).
+    uint8_t *q_codes, *q_scales, *q_scales_t;
 } AttnPrefillArgs;
 
 // Batched prefill row kernels (device/prefill.h).

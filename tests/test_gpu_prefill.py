@@ -325,3 +325,10 @@ def test_prefill_residual_in_gemm_epilogue(rf, orc, tile, kz, reduce_kernel):
     assert tok == rtok, f"gpu {tok} cpu {rtok} margin {top2[1] - top2[0]:.4g}"
     eng.close()
     ref.close()
+
+
+def test_prefill_attn_quant_hook_rejects_bad_values(rf):
+    lib = rf.load()
+    assert lib.rfp4_debug_prefill_attn_quant(2) == -1
+    assert lib.rfp4_debug_prefill_attn_quant(-1) == -1
+    rf.check(lib.rfp4_debug_prefill_attn_quant(0))
