@@ -323,6 +323,12 @@ int rfp4_debug_prefill_stop(int after);
 /* Test hook: waves per workgroup of the matrix-core prefill attention on
  * this thread (0 = automatic, 4 or 8).  No reference counterpart. */
 int rfp4_debug_prefill_waves(int waves);
+/* Test hook (this thread): key groups per workgroup of the batched
+ * prefill's attention: 0 = automatic (two where the plan is 4 waves and
+ * groups of up to 4 query heads), 1 = one, 2 = two where compiled (two
+ * groups of waves take alternate key blocks of the same query tiles and
+ * merge their softmax states).  No reference counterpart. */
+int rfp4_debug_prefill_ksplit(int groups);
 /* Test hook: query-tile pairing of the matrix-core prefill attention on this
  * thread (0 = automatic, 1 = one tile per workgroup, 2 = tiles t and
  * ntiles-1-t per workgroup).  No reference counterpart. */

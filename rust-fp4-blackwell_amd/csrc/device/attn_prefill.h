@@ -42,7 +42,12 @@
 // kernel variant that can quantize its output rows (AttnPrefillArgs::q_codes;
 // a separate instantiation: the epilogue's code changes how the compiler
 // schedules the main loop's LDS reads in the same function).
-template <int HD, int GT, int NW, bool QO>
+// KSP: key groups.  KSP groups of NW waves take the same query tiles and
+// alternate key blocks (group g blocks g, g + KSP, ...; each staging step
+// brings KSP blocks into LDS), then merge their softmax states through LDS
+// (m the maximum, l and O rescaled by 2^(m_g - m) and summed): the serial
+// chain of blocks of a tile is KSP times shorter.
+template <int HD, int GT, int NW, bool QO, int KSP = 1>
 RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
 {
     const uint32_t pos0 = a.pos0, nrows = a.rows;
@@ -56,16 +61,19 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
     constexpr int PF_BK = HD == 64 ? 64 : 32;
     constexpr int KROW = HD + PF_KPAD, TROW = PF_BK + PF_TPAD;
     constexpr int LPK = HD / 8;                      // 16-byte pieces per K/V row
-    constexpr int T = 64 * NW;                       // threads
-    constexpr int LD = (PF_BK * LPK + T - 1) / T;    // K (and V) pieces per thread per block
-    constexpr bool LFULL = PF_BK * LPK % T == 0;     // every thread loads LD pieces
+    constexpr int T = 64 * NW * KSP;                 // threads
+    constexpr int NP = KSP * PF_BK * LPK;            // 16-byte K (and V) pieces per staging step
+    constexpr int LD = (NP + T - 1) / T;             // K (and V) pieces per thread per step
+    constexpr bool LFULL = NP % T == 0;              // every thread loads LD pieces
     static_assert(NT % NW == 0 && MT >= 1, "tiles per wave");
     static_assert(LFULL || LD == 1, "block load split");
-    __shared__ __align__(16) _Float16 ks[PF_BK][KROW];
-    __shared__ __align__(16) _Float16 vt[HD][TROW];
+    __shared__ __align__(16) _Float16 ks[KSP][PF_BK][KROW];
+    __shared__ __align__(16) _Float16 vt[KSP][HD][TROW];
 
     const uint32_t kvh = blockIdx.y;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    // key group; wave within it (KSP = 1: the plain kernel's code, group 0)
+    const int kgrp = KSP > 1 ? (tid >> 6) / NW : 0, wave = KSP > 1 ? (tid >> 6) % NW : tid >> 6;
     const uint32_t l16 = (uint32_t)lane & 15u, q4 = (uint32_t)lane >> 4;
     const uint32_t G = a.n_heads / a.n_kv_heads;
     const uint16_t *kc = a.kc + (size_t)kvh * a.hs;
@@ -74,6 +82,7 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
     const uint32_t last_row = min(r0 + (uint32_t)BQ, nrows) - 1u;
     const uint32_t nk = pos0 + last_row + 1u;
     const uint32_t nblk = (nk + PF_BK - 1) / PF_BK;
+    const uint32_t niter = KSP > 1 ? (nblk + KSP - 1) / KSP : nblk; // staging steps
     const float scale = __fmul_rn(1.4426950408889634f, __fdiv_rn(1.0f, __fsqrt_rn((float)HD))); // log2(e) / sqrt(HD)
 
     // ---- Q tiles of this wave as fp16 A operands (rows past the prompt or heads past G: zero)
@@ -118,13 +127,16 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
     static_assert(LD == 1 || LD == 2 || LD == 4, "16-byte pieces per thread and block");
     typedef uint32_t pf_vec __attribute__((ext_vector_type(4 * LD)));
     pf_vec kr0, vr0, kr1, vr1;
-#define RFP4_PF_LOAD(B, KR, VR)                                                                           \
+    // staging step I holds blocks I KSP .. I KSP + KSP - 1: piece p is piece
+    // p % (PF_BK LPK) of block slot p / (PF_BK LPK)
+#define RFP4_PF_LOAD(I, KR, VR)                                                                           \
     do {                                                                                                  \
         _Pragma("unroll") for (int j = 0; j < LD; j++) {                                                  \
-            /* threads past the block's pieces load the last one again (unused) */                        \
-            const uint32_t p = min((uint32_t)tid + (uint32_t)T * (uint32_t)j, (uint32_t)(PF_BK * LPK) - 1u); \
-            const uint32_t kk = min((B) * PF_BK + p / LPK, nk - 1u), kd = 8u * (p % LPK);                 \
-            const uint32_t vk = min((B) * PF_BK + p % PF_BK, nk - 1u), vd = 8u * (p / PF_BK);              \
+            /* threads past the step's pieces load the last one again (unused) */                         \
+            const uint32_t pa = min((uint32_t)tid + (uint32_t)T * (uint32_t)j, (uint32_t)NP - 1u);        \
+            const uint32_t kb0 = ((I) * KSP + pa / (PF_BK * LPK)) * PF_BK, p = pa % (PF_BK * LPK);       \
+            const uint32_t kk = min(kb0 + p / LPK, nk - 1u), kd = 8u * (p % LPK);                         \
+            const uint32_t vk = min(kb0 + p % PF_BK, nk - 1u), vd = 8u * (p / PF_BK);                      \
             const u32x4 kx = *(const u32x4 *)(kc + (size_t)kk * a.ts + kd);                               \
             const u32x4 vx = *(const u32x4 *)(vc + (size_t)vk * a.ts + vd);                               \
             _Pragma("unroll") for (int i = 0; i < 4; i++) {                                               \
@@ -134,23 +146,24 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
         }                                                                                                 \
     } while (0)
     // block b's K rows and transposed V rows into LDS, then block b + 2's loads into the same registers
-#define RFP4_PF_STAGE(b, KR, VR)                                                                          \
+#define RFP4_PF_STAGE(I, KR, VR)                                                                          \
     do {                                                                                                  \
-        __syncthreads(); /* the previous block's LDS reads are done */                                    \
+        __syncthreads(); /* the previous step's LDS reads are done */                                     \
         _Pragma("unroll") for (int j = 0; j < LD; j++) {                                                  \
-            const uint32_t p = (uint32_t)tid + (uint32_t)T * (uint32_t)j;                                 \
-            if (!LFULL && p >= (uint32_t)(PF_BK * LPK)) break;                                            \
+            const uint32_t pa = (uint32_t)tid + (uint32_t)T * (uint32_t)j;                                \
+            if (!LFULL && pa >= (uint32_t)NP) break;                                                      \
+            const uint32_t sl = pa / (PF_BK * LPK), p = pa % (PF_BK * LPK);                              \
             const u32x4 kx = {KR[4 * j], KR[4 * j + 1], KR[4 * j + 2], KR[4 * j + 3]};                    \
             const u32x4 vx = {VR[4 * j], VR[4 * j + 1], VR[4 * j + 2], VR[4 * j + 3]};                    \
-            *(u32x4 *)&ks[p / LPK][8u * (p % LPK)] = kx;                                                  \
+            *(u32x4 *)&ks[sl][p / LPK][8u * (p % LPK)] = kx;                                              \
             const uint32_t vk = p % PF_BK, vd = 8u * (p / PF_BK);                                          \
             _Pragma("unroll") for (int i = 0; i < 4; i++) {                                               \
-                vt[vd + 2u * i][vk] = __builtin_bit_cast(_Float16, (uint16_t)(vx[i] & 0xFFFFu));          \
-                vt[vd + 2u * i + 1u][vk] = __builtin_bit_cast(_Float16, (uint16_t)(vx[i] >> 16));         \
+                vt[sl][vd + 2u * i][vk] = __builtin_bit_cast(_Float16, (uint16_t)(vx[i] & 0xFFFFu));      \
+                vt[sl][vd + 2u * i + 1u][vk] = __builtin_bit_cast(_Float16, (uint16_t)(vx[i] >> 16));     \
             }                                                                                             \
         }                                                                                                 \
         __syncthreads();                                                                                  \
-        RFP4_PF_LOAD((b) + 2u, KR, VR);                                                                   \
+        RFP4_PF_LOAD((I) + 2u, KR, VR);                                                                   \
     } while (0)
     // Every load is issued on every path (keys clamped to the last one, so a
     // block past the end re-reads it): the compiler's wait for a set then
@@ -159,8 +172,10 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
     RFP4_PF_LOAD(0u, kr0, vr0);
     RFP4_PF_LOAD(1u, kr1, vr1);
 
-    // the block's scores, softmax and P V from the staged K / V
+    // the block's scores, softmax and P V from the staged K / V (this key
+    // group's block b of the step in slot kgrp; none past the last block)
     auto block = [&](uint32_t b) {
+        if (KSP > 1 && b >= nblk) return; // the same for the whole key group
 #pragma unroll
         for (int mt = 0; mt < MT; mt++) {
             const uint32_t t = (uint32_t)(wave * MT + mt);
@@ -173,7 +188,7 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
                 s[h] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
                 for (int k = 0; k < KS; k++) {
-                    const f16x8 ka = *(const f16x8 *)&ks[16u * h + l16][32 * k + 8u * q4];
+                    const f16x8 ka = *(const f16x8 *)&ks[kgrp][16u * h + l16][32 * k + 8u * q4];
                     s[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, qa[mt][k], s[h], 0, 0, 0);
                     s[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[mt][k], s[h], 0, 0, 0);
                 }
@@ -214,7 +229,7 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
                 split_hi_lo8(p + 8 * c, pb, pl);
 #pragma unroll
                 for (int n = 0; n < NN; n++) {
-                    const _Float16 *vrow = &vt[16u * n + l16][32u * c + 4u * q4];
+                    const _Float16 *vrow = &vt[kgrp][16u * n + l16][32u * c + 4u * q4];
                     typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
                     const f16x4 v0 = *(const f16x4 *)vrow, v1 = *(const f16x4 *)(vrow + 16);
                     const f16x8 va = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
@@ -224,19 +239,54 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
             }
         }
     };
-    uint32_t b = 0;
-    for (; b + 1u < nblk; b += 2u) {
-        RFP4_PF_STAGE(b, kr0, vr0);
-        block(b);
-        RFP4_PF_STAGE(b + 1u, kr1, vr1);
-        block(b + 1u);
+    uint32_t it = 0;
+    for (; it + 1u < niter; it += 2u) {
+        RFP4_PF_STAGE(it, kr0, vr0);
+        block(it * KSP + (uint32_t)kgrp);
+        RFP4_PF_STAGE(it + 1u, kr1, vr1);
+        block((it + 1u) * KSP + (uint32_t)kgrp);
     }
-    if (b < nblk) {
-        RFP4_PF_STAGE(b, kr0, vr0);
-        block(b);
+    if (it < niter) {
+        RFP4_PF_STAGE(it, kr0, vr0);
+        block(it * KSP + (uint32_t)kgrp);
     }
 #undef RFP4_PF_STAGE
 #undef RFP4_PF_LOAD
+
+    if constexpr (KSP > 1) {
+        // ---- the key groups' states merged into group 0's: groups 1.. put
+        // (O, m, l) in LDS (lane-contiguous words), group 0 combines
+        __shared__ float mg[KSP - 1][NW][MT][NN * 4 + 2][64];
+        if (kgrp > 0) {
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                float(*w)[64] = mg[kgrp - 1][wave][mt];
+#pragma unroll
+                for (int n = 0; n < NN; n++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) w[4 * n + r][lane] = o[mt][n][r];
+                w[NN * 4][lane] = mrun[mt];
+                w[NN * 4 + 1][lane] = lrun[mt];
+            }
+        }
+        __syncthreads();
+        if (kgrp > 0) return; // group 0 writes the output
+#pragma unroll
+        for (int g2 = 0; g2 < KSP - 1; g2++)
+#pragma unroll
+            for (int mt = 0; mt < MT; mt++) {
+                const float(*w)[64] = mg[g2][wave][mt];
+                const float m2 = w[NN * 4][lane], l2 = w[NN * 4 + 1][lane];
+                const float m = fmaxf(mrun[mt], m2);
+                const float a0 = __builtin_amdgcn_exp2f(mrun[mt] - m), a1 = __builtin_amdgcn_exp2f(m2 - m);
+                mrun[mt] = m;
+                lrun[mt] = fmaf(lrun[mt], a0, l2 * a1);
+#pragma unroll
+                for (int n = 0; n < NN; n++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) o[mt][n][r] = fmaf(o[mt][n][r], a0, w[4 * n + r][lane] * a1);
+            }
+    }
 
     // ---- out[row][head][dim] = O / l for rows in the prompt and heads < G
     // (lane: row l16, dimensions 16 n + 4 q4 .. +3 of each tile n)
@@ -302,7 +352,7 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
 // Workgroup x of KV head blockIdx.y: query tile x, or, paired, tiles
 // ntiles - 1 - x (the longer causal range, first) and x, so that every
 // workgroup walks ntiles + 1 key ranges' worth of blocks.
-template <int HD, int GT, int NW = 4, bool QO = false>
+template <int HD, int GT, int NW = 4, bool QO = false, int KSP = 1>
 RFP4_DEV void attn_prefill_body(const AttnPrefillArgs &a)
 {
     constexpr uint32_t BQ = (uint32_t)attn_prefill_rows(GT, NW);
@@ -310,5 +360,5 @@ RFP4_DEV void attn_prefill_body(const AttnPrefillArgs &a)
     const uint32_t t0 = a.paired ? ntiles - 1u - x : x;
     const uint32_t npass = a.paired && x < t0 ? 2u : 1u;
 #pragma nounroll
-    for (uint32_t pass = 0; pass < npass; pass++) attn_prefill_tile<HD, GT, NW, QO>(a, (pass == 0 ? t0 : x) * BQ);
+    for (uint32_t pass = 0; pass < npass; pass++) attn_prefill_tile<HD, GT, NW, QO, KSP>(a, (pass == 0 ? t0 : x) * BQ);
 }

@@ -126,6 +126,18 @@ ATTN_KERNELS(128, f16, uint16_t)
     K512Q void rfp4_attn_prefill_hd##HD##_g8_w8_q(AttnPrefillArgs a) { attn_prefill_body<HD, 8, 8, true>(a); }
 ATTN_PREFILL_KERNELS(64)
 ATTN_PREFILL_KERNELS(128)
+// key-split variants (two key groups of 4 waves each, _s2; groups of up to 4
+// query heads: runtime.cpp attn_prefill_launch)
+#define ATTN_PREFILL_SPLIT_KERNELS(HD) \
+    K512 void rfp4_attn_prefill_hd##HD##_g1_w4_s2(AttnPrefillArgs a) { attn_prefill_body<HD, 1, 4, false, 2>(a); } \
+    K512 void rfp4_attn_prefill_hd##HD##_g2_w4_s2(AttnPrefillArgs a) { attn_prefill_body<HD, 2, 4, false, 2>(a); } \
+    K512 void rfp4_attn_prefill_hd##HD##_g4_w4_s2(AttnPrefillArgs a) { attn_prefill_body<HD, 4, 4, false, 2>(a); } \
+    K512Q void rfp4_attn_prefill_hd##HD##_g1_w4_q_s2(AttnPrefillArgs a) { attn_prefill_body<HD, 1, 4, true, 2>(a); } \
+    K512Q void rfp4_attn_prefill_hd##HD##_g2_w4_q_s2(AttnPrefillArgs a) { attn_prefill_body<HD, 2, 4, true, 2>(a); } \
+    K512Q void rfp4_attn_prefill_hd##HD##_g4_w4_q_s2(AttnPrefillArgs a) { attn_prefill_body<HD, 4, 4, true, 2>(a); }
+ATTN_PREFILL_SPLIT_KERNELS(64)
+ATTN_PREFILL_SPLIT_KERNELS(128)
+#undef ATTN_PREFILL_SPLIT_KERNELS
 // ---- fused q|k|v GEMV + attention: rfp4_qkva_hd<HD>_g<group>[_t: tagged merge]
 // (device/qkva.h).  HD 64 with K = 2048 (one slice, R = 2 or 1 (_r1), the
 // 8-wave GEMV's RMS order); HD 128 with K = 4096 (two slices, R = 4, the

@@ -516,6 +516,7 @@ int qkva_mode() { return t_qkva; }
 static thread_local int t_prefill_attn = 0; // 0 matrix-core prefill kernel, 1 one decode-kernel row per prompt row
 static thread_local int t_prefill_waves = 0; // prefill attention waves per workgroup (0 = automatic)
 static thread_local int t_prefill_pairing = 0; // 0 automatic, 1 one query tile per workgroup, 2 paired tiles
+static thread_local int t_prefill_ksplit = 0; // prefill attention key groups per workgroup (0 automatic, 1, 2)
 int prefill_attn_mode() { return t_prefill_attn; }
 static thread_local int t_prefill_stop = -2; // stage after which the batched prefill stops (-2: none)
 int prefill_stop() { return t_prefill_stop; }
@@ -617,6 +618,15 @@ extern "C" int rfp4_debug_prefill_waves(int waves)
     using namespace rfp4;
     if (waves != 0 && waves != 4 && waves != 8) return set_error(RFP4_E_INVALID, "prefill attention waves must be 0 (auto), 4 or 8");
     t_prefill_waves = waves;
+    return RFP4_OK;
+}
+
+extern "C" int rfp4_debug_prefill_ksplit(int groups)
+{
+    using namespace rfp4;
+    if (groups < 0 || groups > 2)
+        return set_error(RFP4_E_INVALID, "prefill attention key groups must be 0 (auto), 1 (one) or 2 (two where compiled)");
+    t_prefill_ksplit = groups;
     return RFP4_OK;
 }
 
@@ -767,11 +777,18 @@ int attn_prefill_launch(const AttnPrefillArgs &a, uint32_t head_dim, hipStream_t
     bool paired = ntiles >= 2 && g_rt && (uint64_t)((ntiles + 1) / 2) * a.n_kv_heads >= (uint64_t)g_rt->num_cus;
     if (t_prefill_pairing) paired = t_prefill_pairing == 2;
     char name[48];
-    snprintf(name, sizeof name, "rfp4_attn_prefill_hd%u_g%u_w%u%s", head_dim, g, waves, a.q_codes ? "_q" : "");
+    // two key groups of 4 waves per workgroup (alternate key blocks, the
+    // states merged at the end: the serial chain of blocks halves) where the
+    // plan is 4 waves and groups of up to 4 heads.  Measured: 8B prefill 512
+    // tokens 5.29-5.35 -> 5.18-5.24 ms; TinyLlama (8 heads, 8 waves) slower
+    // split (2.21 -> 2.24 ms), so not compiled there.
+    const bool ksplit = t_prefill_ksplit != 1 && waves == 4u && g < 8u;
+    snprintf(name, sizeof name, "rfp4_attn_prefill_hd%u_g%u_w%u%s%s", head_dim, g, waves, a.q_codes ? "_q" : "",
+             ksplit ? "_s2" : "");
     AttnPrefillArgs args = a;
     args.paired = paired ? 1u : 0u;
     const uint32_t gx = paired ? (ntiles + 1) / 2 : ntiles;
-    return launch(name, dim3(gx, a.n_kv_heads), dim3(64u * waves), s, &args);
+    return launch(name, dim3(gx, a.n_kv_heads), dim3(64u * waves * (ksplit ? 2u : 1u)), s, &args);
 }
 
 uint32_t attn_group_pad(uint32_t group) { return group <= 1u ? 1u : group <= 2u ? 2u : group <= 4u ? 4u : 8u; }

@@ -120,6 +120,7 @@ _SIGS = {
     "rfp4_debug_prefill_swiglu": (I32, [I32]),
     "rfp4_debug_prefill_rope": (I32, [I32]),
     "rfp4_debug_prefill_attn_quant": (I32, [I32]),
+    "rfp4_debug_prefill_ksplit": (I32, [I32]),
     "rfp4_debug_attn_head_split": (I32, [I32]),
     "rfp4_debug_qkv_attn": (I32, [I32]),
     "rfp4_debug_gemm_stages": (I32, [I32]),

@@ -266,14 +266,14 @@ def test_attn_decode_f16_parity(rf, orc, stream, nh, nkv, hd, seq):
                                                   (16, 8, 128, 300, 33), (32, 8, 128, 4000, 16), (6, 2, 64, 5, 9),
                                                   (32, 8, 128, 7, 1), (4, 2, 64, 0, 5), (4, 2, 64, 5, 40),
                                                   (8, 2, 128, 0, 3), (2, 2, 128, 0, 130)])
-@pytest.mark.parametrize("waves,pairing", [(4, 1), (8, 1), (4, 2), (8, 2)])
-def test_attn_prefill_f16(rf, orc, stream, nh, nkv, hd, pos0, rows, waves, pairing):
+@pytest.mark.parametrize("waves,pairing,ksplit", [(4, 1, 1), (8, 1, 1), (4, 2, 1), (8, 2, 1), (4, 1, 2), (8, 2, 2)])
+def test_attn_prefill_f16(rf, orc, stream, nh, nkv, hd, pos0, rows, waves, pairing, ksplit):
     """Causal prefill attention on the matrix cores: row r equals the
     oracle's attn_decode at seq = pos0 + r + 1 over the same fp16 caches,
     within the decode kernel's bar (q and p enter the fp16 MFMAs as hi + lo
     fp16 terms, about 2^-22 relative); query-head groups 1, 2, 3 (padded to
     4), 4 and 8, both head dims, 4- and 8-wave workgroups, one or two (paired causal)
-    query tiles per workgroup."""
+    query tiles per workgroup, one or two key groups (where compiled)."""
     rng = np.random.default_rng(pos0 * 31 + rows + hd)
     cap = pos0 + rows + 3
     q = rng.standard_normal((rows, nh * hd)).astype(np.float32)
@@ -283,12 +283,14 @@ def test_attn_prefill_f16(rf, orc, stream, nh, nkv, hd, pos0, rows, waves, pairi
     dout = rf.DeviceBuffer.zeroed(rows * nh * hd, np.float32, stream)
     rf.check(rf.load().rfp4_debug_prefill_waves(waves))
     rf.check(rf.load().rfp4_debug_prefill_pairing(pairing))
+    rf.check(rf.load().rfp4_debug_prefill_ksplit(ksplit))
     try:
         rf.attn_prefill_f16(stream, nh, nkv, hd, pos0, rows, _dev(rf, q.reshape(-1), stream), nh * hd,
                             _dev(rf, kc, stream), _dev(rf, vc, stream), hd, cap * hd, dout, nh * hd)
     finally:
         rf.check(rf.load().rfp4_debug_prefill_waves(0))
         rf.check(rf.load().rfp4_debug_prefill_pairing(0))
+        rf.check(rf.load().rfp4_debug_prefill_ksplit(0))
     got = dout.to_host(rows * nh * hd, np.float32, stream).reshape(rows, nh * hd)
     _assert_attn_close(got, oref)
 
@@ -297,7 +299,10 @@ def test_attn_prefill_f16(rf, orc, stream, nh, nkv, hd, pos0, rows, waves, pairi
 def test_attn_prefill_f16_grouping_invariant(rf, stream, nh, nkv, hd, pos0, rows):
     """Workgroup shape does not change a row's arithmetic: 4- or 8-wave
     workgroups, one or paired causal tiles give bit-identical outputs (key
-    blocks past a row's position add exact zeros with an exact factor 1)."""
+    blocks past a row's position add exact zeros with an exact factor 1).
+    One key group throughout: two (the 4-wave default) merge two partial
+    softmax states, another order of the same sums, held to the oracle's bar
+    by test_attn_prefill_f16."""
     rng = np.random.default_rng(rows + hd)
     cap = pos0 + rows + 3
     q = rng.standard_normal((rows, nh * hd)).astype(np.float32)
@@ -309,11 +314,13 @@ def test_attn_prefill_f16_grouping_invariant(rf, stream, nh, nkv, hd, pos0, rows
         dout = rf.DeviceBuffer.zeroed(rows * nh * hd, np.float32, stream)
         rf.check(rf.load().rfp4_debug_prefill_waves(waves))
         rf.check(rf.load().rfp4_debug_prefill_pairing(pairing))
+        rf.check(rf.load().rfp4_debug_prefill_ksplit(1))
         try:
             rf.attn_prefill_f16(stream, nh, nkv, hd, pos0, rows, dq, nh * hd, dk, dv, hd, cap * hd, dout, nh * hd)
         finally:
             rf.check(rf.load().rfp4_debug_prefill_waves(0))
             rf.check(rf.load().rfp4_debug_prefill_pairing(0))
+            rf.check(rf.load().rfp4_debug_prefill_ksplit(0))
         outs.append(dout.to_host(rows * nh * hd, np.float32, stream))
     for o in outs[1:]:
         np.testing.assert_array_equal(o, outs[0])

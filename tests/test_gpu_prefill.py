@@ -332,3 +332,38 @@ def test_prefill_attn_quant_hook_rejects_bad_values(rf):
     assert lib.rfp4_debug_prefill_attn_quant(2) == -1
     assert lib.rfp4_debug_prefill_attn_quant(-1) == -1
     rf.check(lib.rfp4_debug_prefill_attn_quant(0))
+
+
+@pytest.mark.parametrize("cfg,n", [(TINY, 37), (TINY128, 200), (G1, 130), (W8B, 300)])
+def test_prefill_attention_key_groups(rf, orc, cfg, n):
+    """Two key groups per attention workgroup (alternate key blocks, softmax
+    states merged through LDS; the default where the plan is 4 waves) against
+    one (rfp4_debug_prefill_ksplit(1)): with the f32 rows (stop after stage 3)
+    and the quantizing epilogue, every stage within its bar, both head dims,
+    query-head groups 1, 2 and 4; the next token equal to the one-group
+    kernel's."""
+    seed = 0x5B11 + n
+    prompt = np.random.default_rng(seed).integers(0, cfg["vocab"], n, dtype=np.uint32)
+    print(f"prefill, two key groups: dim={cfg['dim']} n={n}", flush=True)
+    lib = rf.load()
+    eng = _engine(rf, cfg, seed)
+    ref = orc.Model(cfg, seed)
+    try:
+        rf.check(lib.rfp4_debug_prefill_ksplit(1))
+        plain = eng.prefill(prompt, 0)
+        rf.check(lib.rfp4_debug_prefill_ksplit(2))
+        rf.check(lib.rfp4_debug_prefill_waves(4))
+        tok = check_prefill_stages(rf, orc, eng, ref, cfg, prompt, 0)
+    finally:
+        rf.check(lib.rfp4_debug_prefill_ksplit(0))
+        rf.check(lib.rfp4_debug_prefill_waves(0))
+    assert tok == plain
+    eng.close()
+    ref.close()
+
+
+def test_prefill_ksplit_hook_rejects_bad_values(rf):
+    lib = rf.load()
+    assert lib.rfp4_debug_prefill_ksplit(3) == -1
+    assert lib.rfp4_debug_prefill_ksplit(-1) == -1
+    rf.check(lib.rfp4_debug_prefill_ksplit(0))
