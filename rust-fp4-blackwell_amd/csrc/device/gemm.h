@@ -309,6 +309,69 @@ RFP4_DEV void gemm_rope_store(const GemmArgs &g, const float *xl, uint32_t xw0, 
     }
 }
 
+// The same epilogue where a wave's 32 FB columns hold whole heads (32 FB >=
+// rope_hd): the partner of fragment fb is fragment fb ^ (rope_hd / 64) of
+// the same lane and register, no exchange.  n0: the wave's first column.
+// RB rows of fragments per batch: the batch's cos and sin loads, one wait,
+// then its rotations and stores with no load in flight (the stores sit in
+// branches on the column's role, where the compiler would otherwise wait
+// for every store before each later load's use).
+template <int FA, int FB, int RB>
+RFP4_DEV void gemm_rope_store_regs(const GemmArgs &g, const v16f32 (&acc)[FA][FB], uint32_t m0, uint32_t n0,
+                                   uint32_t lane)
+{
+    static_assert(FA % RB == 0, "whole batches");
+    const uint32_t r32 = lane & 31u, h = lane >> 5;
+    const uint32_t hd = g.rope_hd, half = hd >> 1, qk = g.rope_q + g.rope_kv;
+    const float *__restrict__ cosv = g.rope_cos;
+    const float *__restrict__ sinv = g.rope_sin;
+#pragma unroll
+    for (int f0 = 0; f0 < FA; f0 += RB) {
+        float cv[RB][FB][16], sv[RB][FB][16];
+#pragma unroll
+        for (int i = 0; i < RB; i++)
+#pragma unroll
+            for (int fb = 0; fb < FB; fb++) {
+                const uint32_t col0 = n0 + 32u * fb, j = (col0 + r32) & (half - 1u);
+                if (col0 < qk) {
+#pragma unroll
+                    for (int r = 0; r < 16; r++) {
+                        const uint32_t row =
+                            min(m0 + 32u * (f0 + i) + 8u * (uint32_t)(r / 4) + 4u * h + (uint32_t)(r % 4), g.m - 1u);
+                        const size_t t = (size_t)(g.rope_pos0 + row) * half + j;
+                        cv[i][fb][r] = cosv[t];
+                        sv[i][fb][r] = sinv[t];
+                    }
+                }
+            }
+        __builtin_amdgcn_s_waitcnt(0x0F70); // vmcnt(0): the batch's cos and sin
+#pragma unroll
+        for (int i = 0; i < RB; i++)
+#pragma unroll
+            for (int fb = 0; fb < FB; fb++) {
+                const int fa = f0 + i;
+                const uint32_t col0 = n0 + 32u * fb, col = col0 + r32;
+                const bool lo = (col0 & (hd - 1u)) < half, kv = col0 >= g.rope_q, is_v = col0 >= qk;
+                const uint32_t kcol = col - g.rope_q - (is_v ? g.rope_kv : 0u); // k or v columns only
+                uint16_t *cache = (is_v ? g.vc : g.kc) + (size_t)(kcol / hd) * g.kv_hs + (kcol & (hd - 1u));
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const uint32_t row = m0 + 32u * fa + 8u * (uint32_t)(r / 4) + 4u * h + (uint32_t)(r % 4);
+                    float v = acc[fa][fb][r];
+                    if (col0 < qk) {
+                        // the partner fragment: fb ^ 1 for heads of 64, fb ^ 2 for 128 (FB = 4)
+                        const float o = FB >= 4 && hd == 128u ? acc[fa][(fb ^ 2) % FB][r] : acc[fa][(fb ^ 1) % FB][r];
+                        v = lo ? __fsub_rn(__fmul_rn(v, cv[i][fb][r]), __fmul_rn(o, sv[i][fb][r]))
+                               : __fadd_rn(__fmul_rn(v, cv[i][fb][r]), __fmul_rn(o, sv[i][fb][r]));
+                    }
+                    if (row >= g.m || col >= g.n) continue;
+                    __builtin_nontemporal_store(v, g.c + (size_t)row * g.n + col);
+                    if (kv) cache[(size_t)(g.rope_pos0 + row) * g.kv_ts] = f32_to_f16_bits(v);
+                }
+            }
+    }
+}
+
 // LDS reads in inline asm (see gemm_body's step) and the wait for them.
 RFP4_DEV void gemm_lds_rd16(u32x4 &dst, uint32_t addr) { asm volatile("ds_read_b128 %0, %1" : "=v"(dst) : "v"(addr)); }
 RFP4_DEV void gemm_lds_rd4(uint32_t &dst, uint32_t addr) { asm volatile("ds_read_b32 %0, %1" : "=v"(dst) : "v"(addr)); }
@@ -705,9 +768,19 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
     // ---- epilogue: accumulator r of lane l is C[8 (r/4) + 4 (l/32) + r%4][l%32] of its fragment
     const uint32_t m0 = mt * BM + wm * (32u * FA), n0 = nt * BN + wn * (32u * FB);
     if constexpr (ROPE) {
-        // the 4 waves' accumulators in the stages (free after the loop's last
-        // LDS reads), slot = wave; a wave's partners sit in its row of waves
-        static_assert(4u * FA * FB * 16u * 64u * 4u <= NST * STAGE, "the accumulators in the stages");
+        // Heads that lie whole in the wave's columns (32 FB >= rope_hd):
+        // partners in its own registers.  Else the 4 waves' accumulators go
+        // to the stages (free after the loop's last LDS reads), slot = wave;
+        // a wave's partners sit in its row of waves (the same wm).  Batches
+        // of cos / sin loads: the whole wave tile (at most 4 fragments here).
+        if constexpr (FB >= 2) {
+            if (32u * FB >= g.rope_hd) {
+                gemm_rope_store_regs<FA, FB, FA >= 2 ? 2 : 1>(g, acc, m0, n0, lane);
+                return;
+            }
+        }
+        static_assert(4u * FA * FB * 16u * 64u * 4u <= NST * STAGE && FA * FB <= 4,
+                      "the RoPE epilogue's tiles: the 4 waves' accumulators in the stages");
         float *xl = (float *)lds_raw;
         __syncthreads();
         gemm_rope_put<FA, FB, FA>(xl, wave, acc, 0, lane);

@@ -213,10 +213,20 @@ GEMM_KERNEL_PP(256, 128, 4, 1)
 // output in the epilogue (GemmArgs::q_codes)
 K512 void rfp4_gemm_256x256_ppsw(GemmArgs a) { gemm_pp_body<4, 2, 1>(a); }
 // the prefill's q|k|v projection with RoPE and the fp16 K/V cache rows in
-// the epilogue (GemmArgs::rope_cos): the plans of that shape at 512 and
-// 2048 prompt rows
-K256 void rfp4_gemm_128x128_rope(GemmArgs a) { gemm_body<2, 2, 2, 2, 2, GEMM_PIPE(2, 2), true>(a); }
-K256 void rfp4_gemm_128x128_p3_rope(GemmArgs a) { gemm_body<2, 2, 2, 2, 3, GEMM_PIPE(2, 2), true>(a); }
+// the epilogue (GemmArgs::rope_cos): the 4-wave tiles up to 128 rows and the
+// ping-pong 256x256 (a 256x128 variant measured slower than the GEMM + the
+// row kernel: TinyLlama 2048 rows 28.5 against 16.8 + 9.6 us)
+#define GEMM_KERNEL_ROPE(BM, BN, WM, WN, FA, FB) \
+    K256 void rfp4_gemm_##BM##x##BN##_rope(GemmArgs a) { gemm_body<WM, WN, FA, FB, 2, GEMM_PIPE(FA, FB), true>(a); }
+#define GEMM_KERNEL_P_ROPE(BM, BN, WM, WN, FA, FB, NST) \
+    K256 void rfp4_gemm_##BM##x##BN##_p##NST##_rope(GemmArgs a) { gemm_body<WM, WN, FA, FB, NST, GEMM_PIPE(FA, FB), true>(a); }
+GEMM_KERNEL_ROPE(32, 128, 1, 4, 1, 1)
+GEMM_KERNEL_ROPE(64, 128, 2, 2, 1, 2)
+GEMM_KERNEL_ROPE(128, 128, 2, 2, 2, 2)
+GEMM_KERNEL_P_ROPE(32, 128, 1, 4, 1, 1, 4)
+GEMM_KERNEL_P_ROPE(64, 128, 2, 2, 1, 2, 4)
+GEMM_KERNEL_P_ROPE(64, 128, 2, 2, 1, 2, 3)
+GEMM_KERNEL_P_ROPE(128, 128, 2, 2, 2, 2, 3)
 K512 void rfp4_gemm_256x256_pp_rope(GemmArgs a) { gemm_pp_body<4, 2, 2>(a); }
 K256 void rfp4_gemm_reduce(GemmArgs a) { gemm_reduce_body(a); }
 // row-major E8M0 scales -> the step-blocked copy the tiled kernels read

@@ -1539,29 +1539,49 @@ int gemm_swiglu_launch(hipStream_t stream, uint32_t m, uint32_t ffn, uint32_t k,
     return launch("rfp4_gemm_256x256_ppsw", dim3((unsigned)tiles), dim3(512), stream, &a);
 }
 
-// The _rope kernel for the plan of (m, n, k): the 128x128 tile with 2 or 3
-// stages, the 256x256 ping-pong tile, no K split (name null: none).
+// The _rope kernel for the plan of (m, n, k), no K split: the plan's
+// 4-wave kernel with the epilogue (kernels.hip GEMM_KERNEL_ROPE /
+// GEMM_KERNEL_P_ROPE: the tiles up to 128 rows, at the stage counts the
+// planner uses), or the ping-pong 256x256 one (false: none).
 struct RopeKernel {
-    const char *name;
+    char name[48];
     int tile;
     unsigned threads;
 };
-static RopeKernel gemm_rope_kernel(uint32_t m, uint32_t n, uint32_t k)
+static bool gemm_rope_kernel(uint32_t m, uint32_t n, uint32_t k, RopeKernel &rk)
 {
     Runtime *rt = g_rt;
-    if (!rt || m == 0 || n == 0 || k == 0 || k % 256u) return {nullptr, 0, 0};
+    if (!rt || m == 0 || n == 0 || k == 0 || k % 256u) return false;
     const GemmPlan p = gemm_plan(m, n, k, (uint32_t)rt->num_cus);
-    if (p.tile == kGemmSkinny || p.kz != 1u) return {nullptr, 0, 0};
+    if (p.tile == kGemmSkinny || p.kz != 1u) return false;
     const bool pp = gemm_use_pp(p, m, n, k);
-    if (p.tile == 0 && pp) return {"rfp4_gemm_256x256_pp_rope", 0, 512u};
-    if (p.tile == 2 && !pp && p.nst == 2) return {"rfp4_gemm_128x128_rope", 2, 256u};
-    if (p.tile == 2 && !pp && p.nst == 3) return {"rfp4_gemm_128x128_p3_rope", 2, 256u};
-    return {nullptr, 0, 0};
+    rk.tile = p.tile;
+    if (p.tile == 0) {
+        if (!pp) return false;
+        snprintf(rk.name, sizeof rk.name, "rfp4_gemm_256x256_pp_rope");
+        rk.threads = 512u;
+        return true;
+    }
+    if (pp) return false;
+    // compiled: 128x128, 64x128 and 32x128 with 2 stages; 3 for 64x128 and
+    // 128x128; 4 for 32x128 and 64x128 (no 256x128: slower than the GEMM +
+    // the row kernel where measured)
+    const int nst = p.nst;
+    const bool ok = p.tile >= 2 && (nst == 2 || (nst == 3 && (p.tile == 2 || p.tile == 3)) ||
+                                    (nst == 4 && (p.tile == 3 || p.tile == 4)));
+    if (!ok) return false;
+    if (nst == 2) snprintf(rk.name, sizeof rk.name, "%s_rope", kGemmTiles[p.tile].name);
+    else snprintf(rk.name, sizeof rk.name, "%s_p%d_rope", kGemmTiles[p.tile].name, nst);
+    rk.threads = 256u;
+    return true;
 }
 
 bool gemm_rope_ok(uint32_t m, uint32_t n, uint32_t k, uint32_t hd)
 {
-    return (hd == 64u || hd == 128u) && n % hd == 0u && gemm_rope_kernel(m, n, k).name != nullptr;
+    RopeKernel rk;
+    if (!(hd == 64u || hd == 128u) || n % hd || !gemm_rope_kernel(m, n, k, rk)) return false;
+    // a head lies in one column tile (the tile widths are multiples of 128)
+    return kGemmTiles[rk.tile].bn % hd == 0u;
 }
 
 int gemm_rope_launch(hipStream_t stream, uint32_t m, uint32_t n, uint32_t k, const uint8_t *a_codes,
@@ -1575,7 +1595,8 @@ int gemm_rope_launch(hipStream_t stream, uint32_t m, uint32_t n, uint32_t k, con
     if (!gemm_rope_ok(m, n, k, r.hd) || r.q % r.hd || r.kv % r.hd || n != r.q + 2u * r.kv)
         return set_error(RFP4_E_SHAPE, "gemm_rope: no RoPE epilogue for %u x %u x %u with heads of %u (q %u, kv %u)", m,
                          n, k, r.hd, r.q, r.kv);
-    const RopeKernel rk = gemm_rope_kernel(m, n, k);
+    RopeKernel rk;
+    gemm_rope_kernel(m, n, k, rk);
     const GemmTile &t = kGemmTiles[rk.tile];
     GemmArgs a{a_codes, a_scales, w_codes, w_scales, c, nullptr, m, n, k, 1u, nullptr, a_st, w_st,
                nullptr, nullptr, nullptr, 0u, 0u, r.cosv, r.sinv, r.kc, r.vc, r.ts, r.hs, r.pos0, r.q, r.kv, r.hd};

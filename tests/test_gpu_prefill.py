@@ -244,11 +244,16 @@ def test_prefill_swiglu_in_gemm_epilogue(rf, orc):
     (TINY128, 250, 0, 2, 3, "rfp4_gemm_128x128_p3/kz1"),      # heads of 128, ragged rows
     (TINY128, 200, 0, 0, 0, "rfp4_gemm_256x256_pp/kz1"),
     (G8, 70, 5, 0, 0, "rfp4_gemm_256x256_pp/kz1"),            # 640 columns: a ragged column tile; pos0 > 0
+    (TINY, 37, 0, 4, 2, "rfp4_gemm_32x128/kz1"),
+    (TINY128, 120, 3, 4, 4, "rfp4_gemm_32x128_p4/kz1"),
+    (TINY128, 250, 0, 3, 3, "rfp4_gemm_64x128_p3/kz1"),
+    (G8, 70, 0, 3, 4, "rfp4_gemm_64x128_p4/kz1"),
+    (G8, 130, 0, 2, 3, "rfp4_gemm_128x128_p3/kz1"),            # heads of 64: partners in the wave's registers
 ])
 def test_prefill_rope_in_gemm_epilogue(rf, orc, cfg, n, pos0, tile, nst, plan):
-    """RoPE and the fp16 K/V cache rows in the q|k|v GEMM's epilogue
-    (rfp4_gemm_128x128_rope, _128x128_p3_rope, _256x256_pp_rope), each reached
-    by a forced plan, heads of 64 and 128: the staged check (stage 2 compares
+    """RoPE and the fp16 K/V cache rows in the q|k|v GEMM's epilogue (the
+    _rope kernels of every tile and stage count compiled), each reached by a
+    forced plan, heads of 64 and 128: the staged check (stage 2 compares
     the rotated q and the fp16 K/V rows bit for bit with the oracle's RoPE of
     the GEMM's own output, which the stop after stage 1 takes from the plain
     GEMM), and against the GEMM + row kernel path (rfp4_debug_prefill_rope(1)):
