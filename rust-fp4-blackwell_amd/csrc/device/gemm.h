@@ -419,7 +419,11 @@ RFP4_DEV void gemm_lds_wait_all(GemmOps<FA, FB> &o)
 
 // PIPE: next step's LDS reads overlap this step's MFMAs (two register sets
 // of operands); without it the reads and MFMAs of a step run back to back.
-template <int WM, int WN, int FA, int FB, int NST = 2, bool PIPE = false, bool ROPE = false>
+// SWQ: the SwiGLU + MXFP4 epilogue of the prefill's gate|up projection, as
+// gemm_pp_body's (GemmArgs::q_codes): column tile nt's W rows are gate rows
+// (BN/2) nt .. +BN/2 - 1 and the matching up rows pair_off + (BN/2) nt ..;
+// the tile writes BN/2 output columns as MXFP4, no C.
+template <int WM, int WN, int FA, int FB, int NST = 2, bool PIPE = false, bool ROPE = false, bool SWQ = false>
 RFP4_DEV void gemm_body(const GemmArgs &g)
 {
     static_assert(WM * WN == 4, "4 waves");
@@ -469,7 +473,10 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
         const uint32_t row = 8u * (wave + 4u * j) + (lane >> 3);
         const uint32_t qq = (lane & 7u) ^ gemm_swz(row);
         if (row < BM) src[j] = g.a_codes + (size_t)min(mt * BM + row, g.m - 1u) * kbytes + qq * 16u;
-        else src[j] = g.w_codes + (size_t)min(nt * BN + (row - BM), g.n - 1u) * kbytes + qq * 16u;
+        else if (SWQ) {
+            const uint32_t wr = row - BM; // gate rows, then the matching up rows
+            src[j] = g.w_codes + (size_t)((wr < BN / 2u ? 0u : g.pair_off - BN / 2u) + nt * (BN / 2u) + wr) * kbytes + qq * 16u;
+        } else src[j] = g.w_codes + (size_t)min(nt * BN + (row - BM), g.n - 1u) * kbytes + qq * 16u;
     }
     // Scale block b of this wave covers tile rows 32 (wave + 4 b) .. +31: the
     // step-blocked block of those rows (clamped to the last block, so that
@@ -478,9 +485,12 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
 #pragma unroll
     for (uint32_t b = 0; b < NSB; b++) {
         const uint32_t tb = min(wave + 4u * b, R / 32u - 1u);
+        const uint32_t wb = tb - BM / 32u; // W block of the tile (tb >= BM / 32)
+        const uint32_t wblk = SWQ ? (wb < BN / 64u ? 0u : (g.pair_off - BN / 2u) >> 5) + nt * (BN / 64u) + wb
+                                  : min(nt * (BN / 32u) + wb, (g.n - 1u) >> 5);
         const uint8_t *base = tb < BM / 32u
                                   ? g.a_st + (size_t)min(mt * (BM / 32u) + tb, (g.m - 1u) >> 5) * nsuper * 256u
-                                  : g.w_st + (size_t)min(nt * (BN / 32u) + (tb - BM / 32u), (g.n - 1u) >> 5) * nsuper * 256u;
+                                  : g.w_st + (size_t)wblk * nsuper * 256u;
         ssrc[b] = base + lane * 4u;
     }
 #define RFP4_GEMM_DMA(S, BUF)                                                                              \
@@ -767,6 +777,50 @@ RFP4_DEV void gemm_body(const GemmArgs &g)
 
     // ---- epilogue: accumulator r of lane l is C[8 (r/4) + 4 (l/32) + r%4][l%32] of its fragment
     const uint32_t m0 = mt * BM + wm * (32u * FA), n0 = nt * BN + wn * (32u * FB);
+    if constexpr (SWQ) {
+        // the 4 waves' accumulators in the stages as a [BM][gate BN/2 | up
+        // BN/2] tile (constant register indices), then each thread takes
+        // blocks of 32 output columns of one row (consecutive threads on
+        // consecutive rows, distinct banks with the padded row) and quantizes
+        // them whole, with the row kernel's arithmetic (quant_block32)
+        constexpr uint32_t GLD = BN + 4u, NBLK = BN / 64u; // floats per LDS row (padded); output blocks per row
+        static_assert(BM * GLD * 4u <= NST * STAGE, "the tile in the stages");
+        float *tl = (float *)lds_raw;
+        __syncthreads(); // the loop's last LDS reads are done
+#pragma unroll
+        for (int fa = 0; fa < FA; fa++)
+#pragma unroll
+            for (int fb = 0; fb < FB; fb++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const uint32_t rl = wm * (32u * FA) + 32u * fa + 8u * (uint32_t)(r / 4) + 4u * h + (uint32_t)(r % 4);
+                    tl[rl * GLD + wn * (32u * FB) + 32u * fb + r32] = acc[fa][fb][r];
+                }
+        __syncthreads();
+        const uint32_t nblk = g.pair_off >> 5, nsup = g.pair_off >> 8;
+        for (uint32_t e = tid; e < BM * NBLK; e += 256u) {
+            const uint32_t rl = e % BM, bl = e / BM;
+            const uint32_t row = mt * BM + rl, blk = nt * NBLK + bl;
+            const float4 *gp = (const float4 *)(tl + rl * GLD + 32u * bl), *up = (const float4 *)(tl + rl * GLD + BN / 2u + 32u * bl);
+            float y[32];
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float4 gv = gp[i], uv = up[i];
+                y[4 * i] = __fmul_rn(silu_ref(gv.x), uv.x);
+                y[4 * i + 1] = __fmul_rn(silu_ref(gv.y), uv.y);
+                y[4 * i + 2] = __fmul_rn(silu_ref(gv.z), uv.z);
+                y[4 * i + 3] = __fmul_rn(silu_ref(gv.w), uv.w);
+            }
+            uint4 q16;
+            const uint32_t sbyte = quant_block32(y, (uint8_t *)&q16);
+            if (row < g.m) {
+                *(uint4 *)(g.q_codes + (size_t)row * (g.pair_off >> 1) + (size_t)blk * 16u) = q16;
+                g.q_scales[(size_t)row * nblk + blk] = (uint8_t)sbyte;
+                if (g.q_scales_t) g.q_scales_t[mx_st_offset(row, blk, nsup)] = (uint8_t)sbyte;
+            }
+        }
+        return;
+    }
     if constexpr (ROPE) {
         // Heads that lie whole in the wave's columns (32 FB >= rope_hd):
         // partners in its own registers.  Else the 4 waves' accumulators go

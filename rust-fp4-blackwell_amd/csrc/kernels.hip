@@ -212,6 +212,9 @@ GEMM_KERNEL_PP(256, 128, 4, 1)
 // the prefill's gate|up projection with SwiGLU and the MXFP4 rows of its
 // output in the epilogue (GemmArgs::q_codes)
 K512 void rfp4_gemm_256x256_ppsw(GemmArgs a) { gemm_pp_body<4, 2, 1>(a); }
+// the same epilogue on the 4-wave 128x128 tile (64 output columns per tile)
+K256 void rfp4_gemm_128x128_sw(GemmArgs a) { gemm_body<2, 2, 2, 2, 2, GEMM_PIPE(2, 2), false, true>(a); }
+K256 void rfp4_gemm_128x128_p3_sw(GemmArgs a) { gemm_body<2, 2, 2, 2, 3, GEMM_PIPE(2, 2), false, true>(a); }
 // the prefill's q|k|v projection with RoPE and the fp16 K/V cache rows in
 // the epilogue (GemmArgs::rope_cos): the 4-wave tiles up to 128 rows and the
 // ping-pong 256x256 (a 256x128 variant measured slower than the GEMM + the

@@ -1515,12 +1515,32 @@ int gemm_launch(hipStream_t stream, uint32_t m, uint32_t n, uint32_t k, const ui
                   (hipStream_t)stream, &a);
 }
 
-bool gemm_swiglu_ok(uint32_t m, uint32_t ffn, uint32_t k)
+// The kernel with the SwiGLU epilogue for the plan of the plain GEMM (m, 2
+// ffn, k), no K split: the 256x256 ping-pong tile (ffn % 256 == 0: whole
+// 128-column pairs and step-blocked output scales), or the 128x128 tile with
+// 2 or 3 stages (64-column pairs).  Null: none.
+static const char *gemm_swiglu_kernel(uint32_t m, uint32_t ffn, uint32_t k, uint32_t &cols)
 {
     Runtime *rt = g_rt;
-    if (!rt || m == 0 || ffn == 0 || ffn % 256u || k == 0 || k % 256u) return false;
+    if (!rt || m == 0 || ffn == 0 || ffn % 256u || k == 0 || k % 256u) return nullptr;
     const GemmPlan p = gemm_plan(m, 2u * ffn, k, (uint32_t)rt->num_cus);
-    return p.tile == 0 && p.kz == 1u && gemm_use_pp(p, m, 2u * ffn, k);
+    if (p.kz != 1u) return nullptr;
+    const bool pp = gemm_use_pp(p, m, 2u * ffn, k);
+    if (p.tile == 0 && pp) {
+        cols = 128u;
+        return "rfp4_gemm_256x256_ppsw";
+    }
+    if (p.tile == 2 && !pp && (p.nst == 2 || p.nst == 3)) {
+        cols = 64u;
+        return p.nst == 2 ? "rfp4_gemm_128x128_sw" : "rfp4_gemm_128x128_p3_sw";
+    }
+    return nullptr;
+}
+
+bool gemm_swiglu_ok(uint32_t m, uint32_t ffn, uint32_t k)
+{
+    uint32_t cols = 0;
+    return gemm_swiglu_kernel(m, ffn, k, cols) != nullptr;
 }
 
 int gemm_swiglu_launch(hipStream_t stream, uint32_t m, uint32_t ffn, uint32_t k, const uint8_t *a_codes,
@@ -1531,12 +1551,15 @@ int gemm_swiglu_launch(hipStream_t stream, uint32_t m, uint32_t ffn, uint32_t k,
         return set_error(RFP4_E_INVALID, "gemm_swiglu: null pointer");
     if (((uintptr_t)a_codes | (uintptr_t)w_codes) & 15u || ((uintptr_t)q_codes | (uintptr_t)a_st | (uintptr_t)w_st) & 3u)
         return set_error(RFP4_E_ALIGN, "gemm_swiglu: misaligned codes or scales");
-    if (!gemm_swiglu_ok(m, ffn, k))
-        return set_error(RFP4_E_SHAPE, "gemm_swiglu: the plan of %u x %u x %u is not the 256x256 ping-pong tile", m, 2u * ffn, k);
+    uint32_t cols = 0;
+    const char *kname = gemm_swiglu_kernel(m, ffn, k, cols);
+    if (!kname)
+        return set_error(RFP4_E_SHAPE, "gemm_swiglu: the plan of %u x %u x %u has no SwiGLU epilogue", m, 2u * ffn, k);
     GemmArgs a{a_codes, a_scales, w_codes, w_scales, nullptr, nullptr, m, 2u * ffn, k, 1u, nullptr, a_st, w_st,
                q_codes, q_scales, q_scales_t, ffn, 0u};
-    const uint64_t tiles = (uint64_t)((m + 255u) / 256u) * (ffn / 128u);
-    return launch("rfp4_gemm_256x256_ppsw", dim3((unsigned)tiles), dim3(512), stream, &a);
+    const uint32_t bm = cols == 128u ? 256u : 128u; // tile rows
+    const uint64_t tiles = (uint64_t)((m + bm - 1u) / bm) * (ffn / cols);
+    return launch(kname, dim3((unsigned)tiles), dim3(cols == 128u ? 512 : 256), stream, &a);
 }
 
 // The _rope kernel for the plan of (m, n, k), no K split: the plan's

@@ -372,3 +372,44 @@ def test_prefill_ksplit_hook_rejects_bad_values(rf):
     assert lib.rfp4_debug_prefill_ksplit(3) == -1
     assert lib.rfp4_debug_prefill_ksplit(-1) == -1
     rf.check(lib.rfp4_debug_prefill_ksplit(0))
+
+
+@pytest.mark.parametrize("cfg,n,nst,kernel", [(TINY128, 200, 2, "rfp4_gemm_128x128/kz1"),
+                                              (TINY128, 130, 3, "rfp4_gemm_128x128_p3/kz1"),
+                                              (W8B, 300, 3, "rfp4_gemm_128x128_p3/kz1")])
+def test_prefill_swiglu_epilogue_128x128(rf, orc, cfg, n, nst, kernel):
+    """SwiGLU and the MXFP4 rows of its output in the 4-wave 128x128 GEMM's
+    epilogue (rfp4_gemm_128x128[_p3]_sw: 64 gate rows paired with the
+    matching 64 up rows per tile), reached by a forced plan: every stage
+    within its bar (the SwiGLU rows against the exact values of the plain
+    GEMM's output), and against the GEMM + row kernel path: the same scale
+    bytes and codes but at rounding boundaries (the paired tile's K order),
+    the same next token."""
+    seed = 0x5E11 + n
+    prompt = np.random.default_rng(seed).integers(0, cfg["vocab"], n, dtype=np.uint32)
+    print(f"prefill SwiGLU epilogue on 128x128: dim={cfg['dim']} n={n} stages {nst}", flush=True)
+    ffn = cfg["ffn"]
+    lib = rf.load()
+    eng = _engine(rf, cfg, seed)
+    ref = orc.Model(cfg, seed)
+    rows = {}
+    try:
+        rf.debug_gemm_plan(2, 1)
+        rf.check(lib.rfp4_debug_gemm_stages(nst))
+        assert rf.gemm_plan_kernel(n, 2 * ffn, cfg["dim"]) == kernel
+        tok = check_prefill_stages(rf, orc, eng, ref, cfg, prompt, 0)
+        for mode in (0, 1):
+            rf.check(lib.rfp4_debug_prefill_swiglu(mode))
+            eng.prefill_stop(prompt, 0, 18)  # layer 1's SwiGLU rows
+            rows[mode] = (eng.prefill_buffer("codes", (n, ffn // 2), np.uint8),
+                          eng.prefill_buffer("scales", (n, ffn // 32), np.uint8), eng.prefill(prompt, 0))
+    finally:
+        rf.check(lib.rfp4_debug_prefill_swiglu(0))
+        rf.check(lib.rfp4_debug_gemm_stages(0))
+        rf.debug_gemm_plan(-1, 0)
+    (cf, sf, tf), (cu, su, tu) = rows[0], rows[1]
+    assert tf == tu == tok
+    assert np.count_nonzero(sf != su) <= max(2, n * ffn // 32 // 10000)
+    assert np.count_nonzero(cf != cu) <= max(4, n * ffn // 2 // 10000)
+    eng.close()
+    ref.close()
