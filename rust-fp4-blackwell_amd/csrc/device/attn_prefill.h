@@ -193,28 +193,39 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
                     s[h] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ka, ql[mt][k], s[h], 0, 0, 0);
                 }
             }
-            // ---- causal mask, online softmax (base 2) of the lane's row
-            const uint32_t qrow = r0 + 16u * (t / GT) + l16;
-            const uint32_t qpos = pos0 + min(qrow, nrows - 1u);
+            // ---- causal mask (only in blocks that reach past the tile's first
+            // row), online softmax (base 2) of the lane's row
+            const uint32_t row0 = r0 + 16u * (t / GT);
+            const uint32_t qpos = pos0 + min(row0 + l16, nrows - 1u);
+            const bool masked = (b + 1u) * PF_BK > pos0 + min(row0, nrows - 1u) + 1u; // the same for the whole wave
             float p[4 * NQ];
-            float mx = -3.402823466e38f;
+            if (masked) {
 #pragma unroll
-            for (int h = 0; h < NQ; h++)
+                for (int h = 0; h < NQ; h++)
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const uint32_t key = b * PF_BK + 16u * h + 4u * q4 + (uint32_t)r;
-                    const float v = s[h][r] * scale;
-                    p[4 * h + r] = key <= qpos ? v : -3.402823466e38f;
-                    mx = fmaxf(mx, p[4 * h + r]);
-                }
-            mx = xor32_max(xor16_max(mx));
+                    for (int r = 0; r < 4; r++) {
+                        const uint32_t key = b * PF_BK + 16u * h + 4u * q4 + (uint32_t)r;
+                        p[4 * h + r] = key <= qpos ? s[h][r] : -3.402823466e38f;
+                    }
+            } else {
+#pragma unroll
+                for (int h = 0; h < NQ; h++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) p[4 * h + r] = s[h][r];
+            }
+            // the maximum of the raw scores, then scaled: rounding is monotonic,
+            // so this is the maximum of the scaled scores
+            float mx = p[0];
+#pragma unroll
+            for (int i = 1; i < 4 * NQ; i++) mx = fmaxf(mx, p[i]);
+            mx = xor32_max(xor16_max(mx)) * scale;
             const float mnew = fmaxf(mrun[mt], mx);
             const float alpha = __builtin_amdgcn_exp2f(mrun[mt] - mnew);
             mrun[mt] = mnew;
             float ls = 0.0f;
 #pragma unroll
             for (int i = 0; i < 4 * NQ; i++) {
-                p[i] = __builtin_amdgcn_exp2f(p[i] - mnew);
+                p[i] = __builtin_amdgcn_exp2f(p[i] * scale - mnew);
                 ls += p[i];
             }
             lrun[mt] = fmaf(lrun[mt], alpha, xor32_sum(xor16_sum(ls)));
@@ -226,7 +237,7 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
 #pragma unroll
             for (int c = 0; c < NQ / 2; c++) {
                 f16x8 pb, pl;
-                split_hi_lo8(p + 8 * c, pb, pl);
+                split_hi_lo8_mix(p + 8 * c, pb, pl);
 #pragma unroll
                 for (int n = 0; n < NN; n++) {
                     const _Float16 *vrow = &vt[kgrp][16u * n + l16][32u * c + 4u * q4];

@@ -120,6 +120,29 @@ RFP4_DEV void split_hi_lo8(const float *v, f16x8 &hi, f16x8 &lo)
     }
 }
 
+// The same split in three instructions per pair of values: hi by the packed
+// conversion, lo = fp16(v - hi) by v_fma_mix{lo,hi}_f16 (v * 1.0 + -hi with
+// hi taken as an fp16 half, one rounding of the exact difference: the same
+// bits as split_hi_lo8).
+RFP4_DEV void split_hi_lo8_mix(const float *v, f16x8 &hi, f16x8 &lo)
+{
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+    u32x4v hw, lw;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){v[2 * j], v[2 * j + 1]}, f16x2));
+        uint32_t l;
+        asm("v_fma_mixlo_f16 %0, %1, 1.0, -%2 op_sel_hi:[0,0,1]" : "=v"(l) : "v"(v[2 * j]), "v"(h));
+        asm("v_fma_mixhi_f16 %0, %1, 1.0, -%2 op_sel:[0,0,1] op_sel_hi:[0,0,1]" : "+v"(l) : "v"(v[2 * j + 1]), "v"(h));
+        hw[j] = h;
+        lw[j] = l;
+    }
+    hi = __builtin_bit_cast(f16x8, hw);
+    lo = __builtin_bit_cast(f16x8, lw);
+}
+
 // ---------------------------------------------------------------- E2M1 / E8M0
 // Two E2M1 codes of byte SEL of w -> (low nibble, high nibble) as f32, via the
 // gfx950 hardware conversion (scale 1.0, so the value is the plain code value).
