@@ -339,12 +339,9 @@ RFP4_DEV void attn_prefill_tile(const AttnPrefillArgs &a, uint32_t r0)
                     se = se < -127 ? -127 : (se > 127 ? 127 : se);
                     sbyte = (uint32_t)(se + 127);
                 }
-                uint32_t lo = 0, hi = 0;
-#pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    lo |= e2m1_rne_code(amax != 0.0f ? ldexpf(y[r], -se) : y[r]) << (4 * r);
-                    hi |= e2m1_rne_code(amax != 0.0f ? ldexpf(y[4 + r], -se) : y[4 + r]) << (4 * r);
-                }
+                const float sc = ldexpf(1.0f, se); // 1 where amax is 0 (se = 0)
+                const uint32_t lo = fp4_pack2<1>(fp4_pack2<0>(0u, y[0], y[1], sc), y[2], y[3], sc);
+                const uint32_t hi = fp4_pack2<1>(fp4_pack2<0>(0u, y[4], y[5], sc), y[6], y[7], sc);
                 if (row < nrows) {
                     uint8_t *cp = a.q_codes + (size_t)row * (qd / 2u) + (size_t)head * (HD / 2) + 16u * b + 2u * q4;
                     *(uint16_t *)cp = (uint16_t)lo;

@@ -134,6 +134,18 @@ RFP4_DEV uint32_t e2m1_rne_code(float v)
     return c;
 }
 
+// e2m1_rne_code(ldexpf(v, -se)) for two values at once: the gfx950 packed
+// conversion divides by its scale operand, here 2^se (se in [-127, 127];
+// 2^-127 is subnormal and used as is), and writes a's code to the low nibble
+// and b's to the high nibble of byte SEL of w.  Checked against
+// e2m1_rne_code on every finite f32 that a block of each shared exponent can
+// hold (|v| < 2^(se + 3)), signed zeros and subnormals included: identical.
+template <int SEL>
+RFP4_DEV uint32_t fp4_pack2(uint32_t w, float a, float b, float scale)
+{
+    return __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(w, a, b, scale, SEL);
+}
+
 // Quantize 32 values; writes 16 code bytes and returns the scale byte.
 RFP4_DEV uint32_t quant_block32(const float *v, uint8_t *out16)
 {
@@ -147,11 +159,15 @@ RFP4_DEV uint32_t quant_block32(const float *v, uint8_t *out16)
         se = se < -127 ? -127 : (se > 127 ? 127 : se);
         sbyte = (uint32_t)(se + 127);
     }
-    uint32_t words[4] = {0, 0, 0, 0};
+    const float sc = ldexpf(1.0f, se); // 1 where amax is 0 (se = 0)
+    uint32_t words[4];
 #pragma unroll
-    for (int i = 0; i < 32; i++) {
-        float s = amax != 0.0f ? ldexpf(v[i], -se) : v[i];
-        words[i >> 3] |= e2m1_rne_code(s) << (4 * (i & 7));
+    for (int j = 0; j < 4; j++) {
+        const float *u = v + 8 * j;
+        uint32_t w = fp4_pack2<0>(0u, u[0], u[1], sc);
+        w = fp4_pack2<1>(w, u[2], u[3], sc);
+        w = fp4_pack2<2>(w, u[4], u[5], sc);
+        words[j] = fp4_pack2<3>(w, u[6], u[7], sc);
     }
     *(uint4 *)out16 = make_uint4(words[0], words[1], words[2], words[3]);
     return sbyte;
@@ -186,13 +202,8 @@ RFP4_DEV void quant_block32_x8(float4 v, uint8_t *codes16, uint8_t *scale, uint8
         se = se < -127 ? -127 : (se > 127 ? 127 : se);
         sbyte = (uint32_t)(se + 127);
     }
-    const float f[4] = {v.x, v.y, v.z, v.w};
-    uint32_t h = 0;
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const float sv = amax != 0.0f ? ldexpf(f[i], -se) : f[i];
-        h |= e2m1_rne_code(sv) << (4 * i);
-    }
+    const float sc = ldexpf(1.0f, se); // 1 where amax is 0 (se = 0)
+    const uint32_t h = fp4_pack2<1>(fp4_pack2<0>(0u, v.x, v.y, sc), v.z, v.w, sc);
     const uint32_t hn = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)h, DPP_QUAD_1032, 0xF, 0xF, false); // part p ^ 1
     if ((p & 1u) == 0) *(uint32_t *)(codes16 + 2u * p) = h | (hn << 16);
     if (p == 0) {

@@ -933,6 +933,17 @@ int rfp4_debug_gemv_fused(rfp4_stream_t stream, int epi, int scale_format, uint3
     return gemv_launch(sname, epi, a, (hipStream_t)stream);
 }
 
+int rfp4_debug_fp4_encode_check(rfp4_stream_t stream, int32_t se0, uint32_t n_se, unsigned long long *mismatches,
+                                unsigned long long *tested)
+{
+    if (!mismatches || !tested) return set_error(RFP4_E_INVALID, "fp4_encode_check: null pointer");
+    if (n_se == 0 || se0 < -127 || (int64_t)se0 + (int64_t)n_se - 1 > 125)
+        return set_error(RFP4_E_INVALID, "fp4_encode_check: exponents %d .. %d outside -127 .. 125", se0,
+                         (int)((int64_t)se0 + (int64_t)n_se - 1));
+    Fp4CheckArgs a{mismatches, tested, se0, 0};
+    return launch("rfp4_fp4_encode_check", dim3(2048, n_se), dim3(256), (hipStream_t)stream, &a);
+}
+
 int rmsnorm(rfp4_stream_t stream, uint32_t dim, float eps, const float *x, const float *weight, float *y)
 {
     if (!x || !weight || !y) return set_error(RFP4_E_INVALID, "rmsnorm: null pointer");

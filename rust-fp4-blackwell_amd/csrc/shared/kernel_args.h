@@ -202,6 +202,15 @@ typedef struct QuantMxArgs {
     uint8_t *scales_t;    // the scales step-blocked as well (GemmArgs; k % 256 == 0), or null
 } QuantMxArgs;
 
+// rfp4_debug_fp4_encode_check: per shared exponent se0 + blockIdx.y, the
+// count of values whose hardware and software FP4 codes differ, and of values
+// compared
+typedef struct Fp4CheckArgs {
+    unsigned long long *mismatches, *tested;
+    int32_t se0;
+    uint32_t pad;
+} Fp4CheckArgs;
+
 // Device-resident decode cursor: lets one captured step graph replay for
 // every token.  pos = absolute position, step = index into ids[].
 typedef struct StepState {

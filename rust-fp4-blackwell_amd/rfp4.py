@@ -128,6 +128,7 @@ _SIGS = {
     "rfp4_debug_gemm_reduce_kernel": (I32, [I32]),
     "rfp4_debug_prefill_waves": (I32, [I32]),
     "rfp4_debug_prefill_pairing": (I32, [I32]),
+    "rfp4_debug_fp4_encode_check": (I32, [P, C.c_int32, U32, P, P]),
     "rfp4_debug_gemv_fused": (I32, [P, I32, I32, U32, U32, U32, P, P, P, P, F32, P, P, P]),
     "rfp4_mma_bf16_tile": (I32, [P, P, P, P]),
     "rfp4_mma_f16_tile": (I32, [P, P, P, P]),

@@ -34,6 +34,29 @@ def test_hw_fp4_conversion_matches_codec(rf, orc, stream):
         np.testing.assert_array_equal(got[:, sel, 1], hi)
 
 
+def test_hw_fp4_encoder_matches_rne_exhaustive(rf, stream):
+    """The encoder every quantizing kernel uses (v_cvt_scalef32_pk_fp4_f32,
+    scale 2^se) against e2m1_rne_code(ldexpf(v, -se)), which the quantizer
+    tests pin on the oracle: every f32 bit pattern with |v| < 2^(se + 3) (all
+    that a block of shared exponent se holds: signed zeros, subnormals, the
+    rounding ties, saturation) for every se the quantizers produce, -127 ..
+    125, v in the low nibble and -v in the high one.  Counts: 2 (E + 127) 2^23
+    patterns below 2^E, E = se + 3."""
+    n = 253
+    mis = rf.DeviceBuffer.zeroed(n, np.uint64, stream)
+    tested = rf.DeviceBuffer.zeroed(n, np.uint64, stream)
+    rf.check(rf.load().rfp4_debug_fp4_encode_check(stream.h, -127, n, mis.ptr, tested.ptr))
+    got_t = tested.to_host(n, np.uint64, stream)
+    got_m = mis.to_host(n, np.uint64, stream)
+    want_t = np.array([2 * ((se + 3 + 127) << 23) for se in range(-127, 126)], np.uint64)
+    np.testing.assert_array_equal(got_t, want_t)
+    assert not got_m.any(), {se: int(m) for se, m in zip(range(-127, 126), got_m) if m}
+    with pytest.raises(rf.Rfp4Error):
+        rf.check(rf.load().rfp4_debug_fp4_encode_check(stream.h, -128, 1, mis.ptr, tested.ptr))
+    with pytest.raises(rf.Rfp4Error):
+        rf.check(rf.load().rfp4_debug_fp4_encode_check(stream.h, 125, 2, mis.ptr, tested.ptr))
+
+
 # ---------------------------------------------------------------- GEMV
 def _config1(orc, n=2048, k=2048, seed=0x12345678):
     """uniform codes, E8M0 exponents in [-6, 2], x ~ N(0,1)."""
