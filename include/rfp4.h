@@ -361,10 +361,11 @@ int rfp4_debug_gemv_waves(int waves);
 /* Test hook: the hardware FP4 encoder every quantizing kernel uses
  * (v_cvt_scalef32_pk_fp4_f32 with scale 2^se) against the software encoder
  * of the OCP MX rules (e2m1, round to nearest even, saturating at 6, the sign
- * kept for zero) on every f32 bit pattern that a block of shared
- * exponent se holds (|v| < 2^(se + 3)), for se = se0 .. se0 + n_se - 1 within
- * -127 .. 125.  mismatches[i] and tested[i] (device, n_se counters each, zeroed
- * by the caller) are incremented for se0 + i.  No reference counterpart. */
+ * kept for zero) on every f32 bit pattern (infinities and NaNs included),
+ * for se = se0 .. se0 + n_se - 1 within -127 .. 125.  mismatches[i] (all
+ * patterns) and tested[i] (the patterns a block of shared exponent se holds,
+ * |v| < 2^(se + 3)) (device, n_se counters each, zeroed by the caller) are
+ * incremented for se0 + i.  No reference counterpart. */
 int rfp4_debug_fp4_encode_check(rfp4_stream_t stream, int32_t se0, uint32_t n_se, unsigned long long *mismatches,
                                 unsigned long long *tested);
 /* Test hook: one GEMV launch with any epilogue (0 store, 1 residual,

@@ -138,8 +138,8 @@ RFP4_DEV uint32_t e2m1_rne_code(float v)
 // conversion divides by its scale operand, here 2^se (se in [-127, 127];
 // 2^-127 is subnormal and used as is), and writes a's code to the low nibble
 // and b's to the high nibble of byte SEL of w.  Checked against
-// e2m1_rne_code on every finite f32 that a block of each shared exponent can
-// hold (|v| < 2^(se + 3)), signed zeros and subnormals included: identical.
+// e2m1_rne_code on every f32 bit pattern at every shared exponent -127 .. 125
+// (signed zeros, subnormals, ties, saturation, infinities, NaNs): identical.
 template <int SEL>
 RFP4_DEV uint32_t fp4_pack2(uint32_t w, float a, float b, float scale)
 {

@@ -172,9 +172,11 @@ K256 void rfp4_synth_weight(SynthWeightArgs a) { synth_weight_body(a); }
 K256 void rfp4_synth_f16(SynthF16Args a) { synth_f16_body(a); }
 K256 void rfp4_synth_kv(SynthKvArgs a) { synth_kv_body(a); }
 // fp4_pack2 (the hardware conversion every quantizer uses) against
-// e2m1_rne_code(ldexpf(v, -se)) on every f32 bit pattern u with |v| < 2^(se + 3)
-// (the values a block of shared exponent se holds), se = se0 + blockIdx.y: v
-// in the low nibble and -v in the high one.  One atomic pair per thread.
+// e2m1_rne_code(ldexpf(v, -se)) on every f32 bit pattern (the values a block
+// of shared exponent se holds, |v| < 2^(se + 3), and all others: saturation,
+// infinities, NaNs), se = se0 + blockIdx.y: v in the low nibble and -v in the
+// high one.  tested counts the patterns below 2^(se + 3).  One atomic pair
+// per thread.
 K256 void rfp4_fp4_encode_check(Fp4CheckArgs a)
 {
     const int se = a.se0 + (int)blockIdx.y;
@@ -183,8 +185,7 @@ K256 void rfp4_fp4_encode_check(Fp4CheckArgs a)
     const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
     for (uint64_t u = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x; u < (1ull << 32); u += stride) {
         const float v = __uint_as_float((uint32_t)u), w = __uint_as_float((uint32_t)u ^ 0x80000000u);
-        if (!(fabsf(v) < lim)) continue;
-        nt++;
+        nt += fabsf(v) < lim ? 1ull : 0ull;
         const uint32_t sw = e2m1_rne_code(ldexpf(v, -se)) | e2m1_rne_code(ldexpf(w, -se)) << 4;
         mis += fp4_pack2<0>(0u, v, w, sc) != sw ? 1ull : 0ull;
     }

@@ -37,11 +37,12 @@ def test_hw_fp4_conversion_matches_codec(rf, orc, stream):
 def test_hw_fp4_encoder_matches_rne_exhaustive(rf, stream):
     """The encoder every quantizing kernel uses (v_cvt_scalef32_pk_fp4_f32,
     scale 2^se) against e2m1_rne_code(ldexpf(v, -se)), which the quantizer
-    tests pin on the oracle: every f32 bit pattern with |v| < 2^(se + 3) (all
-    that a block of shared exponent se holds: signed zeros, subnormals, the
-    rounding ties, saturation) for every se the quantizers produce, -127 ..
-    125, v in the low nibble and -v in the high one.  Counts: 2 (E + 127) 2^23
-    patterns below 2^E, E = se + 3."""
+    tests pin on the oracle: every f32 bit pattern (those a block of shared
+    exponent se holds, |v| < 2^(se + 3): signed zeros, subnormals, the
+    rounding ties; and the rest: saturation, infinities, NaNs) for every se
+    the quantizers produce, -127 .. 125, v in the low nibble and -v in the
+    high one.  tested counts the in-block patterns: 2 (E + 127) 2^23 below
+    2^E, E = se + 3."""
     n = 253
     mis = rf.DeviceBuffer.zeroed(n, np.uint64, stream)
     tested = rf.DeviceBuffer.zeroed(n, np.uint64, stream)
